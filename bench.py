@@ -1,0 +1,185 @@
+#!/usr/bin/env python3
+"""Headline benchmark: ms per forward+backward and Mpix/s of the batched
+rasterizer at 4096x4096, 65,536 splats, B=1 on one MI355X.
+
+A step is one call of rasterize_projected_gaussians on GPU-resident inputs
+followed by backward with loss = sum(image * w) (w fixed, seeded), i.e. the
+whole public-API path: depth sort, binning, pair sort, forward compositing,
+backward compositing, gradients in the original order.
+
+Prints ONE JSON line.  `roofline` is for the dominant kernel (the backward
+compositor, which dominates step time): its launch time is measured live with
+HIP events (torch.cuda.Event on the stream the library launches on) over the
+timed steps.  `cpu_baseline` times the CPU oracle (single-threaded C
+restatement of the reference algorithm, oracle/tile_oracle.c) on the same
+scene, forward+backward, once.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 2]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "fast-mac-gsplat_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+KEYS = ("means2d", "conics", "colors", "opacities", "depths")
+PEAK_FP32_TFLOPS = 157.3   # MI355X published fp32 peak
+PEAK_HBM_GBS = 8000.0      # MI355X published HBM3E bandwidth
+# Algorithmic work per unit (per (pixel, tile-pair) evaluation inside a tile's
+# processed range, upper bound 256 per pair): forward ~24 FLOP, backward ~60.
+FLOP_PER_EVAL = {"render_forward": 24.0, "render_backward": 60.0}
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(sc, H, W, B, G, w_np):
+    """Times the CPU oracle (forward + backward) once on the full scene."""
+    from oracle import tile_oracle as TO
+
+    meta = TO.make_meta(H, W, B, G)
+    s = TO.Scene(*(sc[k].numpy() for k in KEYS), B, G)
+    t0 = time.perf_counter()
+    bins = TO.bin_scene(meta, s)
+    TO.render_forward(meta, s, bins)
+    TO.render_backward(meta, s, bins, w_np)
+    dt = time.perf_counter() - t0
+    return {
+        "value": (B * H * W) / dt / 1e6,
+        "unit": "Mpix/s",
+        "ms_per_step": dt * 1e3,
+        "cores": 1,
+        "kind": "port",
+        "sample": f"full workload ({W}x{H}, B={B}, G={G}), one forward+backward, single thread; "
+                  f"C restatement of the reference tile algorithm; CPU: {_cpu_model()}",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, help="scene config id (torch_gsplat_bridge_fast.scenes)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: every box in this build has one MI355X and the path has no "
+              f"cross-GPU step (got --gpus {args.gpus}, WORLD_SIZE {world}); run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from torch_gsplat_bridge_fast import RasterConfig, _ops, rasterize_projected_gaussians
+    from torch_gsplat_bridge_fast.scenes import CONFIGS, make_scene_2d
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    sc = make_scene_2d(args.config, seed=0)
+    H, W, B, G = sc["H"], sc["W"], sc["B"], sc["G"]
+    leaves = [sc[k].to(dev).requires_grad_(k != "depths") for k in KEYS]
+    w_cpu = torch.rand(B, H, W, 3, generator=torch.Generator().manual_seed(123))
+    w = w_cpu.to(dev)
+    cfg = RasterConfig(height=H, width=W)
+
+    def step():
+        for t in leaves[:4]:
+            t.grad = None
+        img = rasterize_projected_gaussians(*leaves, cfg)
+        img.backward(w)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    _ops.set_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    events = _ops.pop_timing()
+
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    per_op = {}
+    for name, e0, e1 in events:
+        per_op.setdefault(name, []).append(e0.elapsed_time(e1))
+    op_ms = {k: float(np.mean(v)) for k, v in per_op.items()}
+
+    with torch.no_grad():
+        st = _ops.bin_gaussians(
+            __import__("torch_gsplat_bridge_fast.rasterize", fromlist=["_meta"])._meta(cfg, B, G),
+            *(t.detach().reshape(B * G, -1).squeeze(-1).contiguous() for t in leaves))
+    n_pairs = st.n_pairs
+    evals = 256.0 * n_pairs
+    dom = max(("render_forward", "render_backward"), key=lambda k: op_ms.get(k, 0.0))
+    achieved_tflops = evals * FLOP_PER_EVAL[dom] / (op_ms[dom] * 1e-3) / 1e12
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{dom}_cfg{args.config}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    mpix = B * H * W / (ms_per_step * 1e-3) / 1e6
+    line = {
+        "metric": "ms per fwd+bwd (and Mpix/s) at 4096² / 64K splats B=1 on 1 MI355X",
+        "value": round(mpix, 2),
+        "unit": "Mpix/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded BASELINE config scene, generated on CPU, resident in HBM)",
+        "config": {
+            "workload": CONFIGS[args.config]["name"],
+            "height": H, "width": W, "batch": B, "gaussians": G,
+            "tile_pairs": n_pairs,
+            "loss": "sum(image * w), w ~ U(0,1) seed 123",
+            "parallelism": "single GPU",
+        },
+        "stage_ms": {k: round(v, 4) for k, v in op_ms.items()},
+        "roofline": {
+            "kernel": f"{dom} ({'render_bwd_kernel' if dom == 'render_backward' else 'render_fwd_kernel'})",
+            "bound": "valu",
+            "achieved": round(achieved_tflops, 3),
+            "peak": PEAK_FP32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved_tflops / PEAK_FP32_TFLOPS, 4),
+            "traffic": traffic,
+            "work": f"256 * tile_pairs evaluations x {FLOP_PER_EVAL[dom]:.0f} FLOP per launch",
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline({k: sc[k] for k in KEYS}, H, W, B, G, w_cpu.numpy())
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

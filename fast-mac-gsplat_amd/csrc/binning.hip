@@ -1,0 +1,181 @@
+// binning.hip -- per-splat tile intersection count + record packing, and
+// deterministic (tile, gid) pair emission.
+//
+// This translation unit is compiled with -ffp-contract=off: the predicate
+// results must match the CPU oracle bit for bit.
+//
+// count_pack_kernel  one thread per depth-sorted splat (gid).  Gathers the
+//   splat's attributes from the original order (via perm), writes the packed
+//   48-byte record, and counts the tiles whose pixel-centre rectangle meets
+//   the splat's alpha>=threshold ellipse (reference count_tiles,
+//   variants/v8/csrc/metal/gsplat_v8_kernels.metal:244-288).  Also bumps the
+//   per-tile pair counters.
+// emit_kernel        one thread per gid; repeats the same tile walk and
+//   writes (tile, gid) at splat_offsets[gid] + k, so pairs land in ascending
+//   gid order (reference emit_binned_ids, :290-327, which uses per-tile
+//   atomic cursors and therefore needs a later per-tile sort).
+#include "gs_internal.h"
+#include "gs_predicate.h"
+
+namespace gs {
+namespace {
+
+constexpr int kThreads = 256;
+
+struct SplatGeom {
+  float mx, my, a, b, c, o;
+};
+
+// Walks the tiles of one splat's snug bbox in row-major order and calls
+// fn(global_tile) for each tile that passes the exact ellipse/rect test.
+template <typename Fn>
+__device__ __forceinline__ int for_each_hit_tile(const RasterParams& P,
+                                                 const SplatGeom& s, int batch,
+                                                 Fn&& fn) {
+#pragma clang fp contract(off)
+  float tau;
+  if (!alpha_support(s.o, P.alpha_thr, P.eps, tau)) return 0;
+  const PixBox bb =
+      snugbox(s.mx, s.my, s.a, s.b, s.c, tau, P.width, P.height, P.eps);
+  if (bb.x0 > bb.x1 || bb.y0 > bb.y1) return 0;
+  const int tx0 = bb.x0 >> 4, tx1 = bb.x1 >> 4;
+  const int ty0 = bb.y0 >> 4, ty1 = bb.y1 >> 4;
+  const int tile_base = batch * P.tiles_per_image;
+  int n = 0;
+  for (int ty = ty0; ty <= ty1; ++ty) {
+    for (int tx = tx0; tx <= tx1; ++tx) {
+      float rx0, ry0, rx1, ry1;
+      tile_rect(tx, ty, P.width, P.height, rx0, ry0, rx1, ry1);
+      if (ellipse_hits_rect(s.mx, s.my, s.a, s.b, s.c, tau, rx0, ry0, rx1,
+                            ry1)) {
+        fn(tile_base + ty * P.tiles_x + tx, n);
+        ++n;
+      }
+    }
+  }
+  return n;
+}
+
+__global__ __launch_bounds__(kThreads) void count_pack_kernel(
+    RasterParams P, const float* __restrict__ means2d,
+    const float* __restrict__ conics, const float* __restrict__ colors,
+    const float* __restrict__ opacities, const uint32_t* __restrict__ perm,
+    float4* __restrict__ packed, int32_t* __restrict__ splat_counts,
+    int32_t* __restrict__ tile_counts) {
+  const int gid = blockIdx.x * kThreads + threadIdx.x;
+  if (gid >= P.num_splats) return;
+  const int batch = gid / P.gpb;
+  const int orig = batch * P.gpb + (int)perm[gid];
+  SplatGeom s;
+  s.mx = means2d[2 * orig + 0];
+  s.my = means2d[2 * orig + 1];
+  s.a = conics[3 * orig + 0];
+  s.b = conics[3 * orig + 1];
+  s.c = conics[3 * orig + 2];
+  s.o = opacities[orig];
+  const float cr = colors[3 * orig + 0];
+  const float cg = colors[3 * orig + 1];
+  const float cb = colors[3 * orig + 2];
+  packed[3 * gid + 0] = make_float4(s.mx, s.my, s.a, s.b);
+  packed[3 * gid + 1] = make_float4(s.c, s.o, cr, cg);
+  packed[3 * gid + 2] = make_float4(cb, __int_as_float(orig), 0.0f, 0.0f);
+  const int n = for_each_hit_tile(P, s, batch, [&](int tile, int) {
+    atomicAdd(&tile_counts[tile], 1);
+  });
+  splat_counts[gid] = n;
+}
+
+__global__ __launch_bounds__(kThreads) void emit_kernel(
+    RasterParams P, const float4* __restrict__ packed,
+    const int32_t* __restrict__ splat_offsets, uint32_t* __restrict__ keys,
+    uint32_t* __restrict__ vals) {
+  const int gid = blockIdx.x * kThreads + threadIdx.x;
+  if (gid >= P.num_splats) return;
+  const float4 p0 = packed[3 * gid + 0];
+  const float4 p1 = packed[3 * gid + 1];
+  const SplatGeom s{p0.x, p0.y, p0.z, p0.w, p1.x, p1.y};
+  const int batch = gid / P.gpb;
+  const int64_t base = splat_offsets[gid];
+  for_each_hit_tile(P, s, batch, [&](int tile, int k) {
+    keys[base + k] = (uint32_t)tile;
+    vals[base + k] = (uint32_t)gid;
+  });
+}
+
+__global__ void fill_i32_kernel(int32_t* dst, int32_t v, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = v;
+}
+
+__global__ void fill_f32_kernel(float* dst, float v, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = v;
+}
+
+// Zeroes the four per-splat gradient arrays (2n, 3n, 3n, n floats) in one
+// launch.
+__global__ void zero_grads_kernel(float* g_m, float* g_q, float* g_c,
+                                  float* g_o, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < 2 * n) g_m[i] = 0.0f;
+  if (i < 3 * n) {
+    g_q[i] = 0.0f;
+    g_c[i] = 0.0f;
+  }
+  if (i < n) g_o[i] = 0.0f;
+}
+
+}  // namespace
+
+int launch_count_pack(const RasterParams& P, const float* means2d,
+                      const float* conics, const float* colors,
+                      const float* opacities, const uint32_t* perm,
+                      float* packed, int32_t* splat_counts,
+                      int32_t* tile_counts, hipStream_t stream) {
+  if (P.num_splats == 0) return GSPLAT_OK;
+  const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
+  hipLaunchKernelGGL(count_pack_kernel, dim3(grid), dim3(kThreads), 0, stream,
+                     P, means2d, conics, colors, opacities, perm,
+                     reinterpret_cast<float4*>(packed), splat_counts,
+                     tile_counts);
+  return check_launch("count_pack_kernel");
+}
+
+int launch_emit(const RasterParams& P, const float* packed,
+                const int32_t* splat_offsets, uint32_t* keys, uint32_t* vals,
+                hipStream_t stream) {
+  if (P.num_splats == 0) return GSPLAT_OK;
+  const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
+  hipLaunchKernelGGL(emit_kernel, dim3(grid), dim3(kThreads), 0, stream, P,
+                     reinterpret_cast<const float4*>(packed), splat_offsets,
+                     keys, vals);
+  return check_launch("emit_kernel");
+}
+
+int launch_fill_i32(int32_t* dst, int32_t value, int64_t n,
+                    hipStream_t stream) {
+  if (n <= 0) return GSPLAT_OK;
+  const int64_t grid = (n + 255) / 256;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     stream, dst, value, n);
+  return check_launch("fill_i32_kernel");
+}
+
+int launch_zero_grads(float* g_m, float* g_q, float* g_c, float* g_o,
+                      int64_t n, hipStream_t stream) {
+  if (n <= 0) return GSPLAT_OK;
+  const int64_t grid = (3 * n + 255) / 256;
+  hipLaunchKernelGGL(zero_grads_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     stream, g_m, g_q, g_c, g_o, n);
+  return check_launch("zero_grads_kernel");
+}
+
+int launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream) {
+  if (n <= 0) return GSPLAT_OK;
+  const int64_t grid = (n + 255) / 256;
+  hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     stream, dst, value, n);
+  return check_launch("fill_f32_kernel");
+}
+
+}  // namespace gs

@@ -1,0 +1,363 @@
+// capi.hip -- extern "C" entry points declared in include/gsplat_hip.h.
+//
+// Validation happens here, before any launch; every launch is followed by a
+// hipGetLastError check.  Nothing here allocates or synchronises: buffers
+// and workspaces belong to the caller and all work is enqueued on the
+// caller's stream.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "gs_internal.h"
+
+namespace gs {
+
+namespace {
+thread_local char g_err[1024] = "";
+}
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return GSPLAT_ERR_HIP;
+  }
+  return GSPLAT_OK;
+}
+
+}  // namespace gs
+
+namespace {
+
+using gs::RasterParams;
+
+constexpr int64_t kMaxSplats = int64_t(1) << 28;
+
+int bits_for(int64_t max_value) {
+  int b = 0;
+  while (b < 32 && (int64_t(1) << b) <= max_value) ++b;
+  return b;
+}
+
+int make_params(const gsplat_raster_meta* m, RasterParams& P) {
+  if (m == nullptr) {
+    gs::set_error("meta is NULL");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  if (m->tile_size != GSPLAT_TILE_SIZE) {
+    gs::set_error("tile_size must be %d (got %d)", GSPLAT_TILE_SIZE,
+                  m->tile_size);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  if (m->height <= 0 || m->width <= 0 || m->batch <= 0 ||
+      m->gaussians_per_batch <= 0) {
+    gs::set_error("height, width, batch and gaussians_per_batch must be > 0");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  const int64_t tiles_x = (m->width + 15) / 16;
+  const int64_t tiles_y = (m->height + 15) / 16;
+  const int64_t tpi = tiles_x * tiles_y;
+  const int64_t T = tpi * m->batch;
+  const int64_t BG = (int64_t)m->batch * m->gaussians_per_batch;
+  const int64_t pixels = (int64_t)m->batch * m->height * m->width;
+  if (T >= 0x7fffffffLL || BG > kMaxSplats || pixels * 3 >= (int64_t(1) << 40)) {
+    gs::set_error("problem too large (tiles %lld, splats %lld)", (long long)T,
+                  (long long)BG);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  P.height = m->height;
+  P.width = m->width;
+  P.tiles_x = (int)tiles_x;
+  P.tiles_y = (int)tiles_y;
+  P.tiles_per_image = (int)tpi;
+  P.num_tiles = (int)T;
+  P.batch = m->batch;
+  P.gpb = m->gaussians_per_batch;
+  P.num_splats = (int)BG;
+  P.alpha_thr = m->alpha_threshold;
+  P.trans_thr = m->transmittance_threshold;
+  P.bg_r = m->background[0];
+  P.bg_g = m->background[1];
+  P.bg_b = m->background[2];
+  P.eps = m->eps;
+  P.max_alpha = m->max_alpha;
+  return GSPLAT_OK;
+}
+
+int null_check(std::initializer_list<const void*> ptrs, const char* what) {
+  for (const void* p : ptrs) {
+    if (p == nullptr) {
+      gs::set_error("%s: NULL pointer argument", what);
+      return GSPLAT_ERR_INVALID_ARGUMENT;
+    }
+  }
+  return GSPLAT_OK;
+}
+
+size_t count_ws(const RasterParams& P) {
+  size_t a = gs::radix_sort_workspace_bytes(P.gpb, P.batch);
+  size_t b = gs::scan_workspace_bytes(P.num_splats);
+  size_t c = gs::scan_workspace_bytes(P.num_tiles);
+  size_t m = a > b ? a : b;
+  return m > c ? m : c;
+}
+
+struct EmitLayout {
+  size_t keys, vals, sort, total;
+};
+
+EmitLayout emit_layout(const RasterParams& P, int64_t n) {
+  EmitLayout L{};
+  const size_t vec = gs::align_up((size_t)n * sizeof(uint32_t), 256);
+  L.keys = 0;
+  L.vals = vec;
+  L.sort = 2 * vec;
+  L.total = L.sort + gs::radix_sort_workspace_bytes(n, 1);
+  (void)P;
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gsplat_hip_abi_version(void) { return GSPLAT_HIP_ABI_VERSION; }
+
+const char* gsplat_hip_last_error(void) { return gs::g_err; }
+
+size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta) {
+  RasterParams P;
+  if (make_params(meta, P)) return 0;
+  return count_ws(P);
+}
+
+int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
+                         const float* conics, const float* colors,
+                         const float* opacities, const float* depths,
+                         int32_t* perm, float* packed, int32_t* splat_offsets,
+                         int32_t* tile_counts, int32_t* tile_offsets,
+                         void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  RasterParams P;
+  int rc = make_params(meta, P);
+  if (rc) return rc;
+  rc = null_check({means2d, conics, colors, opacities, depths, perm, packed,
+                   splat_offsets, tile_counts, tile_offsets},
+                  "gsplat_hip_bin_count");
+  if (rc) return rc;
+  const size_t need = count_ws(P);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr)) {
+    gs::set_error("gsplat_hip_bin_count: workspace too small (%zu < %zu)",
+                  workspace_bytes, need);
+    return GSPLAT_ERR_WORKSPACE;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = gs::launch_fill_i32(tile_counts, 0, P.num_tiles, s);
+  if (rc) return rc;
+  rc = gs::radix_sort_pairs(nullptr, nullptr, depths, nullptr,
+                            reinterpret_cast<uint32_t*>(perm), P.gpb, P.batch,
+                            0, 32, workspace, workspace_bytes, s);
+  if (rc) return rc;
+  rc = gs::launch_count_pack(P, means2d, conics, colors, opacities,
+                             reinterpret_cast<const uint32_t*>(perm), packed,
+                             splat_offsets, tile_counts, s);
+  if (rc) return rc;
+  rc = gs::exclusive_scan_i32(splat_offsets, splat_offsets, P.num_splats,
+                              workspace, workspace_bytes, s);
+  if (rc) return rc;
+  return gs::exclusive_scan_i32(tile_counts, tile_offsets, P.num_tiles,
+                                workspace, workspace_bytes, s);
+}
+
+size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
+                                           int64_t n_pairs) {
+  RasterParams P;
+  if (make_params(meta, P) || n_pairs < 0) return 0;
+  return emit_layout(P, n_pairs).total;
+}
+
+int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
+                        const int32_t* splat_offsets, int64_t n_pairs,
+                        int32_t* binned_ids, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  RasterParams P;
+  int rc = make_params(meta, P);
+  if (rc) return rc;
+  if (n_pairs < 0 || n_pairs > 0x7fffffffLL) {
+    gs::set_error("gsplat_hip_bin_emit: invalid pair count %lld",
+                  (long long)n_pairs);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  if (n_pairs == 0) return GSPLAT_OK;
+  rc = null_check({packed, splat_offsets, binned_ids, workspace},
+                  "gsplat_hip_bin_emit");
+  if (rc) return rc;
+  const EmitLayout L = emit_layout(P, n_pairs);
+  if (workspace_bytes < L.total) {
+    gs::set_error("gsplat_hip_bin_emit: workspace too small (%zu < %zu)",
+                  workspace_bytes, L.total);
+    return GSPLAT_ERR_WORKSPACE;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* base = static_cast<char*>(workspace);
+  uint32_t* keys = reinterpret_cast<uint32_t*>(base + L.keys);
+  uint32_t* vals = reinterpret_cast<uint32_t*>(base + L.vals);
+  rc = gs::launch_emit(P, packed, splat_offsets, keys, vals, s);
+  if (rc) return rc;
+  const int end_bit = bits_for((int64_t)P.num_tiles - 1);
+  return gs::radix_sort_pairs(keys, vals, nullptr, nullptr,
+                              reinterpret_cast<uint32_t*>(binned_ids), n_pairs,
+                              1, 0, end_bit, base + L.sort,
+                              workspace_bytes - L.sort, s);
+}
+
+int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
+                              const float* packed, const int32_t* tile_offsets,
+                              const int32_t* binned_ids, float* out_rgb,
+                              float* out_final_T, int32_t* out_last,
+                              int32_t* out_tile_stop, void* stream) {
+  RasterParams P;
+  int rc = make_params(meta, P);
+  if (rc) return rc;
+  rc = null_check({packed, tile_offsets, out_rgb}, "gsplat_hip_render_forward");
+  if (rc) return rc;
+  if ((out_final_T == nullptr) != (out_last == nullptr)) {
+    gs::set_error(
+        "gsplat_hip_render_forward: out_final_T and out_last must both be "
+        "given or both be NULL");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  return gs::launch_render_forward(P, packed, tile_offsets, binned_ids, out_rgb,
+                                   out_final_T, out_last, out_tile_stop,
+                                   static_cast<hipStream_t>(stream));
+}
+
+int gsplat_hip_render_backward(const gsplat_raster_meta* meta,
+                               const float* packed,
+                               const int32_t* tile_offsets,
+                               const int32_t* binned_ids,
+                               const float* final_T, const int32_t* last,
+                               const int32_t* tile_stop, const float* grad_rgb,
+                               float* g_means2d, float* g_conics,
+                               float* g_colors, float* g_opacities,
+                               void* stream) {
+  RasterParams P;
+  int rc = make_params(meta, P);
+  if (rc) return rc;
+  rc = null_check({packed, tile_offsets, final_T, last, tile_stop, grad_rgb,
+                   g_means2d, g_conics, g_colors, g_opacities},
+                  "gsplat_hip_render_backward");
+  if (rc) return rc;
+  return gs::launch_render_backward(P, packed, tile_offsets, binned_ids,
+                                    final_T, last, tile_stop, grad_rgb,
+                                    g_means2d, g_conics, g_colors, g_opacities,
+                                    static_cast<hipStream_t>(stream));
+}
+
+static int make_project_params(const gsplat_project_meta* m,
+                               gs::ProjectParams& P) {
+  if (m == nullptr || m->batch <= 0 || m->gaussians_per_batch <= 0) {
+    gs::set_error("project meta: batch and gaussians_per_batch must be > 0");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  const int64_t BG = (int64_t)m->batch * m->gaussians_per_batch;
+  if (BG > kMaxSplats) {
+    gs::set_error("project meta: too many splats (%lld)", (long long)BG);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  P.batch = m->batch;
+  P.gpb = m->gaussians_per_batch;
+  P.num_splats = (int)BG;
+  P.near_plane = m->near_plane;
+  return GSPLAT_OK;
+}
+
+int gsplat_hip_project_forward(const gsplat_project_meta* meta,
+                               const float* means3d, const float* scales,
+                               const float* quats, const float* opacities,
+                               const float* camera_to_world,
+                               const float* camera_params, float* out_means2d,
+                               float* out_conics, float* out_opacities,
+                               float* out_depths, void* stream) {
+  gs::ProjectParams P;
+  int rc = make_project_params(meta, P);
+  if (rc) return rc;
+  rc = null_check({means3d, scales, quats, opacities, camera_to_world,
+                   camera_params, out_means2d, out_conics, out_opacities,
+                   out_depths},
+                  "gsplat_hip_project_forward");
+  if (rc) return rc;
+  return gs::launch_project_forward(P, means3d, scales, quats, opacities,
+                                    camera_to_world, camera_params,
+                                    out_means2d, out_conics, out_opacities,
+                                    out_depths,
+                                    static_cast<hipStream_t>(stream));
+}
+
+int gsplat_hip_project_backward(
+    const gsplat_project_meta* meta, const float* grad_means2d,
+    const float* grad_conics, const float* grad_opacities,
+    const float* grad_depths, const float* means3d, const float* scales,
+    const float* quats, const float* opacities, const float* camera_to_world,
+    const float* camera_params, float* g_means3d, float* g_scales,
+    float* g_quats, float* g_opacities, float* g_camera_to_world,
+    float* g_camera_params, void* stream) {
+  gs::ProjectParams P;
+  int rc = make_project_params(meta, P);
+  if (rc) return rc;
+  rc = null_check({grad_means2d, grad_conics, grad_opacities, grad_depths,
+                   means3d, scales, quats, opacities, camera_to_world,
+                   camera_params, g_means3d, g_scales, g_quats, g_opacities,
+                   g_camera_to_world, g_camera_params},
+                  "gsplat_hip_project_backward");
+  if (rc) return rc;
+  return gs::launch_project_backward(
+      P, grad_means2d, grad_conics, grad_opacities, grad_depths, means3d,
+      scales, quats, opacities, camera_to_world, camera_params, g_means3d,
+      g_scales, g_quats, g_opacities, g_camera_to_world, g_camera_params,
+      static_cast<hipStream_t>(stream));
+}
+
+size_t gsplat_hip_scan_workspace_bytes(int64_t n) {
+  return gs::scan_workspace_bytes(n);
+}
+
+int gsplat_hip_exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  if (n > 0x7fffffffLL) {
+    gs::set_error("exclusive_scan: n too large");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  // An empty input may come with a NULL pointer; out always receives out[0].
+  int rc = null_check({n > 0 ? in : out, out}, "gsplat_hip_exclusive_scan_i32");
+  if (rc) return rc;
+  return gs::exclusive_scan_i32(in, out, n, workspace, workspace_bytes,
+                                static_cast<hipStream_t>(stream));
+}
+
+size_t gsplat_hip_radix_sort_workspace_bytes(int64_t n_per_segment,
+                                             int32_t segments) {
+  return gs::radix_sort_workspace_bytes(n_per_segment, segments);
+}
+
+int gsplat_hip_radix_sort_pairs_u32(const uint32_t* keys_in,
+                                    const uint32_t* vals_in,
+                                    uint32_t* keys_out, uint32_t* vals_out,
+                                    int64_t n_per_segment, int32_t segments,
+                                    int32_t begin_bit, int32_t end_bit,
+                                    void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  return gs::radix_sort_pairs(keys_in, vals_in, nullptr, keys_out, vals_out,
+                              n_per_segment, segments, begin_bit, end_bit,
+                              workspace, workspace_bytes,
+                              static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,145 @@
+// gs_predicate.h -- splat support / tile-overlap predicate used by binning.
+//
+// These functions decide which (splat, tile) pairs exist, so their results
+// must be reproducible bit for bit by the CPU oracle.  Every operation here
+// is an IEEE-754 single-precision +, -, *, /, sqrt, floor, ceil, min, max or
+// compare (all correctly rounded on gfx950 with the library's build flags),
+// FP contraction is switched off, and the one transcendental (log) is
+// computed by gs_logf below from those operations only.
+//
+// Semantics follow the reference's predicate:
+//   alpha_support_params  variants/v8/csrc/metal/gsplat_v8_kernels.metal:77-82
+//   snugbox               gsplat_v8_kernels.metal:84-93
+//   ellipse_intersects_rect gsplat_v8_kernels.metal:95-119
+//   tile rectangle        gsplat_v8_kernels.metal:275-281
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gs {
+
+// Natural logarithm for x > 0 by binary range reduction and the atanh series
+// (Abramowitz & Stegun 4.1.27: ln m = 2 atanh(s), s = (m-1)/(m+1)), with
+// m in [sqrt(1/2), sqrt(2)) so |s| <= 0.1716 and terms through s^11 leave a
+// truncation error below 1e-10 relative.  ln 2 is split Cody-Waite style
+// (hi has 12 trailing zero bits, so e*hi is exact).  Accuracy is a few ulp;
+// what matters is that the result is a fixed function of x built only from
+// correctly rounded operations, so host and device agree exactly.
+__device__ __forceinline__ float gs_logf(float x) {
+#pragma clang fp contract(off)
+  if (!(x == x)) return x;                                    // NaN
+  if (x <= 0.0f) return (x == 0.0f) ? -__builtin_inff() : __builtin_nanf("");
+  if (x == __builtin_inff()) return x;
+  uint32_t u = __float_as_uint(x);
+  int e = 0;
+  if ((u >> 23) == 0u) {                                      // subnormal
+    x = x * 8388608.0f;                                       // 2^23, exact
+    u = __float_as_uint(x);
+    e = -23;
+  }
+  e += (int)((u >> 23) & 0xffu) - 127;
+  float m = __uint_as_float((u & 0x007fffffu) | 0x3f800000u); // [1, 2)
+  if (m > 1.41421354f) {
+    m = m * 0.5f;
+    e += 1;
+  }
+  const float s = (m - 1.0f) / (m + 1.0f);
+  const float z = s * s;
+  float p = 0.0909090936f;                 // 1/11
+  p = p * z + 0.111111112f;                // 1/9
+  p = p * z + 0.142857149f;                // 1/7
+  p = p * z + 0.200000003f;                // 1/5
+  p = p * z + 0.333333343f;                // 1/3
+  p = p * z;
+  const float two_s = s + s;
+  const float lnm = two_s + two_s * p;
+  const float fe = (float)e;
+  return fe * 0.693115234f + (fe * 3.19461833e-05f + lnm);
+}
+
+// Support of o*exp(-q/2) >= thr:  q <= tau = -2 ln(max(thr / max(o,eps), eps)).
+__device__ __forceinline__ bool alpha_support(float opacity, float thr,
+                                              float eps, float& tau) {
+#pragma clang fp contract(off)
+  if (opacity <= thr) return false;
+  const float ratio = fmaxf(thr / fmaxf(opacity, eps), eps);
+  tau = -2.0f * gs_logf(ratio);
+  return __builtin_isfinite(tau) && (tau > 0.0f);
+}
+
+__device__ __forceinline__ int clamp_to_int(float v) {
+  // Saturating float->int for the bbox corners (NaN -> 0).  Values that
+  // matter are small integers already.
+  v = fminf(fmaxf(v, -1073741824.0f), 1073741824.0f);
+  return (int)v;
+}
+
+struct PixBox {
+  int x0, y0, x1, y1;  // inclusive pixel bbox; empty if x0 > x1 or y0 > y1
+};
+
+__device__ __forceinline__ PixBox snugbox(float mx, float my, float a, float b,
+                                          float c, float tau, int width,
+                                          int height, float eps) {
+#pragma clang fp contract(off)
+  const float det = fmaxf(a * c - b * b, eps);
+  const float hx = __builtin_sqrtf(fmaxf(tau * c / det, 0.0f));
+  const float hy = __builtin_sqrtf(fmaxf(tau * a / det, 0.0f));
+  PixBox r;
+  r.x0 = max(0, clamp_to_int(floorf(mx - hx - 0.5f)));
+  r.x1 = min(width - 1, clamp_to_int(ceilf(mx + hx - 0.5f)));
+  r.y0 = max(0, clamp_to_int(floorf(my - hy - 0.5f)));
+  r.y1 = min(height - 1, clamp_to_int(ceilf(my + hy - 0.5f)));
+  return r;
+}
+
+__device__ __forceinline__ float quad_form(float a, float b, float c, float dx,
+                                           float dy) {
+#pragma clang fp contract(off)
+  return a * dx * dx + 2.0f * b * dx * dy + c * dy * dy;
+}
+
+// Exact minimum of the conic quadratic over the axis-aligned rectangle of
+// pixel centres [rx0,rx1]x[ry0,ry1] compared against tau.
+__device__ __forceinline__ bool ellipse_hits_rect(float mx, float my, float a,
+                                                  float b, float c, float tau,
+                                                  float rx0, float ry0,
+                                                  float rx1, float ry1) {
+#pragma clang fp contract(off)
+  if (mx >= rx0 && mx <= rx1 && my >= ry0 && my <= ry1) return true;
+  const float dx0 = rx0 - mx, dx1 = rx1 - mx;
+  const float dy0 = ry0 - my, dy1 = ry1 - my;
+  float q = quad_form(a, b, c, dx0, dy0);
+  q = fminf(q, quad_form(a, b, c, dx0, dy1));
+  q = fminf(q, quad_form(a, b, c, dx1, dy0));
+  q = fminf(q, quad_form(a, b, c, dx1, dy1));
+  if (c > 1e-8f) {
+    const float k = -(b / c);
+    float dy = fminf(fmaxf(k * dx0, dy0), dy1);
+    q = fminf(q, quad_form(a, b, c, dx0, dy));
+    dy = fminf(fmaxf(k * dx1, dy0), dy1);
+    q = fminf(q, quad_form(a, b, c, dx1, dy));
+  }
+  if (a > 1e-8f) {
+    const float k = -(b / a);
+    float dx = fminf(fmaxf(k * dy0, dx0), dx1);
+    q = fminf(q, quad_form(a, b, c, dx, dy0));
+    dx = fminf(fmaxf(k * dy1, dx0), dx1);
+    q = fminf(q, quad_form(a, b, c, dx, dy1));
+  }
+  return q <= tau;
+}
+
+// Pixel-centre rectangle of tile (tx, ty), clipped to the image.
+__device__ __forceinline__ void tile_rect(int tx, int ty, int width, int height,
+                                          float& rx0, float& ry0, float& rx1,
+                                          float& ry1) {
+#pragma clang fp contract(off)
+  rx0 = (float)(tx * 16) + 0.5f;
+  rx1 = fminf((float)(width - 1) + 0.5f, (float)(tx * 16 + 15) + 0.5f);
+  ry0 = (float)(ty * 16) + 0.5f;
+  ry1 = fminf((float)(height - 1) + 0.5f, (float)(ty * 16 + 15) + 0.5f);
+}
+
+}  // namespace gs

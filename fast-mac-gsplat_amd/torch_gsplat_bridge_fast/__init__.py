@@ -1,0 +1,23 @@
+"""MI355X (gfx950) differentiable Gaussian-splat rasterizer.
+
+Drop-in for the reference package of the same name, exposing its batched
+projected-2D API plus the pinhole projection front end.
+"""
+from .rasterize import (
+    ProjectedGaussianRasterizer,
+    RasterConfig,
+    get_runtime_shader_config,
+    profile_projected_gaussians,
+    rasterize_projected_gaussians,
+)
+from .project import project_pinhole_gaussians, rasterize_pinhole_gaussians
+
+__all__ = [
+    "RasterConfig",
+    "ProjectedGaussianRasterizer",
+    "rasterize_projected_gaussians",
+    "profile_projected_gaussians",
+    "get_runtime_shader_config",
+    "project_pinhole_gaussians",
+    "rasterize_pinhole_gaussians",
+]

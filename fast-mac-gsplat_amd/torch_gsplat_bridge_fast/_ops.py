@@ -1,0 +1,205 @@
+"""Tensor-level wrappers over the C ABI.
+
+Each function allocates its outputs with torch's caching allocator on the
+inputs' device, enqueues the HIP work on the current stream and returns the
+tensors.  The only host synchronisation on the raster path is the read of the
+pair count N between binning's count and emit stages (the reference makes the
+same read, variants/v8/csrc/metal/gsplat_metal.mm:188).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from ._lib import check, ptr, stream_of
+
+
+# Optional per-op timing: when enabled, every C-ABI call below is bracketed by
+# torch.cuda events recorded on the stream the work is enqueued on.
+_timing: Optional[list] = None
+
+
+def set_timing(enabled: bool) -> None:
+    global _timing
+    _timing = [] if enabled else None
+
+
+def pop_timing() -> list:
+    """Returns [(op_name, start_event, end_event)] recorded since set_timing(True)."""
+    global _timing
+    out = _timing or []
+    _timing = None
+    return out
+
+
+class _timed:
+    def __init__(self, name):
+        self.name = name
+
+    def __enter__(self):
+        if _timing is not None:
+            self.e0 = torch.cuda.Event(enable_timing=True)
+            self.e0.record()
+        return self
+
+    def __exit__(self, *exc):
+        if _timing is not None and exc[0] is None:
+            e1 = torch.cuda.Event(enable_timing=True)
+            e1.record()
+            _timing.append((self.name, self.e0, e1))
+        return False
+
+
+@dataclass
+class BinState:
+    perm: Tensor          # int32 [BG]  depth rank -> original index within image
+    packed: Tensor        # float32 [BG, 12]  packed records in gid order
+    splat_offsets: Tensor # int32 [BG+1]
+    tile_counts: Tensor   # int32 [T]
+    tile_offsets: Tensor  # int32 [T+1]
+    binned_ids: Tensor    # int32 [N]
+    n_pairs: int
+
+
+def _empty(n, dtype, device):
+    return torch.empty((n,), dtype=dtype, device=device)
+
+
+def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
+                  opacities: Tensor, depths: Tensor) -> BinState:
+    """Stable depth order + record packing + tile binning + pair sort.
+
+    Inputs are flat contiguous fp32 [BG,2], [BG,3], [BG,3], [BG], [BG] in the
+    original splat order."""
+    L = _lib.lib()
+    dev = means2d.device
+    B, G = meta.batch, meta.gaussians_per_batch
+    BG = B * G
+    tiles = B * ((meta.height + 15) // 16) * ((meta.width + 15) // 16)
+    perm = _empty(BG, torch.int32, dev)
+    packed = torch.empty((BG, _lib.RECORD_FLOATS), dtype=torch.float32, device=dev)
+    splat_offsets = _empty(BG + 1, torch.int32, dev)
+    tile_counts = _empty(tiles, torch.int32, dev)
+    tile_offsets = _empty(tiles + 1, torch.int32, dev)
+    ws_bytes = L.gsplat_hip_bin_count_workspace_bytes(meta)
+    ws = _empty(max(ws_bytes, 1), torch.uint8, dev)
+    s = stream_of(means2d)
+    with _timed("bin_count"):
+        check(L.gsplat_hip_bin_count(meta, ptr(means2d), ptr(conics), ptr(colors), ptr(opacities), ptr(depths),
+                                     ptr(perm), ptr(packed), ptr(splat_offsets), ptr(tile_counts),
+                                     ptr(tile_offsets), ptr(ws), ws_bytes, s), "gsplat_hip_bin_count")
+    n = int(tile_offsets[-1].item())
+    if n < 0:
+        raise RuntimeError(f"pair count overflowed int32 ({n})")
+    binned = _empty(n, torch.int32, dev)
+    if n > 0:
+        ws2_bytes = L.gsplat_hip_bin_emit_workspace_bytes(meta, n)
+        ws2 = _empty(ws2_bytes, torch.uint8, dev)
+        with _timed("bin_emit"):
+            check(L.gsplat_hip_bin_emit(meta, ptr(packed), ptr(splat_offsets), n, ptr(binned), ptr(ws2), ws2_bytes,
+                                        s), "gsplat_hip_bin_emit")
+    return BinState(perm, packed, splat_offsets, tile_counts, tile_offsets, binned, n)
+
+
+def render_forward(meta: _lib.RasterMeta, st: BinState, *, save_state: bool):
+    L = _lib.lib()
+    dev = st.packed.device
+    B, H, W = meta.batch, meta.height, meta.width
+    tiles = st.tile_counts.numel()
+    img = torch.empty((B, H, W, 3), dtype=torch.float32, device=dev)
+    final_T = last = tile_stop = None
+    if save_state:
+        final_T = torch.empty((B, H, W), dtype=torch.float32, device=dev)
+        last = torch.empty((B, H, W), dtype=torch.int32, device=dev)
+        tile_stop = _empty(tiles, torch.int32, dev)
+    with _timed("render_forward"):
+        check(L.gsplat_hip_render_forward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.binned_ids), ptr(img),
+                                          ptr(final_T), ptr(last), ptr(tile_stop), stream_of(img)),
+              "gsplat_hip_render_forward")
+    return img, final_T, last, tile_stop
+
+
+def render_backward(meta: _lib.RasterMeta, st: BinState, final_T: Tensor, last: Tensor, tile_stop: Tensor,
+                    grad_img: Tensor):
+    """Returns (g_means2d [BG,2], g_conics [BG,3], g_colors [BG,3], g_opacities [BG]) in ORIGINAL order."""
+    L = _lib.lib()
+    dev = st.packed.device
+    BG = meta.batch * meta.gaussians_per_batch
+    g_m = torch.empty((BG, 2), dtype=torch.float32, device=dev)
+    g_q = torch.empty((BG, 3), dtype=torch.float32, device=dev)
+    g_c = torch.empty((BG, 3), dtype=torch.float32, device=dev)
+    g_o = torch.empty((BG,), dtype=torch.float32, device=dev)
+    grad_img = grad_img.contiguous()
+    with _timed("render_backward"):
+        check(L.gsplat_hip_render_backward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.binned_ids),
+                                           ptr(final_T), ptr(last), ptr(tile_stop), ptr(grad_img), ptr(g_m), ptr(g_q),
+                                           ptr(g_c), ptr(g_o), stream_of(grad_img)),
+              "gsplat_hip_render_backward")
+    return g_m, g_q, g_c, g_o
+
+
+def project_forward(meta: _lib.ProjectMeta, means3d, scales, quats, opacities, c2w, cam):
+    L = _lib.lib()
+    dev = means3d.device
+    BG = meta.batch * meta.gaussians_per_batch
+    m2 = torch.empty((BG, 2), dtype=torch.float32, device=dev)
+    cq = torch.empty((BG, 3), dtype=torch.float32, device=dev)
+    op = torch.empty((BG,), dtype=torch.float32, device=dev)
+    dp = torch.empty((BG,), dtype=torch.float32, device=dev)
+    with _timed("project_forward"):
+        check(L.gsplat_hip_project_forward(meta, ptr(means3d), ptr(scales), ptr(quats), ptr(opacities), ptr(c2w),
+                                           ptr(cam), ptr(m2), ptr(cq), ptr(op), ptr(dp), stream_of(means3d)),
+              "gsplat_hip_project_forward")
+    return m2, cq, op, dp
+
+
+def project_backward(meta: _lib.ProjectMeta, g_m2, g_cq, g_op, g_dp, means3d, scales, quats, opacities, c2w, cam):
+    L = _lib.lib()
+    dev = means3d.device
+    B = meta.batch
+    BG = B * meta.gaussians_per_batch
+    gm3 = torch.empty((BG, 3), dtype=torch.float32, device=dev)
+    gs = torch.empty((BG, 3), dtype=torch.float32, device=dev)
+    gq = torch.empty((BG, 4), dtype=torch.float32, device=dev)
+    go = torch.empty((BG,), dtype=torch.float32, device=dev)
+    gc2w = torch.empty((B, 4, 4), dtype=torch.float32, device=dev)
+    gcam = torch.empty((B, 4), dtype=torch.float32, device=dev)
+    with _timed("project_backward"):
+        check(L.gsplat_hip_project_backward(meta, ptr(g_m2), ptr(g_cq), ptr(g_op), ptr(g_dp), ptr(means3d),
+                                            ptr(scales), ptr(quats), ptr(opacities), ptr(c2w), ptr(cam), ptr(gm3),
+                                            ptr(gs), ptr(gq), ptr(go), ptr(gc2w), ptr(gcam), stream_of(means3d)),
+              "gsplat_hip_project_backward")
+    return gm3, gs, gq, go, gc2w, gcam
+
+
+def exclusive_scan_i32(x: Tensor) -> Tensor:
+    """out[0..n]: exclusive prefix sum of int32 x with the total at out[n]."""
+    L = _lib.lib()
+    n = x.numel()
+    out = _empty(n + 1, torch.int32, x.device)
+    wsb = L.gsplat_hip_scan_workspace_bytes(n)
+    ws = _empty(max(wsb, 1), torch.uint8, x.device)
+    check(L.gsplat_hip_exclusive_scan_i32(ptr(x), ptr(out), n, ptr(ws), wsb, stream_of(x)),
+          "gsplat_hip_exclusive_scan_i32")
+    return out
+
+
+def radix_sort_pairs_u32(keys: Tensor, vals: Optional[Tensor], *, segments: int = 1, begin_bit: int = 0,
+                         end_bit: int = 32):
+    """Stable per-segment LSD sort of int32-typed (bit pattern uint32) keys."""
+    L = _lib.lib()
+    n = keys.numel()
+    assert n % segments == 0
+    n_seg = n // segments
+    ko = torch.empty_like(keys)
+    vo = torch.empty((n,), dtype=torch.int32, device=keys.device)
+    wsb = L.gsplat_hip_radix_sort_workspace_bytes(n_seg, segments)
+    ws = _empty(max(wsb, 1), torch.uint8, keys.device)
+    check(L.gsplat_hip_radix_sort_pairs_u32(ptr(keys), ptr(vals), ptr(ko), ptr(vo), n_seg, segments, begin_bit,
+                                            end_bit, ptr(ws), wsb, stream_of(keys)),
+          "gsplat_hip_radix_sort_pairs_u32")
+    return ko, vo

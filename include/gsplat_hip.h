@@ -1,0 +1,220 @@
+/*
+ * gsplat_hip.h -- C ABI of the MI355X (gfx950) differentiable Gaussian-splat
+ * rasterizer.
+ *
+ * Every entry point takes plain device pointers, element counts and a HIP
+ * stream (passed as void*).  The caller owns all memory: outputs and
+ * workspaces are allocated by the caller (the Python layer uses torch's
+ * caching allocator) and sized with the *_workspace_bytes queries.  No entry
+ * point allocates, frees or synchronises the stream.
+ *
+ * All functions return GSPLAT_OK (0) on success.  On failure they return a
+ * non-zero status and a thread-local message is available from
+ * gsplat_hip_last_error().  Kernel launch errors are checked after every
+ * launch.
+ *
+ * Conventions (shared with the reference's batched API):
+ *   B      images in the batch, G splats per image, BG = B*G
+ *   tiles  16x16 pixels, tiles_x = ceil(W/16), tiles_y = ceil(H/16),
+ *          tile id = b*tiles_y*tiles_x + ty*tiles_x + tx, T = B*tiles_y*tiles_x
+ *   "gid"  flat index b*G + r where r is the splat's rank in a stable sort of
+ *          image b's depths (ascending, ties by original index); ascending gid
+ *          within a tile is front-to-back order.
+ *   packed splat record: 12 floats per gid,
+ *          {mx, my, a, b, c, opacity, r, g, b, orig_index(bits), 0, 0}
+ *          with the conic (a,b,c) meaning power = -0.5*(a dx^2 + 2 b dx dy + c dy^2).
+ */
+#ifndef GSPLAT_HIP_H
+#define GSPLAT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GSPLAT_HIP_ABI_VERSION 1
+#define GSPLAT_TILE_SIZE 16
+#define GSPLAT_RECORD_FLOATS 12
+
+enum gsplat_status {
+  GSPLAT_OK = 0,
+  GSPLAT_ERR_INVALID_ARGUMENT = 1,
+  GSPLAT_ERR_HIP = 2,
+  GSPLAT_ERR_WORKSPACE = 3
+};
+
+/* Static render parameters.  Mirrors the reference's RasterConfig plus the
+ * meta packing of variants/v8/torch_gsplat_bridge_v8/rasterize.py:129-173
+ * (eps = 1e-8 and max_alpha = 0.99 are fixed there and passed here). */
+typedef struct gsplat_raster_meta {
+  int32_t height;
+  int32_t width;
+  int32_t tile_size;           /* must be 16 */
+  int32_t batch;               /* B >= 1 */
+  int32_t gaussians_per_batch; /* G >= 1 */
+  float alpha_threshold;       /* 1/255 by default */
+  float transmittance_threshold; /* 1e-4 by default */
+  float background[3];
+  float eps;                   /* 1e-8 */
+  float max_alpha;             /* 0.99 */
+} gsplat_raster_meta;
+
+/* Pinhole projection parameters (variants/v9_project3d_train/
+ * torch_gsplat_bridge_v9_project3d_train/rasterize.py:265-285). */
+typedef struct gsplat_project_meta {
+  int32_t batch;
+  int32_t gaussians_per_batch;
+  float near_plane;            /* 1e-4 by default */
+} gsplat_project_meta;
+
+int gsplat_hip_abi_version(void);
+const char* gsplat_hip_last_error(void);
+
+/* ---------------------------------------------------------------- binning
+ * Replaces torch.ops.gsplat_metal_v8.bin (variants/v8/csrc/bindings.cpp:201,
+ * host side variants/v8/csrc/metal/gsplat_metal.mm:140-204) together with the
+ * stable depth argsort + gathers of variants/v8/torch_gsplat_bridge_v8/
+ * rasterize.py:465-475.  The reference sizes binned_ids with a host read of
+ * tile_offsets[-1] (gsplat_metal.mm:188); here binning is split at the same
+ * point: gsplat_hip_bin_count leaves the pair count N in tile_offsets[T] (and
+ * splat_offsets[BG]), the caller reads it and sizes gsplat_hip_bin_emit. */
+
+size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta);
+
+/* Inputs (original order): means2d [BG,2], conics [BG,3], colors [BG,3],
+ * opacities [BG], depths [BG].  Outputs:
+ *   perm          int32 [BG]   perm[b*G+r] = original index (within image b)
+ *                              of the splat of depth rank r
+ *   packed        float [BG*12] packed records in gid order
+ *   splat_offsets int32 [BG+1] exclusive scan of per-gid tile-hit counts
+ *   tile_counts   int32 [T]    pairs per tile
+ *   tile_offsets  int32 [T+1]  exclusive scan of tile_counts (tile ranges) */
+int gsplat_hip_bin_count(const gsplat_raster_meta* meta,
+                         const float* means2d, const float* conics,
+                         const float* colors, const float* opacities,
+                         const float* depths,
+                         int32_t* perm, float* packed, int32_t* splat_offsets,
+                         int32_t* tile_counts, int32_t* tile_offsets,
+                         void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
+                                           int64_t n_pairs);
+
+/* Emits one (tile, gid) pair per tile hit at the deterministic scan offsets,
+ * then sorts the pairs by tile with a stable LSD radix sort (8-bit digits).
+ * binned_ids int32 [N]: gids grouped by tile, ascending gid (= depth order)
+ * inside each tile range [tile_offsets[t], tile_offsets[t+1]).  The sorted
+ * 64-bit key of pair i is (tile << 32) | binned_ids[i].
+ * Replaces emit_binned_ids (variants/v8/csrc/metal/gsplat_v8_kernels.metal:
+ * 290-327) and the per-tile bitonic sort (:141-164, :441-442). */
+int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
+                        const int32_t* splat_offsets, int64_t n_pairs,
+                        int32_t* binned_ids,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* -------------------------------------------------------------- composite
+ * Forward compositor.  Replaces render_fast_forward_state / _eval
+ * (variants/v8/csrc/bindings.cpp:202-203; kernels gsplat_v8_kernels.metal:
+ * 330-476).  out_rgb float [B,H,W,3].  State outputs (all nullable together
+ * for the eval path): out_final_T float [B,H,W] transmittance after the last
+ * composited splat, out_last int32 [B,H,W] = 1 + index (within the tile
+ * range) of the last composited splat (0 if none), out_tile_stop int32 [T]
+ * = max of out_last over the tile's pixels. */
+int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
+                              const float* packed,
+                              const int32_t* tile_offsets,
+                              const int32_t* binned_ids,
+                              float* out_rgb, float* out_final_T,
+                              int32_t* out_last, int32_t* out_tile_stop,
+                              void* stream);
+
+/* Backward compositor.  Replaces render_fast_backward_saved
+ * (variants/v8/csrc/bindings.cpp:204; kernel gsplat_v8_kernels.metal:
+ * 478-608).  Gradients are accumulated (atomically) into the ORIGINAL splat
+ * order using the orig_index stored in each packed record; the four gradient
+ * buffers are zeroed by this call.  g_means2d [BG,2], g_conics [BG,3],
+ * g_colors [BG,3], g_opacities [BG]. */
+int gsplat_hip_render_backward(const gsplat_raster_meta* meta,
+                               const float* packed,
+                               const int32_t* tile_offsets,
+                               const int32_t* binned_ids,
+                               const float* final_T, const int32_t* last,
+                               const int32_t* tile_stop,
+                               const float* grad_rgb,
+                               float* g_means2d, float* g_conics,
+                               float* g_colors, float* g_opacities,
+                               void* stream);
+
+/* ------------------------------------------------------------- projection
+ * Pinhole projection.  Replaces torch.ops.gsplat_metal_v9_project3d_train.
+ * project_pinhole_forward / _backward (variants/v9_project3d_train/csrc/
+ * bindings.cpp:175-176; kernels gsplat_v9_project3d_train_kernels.metal:
+ * 66-174 and 217-501).  means3d [BG,3], scales [BG,3] (linear), quats [BG,4]
+ * (r,i,j,k, not normalised), opacities [BG], camera_to_world [B,4,4]
+ * row-major, camera_params [B,4] = (fx, fy, cx, cy).  Outputs means2d
+ * [BG,2], conics [BG,3], opacities [BG] (0 behind the near plane), depths
+ * [BG] (camera z). */
+int gsplat_hip_project_forward(const gsplat_project_meta* meta,
+                               const float* means3d, const float* scales,
+                               const float* quats, const float* opacities,
+                               const float* camera_to_world,
+                               const float* camera_params,
+                               float* out_means2d, float* out_conics,
+                               float* out_opacities, float* out_depths,
+                               void* stream);
+
+/* Vector-Jacobian product of gsplat_hip_project_forward.  Per-splat grads are
+ * written directly; g_camera_to_world [B,4,4] and g_camera_params [B,4] are
+ * zeroed by this call and accumulated atomically (one atomic per wavefront
+ * and entry after an in-wave reduction). */
+int gsplat_hip_project_backward(const gsplat_project_meta* meta,
+                                const float* grad_means2d,
+                                const float* grad_conics,
+                                const float* grad_opacities,
+                                const float* grad_depths,
+                                const float* means3d, const float* scales,
+                                const float* quats, const float* opacities,
+                                const float* camera_to_world,
+                                const float* camera_params,
+                                float* g_means3d, float* g_scales,
+                                float* g_quats, float* g_opacities,
+                                float* g_camera_to_world,
+                                float* g_camera_params,
+                                void* stream);
+
+/* ------------------------------------------------------------- primitives
+ * Device-wide building blocks used by the stages above, exported so they can
+ * be tested in isolation.  They have no counterpart in the reference (which
+ * uses torch::cumsum, gsplat_metal.mm:183, and an in-threadgroup bitonic
+ * sort). */
+
+size_t gsplat_hip_scan_workspace_bytes(int64_t n);
+/* out[0..n] = exclusive prefix sum of in[0..n-1]; out[n] = total.  In-place
+ * (out == in) is allowed. */
+int gsplat_hip_exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+size_t gsplat_hip_radix_sort_workspace_bytes(int64_t n_per_segment,
+                                             int32_t segments);
+/* Stable LSD radix sort of (key, value) pairs on key bits
+ * [begin_bit, end_bit), 8-bit digits, independently inside each of
+ * `segments` contiguous segments of n_per_segment elements.  vals_in may be
+ * NULL (values are then the index within the segment); keys_out may be NULL
+ * (keys are then not written). */
+int gsplat_hip_radix_sort_pairs_u32(const uint32_t* keys_in,
+                                    const uint32_t* vals_in,
+                                    uint32_t* keys_out, uint32_t* vals_out,
+                                    int64_t n_per_segment, int32_t segments,
+                                    int32_t begin_bit, int32_t end_bit,
+                                    void* workspace, size_t workspace_bytes,
+                                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSPLAT_HIP_H */

@@ -1,0 +1,180 @@
+"""TEST INFRASTRUCTURE ONLY -- numpy interface to the CPU oracle tile_oracle.c.
+
+Used by tests/ as the parity checker and by bench.py's cpu_baseline leg;
+never by the product path.  See tile_oracle.c for the reference lines each
+function restates.  Build: ``make -C oracle`` (also done by
+``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_build", "libtile_oracle.so")
+
+
+class OracleMeta(ctypes.Structure):
+    _fields_ = [
+        ("height", ctypes.c_int32),
+        ("width", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("gpb", ctypes.c_int32),
+        ("alpha_threshold", ctypes.c_float),
+        ("transmittance_threshold", ctypes.c_float),
+        ("bg", ctypes.c_float * 3),
+        ("eps", ctypes.c_float),
+        ("max_alpha", ctypes.c_float),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library missing at {LIB_PATH}; run `make -C oracle`")
+        L = ctypes.CDLL(LIB_PATH)
+        vp = ctypes.c_void_p
+        pm = ctypes.POINTER(OracleMeta)
+        L.oracle_logf.restype = ctypes.c_float
+        L.oracle_logf.argtypes = [ctypes.c_float]
+        L.oracle_depth_order.restype = None
+        L.oracle_depth_order.argtypes = [vp, ctypes.c_int32, ctypes.c_int32, vp]
+        L.oracle_bin_count.restype = ctypes.c_int64
+        L.oracle_bin_count.argtypes = [pm, vp, vp, vp, vp, vp, vp]
+        L.oracle_bin_fill.restype = None
+        L.oracle_bin_fill.argtypes = [pm, vp, vp, vp, vp, vp, vp]
+        L.oracle_render_forward.restype = None
+        L.oracle_render_forward.argtypes = [pm] + [vp] * 12
+        L.oracle_render_backward.restype = None
+        L.oracle_render_backward.argtypes = [pm] + [vp] * 12
+        L.oracle_taint.restype = None
+        L.oracle_taint.argtypes = [pm] + [vp] * 9
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def _f32(a, shape=None):
+    a = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+    return a if shape is None else a.reshape(shape)
+
+
+def make_meta(height, width, batch, gpb, alpha_threshold=1.0 / 255.0, transmittance_threshold=1e-4,
+              background=(0.0, 0.0, 0.0), eps=1e-8, max_alpha=0.99) -> OracleMeta:
+    m = OracleMeta()
+    m.height, m.width, m.batch, m.gpb = int(height), int(width), int(batch), int(gpb)
+    m.alpha_threshold = float(alpha_threshold)
+    m.transmittance_threshold = float(transmittance_threshold)
+    for i in range(3):
+        m.bg[i] = float(background[i])
+    m.eps = float(eps)
+    m.max_alpha = float(max_alpha)
+    return m
+
+
+def logf(x: float) -> float:
+    return float(lib().oracle_logf(ctypes.c_float(x)))
+
+
+@dataclass
+class OracleBins:
+    perm: np.ndarray         # int32 [BG]
+    tile_counts: np.ndarray  # int32 [T]
+    tile_offsets: np.ndarray # int32 [T+1]
+    binned_ids: np.ndarray   # int32 [N]
+
+    def sorted_keys(self) -> np.ndarray:
+        """64-bit keys (tile << 32) | gid of the sorted pair list."""
+        tiles = np.repeat(np.arange(self.tile_counts.size, dtype=np.uint64), self.tile_counts.astype(np.int64))
+        return (tiles << np.uint64(32)) | self.binned_ids.astype(np.uint64)
+
+
+class Scene:
+    """Flat float32 inputs in original order: means2d [BG,2], conics [BG,3],
+    colors [BG,3], opacities [BG], depths [BG]."""
+
+    def __init__(self, means2d, conics, colors, opacities, depths, B, G):
+        self.B, self.G = int(B), int(G)
+        n = self.B * self.G
+        self.means2d = _f32(means2d, (n, 2))
+        self.conics = _f32(conics, (n, 3))
+        self.colors = _f32(colors, (n, 3))
+        self.opacities = _f32(opacities, (n,))
+        self.depths = _f32(depths, (n,))
+
+
+def depth_order(depths, B, G) -> np.ndarray:
+    d = _f32(depths, (B * G,))
+    perm = np.empty(B * G, dtype=np.int32)
+    lib().oracle_depth_order(_p(d), B, G, _p(perm))
+    return perm
+
+
+def bin_scene(meta: OracleMeta, s: Scene) -> OracleBins:
+    L = lib()
+    perm = depth_order(s.depths, s.B, s.G)
+    tiles = meta.batch * ((meta.width + 15) // 16) * ((meta.height + 15) // 16)
+    counts = np.empty(tiles, dtype=np.int32)
+    offsets = np.empty(tiles + 1, dtype=np.int32)
+    n = L.oracle_bin_count(ctypes.byref(meta), _p(s.means2d), _p(s.conics), _p(s.opacities), _p(perm), _p(counts),
+                           _p(offsets))
+    ids = np.empty(max(n, 0), dtype=np.int32)
+    L.oracle_bin_fill(ctypes.byref(meta), _p(s.means2d), _p(s.conics), _p(s.opacities), _p(perm), _p(offsets),
+                      _p(ids))
+    return OracleBins(perm, counts, offsets, ids)
+
+
+AMB_ALPHA, AMB_STOP, AMB_GATE = 1, 2, 4
+
+
+def render_forward(meta: OracleMeta, s: Scene, bins: OracleBins, with_ambiguity: bool = False):
+    """Returns (img, final_T, last, tile_stop[, ambiguity]).  ambiguity[b,y,x] is a
+    bit mask: AMB_ALPHA / AMB_STOP when an alpha-threshold or early-stop decision
+    of the pixel lies within exp's last-ulp window (another exact-arithmetic
+    implementation may decide it the other way), AMB_GATE for the max_alpha
+    gradient gate."""
+    B, H, W = meta.batch, meta.height, meta.width
+    img = np.empty((B, H, W, 3), dtype=np.float32)
+    T = np.empty((B, H, W), dtype=np.float32)
+    last = np.empty((B, H, W), dtype=np.int32)
+    stop = np.empty(bins.tile_counts.size, dtype=np.int32)
+    amb = np.empty((B, H, W), dtype=np.uint8)
+    lib().oracle_render_forward(ctypes.byref(meta), _p(s.means2d), _p(s.conics), _p(s.colors), _p(s.opacities),
+                                _p(bins.perm), _p(bins.tile_offsets), _p(bins.binned_ids), _p(img), _p(T), _p(last),
+                                _p(stop), _p(amb))
+    if with_ambiguity:
+        return img, T, last, stop, amb
+    return img, T, last, stop
+
+
+def tainted_splats(meta: OracleMeta, s: Scene, bins: OracleBins, amb: np.ndarray) -> np.ndarray:
+    """Boolean [B*G] (original order): splats visible at some ambiguous pixel.
+    Their gradients may legitimately differ between two exact implementations."""
+    out = np.zeros(s.B * s.G, dtype=np.uint8)
+    a = np.ascontiguousarray(amb, dtype=np.uint8)
+    lib().oracle_taint(ctypes.byref(meta), _p(s.means2d), _p(s.conics), _p(s.colors), _p(s.opacities),
+                       _p(bins.perm), _p(bins.tile_offsets), _p(bins.binned_ids), _p(a), _p(out))
+    return out.astype(bool)
+
+
+def render_backward(meta: OracleMeta, s: Scene, bins: OracleBins, grad_img):
+    n = s.B * s.G
+    g = _f32(grad_img, (meta.batch, meta.height, meta.width, 3))
+    gm = np.zeros((n, 2), dtype=np.float32)
+    gq = np.zeros((n, 3), dtype=np.float32)
+    gc = np.zeros((n, 3), dtype=np.float32)
+    go = np.zeros((n,), dtype=np.float32)
+    lib().oracle_render_backward(ctypes.byref(meta), _p(s.means2d), _p(s.conics), _p(s.colors), _p(s.opacities),
+                                 _p(bins.perm), _p(bins.tile_offsets), _p(bins.binned_ids), _p(g), _p(gm), _p(gq),
+                                 _p(gc), _p(go))
+    return gm, gq, gc, go

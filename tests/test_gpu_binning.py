@@ -1,0 +1,161 @@
+"""GPU parity: scan, radix sort, depth order and tile binning vs the CPU oracle.
+
+Bar: bit-exact (integer / index work).  Calls go through the C ABI
+(libgsplat_hip.so via torch_gsplat_bridge_fast._ops / _lib).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tile_oracle as TO
+from torch_gsplat_bridge_fast import _lib, _ops
+from torch_gsplat_bridge_fast.scenes import make_scene_2d
+
+pytestmark = pytest.mark.gpu
+
+KEYS = ("means2d", "conics", "colors", "opacities", "depths")
+
+
+@pytest.mark.parametrize("n", [0, 1, 63, 8191, 8192, 8193, 100_000, (1 << 18), (1 << 18) + 1, 3_000_017])
+def test_exclusive_scan(gpu, n):
+    print(f"scan n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    x = rng.integers(0, 50, size=n).astype(np.int32)
+    out = _ops.exclusive_scan_i32(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    ref = np.concatenate([[0], np.cumsum(x, dtype=np.int64)]).astype(np.int32)
+    np.testing.assert_array_equal(out, ref)
+
+
+def test_exclusive_scan_in_place(gpu):
+    x = torch.randint(0, 9, (300_001,), dtype=torch.int32)
+    ref = np.concatenate([[0], np.cumsum(x.numpy(), dtype=np.int64)]).astype(np.int32)
+    buf = torch.zeros(300_002, dtype=torch.int32, device=gpu)
+    buf[:-1] = x.to(gpu)
+    L = _lib.lib()
+    wsb = L.gsplat_hip_scan_workspace_bytes(300_001)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    _lib.check(L.gsplat_hip_exclusive_scan_i32(buf.data_ptr(), buf.data_ptr(), 300_001, ws.data_ptr(), wsb,
+                                               _lib.stream_of(buf)), "scan")
+    np.testing.assert_array_equal(buf.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("n,segments,begin,end,keyrange", [
+    (1, 1, 0, 32, 1 << 32),
+    (5000, 1, 0, 16, 1 << 16),
+    (4096, 1, 0, 32, 1 << 32),
+    (100_003, 1, 0, 13, 37),          # many duplicates, partial digit
+    (700_001, 1, 0, 16, 1 << 16),
+    (65536, 4, 0, 32, 1 << 32),       # segmented
+    (10_000, 3, 8, 24, 1 << 32),      # bit window
+    (1000, 2, 0, 0, 1 << 32),         # zero passes: copy
+])
+def test_radix_sort_stable(gpu, n, segments, begin, end, keyrange):
+    print(f"radix n={n} seg={segments} bits=[{begin},{end})", flush=True)
+    rng = np.random.default_rng(n + segments)
+    keys = rng.integers(0, keyrange, size=n * segments, dtype=np.uint64).astype(np.uint32)
+    vals = rng.integers(0, 1 << 31, size=n * segments).astype(np.int32)
+    ko, vo = _ops.radix_sort_pairs_u32(torch.from_numpy(keys.view(np.int32)).to(gpu), torch.from_numpy(vals).to(gpu),
+                                       segments=segments, begin_bit=begin, end_bit=end)
+    ko = ko.cpu().numpy().view(np.uint32)
+    vo = vo.cpu().numpy()
+    mask = np.uint64(((1 << end) - 1) - ((1 << begin) - 1)) if end > begin else np.uint64(0)
+    for s in range(segments):
+        sl = slice(s * n, (s + 1) * n)
+        sub = keys[sl].astype(np.uint64) & mask
+        order = np.argsort(sub, kind="stable")
+        np.testing.assert_array_equal(ko[sl], keys[sl][order])
+        np.testing.assert_array_equal(vo[sl], vals[sl][order])
+
+
+def _gpu_bins(scene, H, W, B, G, background=(0.0, 0.0, 0.0)):
+    dev = torch.device("cuda:0")
+    meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, background)
+    flat = [scene[k].reshape(B * G, -1).squeeze(-1).contiguous().to(dev) for k in KEYS]
+    return _ops.bin_gaussians(meta, *flat)
+
+
+def _oracle_bins(scene, H, W, B, G):
+    meta = TO.make_meta(H, W, B, G)
+    s = TO.Scene(*(scene[k].numpy() for k in KEYS), B, G)
+    return meta, s, TO.bin_scene(meta, s)
+
+
+def _assert_bins_equal(st, ob, scene, B, G):
+    np.testing.assert_array_equal(st.perm.cpu().numpy(), ob.perm, err_msg="depth order")
+    np.testing.assert_array_equal(st.tile_counts.cpu().numpy(), ob.tile_counts, err_msg="tile counts")
+    np.testing.assert_array_equal(st.tile_offsets.cpu().numpy(), ob.tile_offsets, err_msg="tile ranges")
+    assert st.n_pairs == ob.binned_ids.size
+    np.testing.assert_array_equal(st.binned_ids.cpu().numpy(), ob.binned_ids, err_msg="sorted pair ids")
+    # packed records are exact copies of the inputs in gid order
+    packed = st.packed.cpu().numpy()
+    orig = (np.arange(B * G) // G) * G + ob.perm
+    m = scene["means2d"].reshape(-1, 2).numpy()
+    q = scene["conics"].reshape(-1, 3).numpy()
+    c = scene["colors"].reshape(-1, 3).numpy()
+    o = scene["opacities"].reshape(-1).numpy()
+    np.testing.assert_array_equal(packed[:, 0:2], m[orig])
+    np.testing.assert_array_equal(packed[:, 2:5], q[orig])
+    np.testing.assert_array_equal(packed[:, 5], o[orig])
+    np.testing.assert_array_equal(packed[:, 6:9], c[orig])
+    np.testing.assert_array_equal(packed[:, 9].view(np.int32), orig.astype(np.int32))
+    # sorted 64-bit keys (tile << 32 | gid) strictly increase
+    keys = ob.sorted_keys()
+    assert np.all(keys[1:] > keys[:-1])
+
+
+@pytest.mark.parametrize("cfg_id,kw", [
+    (0, {}),
+    (1, {}),
+    (2, {}),
+    (3, {}),
+    (0, dict(H=37, W=53, G=777)),       # ragged image, G not a multiple of 64
+    (3, dict(B=3, G=1000, H=100, W=90)),
+])
+def test_binning_bit_exact(gpu, cfg_id, kw):
+    sc = make_scene_2d(cfg_id, seed=11, **kw)
+    H, W, B, G = sc["H"], sc["W"], sc["B"], sc["G"]
+    print(f"binning cfg{cfg_id} {W}x{H} B={B} G={G}", flush=True)
+    st = _gpu_bins(sc, H, W, B, G)
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    _assert_bins_equal(st, ob, sc, B, G)
+
+
+def test_binning_edge_cases(gpu):
+    """Off-screen, zero/threshold opacity, degenerate and huge conics, depth ties, -0/+0, NaN depth."""
+    rng = np.random.default_rng(5)
+    B, G, H, W = 2, 300, 70, 45
+    m = rng.uniform(-60, 110, size=(B, G, 2)).astype(np.float32)
+    sig = rng.uniform(0.2, 40, size=(B, G, 2))
+    th = rng.uniform(0, np.pi, size=(B, G))
+    c, s = np.cos(th), np.sin(th)
+    ix, iy = 1 / sig[..., 0] ** 2, 1 / sig[..., 1] ** 2
+    q = np.stack([c * c * ix + s * s * iy, c * s * (ix - iy), s * s * ix + c * c * iy], -1).astype(np.float32)
+    q[:, :10] = [1e-9, 0.0, 1e-9]           # near-zero conic: huge support
+    q[:, 10:20] = [50.0, 0.0, 50.0]         # tiny support
+    o = rng.uniform(0, 1, size=(B, G)).astype(np.float32)
+    o[:, 20:30] = 0.0
+    o[:, 30:40] = 1.0 / 255.0
+    o[:, 40:50] = 1.0
+    d = rng.integers(0, 5, size=(B, G)).astype(np.float32)   # many ties
+    d[:, 50] = -0.0
+    d[:, 51] = 0.0
+    d[:, 52] = np.nan
+    d[:, 53] = -np.inf
+    col = rng.uniform(0, 1, size=(B, G, 3)).astype(np.float32)
+    sc = {k: torch.from_numpy(v) for k, v in
+          dict(means2d=m, conics=q, colors=col, opacities=o, depths=d).items()}
+    st = _gpu_bins(sc, H, W, B, G)
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    _assert_bins_equal(st, ob, sc, B, G)
+    # stable argsort semantics: ties by index, -0 == +0, NaN last
+    for b in range(B):
+        np.testing.assert_array_equal(ob.perm[b * G:(b + 1) * G], np.argsort(d[b], kind="stable"))
+
+
+def test_binning_all_culled(gpu):
+    B, G, H, W = 1, 100, 32, 32
+    sc = make_scene_2d(0, seed=1, G=G, H=H, W=W)
+    sc["opacities"] = torch.zeros_like(sc["opacities"])
+    st = _gpu_bins(sc, H, W, B, G)
+    assert st.n_pairs == 0
+    assert int(st.tile_counts.sum()) == 0
