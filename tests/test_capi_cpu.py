@@ -1,0 +1,95 @@
+"""CPU checks of the C ABI library: it loads, exports exactly what
+include/gsplat_hip.h declares, and validates arguments before launching
+anything (these calls never reach the GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from torch_gsplat_bridge_fast import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gsplat_hip.h")
+
+
+def _declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(gsplat_hip_\w+)\s*\(", src)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared_functions()
+    assert len(names) >= 14
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in gsplat_hip.h but not exported"
+    # the Python binding covers exactly the declared surface
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_abi_version():
+    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 1
+
+
+def _meta(**kw):
+    m = _lib.make_raster_meta(64, 80, 2, 100, 1 / 255, 1e-4, (0, 0, 0))
+    for k, v in kw.items():
+        setattr(m, k, v)
+    return m
+
+
+def test_workspace_queries():
+    L = _lib.lib()
+    assert L.gsplat_hip_bin_count_workspace_bytes(_meta()) > 0
+    assert L.gsplat_hip_bin_emit_workspace_bytes(_meta(), 12345) >= 2 * 12345 * 4
+    assert L.gsplat_hip_scan_workspace_bytes(1000) == 0          # single-workgroup path
+    assert L.gsplat_hip_scan_workspace_bytes(10_000_000) > 0
+    assert L.gsplat_hip_radix_sort_workspace_bytes(100_000, 3) > 0
+    # invalid meta -> 0 bytes
+    assert L.gsplat_hip_bin_count_workspace_bytes(_meta(tile_size=8)) == 0
+
+
+@pytest.mark.parametrize("field,value,msg", [
+    ("tile_size", 8, "tile_size must be 16"),
+    ("height", 0, "must be > 0"),
+    ("batch", 0, "must be > 0"),
+    ("gaussians_per_batch", -3, "must be > 0"),
+])
+def test_invalid_meta_rejected_before_launch(field, value, msg):
+    L = _lib.lib()
+    m = _meta(**{field: value})
+    dummy = ctypes.c_void_p(1)
+    rc = L.gsplat_hip_render_forward(m, dummy, dummy, dummy, dummy, None, None, None, None)
+    assert rc == 1
+    assert msg in L.gsplat_hip_last_error().decode()
+
+
+def test_null_pointers_rejected():
+    L = _lib.lib()
+    rc = L.gsplat_hip_render_backward(_meta(), None, None, None, None, None, None, None, None, None, None, None,
+                                      None)
+    assert rc == 1
+    assert "NULL" in L.gsplat_hip_last_error().decode()
+    rc = L.gsplat_hip_render_forward(_meta(), ctypes.c_void_p(1), ctypes.c_void_p(1), None, ctypes.c_void_p(1),
+                                     ctypes.c_void_p(1), None, None, None)
+    assert rc == 1 and "both" in L.gsplat_hip_last_error().decode()
+
+
+def test_workspace_too_small_rejected():
+    L = _lib.lib()
+    one = ctypes.c_void_p(1)
+    rc = L.gsplat_hip_bin_count(_meta(), *([one] * 10), one, 1, None)
+    assert rc == 3
+    assert "workspace" in L.gsplat_hip_last_error().decode()
+    rc = L.gsplat_hip_bin_emit(_meta(), one, one, 10, one, one, 1, None)
+    assert rc == 3
+
+
+def test_projection_meta_rejected():
+    L = _lib.lib()
+    pm = _lib.make_project_meta(0, 10, 1e-4)
+    one = ctypes.c_void_p(1)
+    rc = L.gsplat_hip_project_forward(pm, *([one] * 10), None)
+    assert rc == 1 and "batch" in L.gsplat_hip_last_error().decode()
