@@ -6,16 +6,20 @@
 //
 // count_pack_kernel  one thread per depth-sorted splat (gid).  Gathers the
 //   splat's attributes from the original order (via perm), writes the packed
-//   48-byte record, and counts the tiles whose pixel-centre rectangle meets
-//   the splat's alpha>=threshold ellipse (reference count_tiles,
-//   variants/v8/csrc/metal/gsplat_v8_kernels.metal:244-288).  Also bumps the
-//   per-tile pair counters.
+//   48-byte record, counts the tiles whose pixel-centre rectangle meets the
+//   splat's alpha >= threshold ellipse (reference count_tiles,
+//   variants/v8/csrc/metal/gsplat_v8_kernels.metal:244-288), bumps the
+//   per-tile pair counters, and turns the per-splat counts into exclusive
+//   offsets in the same launch (workgroup scan + decoupled look-back).
 // emit_kernel        one thread per gid; repeats the same tile walk and
 //   writes (tile, gid) at splat_offsets[gid] + k, so pairs land in ascending
 //   gid order (reference emit_binned_ids, :290-327, which uses per-tile
-//   atomic cursors and therefore needs a later per-tile sort).
+//   atomic cursors and therefore needs a later per-tile sort).  The same
+//   launch also prepares the pair sort: it zeroes the sort's look-back status
+//   and accumulates its per-pass digit histograms from the tile counts.
 #include "gs_internal.h"
 #include "gs_predicate.h"
+#include "lookback.h"
 
 namespace gs {
 namespace {
@@ -27,7 +31,7 @@ struct SplatGeom {
 };
 
 // Walks the tiles of one splat's snug bbox in row-major order and calls
-// fn(global_tile) for each tile that passes the exact ellipse/rect test.
+// fn(global_tile, k) for the k-th tile that passes the exact ellipse/rect test.
 template <typename Fn>
 __device__ __forceinline__ int for_each_hit_tile(const RasterParams& P,
                                                  const SplatGeom& s, int batch,
@@ -41,12 +45,13 @@ __device__ __forceinline__ int for_each_hit_tile(const RasterParams& P,
   const int tx0 = bb.x0 >> 4, tx1 = bb.x1 >> 4;
   const int ty0 = bb.y0 >> 4, ty1 = bb.y1 >> 4;
   const int tile_base = batch * P.tiles_per_image;
+  const ConicSlopes k = conic_slopes(s.a, s.b, s.c);
   int n = 0;
   for (int ty = ty0; ty <= ty1; ++ty) {
     for (int tx = tx0; tx <= tx1; ++tx) {
       float rx0, ry0, rx1, ry1;
       tile_rect(tx, ty, P.width, P.height, rx0, ry0, rx1, ry1);
-      if (ellipse_hits_rect(s.mx, s.my, s.a, s.b, s.c, tau, rx0, ry0, rx1,
+      if (ellipse_hits_rect(s.mx, s.my, s.a, s.b, s.c, k, tau, rx0, ry0, rx1,
                             ry1)) {
         fn(tile_base + ty * P.tiles_x + tx, n);
         ++n;
@@ -60,36 +65,99 @@ __global__ __launch_bounds__(kThreads) void count_pack_kernel(
     RasterParams P, const float* __restrict__ means2d,
     const float* __restrict__ conics, const float* __restrict__ colors,
     const float* __restrict__ opacities, const uint32_t* __restrict__ perm,
-    float4* __restrict__ packed, int32_t* __restrict__ splat_counts,
-    int32_t* __restrict__ tile_counts) {
-  const int gid = blockIdx.x * kThreads + threadIdx.x;
-  if (gid >= P.num_splats) return;
-  const int batch = gid / P.gpb;
-  const int orig = batch * P.gpb + (int)perm[gid];
-  SplatGeom s;
-  s.mx = means2d[2 * orig + 0];
-  s.my = means2d[2 * orig + 1];
-  s.a = conics[3 * orig + 0];
-  s.b = conics[3 * orig + 1];
-  s.c = conics[3 * orig + 2];
-  s.o = opacities[orig];
-  const float cr = colors[3 * orig + 0];
-  const float cg = colors[3 * orig + 1];
-  const float cb = colors[3 * orig + 2];
-  packed[3 * gid + 0] = make_float4(s.mx, s.my, s.a, s.b);
-  packed[3 * gid + 1] = make_float4(s.c, s.o, cr, cg);
-  packed[3 * gid + 2] = make_float4(cb, __int_as_float(orig), 0.0f, 0.0f);
-  const int n = for_each_hit_tile(P, s, batch, [&](int tile, int) {
-    atomicAdd(&tile_counts[tile], 1);
-  });
-  splat_counts[gid] = n;
+    float4* __restrict__ packed, int32_t* __restrict__ splat_offsets,
+    int32_t* __restrict__ tile_counts, uint64_t* scan_status,
+    uint32_t* scan_ticket) {
+  __shared__ int wsum[kThreads / 64];
+  __shared__ int s_prefix;
+  const int vb = take_ticket(scan_ticket);
+  const int gid = vb * kThreads + threadIdx.x;
+  int n = 0;
+  if (gid < P.num_splats) {
+    const int batch = gid / P.gpb;
+    const int orig = batch * P.gpb + (int)perm[gid];
+    SplatGeom s;
+    s.mx = means2d[2 * orig + 0];
+    s.my = means2d[2 * orig + 1];
+    s.a = conics[3 * orig + 0];
+    s.b = conics[3 * orig + 1];
+    s.c = conics[3 * orig + 2];
+    s.o = opacities[orig];
+    const float cr = colors[3 * orig + 0];
+    const float cg = colors[3 * orig + 1];
+    const float cb = colors[3 * orig + 2];
+    packed[3 * gid + 0] = make_float4(s.mx, s.my, s.a, s.b);
+    packed[3 * gid + 1] = make_float4(s.c, s.o, cr, cg);
+    packed[3 * gid + 2] = make_float4(cb, __int_as_float(orig), 0.0f, 0.0f);
+    n = for_each_hit_tile(P, s, batch, [&](int tile, int) {
+      atomicAdd(&tile_counts[tile], 1);
+    });
+  }
+  // Workgroup exclusive scan of the counts.
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = n;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += y;
+  }
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  int pre = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) {
+    pre += (w < wave) ? wsum[w] : 0;
+    total += wsum[w];
+  }
+  if (wave == 0) {
+    if (lane == 0)
+      status_store(&scan_status[vb], (vb == 0 ? kFlagInc64 : kFlagAgg64) |
+                                         (uint64_t)(uint32_t)total);
+    uint64_t prefix = 0;
+    if (vb > 0) {
+      prefix = lookback64_wave(scan_status, vb);
+      if (lane == 0)
+        status_store(&scan_status[vb], kFlagInc64 | (prefix + (uint32_t)total));
+    }
+    if (lane == 0) s_prefix = (int)prefix;
+  }
+  __syncthreads();
+  const int off = s_prefix + pre + inc - n;
+  if (gid < P.num_splats) splat_offsets[gid] = off;
+  if (gid == P.num_splats - 1) splat_offsets[P.num_splats] = off + n;
 }
 
 __global__ __launch_bounds__(kThreads) void emit_kernel(
     RasterParams P, const float4* __restrict__ packed,
-    const int32_t* __restrict__ splat_offsets, uint32_t* __restrict__ keys,
-    uint32_t* __restrict__ vals) {
-  const int gid = blockIdx.x * kThreads + threadIdx.x;
+    const int32_t* __restrict__ splat_offsets,
+    const int32_t* __restrict__ tile_counts, uint32_t* __restrict__ keys,
+    uint32_t* __restrict__ vals, int pair_passes, uint32_t* pair_ghist,
+    uint32_t* pair_status, int64_t pair_status_words) {
+  __shared__ uint32_t h[4][256];
+  const int t = threadIdx.x;
+  // (1) zero the pair sort's look-back status (grid-stride)
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + t; i < pair_status_words;
+       i += (int64_t)gridDim.x * kThreads)
+    pair_status[i] = 0u;
+  // (2) pair-sort digit histograms from this workgroup's slice of tiles
+  for (int i = t; i < 4 * 256; i += kThreads) (&h[0][0])[i] = 0u;
+  __syncthreads();
+  const int per = (P.num_tiles + gridDim.x - 1) / gridDim.x;
+  const int t0 = blockIdx.x * per;
+  const int t1 = min(P.num_tiles, t0 + per);
+  for (int tile = t0 + t; tile < t1; tile += kThreads) {
+    const uint32_t c = (uint32_t)tile_counts[tile];
+    if (c == 0u) continue;
+    for (int p = 0; p < pair_passes; ++p)
+      atomicAdd(&h[p][((uint32_t)tile >> (8 * p)) & 255u], c);
+  }
+  __syncthreads();
+  for (int p = 0; p < pair_passes; ++p) {
+    const uint32_t c = h[p][t];
+    if (c) atomicAdd(&pair_ghist[p * 256 + t], c);
+  }
+  // (3) pair emission
+  const int gid = blockIdx.x * kThreads + t;
   if (gid >= P.num_splats) return;
   const float4 p0 = packed[3 * gid + 0];
   const float4 p1 = packed[3 * gid + 1];
@@ -112,6 +180,16 @@ __global__ void fill_f32_kernel(float* dst, float v, int64_t n) {
   if (i < n) dst[i] = v;
 }
 
+// Zeroes two word ranges in one launch (grid-stride).
+__global__ void zero2_kernel(uint32_t* a, int64_t na, uint32_t* b, int64_t nb) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+       i < na || i < nb; i += stride) {
+    if (i < na) a[i] = 0u;
+    if (i < nb) b[i] = 0u;
+  }
+}
+
 // Zeroes the four per-splat gradient arrays (2n, 3n, 3n, n floats) in one
 // launch.
 __global__ void zero_grads_kernel(float* g_m, float* g_q, float* g_c,
@@ -130,26 +208,45 @@ __global__ void zero_grads_kernel(float* g_m, float* g_q, float* g_c,
 int launch_count_pack(const RasterParams& P, const float* means2d,
                       const float* conics, const float* colors,
                       const float* opacities, const uint32_t* perm,
-                      float* packed, int32_t* splat_counts,
-                      int32_t* tile_counts, hipStream_t stream) {
+                      float* packed, int32_t* splat_offsets,
+                      int32_t* tile_counts, uint64_t* scan_status,
+                      uint32_t* scan_ticket, hipStream_t stream) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
   hipLaunchKernelGGL(count_pack_kernel, dim3(grid), dim3(kThreads), 0, stream,
                      P, means2d, conics, colors, opacities, perm,
-                     reinterpret_cast<float4*>(packed), splat_counts,
-                     tile_counts);
+                     reinterpret_cast<float4*>(packed), splat_offsets,
+                     tile_counts, scan_status, scan_ticket);
   return check_launch("count_pack_kernel");
 }
 
+int count_scan_blocks(const RasterParams& P) {
+  return (P.num_splats + kThreads - 1) / kThreads;
+}
+
 int launch_emit(const RasterParams& P, const float* packed,
-                const int32_t* splat_offsets, uint32_t* keys, uint32_t* vals,
-                hipStream_t stream) {
+                const int32_t* splat_offsets, const int32_t* tile_counts,
+                uint32_t* keys, uint32_t* vals, int pair_passes,
+                uint32_t* pair_ghist, uint32_t* pair_status,
+                int64_t pair_status_words, hipStream_t stream) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
   hipLaunchKernelGGL(emit_kernel, dim3(grid), dim3(kThreads), 0, stream, P,
                      reinterpret_cast<const float4*>(packed), splat_offsets,
-                     keys, vals);
+                     tile_counts, keys, vals, pair_passes, pair_ghist,
+                     pair_status, pair_status_words);
   return check_launch("emit_kernel");
+}
+
+int launch_zero2(uint32_t* a, int64_t na, uint32_t* b, int64_t nb,
+                 hipStream_t stream) {
+  const int64_t n = na > nb ? na : nb;
+  if (n <= 0) return GSPLAT_OK;
+  int64_t grid = (n + 255) / 256;
+  if (grid > 4096) grid = 4096;
+  hipLaunchKernelGGL(zero2_kernel, dim3((unsigned)grid), dim3(256), 0, stream,
+                     a, na, b, nb);
+  return check_launch("zero2_kernel");
 }
 
 int launch_fill_i32(int32_t* dst, int32_t value, int64_t n,

@@ -100,29 +100,56 @@ int null_check(std::initializer_list<const void*> ptrs, const char* what) {
   return GSPLAT_OK;
 }
 
-size_t count_ws(const RasterParams& P) {
-  size_t a = gs::radix_sort_workspace_bytes(P.gpb, P.batch);
-  size_t b = gs::scan_workspace_bytes(P.num_splats);
-  size_t c = gs::scan_workspace_bytes(P.num_tiles);
-  size_t m = a > b ? a : b;
-  return m > c ? m : c;
+// Count-stage workspace: a zeroed control region (depth-sort control block,
+// count-scan look-back status and ticket, pair-sort histograms and tickets,
+// tile-offset scan status and ticket), then the depth sort's ping-pong
+// buffers.
+struct CountLayout {
+  gs::RadixPlan depth;
+  size_t scan_status, scan_ticket, pair_ghist, pair_tickets, ctl_end;
+  size_t depth_buffers, tile_scan, total;
+};
+
+CountLayout count_layout(const RasterParams& P) {
+  CountLayout L{};
+  L.depth = gs::radix_plan(P.gpb, P.batch, 0, 32);
+  size_t off = gs::radix_ctl_bytes(L.depth);
+  L.scan_status = off;
+  off += gs::align_up((size_t)gs::count_scan_blocks(P) * sizeof(uint64_t), 256);
+  L.scan_ticket = off;
+  off += 256;
+  L.pair_ghist = off;
+  off += 4 * 256 * sizeof(uint32_t);
+  L.pair_tickets = off;
+  off += 256;
+  L.tile_scan = off;
+  off += gs::scan_workspace_bytes(P.num_tiles);
+  L.ctl_end = off;
+  L.depth_buffers = off;
+  off += gs::align_up(L.depth.buffer_bytes, 256);
+  L.total = off;
+  return L;
 }
 
+// Emit-stage workspace: emitted keys and values, the pair sort's look-back
+// status, and its ping-pong buffers.
 struct EmitLayout {
-  size_t keys, vals, sort, total;
+  gs::RadixPlan pairs;
+  size_t keys, vals, status, buffers, total;
 };
 
 EmitLayout emit_layout(const RasterParams& P, int64_t n) {
   EmitLayout L{};
+  L.pairs = gs::radix_plan(n, 1, 0, bits_for((int64_t)P.num_tiles - 1));
   const size_t vec = gs::align_up((size_t)n * sizeof(uint32_t), 256);
   L.keys = 0;
   L.vals = vec;
-  L.sort = 2 * vec;
-  L.total = L.sort + gs::radix_sort_workspace_bytes(n, 1);
-  (void)P;
+  L.status = 2 * vec;
+  L.buffers =
+      L.status + gs::align_up((size_t)L.pairs.status_words * sizeof(uint32_t), 256);
+  L.total = L.buffers + L.pairs.buffer_bytes;
   return L;
 }
-
 }  // namespace
 
 extern "C" {
@@ -134,7 +161,7 @@ const char* gsplat_hip_last_error(void) { return gs::g_err; }
 size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta) {
   RasterParams P;
   if (make_params(meta, P)) return 0;
-  return count_ws(P);
+  return count_layout(P).total;
 }
 
 int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
@@ -148,31 +175,46 @@ int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
   int rc = make_params(meta, P);
   if (rc) return rc;
   rc = null_check({means2d, conics, colors, opacities, depths, perm, packed,
-                   splat_offsets, tile_counts, tile_offsets},
+                   splat_offsets, tile_counts, tile_offsets, workspace},
                   "gsplat_hip_bin_count");
   if (rc) return rc;
-  const size_t need = count_ws(P);
-  if (workspace_bytes < need || (need > 0 && workspace == nullptr)) {
+  const CountLayout L = count_layout(P);
+  if (workspace_bytes < L.total) {
     gs::set_error("gsplat_hip_bin_count: workspace too small (%zu < %zu)",
-                  workspace_bytes, need);
+                  workspace_bytes, L.total);
     return GSPLAT_ERR_WORKSPACE;
   }
+  if (!gs::radix_size_ok(P.gpb, P.batch)) {
+    gs::set_error("gsplat_hip_bin_count: too many splats per image");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  rc = gs::launch_fill_i32(tile_counts, 0, P.num_tiles, s);
-  if (rc) return rc;
-  rc = gs::radix_sort_pairs(nullptr, nullptr, depths, nullptr,
-                            reinterpret_cast<uint32_t*>(perm), P.gpb, P.batch,
-                            0, 32, workspace, workspace_bytes, s);
-  if (rc) return rc;
-  rc = gs::launch_count_pack(P, means2d, conics, colors, opacities,
-                             reinterpret_cast<const uint32_t*>(perm), packed,
-                             splat_offsets, tile_counts, s);
-  if (rc) return rc;
-  rc = gs::exclusive_scan_i32(splat_offsets, splat_offsets, P.num_splats,
-                              workspace, workspace_bytes, s);
-  if (rc) return rc;
-  return gs::exclusive_scan_i32(tile_counts, tile_offsets, P.num_tiles,
-                                workspace, workspace_bytes, s);
+  char* base = static_cast<char*>(workspace);
+  const gs::RadixCtl depth_ctl = gs::radix_ctl_at(L.depth, base);
+  // 1. zero the control region and the tile counters
+  rc = gs::launch_zero2(reinterpret_cast<uint32_t*>(base),
+                        (int64_t)(L.ctl_end / sizeof(uint32_t)),
+                        reinterpret_cast<uint32_t*>(tile_counts), P.num_tiles, s);
+  // 2. stable depth order per image (onesweep LSD over the 32 key bits)
+  if (!rc) rc = gs::radix_global_hist(L.depth, depth_ctl, nullptr, depths, s);
+  if (!rc)
+    rc = gs::radix_passes(L.depth, depth_ctl, base + L.depth_buffers, nullptr,
+                          nullptr, depths, nullptr,
+                          reinterpret_cast<uint32_t*>(perm), s);
+  // 3. pack + count + per-splat offsets
+  if (!rc)
+    rc = gs::launch_count_pack(
+        P, means2d, conics, colors, opacities,
+        reinterpret_cast<const uint32_t*>(perm), packed, splat_offsets,
+        tile_counts, reinterpret_cast<uint64_t*>(base + L.scan_status),
+        reinterpret_cast<uint32_t*>(base + L.scan_ticket), s);
+  // 4. tile ranges
+  if (!rc)
+    rc = gs::exclusive_scan_i32(tile_counts, tile_offsets, P.num_tiles,
+                                base + L.tile_scan,
+                                gs::scan_workspace_bytes(P.num_tiles), s,
+                                /*ctl_zeroed=*/true);
+  return rc;
 }
 
 size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
@@ -183,8 +225,10 @@ size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
 }
 
 int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
-                        const int32_t* splat_offsets, int64_t n_pairs,
-                        int32_t* binned_ids, void* workspace,
+                        const int32_t* splat_offsets,
+                        const int32_t* tile_counts, int64_t n_pairs,
+                        int32_t* binned_ids, void* count_workspace,
+                        size_t count_workspace_bytes, void* workspace,
                         size_t workspace_bytes, void* stream) {
   RasterParams P;
   int rc = make_params(meta, P);
@@ -195,26 +239,35 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
   if (n_pairs == 0) return GSPLAT_OK;
-  rc = null_check({packed, splat_offsets, binned_ids, workspace},
+  rc = null_check({packed, splat_offsets, tile_counts, binned_ids,
+                   count_workspace, workspace},
                   "gsplat_hip_bin_emit");
   if (rc) return rc;
+  const CountLayout C = count_layout(P);
   const EmitLayout L = emit_layout(P, n_pairs);
-  if (workspace_bytes < L.total) {
-    gs::set_error("gsplat_hip_bin_emit: workspace too small (%zu < %zu)",
-                  workspace_bytes, L.total);
+  if (count_workspace_bytes < C.total || workspace_bytes < L.total) {
+    gs::set_error("gsplat_hip_bin_emit: workspace too small (%zu < %zu or %zu < %zu)",
+                  count_workspace_bytes, C.total, workspace_bytes, L.total);
     return GSPLAT_ERR_WORKSPACE;
   }
+  if (!gs::radix_size_ok(n_pairs, 1)) {
+    gs::set_error("gsplat_hip_bin_emit: too many pairs");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  char* cbase = static_cast<char*>(count_workspace);
   char* base = static_cast<char*>(workspace);
   uint32_t* keys = reinterpret_cast<uint32_t*>(base + L.keys);
   uint32_t* vals = reinterpret_cast<uint32_t*>(base + L.vals);
-  rc = gs::launch_emit(P, packed, splat_offsets, keys, vals, s);
+  const gs::RadixCtl ctl{reinterpret_cast<uint32_t*>(cbase + C.pair_ghist),
+                         reinterpret_cast<uint32_t*>(base + L.status),
+                         reinterpret_cast<uint32_t*>(cbase + C.pair_tickets)};
+  rc = gs::launch_emit(P, packed, splat_offsets, tile_counts, keys, vals,
+                       L.pairs.passes, ctl.ghist, ctl.status,
+                       L.pairs.status_words, s);
   if (rc) return rc;
-  const int end_bit = bits_for((int64_t)P.num_tiles - 1);
-  return gs::radix_sort_pairs(keys, vals, nullptr, nullptr,
-                              reinterpret_cast<uint32_t*>(binned_ids), n_pairs,
-                              1, 0, end_bit, base + L.sort,
-                              workspace_bytes - L.sort, s);
+  return gs::radix_passes(L.pairs, ctl, base + L.buffers, keys, vals, nullptr,
+                          nullptr, reinterpret_cast<uint32_t*>(binned_ids), s);
 }
 
 int gsplat_hip_render_forward(const gsplat_raster_meta* meta,

@@ -37,13 +37,44 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // ---- scan (scan.hip)
 size_t scan_workspace_bytes(int64_t n);
+// ctl_zeroed: the workspace's look-back status and ticket are already zero
+// (otherwise they are zeroed by an extra launch).
 int exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n, void* ws,
-                       size_t ws_bytes, hipStream_t stream);
+                       size_t ws_bytes, hipStream_t stream,
+                       bool ctl_zeroed = false);
 
 // ---- radix sort (radix_sort.hip)
+// Layout of one sort: a control block (global digit histograms, look-back
+// status, tickets; must be zero before the sort, except that the histograms
+// may be filled by the caller) and ping-pong key/value buffers.
+struct RadixPlan {
+  int64_t n_seg;
+  int segments, nblk, passes, begin_bit, end_bit;
+  int64_t ghist_words, status_words, ticket_words;
+  size_t a_keys, a_vals, b_keys, b_vals, buffer_bytes;
+};
+struct RadixCtl {
+  uint32_t* ghist;    // [4][segments][256]
+  uint32_t* status;   // [passes][segments][nblk][256]
+  uint32_t* tickets;  // [4]
+};
+RadixPlan radix_plan(int64_t n_seg, int segments, int begin_bit, int end_bit);
+size_t radix_ctl_bytes(const RadixPlan& L);
+RadixCtl radix_ctl_at(const RadixPlan& L, void* p);
+bool radix_size_ok(int64_t n_seg, int segments);
 size_t radix_sort_workspace_bytes(int64_t n_per_segment, int segments);
-// key_from_depth: first pass derives keys from float depths (depth_src) and
-// values from the in-segment index.
+int launch_zero_u32(uint32_t* p, int64_t n, hipStream_t stream);
+// Fills C.ghist (zeroed) from the keys, or from float depths when depth_src.
+int radix_global_hist(const RadixPlan& L, const RadixCtl& C,
+                      const uint32_t* keys, const float* depth_src,
+                      hipStream_t stream);
+// One onesweep launch per pass.  depth_src: first pass derives keys from
+// float depths and values from the in-segment index.
+int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
+                 const uint32_t* keys_in, const uint32_t* vals_in,
+                 const float* depth_src, uint32_t* keys_out,
+                 uint32_t* vals_out, hipStream_t stream);
+// Self-contained sort (zeroes its control block, computes the histograms).
 int radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in,
                      const float* depth_src, uint32_t* keys_out,
                      uint32_t* vals_out, int64_t n_per_segment, int segments,
@@ -51,14 +82,25 @@ int radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in,
                      hipStream_t stream);
 
 // ---- binning (binning.hip)
+// count_pack: packs records, counts tile hits, bumps tile_counts (zeroed)
+// and writes splat_offsets[0..BG] via a look-back scan whose status
+// (count_scan_blocks(P) words) and ticket must be zero.
 int launch_count_pack(const RasterParams& P, const float* means2d,
                       const float* conics, const float* colors,
                       const float* opacities, const uint32_t* perm,
-                      float* packed, int32_t* splat_counts,
-                      int32_t* tile_counts, hipStream_t stream);
+                      float* packed, int32_t* splat_offsets,
+                      int32_t* tile_counts, uint64_t* scan_status,
+                      uint32_t* scan_ticket, hipStream_t stream);
+int count_scan_blocks(const RasterParams& P);
+// emit: writes (tile, gid) pairs; also zeroes pair_status and adds the
+// pair sort's per-pass digit histograms into pair_ghist (zeroed).
 int launch_emit(const RasterParams& P, const float* packed,
-                const int32_t* splat_offsets, uint32_t* keys, uint32_t* vals,
-                hipStream_t stream);
+                const int32_t* splat_offsets, const int32_t* tile_counts,
+                uint32_t* keys, uint32_t* vals, int pair_passes,
+                uint32_t* pair_ghist, uint32_t* pair_status,
+                int64_t pair_status_words, hipStream_t stream);
+int launch_zero2(uint32_t* a, int64_t na, uint32_t* b, int64_t nb,
+                 hipStream_t stream);
 int launch_fill_i32(int32_t* dst, int32_t value, int64_t n, hipStream_t stream);
 int launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream);
 int launch_zero_grads(float* g_m, float* g_q, float* g_c, float* g_o,

@@ -100,12 +100,32 @@ __device__ __forceinline__ float quad_form(float a, float b, float c, float dx,
   return a * dx * dx + 2.0f * b * dx * dy + c * dy * dy;
 }
 
+// Per-splat constants of the rectangle test: the slopes -(b/c) and -(b/a) of
+// the lines where the quadratic is minimal along x = const and y = const.
+struct ConicSlopes {
+  float kc, ka;
+  bool use_c, use_a;
+};
+
+__device__ __forceinline__ ConicSlopes conic_slopes(float a, float b,
+                                                    float c) {
+#pragma clang fp contract(off)
+  ConicSlopes s;
+  s.use_c = c > 1e-8f;
+  s.use_a = a > 1e-8f;
+  s.kc = s.use_c ? -(b / c) : 0.0f;
+  s.ka = s.use_a ? -(b / a) : 0.0f;
+  return s;
+}
+
 // Exact minimum of the conic quadratic over the axis-aligned rectangle of
 // pixel centres [rx0,rx1]x[ry0,ry1] compared against tau.
 __device__ __forceinline__ bool ellipse_hits_rect(float mx, float my, float a,
-                                                  float b, float c, float tau,
-                                                  float rx0, float ry0,
-                                                  float rx1, float ry1) {
+                                                  float b, float c,
+                                                  const ConicSlopes& k,
+                                                  float tau, float rx0,
+                                                  float ry0, float rx1,
+                                                  float ry1) {
 #pragma clang fp contract(off)
   if (mx >= rx0 && mx <= rx1 && my >= ry0 && my <= ry1) return true;
   const float dx0 = rx0 - mx, dx1 = rx1 - mx;
@@ -114,18 +134,16 @@ __device__ __forceinline__ bool ellipse_hits_rect(float mx, float my, float a,
   q = fminf(q, quad_form(a, b, c, dx0, dy1));
   q = fminf(q, quad_form(a, b, c, dx1, dy0));
   q = fminf(q, quad_form(a, b, c, dx1, dy1));
-  if (c > 1e-8f) {
-    const float k = -(b / c);
-    float dy = fminf(fmaxf(k * dx0, dy0), dy1);
+  if (k.use_c) {
+    float dy = fminf(fmaxf(k.kc * dx0, dy0), dy1);
     q = fminf(q, quad_form(a, b, c, dx0, dy));
-    dy = fminf(fmaxf(k * dx1, dy0), dy1);
+    dy = fminf(fmaxf(k.kc * dx1, dy0), dy1);
     q = fminf(q, quad_form(a, b, c, dx1, dy));
   }
-  if (a > 1e-8f) {
-    const float k = -(b / a);
-    float dx = fminf(fmaxf(k * dy0, dx0), dx1);
+  if (k.use_a) {
+    float dx = fminf(fmaxf(k.ka * dy0, dx0), dx1);
     q = fminf(q, quad_form(a, b, c, dx, dy0));
-    dx = fminf(fmaxf(k * dy1, dx0), dx1);
+    dx = fminf(fmaxf(k.ka * dy1, dx0), dx1);
     q = fminf(q, quad_form(a, b, c, dx, dy1));
   }
   return q <= tau;

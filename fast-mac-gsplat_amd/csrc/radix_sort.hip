@@ -1,24 +1,21 @@
 // radix_sort.hip -- stable LSD radix sort of (uint32 key, uint32 value) pairs
 // with 8-bit digits, independently inside equal-length segments.
 //
-// Each pass is three launches with no inter-workgroup waiting:
-//   1. rs_hist_kernel    per 4096-element block, digit counts
-//                        -> hist[(segment*256 + digit)*nblk + block]
-//   2. exclusive scan of hist (flattened), which yields for every
-//      (segment, digit, block) the absolute output position of that block's
-//      first element with that digit (segments are contiguous and equal, so
-//      the flattened scan already includes segment*n)
-//   3. rs_scatter_kernel recomputes stable in-block ranks, stages the block
-//      in LDS in sorted order and writes it out so that each digit's run is a
-//      contiguous, coalesced store.
+// One launch per digit pass ("onesweep"): the global digit histogram of every
+// pass is known before the first pass (rs_global_hist_kernel, or supplied by
+// the caller), so a workgroup only needs the counts of the workgroups before
+// it in its segment, which it gets by decoupled look-back (lookback.h).
 //
-// In-block ranking is wave-level: every wave owns 1024 consecutive elements
-// and walks them 64 at a time; lanes holding the same digit are found with
-// eight ballots ("match"), the rank is the popcount of matching lower lanes,
-// and one leader lane per digit bumps the wave's running count.  Order
-// inside a block is (wave, round, lane), which is input order, so the sort
-// is stable.
+// Inside a workgroup (256 lanes, 4096 elements) each wavefront owns 1024
+// consecutive elements and ranks them 64 at a time: lanes holding the same
+// digit are found with one ballot per digit bit ("match"), the rank is the
+// popcount of matching lower lanes, and one leader lane per digit bumps the
+// wave's running count in LDS.  Element order inside a workgroup is therefore
+// (wave, round, lane) = input order, which makes the sort stable.  The block
+// is then staged in LDS in sorted order and written out so that each digit's
+// run is one contiguous, coalesced store.
 #include "gs_internal.h"
+#include "lookback.h"
 
 namespace gs {
 namespace {
@@ -59,50 +56,73 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active,
 struct PassArgs {
   const uint32_t* keys_in;   // nullptr when depth_src is used
   const uint32_t* vals_in;   // nullptr -> in-segment index
-  const float* depth_src;    // nullptr unless first pass of a depth sort
+  const float* depth_src;    // non-null only for the first pass of a depth sort
   uint32_t* keys_out;        // nullptr -> keys not written (last pass)
   uint32_t* vals_out;
   int64_t n_seg;
-  int nblk;                  // blocks per segment
+  int nblk;                  // workgroups per segment
+  int segments;
   int shift;
   int digit_bits;
+  const uint32_t* ghist;     // [segments][256] global digit counts of this pass
+  uint32_t* status;          // [segments][nblk][256], zeroed
+  uint32_t* ticket;          // zeroed
 };
 
 __device__ __forceinline__ uint32_t load_key(const PassArgs& a, int64_t idx) {
   return a.depth_src ? depth_key(a.depth_src[idx]) : a.keys_in[idx];
 }
 
-__global__ __launch_bounds__(kThreads) void rs_hist_kernel(PassArgs a,
-                                                           uint32_t* hist) {
-  __shared__ uint32_t cnt[kWaves][256];
-  const int seg = blockIdx.x / a.nblk;
-  const int blk = blockIdx.x - seg * a.nblk;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  for (int i = t; i < kWaves * 256; i += kThreads) (&cnt[0][0])[i] = 0u;
-  __syncthreads();
-  const int64_t seg_base = (int64_t)seg * a.n_seg;
-  const int64_t lo = (int64_t)blk * kBlockItems + (int64_t)wave * kWaveItems;
-  const uint32_t dmask = (1u << a.digit_bits) - 1u;
-  for (int r = 0; r < kRounds; ++r) {
-    const int64_t j = lo + r * 64 + lane;
-    const bool valid = j < a.n_seg;
-    const uint64_t act = __ballot(valid);
-    if (act == 0ull) break;
-    const uint32_t key = valid ? load_key(a, seg_base + j) : 0u;
-    const uint32_t d = (key >> a.shift) & dmask;
-    const uint64_t peers = match_digit(d, act, a.digit_bits);
-    if (valid && (peers & lanemask_lt()) == 0ull)
-      cnt[wave][d] += (uint32_t)__popcll(peers);
-    // Other lanes read these counters next round: keep LDS ops in order.
-    __builtin_amdgcn_wave_barrier();
+// Exclusive scan of one value per thread over the 256-thread block.
+__device__ __forceinline__ uint32_t block_excl_scan256(uint32_t v,
+                                                       uint32_t* wsum) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += y;
   }
+  if (lane == 63) wsum[wave] = inc;
   __syncthreads();
-  const uint32_t total = cnt[0][t] + cnt[1][t] + cnt[2][t] + cnt[3][t];
-  hist[((int64_t)seg * 256 + t) * a.nblk + blk] = total;
+  uint32_t pre = 0u;
+  for (int w = 0; w < wave; ++w) pre += wsum[w];
+  __syncthreads();
+  return pre + inc - v;
 }
 
-__global__ __launch_bounds__(kThreads) void rs_scatter_kernel(
-    PassArgs a, const uint32_t* __restrict__ offs) {
+// Per-pass global digit histograms: ghist[(p*segments + seg)*256 + d] (zeroed
+// by the caller) for passes p = 0..passes-1 with digits at begin_bit + 8p.
+__global__ __launch_bounds__(kThreads) void rs_global_hist_kernel(
+    const uint32_t* keys, const float* depth_src, int64_t n_seg, int nblk,
+    int segments, int begin_bit, int end_bit, int passes, uint32_t* ghist) {
+  __shared__ uint32_t h[4][256];
+  const int seg = blockIdx.x / nblk;
+  const int blk = blockIdx.x - seg * nblk;
+  const int t = threadIdx.x;
+  for (int i = t; i < 4 * 256; i += kThreads) (&h[0][0])[i] = 0u;
+  __syncthreads();
+  const int64_t base = (int64_t)seg * n_seg;
+  const int64_t lo = (int64_t)blk * kBlockItems;
+  for (int i = t; i < kBlockItems; i += kThreads) {
+    const int64_t j = lo + i;
+    if (j >= n_seg) break;
+    const uint32_t key =
+        depth_src ? depth_key(depth_src[base + j]) : keys[base + j];
+    for (int p = 0; p < passes; ++p) {
+      const int sh = begin_bit + 8 * p;
+      const int bits = min(8, end_bit - sh);
+      atomicAdd(&h[p][(key >> sh) & ((1u << bits) - 1u)], 1u);
+    }
+  }
+  __syncthreads();
+  for (int p = 0; p < passes; ++p) {
+    const uint32_t c = h[p][t];
+    if (c) atomicAdd(&ghist[((int64_t)p * segments + seg) * 256 + t], c);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   __shared__ uint32_t cnt[kWaves][256];
   __shared__ uint32_t dstart[256];
   __shared__ uint32_t gbase[256];
@@ -110,66 +130,65 @@ __global__ __launch_bounds__(kThreads) void rs_scatter_kernel(
   __shared__ uint32_t sk[kBlockItems];
   __shared__ uint32_t sv[kBlockItems];
 
-  const int seg = blockIdx.x / a.nblk;
-  const int blk = blockIdx.x - seg * a.nblk;
+  const int vb = take_ticket(a.ticket);
+  const int seg = vb / a.nblk;
+  const int blk = vb - seg * a.nblk;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   for (int i = t; i < kWaves * 256; i += kThreads) (&cnt[0][0])[i] = 0u;
-  __syncthreads();
 
   const int64_t seg_base = (int64_t)seg * a.n_seg;
   const int64_t lo = (int64_t)blk * kBlockItems + (int64_t)wave * kWaveItems;
   const uint32_t dmask = (1u << a.digit_bits) - 1u;
+
+  // Issue every load of this lane's 16 elements before ranking any of them.
   uint32_t kreg[kRounds], vreg[kRounds], rreg[kRounds];
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int64_t j = lo + r * 64 + lane;
+    const bool valid = j < a.n_seg;
+    kreg[r] = valid ? load_key(a, seg_base + j) : 0u;
+    vreg[r] = valid ? (a.vals_in ? a.vals_in[seg_base + j] : (uint32_t)j) : 0u;
+  }
+  __syncthreads();
+
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     const int64_t j = lo + r * 64 + lane;
     const bool valid = j < a.n_seg;
     const uint64_t act = __ballot(valid);
     rreg[r] = 0xffffffffu;
-    kreg[r] = 0u;
-    vreg[r] = 0u;
     if (act != 0ull) {
-      const uint32_t key = valid ? load_key(a, seg_base + j) : 0u;
-      const uint32_t val =
-          valid ? (a.vals_in ? a.vals_in[seg_base + j] : (uint32_t)j) : 0u;
-      const uint32_t d = (key >> a.shift) & dmask;
+      const uint32_t d = (kreg[r] >> a.shift) & dmask;
       const uint64_t peers = match_digit(d, act, a.digit_bits);
       const uint32_t below = (uint32_t)__popcll(peers & lanemask_lt());
       const uint32_t old = valid ? cnt[wave][d] : 0u;
       if (valid && below == 0u) cnt[wave][d] = old + (uint32_t)__popcll(peers);
+      // Other lanes read these counters next round: keep LDS ops in order.
       __builtin_amdgcn_wave_barrier();
-      if (valid) {
-        kreg[r] = key;
-        vreg[r] = val;
-        rreg[r] = (old + below) | (d << 16);
-      }
+      if (valid) rreg[r] = (old + below) | (d << 16);
     }
   }
   __syncthreads();
 
-  // Thread t owns digit t: exclusive prefix across waves, block-local digit
-  // start (exclusive scan over digits) and the global base for this block.
-  {
-    const uint32_t c0 = cnt[0][t], c1 = cnt[1][t], c2 = cnt[2][t],
-                   c3 = cnt[3][t];
-    const uint32_t tot = c0 + c1 + c2 + c3;
-    cnt[0][t] = 0u;
-    cnt[1][t] = c0;
-    cnt[2][t] = c0 + c1;
-    cnt[3][t] = c0 + c1 + c2;
-    uint32_t inc = tot;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t y = __shfl_up(inc, off, 64);
-      if (lane >= off) inc += y;
-    }
-    if (lane == 63) wsum[wave] = inc;
-    __syncthreads();
-    uint32_t wprefix = 0u;
-    for (int w = 0; w < wave; ++w) wprefix += wsum[w];
-    dstart[t] = wprefix + inc - tot;
-    gbase[t] = offs[((int64_t)seg * 256 + t) * a.nblk + blk];
+  // Thread t owns digit t.
+  const uint32_t c0 = cnt[0][t], c1 = cnt[1][t], c2 = cnt[2][t], c3 = cnt[3][t];
+  const uint32_t tot = c0 + c1 + c2 + c3;
+  uint32_t* my_status = a.status + ((int64_t)seg * a.nblk + blk) * 256 + t;
+  status_store(my_status, (blk == 0 ? kFlagInc32 : kFlagAgg32) | tot);
+  cnt[0][t] = 0u;
+  cnt[1][t] = c0;
+  cnt[2][t] = c0 + c1;
+  cnt[3][t] = c0 + c1 + c2;
+  const uint32_t gh = a.ghist[(int64_t)seg * 256 + t];
+  const uint32_t dbase = block_excl_scan256(gh, wsum);
+  const uint32_t local = block_excl_scan256(tot, wsum);
+  uint32_t prefix = 0u;
+  if (blk > 0) {
+    prefix = lookback32(a.status + (int64_t)seg * a.nblk * 256 + t, blk, 256);
+    status_store(my_status, kFlagInc32 | (prefix + tot));
   }
+  dstart[t] = local;
+  gbase[t] = dbase + prefix;
   __syncthreads();
 
 #pragma unroll
@@ -188,7 +207,7 @@ __global__ __launch_bounds__(kThreads) void rs_scatter_kernel(
   for (int i = t; i < count; i += kThreads) {
     const uint32_t key = sk[i];
     const uint32_t d = (key >> a.shift) & dmask;
-    const int64_t dst = (int64_t)gbase[d] + (int64_t)(i - (int)dstart[d]);
+    const int64_t dst = seg_base + (int64_t)gbase[d] + (int64_t)(i - (int)dstart[d]);
     if (a.keys_out) a.keys_out[dst] = key;
     a.vals_out[dst] = sv[i];
   }
@@ -203,43 +222,126 @@ __global__ void rs_copy_kernel(PassArgs a, int64_t n_total) {
   a.vals_out[i] = a.vals_in ? a.vals_in[i] : (uint32_t)j;
 }
 
-struct WsLayout {
-  size_t a_keys, a_vals, b_keys, b_vals, hist, scan, total;
-};
-
-WsLayout layout(int64_t n_seg, int segments, int passes) {
-  const int64_t n = n_seg * (int64_t)segments;
-  const int64_t nblk = (n_seg + kBlockItems - 1) / kBlockItems;
-  const int64_t entries = (int64_t)segments * 256 * nblk;
-  WsLayout L{};
-  size_t off = 0;
-  const size_t vec = align_up((size_t)n * sizeof(uint32_t), 256);
-  if (passes >= 2) {
-    L.a_keys = off; off += vec;
-    L.a_vals = off; off += vec;
-  }
-  if (passes >= 3) {
-    L.b_keys = off; off += vec;
-    L.b_vals = off; off += vec;
-  }
-  L.hist = off;
-  off += align_up((size_t)(entries + 1) * sizeof(uint32_t), 256);
-  L.scan = off;
-  off += scan_workspace_bytes(entries);
-  L.total = off;
-  return L;
-}
-
-int num_passes(int begin_bit, int end_bit) {
-  return end_bit > begin_bit ? (end_bit - begin_bit + 7) / 8 : 0;
+__global__ void zero_u32_kernel(uint32_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
 }
 
 }  // namespace
 
+RadixPlan radix_plan(int64_t n_seg, int segments, int begin_bit, int end_bit) {
+  RadixPlan L{};
+  L.n_seg = n_seg;
+  L.segments = segments;
+  L.begin_bit = begin_bit;
+  L.end_bit = end_bit;
+  L.passes = end_bit > begin_bit ? (end_bit - begin_bit + 7) / 8 : 0;
+  L.nblk = (int)((n_seg + kBlockItems - 1) / kBlockItems);
+  L.ghist_words = (int64_t)4 * segments * 256;
+  L.status_words = (int64_t)(L.passes > 0 ? L.passes : 1) * segments * L.nblk * 256;
+  L.ticket_words = 4;
+  const int64_t n = n_seg * (int64_t)segments;
+  const size_t vec = align_up((size_t)n * sizeof(uint32_t), 256);
+  size_t off = 0;
+  L.a_keys = L.a_vals = L.b_keys = L.b_vals = 0;
+  if (L.passes >= 2) {
+    L.a_keys = off; off += vec;
+    L.a_vals = off; off += vec;
+  }
+  if (L.passes >= 3) {
+    L.b_keys = off; off += vec;
+    L.b_vals = off; off += vec;
+  }
+  L.buffer_bytes = off;
+  return L;
+}
+
+size_t radix_ctl_bytes(const RadixPlan& L) {
+  return align_up((size_t)(L.ghist_words + L.status_words + L.ticket_words) *
+                      sizeof(uint32_t), 256);
+}
+
+RadixCtl radix_ctl_at(const RadixPlan& L, void* p) {
+  uint32_t* w = static_cast<uint32_t*>(p);
+  return RadixCtl{w, w + L.ghist_words, w + L.ghist_words + L.status_words};
+}
+
 size_t radix_sort_workspace_bytes(int64_t n_per_segment, int segments) {
-  // Worst case: 4 passes over 32 bits.
   if (n_per_segment <= 0 || segments <= 0) return 0;
-  return layout(n_per_segment, segments, 4).total;
+  const RadixPlan L = radix_plan(n_per_segment, segments, 0, 32);
+  return radix_ctl_bytes(L) + L.buffer_bytes;
+}
+
+int launch_zero_u32(uint32_t* p, int64_t n, hipStream_t stream) {
+  if (n <= 0) return GSPLAT_OK;
+  int64_t grid = (n + 255) / 256;
+  if (grid > 2048) grid = 2048;
+  hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     stream, p, n);
+  return check_launch("zero_u32_kernel");
+}
+
+int radix_global_hist(const RadixPlan& L, const RadixCtl& C,
+                      const uint32_t* keys, const float* depth_src,
+                      hipStream_t stream) {
+  if (L.passes == 0 || L.n_seg == 0 || L.segments == 0) return GSPLAT_OK;
+  hipLaunchKernelGGL(rs_global_hist_kernel,
+                     dim3((unsigned)(L.nblk * (int64_t)L.segments)),
+                     dim3(kThreads), 0, stream, keys, depth_src, L.n_seg,
+                     L.nblk, L.segments, L.begin_bit, L.end_bit, L.passes,
+                     C.ghist);
+  return check_launch("rs_global_hist_kernel");
+}
+
+int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
+                 const uint32_t* keys_in, const uint32_t* vals_in,
+                 const float* depth_src, uint32_t* keys_out,
+                 uint32_t* vals_out, hipStream_t stream) {
+  if (L.n_seg == 0 || L.segments == 0) return GSPLAT_OK;
+  char* base = static_cast<char*>(buffers);
+  const int64_t n = L.n_seg * L.segments;
+  if (L.passes == 0) {
+    PassArgs a{keys_in, vals_in, depth_src, keys_out, vals_out, L.n_seg,
+               L.nblk, L.segments, 0, 0, nullptr, nullptr, nullptr};
+    hipLaunchKernelGGL(rs_copy_kernel, dim3((unsigned)((n + 255) / 256)),
+                       dim3(256), 0, stream, a, n);
+    return check_launch("rs_copy_kernel");
+  }
+  uint32_t* bufk[2] = {reinterpret_cast<uint32_t*>(base + L.a_keys),
+                       reinterpret_cast<uint32_t*>(base + L.b_keys)};
+  uint32_t* bufv[2] = {reinterpret_cast<uint32_t*>(base + L.a_vals),
+                       reinterpret_cast<uint32_t*>(base + L.b_vals)};
+  const int64_t status_per_pass = (int64_t)L.segments * L.nblk * 256;
+  const uint32_t* cur_k = keys_in;
+  const uint32_t* cur_v = vals_in;
+  const float* cur_depth = depth_src;
+  for (int p = 0; p < L.passes; ++p) {
+    const int shift = L.begin_bit + 8 * p;
+    const int bits = (L.end_bit - shift) < 8 ? (L.end_bit - shift) : 8;
+    const bool last = (p == L.passes - 1);
+    uint32_t* out_k = last ? keys_out : bufk[p & 1];
+    uint32_t* out_v = last ? vals_out : bufv[p & 1];
+    PassArgs a{cur_k, cur_v, cur_depth, out_k, out_v, L.n_seg, L.nblk,
+               L.segments, shift, bits,
+               C.ghist + (int64_t)p * L.segments * 256,
+               C.status + p * status_per_pass, C.tickets + p};
+    hipLaunchKernelGGL(rs_onesweep_kernel,
+                       dim3((unsigned)(L.nblk * (int64_t)L.segments)),
+                       dim3(kThreads), 0, stream, a);
+    const int rc = check_launch("rs_onesweep_kernel");
+    if (rc) return rc;
+    cur_k = out_k;
+    cur_v = out_v;
+    cur_depth = nullptr;
+  }
+  return GSPLAT_OK;
+}
+
+bool radix_size_ok(int64_t n_seg, int segments) {
+  const int64_t nblk = (n_seg + kBlockItems - 1) / kBlockItems;
+  return nblk * segments <= 0x7fffffffLL && n_seg <= (int64_t(1) << 29) &&
+         n_seg * segments <= 0x7fffffffLL;
 }
 
 int radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in,
@@ -253,64 +355,25 @@ int radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in,
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
   if (n_seg == 0 || segments == 0) return GSPLAT_OK;
-  const int64_t nblk = (n_seg + kBlockItems - 1) / kBlockItems;
-  if (nblk * segments > 0x7fffffffLL || n_seg * segments > 0x7fffffffLL) {
+  if (!radix_size_ok(n_seg, segments)) {
     set_error("radix_sort: input too large");
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
-  const int passes = num_passes(begin_bit, end_bit);
-  const int64_t n = n_seg * segments;
-  if (passes == 0) {
-    PassArgs a{keys_in, vals_in, depth_src, keys_out, vals_out, n_seg, (int)nblk,
-               0, 0};
-    const int64_t grid = (n + 255) / 256;
-    hipLaunchKernelGGL(rs_copy_kernel, dim3((unsigned)grid), dim3(256), 0,
-                       stream, a, n);
-    return check_launch("rs_copy_kernel");
-  }
-  const WsLayout L = layout(n_seg, segments, passes);
-  if (ws == nullptr || ws_bytes < L.total) {
-    set_error("radix_sort: workspace too small (%zu < %zu)", ws_bytes, L.total);
+  const RadixPlan L = radix_plan(n_seg, segments, begin_bit, end_bit);
+  const size_t ctl = radix_ctl_bytes(L);
+  if (L.passes > 0 && (ws == nullptr || ws_bytes < ctl + L.buffer_bytes)) {
+    set_error("radix_sort: workspace too small (%zu < %zu)", ws_bytes,
+              ctl + L.buffer_bytes);
     return GSPLAT_ERR_WORKSPACE;
   }
-  char* base = static_cast<char*>(ws);
-  uint32_t* bufk[2] = {reinterpret_cast<uint32_t*>(base + L.a_keys),
-                       reinterpret_cast<uint32_t*>(base + L.b_keys)};
-  uint32_t* bufv[2] = {reinterpret_cast<uint32_t*>(base + L.a_vals),
-                       reinterpret_cast<uint32_t*>(base + L.b_vals)};
-  uint32_t* hist = reinterpret_cast<uint32_t*>(base + L.hist);
-  void* scan_ws = base + L.scan;
-  const int64_t entries = (int64_t)segments * 256 * nblk;
-  const unsigned grid = (unsigned)(nblk * segments);
-
-  const uint32_t* cur_k = keys_in;
-  const uint32_t* cur_v = vals_in;
-  const float* cur_depth = depth_src;
-  for (int p = 0; p < passes; ++p) {
-    const int shift = begin_bit + 8 * p;
-    const int bits = (end_bit - shift) < 8 ? (end_bit - shift) : 8;
-    const bool last = (p == passes - 1);
-    uint32_t* out_k = last ? keys_out : bufk[p & 1];
-    uint32_t* out_v = last ? vals_out : bufv[p & 1];
-    PassArgs a{cur_k, cur_v, cur_depth, out_k, out_v, n_seg, (int)nblk, shift,
-               bits};
-    hipLaunchKernelGGL(rs_hist_kernel, dim3(grid), dim3(kThreads), 0, stream,
-                       a, hist);
-    int rc = check_launch("rs_hist_kernel");
+  const RadixCtl C = radix_ctl_at(L, ws);
+  if (L.passes > 0) {
+    int rc = launch_zero_u32(C.ghist, (int64_t)(ctl / sizeof(uint32_t)), stream);
+    if (!rc) rc = radix_global_hist(L, C, keys_in, depth_src, stream);
     if (rc) return rc;
-    rc = exclusive_scan_i32(reinterpret_cast<const int32_t*>(hist),
-                            reinterpret_cast<int32_t*>(hist), entries, scan_ws,
-                            scan_workspace_bytes(entries), stream);
-    if (rc) return rc;
-    hipLaunchKernelGGL(rs_scatter_kernel, dim3(grid), dim3(kThreads), 0,
-                       stream, a, hist);
-    rc = check_launch("rs_scatter_kernel");
-    if (rc) return rc;
-    cur_k = out_k;
-    cur_v = out_v;
-    cur_depth = nullptr;
   }
-  return GSPLAT_OK;
+  return radix_passes(L, C, static_cast<char*>(ws) + ctl, keys_in, vals_in,
+                      depth_src, keys_out, vals_out, stream);
 }
 
 }  // namespace gs

@@ -1,170 +1,121 @@
-// scan.hip -- device-wide exclusive prefix sum over int32.
+// scan.hip -- device-wide exclusive prefix sum over int32 in one launch.
 //
-// Small inputs (<= kSingleMax) use one 1024-thread workgroup that walks the
-// array in 8192-element chunks with a running carry (one launch).  Larger
-// inputs use reduce-then-scan: per-chunk sums, a single-workgroup scan of the
-// chunk sums, and a rescan of each chunk with its carry (three launches, no
-// inter-workgroup waiting).
+// Workgroups of 256 lanes each scan 4096 consecutive elements (coalesced
+// loads into LDS, 16 consecutive elements per lane, a workgroup scan of the
+// lane sums) and obtain the total of all earlier workgroups by decoupled
+// look-back (lookback.h).  The look-back status (one 64-bit word per
+// workgroup) and the ticket live in the caller's workspace and must be zero;
+// exclusive_scan_i32 zeroes them unless told they already are.
 #include "gs_internal.h"
+#include "lookback.h"
 
 namespace gs {
 namespace {
 
-constexpr int kThreads = 1024;
-constexpr int kItems = 8;
-constexpr int kChunk = kThreads * kItems;   // 8192
-constexpr int64_t kSingleMax = 1 << 18;
+constexpr int kThreads = 256;
+constexpr int kItems = 16;
+constexpr int kChunk = kThreads * kItems;   // 4096
+constexpr int kPadded = kChunk + kChunk / 16;
 
-__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
-  return x;
-}
+__device__ __forceinline__ int pad(int j) { return j + (j >> 4); }
 
-// Exclusive scan of one value per thread across the 1024-thread block.
-// Returns the exclusive prefix; *total receives the block sum.
-__device__ __forceinline__ int block_exclusive_scan(int v, int* wave_sums,
-                                                    int* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int inc = wave_inclusive_scan(v, lane);
-  if (lane == 63) wave_sums[wave] = inc;
-  __syncthreads();
-  if (wave == 0) {
-    const int w = (lane < kThreads / 64) ? wave_sums[lane] : 0;
-    const int winc = wave_inclusive_scan(w, lane);
-    if (lane < kThreads / 64) wave_sums[lane] = winc - w;   // exclusive
-    if (lane == kThreads / 64 - 1) wave_sums[kThreads / 64] = winc;
-  }
-  __syncthreads();
-  const int r = wave_sums[wave] + inc - v;
-  *total = wave_sums[kThreads / 64];
-  __syncthreads();
-  return r;
-}
-
-// Scans chunk [base, base+kChunk) of `in` into `out` with the given carry.
-// Returns the chunk's sum.
-__device__ __forceinline__ int scan_chunk(const int32_t* in, int32_t* out,
-                                          int64_t n, int64_t base, int carry,
-                                          int* sh, int* wave_sums) {
-  const int t = threadIdx.x;
+__global__ __launch_bounds__(kThreads) void scan_lookback_kernel(
+    const int32_t* in, int32_t* out, int64_t n, uint64_t* status,
+    uint32_t* ticket) {
+  __shared__ int sh[kPadded];
+  __shared__ int wsum[kThreads / 64];
+  __shared__ int64_t s_prefix;
+  const int vb = take_ticket(ticket);
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t base = (int64_t)vb * kChunk;
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = base + (int64_t)i * kThreads + t;
-    sh[i * kThreads + t] = (idx < n) ? in[idx] : 0;
+    const int j = i * kThreads + t;
+    sh[pad(j)] = (base + j < n) ? in[base + j] : 0;
   }
   __syncthreads();
-  int vals[kItems];
+  int v[kItems];
   int sum = 0;
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    vals[i] = sh[t * kItems + i];
-    sum += vals[i];
+  for (int k = 0; k < kItems; ++k) {
+    v[k] = sh[pad(t * kItems + k)];
+    sum += v[k];
   }
-  int total;
-  int run = block_exclusive_scan(sum, wave_sums, &total) + carry;
+  int inc = sum;
 #pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    sh[t * kItems + i] = run;
-    run += vals[i];
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += y;
+  }
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  int pre = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) {
+    pre += (w < wave) ? wsum[w] : 0;
+    total += wsum[w];
+  }
+  if (wave == 0) {
+    if (lane == 0)
+      status_store(&status[vb], (vb == 0 ? kFlagInc64 : kFlagAgg64) |
+                                    (uint64_t)(uint32_t)total);
+    uint64_t prefix = 0ull;
+    if (vb > 0) {
+      prefix = lookback64_wave(status, vb);
+      if (lane == 0)
+        status_store(&status[vb], kFlagInc64 | (prefix + (uint32_t)total));
+    }
+    if (lane == 0) s_prefix = (int64_t)prefix;
+  }
+  __syncthreads();
+  int run = (int)s_prefix + pre + inc - sum;
+#pragma unroll
+  for (int k = 0; k < kItems; ++k) {
+    sh[pad(t * kItems + k)] = run;
+    run += v[k];
   }
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = base + (int64_t)i * kThreads + t;
-    if (idx < n) out[idx] = sh[i * kThreads + t];
+    const int j = i * kThreads + t;
+    if (base + j < n) out[base + j] = sh[pad(j)];
   }
-  __syncthreads();
-  return total;
-}
-
-__global__ __launch_bounds__(kThreads) void scan_single_kernel(
-    const int32_t* in, int32_t* out, int64_t n) {
-  __shared__ int sh[kChunk];
-  __shared__ int wave_sums[kThreads / 64 + 1];
-  int carry = 0;
-  for (int64_t base = 0; base < n; base += kChunk) {
-    carry += scan_chunk(in, out, n, base, carry, sh, wave_sums);
-  }
-  if (threadIdx.x == 0) out[n] = carry;
-}
-
-__global__ __launch_bounds__(kThreads) void chunk_sum_kernel(
-    const int32_t* in, int64_t n, int32_t* partial) {
-  __shared__ int wave_sums[kThreads / 64];
-  const int64_t base = (int64_t)blockIdx.x * kChunk;
-  int s = 0;
-#pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const int64_t idx = base + (int64_t)i * kThreads + threadIdx.x;
-    if (idx < n) s += in[idx];
-  }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-  if (lane == 0) wave_sums[wave] = s;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int t = 0;
-    for (int w = 0; w < kThreads / 64; ++w) t += wave_sums[w];
-    partial[blockIdx.x] = t;
-  }
-}
-
-__global__ __launch_bounds__(kThreads) void chunk_rescan_kernel(
-    const int32_t* in, int32_t* out, int64_t n, const int32_t* partial,
-    int64_t nb) {
-  __shared__ int sh[kChunk];
-  __shared__ int wave_sums[kThreads / 64 + 1];
-  const int64_t base = (int64_t)blockIdx.x * kChunk;
-  scan_chunk(in, out, n, base, partial[blockIdx.x], sh, wave_sums);
-  if (blockIdx.x == 0 && threadIdx.x == 0) out[n] = partial[nb];
+  // The workgroup holding element n-1 (the only one, for n == 0) writes the
+  // total.
+  const bool holds_last = (n == 0) ? (vb == 0) : (base < n && n <= base + kChunk);
+  if (t == kThreads - 1 && holds_last) out[n] = (int)s_prefix + total;
 }
 
 }  // namespace
 
+int64_t scan_blocks(int64_t n) { return n <= 0 ? 1 : (n + kChunk - 1) / kChunk; }
+
 size_t scan_workspace_bytes(int64_t n) {
-  if (n <= kSingleMax) return 0;
-  const int64_t nb = (n + kChunk - 1) / kChunk;
-  return align_up((size_t)(nb + 1) * sizeof(int32_t), 256);
+  return align_up((size_t)scan_blocks(n) * sizeof(uint64_t) + 256, 256);
 }
 
 int exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n, void* ws,
-                       size_t ws_bytes, hipStream_t stream) {
-  if (n < 0) {
-    set_error("exclusive_scan: negative length");
+                       size_t ws_bytes, hipStream_t stream, bool ctl_zeroed) {
+  if (n < 0 || n > 0x7fffffffLL) {
+    set_error("exclusive_scan: invalid length %lld", (long long)n);
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
-  if (n <= kSingleMax) {
-    hipLaunchKernelGGL(scan_single_kernel, dim3(1), dim3(kThreads), 0, stream,
-                       in, out, n);
-    return check_launch("scan_single_kernel");
-  }
-  const int64_t nb = (n + kChunk - 1) / kChunk;
   if (ws == nullptr || ws_bytes < scan_workspace_bytes(n)) {
     set_error("exclusive_scan: workspace too small (%zu < %zu)", ws_bytes,
               scan_workspace_bytes(n));
     return GSPLAT_ERR_WORKSPACE;
   }
-  if (nb > 0x7fffffff) {
-    set_error("exclusive_scan: input too large");
-    return GSPLAT_ERR_INVALID_ARGUMENT;
+  const int64_t nb = scan_blocks(n);
+  uint64_t* status = static_cast<uint64_t*>(ws);
+  uint32_t* ticket = reinterpret_cast<uint32_t*>(status + nb);
+  if (!ctl_zeroed) {
+    const int rc = launch_zero_u32(static_cast<uint32_t*>(ws),
+                                   (int64_t)(scan_workspace_bytes(n) / 4), stream);
+    if (rc) return rc;
   }
-  int32_t* partial = static_cast<int32_t*>(ws);
-  hipLaunchKernelGGL(chunk_sum_kernel, dim3((unsigned)nb), dim3(kThreads), 0,
-                     stream, in, n, partial);
-  int rc = check_launch("chunk_sum_kernel");
-  if (rc) return rc;
-  hipLaunchKernelGGL(scan_single_kernel, dim3(1), dim3(kThreads), 0, stream,
-                     partial, partial, nb);
-  rc = check_launch("scan_single_kernel(partials)");
-  if (rc) return rc;
-  hipLaunchKernelGGL(chunk_rescan_kernel, dim3((unsigned)nb), dim3(kThreads),
-                     0, stream, in, out, n, partial, nb);
-  return check_launch("chunk_rescan_kernel");
+  hipLaunchKernelGGL(scan_lookback_kernel, dim3((unsigned)nb), dim3(kThreads),
+                     0, stream, in, out, n, status, ticket);
+  return check_launch("scan_lookback_kernel");
 }
 
 }  // namespace gs

@@ -64,7 +64,7 @@ SIGNATURES = {
     "gsplat_hip_bin_count_workspace_bytes": (_sz, [_PM]),
     "gsplat_hip_bin_count": (ctypes.c_int, [_PM] + [_vp] * 10 + [_vp, _sz, _vp]),
     "gsplat_hip_bin_emit_workspace_bytes": (_sz, [_PM, _i64]),
-    "gsplat_hip_bin_emit": (ctypes.c_int, [_PM, _vp, _vp, _i64, _vp, _vp, _sz, _vp]),
+    "gsplat_hip_bin_emit": (ctypes.c_int, [_PM, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _vp, _sz, _vp]),
     "gsplat_hip_render_forward": (ctypes.c_int, [_PM] + [_vp] * 7 + [_vp]),
     "gsplat_hip_render_backward": (ctypes.c_int, [_PM] + [_vp] * 11 + [_vp]),
     "gsplat_hip_project_forward": (ctypes.c_int, [_PP] + [_vp] * 10 + [_vp]),

@@ -100,8 +100,8 @@ def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors
         ws2_bytes = L.gsplat_hip_bin_emit_workspace_bytes(meta, n)
         ws2 = _empty(ws2_bytes, torch.uint8, dev)
         with _timed("bin_emit"):
-            check(L.gsplat_hip_bin_emit(meta, ptr(packed), ptr(splat_offsets), n, ptr(binned), ptr(ws2), ws2_bytes,
-                                        s), "gsplat_hip_bin_emit")
+            check(L.gsplat_hip_bin_emit(meta, ptr(packed), ptr(splat_offsets), ptr(tile_counts), n, ptr(binned),
+                                        ptr(ws), ws_bytes, ptr(ws2), ws2_bytes, s), "gsplat_hip_bin_emit")
     return BinState(perm, packed, splat_offsets, tile_counts, tile_offsets, binned, n)
 
 

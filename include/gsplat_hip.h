@@ -90,7 +90,9 @@ size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta);
  *   packed        float [BG*12] packed records in gid order
  *   splat_offsets int32 [BG+1] exclusive scan of per-gid tile-hit counts
  *   tile_counts   int32 [T]    pairs per tile
- *   tile_offsets  int32 [T+1]  exclusive scan of tile_counts (tile ranges) */
+ *   tile_offsets  int32 [T+1]  exclusive scan of tile_counts (tile ranges)
+ * The workspace also carries state that gsplat_hip_bin_emit consumes: pass
+ * the same workspace to it, unmodified. */
 int gsplat_hip_bin_count(const gsplat_raster_meta* meta,
                          const float* means2d, const float* conics,
                          const float* colors, const float* opacities,
@@ -111,8 +113,10 @@ size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
  * Replaces emit_binned_ids (variants/v8/csrc/metal/gsplat_v8_kernels.metal:
  * 290-327) and the per-tile bitonic sort (:141-164, :441-442). */
 int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
-                        const int32_t* splat_offsets, int64_t n_pairs,
+                        const int32_t* splat_offsets,
+                        const int32_t* tile_counts, int64_t n_pairs,
                         int32_t* binned_ids,
+                        void* count_workspace, size_t count_workspace_bytes,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* -------------------------------------------------------------- composite

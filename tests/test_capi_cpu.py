@@ -44,7 +44,7 @@ def test_workspace_queries():
     L = _lib.lib()
     assert L.gsplat_hip_bin_count_workspace_bytes(_meta()) > 0
     assert L.gsplat_hip_bin_emit_workspace_bytes(_meta(), 12345) >= 2 * 12345 * 4
-    assert L.gsplat_hip_scan_workspace_bytes(1000) == 0          # single-workgroup path
+    assert L.gsplat_hip_scan_workspace_bytes(1000) > 0           # look-back status + ticket
     assert L.gsplat_hip_scan_workspace_bytes(10_000_000) > 0
     assert L.gsplat_hip_radix_sort_workspace_bytes(100_000, 3) > 0
     # invalid meta -> 0 bytes
@@ -83,7 +83,7 @@ def test_workspace_too_small_rejected():
     rc = L.gsplat_hip_bin_count(_meta(), *([one] * 10), one, 1, None)
     assert rc == 3
     assert "workspace" in L.gsplat_hip_last_error().decode()
-    rc = L.gsplat_hip_bin_emit(_meta(), one, one, 10, one, one, 1, None)
+    rc = L.gsplat_hip_bin_emit(_meta(), one, one, one, 10, one, one, 1, one, 1, None)
     assert rc == 3
 
 
