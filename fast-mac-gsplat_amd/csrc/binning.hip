@@ -88,7 +88,9 @@ __global__ __launch_bounds__(kThreads) void count_pack_kernel(
     const float cb = colors[3 * orig + 2];
     packed[3 * gid + 0] = make_float4(s.mx, s.my, s.a, s.b);
     packed[3 * gid + 1] = make_float4(s.c, s.o, cr, cg);
-    packed[3 * gid + 2] = make_float4(cb, __int_as_float(orig), 0.0f, 0.0f);
+    packed[3 * gid + 2] =
+        make_float4(cb, __int_as_float(orig),
+                    visibility_limit(s.o, P.alpha_thr, P.max_alpha), 0.0f);
     n = for_each_hit_tile(P, s, batch, [&](int tile, int) {
       atomicAdd(&tile_counts[tile], 1);
     });

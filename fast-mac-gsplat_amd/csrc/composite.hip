@@ -2,22 +2,34 @@
 // reverse-order adjoint (backward).
 //
 // Work decomposition (gfx950): one 64-lane workgroup (= one wavefront) per
-// 16x16 tile.  Slot k = 0..3 of the wave is one 8x8 quadrant of the tile and
-// lane l owns pixel (l%8, l/8) of every quadrant, so every splat record is
-// read once per wave and reused for four pixels, and no barrier spans more
-// than one wavefront.  Splat records of the tile's range are staged 64 at a
-// time in LDS (each lane gathers one 48-byte record) and read by all lanes as
-// broadcasts.  A quadrant is skipped (wave-uniform branch) when it lies
-// outside the splat's bounding box, padded by 1% + 0.01 px so that no pixel
-// that could pass the alpha test is ever skipped.
+// 16x16 tile.  Slot k = 0..3 is the strip of tile rows 4k..4k+3 and lane l
+// owns pixel (l%16, 4k + l/16) of every strip, so the four pixels of a lane
+// share their x coordinate (and the x-only part of the Gaussian exponent),
+// every splat record is read once per wave and reused for four pixels, and no
+// barrier spans more than one wavefront.  Splat records of the tile's range
+// are staged 64 at a time in LDS (each lane gathers one 48-byte record and
+// derives the per-tile constants) and read by all lanes as broadcasts.  A
+// strip is skipped (scalar branch on a per-record bit mask) when the
+// minimum of the splat's quadratic form over the strip's pixel centres
+// exceeds the alpha-support radius by a safety margin, so no pixel that
+// could pass the alpha test is ever skipped.
 //
-// Forward (reference tile_fast_forward_state,
-// variants/v8/csrc/metal/gsplat_v8_kernels.metal:400-476):
-//   alpha = min(max_alpha, o*exp(power)), visible iff power <= 0 and
-//   alpha >= alpha_threshold; C += T*alpha*c; T *= 1-alpha; a pixel stops
-//   after the splat that brings T <= transmittance_threshold.  Saves per
-//   pixel the final T and last = 1 + index of the last composited splat, and
-//   per tile the max of last, so backward needs no forward replay.
+// Alpha test (reference eval_alpha, variants/v8/csrc/metal/gsplat_v8_kernels.metal:121-139):
+// the exponent is evaluated in base 2, p = log2(e) * power, by the fixed
+// rounding chain
+//   A = (-a/2)*L, B = (-b)*L, C = (-c/2)*L  (L = log2(e) rounded to float),
+//   p = fma(C*dy, dy, fma(B*dx, dy, (A*dx)*dx)),
+// and a pixel sees the splat iff p <= 0 and p >= plim, where plim (stored in
+// the packed record by binning) is the exponent at which o * 2^p equals the
+// alpha threshold.  Both decisions are therefore exact functions of the
+// inputs that the CPU oracle reproduces; alpha = min(max_alpha, o * 2^p) with
+// the hardware exp2 (within 1 ulp).
+//
+// Forward (reference tile_fast_forward_state, gsplat_v8_kernels.metal:400-476):
+//   C += T*alpha*c; T *= 1-alpha; a pixel stops after the splat that brings
+//   T <= transmittance_threshold.  Saves per pixel the final T and last = 1 +
+//   index of the last composited splat, and per tile the max of last, so the
+//   backward pass needs no forward replay.
 // Backward (reference tile_fast_backward_saved, :478-608, and the recurrence
 // of docs/v8_critical_theory_notes.md:113-141): walks the tile range in
 // reverse from the tile's max(last); T_prev = T/(1-alpha),
@@ -26,12 +38,16 @@
 //   g_conic = g_power (-dx^2/2, -dx dy, -dy^2/2),
 //   g_mean = g_power (a dx + b dy, b dx + c dy), g_opacity = g_raw exp(power),
 //   gT <- gT + alpha (<g,c> - gT).
-// Per pixel only the moments g_power*(dx, dy, dx^2, dx*dy, dy^2) are
-// accumulated; the conic and mean gradients are formed from their wave sums
-// once per splat.  The nine per-splat sums are reduced across the wavefront
-// with DPP lane-permute adds (no LDS traffic) and one lane issues nine float
-// atomics into the original splat order.
+// Per lane only S0 = sum g_power, S1 = sum g_power dy, S2 = sum g_power dy^2
+// (dx is shared by the lane's pixels) and the colour/opacity sums are kept;
+// the nine per-splat values are formed from them and reduced across the
+// wavefront by a transposed butterfly: two rounds of half-wave register swaps
+// (v_permlane32_swap / v_permlane16_swap) fold eight values into two
+// registers whose four rows each hold one value, four DPP row steps finish
+// them, and lanes 0, 16, 32 and 48 each issue the float atomic for their row
+// into the original splat order (the ninth value uses a plain DPP reduction).
 #include "gs_internal.h"
+#include "gs_predicate.h"
 
 namespace gs {
 namespace {
@@ -42,7 +58,7 @@ constexpr int kBatch = 64;
 
 struct TileCoord {
   int tile, batch, x0, y0;  // tile origin
-  int lx, ly;               // this lane's offset inside a quadrant
+  int lx, ly;               // this lane's column and row inside a strip
 };
 
 __device__ __forceinline__ TileCoord tile_coord(const RasterParams& P) {
@@ -54,81 +70,104 @@ __device__ __forceinline__ TileCoord tile_coord(const RasterParams& P) {
   const int tx = lt - ty * P.tiles_x;
   c.x0 = tx * 16;
   c.y0 = ty * 16;
-  c.lx = threadIdx.x & 7;
-  c.ly = threadIdx.x >> 3;
+  c.lx = threadIdx.x & 15;
+  c.ly = threadIdx.x >> 4;
   return c;
 }
 
-// Pixel of slot (quadrant) k for this lane.
-__device__ __forceinline__ int slot_x(const TileCoord& c, int k) {
-  return c.x0 + 8 * (k & 1) + c.lx;
-}
 __device__ __forceinline__ int slot_y(const TileCoord& c, int k) {
-  return c.y0 + 8 * (k >> 1) + c.ly;
+  return c.y0 + 4 * k + c.ly;
 }
 
 struct Staged {
   float4 s0[kBatch];  // mx, my, A, B
   float4 s1[kBatch];  // C, opacity, r, g
-  float4 s2[kBatch];  // blue, orig index bits, -, -
-  float4 s3[kBatch];  // xlo, xhi, ylo, yhi
+  float4 s2[kBatch];  // blue, orig index bits, plim, strip mask bits
 };
 
-// Stages records [first, first+n) of the tile range into LDS with
-// A = -a/2, B = -b, C = -c/2 (exact scalings of the conic) and a padded
-// bounding box of the pixels where alpha >= alpha_threshold is possible:
-// |dx| <= sqrt(tau c / det), |dy| <= sqrt(tau a / det), tau = -2 ln(thr / o).
-__device__ __forceinline__ void stage_batch(const RasterParams& P,
-                                            const float4* __restrict__ packed,
+__device__ __forceinline__ float conic_q(float a, float b, float c, float dx,
+                                         float dy) {
+  return a * dx * dx + 2.0f * b * dx * dy + c * dy * dy;
+}
+
+// Bit k set unless strip k of the tile at (x0, y0) certainly holds no pixel
+// with p >= plim.  Exact minimum of the conic quadratic q over each strip's
+// pixel-centre rectangle (the centre if inside, else the minima along the
+// four edges), compared with the support radius tau = -2 ln(thr/o) =
+// -2 ln(2) plim enlarged by 2% + 1e-3, which covers the rounding of p's chain
+// and of this test as long as det > 1e-3 a c (|b| < (1 - 5e-4) sqrt(ac)).
+// Conics outside that range are never culled.
+__device__ __forceinline__ uint32_t strip_mask(float mx, float my, float a,
+                                               float b, float c, float plim,
+                                               int x0, int y0) {
+  if (plim > 0.0f) return 0u;  // p <= 0 < plim: invisible everywhere
+  const float tau = -1.38629436f * plim;
+  const float det = a * c - b * b;
+  if (!(a > 0.0f && c > 0.0f && det > 1e-3f * (a * c) && tau < 3.0e38f))
+    return 0xFu;
+  const float tc = tau * 1.02f + 1e-3f;
+  const float dx0 = ((float)x0 + 0.5f) - mx, dx1 = dx0 + 15.0f;
+  const float kc = -b / c, ka = -b / a;
+  const float ex0 = kc * dx0, ex1 = kc * dx1;  // dy minimising q on x = dx0/dx1
+  uint32_t m = 0u;
+#pragma unroll
+  for (int k = 0; k < kPix; ++k) {
+    const float dy0 = ((float)(y0 + 4 * k) + 0.5f) - my, dy1 = dy0 + 3.0f;
+    const bool inside = dx0 <= 0.0f && dx1 >= 0.0f && dy0 <= 0.0f && dy1 >= 0.0f;
+    float q = conic_q(a, b, c, dx0, fminf(fmaxf(ex0, dy0), dy1));
+    q = fminf(q, conic_q(a, b, c, dx1, fminf(fmaxf(ex1, dy0), dy1)));
+    q = fminf(q, conic_q(a, b, c, fminf(fmaxf(ka * dy0, dx0), dx1), dy0));
+    q = fminf(q, conic_q(a, b, c, fminf(fmaxf(ka * dy1, dx0), dx1), dy1));
+    if (inside || q <= tc) m |= 1u << k;
+  }
+  return m;
+}
+
+// Stages records [first, first+n) of the tile range into LDS with the
+// base-2 exponent coefficients and the tile's strip mask.
+__device__ __forceinline__ void stage_batch(const float4* __restrict__ packed,
                                             const int32_t* __restrict__ binned,
-                                            int first, int n, Staged& S) {
+                                            int first, int n,
+                                            const TileCoord& tc, Staged& S) {
   const int lane = threadIdx.x;
   if (lane < n) {
     const int gid = binned[first + lane];
     const float4 p0 = packed[3 * gid + 0];
     const float4 p1 = packed[3 * gid + 1];
     const float4 p2 = packed[3 * gid + 2];
-    const float a = p0.z, b = p0.w, c = p1.x, o = p1.y;
-    const float det = fmaxf(a * c - b * b, 1e-30f);
-    const float tau = fmaxf(-2.0f * __logf(P.alpha_thr / o), 0.0f);
-    const float hx = __builtin_sqrtf(tau * c / det) * 1.01f + 0.01f;
-    const float hy = __builtin_sqrtf(tau * a / det) * 1.01f + 0.01f;
-    // No culling when det is not accurate to well under 1% (nearly
-    // degenerate conic) or a bound is not finite.
-    const bool finite = hx == hx && hy == hy && hx < 3.0e38f &&
-                        hy < 3.0e38f && det > 1e-4f * (a * c);
-    S.s0[lane] = make_float4(p0.x, p0.y, -0.5f * a, -b);
-    S.s1[lane] = make_float4(-0.5f * c, o, p1.z, p1.w);
-    S.s2[lane] = p2;
-    S.s3[lane] = finite
-        ? make_float4(p0.x - hx, p0.x + hx, p0.y - hy, p0.y + hy)
-        : make_float4(-3.0e38f, 3.0e38f, -3.0e38f, 3.0e38f);
+    const float a = p0.z, b = p0.w, c = p1.x;
+    const uint32_t m = strip_mask(p0.x, p0.y, a, b, c, p2.z, tc.x0, tc.y0);
+    float A, B, C;
+    {
+#pragma clang fp contract(off)
+      A = (-0.5f * a) * kLog2e;
+      B = (-b) * kLog2e;
+      C = (-0.5f * c) * kLog2e;
+    }
+    S.s0[lane] = make_float4(p0.x, p0.y, A, B);
+    S.s1[lane] = make_float4(C, p1.y, p1.z, p1.w);
+    S.s2[lane] = make_float4(p2.x, p2.y, p2.z, __uint_as_float(m));
   }
 }
 
-// power = -0.5*(a dx^2 + 2 b dx dy + c dy^2), evaluated as one fixed chain of
-// roundings (two explicit FMAs) so that the CPU oracle can reproduce it bit
-// for bit; A, B, C as staged above.
-__device__ __forceinline__ float splat_power(float A, float B, float C,
-                                             float dx, float dy) {
+// p = fma(C dy, dy, fma(B dx, dy, (A dx) dx)) with the x-only products
+// Adxdx = (A dx) dx and Bdx = B dx precomputed; contraction stays off so the
+// chain of roundings is exactly the one the CPU oracle evaluates.
+__device__ __forceinline__ float splat_exponent(float Adxdx, float Bdx, float C,
+                                                float dy) {
 #pragma clang fp contract(off)
-  return __builtin_fmaf(C * dy, dy, __builtin_fmaf(B * dx, dy, (A * dx) * dx));
+  return __builtin_fmaf(C * dy, dy, __builtin_fmaf(Bdx, dy, Adxdx));
 }
 
-// exp(power) as 2^(power * log2(e)) with the float-rounded constant; the
-// hardware exp2 is within 1 ulp.
-__device__ __forceinline__ float splat_exp(float power) {
+__device__ __forceinline__ void x_terms(float A, float B, float dx,
+                                        float& Adxdx, float& Bdx) {
 #pragma clang fp contract(off)
-  return __builtin_amdgcn_exp2f(power * 1.44269502f);
+  Adxdx = (A * dx) * dx;
+  Bdx = B * dx;
 }
 
-// Does quadrant k (pixel centres x0+8(k&1)+0.5 .. +7.5, y0+8(k>>1)+0.5 ..
-// +7.5) meet the box b = (xlo, xhi, ylo, yhi)?
-__device__ __forceinline__ bool quad_hit(const TileCoord& c, int k,
-                                         const float4& b) {
-  const float qx = (float)(c.x0 + 8 * (k & 1)) + 0.5f;
-  const float qy = (float)(c.y0 + 8 * (k >> 1)) + 0.5f;
-  return !(b.y < qx || b.x > qx + 7.0f || b.w < qy || b.z > qy + 7.0f);
+__device__ __forceinline__ uint32_t uniform_bits(float v) {
+  return __builtin_amdgcn_readfirstlane(__float_as_uint(v));
 }
 
 __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
@@ -139,14 +178,15 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     int32_t* __restrict__ out_tile_stop) {
   __shared__ Staged S;
   const TileCoord tc = tile_coord(P);
-  float px[kPix], py[kPix], T[kPix], cr[kPix], cg[kPix], cb[kPix];
+  const int x = tc.x0 + tc.lx;
+  const float px = (float)x + 0.5f;
+  float py[kPix], T[kPix], cr[kPix], cg[kPix], cb[kPix];
   int last[kPix];
   bool valid[kPix], alive[kPix];
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
-    const int x = slot_x(tc, k), y = slot_y(tc, k);
+    const int y = slot_y(tc, k);
     valid[k] = (x < P.width) && (y < P.height);
-    px[k] = (float)x + 0.5f;
     py[k] = (float)y + 0.5f;
     T[k] = 1.0f;
     cr[k] = cg[k] = cb[k] = 0.0f;
@@ -160,33 +200,33 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     if (!__any(any_alive)) break;
     const int n = min(kBatch, end - base);
     __syncthreads();
-    stage_batch(P, packed, binned, base, n, S);
+    stage_batch(packed, binned, base, n, tc, S);
     __syncthreads();
     for (int j = 0; j < n; ++j) {
+      const float4 a2 = S.s2[j];
+      const uint32_t mask = uniform_bits(a2.w);
+      if (mask == 0u) continue;
       const float4 a0 = S.s0[j];
       const float4 a1 = S.s1[j];
-      const float blue = S.s2[j].x;
-      const float4 box = S.s3[j];
+      const float plim = a2.z;
+      float Adxdx, Bdx;
+      x_terms(a0.z, a0.w, px - a0.x, Adxdx, Bdx);
       const int idx1 = base - start + j + 1;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
-        if (!quad_hit(tc, k, box)) continue;  // wave-uniform
+        if (!((mask >> k) & 1u)) continue;  // scalar branch
         if (alive[k]) {
-          const float dx = px[k] - a0.x;
-          const float dy = py[k] - a0.y;
-          const float power = splat_power(a0.z, a0.w, a1.x, dx, dy);
-          if (power <= 0.0f) {
-            const float raw = a1.y * splat_exp(power);
-            const float alpha = fminf(P.max_alpha, raw);
-            if (alpha >= P.alpha_thr) {
-              const float w = T[k] * alpha;
-              cr[k] += w * a1.z;
-              cg[k] += w * a1.w;
-              cb[k] += w * blue;
-              T[k] *= (1.0f - alpha);
-              last[k] = idx1;
-              if (T[k] <= P.trans_thr) alive[k] = false;
-            }
+          const float p = splat_exponent(Adxdx, Bdx, a1.x, py[k] - a0.y);
+          if (p <= 0.0f && p >= plim) {
+            const float alpha =
+                fminf(P.max_alpha, a1.y * __builtin_amdgcn_exp2f(p));
+            const float w = T[k] * alpha;
+            cr[k] += w * a1.z;
+            cg[k] += w * a1.w;
+            cb[k] += w * a2.x;
+            T[k] *= (1.0f - alpha);
+            last[k] = idx1;
+            if (T[k] <= P.trans_thr) alive[k] = false;
           }
         }
       }
@@ -197,7 +237,7 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
   for (int k = 0; k < kPix; ++k) {
     if (valid[k]) {
       const int64_t pix =
-          ((int64_t)tc.batch * P.height + slot_y(tc, k)) * P.width + slot_x(tc, k);
+          ((int64_t)tc.batch * P.height + slot_y(tc, k)) * P.width + x;
       out_rgb[3 * pix + 0] = cr[k] + T[k] * P.bg_r;
       out_rgb[3 * pix + 1] = cg[k] + T[k] * P.bg_g;
       out_rgb[3 * pix + 2] = cb[k] + T[k] * P.bg_b;
@@ -225,18 +265,80 @@ __device__ __forceinline__ float dpp_src(float x) {
       0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
 }
 
-// Sum over the 64 lanes (all active), returned as a wave-uniform value:
-// quad_perm [1,0,3,2] and [2,3,0,1] reduce quads, row_half_mirror and
-// row_mirror reduce 16-lane rows, row_bcast:15 / row_bcast:31 carry row sums
-// upward so lane 63 ends with the total.
-__device__ __forceinline__ float wave_sum_dpp(float x) {
+// Sum over each 16-lane row, left in every lane of the row: quad_perm
+// [1,0,3,2] and [2,3,0,1] reduce quads, row_half_mirror and row_mirror
+// combine them.
+__device__ __forceinline__ float row_sum_dpp(float x) {
   x += dpp_src<0xB1>(x);
   x += dpp_src<0x4E>(x);
   x += dpp_src<0x141>(x);
   x += dpp_src<0x140>(x);
+  return x;
+}
+
+// Sum over the 64 lanes, left in every lane of row 3 (lanes 48..63):
+// row sums, then row_bcast:15 and row_bcast:31 carry them upward.
+__device__ __forceinline__ float wave_sum_row3(float x) {
+  x = row_sum_dpp(x);
   x += dpp_src<0x142, 0xA>(x);
   x += dpp_src<0x143, 0xC>(x);
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+  return x;
+}
+
+// Sums of four values over the 64 lanes: returns a register whose row r
+// (lanes 16r..16r+15) holds in every lane the total of v[order[r]] with
+// order = {0, 2, 1, 3}.  v_permlane32_swap exchanges the upper half of its
+// first operand with the lower half of its second, v_permlane16_swap the odd
+// rows of the first with the even rows of the second.
+__device__ __forceinline__ float wave_sum4(float v0, float v1, float v2,
+                                           float v3) {
+  const auto s01 = __builtin_amdgcn_permlane32_swap(
+      __float_as_uint(v0), __float_as_uint(v1), false, false);
+  const auto s23 = __builtin_amdgcn_permlane32_swap(
+      __float_as_uint(v2), __float_as_uint(v3), false, false);
+  // rows of h01: v0(rows 0+2), v0(1+3), v1(0+2), v1(1+3); h23 likewise
+  const float h01 = __uint_as_float(s01[0]) + __uint_as_float(s01[1]);
+  const float h23 = __uint_as_float(s23[0]) + __uint_as_float(s23[1]);
+  const auto s = __builtin_amdgcn_permlane16_swap(
+      __float_as_uint(h01), __float_as_uint(h23), false, false);
+  return row_sum_dpp(__uint_as_float(s[0]) + __uint_as_float(s[1]));
+}
+
+// Where lanes 0, 16, 32 and 48 send their reduced values.  Register 1 rows
+// hold {V_mx, V_ca, V_my, V_cb}, register 2 rows {V_cc, V_g, V_r, V_b}, and
+// row 3 of register 3 holds V_o (see the backward kernel for the values).
+struct AtomicRole {
+  float* base1;
+  float* base2;
+  int stride1, stride2;
+  float scale1, scale2;
+};
+
+__device__ __forceinline__ AtomicRole atomic_role(float* g_means2d,
+                                                  float* g_conics,
+                                                  float* g_colors) {
+  // g_mean = -(2/L) V_m since a = -2A/L, b = -B/L, c = -2C/L.
+  constexpr float kMeanScale = -2.0f / kLog2e;
+  AtomicRole r;
+  switch (threadIdx.x >> 4) {
+    case 0:
+      r.base1 = g_means2d + 0; r.stride1 = 2; r.scale1 = kMeanScale;
+      r.base2 = g_conics + 2;  r.stride2 = 3; r.scale2 = -0.5f;
+      break;
+    case 1:
+      r.base1 = g_conics + 0;  r.stride1 = 3; r.scale1 = -0.5f;
+      r.base2 = g_colors + 1;  r.stride2 = 3; r.scale2 = 1.0f;
+      break;
+    case 2:
+      r.base1 = g_means2d + 1; r.stride1 = 2; r.scale1 = kMeanScale;
+      r.base2 = g_colors + 0;  r.stride2 = 3; r.scale2 = 1.0f;
+      break;
+    default:
+      r.base1 = g_conics + 1;  r.stride1 = 3; r.scale1 = -1.0f;
+      r.base2 = g_colors + 2;  r.stride2 = 3; r.scale2 = 1.0f;
+      break;
+  }
+  return r;
 }
 
 __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
@@ -252,13 +354,16 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
   const int nstop = tile_stop[tc.tile];
   if (nstop <= 0) return;
   const int start = tile_offsets[tc.tile];
-  float px[kPix], py[kPix], Tc[kPix], gr[kPix], gg[kPix], gb[kPix], gT[kPix];
+  const AtomicRole role = atomic_role(g_means2d, g_conics, g_colors);
+  const bool row_head = (threadIdx.x & 15) == 0;
+  const int x = tc.x0 + tc.lx;
+  const float px = (float)x + 0.5f;
+  float py[kPix], Tc[kPix], gr[kPix], gg[kPix], gb[kPix], gT[kPix];
   int lk[kPix];
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
-    const int x = slot_x(tc, k), y = slot_y(tc, k);
+    const int y = slot_y(tc, k);
     const bool valid = (x < P.width) && (y < P.height);
-    px[k] = (float)x + 0.5f;
     py[k] = (float)y + 0.5f;
     if (valid) {
       const int64_t pix = ((int64_t)tc.batch * P.height + y) * P.width + x;
@@ -278,78 +383,73 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
     const int cstart = max(0, cend - kBatch);
     const int n = cend - cstart;
     __syncthreads();
-    stage_batch(P, packed, binned, start + cstart, n, S);
+    stage_batch(packed, binned, start + cstart, n, tc, S);
     __syncthreads();
     for (int j = n - 1; j >= 0; --j) {
+      const float4 a2 = S.s2[j];
+      const uint32_t mask = uniform_bits(a2.w);
+      if (mask == 0u) continue;
       const int i = cstart + j;
       const float4 a0 = S.s0[j];
       const float4 a1 = S.s1[j];
-      const float2 a2 = make_float2(S.s2[j].x, S.s2[j].y);
-      const float4 box = S.s3[j];
-      // moments of g_power over this lane's pixels
-      float m_x = 0.f, m_y = 0.f, m_xx = 0.f, m_xy = 0.f, m_yy = 0.f;
-      float acc_r = 0.f, acc_g = 0.f, acc_bl = 0.f, acc_o = 0.f;
+      const float dx = px - a0.x;
+      float Adxdx, Bdx;
+      x_terms(a0.z, a0.w, dx, Adxdx, Bdx);
+      float S0 = 0.f, S1 = 0.f, S2 = 0.f;
+      float acc_r = 0.f, acc_g = 0.f, acc_b = 0.f, acc_o = 0.f;
       bool contrib = false;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
-        if (!quad_hit(tc, k, box)) continue;  // wave-uniform
+        if (!((mask >> k) & 1u)) continue;  // scalar branch
         if (i < lk[k]) {
-          const float dx = px[k] - a0.x;
           const float dy = py[k] - a0.y;
-          const float power = splat_power(a0.z, a0.w, a1.x, dx, dy);
-          if (power <= 0.0f) {
-            const float e = splat_exp(power);
+          const float p = splat_exponent(Adxdx, Bdx, a1.x, dy);
+          if (p <= 0.0f && p >= a2.z) {
+            contrib = true;
+            const float e = __builtin_amdgcn_exp2f(p);
             const float raw = a1.y * e;
             const float alpha = fminf(P.max_alpha, raw);
-            if (alpha >= P.alpha_thr) {
-              contrib = true;
-              // alpha <= max_alpha < 1, so 1 - alpha > 0
-              const float T_prev =
-                  Tc[k] * __builtin_amdgcn_rcpf(fmaxf(1.0f - alpha, P.eps));
-              const float dot_gc = gr[k] * a1.z + gg[k] * a1.w + gb[k] * a2.x;
-              const float diff = dot_gc - gT[k];
-              const float wgt = T_prev * alpha;
-              acc_r += gr[k] * wgt;
-              acc_g += gg[k] * wgt;
-              acc_bl += gb[k] * wgt;
-              const float g_raw = (raw < P.max_alpha) ? T_prev * diff : 0.0f;
-              const float g_pow = g_raw * raw;
-              const float hdx = g_pow * dx, hdy = g_pow * dy;
-              m_x += hdx;
-              m_y += hdy;
-              m_xx += hdx * dx;
-              m_xy += hdx * dy;
-              m_yy += hdy * dy;
-              acc_o += g_raw * e;
-              gT[k] += alpha * diff;
-              Tc[k] = T_prev;
-            }
+            // alpha <= max_alpha < 1, so 1 - alpha > 0
+            const float T_prev =
+                Tc[k] * __builtin_amdgcn_rcpf(fmaxf(1.0f - alpha, P.eps));
+            const float dot_gc = gr[k] * a1.z + gg[k] * a1.w + gb[k] * a2.x;
+            const float diff = dot_gc - gT[k];
+            const float wgt = T_prev * alpha;
+            acc_r += gr[k] * wgt;
+            acc_g += gg[k] * wgt;
+            acc_b += gb[k] * wgt;
+            const float g_raw = (raw < P.max_alpha) ? T_prev * diff : 0.0f;
+            const float g_pow = g_raw * raw;
+            const float hdy = g_pow * dy;
+            S0 += g_pow;
+            S1 += hdy;
+            S2 += hdy * dy;
+            acc_o += g_raw * e;
+            gT[k] += alpha * diff;
+            Tc[k] = T_prev;
           }
         }
       }
       if (__any(contrib)) {
-        m_x = wave_sum_dpp(m_x);
-        m_y = wave_sum_dpp(m_y);
-        m_xx = wave_sum_dpp(m_xx);
-        m_xy = wave_sum_dpp(m_xy);
-        m_yy = wave_sum_dpp(m_yy);
-        acc_r = wave_sum_dpp(acc_r);
-        acc_g = wave_sum_dpp(acc_g);
-        acc_bl = wave_sum_dpp(acc_bl);
-        acc_o = wave_sum_dpp(acc_o);
-        if (threadIdx.x == 0) {
-          const int64_t orig = __float_as_int(a2.y);
-          // a = -2A, b = -B, c = -2C
-          const float a = -2.0f * a0.z, b = -a0.w, c = -2.0f * a1.x;
-          unsafeAtomicAdd(&g_means2d[2 * orig + 0], a * m_x + b * m_y);
-          unsafeAtomicAdd(&g_means2d[2 * orig + 1], b * m_x + c * m_y);
-          unsafeAtomicAdd(&g_conics[3 * orig + 0], -0.5f * m_xx);
-          unsafeAtomicAdd(&g_conics[3 * orig + 1], -m_xy);
-          unsafeAtomicAdd(&g_conics[3 * orig + 2], -0.5f * m_yy);
-          unsafeAtomicAdd(&g_colors[3 * orig + 0], acc_r);
-          unsafeAtomicAdd(&g_colors[3 * orig + 1], acc_g);
-          unsafeAtomicAdd(&g_colors[3 * orig + 2], acc_bl);
-          unsafeAtomicAdd(&g_opac[orig], acc_o);
+        // Per-lane parts of the splat's gradients (a, b, c = -2A/L, -B/L,
+        // -2C/L): g_mean = -(2/L) (V_mx, V_my), g_conic = (-V_ca/2, -V_cb,
+        // -V_cc/2).
+        const float X = dx * S0;             // sum g_power dx
+        const float hB = 0.5f * a0.w;
+        const float V_mx = a0.z * X + hB * S1;
+        const float V_my = hB * X + a1.x * S1;
+        const float V_ca = dx * X;           // sum g_power dx^2
+        const float V_cb = dx * S1;          // sum g_power dx dy
+        const float r1 = wave_sum4(V_mx, V_my, V_ca, V_cb);
+        const float r2 = wave_sum4(S2, acc_r, acc_g, acc_b);
+        const float r3 = wave_sum_row3(acc_o);
+        if (row_head) {
+          const int orig = (int)uniform_bits(a2.y);
+          unsafeAtomicAdd(role.base1 + (int64_t)orig * role.stride1,
+                          r1 * role.scale1);
+          unsafeAtomicAdd(role.base2 + (int64_t)orig * role.stride2,
+                          r2 * role.scale2);
+          if (threadIdx.x == 48) unsafeAtomicAdd(g_opac + orig, r3);
         }
       }
     }

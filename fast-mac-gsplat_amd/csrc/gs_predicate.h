@@ -68,6 +68,27 @@ __device__ __forceinline__ bool alpha_support(float opacity, float thr,
   return __builtin_isfinite(tau) && (tau > 0.0f);
 }
 
+// log2(e) rounded to float.  The compositor evaluates the exponent in base 2:
+// p = kLog2e * power, alpha = min(max_alpha, o * 2^p).
+constexpr float kLog2e = 1.44269502f;
+
+// Base-2 exponent limit of the compositor's alpha test.  The reference's test
+// min(max_alpha, o*exp(power)) >= alpha_threshold (eval_alpha,
+// gsplat_v8_kernels.metal:121-139) is evaluated as p >= plim with
+//   plim = kLog2e * ln(max(alpha_threshold / o, FLT_MIN)),
+// which is the same condition up to rounding, but is decided by a fixed
+// function of the inputs that the CPU oracle reproduces bit for bit.
+// +inf (nothing visible) when o is not positive or max_alpha < threshold;
+// -inf (every p <= 0 visible) when the threshold is not positive.
+__device__ __forceinline__ float visibility_limit(float opacity, float thr,
+                                                  float max_alpha) {
+#pragma clang fp contract(off)
+  if (!(opacity > 0.0f) || max_alpha < thr) return __builtin_inff();
+  if (!(thr > 0.0f)) return -__builtin_inff();
+  const float ratio = fmaxf(thr / opacity, 1.17549435e-38f);
+  return kLog2e * gs_logf(ratio);
+}
+
 __device__ __forceinline__ int clamp_to_int(float v) {
   // Saturating float->int for the bbox corners (NaN -> 0).  Values that
   // matter are small integers already.

@@ -21,9 +21,10 @@
  * (build with -ffp-contract=off) and with the logarithm below, so that its
  * results are a fixed function of the inputs: the HIP kernels must reproduce
  * the tile lists bit for bit.  Compositing is float32 like the reference
- * kernels with a fixed rounding chain for the Gaussian exponent (see
- * eval_alpha); it is compared with tolerances, and pixels whose threshold
- * decisions fall inside exp's last-ulp window are flagged.
+ * kernels with a fixed rounding chain for the Gaussian exponent and an exact
+ * visibility decision (see eval_alpha); it is compared with tolerances, and
+ * pixels whose early-stop or gradient-gate decisions fall inside exp's
+ * last-ulp window are flagged.
  *
  * Pinned by (tests/test_oracle_cpu.py): brute-force completeness/tightness of
  * the predicate in double precision, oracle_logf against libm, the dense
@@ -233,8 +234,25 @@ void oracle_bin_fill(const oracle_meta* M, const float* means2d, const float* co
 /* ---------------------------------------------------------- compositing */
 typedef struct {
   float mx, my, a, b, c, o, r, g, bl;
+  float plim; /* base-2 exponent limit of the alpha test (oracle_plim) */
   int64_t orig;
 } splat_t;
+
+#define LOG2E_F 1.44269502f
+
+/* Base-2 exponent at which o * 2^p reaches alpha_threshold:
+ * log2(e)_f32 * ln(max(thr / o, FLT_MIN)) with oracle_logf; +inf when nothing
+ * can be visible (o <= 0 or max_alpha < thr), -inf when thr <= 0.  The
+ * compositor tests p >= plim, which is the reference's
+ * min(max_alpha, o*exp(power)) >= alpha_threshold (eval_alpha,
+ * gsplat_v8_kernels.metal:121-139) up to rounding; the packed records written
+ * by binning carry this exact value. */
+float oracle_plim(float o, float thr, float max_alpha) {
+  if (!(o > 0.0f) || max_alpha < thr) return INFINITY;
+  if (!(thr > 0.0f)) return -INFINITY;
+  const float ratio = fmaxf(thr / o, 1.17549435e-38f);
+  return LOG2E_F * oracle_logf(ratio);
+}
 
 static splat_t load_splat(const oracle_meta* M, const float* means2d, const float* conics,
                           const float* colors, const float* opac, const int32_t* perm,
@@ -246,37 +264,42 @@ static splat_t load_splat(const oracle_meta* M, const float* means2d, const floa
   s.a = conics[3 * o]; s.b = conics[3 * o + 1]; s.c = conics[3 * o + 2];
   s.r = colors[3 * o]; s.g = colors[3 * o + 1]; s.bl = colors[3 * o + 2];
   s.o = opac[o];
+  s.plim = oracle_plim(s.o, M->alpha_threshold, M->max_alpha);
   s.orig = o;
   return s;
 }
 
 /* Reference eval_alpha: visible iff power <= 0 and alpha >= threshold, with
- * power = -0.5*(a dx^2 + 2 b dx dy + c dy^2).  The power is evaluated as a
- * fixed chain of roundings -- A=-a/2, B=-b, C=-c/2 (exact scalings) and
- * power = fma(C dy, dy, fma(B dx, dy, (A dx) dx)) -- and exp(power) as
- * 2^(power * log2(e)_f32) rounded once from double, so the HIP compositor
- * (which uses the same chain and a hardware exp2 within 1 ulp) can differ only
- * in the last ulp of exp.  Decisions taken within that window are reported
- * through the ambiguity flags below. */
-#define AMB_ALPHA 1 /* raw alpha within rounding of alpha_threshold */
+ * power = -0.5*(a dx^2 + 2 b dx dy + c dy^2) and alpha = min(max_alpha,
+ * o exp(power)).  Evaluated in base 2 by a fixed chain of roundings,
+ *   A = (-a/2) L, B = (-b) L, C = (-c/2) L   (L = log2(e) rounded to float)
+ *   p = fma(C dy, dy, fma(B dx, dy, (A dx) dx))
+ * with the visibility decision p <= 0 and p >= plim (oracle_plim), which the
+ * HIP compositor takes bit for bit the same way.  2^p is rounded once from
+ * double; the hardware exp2 is within 1 ulp, so later decisions that depend
+ * on the value of alpha (early stop on T, the max_alpha gradient gate) can
+ * differ in their last-ulp window, reported through the ambiguity flags. */
+#define AMB_ALPHA 1 /* unused: the alpha-threshold decision is exact */
 #define AMB_STOP 2  /* T within rounding of transmittance_threshold */
 #define AMB_GATE 4  /* raw alpha within rounding of max_alpha (gradient gate) */
 #define AMB_REL 4e-7f
+
+static float splat_exponent(const splat_t* s, float dx, float dy) {
+  const float A = (-0.5f * s->a) * LOG2E_F, B = (-s->b) * LOG2E_F;
+  const float C = (-0.5f * s->c) * LOG2E_F;
+  return fmaf(C * dy, dy, fmaf(B * dx, dy, (A * dx) * dx));
+}
 
 static int eval_alpha(const oracle_meta* M, const splat_t* s, float px, float py,
                       float* alpha, float* raw, float* dx, float* dy, int* amb) {
   *dx = px - s->mx;
   *dy = py - s->my;
-  const float A = -0.5f * s->a, B = -s->b, C = -0.5f * s->c;
-  const float power = fmaf(C * *dy, *dy, fmaf(B * *dx, *dy, (A * *dx) * *dx));
-  if (!(power <= 0.0f)) return 0;
-  *raw = s->o * (float)exp2((double)(power * 1.44269502f));
+  const float p = splat_exponent(s, *dx, *dy);
+  if (!(p <= 0.0f && p >= s->plim)) return 0;
+  *raw = s->o * (float)exp2((double)p);
   *alpha = fminf(M->max_alpha, *raw);
-  if (amb) {
-    if (fabsf(*raw - M->alpha_threshold) <= AMB_REL * M->alpha_threshold) *amb |= AMB_ALPHA;
-    if (fabsf(*raw - M->max_alpha) <= AMB_REL * M->max_alpha) *amb |= AMB_GATE;
-  }
-  return *alpha >= M->alpha_threshold;
+  if (amb && fabsf(*raw - M->max_alpha) <= AMB_REL * M->max_alpha) *amb |= AMB_GATE;
+  return 1;
 }
 
 /* out_rgb [B,H,W,3]; out_T [B,H,W]; out_last [B,H,W] = 1 + index of the last
@@ -393,8 +416,8 @@ void oracle_render_backward(const oracle_meta* M, const float* means2d, const fl
 }
 
 /* Marks (tainted[orig] = 1) every splat whose gradient an ambiguous pixel of
- * `amb` can change: the splats visible at that pixel (alpha test passes, with
- * the same last-ulp window) anywhere in its tile list.  Conservative: a
+ * `amb` can change: the splats visible at that pixel anywhere in its tile
+ * list.  Conservative: a
  * different decision at one splat changes T for the pixel's later splats and
  * the suffix colour seen by its earlier ones, all of which are visible ones. */
 void oracle_taint(const oracle_meta* M, const float* means2d, const float* conics,
@@ -412,9 +435,8 @@ void oracle_taint(const oracle_meta* M, const float* means2d, const float* conic
         for (int i = tile_offsets[t]; i < tile_offsets[t + 1]; ++i) {
           const splat_t s = load_splat(M, means2d, conics, colors, opac, perm, binned_ids[i]);
           float alpha, raw, dx, dy;
-          int a2 = 0;
-          const int vis = eval_alpha(M, &s, (float)x + 0.5f, (float)y + 0.5f, &alpha, &raw, &dx, &dy, &a2);
-          if (vis || (a2 & AMB_ALPHA)) tainted[s.orig] = 1;
+          if (eval_alpha(M, &s, (float)x + 0.5f, (float)y + 0.5f, &alpha, &raw, &dx, &dy, NULL))
+            tainted[s.orig] = 1;
         }
       }
     }

@@ -44,6 +44,8 @@ def lib():
         pm = ctypes.POINTER(OracleMeta)
         L.oracle_logf.restype = ctypes.c_float
         L.oracle_logf.argtypes = [ctypes.c_float]
+        L.oracle_plim.restype = ctypes.c_float
+        L.oracle_plim.argtypes = [ctypes.c_float] * 3
         L.oracle_depth_order.restype = None
         L.oracle_depth_order.argtypes = [vp, ctypes.c_int32, ctypes.c_int32, vp]
         L.oracle_bin_count.restype = ctypes.c_int64
@@ -84,6 +86,12 @@ def make_meta(height, width, batch, gpb, alpha_threshold=1.0 / 255.0, transmitta
 
 def logf(x: float) -> float:
     return float(lib().oracle_logf(ctypes.c_float(x)))
+
+
+def plim(opacity: float, alpha_threshold: float, max_alpha: float) -> float:
+    """Base-2 exponent limit of the alpha test (float32 value as a Python float)."""
+    return float(lib().oracle_plim(ctypes.c_float(opacity), ctypes.c_float(alpha_threshold),
+                                   ctypes.c_float(max_alpha)))
 
 
 @dataclass
@@ -139,10 +147,10 @@ AMB_ALPHA, AMB_STOP, AMB_GATE = 1, 2, 4
 
 def render_forward(meta: OracleMeta, s: Scene, bins: OracleBins, with_ambiguity: bool = False):
     """Returns (img, final_T, last, tile_stop[, ambiguity]).  ambiguity[b,y,x] is a
-    bit mask: AMB_ALPHA / AMB_STOP when an alpha-threshold or early-stop decision
-    of the pixel lies within exp's last-ulp window (another exact-arithmetic
-    implementation may decide it the other way), AMB_GATE for the max_alpha
-    gradient gate."""
+    bit mask: AMB_STOP when an early-stop decision of the pixel lies within
+    exp's last-ulp window (another implementation with a 1-ulp exp2 may decide
+    it the other way), AMB_GATE likewise for the max_alpha gradient gate.  The
+    alpha-threshold decision itself is exact (AMB_ALPHA is never set)."""
     B, H, W = meta.batch, meta.height, meta.width
     img = np.empty((B, H, W, 3), dtype=np.float32)
     T = np.empty((B, H, W), dtype=np.float32)

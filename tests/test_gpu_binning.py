@@ -98,6 +98,11 @@ def _assert_bins_equal(st, ob, scene, B, G):
     np.testing.assert_array_equal(packed[:, 5], o[orig])
     np.testing.assert_array_equal(packed[:, 6:9], c[orig])
     np.testing.assert_array_equal(packed[:, 9].view(np.int32), orig.astype(np.int32))
+    # the alpha-test exponent limit is bit-exact with the oracle's
+    meta = TO.make_meta(8, 8, 1, 1)
+    want = np.array([TO.plim(float(v), meta.alpha_threshold, meta.max_alpha) for v in o[orig]],
+                    dtype=np.float32)
+    np.testing.assert_array_equal(packed[:, 10].view(np.uint32), want.view(np.uint32), err_msg="plim")
     # sorted 64-bit keys (tile << 32 | gid) strictly increase
     keys = ob.sorted_keys()
     assert np.all(keys[1:] > keys[:-1])

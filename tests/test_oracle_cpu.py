@@ -58,6 +58,32 @@ def test_logf_special_values():
     assert TO.logf(math.inf) == math.inf
 
 
+# ----------------------------------------------------------------- plim
+def test_plim_is_the_alpha_threshold_exponent():
+    """o * 2^plim == alpha_threshold up to a few float ulps (closed form), so the
+    compositor's p >= plim is the reference's o*exp(power) >= threshold."""
+    rng = np.random.default_rng(5)
+    thr = np.float32(THR)
+    for o in np.concatenate([rng.uniform(0.004, 1.0, 2000), [1.0, 0.5, 0.99, float(thr)]]).astype(np.float32):
+        p = TO.plim(float(o), float(thr), 0.99)
+        exact = math.log2(float(thr) / float(o))
+        assert abs(p - exact) <= 8 * abs(_ulp(exact)) + 1e-7, (o, p, exact)
+        assert abs(float(o) * 2.0 ** p - float(thr)) <= 1e-6 * float(thr) + 1e-12
+    # opacity exactly at the threshold: plim == 0, only p == 0 is visible
+    assert TO.plim(float(thr), float(thr), 0.99) == 0.0
+
+
+def test_plim_special_cases():
+    assert TO.plim(0.0, THR, 0.99) == math.inf            # nothing visible
+    assert TO.plim(-0.5, THR, 0.99) == math.inf
+    assert TO.plim(float("nan"), THR, 0.99) == math.inf
+    assert TO.plim(0.5, 0.5, 0.4) == math.inf             # max_alpha < threshold
+    assert TO.plim(0.5, 0.0, 0.99) == -math.inf           # every p <= 0 visible
+    assert TO.plim(1e-45, THR, 0.99) > 100                # thr/o overflows: invisible
+    # o far above thr: thr/o clamps at FLT_MIN, plim = log2(FLT_MIN) = -126
+    assert abs(TO.plim(3e38, 1e-30, 0.99) + 126.0) < 1e-4
+
+
 # ----------------------------------------------------------- depth order
 def test_depth_order_matches_stable_argsort():
     rng = np.random.default_rng(1)
