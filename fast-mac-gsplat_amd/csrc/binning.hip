@@ -1,22 +1,22 @@
-// binning.hip -- per-splat tile intersection count + record packing, and
+// binning.hip -- per-splat tile intersection count, record packing, and
 // deterministic (tile, gid) pair emission.
 //
 // This translation unit is compiled with -ffp-contract=off: the predicate
 // results must match the CPU oracle bit for bit.
 //
-// count_pack_kernel  one thread per depth-sorted splat (gid).  Gathers the
-//   splat's attributes from the original order (via perm), writes the packed
-//   48-byte record, counts the tiles whose pixel-centre rectangle meets the
-//   splat's alpha >= threshold ellipse (reference count_tiles,
-//   variants/v8/csrc/metal/gsplat_v8_kernels.metal:244-288), bumps the
-//   per-tile pair counters, and turns the per-splat counts into exclusive
-//   offsets in the same launch (workgroup scan + decoupled look-back).
-// emit_kernel        one thread per gid; repeats the same tile walk and
-//   writes (tile, gid) at splat_offsets[gid] + k, so pairs land in ascending
-//   gid order (reference emit_binned_ids, :290-327, which uses per-tile
-//   atomic cursors and therefore needs a later per-tile sort).  The same
-//   launch also prepares the pair sort: it zeroes the sort's look-back status
-//   and accumulates its per-pass digit histograms from the tile counts.
+// count_kernel  one thread per splat in the original order: counts the tiles
+//   whose pixel-centre rectangle meets the splat's alpha >= threshold ellipse
+//   (reference count_tiles, variants/v8/csrc/metal/gsplat_v8_kernels.metal:
+//   244-288) and bumps the per-tile pair counters.
+// pack_kernel   one thread per depth-sorted splat (gid): writes the packed
+//   48-byte record and the exclusive per-gid pair offsets (workgroup scan +
+//   decoupled look-back in the same launch).
+// emit_kernel   one thread per gid; repeats the same tile walk and writes
+//   (tile, gid) at splat_offsets[gid] + k, so pairs land in ascending gid
+//   order (reference emit_binned_ids, :290-327, which uses per-tile atomic
+//   cursors and therefore needs a later per-tile sort).  The same launch also
+//   prepares the pair sort: it zeroes the sort's look-back status and
+//   accumulates its per-pass digit histograms from the tile counts.
 #include "gs_internal.h"
 #include "gs_predicate.h"
 #include "lookback.h"
@@ -61,12 +61,38 @@ __device__ __forceinline__ int for_each_hit_tile(const RasterParams& P,
   return n;
 }
 
-__global__ __launch_bounds__(kThreads) void count_pack_kernel(
+// One thread per splat in the ORIGINAL order: tile-hit count into
+// splat_count[orig] and per-tile pair counters (reference count_tiles,
+// gsplat_v8_kernels.metal:244-288).  Runs before the depth sort, so the pair
+// count N = sum(tile_counts) is known while the sort is still running.
+__global__ __launch_bounds__(kThreads) void count_kernel(
+    RasterParams P, const float* __restrict__ means2d,
+    const float* __restrict__ conics, const float* __restrict__ opacities,
+    int32_t* __restrict__ splat_count, int32_t* __restrict__ tile_counts) {
+  const int orig = blockIdx.x * kThreads + threadIdx.x;
+  if (orig >= P.num_splats) return;
+  SplatGeom s;
+  s.mx = means2d[2 * orig + 0];
+  s.my = means2d[2 * orig + 1];
+  s.a = conics[3 * orig + 0];
+  s.b = conics[3 * orig + 1];
+  s.c = conics[3 * orig + 2];
+  s.o = opacities[orig];
+  splat_count[orig] = for_each_hit_tile(P, s, orig / P.gpb, [&](int tile, int) {
+    atomicAdd(&tile_counts[tile], 1);
+  });
+}
+
+// One thread per depth-sorted splat (gid): gathers the attributes of
+// orig = perm[gid] into the packed 48-byte record and turns the per-gid
+// tile-hit counts into exclusive offsets splat_offsets in the same launch
+// (workgroup scan + decoupled look-back).
+__global__ __launch_bounds__(kThreads) void pack_kernel(
     RasterParams P, const float* __restrict__ means2d,
     const float* __restrict__ conics, const float* __restrict__ colors,
     const float* __restrict__ opacities, const uint32_t* __restrict__ perm,
-    float4* __restrict__ packed, int32_t* __restrict__ splat_offsets,
-    int32_t* __restrict__ tile_counts, uint64_t* scan_status,
+    const int32_t* __restrict__ splat_count, float4* __restrict__ packed,
+    int32_t* __restrict__ splat_offsets, uint64_t* scan_status,
     uint32_t* scan_ticket) {
   __shared__ int wsum[kThreads / 64];
   __shared__ int s_prefix;
@@ -76,24 +102,21 @@ __global__ __launch_bounds__(kThreads) void count_pack_kernel(
   if (gid < P.num_splats) {
     const int batch = gid / P.gpb;
     const int orig = batch * P.gpb + (int)perm[gid];
-    SplatGeom s;
-    s.mx = means2d[2 * orig + 0];
-    s.my = means2d[2 * orig + 1];
-    s.a = conics[3 * orig + 0];
-    s.b = conics[3 * orig + 1];
-    s.c = conics[3 * orig + 2];
-    s.o = opacities[orig];
+    const float mx = means2d[2 * orig + 0];
+    const float my = means2d[2 * orig + 1];
+    const float a = conics[3 * orig + 0];
+    const float b = conics[3 * orig + 1];
+    const float c = conics[3 * orig + 2];
+    const float o = opacities[orig];
     const float cr = colors[3 * orig + 0];
     const float cg = colors[3 * orig + 1];
     const float cb = colors[3 * orig + 2];
-    packed[3 * gid + 0] = make_float4(s.mx, s.my, s.a, s.b);
-    packed[3 * gid + 1] = make_float4(s.c, s.o, cr, cg);
+    n = splat_count[orig];
+    packed[3 * gid + 0] = make_float4(mx, my, a, b);
+    packed[3 * gid + 1] = make_float4(c, o, cr, cg);
     packed[3 * gid + 2] =
         make_float4(cb, __int_as_float(orig),
-                    visibility_limit(s.o, P.alpha_thr, P.max_alpha), 0.0f);
-    n = for_each_hit_tile(P, s, batch, [&](int tile, int) {
-      atomicAdd(&tile_counts[tile], 1);
-    });
+                    visibility_limit(o, P.alpha_thr, P.max_alpha), 0.0f);
   }
   // Workgroup exclusive scan of the counts.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -207,19 +230,30 @@ __global__ void zero_grads_kernel(float* g_m, float* g_q, float* g_c,
 
 }  // namespace
 
-int launch_count_pack(const RasterParams& P, const float* means2d,
-                      const float* conics, const float* colors,
-                      const float* opacities, const uint32_t* perm,
-                      float* packed, int32_t* splat_offsets,
-                      int32_t* tile_counts, uint64_t* scan_status,
-                      uint32_t* scan_ticket, hipStream_t stream) {
+int launch_count(const RasterParams& P, const float* means2d,
+                 const float* conics, const float* opacities,
+                 int32_t* splat_count, int32_t* tile_counts,
+                 hipStream_t stream) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
-  hipLaunchKernelGGL(count_pack_kernel, dim3(grid), dim3(kThreads), 0, stream,
-                     P, means2d, conics, colors, opacities, perm,
+  hipLaunchKernelGGL(count_kernel, dim3(grid), dim3(kThreads), 0, stream, P,
+                     means2d, conics, opacities, splat_count, tile_counts);
+  return check_launch("count_kernel");
+}
+
+int launch_pack(const RasterParams& P, const float* means2d,
+                const float* conics, const float* colors,
+                const float* opacities, const uint32_t* perm,
+                const int32_t* splat_count, float* packed,
+                int32_t* splat_offsets, uint64_t* scan_status,
+                uint32_t* scan_ticket, hipStream_t stream) {
+  if (P.num_splats == 0) return GSPLAT_OK;
+  const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
+  hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(kThreads), 0, stream, P,
+                     means2d, conics, colors, opacities, perm, splat_count,
                      reinterpret_cast<float4*>(packed), splat_offsets,
-                     tile_counts, scan_status, scan_ticket);
-  return check_launch("count_pack_kernel");
+                     scan_status, scan_ticket);
+  return check_launch("pack_kernel");
 }
 
 int count_scan_blocks(const RasterParams& P) {

@@ -100,14 +100,15 @@ int null_check(std::initializer_list<const void*> ptrs, const char* what) {
   return GSPLAT_OK;
 }
 
-// Count-stage workspace: a zeroed control region (depth-sort control block,
-// count-scan look-back status and ticket, pair-sort histograms and tickets,
-// tile-offset scan status and ticket), then the depth sort's ping-pong
-// buffers.
+// Binning workspace shared by bin_count, bin_pack and bin_emit: a control
+// region zeroed by bin_count (depth-sort control block, pack-scan look-back
+// status and ticket, pair-sort histograms and tickets, tile-offset scan
+// status and ticket), the per-splat tile-hit counts (original order), then
+// the depth sort's ping-pong buffers.
 struct CountLayout {
   gs::RadixPlan depth;
-  size_t scan_status, scan_ticket, pair_ghist, pair_tickets, ctl_end;
-  size_t depth_buffers, tile_scan, total;
+  size_t scan_status, scan_ticket, pair_ghist, pair_tickets, tile_scan, ctl_end;
+  size_t splat_count, depth_buffers, total;
 };
 
 CountLayout count_layout(const RasterParams& P) {
@@ -125,6 +126,8 @@ CountLayout count_layout(const RasterParams& P) {
   L.tile_scan = off;
   off += gs::scan_workspace_bytes(P.num_tiles);
   L.ctl_end = off;
+  L.splat_count = off;
+  off += gs::align_up((size_t)P.num_splats * sizeof(int32_t), 256);
   L.depth_buffers = off;
   off += gs::align_up(L.depth.buffer_bytes, 256);
   L.total = off;
@@ -165,17 +168,15 @@ size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta) {
 }
 
 int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
-                         const float* conics, const float* colors,
-                         const float* opacities, const float* depths,
-                         int32_t* perm, float* packed, int32_t* splat_offsets,
+                         const float* conics, const float* opacities,
                          int32_t* tile_counts, int32_t* tile_offsets,
                          void* workspace, size_t workspace_bytes,
                          void* stream) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
-  rc = null_check({means2d, conics, colors, opacities, depths, perm, packed,
-                   splat_offsets, tile_counts, tile_offsets, workspace},
+  rc = null_check({means2d, conics, opacities, tile_counts, tile_offsets,
+                   workspace},
                   "gsplat_hip_bin_count");
   if (rc) return rc;
   const CountLayout L = count_layout(P);
@@ -190,30 +191,59 @@ int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* base = static_cast<char*>(workspace);
-  const gs::RadixCtl depth_ctl = gs::radix_ctl_at(L.depth, base);
   // 1. zero the control region and the tile counters
   rc = gs::launch_zero2(reinterpret_cast<uint32_t*>(base),
                         (int64_t)(L.ctl_end / sizeof(uint32_t)),
                         reinterpret_cast<uint32_t*>(tile_counts), P.num_tiles, s);
-  // 2. stable depth order per image (onesweep LSD over the 32 key bits)
-  if (!rc) rc = gs::radix_global_hist(L.depth, depth_ctl, nullptr, depths, s);
+  // 2. per-splat tile-hit counts and per-tile pair counters
   if (!rc)
-    rc = gs::radix_passes(L.depth, depth_ctl, base + L.depth_buffers, nullptr,
-                          nullptr, depths, nullptr,
-                          reinterpret_cast<uint32_t*>(perm), s);
-  // 3. pack + count + per-splat offsets
-  if (!rc)
-    rc = gs::launch_count_pack(
-        P, means2d, conics, colors, opacities,
-        reinterpret_cast<const uint32_t*>(perm), packed, splat_offsets,
-        tile_counts, reinterpret_cast<uint64_t*>(base + L.scan_status),
-        reinterpret_cast<uint32_t*>(base + L.scan_ticket), s);
-  // 4. tile ranges
+    rc = gs::launch_count(P, means2d, conics, opacities,
+                          reinterpret_cast<int32_t*>(base + L.splat_count),
+                          tile_counts, s);
+  // 3. tile ranges (N = tile_offsets[T])
   if (!rc)
     rc = gs::exclusive_scan_i32(tile_counts, tile_offsets, P.num_tiles,
                                 base + L.tile_scan,
                                 gs::scan_workspace_bytes(P.num_tiles), s,
                                 /*ctl_zeroed=*/true);
+  return rc;
+}
+
+int gsplat_hip_bin_pack(const gsplat_raster_meta* meta, const float* means2d,
+                        const float* conics, const float* colors,
+                        const float* opacities, const float* depths,
+                        int32_t* perm, float* packed, int32_t* splat_offsets,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  RasterParams P;
+  int rc = make_params(meta, P);
+  if (rc) return rc;
+  rc = null_check({means2d, conics, colors, opacities, depths, perm, packed,
+                   splat_offsets, workspace},
+                  "gsplat_hip_bin_pack");
+  if (rc) return rc;
+  const CountLayout L = count_layout(P);
+  if (workspace_bytes < L.total) {
+    gs::set_error("gsplat_hip_bin_pack: workspace too small (%zu < %zu)",
+                  workspace_bytes, L.total);
+    return GSPLAT_ERR_WORKSPACE;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* base = static_cast<char*>(workspace);
+  const gs::RadixCtl depth_ctl = gs::radix_ctl_at(L.depth, base);
+  // 1. stable depth order per image (onesweep LSD over the 32 key bits)
+  rc = gs::radix_global_hist(L.depth, depth_ctl, nullptr, depths, s);
+  if (!rc)
+    rc = gs::radix_passes(L.depth, depth_ctl, base + L.depth_buffers, nullptr,
+                          nullptr, depths, nullptr,
+                          reinterpret_cast<uint32_t*>(perm), s);
+  // 2. packed records and per-gid pair offsets
+  if (!rc)
+    rc = gs::launch_pack(P, means2d, conics, colors, opacities,
+                         reinterpret_cast<const uint32_t*>(perm),
+                         reinterpret_cast<const int32_t*>(base + L.splat_count),
+                         packed, splat_offsets,
+                         reinterpret_cast<uint64_t*>(base + L.scan_status),
+                         reinterpret_cast<uint32_t*>(base + L.scan_ticket), s);
   return rc;
 }
 

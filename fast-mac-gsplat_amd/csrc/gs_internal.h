@@ -50,6 +50,7 @@ int exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n, void* ws,
 struct RadixPlan {
   int64_t n_seg;
   int segments, nblk, passes, begin_bit, end_bit;
+  int rounds;  // 64-element groups per wavefront of a sort workgroup
   int64_t ghist_words, status_words, ticket_words;
   size_t a_keys, a_vals, b_keys, b_vals, buffer_bytes;
 };
@@ -82,15 +83,21 @@ int radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in,
                      hipStream_t stream);
 
 // ---- binning (binning.hip)
-// count_pack: packs records, counts tile hits, bumps tile_counts (zeroed)
-// and writes splat_offsets[0..BG] via a look-back scan whose status
+// count: per-splat tile-hit counts (original order) into splat_count and
+// per-tile pair counters into tile_counts (zeroed).
+int launch_count(const RasterParams& P, const float* means2d,
+                 const float* conics, const float* opacities,
+                 int32_t* splat_count, int32_t* tile_counts,
+                 hipStream_t stream);
+// pack: packed records in gid order and splat_offsets[0..BG] (exclusive scan
+// of splat_count[perm]) via a look-back scan whose status
 // (count_scan_blocks(P) words) and ticket must be zero.
-int launch_count_pack(const RasterParams& P, const float* means2d,
-                      const float* conics, const float* colors,
-                      const float* opacities, const uint32_t* perm,
-                      float* packed, int32_t* splat_offsets,
-                      int32_t* tile_counts, uint64_t* scan_status,
-                      uint32_t* scan_ticket, hipStream_t stream);
+int launch_pack(const RasterParams& P, const float* means2d,
+                const float* conics, const float* colors,
+                const float* opacities, const uint32_t* perm,
+                const int32_t* splat_count, float* packed,
+                int32_t* splat_offsets, uint64_t* scan_status,
+                uint32_t* scan_ticket, hipStream_t stream);
 int count_scan_blocks(const RasterParams& P);
 // emit: writes (tile, gid) pairs; also zeroes pair_status and adds the
 // pair sort's per-pass digit histograms into pair_ghist (zeroed).

@@ -39,19 +39,23 @@ __device__ __forceinline__ void status_store(uint64_t* p, uint64_t v) {
 }
 
 // Exclusive prefix of slot `blk` from the 32-bit statuses of slots
-// blk-1, blk-2, ... stored `stride` words apart; one thread, windows of 8.
+// blk-1, blk-2, ... stored `stride` words apart; one thread, windows of W.
+template <int W>
 __device__ __forceinline__ uint32_t lookback32(const uint32_t* status, int blk,
                                               int stride) {
-  constexpr int W = 8;
   uint32_t prefix = 0u;
   int b = blk - 1;
   int spins = 0;
   while (b >= 0) {
+    // Clamped indices and a select after the load keep the W loads
+    // independent (no branch between a load and its use).
     uint32_t s[W];
 #pragma unroll
     for (int k = 0; k < W; ++k)
-      s[k] = (b - k >= 0) ? status_load(status + (int64_t)(b - k) * stride)
-                          : kFlagInc32;
+      s[k] = status_load(status + (int64_t)max(b - k, 0) * stride);
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+      if (b - k < 0) s[k] = kFlagInc32;
     int consumed = 0;
     bool done = false, wait = false;
 #pragma unroll

@@ -6,11 +6,12 @@
 // the caller), so a workgroup only needs the counts of the workgroups before
 // it in its segment, which it gets by decoupled look-back (lookback.h).
 //
-// Inside a workgroup (256 lanes, 4096 elements) each wavefront owns 1024
-// consecutive elements and ranks them 64 at a time: lanes holding the same
-// digit are found with one ballot per digit bit ("match"), the rank is the
-// popcount of matching lower lanes, and one leader lane per digit bumps the
-// wave's running count in LDS.  Element order inside a workgroup is therefore
+// Inside a workgroup (256 lanes, 64*kR elements per wavefront) each wavefront
+// ranks its consecutive elements 64 at a time: lanes holding the same digit
+// are found with eight ballots ("match"), the rank is the popcount of
+// matching lower lanes plus the wave's running count of that digit, which the
+// digit's lowest lane bumps with one LDS atomic (returning the old count) and
+// broadcasts to its peers.  Element order inside a workgroup is
 // (wave, round, lane) = input order, which makes the sort stable.  The block
 // is then staged in LDS in sorted order and written out so that each digit's
 // run is one contiguous, coalesced store.
@@ -22,9 +23,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kRounds = 16;
-constexpr int kWaveItems = 64 * kRounds;           // 1024
-constexpr int kBlockItems = kWaves * kWaveItems;   // 4096
+// Look-back window: predecessor statuses read per round trip.
+constexpr int kLookbackWindow = 16;
 
 // Order-preserving map of a float depth to uint32 (ascending float order ==
 // ascending key).  -0.0 and +0.0 map to the same key (they compare equal in
@@ -41,11 +41,11 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return (lane == 0u) ? 0ull : (~0ull >> (64u - lane));
 }
 
-// Lanes of `active` whose digit equals this lane's digit.
-__device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active,
-                                                int digit_bits) {
+// Lanes of `active` whose 8-bit digit equals this lane's digit.
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active) {
   uint64_t m = active;
-  for (int bit = 0; bit < digit_bits; ++bit) {
+#pragma unroll
+  for (int bit = 0; bit < 8; ++bit) {
     const bool p = (d >> bit) & 1u;
     const uint64_t b = __ballot(p);
     m &= p ? b : ~b;
@@ -54,10 +54,10 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active,
 }
 
 struct PassArgs {
-  const uint32_t* keys_in;   // nullptr when depth_src is used
-  const uint32_t* vals_in;   // nullptr -> in-segment index
-  const float* depth_src;    // non-null only for the first pass of a depth sort
-  uint32_t* keys_out;        // nullptr -> keys not written (last pass)
+  const uint32_t* keys_in;   // unused with kDepthKeys
+  const uint32_t* vals_in;   // unused without kValsIn (values = in-segment index)
+  const float* depth_src;    // keys derived from float depths (kDepthKeys)
+  uint32_t* keys_out;        // unused without kKeysOut (last pass)
   uint32_t* vals_out;
   int64_t n_seg;
   int nblk;                  // workgroups per segment
@@ -69,9 +69,11 @@ struct PassArgs {
   uint32_t* ticket;          // zeroed
 };
 
-__device__ __forceinline__ uint32_t load_key(const PassArgs& a, int64_t idx) {
-  return a.depth_src ? depth_key(a.depth_src[idx]) : a.keys_in[idx];
-}
+// Kernel variants, chosen on the host, so that the load loops hold no
+// data-dependent branches: every load of a lane is in flight before the first
+// one is used (a branch between a load and its use makes the compiler wait
+// for that load before the next is issued).
+enum : int { kDepthKeys = 1, kValsIn = 2, kKeysOut = 4 };
 
 // Exclusive scan of one value per thread over the 256-thread block.
 __device__ __forceinline__ uint32_t block_excl_scan256(uint32_t v,
@@ -93,6 +95,9 @@ __device__ __forceinline__ uint32_t block_excl_scan256(uint32_t v,
 
 // Per-pass global digit histograms: ghist[(p*segments + seg)*256 + d] (zeroed
 // by the caller) for passes p = 0..passes-1 with digits at begin_bit + 8p.
+// Each thread loads kR keys (clamped indices, no branches) before
+// counting any of them.
+template <bool kDepth, int kR>
 __global__ __launch_bounds__(kThreads) void rs_global_hist_kernel(
     const uint32_t* keys, const float* depth_src, int64_t n_seg, int nblk,
     int segments, int begin_bit, int end_bit, int passes, uint32_t* ghist) {
@@ -101,18 +106,24 @@ __global__ __launch_bounds__(kThreads) void rs_global_hist_kernel(
   const int blk = blockIdx.x - seg * nblk;
   const int t = threadIdx.x;
   for (int i = t; i < 4 * 256; i += kThreads) (&h[0][0])[i] = 0u;
-  __syncthreads();
   const int64_t base = (int64_t)seg * n_seg;
-  const int64_t lo = (int64_t)blk * kBlockItems;
-  for (int i = t; i < kBlockItems; i += kThreads) {
-    const int64_t j = lo + i;
-    if (j >= n_seg) break;
-    const uint32_t key =
-        depth_src ? depth_key(depth_src[base + j]) : keys[base + j];
-    for (int p = 0; p < passes; ++p) {
-      const int sh = begin_bit + 8 * p;
-      const int bits = min(8, end_bit - sh);
-      atomicAdd(&h[p][(key >> sh) & ((1u << bits) - 1u)], 1u);
+  const int64_t lo = (int64_t)blk * (kThreads * kR);
+  uint32_t kv[kR];
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    const int64_t j = min(lo + r * kThreads + t, n_seg - 1);
+    kv[r] = kDepth ? __float_as_uint(depth_src[base + j]) : keys[base + j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    if (lo + r * kThreads + t < n_seg) {
+      const uint32_t key = kDepth ? depth_key(__uint_as_float(kv[r])) : kv[r];
+      for (int p = 0; p < passes; ++p) {
+        const int sh = begin_bit + 8 * p;
+        const int bits = min(8, end_bit - sh);
+        atomicAdd(&h[p][(key >> sh) & ((1u << bits) - 1u)], 1u);
+      }
     }
   }
   __syncthreads();
@@ -122,7 +133,10 @@ __global__ __launch_bounds__(kThreads) void rs_global_hist_kernel(
   }
 }
 
+template <int kMode, int kR>
 __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
+  constexpr int kWaveItems = 64 * kR;
+  constexpr int kBlockItems = kWaves * kWaveItems;
   __shared__ uint32_t cnt[kWaves][256];
   __shared__ uint32_t dstart[256];
   __shared__ uint32_t gbase[256];
@@ -140,33 +154,37 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   const int64_t lo = (int64_t)blk * kBlockItems + (int64_t)wave * kWaveItems;
   const uint32_t dmask = (1u << a.digit_bits) - 1u;
 
-  // Issue every load of this lane's 16 elements before ranking any of them.
-  uint32_t kreg[kRounds], vreg[kRounds], rreg[kRounds];
+  // Issue every load of this lane's kR elements before ranking any of them
+  // (indices clamped into the segment; lanes past its end are masked out of
+  // the ranking below).
+  uint32_t kreg[kR], vreg[kR], rreg[kR];
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    const int64_t j = lo + r * 64 + lane;
-    const bool valid = j < a.n_seg;
-    kreg[r] = valid ? load_key(a, seg_base + j) : 0u;
-    vreg[r] = valid ? (a.vals_in ? a.vals_in[seg_base + j] : (uint32_t)j) : 0u;
+  for (int r = 0; r < kR; ++r) {
+    const int64_t src = seg_base + min(lo + r * 64 + lane, a.n_seg - 1);
+    kreg[r] = (kMode & kDepthKeys) ? __float_as_uint(a.depth_src[src])
+                                   : a.keys_in[src];
+    if (kMode & kValsIn) vreg[r] = a.vals_in[src];
   }
+  // this pass's global digit count of digit t (digit bases below)
+  const uint32_t gh = a.ghist[(int64_t)seg * 256 + t];
   __syncthreads();
 
+  const uint64_t lt = lanemask_lt();
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
+  for (int r = 0; r < kR; ++r) {
     const int64_t j = lo + r * 64 + lane;
     const bool valid = j < a.n_seg;
-    const uint64_t act = __ballot(valid);
-    rreg[r] = 0xffffffffu;
-    if (act != 0ull) {
-      const uint32_t d = (kreg[r] >> a.shift) & dmask;
-      const uint64_t peers = match_digit(d, act, a.digit_bits);
-      const uint32_t below = (uint32_t)__popcll(peers & lanemask_lt());
-      const uint32_t old = valid ? cnt[wave][d] : 0u;
-      if (valid && below == 0u) cnt[wave][d] = old + (uint32_t)__popcll(peers);
-      // Other lanes read these counters next round: keep LDS ops in order.
-      __builtin_amdgcn_wave_barrier();
-      if (valid) rreg[r] = (old + below) | (d << 16);
-    }
+    if (kMode & kDepthKeys) kreg[r] = depth_key(__uint_as_float(kreg[r]));
+    if (!(kMode & kValsIn)) vreg[r] = (uint32_t)j;
+    const uint32_t d = (kreg[r] >> a.shift) & dmask;
+    const uint64_t peers = match_digit(d, __ballot(valid));
+    const uint32_t below = (uint32_t)__popcll(peers & lt);
+    uint32_t old = 0u;
+    if (valid && below == 0u)
+      old = atomicAdd(&cnt[wave][d], (uint32_t)__popcll(peers));
+    // every lane takes the old count from its digit's lowest lane
+    old = (uint32_t)__shfl((int)old, __ffsll((long long)peers) - 1, 64);
+    rreg[r] = valid ? ((old + below) | (d << 16)) : 0xffffffffu;
   }
   __syncthreads();
 
@@ -179,12 +197,12 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   cnt[1][t] = c0;
   cnt[2][t] = c0 + c1;
   cnt[3][t] = c0 + c1 + c2;
-  const uint32_t gh = a.ghist[(int64_t)seg * 256 + t];
   const uint32_t dbase = block_excl_scan256(gh, wsum);
   const uint32_t local = block_excl_scan256(tot, wsum);
   uint32_t prefix = 0u;
   if (blk > 0) {
-    prefix = lookback32(a.status + (int64_t)seg * a.nblk * 256 + t, blk, 256);
+    prefix = lookback32<kLookbackWindow>(
+        a.status + (int64_t)seg * a.nblk * 256 + t, blk, 256);
     status_store(my_status, kFlagInc32 | (prefix + tot));
   }
   dstart[t] = local;
@@ -192,7 +210,7 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   __syncthreads();
 
 #pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
+  for (int r = 0; r < kR; ++r) {
     if (rreg[r] != 0xffffffffu) {
       const uint32_t d = rreg[r] >> 16;
       const uint32_t pos = dstart[d] + cnt[wave][d] + (rreg[r] & 0xffffu);
@@ -208,7 +226,7 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
     const uint32_t key = sk[i];
     const uint32_t d = (key >> a.shift) & dmask;
     const int64_t dst = seg_base + (int64_t)gbase[d] + (int64_t)(i - (int)dstart[d]);
-    if (a.keys_out) a.keys_out[dst] = key;
+    if (kMode & kKeysOut) a.keys_out[dst] = key;
     a.vals_out[dst] = sv[i];
   }
 }
@@ -218,7 +236,8 @@ __global__ void rs_copy_kernel(PassArgs a, int64_t n_total) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n_total) return;
   const int64_t j = i % a.n_seg;
-  if (a.keys_out) a.keys_out[i] = load_key(a, i);
+  if (a.keys_out)
+    a.keys_out[i] = a.depth_src ? depth_key(a.depth_src[i]) : a.keys_in[i];
   a.vals_out[i] = a.vals_in ? a.vals_in[i] : (uint32_t)j;
 }
 
@@ -230,6 +249,12 @@ __global__ void zero_u32_kernel(uint32_t* p, int64_t n) {
 
 }  // namespace
 
+// Rounds (64-element groups per wavefront) of one onesweep workgroup: small
+// segments use smaller workgroups so that more of them run side by side.
+int radix_rounds(int64_t n_seg) {
+  return n_seg <= (int64_t(1) << 18) ? 4 : 16;
+}
+
 RadixPlan radix_plan(int64_t n_seg, int segments, int begin_bit, int end_bit) {
   RadixPlan L{};
   L.n_seg = n_seg;
@@ -237,7 +262,9 @@ RadixPlan radix_plan(int64_t n_seg, int segments, int begin_bit, int end_bit) {
   L.begin_bit = begin_bit;
   L.end_bit = end_bit;
   L.passes = end_bit > begin_bit ? (end_bit - begin_bit + 7) / 8 : 0;
-  L.nblk = (int)((n_seg + kBlockItems - 1) / kBlockItems);
+  L.rounds = radix_rounds(n_seg);
+  const int64_t block_items = (int64_t)kThreads * L.rounds;
+  L.nblk = (int)((n_seg + block_items - 1) / block_items);
   L.ghist_words = (int64_t)4 * segments * 256;
   L.status_words = (int64_t)(L.passes > 0 ? L.passes : 1) * segments * L.nblk * 256;
   L.ticket_words = 4;
@@ -286,11 +313,17 @@ int radix_global_hist(const RadixPlan& L, const RadixCtl& C,
                       const uint32_t* keys, const float* depth_src,
                       hipStream_t stream) {
   if (L.passes == 0 || L.n_seg == 0 || L.segments == 0) return GSPLAT_OK;
-  hipLaunchKernelGGL(rs_global_hist_kernel,
-                     dim3((unsigned)(L.nblk * (int64_t)L.segments)),
-                     dim3(kThreads), 0, stream, keys, depth_src, L.n_seg,
-                     L.nblk, L.segments, L.begin_bit, L.end_bit, L.passes,
-                     C.ghist);
+  const dim3 grid((unsigned)(L.nblk * (int64_t)L.segments));
+#define GS_HIST_LAUNCH(D, R)                                                   \
+  hipLaunchKernelGGL((rs_global_hist_kernel<D, R>), grid, dim3(kThreads), 0,  \
+                     stream, keys, depth_src, L.n_seg, L.nblk, L.segments,    \
+                     L.begin_bit, L.end_bit, L.passes, C.ghist)
+  if (L.rounds == 4) {
+    if (depth_src) GS_HIST_LAUNCH(true, 4); else GS_HIST_LAUNCH(false, 4);
+  } else {
+    if (depth_src) GS_HIST_LAUNCH(true, 16); else GS_HIST_LAUNCH(false, 16);
+  }
+#undef GS_HIST_LAUNCH
   return check_launch("rs_global_hist_kernel");
 }
 
@@ -326,9 +359,26 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
                L.segments, shift, bits,
                C.ghist + (int64_t)p * L.segments * 256,
                C.status + p * status_per_pass, C.tickets + p};
-    hipLaunchKernelGGL(rs_onesweep_kernel,
-                       dim3((unsigned)(L.nblk * (int64_t)L.segments)),
-                       dim3(kThreads), 0, stream, a);
+    const int mode = (cur_depth ? kDepthKeys : 0) | (cur_v ? kValsIn : 0) |
+                     (out_k ? kKeysOut : 0);
+    const dim3 grid((unsigned)(L.nblk * (int64_t)L.segments));
+    switch (mode * 32 + L.rounds) {
+#define GS_ONESWEEP_CASE(M, R)                                              \
+  case M * 32 + R:                                                          \
+    hipLaunchKernelGGL((rs_onesweep_kernel<M, R>), grid, dim3(kThreads), 0, \
+                       stream, a);                                          \
+    break;
+#define GS_ONESWEEP_MODE(M) GS_ONESWEEP_CASE(M, 4) GS_ONESWEEP_CASE(M, 16)
+      GS_ONESWEEP_MODE(0) GS_ONESWEEP_MODE(1) GS_ONESWEEP_MODE(2)
+      GS_ONESWEEP_MODE(3) GS_ONESWEEP_MODE(4) GS_ONESWEEP_MODE(5)
+      GS_ONESWEEP_MODE(6) GS_ONESWEEP_MODE(7)
+#undef GS_ONESWEEP_MODE
+#undef GS_ONESWEEP_CASE
+      default:
+        set_error("radix sort: no kernel for mode %d, %d rounds", mode,
+                  L.rounds);
+        return GSPLAT_ERR_INVALID_ARGUMENT;
+    }
     const int rc = check_launch("rs_onesweep_kernel");
     if (rc) return rc;
     cur_k = out_k;
@@ -339,7 +389,8 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
 }
 
 bool radix_size_ok(int64_t n_seg, int segments) {
-  const int64_t nblk = (n_seg + kBlockItems - 1) / kBlockItems;
+  const int64_t block_items = (int64_t)kThreads * radix_rounds(n_seg);
+  const int64_t nblk = (n_seg + block_items - 1) / block_items;
   return nblk * segments <= 0x7fffffffLL && n_seg <= (int64_t(1) << 29) &&
          n_seg * segments <= 0x7fffffffLL;
 }

@@ -28,10 +28,18 @@ __global__ __launch_bounds__(kThreads) void scan_lookback_kernel(
   const int vb = take_ticket(ticket);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int64_t base = (int64_t)vb * kChunk;
+  // All loads in flight before any is used: clamped indices, no branches
+  // between a load and its use (n == 0 loads nothing).
+  int ld[kItems];
+  if (n > 0) {
+#pragma unroll
+    for (int i = 0; i < kItems; ++i)
+      ld[i] = in[min(base + i * kThreads + t, n - 1)];
+  }
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const int j = i * kThreads + t;
-    sh[pad(j)] = (base + j < n) ? in[base + j] : 0;
+    sh[pad(j)] = (base + j < n) ? ld[i] : 0;
   }
   __syncthreads();
   int v[kItems];

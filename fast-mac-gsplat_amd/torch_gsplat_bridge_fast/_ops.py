@@ -71,10 +71,14 @@ def _empty(n, dtype, device):
 
 def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
                   opacities: Tensor, depths: Tensor) -> BinState:
-    """Stable depth order + record packing + tile binning + pair sort.
+    """Tile binning + stable depth order + record packing + pair sort.
 
     Inputs are flat contiguous fp32 [BG,2], [BG,3], [BG,3], [BG], [BG] in the
-    original splat order."""
+    original splat order.  The pair count N (needed on the host to size the
+    pair buffers, like the reference's tile_offsets[-1] read,
+    variants/v8/csrc/metal/gsplat_metal.mm:188) is copied to pinned memory
+    right after the tile counts are known and read after the depth sort has
+    been enqueued, so the wait overlaps GPU work."""
     L = _lib.lib()
     dev = means2d.device
     B, G = meta.batch, meta.gaussians_per_batch
@@ -89,10 +93,18 @@ def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors
     ws = _empty(max(ws_bytes, 1), torch.uint8, dev)
     s = stream_of(means2d)
     with _timed("bin_count"):
-        check(L.gsplat_hip_bin_count(meta, ptr(means2d), ptr(conics), ptr(colors), ptr(opacities), ptr(depths),
-                                     ptr(perm), ptr(packed), ptr(splat_offsets), ptr(tile_counts),
+        check(L.gsplat_hip_bin_count(meta, ptr(means2d), ptr(conics), ptr(opacities), ptr(tile_counts),
                                      ptr(tile_offsets), ptr(ws), ws_bytes, s), "gsplat_hip_bin_count")
-    n = int(tile_offsets[-1].item())
+    n_host = torch.empty((1,), dtype=torch.int32, pin_memory=True)
+    n_host.copy_(tile_offsets[-1:], non_blocking=True)
+    n_ready = torch.cuda.Event()
+    n_ready.record()
+    with _timed("bin_pack"):
+        check(L.gsplat_hip_bin_pack(meta, ptr(means2d), ptr(conics), ptr(colors), ptr(opacities), ptr(depths),
+                                    ptr(perm), ptr(packed), ptr(splat_offsets), ptr(ws), ws_bytes, s),
+              "gsplat_hip_bin_pack")
+    n_ready.synchronize()
+    n = int(n_host[0])
     if n < 0:
         raise RuntimeError(f"pair count overflowed int32 ({n})")
     binned = _empty(n, torch.int32, dev)
@@ -125,14 +137,16 @@ def render_forward(meta: _lib.RasterMeta, st: BinState, *, save_state: bool):
 
 def render_backward(meta: _lib.RasterMeta, st: BinState, final_T: Tensor, last: Tensor, tile_stop: Tensor,
                     grad_img: Tensor):
-    """Returns (g_means2d [BG,2], g_conics [BG,3], g_colors [BG,3], g_opacities [BG]) in ORIGINAL order."""
+    """Returns (g_means2d [B,G,2], g_conics [B,G,3], g_colors [B,G,3], g_opacities [B,G]) in ORIGINAL
+    order.  They are allocated in the leaves' batched shapes (not as views of flat buffers) so that
+    autograd can hand them to .grad without a copy."""
     L = _lib.lib()
     dev = st.packed.device
-    BG = meta.batch * meta.gaussians_per_batch
-    g_m = torch.empty((BG, 2), dtype=torch.float32, device=dev)
-    g_q = torch.empty((BG, 3), dtype=torch.float32, device=dev)
-    g_c = torch.empty((BG, 3), dtype=torch.float32, device=dev)
-    g_o = torch.empty((BG,), dtype=torch.float32, device=dev)
+    B, G = meta.batch, meta.gaussians_per_batch
+    g_m = torch.empty((B, G, 2), dtype=torch.float32, device=dev)
+    g_q = torch.empty((B, G, 3), dtype=torch.float32, device=dev)
+    g_c = torch.empty((B, G, 3), dtype=torch.float32, device=dev)
+    g_o = torch.empty((B, G), dtype=torch.float32, device=dev)
     grad_img = grad_img.contiguous()
     with _timed("render_backward"):
         check(L.gsplat_hip_render_backward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.binned_ids),

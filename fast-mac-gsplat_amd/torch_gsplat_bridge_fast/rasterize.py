@@ -241,10 +241,10 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
         g_m, g_q, g_c, g_o = _ops.render_backward(ctx.meta, st, final_T, last, tile_stop, grad_out)
         need = ctx.needs_input_grad
         g_depth = torch.zeros(ctx.depth_shape, dtype=torch.float32, device=grad_out.device) if need[4] else None
-        return (g_m.view(B, G, 2) if need[0] else None,
-                g_q.view(B, G, 3) if need[1] else None,
-                g_c.view(B, G, 3) if need[2] else None,
-                g_o.view(B, G) if need[3] else None,
+        return (g_m if need[0] else None,
+                g_q if need[1] else None,
+                g_c if need[2] else None,
+                g_o if need[3] else None,
                 g_depth, None)
 
 
@@ -266,7 +266,11 @@ def _rasterize_batched(means2d_b, conics_b, colors_b, opacities_b, depths_b, con
     outs = []
     for b0 in range(0, B, chunk_b):
         b1 = min(B, b0 + chunk_b)
-        args = (means2d_b[b0:b1], conics_b[b0:b1], colors_b[b0:b1], opacities_b[b0:b1], depths_b[b0:b1])
+        if b0 == 0 and b1 == B:
+            # one chunk: no slice views (their backward would zero-fill and copy every gradient)
+            args = (means2d_b, conics_b, colors_b, opacities_b, depths_b)
+        else:
+            args = (means2d_b[b0:b1], conics_b[b0:b1], colors_b[b0:b1], opacities_b[b0:b1], depths_b[b0:b1])
         if train_mode:
             outs.append(_RasterizeProjectedGaussians.apply(*args, config))
         else:

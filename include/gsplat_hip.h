@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 1
+#define GSPLAT_HIP_ABI_VERSION 2
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -82,30 +82,47 @@ const char* gsplat_hip_last_error(void);
  * host side variants/v8/csrc/metal/gsplat_metal.mm:140-204) together with the
  * stable depth argsort + gathers of variants/v8/torch_gsplat_bridge_v8/
  * rasterize.py:465-475.  The reference sizes binned_ids with a host read of
- * tile_offsets[-1] (gsplat_metal.mm:188); here binning is split at the same
- * point: gsplat_hip_bin_count leaves the pair count N in tile_offsets[T] (and
- * splat_offsets[BG]), the caller reads it and sizes gsplat_hip_bin_emit. */
+ * tile_offsets[-1] (gsplat_metal.mm:188).  Here binning is three calls on one
+ * stream sharing one workspace:
+ *   gsplat_hip_bin_count  tile-hit counts and tile ranges; leaves the pair
+ *                         count N in tile_offsets[T];
+ *   gsplat_hip_bin_pack   stable depth order, packed records, per-splat pair
+ *                         offsets;
+ *   gsplat_hip_bin_emit   pair emission and the sort by tile.
+ * A caller that needs N on the host (to size binned_ids) can copy
+ * tile_offsets[T] asynchronously after bin_count and wait for it after
+ * enqueuing bin_pack, so the read overlaps the depth sort. */
 
+/* Bytes of the binning workspace used by bin_count, bin_pack and bin_emit. */
 size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta);
 
-/* Inputs (original order): means2d [BG,2], conics [BG,3], colors [BG,3],
- * opacities [BG], depths [BG].  Outputs:
- *   perm          int32 [BG]   perm[b*G+r] = original index (within image b)
- *                              of the splat of depth rank r
- *   packed        float [BG*12] packed records in gid order
- *   splat_offsets int32 [BG+1] exclusive scan of per-gid tile-hit counts
+/* Inputs (original order): means2d [BG,2], conics [BG,3], opacities [BG].
+ * Outputs:
  *   tile_counts   int32 [T]    pairs per tile
- *   tile_offsets  int32 [T+1]  exclusive scan of tile_counts (tile ranges)
- * The workspace also carries state that gsplat_hip_bin_emit consumes: pass
- * the same workspace to it, unmodified. */
+ *   tile_offsets  int32 [T+1]  exclusive scan of tile_counts (tile ranges);
+ *                              tile_offsets[T] = N
+ * The workspace keeps the per-splat tile-hit counts and the zeroed control
+ * state that bin_pack and bin_emit consume: pass the same workspace to them,
+ * unmodified, on the same stream. */
 int gsplat_hip_bin_count(const gsplat_raster_meta* meta,
                          const float* means2d, const float* conics,
-                         const float* colors, const float* opacities,
-                         const float* depths,
-                         int32_t* perm, float* packed, int32_t* splat_offsets,
+                         const float* opacities,
                          int32_t* tile_counts, int32_t* tile_offsets,
                          void* workspace, size_t workspace_bytes,
                          void* stream);
+
+/* Inputs (original order): means2d [BG,2], conics [BG,3], colors [BG,3],
+ * opacities [BG], depths [BG], and the workspace of bin_count.  Outputs:
+ *   perm          int32 [BG]   perm[b*G+r] = original index (within image b)
+ *                              of the splat of depth rank r
+ *   packed        float [BG*12] packed records in gid order
+ *   splat_offsets int32 [BG+1] exclusive scan of per-gid tile-hit counts */
+int gsplat_hip_bin_pack(const gsplat_raster_meta* meta,
+                        const float* means2d, const float* conics,
+                        const float* colors, const float* opacities,
+                        const float* depths,
+                        int32_t* perm, float* packed, int32_t* splat_offsets,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
                                            int64_t n_pairs);
@@ -123,6 +140,7 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
                         int32_t* binned_ids,
                         void* count_workspace, size_t count_workspace_bytes,
                         void* workspace, size_t workspace_bytes, void* stream);
+/* count_workspace is the workspace of bin_count / bin_pack. */
 
 /* -------------------------------------------------------------- composite
  * Forward compositor.  Replaces render_fast_forward_state / _eval
