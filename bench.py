@@ -15,6 +15,15 @@ restatement of the reference algorithm, oracle/tile_oracle.c) on the same
 scene, forward+backward, once.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 2]
+
+Measurement helpers (used for the committed rocprofv3 summaries):
+    python bench.py --calibrate-copy     a plain copy of 256 MiB (read + write),
+                                         run under rocprofv3 --pmc FETCH_SIZE /
+                                         WRITE_SIZE to convert those counters
+                                         into bytes
+    python bench.py --summarize DIR      markdown summary of the rocprofv3 CSV
+                                         output in DIR (kernel stats and/or
+                                         counter collection)
 """
 from __future__ import annotations
 
@@ -71,7 +80,67 @@ def cpu_baseline(sc, H, W, B, G, w_np):
     }
 
 
+CALIBRATION_BYTES = 256 << 20
+
+
+def calibrate_copy() -> int:
+    """One elementwise copy kernel (dst = src * 1) over CALIBRATION_BYTES, three
+    times: under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch,
+    divided by the bytes really moved, is the counter-to-bytes factor."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "kernel": "at::native elementwise mul (dst = src * 1)",
+                      "bytes_read": CALIBRATION_BYTES, "bytes_written": CALIBRATION_BYTES, "dispatches": 3}))
+    return 0
+
+
+def summarize(d: str) -> int:
+    """Markdown tables from rocprofv3 --output-format csv results under d."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    for path in sorted(glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)):
+        rows = list(csv.DictReader(open(path)))
+        total = sum(float(r["TotalDurationNs"]) for r in rows) or 1.0
+        print(f"kernel stats: {os.path.relpath(path, d)}\n")
+        print("| kernel | calls | avg us | min us | max us | share |")
+        print("|---|---:|---:|---:|---:|---:|")
+        for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+            print(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                  f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                  f"{100.0 * float(r['TotalDurationNs']) / total:.1f}% |")
+        print()
+    for path in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
+        acc = defaultdict(lambda: defaultdict(list))
+        for r in csv.DictReader(open(path)):
+            name = r.get("Kernel_Name", "")
+            key = (r.get("Dispatch_Id", ""), r.get("Counter_Name", ""))
+            acc[name][key].append(float(r.get("Counter_Value", "0") or 0.0))
+        print(f"counters (mean per dispatch, summed over hardware instances): {os.path.relpath(path, d)}\n")
+        print("| kernel | counter | dispatches | mean per dispatch |")
+        print("|---|---|---:|---:|")
+        for name, per in sorted(acc.items()):
+            by_counter = defaultdict(list)
+            for (disp, cname), vals in per.items():
+                by_counter[cname].append(sum(vals))
+            for cname, vals in sorted(by_counter.items()):
+                print(f"| `{name[:70]}` | {cname} | {len(vals)} | {sum(vals) / len(vals):.6g} |")
+        print()
+    return 0
+
+
 def main() -> int:
+    if "--summarize" in sys.argv:
+        return summarize(sys.argv[sys.argv.index("--summarize") + 1])
+    if "--calibrate-copy" in sys.argv:
+        return calibrate_copy()
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)

@@ -71,6 +71,22 @@ int make_params(const gsplat_raster_meta* m, RasterParams& P) {
                   (long long)BG);
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
+  // The compositors rely on 1 - alpha >= 1 - max_alpha >= eps (the
+  // reference's max(1 - alpha, eps) guard is then a no-op) and on pixels
+  // starting alive (T = 1 > transmittance_threshold).
+  if (!(m->eps >= 0.0f && m->max_alpha >= 0.0f && m->max_alpha < 1.0f &&
+        1.0f - m->max_alpha >= m->eps)) {
+    gs::set_error("max_alpha must lie in [0, 1) with 1 - max_alpha >= eps "
+                  "(got %g, eps %g)",
+                  (double)m->max_alpha, (double)m->eps);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  if (!(m->transmittance_threshold >= 0.0f &&
+        m->transmittance_threshold < 1.0f)) {
+    gs::set_error("transmittance_threshold must lie in [0, 1) (got %g)",
+                  (double)m->transmittance_threshold);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
   P.height = m->height;
   P.width = m->width;
   P.tiles_x = (int)tiles_x;

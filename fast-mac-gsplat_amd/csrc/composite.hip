@@ -39,7 +39,8 @@
 //   g_mean = g_power (a dx + b dy, b dx + c dy), g_opacity = g_raw exp(power),
 //   gT <- gT + alpha (<g,c> - gT).
 // Per lane only S0 = sum g_power, S1 = sum g_power dy, S2 = sum g_power dy^2
-// (dx is shared by the lane's pixels) and the colour/opacity sums are kept;
+// (dx is shared by the lane's pixels) and the colour sums are kept (the
+// opacity gradient is sum g_raw exp(power) = S0 / o);
 // the nine per-splat values are formed from them and reduced across the
 // wavefront by a transposed butterfly: two rounds of half-wave register swaps
 // (v_permlane32_swap / v_permlane16_swap) fold eight values into two
@@ -180,23 +181,27 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
   const TileCoord tc = tile_coord(P);
   const int x = tc.x0 + tc.lx;
   const float px = (float)x + 0.5f;
+  // A pixel is alive while T > transmittance_threshold (< 1, checked on the
+  // host); pixels outside the image start at T = 0 and are never written.
+  const float t_thr = P.trans_thr;
+  const float max_alpha = fminf(P.max_alpha, 1.0f);
   float py[kPix], T[kPix], cr[kPix], cg[kPix], cb[kPix];
   int last[kPix];
-  bool valid[kPix], alive[kPix];
+  bool valid[kPix];
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
     const int y = slot_y(tc, k);
     valid[k] = (x < P.width) && (y < P.height);
     py[k] = (float)y + 0.5f;
-    T[k] = 1.0f;
+    T[k] = valid[k] ? 1.0f : 0.0f;
     cr[k] = cg[k] = cb[k] = 0.0f;
     last[k] = 0;
-    alive[k] = valid[k];
   }
   const int start = tile_offsets[tc.tile];
   const int end = tile_offsets[tc.tile + 1];
   for (int base = start; base < end; base += kBatch) {
-    const bool any_alive = alive[0] | alive[1] | alive[2] | alive[3];
+    const bool any_alive = (T[0] > t_thr) | (T[1] > t_thr) | (T[2] > t_thr) |
+                           (T[3] > t_thr);
     if (!__any(any_alive)) break;
     const int n = min(kBatch, end - base);
     __syncthreads();
@@ -215,18 +220,17 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
         if (!((mask >> k) & 1u)) continue;  // scalar branch
-        if (alive[k]) {
+        if (T[k] > t_thr) {
           const float p = splat_exponent(Adxdx, Bdx, a1.x, py[k] - a0.y);
           if (p <= 0.0f && p >= plim) {
             const float alpha =
-                fminf(P.max_alpha, a1.y * __builtin_amdgcn_exp2f(p));
+                fminf(max_alpha, a1.y * __builtin_amdgcn_exp2f(p));
             const float w = T[k] * alpha;
             cr[k] += w * a1.z;
             cg[k] += w * a1.w;
             cb[k] += w * a2.x;
             T[k] *= (1.0f - alpha);
             last[k] = idx1;
-            if (T[k] <= P.trans_thr) alive[k] = false;
           }
         }
       }
@@ -304,13 +308,14 @@ __device__ __forceinline__ float wave_sum4(float v0, float v1, float v2,
   return row_sum_dpp(__uint_as_float(s[0]) + __uint_as_float(s[1]));
 }
 
-// Where lanes 0, 16, 32 and 48 send their reduced values.  Register 1 rows
-// hold {V_mx, V_ca, V_my, V_cb}, register 2 rows {V_cc, V_g, V_r, V_b}, and
-// row 3 of register 3 holds V_o (see the backward kernel for the values).
+// Where lanes 0, 16, 32 and 48 (the row heads) send their reduced values.
+// Register 1 rows hold {V_mx, V_ca, V_my, V_cb}, register 2 rows
+// {V_cc, V_g, V_r, V_b}, and row 3 of register 3 holds S0 (see the backward
+// kernel for the values).  A row's destination is base + orig * stride floats.
 struct AtomicRole {
   float* base1;
   float* base2;
-  int stride1, stride2;
+  bool stride3;  // register 1 target has 3 floats per splat (else 2)
   float scale1, scale2;
 };
 
@@ -322,20 +327,20 @@ __device__ __forceinline__ AtomicRole atomic_role(float* g_means2d,
   AtomicRole r;
   switch (threadIdx.x >> 4) {
     case 0:
-      r.base1 = g_means2d + 0; r.stride1 = 2; r.scale1 = kMeanScale;
-      r.base2 = g_conics + 2;  r.stride2 = 3; r.scale2 = -0.5f;
+      r.base1 = g_means2d + 0; r.stride3 = false; r.scale1 = kMeanScale;
+      r.base2 = g_conics + 2; r.scale2 = -0.5f;
       break;
     case 1:
-      r.base1 = g_conics + 0;  r.stride1 = 3; r.scale1 = -0.5f;
-      r.base2 = g_colors + 1;  r.stride2 = 3; r.scale2 = 1.0f;
+      r.base1 = g_conics + 0; r.stride3 = true; r.scale1 = -0.5f;
+      r.base2 = g_colors + 1; r.scale2 = 1.0f;
       break;
     case 2:
-      r.base1 = g_means2d + 1; r.stride1 = 2; r.scale1 = kMeanScale;
-      r.base2 = g_colors + 0;  r.stride2 = 3; r.scale2 = 1.0f;
+      r.base1 = g_means2d + 1; r.stride3 = false; r.scale1 = kMeanScale;
+      r.base2 = g_colors + 0; r.scale2 = 1.0f;
       break;
     default:
-      r.base1 = g_conics + 1;  r.stride1 = 3; r.scale1 = -1.0f;
-      r.base2 = g_colors + 2;  r.stride2 = 3; r.scale2 = 1.0f;
+      r.base1 = g_conics + 1; r.stride3 = true; r.scale1 = -1.0f;
+      r.base2 = g_colors + 2; r.scale2 = 1.0f;
       break;
   }
   return r;
@@ -356,6 +361,7 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
   const int start = tile_offsets[tc.tile];
   const AtomicRole role = atomic_role(g_means2d, g_conics, g_colors);
   const bool row_head = (threadIdx.x & 15) == 0;
+  const float max_alpha = fminf(P.max_alpha, 1.0f);
   const int x = tc.x0 + tc.lx;
   const float px = (float)x + 0.5f;
   float py[kPix], Tc[kPix], gr[kPix], gg[kPix], gb[kPix], gT[kPix];
@@ -379,6 +385,9 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
     }
     gT[k] = gr[k] * P.bg_r + gg[k] * P.bg_g + gb[k] * P.bg_b;
   }
+  // Per-lane partial sums of the current splat; zero between splats.
+  float S0 = 0.f, S1 = 0.f, S2 = 0.f;
+  float acc_r = 0.f, acc_g = 0.f, acc_b = 0.f;
   for (int cend = nstop; cend > 0; cend -= kBatch) {
     const int cstart = max(0, cend - kBatch);
     const int n = cend - cstart;
@@ -395,8 +404,6 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
       const float dx = px - a0.x;
       float Adxdx, Bdx;
       x_terms(a0.z, a0.w, dx, Adxdx, Bdx);
-      float S0 = 0.f, S1 = 0.f, S2 = 0.f;
-      float acc_r = 0.f, acc_g = 0.f, acc_b = 0.f, acc_o = 0.f;
       bool contrib = false;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
@@ -408,23 +415,23 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
             contrib = true;
             const float e = __builtin_amdgcn_exp2f(p);
             const float raw = a1.y * e;
-            const float alpha = fminf(P.max_alpha, raw);
-            // alpha <= max_alpha < 1, so 1 - alpha > 0
+            const bool open = raw < max_alpha;  // gradient gate
+            const float alpha = open ? raw : max_alpha;
+            // 1 - alpha >= 1 - max_alpha >= eps (checked on the host), so the
+            // reference's max(1 - alpha, eps) is 1 - alpha.
             const float T_prev =
-                Tc[k] * __builtin_amdgcn_rcpf(fmaxf(1.0f - alpha, P.eps));
+                Tc[k] * __builtin_amdgcn_rcpf(1.0f - alpha);
             const float dot_gc = gr[k] * a1.z + gg[k] * a1.w + gb[k] * a2.x;
             const float diff = dot_gc - gT[k];
             const float wgt = T_prev * alpha;
             acc_r += gr[k] * wgt;
             acc_g += gg[k] * wgt;
             acc_b += gb[k] * wgt;
-            const float g_raw = (raw < P.max_alpha) ? T_prev * diff : 0.0f;
-            const float g_pow = g_raw * raw;
+            const float g_pow = open ? (T_prev * diff) * raw : 0.0f;
             const float hdy = g_pow * dy;
             S0 += g_pow;
             S1 += hdy;
             S2 += hdy * dy;
-            acc_o += g_raw * e;
             gT[k] += alpha * diff;
             Tc[k] = T_prev;
           }
@@ -433,23 +440,31 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
       if (__any(contrib)) {
         // Per-lane parts of the splat's gradients (a, b, c = -2A/L, -B/L,
         // -2C/L): g_mean = -(2/L) (V_mx, V_my), g_conic = (-V_ca/2, -V_cb,
-        // -V_cc/2).
+        // -V_cc/2) with V_cc = S2, and g_opacity = sum g_raw exp(power) =
+        // (sum g_power) / o = S0 / o.
         const float X = dx * S0;             // sum g_power dx
         const float hB = 0.5f * a0.w;
         const float V_mx = a0.z * X + hB * S1;
         const float V_my = hB * X + a1.x * S1;
         const float V_ca = dx * X;           // sum g_power dx^2
         const float V_cb = dx * S1;          // sum g_power dx dy
+        const float r3 = wave_sum_row3(S0);
         const float r1 = wave_sum4(V_mx, V_my, V_ca, V_cb);
         const float r2 = wave_sum4(S2, acc_r, acc_g, acc_b);
-        const float r3 = wave_sum_row3(acc_o);
+        S0 = S1 = S2 = 0.f;
+        acc_r = acc_g = acc_b = 0.f;
         if (row_head) {
-          const int orig = (int)uniform_bits(a2.y);
-          unsafeAtomicAdd(role.base1 + (int64_t)orig * role.stride1,
-                          r1 * role.scale1);
-          unsafeAtomicAdd(role.base2 + (int64_t)orig * role.stride2,
-                          r2 * role.scale2);
-          if (threadIdx.x == 48) unsafeAtomicAdd(g_opac + orig, r3);
+          const uint32_t orig = uniform_bits(a2.y);
+          const uint64_t off2 = (uint64_t)orig * 8u;   // bytes, 2 floats
+          const uint64_t off3 = (uint64_t)orig * 12u;  // bytes, 3 floats
+          float* p1 = reinterpret_cast<float*>(
+              reinterpret_cast<char*>(role.base1) + (role.stride3 ? off3 : off2));
+          float* p2 = reinterpret_cast<float*>(
+              reinterpret_cast<char*>(role.base2) + off3);
+          unsafeAtomicAdd(p1, r1 * role.scale1);
+          unsafeAtomicAdd(p2, r2 * role.scale2);
+          if (threadIdx.x == 48)
+            unsafeAtomicAdd(g_opac + orig, r3 * __builtin_amdgcn_rcpf(a1.y));
         }
       }
     }

@@ -56,6 +56,11 @@ def test_workspace_queries():
     ("height", 0, "must be > 0"),
     ("batch", 0, "must be > 0"),
     ("gaussians_per_batch", -3, "must be > 0"),
+    ("max_alpha", 1.0, "max_alpha must lie in [0, 1)"),
+    ("max_alpha", float("nan"), "max_alpha must lie in [0, 1)"),
+    ("eps", 0.5, "1 - max_alpha >= eps"),
+    ("transmittance_threshold", 1.0, "transmittance_threshold must lie in [0, 1)"),
+    ("transmittance_threshold", -0.5, "transmittance_threshold must lie in [0, 1)"),
 ])
 def test_invalid_meta_rejected_before_launch(field, value, msg):
     L = _lib.lib()
