@@ -42,6 +42,10 @@ for _p in (ROOT, os.path.join(ROOT, "fast-mac-gsplat_amd")):
 KEYS = ("means2d", "conics", "colors", "opacities", "depths")
 PEAK_FP32_TFLOPS = 157.3   # MI355X published fp32 peak
 PEAK_HBM_GBS = 8000.0      # MI355X published HBM3E bandwidth
+# The reference's best published cfg2 forward+backward: 65.754 ms on an Apple
+# M4 (v8_direct; benchmarks/full_rasterizer_benchmark_v8_prior_compare_4k64k.md:34)
+# = 4096*4096 / 65.754 ms = 255.15 Mpix/s.
+REFERENCE_MPIX_S = {2: 4096 * 4096 / 65.754e-3 / 1e6}
 # Algorithmic work per unit (per (pixel, tile-pair) evaluation inside a tile's
 # processed range, upper bound 256 per pair): forward ~24 FLOP, backward ~60.
 FLOP_PER_EVAL = {"render_forward": 24.0, "render_backward": 60.0}
@@ -222,7 +226,8 @@ def main() -> int:
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": None,
+        "vs_baseline": (round(mpix / REFERENCE_MPIX_S[args.config], 2)
+                        if args.config in REFERENCE_MPIX_S else None),
         "dtype": "f32",
         "data": "synthetic (seeded BASELINE config scene, generated on CPU, resident in HBM)",
         "config": {
