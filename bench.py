@@ -162,24 +162,38 @@ def main() -> int:
     import numpy as np
     import torch
 
-    from torch_gsplat_bridge_fast import RasterConfig, _ops, rasterize_projected_gaussians
-    from torch_gsplat_bridge_fast.scenes import CONFIGS, make_scene_2d
+    from torch_gsplat_bridge_fast import (RasterConfig, _ops, project_pinhole_gaussians,
+                                          rasterize_pinhole_gaussians, rasterize_projected_gaussians)
+    from torch_gsplat_bridge_fast.scenes import CONFIGS, make_scene_2d, make_scene_3d
 
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
-    sc = make_scene_2d(args.config, seed=0)
+    three_d = CONFIGS[args.config]["kind"] == "3d"
+    if three_d:
+        # Config 4: projection + rasterization, gradients to means3d/scales/quats/opacities.
+        sc = make_scene_3d(seed=0)
+        keys3 = ("means3d", "scales", "quats", "opacities")
+        leaves = [sc[k].to(dev).requires_grad_(True) for k in keys3]
+        colors3 = sc["colors"].to(dev)
+        c2w = sc["camera_to_world"].to(dev)
+        cam = (sc["fx"], sc["fy"], sc["cx"], sc["cy"])
+    else:
+        sc = make_scene_2d(args.config, seed=0)
+        leaves = [sc[k].to(dev).requires_grad_(k != "depths") for k in KEYS]
     H, W, B, G = sc["H"], sc["W"], sc["B"], sc["G"]
-    leaves = [sc[k].to(dev).requires_grad_(k != "depths") for k in KEYS]
     w_cpu = torch.rand(B, H, W, 3, generator=torch.Generator().manual_seed(123))
     w = w_cpu.to(dev)
     cfg = RasterConfig(height=H, width=W)
 
     def step():
-        for t in leaves[:4]:
+        for t in leaves:
             t.grad = None
-        img = rasterize_projected_gaussians(*leaves, cfg)
+        if three_d:
+            img = rasterize_pinhole_gaussians(*leaves, colors3, *cam, camera_to_world=c2w, config=cfg)
+        else:
+            img = rasterize_projected_gaussians(*leaves, cfg)
         img.backward(w)
 
     for _ in range(args.warmup):
@@ -202,9 +216,14 @@ def main() -> int:
     op_ms = {k: float(np.mean(v)) for k, v in per_op.items()}
 
     with torch.no_grad():
+        if three_d:
+            m2, cq, op, dp = project_pinhole_gaussians(*leaves, *cam, camera_to_world=c2w)
+            flat = (m2, cq, colors3, op, dp)
+        else:
+            flat = leaves
         st = _ops.bin_gaussians(
             __import__("torch_gsplat_bridge_fast.rasterize", fromlist=["_meta"])._meta(cfg, B, G),
-            *(t.detach().reshape(B * G, -1).squeeze(-1).contiguous() for t in leaves))
+            *(t.detach().reshape(B * G, -1).squeeze(-1).contiguous() for t in flat))
     n_pairs = st.n_pairs
     evals = 256.0 * n_pairs
     dom = max(("render_forward", "render_backward"), key=lambda k: op_ms.get(k, 0.0))
@@ -249,7 +268,7 @@ def main() -> int:
             "work": f"256 * tile_pairs evaluations x {FLOP_PER_EVAL[dom]:.0f} FLOP per launch",
         },
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not three_d:
         line["cpu_baseline"] = cpu_baseline({k: sc[k] for k in KEYS}, H, W, B, G, w_cpu.numpy())
     print(json.dumps(line), flush=True)
     return 0

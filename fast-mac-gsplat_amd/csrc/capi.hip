@@ -406,21 +406,34 @@ int gsplat_hip_project_backward(
     const float* quats, const float* opacities, const float* camera_to_world,
     const float* camera_params, float* g_means3d, float* g_scales,
     float* g_quats, float* g_opacities, float* g_camera_to_world,
-    float* g_camera_params, void* stream) {
+    float* g_camera_params, void* workspace, size_t workspace_bytes,
+    void* stream) {
   gs::ProjectParams P;
   int rc = make_project_params(meta, P);
   if (rc) return rc;
   rc = null_check({grad_means2d, grad_conics, grad_opacities, grad_depths,
                    means3d, scales, quats, opacities, camera_to_world,
                    camera_params, g_means3d, g_scales, g_quats, g_opacities,
-                   g_camera_to_world, g_camera_params},
+                   g_camera_to_world, g_camera_params, workspace},
                   "gsplat_hip_project_backward");
   if (rc) return rc;
+  if (workspace_bytes < gs::project_backward_workspace_bytes(P)) {
+    gs::set_error("gsplat_hip_project_backward: workspace too small (%zu < %zu)",
+                  workspace_bytes, gs::project_backward_workspace_bytes(P));
+    return GSPLAT_ERR_WORKSPACE;
+  }
   return gs::launch_project_backward(
       P, grad_means2d, grad_conics, grad_opacities, grad_depths, means3d,
       scales, quats, opacities, camera_to_world, camera_params, g_means3d,
       g_scales, g_quats, g_opacities, g_camera_to_world, g_camera_params,
-      static_cast<hipStream_t>(stream));
+      workspace, static_cast<hipStream_t>(stream));
+}
+
+size_t gsplat_hip_project_backward_workspace_bytes(
+    const gsplat_project_meta* meta) {
+  gs::ProjectParams P;
+  if (make_project_params(meta, P)) return 0;
+  return gs::project_backward_workspace_bytes(P);
 }
 
 size_t gsplat_hip_scan_workspace_bytes(int64_t n) {

@@ -141,7 +141,10 @@ int launch_project_backward(const ProjectParams& P, const float* g_means2d,
                             const float* opacities, const float* c2w,
                             const float* cam, float* g_means3d,
                             float* g_scales, float* g_quats, float* g_opac,
-                            float* g_c2w, float* g_cam, hipStream_t stream);
+                            float* g_c2w, float* g_cam, void* workspace,
+                            hipStream_t stream);
+// Camera-gradient partial sums: B * ceil(G/256) * 16 floats.
+size_t project_backward_workspace_bytes(const ProjectParams& P);
 
 // Maps a linear workgroup id onto a linear work index so that the 8 XCDs of
 // an MI355X (which receive workgroups round-robin) each process one

@@ -18,8 +18,9 @@
 //   dSigma = W dSigma_c W^T, dW += 2 Sigma W dSigma_c + (x - t) dx_c^T
 //   dM = 2 dSigma M, dR = dM diag(s), ds_c = sum_a dM[a][c] R[a][c]
 // plus dR/dq; the det clamp blocks the det gradient when it is active
-// (reference :338-342).  Camera gradients are reduced across the
-// wavefront and added with one atomic per entry and wavefront.
+// (reference :338-342).  Camera gradients are summed per workgroup (one
+// image per workgroup) into a workspace and reduced by a second launch in a
+// fixed order, without atomics.
 #include "gs_internal.h"
 
 namespace gs {
@@ -182,12 +183,13 @@ __global__ __launch_bounds__(kThreads) void project_bwd_kernel(
     const float* __restrict__ opacities, const float* __restrict__ c2w,
     const float* __restrict__ cam, float* __restrict__ out_g_means3d,
     float* __restrict__ out_g_scales, float* __restrict__ out_g_quats,
-    float* __restrict__ out_g_opac, float* __restrict__ out_g_c2w,
-    float* __restrict__ out_g_cam) {
-  const int gid = blockIdx.x * kThreads + threadIdx.x;
-  const bool active = gid < P.num_splats;
-  const int g = active ? gid : (P.num_splats - 1);
-  const int b = g / P.gpb;
+    float* __restrict__ out_g_opac, float* __restrict__ cam_partials) {
+  // Workgroup (x, b) handles splats x*256 .. x*256+255 of image b, so its
+  // camera-gradient partial sums belong to one camera.
+  const int b = blockIdx.y;
+  const int local = blockIdx.x * kThreads + threadIdx.x;
+  const bool active = local < P.gpb;
+  const int g = b * P.gpb + (active ? local : (P.gpb - 1));
   const Camera C = load_camera(c2w, cam, b);
   ProjState S;
   project_state(P, C, means3d, scales, quats, g, S);
@@ -343,26 +345,47 @@ __global__ __launch_bounds__(kThreads) void project_bwd_kernel(
   cv[13] = active ? g_fy : 0.0f;
   cv[14] = active ? g_cx : 0.0f;
   cv[15] = active ? g_cy : 0.0f;
-  // Is the whole wavefront inside one image?  (G need not be a multiple of
-  // 64, so a wave can straddle two images.)
-  const int b_first = __shfl(b, 0, 64);
-  const bool uniform = __all(b == b_first);
-  if (uniform) {
+  // Workgroup sum of the 16 values -> cam_partials[(b * nbx + x) * 16 + v].
+  __shared__ float part[kThreads / 64][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) cv[v] = wave_sum(cv[v]);
-    if ((threadIdx.x & 63) != 0) return;
-  } else if (!active) {
-    return;
+  for (int v = 0; v < 16; ++v) {
+    const float sv = wave_sum(cv[v]);
+    if (lane == 0) part[wave][v] = sv;
   }
-  float* gc2w = out_g_c2w + 16 * b;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float sum = 0.0f;
 #pragma unroll
-  for (int a = 0; a < 3; ++a) {
-#pragma unroll
-    for (int j = 0; j < 3; ++j) unsafeAtomicAdd(&gc2w[4 * a + j], cv[3 * a + j]);
-    unsafeAtomicAdd(&gc2w[4 * a + 3], cv[9 + a]);
+    for (int w = 0; w < kThreads / 64; ++w) sum += part[w][threadIdx.x];
+    cam_partials[((int64_t)b * gridDim.x + blockIdx.x) * 16 + threadIdx.x] = sum;
   }
-#pragma unroll
-  for (int v = 0; v < 4; ++v) unsafeAtomicAdd(&out_g_cam[4 * b + v], cv[12 + v]);
+}
+
+// One workgroup per image: sums the nbx workgroup partials of each of the 16
+// camera-gradient values (fixed order, no atomics) and writes
+// g_camera_to_world [B,4,4] (rotation 3x3, translation column, zero last row)
+// and g_camera_params [B,4].
+__global__ __launch_bounds__(kThreads) void project_cam_reduce_kernel(
+    const float* __restrict__ cam_partials, int nbx, float* __restrict__ g_c2w,
+    float* __restrict__ g_cam) {
+  __shared__ float red[kThreads];
+  const int b = blockIdx.x;
+  const int v = threadIdx.x & 15, slot = threadIdx.x >> 4;  // 16 slots
+  float sum = 0.0f;
+  for (int x = slot; x < nbx; x += kThreads / 16)
+    sum += cam_partials[((int64_t)b * nbx + x) * 16 + v];
+  red[threadIdx.x] = sum;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float total = 0.0f;
+    for (int k = 0; k < kThreads / 16; ++k) total += red[k * 16 + v];
+    float* gc2w = g_c2w + 16 * b;
+    if (v < 9) gc2w[4 * (v / 3) + (v % 3)] = total;        // rotation
+    else if (v < 12) gc2w[4 * (v - 9) + 3] = total;         // translation
+    else g_cam[4 * b + (v - 12)] = total;                   // fx, fy, cx, cy
+    if (v < 4) gc2w[12 + v] = 0.0f;                         // last row
+  }
 }
 
 }  // namespace
@@ -381,6 +404,11 @@ int launch_project_forward(const ProjectParams& P, const float* means3d,
   return check_launch("project_fwd_kernel");
 }
 
+size_t project_backward_workspace_bytes(const ProjectParams& P) {
+  const int64_t nbx = (P.gpb + kThreads - 1) / kThreads;
+  return align_up((size_t)(P.batch * nbx * 16) * sizeof(float), 256);
+}
+
 int launch_project_backward(const ProjectParams& P, const float* g_means2d,
                             const float* g_conics, const float* g_opac_out,
                             const float* g_depths, const float* means3d,
@@ -388,17 +416,24 @@ int launch_project_backward(const ProjectParams& P, const float* g_means2d,
                             const float* opacities, const float* c2w,
                             const float* cam, float* g_means3d,
                             float* g_scales, float* g_quats, float* g_opac,
-                            float* g_c2w, float* g_cam, hipStream_t stream) {
-  int rc = launch_fill_f32(g_c2w, 0.0f, 16 * (int64_t)P.batch, stream);
-  if (!rc) rc = launch_fill_f32(g_cam, 0.0f, 4 * (int64_t)P.batch, stream);
+                            float* g_c2w, float* g_cam, void* workspace,
+                            hipStream_t stream) {
+  if (P.num_splats == 0) {
+    int rc = launch_fill_f32(g_c2w, 0.0f, 16 * (int64_t)P.batch, stream);
+    if (!rc) rc = launch_fill_f32(g_cam, 0.0f, 4 * (int64_t)P.batch, stream);
+    return rc;
+  }
+  const int nbx = (P.gpb + kThreads - 1) / kThreads;
+  float* partials = static_cast<float*>(workspace);
+  hipLaunchKernelGGL(project_bwd_kernel, dim3((unsigned)nbx, (unsigned)P.batch),
+                     dim3(kThreads), 0, stream, P, g_means2d, g_conics,
+                     g_opac_out, g_depths, means3d, scales, quats, opacities,
+                     c2w, cam, g_means3d, g_scales, g_quats, g_opac, partials);
+  int rc = check_launch("project_bwd_kernel");
   if (rc) return rc;
-  if (P.num_splats == 0) return GSPLAT_OK;
-  const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
-  hipLaunchKernelGGL(project_bwd_kernel, dim3(grid), dim3(kThreads), 0, stream,
-                     P, g_means2d, g_conics, g_opac_out, g_depths, means3d,
-                     scales, quats, opacities, c2w, cam, g_means3d, g_scales,
-                     g_quats, g_opac, g_c2w, g_cam);
-  return check_launch("project_bwd_kernel");
+  hipLaunchKernelGGL(project_cam_reduce_kernel, dim3((unsigned)P.batch),
+                     dim3(kThreads), 0, stream, partials, nbx, g_c2w, g_cam);
+  return check_launch("project_cam_reduce_kernel");
 }
 
 }  // namespace gs

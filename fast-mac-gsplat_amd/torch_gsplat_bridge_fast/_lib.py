@@ -69,7 +69,8 @@ SIGNATURES = {
     "gsplat_hip_render_forward": (ctypes.c_int, [_PM] + [_vp] * 7 + [_vp]),
     "gsplat_hip_render_backward": (ctypes.c_int, [_PM] + [_vp] * 11 + [_vp]),
     "gsplat_hip_project_forward": (ctypes.c_int, [_PP] + [_vp] * 10 + [_vp]),
-    "gsplat_hip_project_backward": (ctypes.c_int, [_PP] + [_vp] * 16 + [_vp]),
+    "gsplat_hip_project_backward_workspace_bytes": (_sz, [_PP]),
+    "gsplat_hip_project_backward": (ctypes.c_int, [_PP] + [_vp] * 16 + [_vp, _sz, _vp]),
     "gsplat_hip_scan_workspace_bytes": (_sz, [_i64]),
     "gsplat_hip_exclusive_scan_i32": (ctypes.c_int, [_vp, _vp, _i64, _vp, _sz, _vp]),
     "gsplat_hip_radix_sort_workspace_bytes": (_sz, [_i64, _i32]),

@@ -182,10 +182,13 @@ def project_backward(meta: _lib.ProjectMeta, g_m2, g_cq, g_op, g_dp, means3d, sc
     go = torch.empty((BG,), dtype=torch.float32, device=dev)
     gc2w = torch.empty((B, 4, 4), dtype=torch.float32, device=dev)
     gcam = torch.empty((B, 4), dtype=torch.float32, device=dev)
+    wsb = L.gsplat_hip_project_backward_workspace_bytes(meta)
+    ws = _empty(max(wsb, 1), torch.uint8, dev)
     with _timed("project_backward"):
         check(L.gsplat_hip_project_backward(meta, ptr(g_m2), ptr(g_cq), ptr(g_op), ptr(g_dp), ptr(means3d),
                                             ptr(scales), ptr(quats), ptr(opacities), ptr(c2w), ptr(cam), ptr(gm3),
-                                            ptr(gs), ptr(gq), ptr(go), ptr(gc2w), ptr(gcam), stream_of(means3d)),
+                                            ptr(gs), ptr(gq), ptr(go), ptr(gc2w), ptr(gcam), ptr(ws), wsb,
+                                            stream_of(means3d)),
               "gsplat_hip_project_backward")
     return gm3, gs, gq, go, gc2w, gcam
 

@@ -193,10 +193,15 @@ int gsplat_hip_project_forward(const gsplat_project_meta* meta,
                                float* out_opacities, float* out_depths,
                                void* stream);
 
+/* Bytes of the workspace of gsplat_hip_project_backward (camera-gradient
+ * partial sums, B * ceil(G/256) * 16 floats). */
+size_t gsplat_hip_project_backward_workspace_bytes(
+    const gsplat_project_meta* meta);
+
 /* Vector-Jacobian product of gsplat_hip_project_forward.  Per-splat grads are
- * written directly; g_camera_to_world [B,4,4] and g_camera_params [B,4] are
- * zeroed by this call and accumulated atomically (one atomic per wavefront
- * and entry after an in-wave reduction). */
+ * written directly; g_camera_to_world [B,4,4] (last row zero) and
+ * g_camera_params [B,4] are overwritten with the camera gradients, summed
+ * per workgroup into the workspace and then in a fixed order (no atomics). */
 int gsplat_hip_project_backward(const gsplat_project_meta* meta,
                                 const float* grad_means2d,
                                 const float* grad_conics,
@@ -210,6 +215,7 @@ int gsplat_hip_project_backward(const gsplat_project_meta* meta,
                                 float* g_quats, float* g_opacities,
                                 float* g_camera_to_world,
                                 float* g_camera_params,
+                                void* workspace, size_t workspace_bytes,
                                 void* stream);
 
 /* ------------------------------------------------------------- primitives

@@ -92,6 +92,11 @@ def test_workspace_too_small_rejected():
     assert rc == 3 and "bin_pack" in L.gsplat_hip_last_error().decode()
     rc = L.gsplat_hip_bin_emit(_meta(), one, one, one, 10, one, one, 1, one, 1, None)
     assert rc == 3
+    pm = _lib.make_project_meta(2, 1000, 1e-4)
+    need = L.gsplat_hip_project_backward_workspace_bytes(pm)
+    assert need >= 2 * 4 * 16 * 4          # B * ceil(G/256) * 16 floats
+    rc = L.gsplat_hip_project_backward(pm, *([one] * 16), one, need - 1, None)
+    assert rc == 3 and "project_backward" in L.gsplat_hip_last_error().decode()
 
 
 def test_projection_meta_rejected():
