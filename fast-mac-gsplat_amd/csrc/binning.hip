@@ -1,22 +1,33 @@
-// binning.hip -- per-splat tile intersection count, record packing, and
-// deterministic (tile, gid) pair emission.
+// binning.hip -- per-splat tile-hit counts, record packing, deterministic
+// (tile, gid) pair emission and tile-range extraction.
 //
 // This translation unit is compiled with -ffp-contract=off: the predicate
 // results must match the CPU oracle bit for bit.
 //
-// count_kernel  one thread per splat in the original order: counts the tiles
-//   whose pixel-centre rectangle meets the splat's alpha >= threshold ellipse
-//   (reference count_tiles, variants/v8/csrc/metal/gsplat_v8_kernels.metal:
-//   244-288) and bumps the per-tile pair counters.
-// pack_kernel   one thread per depth-sorted splat (gid): writes the packed
-//   48-byte record and the exclusive per-gid pair offsets (workgroup scan +
-//   decoupled look-back in the same launch).
-// emit_kernel   one thread per gid; repeats the same tile walk and writes
-//   (tile, gid) at splat_offsets[gid] + k, so pairs land in ascending gid
-//   order (reference emit_binned_ids, :290-327, which uses per-tile atomic
-//   cursors and therefore needs a later per-tile sort).  The same launch also
-//   prepares the pair sort: it zeroes the sort's look-back status and
-//   accumulates its per-pass digit histograms from the tile counts.
+// Tile walk (count_kernel and emit_kernel).  The candidate tiles of a splat
+// are the tiles of its snug pixel bbox, row-major; a candidate is a hit when
+// the tile's pixel-centre rectangle meets the splat's alpha >= threshold
+// ellipse (reference count_tiles / emit_binned_ids,
+// variants/v8/csrc/metal/gsplat_v8_kernels.metal:244-327).  A wavefront takes
+// 64 splats, prefix-sums their candidate counts in registers and then tests
+// 64 candidates per step whatever splats they belong to (each lane finds its
+// candidate's splat by binary search over the prefix sums in LDS), so a splat
+// with thousands of candidate tiles no longer serialises one lane.
+//
+// count_kernel  original order: per-splat hit counts and per-workgroup sums
+//   (sum_kernel turns them into the pair count N).
+// pack_kernel   one thread per depth-sorted splat (gid): packed 48-byte
+//   record and exclusive per-gid pair offsets (workgroup scan + decoupled
+//   look-back in the same launch).
+// emit_kernel   gid order: each hit claims a slot in its splat's range
+//   [splat_offsets[gid], splat_offsets[gid+1]) and writes (tile, gid); the
+//   same launch zeroes the pair sort's look-back status and counts the pair
+//   sort's digit histograms per workgroup (reduced by hist_reduce_kernel).
+//   Pairs of one splat have distinct tiles and splats occupy consecutive
+//   ranges in gid order, so a stable sort by tile yields (tile, gid) order
+//   whatever order the slots inside a splat's range were claimed in.
+// ranges_kernel / counts_kernel  tile_offsets and tile_counts from the
+//   sorted tile keys (the reference reads them from its atomic counters).
 #include "gs_internal.h"
 #include "gs_predicate.h"
 #include "lookback.h"
@@ -30,57 +41,156 @@ struct SplatGeom {
   float mx, my, a, b, c, o;
 };
 
-// Walks the tiles of one splat's snug bbox in row-major order and calls
-// fn(global_tile, k) for the k-th tile that passes the exact ellipse/rect test.
-template <typename Fn>
-__device__ __forceinline__ int for_each_hit_tile(const RasterParams& P,
-                                                 const SplatGeom& s, int batch,
-                                                 Fn&& fn) {
+constexpr int kWaves = kThreads / 64;
+
+// One wavefront's 64 splats, staged for the cooperative tile walk.
+struct WalkSlots {
+  float4 g0[64];  // mx, my, a, b
+  float4 g1[64];  // c, tau, kc, ka
+  int4 box[64];   // tx0, ty0, tiles per bbox row, first tile of the image
+  int flags[64];  // bit 0: use_c, bit 1: use_a
+  int cend[64];   // inclusive prefix sum of candidate counts
+  int cnt[64];    // hits found so far
+};
+
+// Stages this lane's splat and returns the wavefront's candidate total.
+// Candidate counts fit in int32: tiles per image are limited to 2^24 on the
+// host, so a wavefront has at most 2^30 candidates.
+__device__ __forceinline__ int walk_setup(const RasterParams& P, bool valid,
+                                          const SplatGeom& s, int batch,
+                                          WalkSlots& W) {
 #pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  int ncand = 0;
+  int4 box = make_int4(0, 0, 1, 0);
+  float4 g1 = make_float4(s.c, 0.0f, 0.0f, 0.0f);
+  int flags = 0;
   float tau;
-  if (!alpha_support(s.o, P.alpha_thr, P.eps, tau)) return 0;
-  const PixBox bb =
-      snugbox(s.mx, s.my, s.a, s.b, s.c, tau, P.width, P.height, P.eps);
-  if (bb.x0 > bb.x1 || bb.y0 > bb.y1) return 0;
-  const int tx0 = bb.x0 >> 4, tx1 = bb.x1 >> 4;
-  const int ty0 = bb.y0 >> 4, ty1 = bb.y1 >> 4;
-  const int tile_base = batch * P.tiles_per_image;
-  const ConicSlopes k = conic_slopes(s.a, s.b, s.c);
-  int n = 0;
-  for (int ty = ty0; ty <= ty1; ++ty) {
-    for (int tx = tx0; tx <= tx1; ++tx) {
-      float rx0, ry0, rx1, ry1;
-      tile_rect(tx, ty, P.width, P.height, rx0, ry0, rx1, ry1);
-      if (ellipse_hits_rect(s.mx, s.my, s.a, s.b, s.c, k, tau, rx0, ry0, rx1,
-                            ry1)) {
-        fn(tile_base + ty * P.tiles_x + tx, n);
-        ++n;
-      }
+  if (valid && alpha_support(s.o, P.alpha_thr, P.eps, tau)) {
+    const PixBox bb =
+        snugbox(s.mx, s.my, s.a, s.b, s.c, tau, P.width, P.height, P.eps);
+    if (bb.x0 <= bb.x1 && bb.y0 <= bb.y1) {
+      const int tx0 = bb.x0 >> 4, tx1 = bb.x1 >> 4;
+      const int ty0 = bb.y0 >> 4, ty1 = bb.y1 >> 4;
+      box = make_int4(tx0, ty0, tx1 - tx0 + 1, batch * P.tiles_per_image);
+      ncand = box.z * (ty1 - ty0 + 1);
+      const ConicSlopes k = conic_slopes(s.a, s.b, s.c);
+      g1 = make_float4(s.c, tau, k.kc, k.ka);
+      flags = (k.use_c ? 1 : 0) | (k.use_a ? 2 : 0);
     }
   }
-  return n;
+  W.g0[lane] = make_float4(s.mx, s.my, s.a, s.b);
+  W.g1[lane] = g1;
+  W.box[lane] = box;
+  W.flags[lane] = flags;
+  W.cnt[lane] = 0;
+  int inc = ncand;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += y;
+  }
+  W.cend[lane] = inc;
+  __builtin_amdgcn_wave_barrier();
+  return __shfl(inc, 63, 64);
 }
 
-// One thread per splat in the ORIGINAL order: tile-hit count into
-// splat_count[orig] and per-tile pair counters (reference count_tiles,
-// gsplat_v8_kernels.metal:244-288).  Runs before the depth sort, so the pair
-// count N = sum(tile_counts) is known while the sort is still running.
+// Tests the wavefront's candidates 64 at a time and calls on_hit(slot, tile)
+// for every hit (slot = 0..63, the splat's lane in walk_setup).
+template <typename Fn>
+__device__ __forceinline__ void walk_candidates(const RasterParams& P,
+                                                const WalkSlots& W, int total,
+                                                Fn&& on_hit) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  for (int c0 = 0; c0 < total; c0 += 64) {
+    const int c = c0 + lane;
+    if (c < total) {
+      // first slot whose inclusive prefix exceeds c
+      int sl = 0;
+#pragma unroll
+      for (int step = 32; step > 0; step >>= 1)
+        if (W.cend[sl + step - 1] <= c) sl += step;
+      const int k = c - (sl == 0 ? 0 : W.cend[sl - 1]);
+      const int4 bx = W.box[sl];
+      const int dy = k / bx.z;
+      const int tx = bx.x + (k - dy * bx.z), ty = bx.y + dy;
+      const float4 g0 = W.g0[sl], g1 = W.g1[sl];
+      const int fl = W.flags[sl];
+      ConicSlopes ks;
+      ks.kc = g1.z;
+      ks.ka = g1.w;
+      ks.use_c = (fl & 1) != 0;
+      ks.use_a = (fl & 2) != 0;
+      float rx0, ry0, rx1, ry1;
+      tile_rect(tx, ty, P.width, P.height, rx0, ry0, rx1, ry1);
+      if (ellipse_hits_rect(g0.x, g0.y, g0.z, g0.w, g1.x, ks, g1.y, rx0, ry0,
+                            rx1, ry1))
+        on_hit(sl, bx.w + ty * P.tiles_x + tx);
+    }
+  }
+}
+
+// Original order: splat_count[orig] = tile hits of splat orig;
+// block_sums[workgroup] = the workgroup's total.
 __global__ __launch_bounds__(kThreads) void count_kernel(
     RasterParams P, const float* __restrict__ means2d,
     const float* __restrict__ conics, const float* __restrict__ opacities,
-    int32_t* __restrict__ splat_count, int32_t* __restrict__ tile_counts) {
+    int32_t* __restrict__ splat_count, int32_t* __restrict__ block_sums,
+    uint32_t* __restrict__ zero_words, int64_t n_zero_words) {
+  __shared__ WalkSlots walk[kWaves];
+  __shared__ int wsum[kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // zero the binning control block (grid-stride; read only by later launches)
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_zero_words;
+       i += (int64_t)gridDim.x * kThreads)
+    zero_words[i] = 0u;
   const int orig = blockIdx.x * kThreads + threadIdx.x;
-  if (orig >= P.num_splats) return;
+  const bool valid = orig < P.num_splats;
+  const int o = valid ? orig : P.num_splats - 1;
   SplatGeom s;
-  s.mx = means2d[2 * orig + 0];
-  s.my = means2d[2 * orig + 1];
-  s.a = conics[3 * orig + 0];
-  s.b = conics[3 * orig + 1];
-  s.c = conics[3 * orig + 2];
-  s.o = opacities[orig];
-  splat_count[orig] = for_each_hit_tile(P, s, orig / P.gpb, [&](int tile, int) {
-    atomicAdd(&tile_counts[tile], 1);
-  });
+  s.mx = means2d[2 * o + 0];
+  s.my = means2d[2 * o + 1];
+  s.a = conics[3 * o + 0];
+  s.b = conics[3 * o + 1];
+  s.c = conics[3 * o + 2];
+  s.o = opacities[o];
+  WalkSlots& W = walk[wave];
+  const int total = walk_setup(P, valid, s, o / P.gpb, W);
+  walk_candidates(P, W, total, [&](int sl, int) { atomicAdd(&W.cnt[sl], 1); });
+  __builtin_amdgcn_wave_barrier();
+  const int n = valid ? W.cnt[lane] : 0;
+  if (valid) splat_count[orig] = n;
+  int v = n;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  if (lane == 0) wsum[wave] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) t += wsum[w];
+    block_sums[blockIdx.x] = t;
+  }
+}
+
+// One workgroup: *pair_count = sum of the n block sums (-1 if it does not fit
+// in int32).
+__global__ __launch_bounds__(kThreads) void sum_kernel(
+    const int32_t* __restrict__ block_sums, int n, int32_t* pair_count) {
+  __shared__ long long part[kThreads];
+  long long v = 0;
+  for (int i = threadIdx.x; i < n; i += kThreads) v += block_sums[i];
+  part[threadIdx.x] = v;
+  __syncthreads();
+  for (int half = kThreads / 2; half > 0; half >>= 1) {
+    if (threadIdx.x < half) part[threadIdx.x] += part[threadIdx.x + half];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const long long total = part[0];
+    *pair_count = total > 0x7fffffffLL ? -1 : (int32_t)total;
+  }
 }
 
 // One thread per depth-sorted splat (gid): gathers the attributes of
@@ -154,45 +264,85 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
 
 __global__ __launch_bounds__(kThreads) void emit_kernel(
     RasterParams P, const float4* __restrict__ packed,
-    const int32_t* __restrict__ splat_offsets,
-    const int32_t* __restrict__ tile_counts, uint32_t* __restrict__ keys,
-    uint32_t* __restrict__ vals, int pair_passes, uint32_t* pair_ghist,
-    uint32_t* pair_status, int64_t pair_status_words) {
+    const int32_t* __restrict__ splat_offsets, uint32_t* __restrict__ keys,
+    uint32_t* __restrict__ vals, int pair_passes,
+    uint32_t* __restrict__ hist_partials, uint32_t* pair_status,
+    int64_t pair_status_words) {
+  __shared__ WalkSlots walk[kWaves];
+  __shared__ int base[kWaves][64];
   __shared__ uint32_t h[4][256];
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   // (1) zero the pair sort's look-back status (grid-stride)
   for (int64_t i = (int64_t)blockIdx.x * kThreads + t; i < pair_status_words;
        i += (int64_t)gridDim.x * kThreads)
     pair_status[i] = 0u;
-  // (2) pair-sort digit histograms from this workgroup's slice of tiles
   for (int i = t; i < 4 * 256; i += kThreads) (&h[0][0])[i] = 0u;
   __syncthreads();
-  const int per = (P.num_tiles + gridDim.x - 1) / gridDim.x;
-  const int t0 = blockIdx.x * per;
-  const int t1 = min(P.num_tiles, t0 + per);
-  for (int tile = t0 + t; tile < t1; tile += kThreads) {
-    const uint32_t c = (uint32_t)tile_counts[tile];
-    if (c == 0u) continue;
-    for (int p = 0; p < pair_passes; ++p)
-      atomicAdd(&h[p][((uint32_t)tile >> (8 * p)) & 255u], c);
-  }
-  __syncthreads();
-  for (int p = 0; p < pair_passes; ++p) {
-    const uint32_t c = h[p][t];
-    if (c) atomicAdd(&pair_ghist[p * 256 + t], c);
-  }
-  // (3) pair emission
+  // (2) pair emission
   const int gid = blockIdx.x * kThreads + t;
-  if (gid >= P.num_splats) return;
-  const float4 p0 = packed[3 * gid + 0];
-  const float4 p1 = packed[3 * gid + 1];
+  const bool valid = gid < P.num_splats;
+  const int g = valid ? gid : P.num_splats - 1;
+  const float4 p0 = packed[3 * g + 0];
+  const float4 p1 = packed[3 * g + 1];
   const SplatGeom s{p0.x, p0.y, p0.z, p0.w, p1.x, p1.y};
-  const int batch = gid / P.gpb;
-  const int64_t base = splat_offsets[gid];
-  for_each_hit_tile(P, s, batch, [&](int tile, int k) {
-    keys[base + k] = (uint32_t)tile;
-    vals[base + k] = (uint32_t)gid;
+  base[wave][lane] = splat_offsets[g];
+  WalkSlots& W = walk[wave];
+  const int total = walk_setup(P, valid, s, g / P.gpb, W);
+  const int gid0 = blockIdx.x * kThreads + wave * 64;
+  walk_candidates(P, W, total, [&](int sl, int tile) {
+    const int slot = atomicAdd(&W.cnt[sl], 1);
+    const int64_t pos = (int64_t)base[wave][sl] + slot;
+    keys[pos] = (uint32_t)tile;
+    vals[pos] = (uint32_t)(gid0 + sl);
+    for (int p = 0; p < pair_passes; ++p)
+      atomicAdd(&h[p][((uint32_t)tile >> (8 * p)) & 255u], 1u);
   });
+  // (3) this workgroup's digit histograms for the pair sort, stored as
+  // hist_partials[(p * 256 + d) * nblk + workgroup]
+  __syncthreads();
+  for (int p = 0; p < pair_passes; ++p)
+    hist_partials[((int64_t)p * 256 + t) * gridDim.x + blockIdx.x] = h[p][t];
+}
+
+// ghist[p][d] = sum over the emit workgroups of their digit-d counts of pass
+// p: one workgroup per (p, d) reads that row of partials contiguously.
+__global__ __launch_bounds__(kThreads) void hist_reduce_kernel(
+    const uint32_t* __restrict__ hist_partials, int nblk,
+    uint32_t* __restrict__ ghist) {
+  __shared__ uint32_t part[kThreads / 64];
+  const uint32_t* row = hist_partials + (int64_t)blockIdx.x * nblk;
+  uint32_t v = 0u;
+  for (int b = threadIdx.x; b < nblk; b += kThreads) v += row[b];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0u;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) t += part[w];
+    ghist[blockIdx.x] = t;   // blockIdx.x = p * 256 + d
+  }
+}
+
+// tile_offsets from the sorted tile keys: index i (0 <= i <= n) is the first
+// pair of every tile t with keys[i-1] < t <= keys[i] (keys[-1] = -1,
+// keys[n] = num_tiles), so tile_offsets[num_tiles] = n.
+__global__ __launch_bounds__(kThreads) void ranges_kernel(
+    const uint32_t* __restrict__ sorted_keys, int64_t n, int num_tiles,
+    int32_t* __restrict__ tile_offsets) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i > n) return;
+  const int64_t prev = (i == 0) ? -1 : (int64_t)sorted_keys[i - 1];
+  const int64_t cur = (i == n) ? (int64_t)num_tiles : (int64_t)sorted_keys[i];
+  for (int64_t t = prev + 1; t <= cur; ++t) tile_offsets[t] = (int32_t)i;
+}
+
+__global__ __launch_bounds__(kThreads) void counts_kernel(
+    const int32_t* __restrict__ tile_offsets, int num_tiles,
+    int32_t* __restrict__ tile_counts) {
+  const int t = blockIdx.x * kThreads + threadIdx.x;
+  if (t < num_tiles) tile_counts[t] = tile_offsets[t + 1] - tile_offsets[t];
 }
 
 __global__ void fill_i32_kernel(int32_t* dst, int32_t v, int64_t n) {
@@ -230,15 +380,24 @@ __global__ void zero_grads_kernel(float* g_m, float* g_q, float* g_c,
 
 }  // namespace
 
+int count_blocks(const RasterParams& P) {
+  return (P.num_splats + kThreads - 1) / kThreads;
+}
+
 int launch_count(const RasterParams& P, const float* means2d,
                  const float* conics, const float* opacities,
-                 int32_t* splat_count, int32_t* tile_counts,
-                 hipStream_t stream) {
-  if (P.num_splats == 0) return GSPLAT_OK;
-  const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
-  hipLaunchKernelGGL(count_kernel, dim3(grid), dim3(kThreads), 0, stream, P,
-                     means2d, conics, opacities, splat_count, tile_counts);
-  return check_launch("count_kernel");
+                 int32_t* splat_count, int32_t* block_sums,
+                 int32_t* pair_count, uint32_t* zero_words,
+                 int64_t n_zero_words, hipStream_t stream) {
+  const int nblk = count_blocks(P);
+  hipLaunchKernelGGL(count_kernel, dim3((unsigned)nblk), dim3(kThreads), 0,
+                     stream, P, means2d, conics, opacities, splat_count,
+                     block_sums, zero_words, n_zero_words);
+  int rc = check_launch("count_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(sum_kernel, dim3(1), dim3(kThreads), 0, stream,
+                     block_sums, nblk, pair_count);
+  return check_launch("sum_kernel");
 }
 
 int launch_pack(const RasterParams& P, const float* means2d,
@@ -260,18 +419,49 @@ int count_scan_blocks(const RasterParams& P) {
   return (P.num_splats + kThreads - 1) / kThreads;
 }
 
+int emit_blocks(const RasterParams& P) {
+  return (P.num_splats + kThreads - 1) / kThreads;
+}
+
 int launch_emit(const RasterParams& P, const float* packed,
-                const int32_t* splat_offsets, const int32_t* tile_counts,
-                uint32_t* keys, uint32_t* vals, int pair_passes,
-                uint32_t* pair_ghist, uint32_t* pair_status,
-                int64_t pair_status_words, hipStream_t stream) {
+                const int32_t* splat_offsets, uint32_t* keys, uint32_t* vals,
+                int pair_passes, uint32_t* hist_partials, uint32_t* pair_ghist,
+                uint32_t* pair_status, int64_t pair_status_words,
+                hipStream_t stream) {
   if (P.num_splats == 0) return GSPLAT_OK;
-  const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
-  hipLaunchKernelGGL(emit_kernel, dim3(grid), dim3(kThreads), 0, stream, P,
-                     reinterpret_cast<const float4*>(packed), splat_offsets,
-                     tile_counts, keys, vals, pair_passes, pair_ghist,
+  const int nblk = emit_blocks(P);
+  hipLaunchKernelGGL(emit_kernel, dim3((unsigned)nblk), dim3(kThreads), 0,
+                     stream, P, reinterpret_cast<const float4*>(packed),
+                     splat_offsets, keys, vals, pair_passes, hist_partials,
                      pair_status, pair_status_words);
-  return check_launch("emit_kernel");
+  int rc = check_launch("emit_kernel");
+  if (rc || pair_passes == 0) return rc;
+  hipLaunchKernelGGL(hist_reduce_kernel, dim3((unsigned)(pair_passes * 256)),
+                     dim3(kThreads), 0, stream, hist_partials, nblk,
+                     pair_ghist);
+  return check_launch("hist_reduce_kernel");
+}
+
+int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
+                       int32_t* tile_offsets, int32_t* tile_counts,
+                       hipStream_t stream) {
+  if (num_tiles <= 0) return GSPLAT_OK;
+  int rc;
+  if (n == 0) {
+    rc = launch_fill_i32(tile_offsets, 0, (int64_t)num_tiles + 1, stream);
+  } else {
+    hipLaunchKernelGGL(ranges_kernel,
+                       dim3((unsigned)((n + 1 + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, stream, sorted_keys, n, num_tiles,
+                       tile_offsets);
+    rc = check_launch("ranges_kernel");
+  }
+  if (rc || tile_counts == nullptr) return rc;
+  hipLaunchKernelGGL(counts_kernel,
+                     dim3((unsigned)((num_tiles + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, stream, tile_offsets, num_tiles,
+                     tile_counts);
+  return check_launch("counts_kernel");
 }
 
 int launch_zero2(uint32_t* a, int64_t na, uint32_t* b, int64_t nb,

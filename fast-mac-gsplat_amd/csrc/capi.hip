@@ -66,7 +66,8 @@ int make_params(const gsplat_raster_meta* m, RasterParams& P) {
   const int64_t T = tpi * m->batch;
   const int64_t BG = (int64_t)m->batch * m->gaussians_per_batch;
   const int64_t pixels = (int64_t)m->batch * m->height * m->width;
-  if (T >= 0x7fffffffLL || BG > kMaxSplats || pixels * 3 >= (int64_t(1) << 40)) {
+  if (T >= 0x7fffffffLL || tpi > (int64_t(1) << 24) || BG > kMaxSplats ||
+      pixels * 3 >= (int64_t(1) << 40)) {
     gs::set_error("problem too large (tiles %lld, splats %lld)", (long long)T,
                   (long long)BG);
     return GSPLAT_ERR_INVALID_ARGUMENT;
@@ -118,13 +119,13 @@ int null_check(std::initializer_list<const void*> ptrs, const char* what) {
 
 // Binning workspace shared by bin_count, bin_pack and bin_emit: a control
 // region zeroed by bin_count (depth-sort control block, pack-scan look-back
-// status and ticket, pair-sort histograms and tickets, tile-offset scan
-// status and ticket), the per-splat tile-hit counts (original order), then
-// the depth sort's ping-pong buffers.
+// status and ticket, pair-sort histograms and tickets), then the per-splat
+// tile-hit counts (original order), the count workgroups' sums and the depth
+// sort's ping-pong buffers.
 struct CountLayout {
   gs::RadixPlan depth;
-  size_t scan_status, scan_ticket, pair_ghist, pair_tickets, tile_scan, ctl_end;
-  size_t splat_count, depth_buffers, total;
+  size_t scan_status, scan_ticket, pair_ghist, pair_tickets, ctl_end;
+  size_t splat_count, block_sums, depth_buffers, total;
 };
 
 CountLayout count_layout(const RasterParams& P) {
@@ -139,11 +140,11 @@ CountLayout count_layout(const RasterParams& P) {
   off += 4 * 256 * sizeof(uint32_t);
   L.pair_tickets = off;
   off += 256;
-  L.tile_scan = off;
-  off += gs::scan_workspace_bytes(P.num_tiles);
   L.ctl_end = off;
   L.splat_count = off;
   off += gs::align_up((size_t)P.num_splats * sizeof(int32_t), 256);
+  L.block_sums = off;
+  off += gs::align_up((size_t)gs::count_blocks(P) * sizeof(int32_t), 256);
   L.depth_buffers = off;
   off += gs::align_up(L.depth.buffer_bytes, 256);
   L.total = off;
@@ -151,22 +152,31 @@ CountLayout count_layout(const RasterParams& P) {
 }
 
 // Emit-stage workspace: emitted keys and values, the pair sort's look-back
-// status, and its ping-pong buffers.
+// status, the emit workgroups' digit histograms, the sorted keys (for the
+// tile ranges) and the sort's ping-pong buffers.
 struct EmitLayout {
   gs::RadixPlan pairs;
-  size_t keys, vals, status, buffers, total;
+  size_t keys, vals, status, hist, sorted_keys, buffers, total;
 };
 
 EmitLayout emit_layout(const RasterParams& P, int64_t n) {
   EmitLayout L{};
   L.pairs = gs::radix_plan(n, 1, 0, bits_for((int64_t)P.num_tiles - 1));
   const size_t vec = gs::align_up((size_t)n * sizeof(uint32_t), 256);
-  L.keys = 0;
-  L.vals = vec;
-  L.status = 2 * vec;
-  L.buffers =
-      L.status + gs::align_up((size_t)L.pairs.status_words * sizeof(uint32_t), 256);
-  L.total = L.buffers + L.pairs.buffer_bytes;
+  size_t off = 0;
+  L.keys = off;
+  off += vec;
+  L.vals = off;
+  off += vec;
+  L.status = off;
+  off += gs::align_up((size_t)L.pairs.status_words * sizeof(uint32_t), 256);
+  L.hist = off;
+  off += gs::align_up((size_t)gs::emit_blocks(P) * 4 * 256 * sizeof(uint32_t), 256);
+  L.sorted_keys = off;
+  off += vec;
+  L.buffers = off;
+  off += L.pairs.buffer_bytes;
+  L.total = off;
   return L;
 }
 }  // namespace
@@ -185,14 +195,12 @@ size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta) {
 
 int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
                          const float* conics, const float* opacities,
-                         int32_t* tile_counts, int32_t* tile_offsets,
-                         void* workspace, size_t workspace_bytes,
-                         void* stream) {
+                         int32_t* pair_count, void* workspace,
+                         size_t workspace_bytes, void* stream) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
-  rc = null_check({means2d, conics, opacities, tile_counts, tile_offsets,
-                   workspace},
+  rc = null_check({means2d, conics, opacities, pair_count, workspace},
                   "gsplat_hip_bin_count");
   if (rc) return rc;
   const CountLayout L = count_layout(P);
@@ -207,22 +215,13 @@ int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* base = static_cast<char*>(workspace);
-  // 1. zero the control region and the tile counters
-  rc = gs::launch_zero2(reinterpret_cast<uint32_t*>(base),
-                        (int64_t)(L.ctl_end / sizeof(uint32_t)),
-                        reinterpret_cast<uint32_t*>(tile_counts), P.num_tiles, s);
-  // 2. per-splat tile-hit counts and per-tile pair counters
-  if (!rc)
-    rc = gs::launch_count(P, means2d, conics, opacities,
+  // Per-splat tile-hit counts and their total N; the same launch zeroes the
+  // control region.
+  return gs::launch_count(P, means2d, conics, opacities,
                           reinterpret_cast<int32_t*>(base + L.splat_count),
-                          tile_counts, s);
-  // 3. tile ranges (N = tile_offsets[T])
-  if (!rc)
-    rc = gs::exclusive_scan_i32(tile_counts, tile_offsets, P.num_tiles,
-                                base + L.tile_scan,
-                                gs::scan_workspace_bytes(P.num_tiles), s,
-                                /*ctl_zeroed=*/true);
-  return rc;
+                          reinterpret_cast<int32_t*>(base + L.block_sums),
+                          pair_count, reinterpret_cast<uint32_t*>(base),
+                          (int64_t)(L.ctl_end / sizeof(uint32_t)), s);
 }
 
 int gsplat_hip_bin_pack(const gsplat_raster_meta* meta, const float* means2d,
@@ -271,9 +270,9 @@ size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
 }
 
 int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
-                        const int32_t* splat_offsets,
-                        const int32_t* tile_counts, int64_t n_pairs,
-                        int32_t* binned_ids, void* count_workspace,
+                        const int32_t* splat_offsets, int64_t n_pairs,
+                        int32_t* binned_ids, int32_t* tile_counts,
+                        int32_t* tile_offsets, void* count_workspace,
                         size_t count_workspace_bytes, void* workspace,
                         size_t workspace_bytes, void* stream) {
   RasterParams P;
@@ -284,9 +283,14 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
                   (long long)n_pairs);
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
-  if (n_pairs == 0) return GSPLAT_OK;
-  rc = null_check({packed, splat_offsets, tile_counts, binned_ids,
-                   count_workspace, workspace},
+  rc = null_check({tile_offsets}, "gsplat_hip_bin_emit");
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n_pairs == 0)
+    return gs::launch_tile_ranges(nullptr, 0, P.num_tiles, tile_offsets,
+                                  tile_counts, s);
+  rc = null_check({packed, splat_offsets, binned_ids, count_workspace,
+                   workspace},
                   "gsplat_hip_bin_emit");
   if (rc) return rc;
   const CountLayout C = count_layout(P);
@@ -300,20 +304,28 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
     gs::set_error("gsplat_hip_bin_emit: too many pairs");
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
   char* cbase = static_cast<char*>(count_workspace);
   char* base = static_cast<char*>(workspace);
   uint32_t* keys = reinterpret_cast<uint32_t*>(base + L.keys);
   uint32_t* vals = reinterpret_cast<uint32_t*>(base + L.vals);
+  uint32_t* sorted_keys = reinterpret_cast<uint32_t*>(base + L.sorted_keys);
   const gs::RadixCtl ctl{reinterpret_cast<uint32_t*>(cbase + C.pair_ghist),
                          reinterpret_cast<uint32_t*>(base + L.status),
                          reinterpret_cast<uint32_t*>(cbase + C.pair_tickets)};
-  rc = gs::launch_emit(P, packed, splat_offsets, tile_counts, keys, vals,
-                       L.pairs.passes, ctl.ghist, ctl.status,
-                       L.pairs.status_words, s);
-  if (rc) return rc;
-  return gs::radix_passes(L.pairs, ctl, base + L.buffers, keys, vals, nullptr,
-                          nullptr, reinterpret_cast<uint32_t*>(binned_ids), s);
+  // 1. pairs at deterministic per-splat ranges + the sort's histograms
+  rc = gs::launch_emit(P, packed, splat_offsets, keys, vals, L.pairs.passes,
+                       reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
+                       ctl.status, L.pairs.status_words, s);
+  // 2. stable sort by tile
+  if (!rc)
+    rc = gs::radix_passes(L.pairs, ctl, base + L.buffers, keys, vals, nullptr,
+                          sorted_keys, reinterpret_cast<uint32_t*>(binned_ids),
+                          s);
+  // 3. tile ranges and counts from the sorted keys
+  if (!rc)
+    rc = gs::launch_tile_ranges(sorted_keys, n_pairs, P.num_tiles,
+                                tile_offsets, tile_counts, s);
+  return rc;
 }
 
 int gsplat_hip_render_forward(const gsplat_raster_meta* meta,

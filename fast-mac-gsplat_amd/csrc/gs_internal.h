@@ -83,12 +83,16 @@ int radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in,
                      hipStream_t stream);
 
 // ---- binning (binning.hip)
-// count: per-splat tile-hit counts (original order) into splat_count and
-// per-tile pair counters into tile_counts (zeroed).
+// count: per-splat tile-hit counts (original order) into splat_count, the
+// per-workgroup sums into block_sums (count_blocks(P) ints) and their total
+// N into *pair_count (-1 if N does not fit in int32); the same launch zeroes
+// zero_words[0..n_zero_words).  Requires P.num_splats > 0.
+int count_blocks(const RasterParams& P);
 int launch_count(const RasterParams& P, const float* means2d,
                  const float* conics, const float* opacities,
-                 int32_t* splat_count, int32_t* tile_counts,
-                 hipStream_t stream);
+                 int32_t* splat_count, int32_t* block_sums,
+                 int32_t* pair_count, uint32_t* zero_words,
+                 int64_t n_zero_words, hipStream_t stream);
 // pack: packed records in gid order and splat_offsets[0..BG] (exclusive scan
 // of splat_count[perm]) via a look-back scan whose status
 // (count_scan_blocks(P) words) and ticket must be zero.
@@ -99,13 +103,21 @@ int launch_pack(const RasterParams& P, const float* means2d,
                 int32_t* splat_offsets, uint64_t* scan_status,
                 uint32_t* scan_ticket, hipStream_t stream);
 int count_scan_blocks(const RasterParams& P);
-// emit: writes (tile, gid) pairs; also zeroes pair_status and adds the
-// pair sort's per-pass digit histograms into pair_ghist (zeroed).
+// emit: writes the (tile, gid) pairs into each splat's range, zeroes
+// pair_status, and fills pair_ghist ([pair_passes][256]) with the pair sort's
+// digit histograms via per-workgroup partials (emit_blocks(P) * 4 * 256
+// words).
+int emit_blocks(const RasterParams& P);
 int launch_emit(const RasterParams& P, const float* packed,
-                const int32_t* splat_offsets, const int32_t* tile_counts,
-                uint32_t* keys, uint32_t* vals, int pair_passes,
-                uint32_t* pair_ghist, uint32_t* pair_status,
-                int64_t pair_status_words, hipStream_t stream);
+                const int32_t* splat_offsets, uint32_t* keys, uint32_t* vals,
+                int pair_passes, uint32_t* hist_partials, uint32_t* pair_ghist,
+                uint32_t* pair_status, int64_t pair_status_words,
+                hipStream_t stream);
+// tile_offsets[0..T] and (unless tile_counts is NULL) tile_counts[0..T)
+// from the n sorted tile keys.
+int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
+                       int32_t* tile_offsets, int32_t* tile_counts,
+                       hipStream_t stream);
 int launch_zero2(uint32_t* a, int64_t na, uint32_t* b, int64_t nb,
                  hipStream_t stream);
 int launch_fill_i32(int32_t* dst, int32_t value, int64_t n, hipStream_t stream);

@@ -56,13 +56,21 @@ class _timed:
 
 @dataclass
 class BinState:
-    perm: Tensor          # int32 [BG]  depth rank -> original index within image
-    packed: Tensor        # float32 [BG, 12]  packed records in gid order
-    splat_offsets: Tensor # int32 [BG+1]
-    tile_counts: Tensor   # int32 [T]
-    tile_offsets: Tensor  # int32 [T+1]
-    binned_ids: Tensor    # int32 [N]
+    perm: Optional[Tensor]          # int32 [BG]  depth rank -> original index within image
+    packed: Tensor                  # float32 [BG, 12]  packed records in gid order
+    splat_offsets: Optional[Tensor] # int32 [BG+1]
+    tile_offsets: Tensor            # int32 [T+1]
+    binned_ids: Tensor              # int32 [N]
     n_pairs: int
+
+    @property
+    def num_tiles(self) -> int:
+        return self.tile_offsets.numel() - 1
+
+    @property
+    def tile_counts(self) -> Tensor:
+        """int32 [T] pairs per tile (computed on demand; the compositors use the offsets)."""
+        return self.tile_offsets[1:] - self.tile_offsets[:-1]
 
 
 def _empty(n, dtype, device):
@@ -71,13 +79,13 @@ def _empty(n, dtype, device):
 
 def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
                   opacities: Tensor, depths: Tensor) -> BinState:
-    """Tile binning + stable depth order + record packing + pair sort.
+    """Tile binning + stable depth order + record packing + pair sort + tile ranges.
 
     Inputs are flat contiguous fp32 [BG,2], [BG,3], [BG,3], [BG], [BG] in the
     original splat order.  The pair count N (needed on the host to size the
     pair buffers, like the reference's tile_offsets[-1] read,
     variants/v8/csrc/metal/gsplat_metal.mm:188) is copied to pinned memory
-    right after the tile counts are known and read after the depth sort has
+    as soon as the per-splat counts exist and read after the depth sort has
     been enqueued, so the wait overlaps GPU work."""
     L = _lib.lib()
     dev = means2d.device
@@ -87,16 +95,16 @@ def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors
     perm = _empty(BG, torch.int32, dev)
     packed = torch.empty((BG, _lib.RECORD_FLOATS), dtype=torch.float32, device=dev)
     splat_offsets = _empty(BG + 1, torch.int32, dev)
-    tile_counts = _empty(tiles, torch.int32, dev)
     tile_offsets = _empty(tiles + 1, torch.int32, dev)
+    pair_count = _empty(1, torch.int32, dev)
     ws_bytes = L.gsplat_hip_bin_count_workspace_bytes(meta)
     ws = _empty(max(ws_bytes, 1), torch.uint8, dev)
     s = stream_of(means2d)
     with _timed("bin_count"):
-        check(L.gsplat_hip_bin_count(meta, ptr(means2d), ptr(conics), ptr(opacities), ptr(tile_counts),
-                                     ptr(tile_offsets), ptr(ws), ws_bytes, s), "gsplat_hip_bin_count")
+        check(L.gsplat_hip_bin_count(meta, ptr(means2d), ptr(conics), ptr(opacities), ptr(pair_count),
+                                     ptr(ws), ws_bytes, s), "gsplat_hip_bin_count")
     n_host = torch.empty((1,), dtype=torch.int32, pin_memory=True)
-    n_host.copy_(tile_offsets[-1:], non_blocking=True)
+    n_host.copy_(pair_count, non_blocking=True)
     n_ready = torch.cuda.Event()
     n_ready.record()
     with _timed("bin_pack"):
@@ -106,22 +114,22 @@ def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors
     n_ready.synchronize()
     n = int(n_host[0])
     if n < 0:
-        raise RuntimeError(f"pair count overflowed int32 ({n})")
+        raise RuntimeError("pair count overflowed int32")
     binned = _empty(n, torch.int32, dev)
-    if n > 0:
-        ws2_bytes = L.gsplat_hip_bin_emit_workspace_bytes(meta, n)
-        ws2 = _empty(ws2_bytes, torch.uint8, dev)
-        with _timed("bin_emit"):
-            check(L.gsplat_hip_bin_emit(meta, ptr(packed), ptr(splat_offsets), ptr(tile_counts), n, ptr(binned),
-                                        ptr(ws), ws_bytes, ptr(ws2), ws2_bytes, s), "gsplat_hip_bin_emit")
-    return BinState(perm, packed, splat_offsets, tile_counts, tile_offsets, binned, n)
+    ws2_bytes = L.gsplat_hip_bin_emit_workspace_bytes(meta, n)
+    ws2 = _empty(max(ws2_bytes, 1), torch.uint8, dev)
+    with _timed("bin_emit"):
+        check(L.gsplat_hip_bin_emit(meta, ptr(packed), ptr(splat_offsets), n, ptr(binned), None,
+                                    ptr(tile_offsets), ptr(ws), ws_bytes, ptr(ws2), ws2_bytes, s),
+              "gsplat_hip_bin_emit")
+    return BinState(perm, packed, splat_offsets, tile_offsets, binned, n)
 
 
 def render_forward(meta: _lib.RasterMeta, st: BinState, *, save_state: bool):
     L = _lib.lib()
     dev = st.packed.device
     B, H, W = meta.batch, meta.height, meta.width
-    tiles = st.tile_counts.numel()
+    tiles = st.num_tiles
     img = torch.empty((B, H, W, 3), dtype=torch.float32, device=dev)
     final_T = last = tile_stop = None
     if save_state:

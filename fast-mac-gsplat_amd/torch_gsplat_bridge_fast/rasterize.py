@@ -237,7 +237,7 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
     def backward(ctx, grad_out):
         packed, tile_offsets, binned_ids, final_T, last, tile_stop = ctx.saved_tensors
         B, G = ctx.shape
-        st = _ops.BinState(None, packed, None, tile_stop, tile_offsets, binned_ids, binned_ids.numel())
+        st = _ops.BinState(None, packed, None, tile_offsets, binned_ids, binned_ids.numel())
         g_m, g_q, g_c, g_o = _ops.render_backward(ctx.meta, st, final_T, last, tile_stop, grad_out)
         need = ctx.needs_input_grad
         g_depth = torch.zeros(ctx.depth_shape, dtype=torch.float32, device=grad_out.device) if need[4] else None

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 2
+#define GSPLAT_HIP_ABI_VERSION 3
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -81,33 +81,31 @@ const char* gsplat_hip_last_error(void);
  * Replaces torch.ops.gsplat_metal_v8.bin (variants/v8/csrc/bindings.cpp:201,
  * host side variants/v8/csrc/metal/gsplat_metal.mm:140-204) together with the
  * stable depth argsort + gathers of variants/v8/torch_gsplat_bridge_v8/
- * rasterize.py:465-475.  The reference sizes binned_ids with a host read of
+ * rasterize.py:465-475 and the per-tile sort (gsplat_v8_kernels.metal:
+ * 141-164).  The reference sizes binned_ids with a host read of
  * tile_offsets[-1] (gsplat_metal.mm:188).  Here binning is three calls on one
  * stream sharing one workspace:
- *   gsplat_hip_bin_count  tile-hit counts and tile ranges; leaves the pair
- *                         count N in tile_offsets[T];
+ *   gsplat_hip_bin_count  per-splat tile-hit counts; writes the pair count N;
  *   gsplat_hip_bin_pack   stable depth order, packed records, per-splat pair
  *                         offsets;
- *   gsplat_hip_bin_emit   pair emission and the sort by tile.
- * A caller that needs N on the host (to size binned_ids) can copy
- * tile_offsets[T] asynchronously after bin_count and wait for it after
- * enqueuing bin_pack, so the read overlaps the depth sort. */
+ *   gsplat_hip_bin_emit   pair emission, the stable sort by tile, and the
+ *                         tile ranges/counts extracted from the sorted keys.
+ * A caller that needs N on the host (to size binned_ids) can copy it
+ * asynchronously after bin_count and wait for it after enqueuing bin_pack,
+ * so the read overlaps the depth sort. */
 
 /* Bytes of the binning workspace used by bin_count, bin_pack and bin_emit. */
 size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta);
 
 /* Inputs (original order): means2d [BG,2], conics [BG,3], opacities [BG].
- * Outputs:
- *   tile_counts   int32 [T]    pairs per tile
- *   tile_offsets  int32 [T+1]  exclusive scan of tile_counts (tile ranges);
- *                              tile_offsets[T] = N
- * The workspace keeps the per-splat tile-hit counts and the zeroed control
- * state that bin_pack and bin_emit consume: pass the same workspace to them,
- * unmodified, on the same stream. */
+ * Output: *pair_count (one int32 in device memory) = N, the number of
+ * (tile, splat) pairs, or -1 if N does not fit in int32.  The workspace keeps
+ * the per-splat tile-hit counts and the zeroed control state that bin_pack
+ * and bin_emit consume: pass the same workspace to them, unmodified, on the
+ * same stream. */
 int gsplat_hip_bin_count(const gsplat_raster_meta* meta,
                          const float* means2d, const float* conics,
-                         const float* opacities,
-                         int32_t* tile_counts, int32_t* tile_offsets,
+                         const float* opacities, int32_t* pair_count,
                          void* workspace, size_t workspace_bytes,
                          void* stream);
 
@@ -127,20 +125,26 @@ int gsplat_hip_bin_pack(const gsplat_raster_meta* meta,
 size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
                                            int64_t n_pairs);
 
-/* Emits one (tile, gid) pair per tile hit at the deterministic scan offsets,
- * then sorts the pairs by tile with a stable LSD radix sort (8-bit digits).
- * binned_ids int32 [N]: gids grouped by tile, ascending gid (= depth order)
- * inside each tile range [tile_offsets[t], tile_offsets[t+1]).  The sorted
- * 64-bit key of pair i is (tile << 32) | binned_ids[i].
- * Replaces emit_binned_ids (variants/v8/csrc/metal/gsplat_v8_kernels.metal:
- * 290-327) and the per-tile bitonic sort (:141-164, :441-442). */
+/* Emits the N (tile, gid) pairs, sorts them by tile with a stable LSD radix
+ * sort (8-bit digits) and extracts the tile ranges.  Outputs:
+ *   binned_ids    int32 [N]    gids grouped by tile, ascending gid (= depth
+ *                              order) inside each tile range; the sorted
+ *                              64-bit key of pair i is
+ *                              (tile << 32) | binned_ids[i]
+ *   tile_counts   int32 [T]    pairs per tile (may be NULL: not computed)
+ *   tile_offsets  int32 [T+1]  tile t's range is [tile_offsets[t],
+ *                              tile_offsets[t+1]); tile_offsets[T] = N
+ * count_workspace is the workspace of bin_count / bin_pack.  Replaces
+ * emit_binned_ids (variants/v8/csrc/metal/gsplat_v8_kernels.metal:290-327),
+ * the reference's tile_counts/tile_offsets (count_tiles :244-288 + the
+ * cumsum of gsplat_metal.mm:183-189) and its per-tile bitonic sort
+ * (:141-164, :441-442). */
 int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
-                        const int32_t* splat_offsets,
-                        const int32_t* tile_counts, int64_t n_pairs,
-                        int32_t* binned_ids,
+                        const int32_t* splat_offsets, int64_t n_pairs,
+                        int32_t* binned_ids, int32_t* tile_counts,
+                        int32_t* tile_offsets,
                         void* count_workspace, size_t count_workspace_bytes,
                         void* workspace, size_t workspace_bytes, void* stream);
-/* count_workspace is the workspace of bin_count / bin_pack. */
 
 /* -------------------------------------------------------------- composite
  * Forward compositor.  Replaces render_fast_forward_state / _eval

@@ -30,7 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 2
+    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 3
 
 
 def _meta(**kw):
@@ -85,12 +85,12 @@ def test_null_pointers_rejected():
 def test_workspace_too_small_rejected():
     L = _lib.lib()
     one = ctypes.c_void_p(1)
-    rc = L.gsplat_hip_bin_count(_meta(), *([one] * 5), one, 1, None)
+    rc = L.gsplat_hip_bin_count(_meta(), *([one] * 4), one, 1, None)
     assert rc == 3
     assert "workspace" in L.gsplat_hip_last_error().decode()
     rc = L.gsplat_hip_bin_pack(_meta(), *([one] * 8), one, 1, None)
     assert rc == 3 and "bin_pack" in L.gsplat_hip_last_error().decode()
-    rc = L.gsplat_hip_bin_emit(_meta(), one, one, one, 10, one, one, 1, one, 1, None)
+    rc = L.gsplat_hip_bin_emit(_meta(), one, one, 10, one, one, one, one, 1, one, 1, None)
     assert rc == 3
     pm = _lib.make_project_meta(2, 1000, 1e-4)
     need = L.gsplat_hip_project_backward_workspace_bytes(pm)
