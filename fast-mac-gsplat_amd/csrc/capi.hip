@@ -332,21 +332,44 @@ int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
                               const float* packed, const int32_t* tile_offsets,
                               const int32_t* binned_ids, float* out_rgb,
                               float* out_final_T, int32_t* out_last,
-                              int32_t* out_tile_stop, void* stream) {
+                              int32_t* out_tile_stop, int64_t n_pairs,
+                              void* workspace, size_t workspace_bytes,
+                              void* stream) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
   rc = null_check({packed, tile_offsets, out_rgb}, "gsplat_hip_render_forward");
   if (rc) return rc;
-  if ((out_final_T == nullptr) != (out_last == nullptr)) {
+  if ((out_final_T == nullptr) != (out_last == nullptr) ||
+      (out_final_T == nullptr) != (out_tile_stop == nullptr)) {
     gs::set_error(
-        "gsplat_hip_render_forward: out_final_T and out_last must both be "
-        "given or both be NULL");
+        "gsplat_hip_render_forward: out_final_T, out_last and out_tile_stop "
+        "must all be given or all be NULL");
     return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  if (n_pairs < 0) {
+    gs::set_error("gsplat_hip_render_forward: invalid pair count %lld",
+                  (long long)n_pairs);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  if (out_final_T == nullptr) workspace = nullptr;  // eval path: no state
+  if (workspace != nullptr &&
+      workspace_bytes < gs::render_workspace_bytes(P, n_pairs)) {
+    gs::set_error("gsplat_hip_render_forward: workspace too small (%zu < %zu)",
+                  workspace_bytes, gs::render_workspace_bytes(P, n_pairs));
+    return GSPLAT_ERR_WORKSPACE;
   }
   return gs::launch_render_forward(P, packed, tile_offsets, binned_ids, out_rgb,
                                    out_final_T, out_last, out_tile_stop,
+                                   n_pairs, workspace,
                                    static_cast<hipStream_t>(stream));
+}
+
+size_t gsplat_hip_render_workspace_bytes(const gsplat_raster_meta* meta,
+                                         int64_t n_pairs) {
+  RasterParams P;
+  if (make_params(meta, P) || n_pairs < 0) return 0;
+  return gs::render_workspace_bytes(P, n_pairs);
 }
 
 int gsplat_hip_render_backward(const gsplat_raster_meta* meta,
@@ -357,7 +380,8 @@ int gsplat_hip_render_backward(const gsplat_raster_meta* meta,
                                const int32_t* tile_stop, const float* grad_rgb,
                                float* g_means2d, float* g_conics,
                                float* g_colors, float* g_opacities,
-                               void* stream) {
+                               int64_t n_pairs, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -365,9 +389,21 @@ int gsplat_hip_render_backward(const gsplat_raster_meta* meta,
                    g_means2d, g_conics, g_colors, g_opacities},
                   "gsplat_hip_render_backward");
   if (rc) return rc;
+  if (n_pairs < 0) {
+    gs::set_error("gsplat_hip_render_backward: invalid pair count %lld",
+                  (long long)n_pairs);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  if (workspace != nullptr &&
+      workspace_bytes < gs::render_workspace_bytes(P, n_pairs)) {
+    gs::set_error("gsplat_hip_render_backward: workspace too small (%zu < %zu)",
+                  workspace_bytes, gs::render_workspace_bytes(P, n_pairs));
+    return GSPLAT_ERR_WORKSPACE;
+  }
   return gs::launch_render_backward(P, packed, tile_offsets, binned_ids,
                                     final_T, last, tile_stop, grad_rgb,
                                     g_means2d, g_conics, g_colors, g_opacities,
+                                    n_pairs, workspace,
                                     static_cast<hipStream_t>(stream));
 }
 

@@ -62,9 +62,10 @@ struct TileCoord {
   int lx, ly;               // this lane's column and row inside a strip
 };
 
-__device__ __forceinline__ TileCoord tile_coord(const RasterParams& P) {
+__device__ __forceinline__ TileCoord tile_coord_of(const RasterParams& P,
+                                                   int tile) {
   TileCoord c;
-  c.tile = xcd_remap((int)blockIdx.x, P.num_tiles);
+  c.tile = tile;
   c.batch = c.tile / P.tiles_per_image;
   const int lt = c.tile - c.batch * P.tiles_per_image;
   const int ty = lt / P.tiles_x;
@@ -74,6 +75,10 @@ __device__ __forceinline__ TileCoord tile_coord(const RasterParams& P) {
   c.lx = threadIdx.x & 15;
   c.ly = threadIdx.x >> 4;
   return c;
+}
+
+__device__ __forceinline__ TileCoord tile_coord(const RasterParams& P) {
+  return tile_coord_of(P, xcd_remap((int)blockIdx.x, P.num_tiles));
 }
 
 __device__ __forceinline__ int slot_y(const TileCoord& c, int k) {
@@ -171,12 +176,55 @@ __device__ __forceinline__ uint32_t uniform_bits(float v) {
   return __builtin_amdgcn_readfirstlane(__float_as_uint(v));
 }
 
+// Heavy tiles.  A tile whose range holds more than kHeavyCount pairs gets
+// ceil(count / kSegSplats) segment slots.  For each segment k the forward
+// records per pixel seg[k] = (colour composited by the segment's splats,
+// transmittance at the segment's end); its colour accumulators restart at
+// every segment boundary, the completed segments' colour being summed in the
+// output pixel.  With those records the backward of segment k needs nothing
+// from the later segments' walks: the gT
+// of the reverse recurrence at the segment's end is
+//   gT_k = (<g, sum_{j>k} colour_j> + <g, bg> T_final) / T_end_k,
+// the closed form of gT <- alpha <g,c> + (1 - alpha) gT over the later
+// splats.  Segments of a tile whose stop exceeds one segment are then walked
+// in parallel, each by its own wavefront, in the same launch as the other
+// tiles.
+constexpr int kSegSplats = 128;   // multiple of kBatch
+constexpr int kHeavyCount = 128;  // >= kSegSplats
+
+struct HeavyState {    // all null: no heavy-tile handling
+  int32_t* counter;    // segment slots handed out (zeroed before the forward)
+  int32_t* tile_slot;  // [T] first slot of a heavy tile, -1 otherwise
+  int32_t* slot_tile;  // [max_slots] tile of each slot
+  float4* seg;         // [max_slots][256] (r, g, b, T at the segment's end)
+  int max_slots;
+};
+
+// Pixel index inside the tile used by the per-pixel heavy-tile buffers.
+__device__ __forceinline__ int tile_pixel(int k) {
+  return 64 * k + (int)threadIdx.x;
+}
+
+// Output pixel of this lane's first strip.  Computed where it is used, from
+// an opaque copy of the lane id, so that the compiler does not keep four
+// 64-bit pixel addresses live across the compositing loop for the rare
+// segment boundaries.
+__device__ __forceinline__ float* heavy_out(const RasterParams& P,
+                                            const TileCoord& tc,
+                                            float* out_rgb) {
+  int lane = (int)threadIdx.x;
+  asm volatile("" : "+v"(lane));
+  const int y = tc.y0 + (lane >> 4);
+  const int x = tc.x0 + (lane & 15);
+  return out_rgb + 3 * (((int64_t)tc.batch * P.height + y) * P.width + x);
+}
+
 __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ tile_offsets,
     const int32_t* __restrict__ binned, float* __restrict__ out_rgb,
     float* __restrict__ out_T, int32_t* __restrict__ out_last,
-    int32_t* __restrict__ out_tile_stop) {
+    int32_t* __restrict__ out_tile_stop, HeavyState H) {
   __shared__ Staged S;
   const TileCoord tc = tile_coord(P);
   const int x = tc.x0 + tc.lx;
@@ -199,10 +247,52 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
   }
   const int start = tile_offsets[tc.tile];
   const int end = tile_offsets[tc.tile + 1];
+  // Heavy tiles sum their colour per segment whether or not the segments are
+  // recorded, so the eval and training forwards give identical images.
+  const bool heavy = end - start > kHeavyCount;
+  int slot = -1;
+  if (H.seg != nullptr) {
+    if (heavy) {
+      const int nseg = (end - start + kSegSplats - 1) / kSegSplats;
+      if (threadIdx.x == 0) {
+        slot = atomicAdd(H.counter, nseg);
+        if (slot + nseg > H.max_slots) slot = -1;  // out of slots: plain tile
+      }
+      slot = __shfl(slot, 0, 64);
+      if (slot >= 0)
+        for (int k = threadIdx.x; k < nseg; k += kLanes) H.slot_tile[slot + k] = tc.tile;
+    }
+    if (threadIdx.x == 0) H.tile_slot[tc.tile] = slot;
+  }
+  int seg_cur = 0;  // segment of the batch being composited
   for (int base = start; base < end; base += kBatch) {
     const bool any_alive = (T[0] > t_thr) | (T[1] > t_thr) | (T[2] > t_thr) |
                            (T[3] > t_thr);
     if (!__any(any_alive)) break;
+    if (heavy && base > start && (base - start) % kSegSplats == 0) {
+      // Segment boundary: record the segment and fold its colour into the
+      // output pixel, which holds the sum of the completed segments (each
+      // lane reads back only what it wrote itself).
+      float4* sp = H.seg + (int64_t)(slot + seg_cur) * 256;
+      float* o0 = heavy_out(P, tc, out_rgb);
+#pragma unroll
+      for (int k = 0; k < kPix; ++k) {
+        if (slot >= 0) sp[tile_pixel(k)] = make_float4(cr[k], cg[k], cb[k], T[k]);
+        if (valid[k]) {
+          float* o = o0 + (int64_t)12 * k * P.width;
+          if (seg_cur > 0) {
+            cr[k] += o[0];
+            cg[k] += o[1];
+            cb[k] += o[2];
+          }
+          o[0] = cr[k];
+          o[1] = cg[k];
+          o[2] = cb[k];
+        }
+        cr[k] = cg[k] = cb[k] = 0.0f;
+      }
+      ++seg_cur;
+    }
     const int n = min(kBatch, end - base);
     __syncthreads();
     stage_batch(packed, binned, base, n, tc, S);
@@ -233,6 +323,20 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
             last[k] = idx1;
           }
         }
+      }
+    }
+  }
+  if (heavy) {
+    // the segment composited last; later segments hold no pixel's last
+    float4* sp = H.seg + (int64_t)(slot + seg_cur) * 256;
+#pragma unroll
+    for (int k = 0; k < kPix; ++k) {
+      if (slot >= 0) sp[tile_pixel(k)] = make_float4(cr[k], cg[k], cb[k], T[k]);
+      if (valid[k] && seg_cur > 0) {
+        const float* o = heavy_out(P, tc, out_rgb) + (int64_t)12 * k * P.width;
+        cr[k] += o[0];
+        cg[k] += o[1];
+        cb[k] += o[2];
       }
     }
   }
@@ -346,50 +450,58 @@ __device__ __forceinline__ AtomicRole atomic_role(float* g_means2d,
   return r;
 }
 
-__global__ __launch_bounds__(kLanes) void render_bwd_kernel(
-    RasterParams P, const float4* __restrict__ packed,
-    const int32_t* __restrict__ tile_offsets,
-    const int32_t* __restrict__ binned, const float* __restrict__ final_T,
-    const int32_t* __restrict__ last_in, const int32_t* __restrict__ tile_stop,
-    const float* __restrict__ grad_rgb, float* __restrict__ g_means2d,
-    float* __restrict__ g_conics, float* __restrict__ g_colors,
-    float* __restrict__ g_opac) {
-  __shared__ Staged S;
-  const TileCoord tc = tile_coord(P);
-  const int nstop = tile_stop[tc.tile];
-  if (nstop <= 0) return;
-  const int start = tile_offsets[tc.tile];
-  const AtomicRole role = atomic_role(g_means2d, g_conics, g_colors);
-  const bool row_head = (threadIdx.x & 15) == 0;
-  const float max_alpha = fminf(P.max_alpha, 1.0f);
-  const int x = tc.x0 + tc.lx;
-  const float px = (float)x + 0.5f;
+// Per-pixel state of the backward walk (4 pixels per lane).
+struct BwdPixels {
+  float px;
   float py[kPix], Tc[kPix], gr[kPix], gg[kPix], gb[kPix], gT[kPix];
   int lk[kPix];
+};
+
+// Loads grad and saved state; T and gT start at final_T and the background
+// term.  Pixels outside the image get lk = 0 (never processed).
+__device__ __forceinline__ void load_bwd_pixels(
+    const RasterParams& P, const TileCoord& tc,
+    const float* __restrict__ final_T, const int32_t* __restrict__ last_in,
+    const float* __restrict__ grad_rgb, BwdPixels& Q) {
+  const int x = tc.x0 + tc.lx;
+  Q.px = (float)x + 0.5f;
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
     const int y = slot_y(tc, k);
     const bool valid = (x < P.width) && (y < P.height);
-    py[k] = (float)y + 0.5f;
+    Q.py[k] = (float)y + 0.5f;
     if (valid) {
       const int64_t pix = ((int64_t)tc.batch * P.height + y) * P.width + x;
-      gr[k] = grad_rgb[3 * pix + 0];
-      gg[k] = grad_rgb[3 * pix + 1];
-      gb[k] = grad_rgb[3 * pix + 2];
-      Tc[k] = final_T[pix];
-      lk[k] = last_in[pix];
+      Q.gr[k] = grad_rgb[3 * pix + 0];
+      Q.gg[k] = grad_rgb[3 * pix + 1];
+      Q.gb[k] = grad_rgb[3 * pix + 2];
+      Q.Tc[k] = final_T[pix];
+      Q.lk[k] = last_in[pix];
     } else {
-      gr[k] = gg[k] = gb[k] = 0.0f;
-      Tc[k] = 1.0f;
-      lk[k] = 0;
+      Q.gr[k] = Q.gg[k] = Q.gb[k] = 0.0f;
+      Q.Tc[k] = 1.0f;
+      Q.lk[k] = 0;
     }
-    gT[k] = gr[k] * P.bg_r + gg[k] * P.bg_g + gb[k] * P.bg_b;
+    Q.gT[k] = Q.gr[k] * P.bg_r + Q.gg[k] * P.bg_g + Q.gb[k] * P.bg_b;
   }
+}
+
+// Reverse walk over the tile-range indices [lo, hi): gradients of every
+// splat, reduced across the wavefront and added atomically in original order.
+__device__ __forceinline__ void bwd_walk(
+    const RasterParams& P, const float4* __restrict__ packed,
+    const int32_t* __restrict__ binned, int start, int lo, int hi,
+    const TileCoord& tc, Staged& S, BwdPixels& Q, float* __restrict__ g_means2d,
+    float* __restrict__ g_conics, float* __restrict__ g_colors,
+    float* __restrict__ g_opac) {
+  const AtomicRole role = atomic_role(g_means2d, g_conics, g_colors);
+  const bool row_head = (threadIdx.x & 15) == 0;
+  const float max_alpha = fminf(P.max_alpha, 1.0f);
   // Per-lane partial sums of the current splat; zero between splats.
   float S0 = 0.f, S1 = 0.f, S2 = 0.f;
   float acc_r = 0.f, acc_g = 0.f, acc_b = 0.f;
-  for (int cend = nstop; cend > 0; cend -= kBatch) {
-    const int cstart = max(0, cend - kBatch);
+  for (int cend = hi; cend > lo; cend -= kBatch) {
+    const int cstart = max(lo, cend - kBatch);
     const int n = cend - cstart;
     __syncthreads();
     stage_batch(packed, binned, start + cstart, n, tc, S);
@@ -401,15 +513,15 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
       const int i = cstart + j;
       const float4 a0 = S.s0[j];
       const float4 a1 = S.s1[j];
-      const float dx = px - a0.x;
+      const float dx = Q.px - a0.x;
       float Adxdx, Bdx;
       x_terms(a0.z, a0.w, dx, Adxdx, Bdx);
       bool contrib = false;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
         if (!((mask >> k) & 1u)) continue;  // scalar branch
-        if (i < lk[k]) {
-          const float dy = py[k] - a0.y;
+        if (i < Q.lk[k]) {
+          const float dy = Q.py[k] - a0.y;
           const float p = splat_exponent(Adxdx, Bdx, a1.x, dy);
           if (p <= 0.0f && p >= a2.z) {
             contrib = true;
@@ -420,20 +532,21 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
             // 1 - alpha >= 1 - max_alpha >= eps (checked on the host), so the
             // reference's max(1 - alpha, eps) is 1 - alpha.
             const float T_prev =
-                Tc[k] * __builtin_amdgcn_rcpf(1.0f - alpha);
-            const float dot_gc = gr[k] * a1.z + gg[k] * a1.w + gb[k] * a2.x;
-            const float diff = dot_gc - gT[k];
+                Q.Tc[k] * __builtin_amdgcn_rcpf(1.0f - alpha);
+            const float dot_gc =
+                Q.gr[k] * a1.z + Q.gg[k] * a1.w + Q.gb[k] * a2.x;
+            const float diff = dot_gc - Q.gT[k];
             const float wgt = T_prev * alpha;
-            acc_r += gr[k] * wgt;
-            acc_g += gg[k] * wgt;
-            acc_b += gb[k] * wgt;
+            acc_r += Q.gr[k] * wgt;
+            acc_g += Q.gg[k] * wgt;
+            acc_b += Q.gb[k] * wgt;
             const float g_pow = open ? (T_prev * diff) * raw : 0.0f;
             const float hdy = g_pow * dy;
             S0 += g_pow;
             S1 += hdy;
             S2 += hdy * dy;
-            gT[k] += alpha * diff;
-            Tc[k] = T_prev;
+            Q.gT[k] += alpha * diff;
+            Q.Tc[k] = T_prev;
           }
         }
       }
@@ -471,18 +584,142 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
   }
 }
 
+__device__ __forceinline__ bool heavy_backward(const HeavyState& H, int tile,
+                                               int nstop) {
+  return H.tile_slot != nullptr && H.tile_slot[tile] >= 0 && nstop > kSegSplats;
+}
+
+// Decodes segment slot m: tile, segment index k, segment count and the range
+// [lo, hi) of tile indices; false if the slot has no backward work.
+__device__ __forceinline__ bool seg_item(const RasterParams& P,
+                                         const HeavyState& H,
+                                         const int32_t* __restrict__ tile_stop,
+                                         int m, int& tile, int& slot0, int& k,
+                                         int& nseg, int& lo, int& hi) {
+  if (H.counter == nullptr || m >= *H.counter || m >= H.max_slots) return false;
+  tile = H.slot_tile[m];
+  // Only slots handed to a recorded tile are meaningful: check the tile id
+  // and that m lies inside that tile's own slot range.
+  if (tile < 0 || tile >= P.num_tiles) return false;
+  slot0 = H.tile_slot[tile];
+  const int nstop = tile_stop[tile];
+  if (slot0 < 0 || m < slot0 || nstop <= kSegSplats) return false;
+  k = m - slot0;
+  nseg = (nstop + kSegSplats - 1) / kSegSplats;
+  if (k >= nseg || slot0 > H.max_slots - nseg) return false;
+  lo = k * kSegSplats;
+  hi = min(lo + kSegSplats, nstop);
+  return true;
+}
+
+// Work items: blocks [0, seg_blocks) are heavy-tile segment slots (the
+// longest walks, dispatched first), the rest are tiles (heavy tiles among
+// them return at once).
+__global__ __launch_bounds__(kLanes) void render_bwd_kernel(
+    RasterParams P, const float4* __restrict__ packed,
+    const int32_t* __restrict__ tile_offsets,
+    const int32_t* __restrict__ binned, const float* __restrict__ final_T,
+    const int32_t* __restrict__ last_in, const int32_t* __restrict__ tile_stop,
+    const float* __restrict__ grad_rgb, float* __restrict__ g_means2d,
+    float* __restrict__ g_conics, float* __restrict__ g_colors,
+    float* __restrict__ g_opac, HeavyState H, int seg_blocks) {
+  __shared__ Staged S;
+  int tile, slot0 = 0, kseg = 0, nseg = 1, lo = 0, hi;
+  const int bid = (int)blockIdx.x;
+  if (bid < seg_blocks) {
+    if (!seg_item(P, H, tile_stop, bid, tile, slot0, kseg, nseg, lo, hi))
+      return;
+  } else {
+    // seg_blocks is a multiple of 8, so the XCD-aware mapping is preserved
+    tile = xcd_remap(bid - seg_blocks, P.num_tiles);
+    hi = tile_stop[tile];
+    if (hi <= 0) return;
+    if (heavy_backward(H, tile, hi)) return;  // walked as segments
+  }
+  const TileCoord tc = tile_coord_of(P, tile);
+  BwdPixels Q;
+  load_bwd_pixels(P, tc, final_T, last_in, grad_rgb, Q);
+  if (kseg < nseg - 1) {
+    // Pixels composited past this segment: T and gT at its end from the
+    // forward's segment records (Q.gT holds <g, bg>, Q.Tc holds T_final).
+    const float4* rec = H.seg + (int64_t)slot0 * 256;
+    float cr[kPix], cg[kPix], cb[kPix];
+#pragma unroll
+    for (int k = 0; k < kPix; ++k) cr[k] = cg[k] = cb[k] = 0.0f;
+    for (int j = kseg + 1; j < nseg; ++j) {
+#pragma unroll
+      for (int k = 0; k < kPix; ++k) {
+        const float4 v = rec[j * 256 + tile_pixel(k)];
+        cr[k] += v.x;
+        cg[k] += v.y;
+        cb[k] += v.z;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kPix; ++k) {
+      if (Q.lk[k] > hi) {
+        const float Te = rec[kseg * 256 + tile_pixel(k)].w;  // > 0: alive
+        const float num = Q.gr[k] * cr[k] + Q.gg[k] * cg[k] +
+                          Q.gb[k] * cb[k] + Q.gT[k] * Q.Tc[k];
+        Q.gT[k] = num / Te;
+        Q.Tc[k] = Te;
+      }
+    }
+  }
+  bwd_walk(P, packed, binned, tile_offsets[tile], lo, hi, tc, S, Q, g_means2d,
+           g_conics, g_colors, g_opac);
+}
+
+size_t heavy_max_slots(const RasterParams& P, int64_t n_pairs) {
+  // A heavy tile (> kHeavyCount pairs) with c pairs takes ceil(c / kSegSplats)
+  // < c / kSegSplats + 1 slots, and there are at most
+  // min(T, n_pairs / kHeavyCount) heavy tiles.
+  const int64_t tiles = std::min<int64_t>(P.num_tiles, n_pairs / kHeavyCount);
+  return (size_t)(n_pairs / kSegSplats + tiles + 1);
+}
+
+}  // namespace
+
+size_t render_workspace_bytes(const RasterParams& P, int64_t n_pairs) {
+  const size_t slots = heavy_max_slots(P, n_pairs);
+  return 256 + align_up((size_t)P.num_tiles * 4, 256) + align_up(slots * 4, 256) +
+         align_up(slots * 256 * sizeof(float4), 256);
+}
+
+namespace {
+HeavyState heavy_state(const RasterParams& P, int64_t n_pairs, void* ws) {
+  HeavyState H{};
+  if (ws == nullptr) return H;
+  const size_t slots = heavy_max_slots(P, n_pairs);
+  char* p = static_cast<char*>(ws);
+  H.counter = reinterpret_cast<int32_t*>(p);
+  p += 256;
+  H.tile_slot = reinterpret_cast<int32_t*>(p);
+  p += align_up((size_t)P.num_tiles * 4, 256);
+  H.slot_tile = reinterpret_cast<int32_t*>(p);
+  p += align_up(slots * 4, 256);
+  H.seg = reinterpret_cast<float4*>(p);
+  H.max_slots = (int)slots;
+  return H;
+}
 }  // namespace
 
 int launch_render_forward(const RasterParams& P, const float* packed,
                           const int32_t* tile_offsets,
                           const int32_t* binned_ids, float* out_rgb,
                           float* out_T, int32_t* out_last,
-                          int32_t* out_tile_stop, hipStream_t stream) {
+                          int32_t* out_tile_stop, int64_t n_pairs,
+                          void* workspace, hipStream_t stream) {
   if (P.num_tiles == 0) return GSPLAT_OK;
+  const HeavyState H = heavy_state(P, n_pairs, workspace);
+  if (H.counter != nullptr) {
+    const int rc = launch_fill_i32(H.counter, 0, 1, stream);
+    if (rc) return rc;
+  }
   hipLaunchKernelGGL(render_fwd_kernel, dim3((unsigned)P.num_tiles),
                      dim3(kLanes), 0, stream, P,
                      reinterpret_cast<const float4*>(packed), tile_offsets,
-                     binned_ids, out_rgb, out_T, out_last, out_tile_stop);
+                     binned_ids, out_rgb, out_T, out_last, out_tile_stop, H);
   return check_launch("render_fwd_kernel");
 }
 
@@ -492,16 +729,20 @@ int launch_render_backward(const RasterParams& P, const float* packed,
                            const int32_t* last, const int32_t* tile_stop,
                            const float* grad_rgb, float* g_means2d,
                            float* g_conics, float* g_colors, float* g_opac,
+                           int64_t n_pairs, void* workspace,
                            hipStream_t stream) {
   int rc = launch_zero_grads(g_means2d, g_conics, g_colors, g_opac,
                              P.num_splats, stream);
   if (rc) return rc;
   if (P.num_tiles == 0) return GSPLAT_OK;
-  hipLaunchKernelGGL(render_bwd_kernel, dim3((unsigned)P.num_tiles),
-                     dim3(kLanes), 0, stream, P,
-                     reinterpret_cast<const float4*>(packed), tile_offsets,
-                     binned_ids, final_T, last, tile_stop, grad_rgb, g_means2d,
-                     g_conics, g_colors, g_opac);
+  const HeavyState H = heavy_state(P, n_pairs, workspace);
+  const float4* pk = reinterpret_cast<const float4*>(packed);
+  const int seg_blocks = H.counter ? (H.max_slots + 7) & ~7 : 0;
+  hipLaunchKernelGGL(render_bwd_kernel,
+                     dim3((unsigned)(seg_blocks + P.num_tiles)), dim3(kLanes),
+                     0, stream, P, pk, tile_offsets, binned_ids, final_T, last,
+                     tile_stop, grad_rgb, g_means2d, g_conics, g_colors,
+                     g_opac, H, seg_blocks);
   return check_launch("render_bwd_kernel");
 }
 

@@ -126,17 +126,22 @@ int launch_zero_grads(float* g_m, float* g_q, float* g_c, float* g_o,
                       int64_t n, hipStream_t stream);
 
 // ---- compositing (composite.hip)
+// workspace (render_workspace_bytes, may be null): heavy-tile segment state,
+// written by the forward and read by the backward of the same binning.
+size_t render_workspace_bytes(const RasterParams& P, int64_t n_pairs);
 int launch_render_forward(const RasterParams& P, const float* packed,
                           const int32_t* tile_offsets,
                           const int32_t* binned_ids, float* out_rgb,
                           float* out_T, int32_t* out_last,
-                          int32_t* out_tile_stop, hipStream_t stream);
+                          int32_t* out_tile_stop, int64_t n_pairs,
+                          void* workspace, hipStream_t stream);
 int launch_render_backward(const RasterParams& P, const float* packed,
                            const int32_t* tile_offsets,
                            const int32_t* binned_ids, const float* final_T,
                            const int32_t* last, const int32_t* tile_stop,
                            const float* grad_rgb, float* g_means2d,
                            float* g_conics, float* g_colors, float* g_opac,
+                           int64_t n_pairs, void* workspace,
                            hipStream_t stream);
 
 // ---- projection (project.hip)

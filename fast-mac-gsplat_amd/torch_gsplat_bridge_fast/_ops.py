@@ -126,28 +126,35 @@ def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors
 
 
 def render_forward(meta: _lib.RasterMeta, st: BinState, *, save_state: bool):
+    """Returns (img, final_T, last, tile_stop, workspace); the last four are None unless save_state.
+    The workspace holds the heavy-tile segment state the backward reads."""
     L = _lib.lib()
     dev = st.packed.device
     B, H, W = meta.batch, meta.height, meta.width
     tiles = st.num_tiles
     img = torch.empty((B, H, W, 3), dtype=torch.float32, device=dev)
-    final_T = last = tile_stop = None
+    final_T = last = tile_stop = ws = None
+    wsb = 0
     if save_state:
         final_T = torch.empty((B, H, W), dtype=torch.float32, device=dev)
         last = torch.empty((B, H, W), dtype=torch.int32, device=dev)
         tile_stop = _empty(tiles, torch.int32, dev)
+        wsb = L.gsplat_hip_render_workspace_bytes(meta, st.n_pairs)
+        ws = _empty(max(wsb, 1), torch.uint8, dev)
     with _timed("render_forward"):
         check(L.gsplat_hip_render_forward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.binned_ids), ptr(img),
-                                          ptr(final_T), ptr(last), ptr(tile_stop), stream_of(img)),
+                                          ptr(final_T), ptr(last), ptr(tile_stop), st.n_pairs, ptr(ws), wsb,
+                                          stream_of(img)),
               "gsplat_hip_render_forward")
-    return img, final_T, last, tile_stop
+    return img, final_T, last, tile_stop, ws
 
 
 def render_backward(meta: _lib.RasterMeta, st: BinState, final_T: Tensor, last: Tensor, tile_stop: Tensor,
-                    grad_img: Tensor):
+                    grad_img: Tensor, workspace: Optional[Tensor] = None):
     """Returns (g_means2d [B,G,2], g_conics [B,G,3], g_colors [B,G,3], g_opacities [B,G]) in ORIGINAL
     order.  They are allocated in the leaves' batched shapes (not as views of flat buffers) so that
-    autograd can hand them to .grad without a copy."""
+    autograd can hand them to .grad without a copy.  workspace: the one render_forward returned for
+    the same binning (heavy tiles are then split into segments), or None."""
     L = _lib.lib()
     dev = st.packed.device
     B, G = meta.batch, meta.gaussians_per_batch
@@ -159,7 +166,8 @@ def render_backward(meta: _lib.RasterMeta, st: BinState, final_T: Tensor, last: 
     with _timed("render_backward"):
         check(L.gsplat_hip_render_backward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.binned_ids),
                                            ptr(final_T), ptr(last), ptr(tile_stop), ptr(grad_img), ptr(g_m), ptr(g_q),
-                                           ptr(g_c), ptr(g_o), stream_of(grad_img)),
+                                           ptr(g_c), ptr(g_o), st.n_pairs, ptr(workspace),
+                                           0 if workspace is None else workspace.numel(), stream_of(grad_img)),
               "gsplat_hip_render_backward")
     return g_m, g_q, g_c, g_o
 

@@ -226,8 +226,8 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
                      depths_b.detach())
         st = _ops.bin_gaussians(meta, *flat)
         _check_overflow(config, st)
-        img, final_T, last, tile_stop = _ops.render_forward(meta, st, save_state=True)
-        ctx.save_for_backward(st.packed, st.tile_offsets, st.binned_ids, final_T, last, tile_stop)
+        img, final_T, last, tile_stop, ws = _ops.render_forward(meta, st, save_state=True)
+        ctx.save_for_backward(st.packed, st.tile_offsets, st.binned_ids, final_T, last, tile_stop, ws)
         ctx.meta = meta
         ctx.shape = (B, G)
         ctx.depth_shape = depths_b.shape
@@ -235,10 +235,9 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        packed, tile_offsets, binned_ids, final_T, last, tile_stop = ctx.saved_tensors
-        B, G = ctx.shape
+        packed, tile_offsets, binned_ids, final_T, last, tile_stop, ws = ctx.saved_tensors
         st = _ops.BinState(None, packed, None, tile_offsets, binned_ids, binned_ids.numel())
-        g_m, g_q, g_c, g_o = _ops.render_backward(ctx.meta, st, final_T, last, tile_stop, grad_out)
+        g_m, g_q, g_c, g_o = _ops.render_backward(ctx.meta, st, final_T, last, tile_stop, grad_out, ws)
         need = ctx.needs_input_grad
         g_depth = torch.zeros(ctx.depth_shape, dtype=torch.float32, device=grad_out.device) if need[4] else None
         return (g_m if need[0] else None,
@@ -254,7 +253,7 @@ def _rasterize_chunk_eval(means2d_b, conics_b, colors_b, opacities_b, depths_b, 
     meta = _meta(config, B, G)
     st = _ops.bin_gaussians(meta, *_flat(means2d_b, conics_b, colors_b, opacities_b, depths_b))
     _check_overflow(config, st)
-    img, _, _, _ = _ops.render_forward(meta, st, save_state=False)
+    img = _ops.render_forward(meta, st, save_state=False)[0]
     return img
 
 
@@ -309,7 +308,7 @@ def profile_projected_gaussians(means2d: Tensor, conics: Tensor, colors: Tensor,
         st = _ops.bin_gaussians(meta, *args)
         counts_all.append(st.tile_counts.cpu().to(torch.float32))
         if run_forward or return_image:
-            img, _, _, tile_stop = _ops.render_forward(meta, st, save_state=True)
+            img, _, _, tile_stop, _ = _ops.render_forward(meta, st, save_state=True)
             stops_all.append(tile_stop.cpu().to(torch.float32))
             if return_image:
                 images.append(img)

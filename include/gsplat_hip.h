@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 3
+#define GSPLAT_HIP_ABI_VERSION 4
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -147,37 +147,45 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* -------------------------------------------------------------- composite
- * Forward compositor.  Replaces render_fast_forward_state / _eval
+ * Compositor workspace: the state that lets the backward split heavy tiles
+ * (more than 256 pairs) into segments processed in parallel.  The forward
+ * fills it and the backward of the same binning reads it; n_pairs is the N of
+ * that binning.  Optional (NULL): every tile is then walked by one
+ * wavefront. */
+size_t gsplat_hip_render_workspace_bytes(const gsplat_raster_meta* meta,
+                                         int64_t n_pairs);
+
+/* Forward compositor.  Replaces render_fast_forward_state / _eval
  * (variants/v8/csrc/bindings.cpp:202-203; kernels gsplat_v8_kernels.metal:
- * 330-476).  out_rgb float [B,H,W,3].  State outputs (all nullable together
- * for the eval path): out_final_T float [B,H,W] transmittance after the last
- * composited splat, out_last int32 [B,H,W] = 1 + index (within the tile
- * range) of the last composited splat (0 if none), out_tile_stop int32 [T]
- * = max of out_last over the tile's pixels. */
+ * 330-476).  out_rgb float [B,H,W,3].  State outputs (all NULL together for
+ * the eval path, which also ignores the workspace): out_final_T float [B,H,W]
+ * transmittance after the last composited splat, out_last int32 [B,H,W] =
+ * 1 + index (within the tile range) of the last composited splat (0 if
+ * none), out_tile_stop int32 [T] = max of out_last over the tile's pixels. */
 int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
-                              const float* packed,
-                              const int32_t* tile_offsets,
-                              const int32_t* binned_ids,
-                              float* out_rgb, float* out_final_T,
-                              int32_t* out_last, int32_t* out_tile_stop,
+                              const float* packed, const int32_t* tile_offsets,
+                              const int32_t* binned_ids, float* out_rgb,
+                              float* out_final_T, int32_t* out_last,
+                              int32_t* out_tile_stop, int64_t n_pairs,
+                              void* workspace, size_t workspace_bytes,
                               void* stream);
 
 /* Backward compositor.  Replaces render_fast_backward_saved
  * (variants/v8/csrc/bindings.cpp:204; kernel gsplat_v8_kernels.metal:
- * 478-608).  Gradients are accumulated (atomically) into the ORIGINAL splat
- * order using the orig_index stored in each packed record; the four gradient
- * buffers are zeroed by this call.  g_means2d [BG,2], g_conics [BG,3],
- * g_colors [BG,3], g_opacities [BG]. */
+ * 478-608) and the unsort of v8 rasterize.py:676-680: gradients are written
+ * in the ORIGINAL splat order using the orig_index stored in each packed
+ * record; the four gradient arrays are zeroed by this call.  workspace: the
+ * forward's (or NULL). */
 int gsplat_hip_render_backward(const gsplat_raster_meta* meta,
                                const float* packed,
                                const int32_t* tile_offsets,
                                const int32_t* binned_ids,
                                const float* final_T, const int32_t* last,
-                               const int32_t* tile_stop,
-                               const float* grad_rgb,
+                               const int32_t* tile_stop, const float* grad_rgb,
                                float* g_means2d, float* g_conics,
                                float* g_colors, float* g_opacities,
-                               void* stream);
+                               int64_t n_pairs, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------- projection
  * Pinhole projection.  Replaces torch.ops.gsplat_metal_v9_project3d_train.

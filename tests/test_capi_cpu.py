@@ -30,7 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 3
+    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 4
 
 
 def _meta(**kw):
@@ -66,7 +66,7 @@ def test_invalid_meta_rejected_before_launch(field, value, msg):
     L = _lib.lib()
     m = _meta(**{field: value})
     dummy = ctypes.c_void_p(1)
-    rc = L.gsplat_hip_render_forward(m, dummy, dummy, dummy, dummy, None, None, None, None)
+    rc = L.gsplat_hip_render_forward(m, dummy, dummy, dummy, dummy, None, None, None, 0, None, 0, None)
     assert rc == 1
     assert msg in L.gsplat_hip_last_error().decode()
 
@@ -74,12 +74,12 @@ def test_invalid_meta_rejected_before_launch(field, value, msg):
 def test_null_pointers_rejected():
     L = _lib.lib()
     rc = L.gsplat_hip_render_backward(_meta(), None, None, None, None, None, None, None, None, None, None, None,
-                                      None)
+                                      0, None, 0, None)
     assert rc == 1
     assert "NULL" in L.gsplat_hip_last_error().decode()
     rc = L.gsplat_hip_render_forward(_meta(), ctypes.c_void_p(1), ctypes.c_void_p(1), None, ctypes.c_void_p(1),
-                                     ctypes.c_void_p(1), None, None, None)
-    assert rc == 1 and "both" in L.gsplat_hip_last_error().decode()
+                                     ctypes.c_void_p(1), None, None, 0, None, 0, None)
+    assert rc == 1 and "all be given" in L.gsplat_hip_last_error().decode()
 
 
 def test_workspace_too_small_rejected():
@@ -97,6 +97,14 @@ def test_workspace_too_small_rejected():
     assert need >= 2 * 4 * 16 * 4          # B * ceil(G/256) * 16 floats
     rc = L.gsplat_hip_project_backward(pm, *([one] * 16), one, need - 1, None)
     assert rc == 3 and "project_backward" in L.gsplat_hip_last_error().decode()
+    need = L.gsplat_hip_render_workspace_bytes(_meta(), 100000)
+    assert need > L.gsplat_hip_render_workspace_bytes(_meta(), 1000) > 0
+    rc = L.gsplat_hip_render_forward(_meta(), *([one] * 7), 100000, one, need - 1, None)
+    assert rc == 3 and "render_forward" in L.gsplat_hip_last_error().decode()
+    rc = L.gsplat_hip_render_backward(_meta(), *([one] * 11), 100000, one, need - 1, None)
+    assert rc == 3 and "render_backward" in L.gsplat_hip_last_error().decode()
+    rc = L.gsplat_hip_render_forward(_meta(), *([one] * 7), -1, None, 0, None)
+    assert rc == 1 and "pair count" in L.gsplat_hip_last_error().decode()
 
 
 def test_projection_meta_rejected():
