@@ -352,7 +352,6 @@ int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
                   (long long)n_pairs);
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
-  if (out_final_T == nullptr) workspace = nullptr;  // eval path: no state
   if (workspace != nullptr &&
       workspace_bytes < gs::render_workspace_bytes(P, n_pairs)) {
     gs::set_error("gsplat_hip_render_forward: workspace too small (%zu < %zu)",

@@ -176,47 +176,176 @@ __device__ __forceinline__ uint32_t uniform_bits(float v) {
   return __builtin_amdgcn_readfirstlane(__float_as_uint(v));
 }
 
-// Heavy tiles.  A tile whose range holds more than kHeavyCount pairs gets
-// ceil(count / kSegSplats) segment slots.  For each segment k the forward
-// records per pixel seg[k] = (colour composited by the segment's splats,
-// transmittance at the segment's end); its colour accumulators restart at
-// every segment boundary, the completed segments' colour being summed in the
-// output pixel.  With those records the backward of segment k needs nothing
-// from the later segments' walks: the gT
-// of the reverse recurrence at the segment's end is
+// Long tiles.  A tile range is cut into segments of kSegSplats splats and
+// colour is summed per segment: at each segment boundary a pixel's colour
+// accumulators are added into its output pixel (which holds the sum of the
+// completed segments; each lane reads back only what it wrote itself) and
+// restart at zero.  The order of the additions depends on the tile range
+// alone, so every variant of the forward gives the same image.
+//
+// With a workspace the forward also
+//  * hands a tile that still has live pixels after kHandoff splats to
+//    render_fwd_long_kernel, where four wavefronts (one per strip) continue
+//    it from the saved state (T in the workspace, last in out_last, the
+//    colour sum in the output), so a long tile no longer serialises one
+//    wavefront;
+//  * with the state outputs (training), records every segment of a tile
+//    whose walk crosses a boundary: rec = (colour composited by the segment,
+//    T at its end) per pixel, in a slot linked into the tile's chain.
+// The backward then walks the segments of a tile whose stop exceeds one
+// segment in parallel: the gT of the reverse recurrence at the end of
+// segment k is
 //   gT_k = (<g, sum_{j>k} colour_j> + <g, bg> T_final) / T_end_k,
 // the closed form of gT <- alpha <g,c> + (1 - alpha) gT over the later
-// splats.  Segments of a tile whose stop exceeds one segment are then walked
-// in parallel, each by its own wavefront, in the same launch as the other
-// tiles.
-constexpr int kSegSplats = 128;   // multiple of kBatch
-constexpr int kHeavyCount = 128;  // >= kSegSplats
+// splats, and T at its end is recorded.
+constexpr int kSegSplats = 128;     // multiple of kBatch
+constexpr int kHandoff = 128;       // multiple of kSegSplats
+constexpr int kLongThreads = 256;   // one wavefront per strip
 
-struct HeavyState {    // all null: no heavy-tile handling
-  int32_t* counter;    // segment slots handed out (zeroed before the forward)
-  int32_t* tile_slot;  // [T] first slot of a heavy tile, -1 otherwise
-  int32_t* slot_tile;  // [max_slots] tile of each slot
-  float4* seg;         // [max_slots][256] (r, g, b, T at the segment's end)
+struct HeavyState {      // all null: every tile is walked whole by one wave
+  int32_t* counters;     // [0] slots handed out, [1] tiles handed off
+                         // (zeroed by the forward)
+  int32_t* tile_slot;    // [T] slot of segment 0, -1: no usable chain
+  int32_t* slot_tile;    // [max_slots] tile of each slot
+  int32_t* slot_seg;     // [max_slots] segment index of each slot
+  int32_t* slot_next;    // [max_slots] slot of the next segment, -1: none
+  int32_t* handoff;      // [T] tiles handed to render_fwd_long_kernel
+  int32_t* handoff_tail; // [T] their chain's last slot, -2: chain broken
+  float* hand_T;         // [T][256] T of each pixel at the hand-off
+  float4* rec;           // [max_slots][256] (r, g, b, T at segment end);
+                         // null: no records (forward without state)
   int max_slots;
 };
 
-// Pixel index inside the tile used by the per-pixel heavy-tile buffers.
+// One lane per tile: the slot for segment `seg` of `tile`, linked after the
+// chain tail `tail` (-1 before segment 0, -2 once broken); -1 if no record
+// is kept.  When the workspace is full the chain breaks for good and
+// tile_slot is cleared, so the backward walks that tile whole.
+__device__ int next_segment(const HeavyState& H, int tile, int seg,
+                            int& tail) {
+  if (H.rec == nullptr || tail == -2) return -1;
+  const int s = atomicAdd(H.counters, 1);
+  if (s >= H.max_slots) {
+    H.tile_slot[tile] = -1;
+    tail = -2;
+    return -1;
+  }
+  H.slot_tile[s] = tile;
+  H.slot_seg[s] = seg;
+  H.slot_next[s] = -1;
+  if (tail < 0)
+    H.tile_slot[tile] = s;
+  else
+    H.slot_next[tail] = s;
+  tail = s;
+  return s;
+}
+
+// Pixel index inside the tile used by the per-pixel segment records.
 __device__ __forceinline__ int tile_pixel(int k) {
   return 64 * k + (int)threadIdx.x;
 }
 
-// Output pixel of this lane's first strip.  Computed where it is used, from
-// an opaque copy of the lane id, so that the compiler does not keep four
-// 64-bit pixel addresses live across the compositing loop for the rare
-// segment boundaries.
-__device__ __forceinline__ float* heavy_out(const RasterParams& P,
+// The thread id through an empty asm: addresses derived from it are
+// computed where they are used, so that the compiler does not keep 64-bit
+// addresses for the rare segment boundaries live across the compositing
+// loop.
+__device__ __forceinline__ int opaque_tid() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
+// Image index of this thread's pixel in its first strip.
+__device__ __forceinline__ int64_t pixel_index(const RasterParams& P,
+                                               const TileCoord& tc) {
+  const int t = opaque_tid();
+  const int y = tc.y0 + (t >> 4);
+  const int x = tc.x0 + (t & 15);
+  return ((int64_t)tc.batch * P.height + y) * P.width + x;
+}
+
+__device__ __forceinline__ float* pixel_out(const RasterParams& P,
+                                           const TileCoord& tc,
+                                           float* out_rgb) {
+  return out_rgb + 3 * pixel_index(P, tc);
+}
+
+// End of segment `seg` for NP strips per thread: record it in `slot`
+// (if >= 0) and fold its colour into the output pixels.
+template <int NP>
+__device__ __forceinline__ void end_segment(const RasterParams& P,
                                             const TileCoord& tc,
-                                            float* out_rgb) {
-  int lane = (int)threadIdx.x;
-  asm volatile("" : "+v"(lane));
-  const int y = tc.y0 + (lane >> 4);
-  const int x = tc.x0 + (lane & 15);
-  return out_rgb + 3 * (((int64_t)tc.batch * P.height + y) * P.width + x);
+                                            float* out_rgb,
+                                            const HeavyState& H, int slot,
+                                            int seg, const bool* valid,
+                                            float* cr, float* cg, float* cb,
+                                            const float* T) {
+  float* o0 = pixel_out(P, tc, out_rgb);
+  float4* r0 = H.rec + (int64_t)slot * 256 + opaque_tid();
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    if (slot >= 0) r0[64 * k] = make_float4(cr[k], cg[k], cb[k], T[k]);
+    if (valid[k]) {
+      float* o = o0 + (int64_t)12 * k * P.width;
+      if (seg > 0) {
+        cr[k] += o[0];
+        cg[k] += o[1];
+        cb[k] += o[2];
+      }
+      o[0] = cr[k];
+      o[1] = cg[k];
+      o[2] = cb[k];
+    }
+    cr[k] = cg[k] = cb[k] = 0.0f;
+  }
+}
+
+// Last segment of a walk that crossed a boundary: record it and add the
+// completed segments' colour (held in the output pixels) to the
+// accumulators.
+template <int NP>
+__device__ __forceinline__ void last_segment(const RasterParams& P,
+                                             const TileCoord& tc,
+                                             const float* out_rgb,
+                                             const HeavyState& H, int slot,
+                                             const bool* valid, float* cr,
+                                             float* cg, float* cb,
+                                             const float* T) {
+  const float* o0 = pixel_out(P, tc, const_cast<float*>(out_rgb));
+  float4* r0 = H.rec + (int64_t)slot * 256 + opaque_tid();
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    if (slot >= 0) r0[64 * k] = make_float4(cr[k], cg[k], cb[k], T[k]);
+    if (valid[k]) {
+      const float* o = o0 + (int64_t)12 * k * P.width;
+      cr[k] += o[0];
+      cg[k] += o[1];
+      cb[k] += o[2];
+    }
+  }
+}
+
+// Front-to-back compositing of splat j of the staged batch into one pixel.
+__device__ __forceinline__ void composite_one(float Adxdx, float Bdx,
+                                              const float4& a1,
+                                              const float4& a2, float py,
+                                              float my, float t_thr,
+                                              float max_alpha, int idx1,
+                                              float& T, float& cr, float& cg,
+                                              float& cb, int& last) {
+  if (T > t_thr) {
+    const float p = splat_exponent(Adxdx, Bdx, a1.x, py - my);
+    if (p <= 0.0f && p >= a2.z) {
+      const float alpha = fminf(max_alpha, a1.y * __builtin_amdgcn_exp2f(p));
+      const float w = T * alpha;
+      cr += w * a1.z;
+      cg += w * a1.w;
+      cb += w * a2.x;
+      T *= (1.0f - alpha);
+      last = idx1;
+    }
+  }
 }
 
 __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
@@ -247,50 +376,19 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
   }
   const int start = tile_offsets[tc.tile];
   const int end = tile_offsets[tc.tile + 1];
-  // Heavy tiles sum their colour per segment whether or not the segments are
-  // recorded, so the eval and training forwards give identical images.
-  const bool heavy = end - start > kHeavyCount;
-  int slot = -1;
-  if (H.seg != nullptr) {
-    if (heavy) {
-      const int nseg = (end - start + kSegSplats - 1) / kSegSplats;
-      if (threadIdx.x == 0) {
-        slot = atomicAdd(H.counter, nseg);
-        if (slot + nseg > H.max_slots) slot = -1;  // out of slots: plain tile
-      }
-      slot = __shfl(slot, 0, 64);
-      if (slot >= 0)
-        for (int k = threadIdx.x; k < nseg; k += kLanes) H.slot_tile[slot + k] = tc.tile;
-    }
-    if (threadIdx.x == 0) H.tile_slot[tc.tile] = slot;
-  }
+  if (H.rec != nullptr && threadIdx.x == 0) H.tile_slot[tc.tile] = -1;
+  // With a workspace a tile longer than kHandoff is walked here only up to
+  // kHandoff, so segment boundaries inside this loop (and records) occur
+  // only without a workspace.
+  const int walk_end =
+      (H.counters != nullptr && end - start > kHandoff) ? start + kHandoff : end;
   int seg_cur = 0;  // segment of the batch being composited
-  for (int base = start; base < end; base += kBatch) {
+  for (int base = start; base < walk_end; base += kBatch) {
     const bool any_alive = (T[0] > t_thr) | (T[1] > t_thr) | (T[2] > t_thr) |
                            (T[3] > t_thr);
     if (!__any(any_alive)) break;
-    if (heavy && base > start && (base - start) % kSegSplats == 0) {
-      // Segment boundary: record the segment and fold its colour into the
-      // output pixel, which holds the sum of the completed segments (each
-      // lane reads back only what it wrote itself).
-      float4* sp = H.seg + (int64_t)(slot + seg_cur) * 256;
-      float* o0 = heavy_out(P, tc, out_rgb);
-#pragma unroll
-      for (int k = 0; k < kPix; ++k) {
-        if (slot >= 0) sp[tile_pixel(k)] = make_float4(cr[k], cg[k], cb[k], T[k]);
-        if (valid[k]) {
-          float* o = o0 + (int64_t)12 * k * P.width;
-          if (seg_cur > 0) {
-            cr[k] += o[0];
-            cg[k] += o[1];
-            cb[k] += o[2];
-          }
-          o[0] = cr[k];
-          o[1] = cg[k];
-          o[2] = cb[k];
-        }
-        cr[k] = cg[k] = cb[k] = 0.0f;
-      }
+    if (base > start && (base - start) % kSegSplats == 0) {
+      end_segment<kPix>(P, tc, out_rgb, H, -1, seg_cur, valid, cr, cg, cb, T);
       ++seg_cur;
     }
     const int n = min(kBatch, end - base);
@@ -303,43 +401,53 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
       if (mask == 0u) continue;
       const float4 a0 = S.s0[j];
       const float4 a1 = S.s1[j];
-      const float plim = a2.z;
       float Adxdx, Bdx;
       x_terms(a0.z, a0.w, px - a0.x, Adxdx, Bdx);
       const int idx1 = base - start + j + 1;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
         if (!((mask >> k) & 1u)) continue;  // scalar branch
-        if (T[k] > t_thr) {
-          const float p = splat_exponent(Adxdx, Bdx, a1.x, py[k] - a0.y);
-          if (p <= 0.0f && p >= plim) {
-            const float alpha =
-                fminf(max_alpha, a1.y * __builtin_amdgcn_exp2f(p));
-            const float w = T[k] * alpha;
-            cr[k] += w * a1.z;
-            cg[k] += w * a1.w;
-            cb[k] += w * a2.x;
-            T[k] *= (1.0f - alpha);
-            last[k] = idx1;
-          }
-        }
+        composite_one(Adxdx, Bdx, a1, a2, py[k], a0.y, t_thr, max_alpha, idx1,
+                      T[k], cr[k], cg[k], cb[k], last[k]);
       }
     }
   }
-  if (heavy) {
-    // the segment composited last; later segments hold no pixel's last
-    float4* sp = H.seg + (int64_t)(slot + seg_cur) * 256;
+  if (walk_end < end) {
+    const bool any_alive = (T[0] > t_thr) | (T[1] > t_thr) | (T[2] > t_thr) |
+                           (T[3] > t_thr);
+    if (__any(any_alive)) {
+      // Close segment 0 and hand the rest of the tile to the four-wavefront
+      // kernel: T to the workspace, last to out_last, the colour sum is in
+      // the output.
+      int tail = -1, slot = -1;  // chain state, meaningful in lane 0
+      if (threadIdx.x == 0) slot = next_segment(H, tc.tile, 0, tail);
+      slot = __shfl(slot, 0, 64);
+      end_segment<kPix>(P, tc, out_rgb, H, slot, 0, valid, cr, cg, cb, T);
+      int item = 0;
+      if (threadIdx.x == 0) item = atomicAdd(H.counters + 1, 1);
+      item = __shfl(item, 0, 64);
+      const int64_t pix0 = pixel_index(P, tc);
+      int tile_max = 0;
 #pragma unroll
-    for (int k = 0; k < kPix; ++k) {
-      if (slot >= 0) sp[tile_pixel(k)] = make_float4(cr[k], cg[k], cb[k], T[k]);
-      if (valid[k] && seg_cur > 0) {
-        const float* o = heavy_out(P, tc, out_rgb) + (int64_t)12 * k * P.width;
-        cr[k] += o[0];
-        cg[k] += o[1];
-        cb[k] += o[2];
+      for (int k = 0; k < kPix; ++k) {
+        H.hand_T[(int64_t)item * 256 + tile_pixel(k)] = T[k];
+        if (out_last != nullptr && valid[k])
+          out_last[pix0 + (int64_t)4 * k * P.width] = last[k];
+        tile_max = max(tile_max, last[k]);
       }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1)
+        tile_max = max(tile_max, __shfl_xor(tile_max, off, 64));
+      if (threadIdx.x == 0) {
+        if (out_tile_stop != nullptr) out_tile_stop[tc.tile] = tile_max;
+        H.handoff[item] = tc.tile;
+        H.handoff_tail[item] = tail;
+      }
+      return;
     }
   }
+  if (seg_cur > 0)  // (no workspace: nothing recorded)
+    last_segment<kPix>(P, tc, out_rgb, H, -1, valid, cr, cg, cb, T);
   int tile_max = 0;
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
@@ -361,6 +469,89 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     for (int off = 32; off > 0; off >>= 1)
       tile_max = max(tile_max, __shfl_xor(tile_max, off, 64));
     if (threadIdx.x == 0) out_tile_stop[tc.tile] = tile_max;
+  }
+}
+
+// Continuation of the tiles handed off by render_fwd_kernel: a workgroup of
+// four wavefronts per tile, wavefront w walking strip w (one pixel per
+// thread) from the saved state with the same per-pixel operations, so the
+// result is bit for bit the one-wavefront walk's.  Workgroup b takes
+// hand-off items b, b + gridDim.x, ...
+__global__ __launch_bounds__(kLongThreads) void render_fwd_long_kernel(
+    RasterParams P, const float4* __restrict__ packed,
+    const int32_t* __restrict__ tile_offsets,
+    const int32_t* __restrict__ binned, float* __restrict__ out_rgb,
+    float* __restrict__ out_T, int32_t* __restrict__ out_last,
+    int32_t* __restrict__ out_tile_stop, HeavyState H) {
+  __shared__ Staged S;
+  __shared__ int sh_slot;
+  const int strip = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int n_items = H.counters[1];
+  const float t_thr = P.trans_thr;
+  const float max_alpha = fminf(P.max_alpha, 1.0f);
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    __syncthreads();  // the previous tile's reads of S and sh_slot are done
+    const int tile = H.handoff[item];
+    int tail = H.handoff_tail[item];  // used by thread 0
+    // tile_coord_of with a 256-thread id: ly = 4 strip + l/16, so slot 0 of
+    // this thread is its pixel of strip `strip`, and tile_pixel(0) its index.
+    const TileCoord tc = tile_coord_of(P, tile);
+    const int x = tc.x0 + tc.lx;
+    const int y = slot_y(tc, 0);
+    const float px = (float)x + 0.5f, py = (float)y + 0.5f;
+    bool valid[1] = {(x < P.width) && (y < P.height)};
+    const int64_t pix = ((int64_t)tc.batch * P.height + y) * P.width + x;
+    float T[1] = {H.hand_T[(int64_t)item * 256 + tile_pixel(0)]};
+    int last = (valid[0] && out_last != nullptr) ? out_last[pix] : 0;
+    float cr[1] = {0.0f}, cg[1] = {0.0f}, cb[1] = {0.0f};
+    const int start = tile_offsets[tile];
+    const int end = tile_offsets[tile + 1];
+    int seg_cur = kHandoff / kSegSplats;
+    for (int base = start + kHandoff; base < end; base += kBatch) {
+      if (!__syncthreads_or(T[0] > t_thr)) break;  // uniform; frees S
+      // (the boundary at kHandoff was closed by render_fwd_kernel)
+      if (base > start + kHandoff && (base - start) % kSegSplats == 0) {
+        if (threadIdx.x == 0) sh_slot = next_segment(H, tile, seg_cur, tail);
+        __syncthreads();
+        end_segment<1>(P, tc, out_rgb, H, sh_slot, seg_cur, valid, cr, cg, cb,
+                       T);
+        ++seg_cur;
+      }
+      const int n = min(kBatch, end - base);
+      stage_batch(packed, binned, base, n, tc, S);
+      __syncthreads();
+      for (int j = 0; j < n; ++j) {
+        const float4 a2 = S.s2[j];
+        const uint32_t mask = uniform_bits(a2.w);
+        if (!((mask >> strip) & 1u)) continue;  // scalar branch
+        const float4 a0 = S.s0[j];
+        const float4 a1 = S.s1[j];
+        float Adxdx, Bdx;
+        x_terms(a0.z, a0.w, px - a0.x, Adxdx, Bdx);
+        composite_one(Adxdx, Bdx, a1, a2, py, a0.y, t_thr, max_alpha,
+                      base - start + j + 1, T[0], cr[0], cg[0], cb[0], last);
+      }
+    }
+    __syncthreads();  // sh_slot of the last boundary has been read
+    if (threadIdx.x == 0) sh_slot = next_segment(H, tile, seg_cur, tail);
+    __syncthreads();
+    last_segment<1>(P, tc, out_rgb, H, sh_slot, valid, cr, cg, cb, T);
+    if (valid[0]) {
+      out_rgb[3 * pix + 0] = cr[0] + T[0] * P.bg_r;
+      out_rgb[3 * pix + 1] = cg[0] + T[0] * P.bg_g;
+      out_rgb[3 * pix + 2] = cb[0] + T[0] * P.bg_b;
+      if (out_T != nullptr) {
+        out_T[pix] = T[0];
+        out_last[pix] = last;
+      }
+    }
+    if (out_tile_stop != nullptr) {
+      int tile_max = valid[0] ? last : 0;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1)
+        tile_max = max(tile_max, __shfl_xor(tile_max, off, 64));
+      if ((threadIdx.x & 63) == 0) atomicMax(out_tile_stop + tile, tile_max);
+    }
   }
 }
 
@@ -594,27 +785,23 @@ __device__ __forceinline__ bool heavy_backward(const HeavyState& H, int tile,
 __device__ __forceinline__ bool seg_item(const RasterParams& P,
                                          const HeavyState& H,
                                          const int32_t* __restrict__ tile_stop,
-                                         int m, int& tile, int& slot0, int& k,
-                                         int& nseg, int& lo, int& hi) {
-  if (H.counter == nullptr || m >= *H.counter || m >= H.max_slots) return false;
+                                         int m, int& tile, int& k, int& nseg,
+                                         int& lo, int& hi) {
   tile = H.slot_tile[m];
-  // Only slots handed to a recorded tile are meaningful: check the tile id
-  // and that m lies inside that tile's own slot range.
   if (tile < 0 || tile >= P.num_tiles) return false;
-  slot0 = H.tile_slot[tile];
   const int nstop = tile_stop[tile];
-  if (slot0 < 0 || m < slot0 || nstop <= kSegSplats) return false;
-  k = m - slot0;
+  if (!heavy_backward(H, tile, nstop)) return false;
+  k = H.slot_seg[m];
   nseg = (nstop + kSegSplats - 1) / kSegSplats;
-  if (k >= nseg || slot0 > H.max_slots - nseg) return false;
+  if (k < 0 || k >= nseg) return false;
   lo = k * kSegSplats;
   hi = min(lo + kSegSplats, nstop);
   return true;
 }
 
-// Work items: blocks [0, seg_blocks) are heavy-tile segment slots (the
-// longest walks, dispatched first), the rest are tiles (heavy tiles among
-// them return at once).
+// Work items: block m < seg_blocks walks segment slot m (the longest walks,
+// dispatched first), the other blocks are tiles (tiles walked as segments
+// return at once).
 __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ tile_offsets,
@@ -624,66 +811,80 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
     float* __restrict__ g_conics, float* __restrict__ g_colors,
     float* __restrict__ g_opac, HeavyState H, int seg_blocks) {
   __shared__ Staged S;
-  int tile, slot0 = 0, kseg = 0, nseg = 1, lo = 0, hi;
   const int bid = (int)blockIdx.x;
-  if (bid < seg_blocks) {
-    if (!seg_item(P, H, tile_stop, bid, tile, slot0, kseg, nseg, lo, hi))
-      return;
-  } else {
-    // seg_blocks is a multiple of 8, so the XCD-aware mapping is preserved
-    tile = xcd_remap(bid - seg_blocks, P.num_tiles);
-    hi = tile_stop[tile];
-    if (hi <= 0) return;
-    if (heavy_backward(H, tile, hi)) return;  // walked as segments
-  }
-  const TileCoord tc = tile_coord_of(P, tile);
-  BwdPixels Q;
-  load_bwd_pixels(P, tc, final_T, last_in, grad_rgb, Q);
-  if (kseg < nseg - 1) {
-    // Pixels composited past this segment: T and gT at its end from the
-    // forward's segment records (Q.gT holds <g, bg>, Q.Tc holds T_final).
-    const float4* rec = H.seg + (int64_t)slot0 * 256;
-    float cr[kPix], cg[kPix], cb[kPix];
+  const bool seg = bid < seg_blocks;
+  const int m = bid;
+  {
+    int tile, kseg = 0, nseg = 1, lo = 0, hi;
+    if (seg) {
+      if (m >= min(H.counters[0], H.max_slots)) return;
+      if (!seg_item(P, H, tile_stop, m, tile, kseg, nseg, lo, hi)) return;
+    } else {
+      // seg_blocks is a multiple of 8, so the XCD-aware mapping is kept
+      tile = xcd_remap(bid - seg_blocks, P.num_tiles);
+      hi = tile_stop[tile];
+      if (hi <= 0) return;
+      if (heavy_backward(H, tile, hi)) return;  // walked as segments
+    }
+    const TileCoord tc = tile_coord_of(P, tile);
+    BwdPixels Q;
+    load_bwd_pixels(P, tc, final_T, last_in, grad_rgb, Q);
+    {
+      if (kseg < nseg - 1) {
+        // Pixels composited past this segment: T and gT at its end from the
+        // forward's segment records (Q.gT holds <g, bg>, Q.Tc T_final).
+        float cr[kPix], cg[kPix], cb[kPix];
 #pragma unroll
-    for (int k = 0; k < kPix; ++k) cr[k] = cg[k] = cb[k] = 0.0f;
-    for (int j = kseg + 1; j < nseg; ++j) {
+        for (int k = 0; k < kPix; ++k) cr[k] = cg[k] = cb[k] = 0.0f;
+        const int t = opaque_tid();
+        int sl = H.slot_next[m];
+        for (int j = kseg + 1;
+             j < nseg && (unsigned)sl < (unsigned)H.max_slots; ++j) {
+          const float4* rj = H.rec + (int64_t)sl * 256 + t;
 #pragma unroll
-      for (int k = 0; k < kPix; ++k) {
-        const float4 v = rec[j * 256 + tile_pixel(k)];
-        cr[k] += v.x;
-        cg[k] += v.y;
-        cb[k] += v.z;
+          for (int k = 0; k < kPix; ++k) {
+            const float4 v = rj[64 * k];
+            cr[k] += v.x;
+            cg[k] += v.y;
+            cb[k] += v.z;
+          }
+          sl = H.slot_next[sl];
+        }
+        const float4* rm = H.rec + (int64_t)m * 256 + t;
+#pragma unroll
+        for (int k = 0; k < kPix; ++k) {
+          if (Q.lk[k] > hi) {
+            const float Te = rm[64 * k].w;  // > 0: the pixel was alive
+            const float num = Q.gr[k] * cr[k] + Q.gg[k] * cg[k] +
+                              Q.gb[k] * cb[k] + Q.gT[k] * Q.Tc[k];
+            Q.gT[k] = num / Te;
+            Q.Tc[k] = Te;
+          }
+        }
       }
     }
-#pragma unroll
-    for (int k = 0; k < kPix; ++k) {
-      if (Q.lk[k] > hi) {
-        const float Te = rec[kseg * 256 + tile_pixel(k)].w;  // > 0: alive
-        const float num = Q.gr[k] * cr[k] + Q.gg[k] * cg[k] +
-                          Q.gb[k] * cb[k] + Q.gT[k] * Q.Tc[k];
-        Q.gT[k] = num / Te;
-        Q.Tc[k] = Te;
-      }
-    }
+    bwd_walk(P, packed, binned, tile_offsets[tile], lo, hi, tc, S, Q,
+             g_means2d, g_conics, g_colors, g_opac);
   }
-  bwd_walk(P, packed, binned, tile_offsets[tile], lo, hi, tc, S, Q, g_means2d,
-           g_conics, g_colors, g_opac);
 }
 
+// Segment records kept at most: one per segment of every tile in the worst
+// case, capped at T + 1024 (4 KB each: at most 16 B per pixel + 4 MB).
+// Tiles that find the records full are walked whole by the backward.
 size_t heavy_max_slots(const RasterParams& P, int64_t n_pairs) {
-  // A heavy tile (> kHeavyCount pairs) with c pairs takes ceil(c / kSegSplats)
-  // < c / kSegSplats + 1 slots, and there are at most
-  // min(T, n_pairs / kHeavyCount) heavy tiles.
-  const int64_t tiles = std::min<int64_t>(P.num_tiles, n_pairs / kHeavyCount);
-  return (size_t)(n_pairs / kSegSplats + tiles + 1);
+  const int64_t per_seg = n_pairs / kSegSplats;
+  const int64_t worst =
+      per_seg + std::min<int64_t>(P.num_tiles, per_seg) + 1;
+  return (size_t)std::min<int64_t>(worst, (int64_t)P.num_tiles + 1024);
 }
 
 }  // namespace
 
 size_t render_workspace_bytes(const RasterParams& P, int64_t n_pairs) {
   const size_t slots = heavy_max_slots(P, n_pairs);
-  return 256 + align_up((size_t)P.num_tiles * 4, 256) + align_up(slots * 4, 256) +
-         align_up(slots * 256 * sizeof(float4), 256);
+  const size_t T = (size_t)P.num_tiles;
+  return 256 + 3 * align_up(T * 4, 256) + align_up(T * 256 * 4, 256) +
+         3 * align_up(slots * 4, 256) + align_up(slots * 256 * sizeof(float4), 256);
 }
 
 namespace {
@@ -691,14 +892,25 @@ HeavyState heavy_state(const RasterParams& P, int64_t n_pairs, void* ws) {
   HeavyState H{};
   if (ws == nullptr) return H;
   const size_t slots = heavy_max_slots(P, n_pairs);
+  const size_t T = (size_t)P.num_tiles;
   char* p = static_cast<char*>(ws);
-  H.counter = reinterpret_cast<int32_t*>(p);
+  H.counters = reinterpret_cast<int32_t*>(p);
   p += 256;
   H.tile_slot = reinterpret_cast<int32_t*>(p);
-  p += align_up((size_t)P.num_tiles * 4, 256);
+  p += align_up(T * 4, 256);
+  H.handoff = reinterpret_cast<int32_t*>(p);
+  p += align_up(T * 4, 256);
+  H.handoff_tail = reinterpret_cast<int32_t*>(p);
+  p += align_up(T * 4, 256);
+  H.hand_T = reinterpret_cast<float*>(p);
+  p += align_up(T * 256 * 4, 256);
   H.slot_tile = reinterpret_cast<int32_t*>(p);
   p += align_up(slots * 4, 256);
-  H.seg = reinterpret_cast<float4*>(p);
+  H.slot_seg = reinterpret_cast<int32_t*>(p);
+  p += align_up(slots * 4, 256);
+  H.slot_next = reinterpret_cast<int32_t*>(p);
+  p += align_up(slots * 4, 256);
+  H.rec = reinterpret_cast<float4*>(p);
   H.max_slots = (int)slots;
   return H;
 }
@@ -711,16 +923,24 @@ int launch_render_forward(const RasterParams& P, const float* packed,
                           int32_t* out_tile_stop, int64_t n_pairs,
                           void* workspace, hipStream_t stream) {
   if (P.num_tiles == 0) return GSPLAT_OK;
-  const HeavyState H = heavy_state(P, n_pairs, workspace);
-  if (H.counter != nullptr) {
-    const int rc = launch_fill_i32(H.counter, 0, 1, stream);
+  HeavyState H = heavy_state(P, n_pairs, workspace);
+  if (out_T == nullptr) H.rec = nullptr;  // no backward: hand-off only
+  const float4* pk = reinterpret_cast<const float4*>(packed);
+  if (H.counters != nullptr) {
+    const int rc = launch_fill_i32(H.counters, 0, 2, stream);
     if (rc) return rc;
   }
   hipLaunchKernelGGL(render_fwd_kernel, dim3((unsigned)P.num_tiles),
-                     dim3(kLanes), 0, stream, P,
-                     reinterpret_cast<const float4*>(packed), tile_offsets,
-                     binned_ids, out_rgb, out_T, out_last, out_tile_stop, H);
-  return check_launch("render_fwd_kernel");
+                     dim3(kLanes), 0, stream, P, pk, tile_offsets, binned_ids,
+                     out_rgb, out_T, out_last, out_tile_stop, H);
+  int rc = check_launch("render_fwd_kernel");
+  if (rc || H.counters == nullptr) return rc;
+  // Workgroups stride over the hand-off list (its length is on the device).
+  const unsigned grid = (unsigned)std::min<int64_t>(P.num_tiles, 2048);
+  hipLaunchKernelGGL(render_fwd_long_kernel, dim3(grid), dim3(kLongThreads), 0,
+                     stream, P, pk, tile_offsets, binned_ids, out_rgb, out_T,
+                     out_last, out_tile_stop, H);
+  return check_launch("render_fwd_long_kernel");
 }
 
 int launch_render_backward(const RasterParams& P, const float* packed,
@@ -737,7 +957,8 @@ int launch_render_backward(const RasterParams& P, const float* packed,
   if (P.num_tiles == 0) return GSPLAT_OK;
   const HeavyState H = heavy_state(P, n_pairs, workspace);
   const float4* pk = reinterpret_cast<const float4*>(packed);
-  const int seg_blocks = H.counter ? (H.max_slots + 7) & ~7 : 0;
+  // One block per possible slot, rounded to a multiple of 8 (XCD mapping).
+  const int seg_blocks = H.counters ? (H.max_slots + 7) & ~7 : 0;
   hipLaunchKernelGGL(render_bwd_kernel,
                      dim3((unsigned)(seg_blocks + P.num_tiles)), dim3(kLanes),
                      0, stream, P, pk, tile_offsets, binned_ids, final_T, last,

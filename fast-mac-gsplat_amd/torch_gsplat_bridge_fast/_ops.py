@@ -126,27 +126,27 @@ def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors
 
 
 def render_forward(meta: _lib.RasterMeta, st: BinState, *, save_state: bool):
-    """Returns (img, final_T, last, tile_stop, workspace); the last four are None unless save_state.
-    The workspace holds the heavy-tile segment state the backward reads."""
+    """Returns (img, final_T, last, tile_stop, workspace); the state tensors are None unless
+    save_state.  The workspace lets long tiles be continued by four wavefronts and, with the state,
+    holds the segment records the backward reads."""
     L = _lib.lib()
     dev = st.packed.device
     B, H, W = meta.batch, meta.height, meta.width
     tiles = st.num_tiles
     img = torch.empty((B, H, W, 3), dtype=torch.float32, device=dev)
-    final_T = last = tile_stop = ws = None
-    wsb = 0
+    final_T = last = tile_stop = None
     if save_state:
         final_T = torch.empty((B, H, W), dtype=torch.float32, device=dev)
         last = torch.empty((B, H, W), dtype=torch.int32, device=dev)
         tile_stop = _empty(tiles, torch.int32, dev)
-        wsb = L.gsplat_hip_render_workspace_bytes(meta, st.n_pairs)
-        ws = _empty(max(wsb, 1), torch.uint8, dev)
+    wsb = L.gsplat_hip_render_workspace_bytes(meta, st.n_pairs)
+    ws = _empty(max(wsb, 1), torch.uint8, dev)
     with _timed("render_forward"):
         check(L.gsplat_hip_render_forward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.binned_ids), ptr(img),
                                           ptr(final_T), ptr(last), ptr(tile_stop), st.n_pairs, ptr(ws), wsb,
                                           stream_of(img)),
               "gsplat_hip_render_forward")
-    return img, final_T, last, tile_stop, ws
+    return img, final_T, last, tile_stop, (ws if save_state else None)
 
 
 def render_backward(meta: _lib.RasterMeta, st: BinState, final_T: Tensor, last: Tensor, tile_stop: Tensor,

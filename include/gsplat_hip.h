@@ -147,18 +147,20 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* -------------------------------------------------------------- composite
- * Compositor workspace: the state that lets the backward split heavy tiles
- * (more than 256 pairs) into segments processed in parallel.  The forward
- * fills it and the backward of the same binning reads it; n_pairs is the N of
- * that binning.  Optional (NULL): every tile is then walked by one
- * wavefront. */
+ * Compositor workspace (optional; n_pairs is the N of the binning).  With it
+ * the forward continues a tile that still has live pixels after 128 splats
+ * with four wavefronts, and, when the state outputs are given, records the
+ * tile's 128-splat segments so that the backward given the same workspace
+ * walks them in parallel.  Without it every tile is walked by one wavefront.
+ * Images are identical either way; gradients differ only in summation
+ * order.  The forward overwrites the workspace; the backward only reads it. */
 size_t gsplat_hip_render_workspace_bytes(const gsplat_raster_meta* meta,
                                          int64_t n_pairs);
 
 /* Forward compositor.  Replaces render_fast_forward_state / _eval
  * (variants/v8/csrc/bindings.cpp:202-203; kernels gsplat_v8_kernels.metal:
  * 330-476).  out_rgb float [B,H,W,3].  State outputs (all NULL together for
- * the eval path, which also ignores the workspace): out_final_T float [B,H,W]
+ * the eval path): out_final_T float [B,H,W]
  * transmittance after the last composited splat, out_last int32 [B,H,W] =
  * 1 + index (within the tile range) of the last composited splat (0 if
  * none), out_tile_stop int32 [T] = max of out_last over the tile's pixels. */

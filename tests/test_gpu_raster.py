@@ -237,9 +237,9 @@ def _faint_crowd(seed, B, G, H, W):
 
 
 def test_heavy_tiles_segmented_backward(gpu):
-    """Tiles with up to ~970 composited splats: the backward splits them into
-    128-splat segments, each started from the forward's per-segment colour and
-    transmittance records.  Checked against the tile oracle at the image/gradient bar,
+    """Tiles with up to ~970 composited splats: the forward continues them
+    with four wavefronts after 128 splats and records 128-splat segments,
+    which the backward walks in parallel, each started from the records.  Checked against the tile oracle at the image/gradient bar,
     and against the single-wavefront backward (no workspace) of the same
     forward state, which differs only in summation order."""
     from torch_gsplat_bridge_fast import _lib, _ops
@@ -263,7 +263,21 @@ def test_heavy_tiles_segmented_backward(gpu):
     meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, (0, 0, 0))
     flat = [sc[k].reshape(B * G, -1).squeeze(-1).contiguous().to(gpu) for k in KEYS]
     st = _ops.bin_gaussians(meta, *flat)
-    _, T, last, stop, ws = _ops.render_forward(meta, st, save_state=True)
+    img_ws, T, last, stop, ws = _ops.render_forward(meta, st, save_state=True)
+    # the forward without a workspace (every tile walked by one wavefront, no
+    # hand-off) gives bit-identical outputs
+    L = _lib.lib()
+    img1 = torch.empty_like(img_ws)
+    T1, last1, stop1 = torch.empty_like(T), torch.empty_like(last), torch.empty_like(stop)
+    _lib.check(L.gsplat_hip_render_forward(meta, _lib.ptr(st.packed), _lib.ptr(st.tile_offsets),
+                                           _lib.ptr(st.binned_ids), _lib.ptr(img1), _lib.ptr(T1), _lib.ptr(last1),
+                                           _lib.ptr(stop1), st.n_pairs, None, 0, _lib.stream_of(img1)),
+               "gsplat_hip_render_forward")
+    img_eval = _ops.render_forward(meta, st, save_state=False)[0]
+    torch.cuda.synchronize()
+    assert torch.equal(img1, img_ws) and torch.equal(img_eval, img_ws)
+    assert torch.equal(T1, T) and torch.equal(last1, last) and torch.equal(stop1, stop)
+    np.testing.assert_array_equal(stop.cpu().numpy(), ostop)
     wd = w.to(gpu)
     seg = _ops.render_backward(meta, st, T, last, stop, wd, ws)
     one = _ops.render_backward(meta, st, T, last, stop, wd, None)
