@@ -521,11 +521,13 @@ __global__ __launch_bounds__(kLongThreads) void render_fwd_long_kernel(
       stage_batch(packed, binned, base, n, tc, S);
       __syncthreads();
       for (int j = 0; j < n; ++j) {
-        const float4 a2 = S.s2[j];
+        // all three reads issued before the mask test: one LDS round trip
+        float4 a0 = S.s0[j], a1 = S.s1[j], a2 = S.s2[j];
+        asm volatile("" : "+v"(a0.x), "+v"(a0.y), "+v"(a0.z), "+v"(a0.w),
+                     "+v"(a1.x), "+v"(a1.y), "+v"(a1.z), "+v"(a1.w),
+                     "+v"(a2.x), "+v"(a2.z), "+v"(a2.w));
         const uint32_t mask = uniform_bits(a2.w);
         if (!((mask >> strip) & 1u)) continue;  // scalar branch
-        const float4 a0 = S.s0[j];
-        const float4 a1 = S.s1[j];
         float Adxdx, Bdx;
         x_terms(a0.z, a0.w, px - a0.x, Adxdx, Bdx);
         composite_one(Adxdx, Bdx, a1, a2, py, a0.y, t_thr, max_alpha,
