@@ -18,14 +18,31 @@ from . import _lib
 from ._lib import check, ptr, stream_of
 
 
-# Optional per-op timing: when enabled, every C-ABI call below is bracketed by
-# torch.cuda events recorded on the stream the work is enqueued on.
+# Optional per-op timing: when enabled, the C-ABI calls below (all, or those
+# named in `ops`) are bracketed by timing events recorded on the stream the
+# work is enqueued on.  The events come from a pool created up front, so a
+# timed call costs two event records and no event creation.
 _timing: Optional[list] = None
+_timing_ops: Optional[set] = None
+_pool: list = []
 
 
-def set_timing(enabled: bool) -> None:
-    global _timing
+def set_timing(enabled: bool, ops=None, pool: int = 0) -> None:
+    """Starts (or stops) recording; `pool` events are created now and used first."""
+    global _timing, _timing_ops, _pool
     _timing = [] if enabled else None
+    _timing_ops = set(ops) if ops is not None else None
+    _pool = []
+    if enabled and pool:
+        _pool = [torch.cuda.Event(enable_timing=True) for _ in range(pool)]
+        for e in _pool:          # creates the underlying HIP events
+            e.record()
+        torch.cuda.synchronize()
+        _pool.reverse()
+
+
+def _event():
+    return _pool.pop() if _pool else torch.cuda.Event(enable_timing=True)
 
 
 def pop_timing() -> list:
@@ -39,16 +56,17 @@ def pop_timing() -> list:
 class _timed:
     def __init__(self, name):
         self.name = name
+        self.on = _timing is not None and (_timing_ops is None or name in _timing_ops)
 
     def __enter__(self):
-        if _timing is not None:
-            self.e0 = torch.cuda.Event(enable_timing=True)
+        if self.on:
+            self.e0 = _event()
             self.e0.record()
         return self
 
     def __exit__(self, *exc):
-        if _timing is not None and exc[0] is None:
-            e1 = torch.cuda.Event(enable_timing=True)
+        if self.on and exc[0] is None:
+            e1 = _event()
             e1.record()
             _timing.append((self.name, self.e0, e1))
         return False
