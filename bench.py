@@ -15,6 +15,9 @@ restatement of the reference algorithm, oracle/tile_oracle.c) on the same
 scene, forward+backward, once.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 2]
+    python bench.py --trace FILE --height H --width W [--trace-batch B] [--trace-gaussians G]
+        a recorded scene (torch.save dict of means2d/conics/colors/opacities/depths,
+        the reference's real-trace format) instead of a synthetic config
 
 Measurement helpers (used for the committed rocprofv3 summaries):
     python bench.py --calibrate-copy     a plain copy of 256 MiB (read + write),
@@ -151,7 +154,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2, help="scene config id (torch_gsplat_bridge_fast.scenes)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--trace", default="", help="recorded scene file (real-trace case)")
+    ap.add_argument("--height", type=int, default=0, help="image height for --trace")
+    ap.add_argument("--width", type=int, default=0, help="image width for --trace")
+    ap.add_argument("--trace-batch", type=int, default=0, help="keep the first B images of the trace")
+    ap.add_argument("--trace-gaussians", type=int, default=0, help="keep the first G splats per image")
     args = ap.parse_args()
+    if args.trace and (args.height <= 0 or args.width <= 0):
+        print("--trace needs --height and --width", file=sys.stderr)
+        return 2
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -164,14 +175,19 @@ def main() -> int:
 
     from torch_gsplat_bridge_fast import (RasterConfig, _ops, project_pinhole_gaussians,
                                           rasterize_pinhole_gaussians, rasterize_projected_gaussians)
-    from torch_gsplat_bridge_fast.scenes import CONFIGS, make_scene_2d, make_scene_3d
+    from torch_gsplat_bridge_fast.scenes import CONFIGS, load_trace, make_scene_2d, make_scene_3d
 
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
-    three_d = CONFIGS[args.config]["kind"] == "3d"
-    if three_d:
+    three_d = not args.trace and CONFIGS[args.config]["kind"] == "3d"
+    if args.trace:
+        sc = load_trace(args.trace, batch=args.trace_batch, gaussians=args.trace_gaussians)
+        sc.update(H=args.height, W=args.width, B=sc["means2d"].shape[0], G=sc["means2d"].shape[1])
+        leaves = [sc[k].to(dev).requires_grad_(k != "depths") for k in KEYS]
+        workload = f"real_trace:{os.path.basename(args.trace)}"
+    elif three_d:
         # Config 4: projection + rasterization, gradients to means3d/scales/quats/opacities.
         sc = make_scene_3d(seed=0)
         keys3 = ("means3d", "scales", "quats", "opacities")
@@ -182,6 +198,8 @@ def main() -> int:
     else:
         sc = make_scene_2d(args.config, seed=0)
         leaves = [sc[k].to(dev).requires_grad_(k != "depths") for k in KEYS]
+    if not args.trace:
+        workload = CONFIGS[args.config]["name"]
     H, W, B, G = sc["H"], sc["W"], sc["B"], sc["G"]
     w_cpu = torch.rand(B, H, W, 3, generator=torch.Generator().manual_seed(123))
     w = w_cpu.to(dev)
@@ -248,7 +266,7 @@ def main() -> int:
     achieved_tflops = evals * FLOP_PER_EVAL[dom] / (comp_ms[dom] * 1e-3) / 1e12
     traffic = None
     tpath = os.path.join(ROOT, "profiles", f"traffic_{dom}_cfg{args.config}.json")
-    if os.path.exists(tpath):
+    if not args.trace and os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
@@ -264,11 +282,12 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": (round(mpix / REFERENCE_MPIX_S[args.config], 2)
-                        if args.config in REFERENCE_MPIX_S else None),
+                        if args.config in REFERENCE_MPIX_S and not args.trace else None),
         "dtype": "f32",
-        "data": "synthetic (seeded BASELINE config scene, generated on CPU, resident in HBM)",
+        "data": ("recorded trace (resident in HBM)" if args.trace else
+                 "synthetic (seeded BASELINE config scene, generated on CPU, resident in HBM)"),
         "config": {
-            "workload": CONFIGS[args.config]["name"],
+            "workload": workload,
             "height": H, "width": W, "batch": B, "gaussians": G,
             "tile_pairs": n_pairs,
             "loss": "sum(image * w), w ~ U(0,1) seed 123",

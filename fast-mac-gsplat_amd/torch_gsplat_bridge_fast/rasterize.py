@@ -21,16 +21,17 @@ same):
     ``enable_overflow_fallback=False`` still raises "Tile overflow detected"
     when a tile holds more than ``max_fast_pairs`` pairs.
   * ``use_active_tiles``, ``active_policy``, ``sort_active_tiles_by_count``,
-    ``stop_count_mode``, ``stop_count_dense_threshold`` and
-    ``max_pairs_per_launch`` are validated like the reference but do not
-    change the computation: empty tiles cost one early-exiting wavefront, and
-    backward always uses exact per-pixel stop state saved by forward.
+    ``stop_count_mode`` and ``stop_count_dense_threshold`` are validated like
+    the reference but do not change the computation: empty tiles cost one
+    early-exiting wavefront, and backward always uses exact per-pixel stop
+    state saved by forward.  ``max_pairs_per_launch`` splits training batches
+    into launches of at most that many tile pairs, as the reference does.
 """
 from __future__ import annotations
 
 import os
 from dataclasses import dataclass
-from typing import Any, Dict, Tuple
+from typing import Any, Dict, List, Tuple
 
 import torch
 from torch import Tensor
@@ -257,14 +258,45 @@ def _rasterize_chunk_eval(means2d_b, conics_b, colors_b, opacities_b, depths_b, 
     return img
 
 
+@torch.no_grad()
+def _choose_batch_slices(means2d_b, conics_b, colors_b, opacities_b, depths_b, config: RasterConfig, *,
+                         train_mode: bool, tiles_per_image: int) -> List[Tuple[int, int]]:
+    """Batch slices per launch (reference _choose_batch_slices, v8 rasterize.py:339-391): contiguous
+    chunks of _choose_batch_chunk_size images; in training with batch_strategy "auto" and a positive
+    max_pairs_per_launch, each chunk is binned and split greedily so that a launch holds at most that
+    many tile pairs (a single image above the budget still gets its own launch)."""
+    B, G = means2d_b.shape[:2]
+    chunk_b = _choose_batch_chunk_size(config, B, G, tiles_per_image)
+    base = [(b0, min(B, b0 + chunk_b)) for b0 in range(0, B, chunk_b)]
+    if not train_mode or config.batch_strategy != "auto" or config.max_pairs_per_launch <= 0 or B <= 1:
+        return base
+    budget = int(config.max_pairs_per_launch)
+    out: List[Tuple[int, int]] = []
+    for b0, b1 in base:
+        st = _ops.bin_gaussians(_meta(config, b1 - b0, G),
+                                *_flat(means2d_b[b0:b1], conics_b[b0:b1], colors_b[b0:b1], opacities_b[b0:b1],
+                                       depths_b[b0:b1]))
+        per_image = st.tile_counts.view(b1 - b0, tiles_per_image).sum(dim=1).tolist()
+        cur, cur_pairs = b0, 0
+        for off, pairs in enumerate(per_image):
+            b = b0 + off
+            if b > cur and cur_pairs + int(pairs) > budget:
+                out.append((cur, b))
+                cur, cur_pairs = b, 0
+            cur_pairs += int(pairs)
+        if cur < b1:
+            out.append((cur, b1))
+    return out
+
+
 def _rasterize_batched(means2d_b, conics_b, colors_b, opacities_b, depths_b, config: RasterConfig) -> Tensor:
     B, G = means2d_b.shape[:2]
     tiles_per_image = ((config.height + 15) // 16) * ((config.width + 15) // 16)
     train_mode = _should_use_training_path(means2d_b, conics_b, colors_b, opacities_b)
-    chunk_b = _choose_batch_chunk_size(config, B, G, tiles_per_image)
+    slices = _choose_batch_slices(means2d_b, conics_b, colors_b, opacities_b, depths_b, config,
+                                  train_mode=train_mode, tiles_per_image=tiles_per_image)
     outs = []
-    for b0 in range(0, B, chunk_b):
-        b1 = min(B, b0 + chunk_b)
+    for b0, b1 in slices:
         if b0 == 0 and b1 == B:
             # one chunk: no slice views (their backward would zero-fill and copy every gradient)
             args = (means2d_b, conics_b, colors_b, opacities_b, depths_b)
@@ -300,37 +332,47 @@ def profile_projected_gaussians(means2d: Tensor, conics: Tensor, colors: Tensor,
     _runtime_validate(config)
     tiles_per_image = ((config.height + 15) // 16) * ((config.width + 15) // 16)
     chunk_b = _choose_batch_chunk_size(config, B, G, tiles_per_image)
-    slices = [(b0, min(B, b0 + chunk_b)) for b0 in range(0, B, chunk_b)]
+    slices = _choose_batch_slices(means2d_b, conics_b, colors_b, opacities_b, depths_b, config,
+                                  train_mode=True, tiles_per_image=tiles_per_image)
     counts_all, stops_all, images = [], [], []
     for b0, b1 in slices:
         args = _flat(means2d_b[b0:b1], conics_b[b0:b1], colors_b[b0:b1], opacities_b[b0:b1], depths_b[b0:b1])
         meta = _meta(config, b1 - b0, G)
         st = _ops.bin_gaussians(meta, *args)
-        counts_all.append(st.tile_counts.cpu().to(torch.float32))
+        counts_all.append(st.tile_counts)
         if run_forward or return_image:
             img, _, _, tile_stop, _ = _ops.render_forward(meta, st, save_state=True)
-            stops_all.append(tile_stop.cpu().to(torch.float32))
+            stops_all.append(tile_stop)
             if return_image:
                 images.append(img)
-    counts = torch.cat(counts_all) if counts_all else torch.zeros(0)
+    # The statistics are reduced on the device; one small vector comes back.
+    counts = torch.cat(counts_all).to(torch.float32)
+    n = counts.numel()
     occupied = counts > 0
     fast = occupied & (counts <= int(config.max_fast_pairs))
     dense = counts >= int(config.stop_count_dense_threshold)
+    if n:
+        vec = torch.stack([counts.sum(), counts.mean(), torch.quantile(counts, 0.95), counts.max(),
+                           (counts > int(config.max_fast_pairs)).sum().to(torch.float32),
+                           fast.sum().to(torch.float32), occupied.sum().to(torch.float32),
+                           (fast & dense).sum().to(torch.float32)]).tolist()
+    else:
+        vec = [0.0] * 8
     stats: Dict[str, Any] = {
         "batch_size": int(B),
         "gaussians_per_batch": int(G),
         "height": int(config.height),
         "width": int(config.width),
         "tile_size": int(config.tile_size),
-        "tiles": int(counts.numel()),
-        "total_pairs": int(counts.sum().item()) if counts.numel() else 0,
-        "mean_pairs_per_tile": float(counts.mean().item()) if counts.numel() else 0.0,
-        "p95_pairs_per_tile": float(torch.quantile(counts, 0.95).item()) if counts.numel() else 0.0,
-        "max_pairs_per_tile": int(counts.max().item()) if counts.numel() else 0,
-        "overflow_tile_count": int((counts > int(config.max_fast_pairs)).sum().item()),
-        "active_tile_count": int(fast.sum().item()),
-        "active_tile_fraction": float(occupied.sum().item() / max(counts.numel(), 1)),
-        "dense_active_tile_count": int((fast & dense).sum().item()),
+        "tiles": int(n),
+        "total_pairs": int(vec[0]),
+        "mean_pairs_per_tile": float(vec[1]),
+        "p95_pairs_per_tile": float(vec[2]),
+        "max_pairs_per_tile": int(vec[3]),
+        "overflow_tile_count": int(vec[4]),
+        "active_tile_count": int(vec[5]),
+        "active_tile_fraction": float(vec[6] / max(n, 1)),
+        "dense_active_tile_count": int(vec[7]),
         "chosen_batch_chunk": int(chunk_b),
         "chosen_batch_chunks": [int(b1 - b0) for b0, b1 in slices],
         "max_pairs_per_launch": int(config.max_pairs_per_launch),
@@ -339,15 +381,17 @@ def profile_projected_gaussians(means2d: Tensor, conics: Tensor, colors: Tensor,
         "resolved_active_chunks": [False for _ in slices],
         "stop_count_mode": config.stop_count_mode,
     }
-    if stops_all:
-        stop = torch.cat(stops_all)
+    if stops_all and n:
+        stop = torch.cat(stops_all).to(torch.float32)
         ratio = torch.where(counts > 0, stop / torch.clamp(counts, min=1.0), torch.zeros_like(stop))
+        sv = torch.stack([stop.mean(), torch.quantile(stop, 0.95), stop.max(), ratio.mean(),
+                          torch.quantile(ratio, 0.95)]).tolist()
         stats.update({
-            "mean_stop_count": float(stop.mean().item()),
-            "p95_stop_count": float(torch.quantile(stop, 0.95).item()),
-            "max_stop_count": int(stop.max().item()),
-            "mean_stop_ratio": float(ratio.mean().item()),
-            "p95_stop_ratio": float(torch.quantile(ratio, 0.95).item()),
+            "mean_stop_count": float(sv[0]),
+            "p95_stop_count": float(sv[1]),
+            "max_stop_count": int(sv[2]),
+            "mean_stop_ratio": float(sv[3]),
+            "p95_stop_ratio": float(sv[4]),
         })
     if return_image:
         out = torch.cat(images, dim=0) if len(images) > 1 else images[0]

@@ -111,3 +111,30 @@ def make_scene_3d(seed: int = 0, device="cpu", *, G: int | None = None, H: int =
            dict(means3d=means3d, scales=scales, quats=quats, opacities=opac, colors=colors).items()}
     out.update(fx=3500.0, fy=3500.0, cx=W / 2.0, cy=H / 2.0, camera_to_world=c2w.to(device), H=H, W=W, B=1, G=G)
     return out
+
+
+TRACE_KEYS = ("means2d", "conics", "colors", "opacities", "depths")
+
+
+def load_trace(path: str, device="cpu", *, batch: int = 0, gaussians: int = 0) -> Dict[str, torch.Tensor]:
+    """Loads a recorded scene: a ``torch.save`` dict with means2d, conics, colors, opacities and depths,
+    shaped [G,...] or [B,G,...] (the format of the reference's real-trace benchmark case,
+    variants/v8/benchmarks/benchmark_mps.py:26-47).  The tensors are converted to float32 on
+    ``device``; [G,...] inputs become B=1; ``batch`` / ``gaussians`` > 0 keep only the first that many
+    images / splats.  The file is read with ``weights_only=True``: nothing in it is executed."""
+    if not path:
+        raise ValueError("a trace file is required for the real-trace case")
+    data = torch.load(path, map_location="cpu", weights_only=True)
+    if not isinstance(data, dict):
+        raise ValueError("trace file must hold a dict of tensors")
+    out = {}
+    for key in TRACE_KEYS:
+        if key not in data:
+            raise ValueError(f"trace file is missing {key!r}")
+        out[key] = torch.as_tensor(data[key]).to(dtype=torch.float32)
+    if out["means2d"].ndim == 2:
+        out = {k: v.unsqueeze(0) for k, v in out.items()}
+    B0, G0 = out["means2d"].shape[:2]
+    B = min(B0, batch) if batch > 0 else B0
+    G = min(G0, gaussians) if gaussians > 0 else G0
+    return {k: v[:B, :G].contiguous().to(device) for k, v in out.items()}

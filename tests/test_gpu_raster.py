@@ -286,3 +286,52 @@ def test_heavy_tiles_segmented_backward(gpu):
     for name, a, b, c in zip(KEYS[:4], seg, one, seg2):
         _grad_close(a.cpu().numpy(), b.cpu().numpy(), name, rtol=1e-4)
         _grad_close(c.cpu().numpy(), a.cpu().numpy(), name, rtol=1e-5)
+
+
+def test_pair_budget_splits_training_launches(gpu):
+    """max_pairs_per_launch (reference _choose_batch_slices, v8 rasterize.py:339-391):
+    a budget below two images' pairs gives one launch per image; image and
+    gradients equal the single-launch result."""
+    from torch_gsplat_bridge_fast import profile_projected_gaussians
+
+    sc0 = make_scene_2d(1, seed=7, G=3000, B=3, H=96, W=128)
+    w = torch.rand(3, 96, 128, 3, generator=torch.Generator().manual_seed(3))
+    base = RasterConfig(height=96, width=128)
+    with torch.no_grad():
+        prof = profile_projected_gaussians(*[sc0[k].to(gpu) for k in KEYS], base)
+    per_image = prof["total_pairs"] / 3
+    split = RasterConfig(height=96, width=128, max_pairs_per_launch=int(per_image * 1.2))
+    img1, g1 = _run_gpu({k: sc0[k] for k in KEYS}, base, w)
+    img2, g2 = _run_gpu({k: sc0[k] for k in KEYS}, split, w)
+    assert torch.equal(img1, img2)
+    for name, a, b in zip(KEYS[:4], g1, g2):
+        _grad_close(a.numpy(), b.numpy(), name, rtol=1e-5)
+    with torch.no_grad():
+        prof2 = profile_projected_gaussians(*[sc0[k].to(gpu) for k in KEYS], split)
+    assert prof["chosen_batch_chunks"] == [3]
+    assert prof2["chosen_batch_chunks"] == [1, 1, 1]
+
+
+def test_profile_statistics_match_host_computation(gpu):
+    """profile_projected_gaussians reduces its statistics on the device; they
+    equal the same statistics computed on the host from the tile lists."""
+    from torch_gsplat_bridge_fast import _lib, _ops, profile_projected_gaussians
+
+    sc = make_scene_2d(3, seed=1, G=4000, B=2, H=128, W=192)
+    cfg = RasterConfig(height=128, width=192, max_fast_pairs=300)
+    with torch.no_grad():
+        st_ = profile_projected_gaussians(*[sc[k].to(gpu) for k in KEYS], cfg, run_forward=True)
+    meta = _lib.make_raster_meta(128, 192, 2, 4000, 1.0 / 255.0, 1e-4, (0, 0, 0))
+    st = _ops.bin_gaussians(meta, *[sc[k].reshape(8000, -1).squeeze(-1).contiguous().to(gpu) for k in KEYS])
+    _, _, _, stop, _ = _ops.render_forward(meta, st, save_state=True)
+    c = st.tile_counts.cpu().double().numpy()
+    s = stop.cpu().double().numpy()
+    assert st_["tiles"] == c.size and st_["total_pairs"] == int(c.sum())
+    assert st_["max_pairs_per_tile"] == int(c.max()) and st_["max_stop_count"] == int(s.max())
+    assert st_["overflow_tile_count"] == int((c > 300).sum())
+    assert st_["active_tile_count"] == int(((c > 0) & (c <= 300)).sum())
+    np.testing.assert_allclose(st_["mean_pairs_per_tile"], c.mean(), rtol=1e-5)
+    np.testing.assert_allclose(st_["p95_pairs_per_tile"], np.quantile(c, 0.95), rtol=1e-5)
+    np.testing.assert_allclose(st_["mean_stop_count"], s.mean(), rtol=1e-5)
+    ratio = np.where(c > 0, s / np.maximum(c, 1), 0)
+    np.testing.assert_allclose(st_["p95_stop_ratio"], np.quantile(ratio, 0.95), rtol=1e-5)
