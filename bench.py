@@ -45,6 +45,39 @@ for _p in (ROOT, os.path.join(ROOT, "fast-mac-gsplat_amd")):
 KEYS = ("means2d", "conics", "colors", "opacities", "depths")
 PEAK_FP32_TFLOPS = 157.3   # MI355X published fp32 peak
 PEAK_HBM_GBS = 8000.0      # MI355X published HBM3E bandwidth
+
+
+def stage_roofline(op_ms, BG, N, walked, T, P, three_d, depth_passes=4, pair_passes=2):
+    """Achieved fraction of each stage against its bound, from the per-unit
+    algorithmic work of the survey's measurement table: bytes for the
+    binning and projection stages (HBM), FLOP for the compositors (VALU)
+    over the `walked` pairs (each tile's list up to its stop).  A stage's
+    time is the mean of its C-ABI call over the breakdown pass."""
+    work = {
+        "project_forward": ("hbm", 72.0 * BG),
+        "project_backward": ("hbm", 116.0 * BG),
+        "bin_count": ("hbm", 28.0 * BG),
+        # depth sort (24 B per splat and pass) + packing (48 B records + 36 B gathered)
+        "bin_pack": ("hbm", 24.0 * BG * depth_passes + 84.0 * BG),
+        # emit (24 B/splat + 12 B/pair), pair sort (24 B/pair/pass), ranges (8 B/pair + 8 B/tile)
+        "bin_emit": ("hbm", 24.0 * BG + 12.0 * N + 24.0 * N * pair_passes + 8.0 * N + 8.0 * T),
+        "render_forward": ("valu", 256.0 * walked * FLOP_PER_EVAL["render_forward"]),
+        "render_backward": ("valu", 256.0 * walked * FLOP_PER_EVAL["render_backward"]),
+    }
+    out = {}
+    for k, ms in op_ms.items():
+        if k not in work or ms <= 0:
+            continue
+        bound, units = work[k]
+        if bound == "hbm":
+            a = units / (ms * 1e-3) / 1e9
+            out[k] = {"bound": "hbm", "achieved": round(a, 1), "unit": "GB/s", "frac": round(a / PEAK_HBM_GBS, 4)}
+        else:
+            a = units / (ms * 1e-3) / 1e12
+            out[k] = {"bound": "valu", "achieved": round(a, 2), "unit": "TFLOP/s",
+                      "frac": round(a / PEAK_FP32_TFLOPS, 4)}
+    return out
+PEAK_HBM_GBS = 8000.0      # MI355X published HBM3E bandwidth
 # The reference's best published cfg2 forward+backward: 65.754 ms on an Apple
 # M4 (v8_direct; benchmarks/full_rasterizer_benchmark_v8_prior_compare_4k64k.md:34)
 # = 4096*4096 / 65.754 ms = 255.15 Mpix/s.
@@ -175,6 +208,7 @@ def main() -> int:
 
     from torch_gsplat_bridge_fast import (RasterConfig, _ops, project_pinhole_gaussians,
                                           rasterize_pinhole_gaussians, rasterize_projected_gaussians)
+    from torch_gsplat_bridge_fast.rasterize import _meta as raster_meta
     from torch_gsplat_bridge_fast.scenes import CONFIGS, load_trace, make_scene_2d, make_scene_3d
 
     if not torch.cuda.is_available():
@@ -258,11 +292,14 @@ def main() -> int:
             flat = (m2, cq, colors3, op, dp)
         else:
             flat = leaves
-        st = _ops.bin_gaussians(
-            __import__("torch_gsplat_bridge_fast.rasterize", fromlist=["_meta"])._meta(cfg, B, G),
-            *(t.detach().reshape(B * G, -1).squeeze(-1).contiguous() for t in flat))
+        meta = raster_meta(cfg, B, G)
+        st = _ops.bin_gaussians(meta, *(t.detach().reshape(B * G, -1).squeeze(-1).contiguous() for t in flat))
+        # pairs up to each tile's stop: the pairs a compositor must evaluate
+        # (equal to N unless pixels saturate before a tile's list ends)
+        walked = int(_ops.render_forward(meta, st, save_state=True)[3].sum().item())
     n_pairs = st.n_pairs
-    evals = 256.0 * n_pairs
+    n_tiles = B * ((H + 15) // 16) * ((W + 15) // 16)
+    evals = 256.0 * walked
     achieved_tflops = evals * FLOP_PER_EVAL[dom] / (comp_ms[dom] * 1e-3) / 1e12
     traffic = None
     tpath = os.path.join(ROOT, "profiles", f"traffic_{dom}_cfg{args.config}.json")
@@ -290,10 +327,13 @@ def main() -> int:
             "workload": workload,
             "height": H, "width": W, "batch": B, "gaussians": G,
             "tile_pairs": n_pairs,
+            "walked_pairs": walked,
             "loss": "sum(image * w), w ~ U(0,1) seed 123",
             "parallelism": "single GPU",
         },
         "stage_ms": {k: round(v, 4) for k, v in op_ms.items()},
+        "stage_roofline": stage_roofline(op_ms, B * G, n_pairs, walked, n_tiles, B * H * W, three_d,
+                                         pair_passes=(max(n_tiles - 1, 0).bit_length() + 7) // 8),
         "roofline": {
             "kernel": f"{dom} ({'render_bwd_kernel' if dom == 'render_backward' else 'render_fwd_kernel'})",
             "launch_us": round(comp_ms[dom] * 1e3, 2),
@@ -303,7 +343,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved_tflops / PEAK_FP32_TFLOPS, 4),
             "traffic": traffic,
-            "work": f"256 * tile_pairs evaluations x {FLOP_PER_EVAL[dom]:.0f} FLOP per launch",
+            "work": f"256 * walked_pairs evaluations x {FLOP_PER_EVAL[dom]:.0f} FLOP per launch",
         },
     }
     if not args.no_cpu_baseline and not three_d:
