@@ -117,11 +117,13 @@ int null_check(std::initializer_list<const void*> ptrs, const char* what) {
   return GSPLAT_OK;
 }
 
-// Binning workspace shared by bin_count, bin_pack and bin_emit: a control
-// region zeroed by bin_count (depth-sort control block, pack-scan look-back
-// status and ticket, pair-sort histograms and tickets), then the per-splat
-// tile-hit counts (original order), the count workgroups' sums and the depth
-// sort's ping-pong buffers.
+// Binning workspace shared by bin_count, bin_depth_order, bin_pack and
+// bin_emit: a control region (the depth sort's control block, zeroed by
+// bin_depth_order; then the pack-scan look-back status and ticket and the
+// pair sort's histograms and tickets, zeroed by bin_count), then the
+// per-splat tile-hit counts (original order), the count workgroups' sums and
+// the depth sort's ping-pong buffers.  bin_count and bin_depth_order touch
+// disjoint parts, so they may run concurrently on two streams.
 struct CountLayout {
   gs::RadixPlan depth;
   size_t scan_status, scan_ticket, pair_ghist, pair_tickets, ctl_end;
@@ -216,23 +218,57 @@ int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* base = static_cast<char*>(workspace);
   // Per-splat tile-hit counts and their total N; the same launch zeroes the
-  // control region.
+  // control words of the pack scan and the pair sort.
+  const size_t z0 = gs::radix_ctl_bytes(L.depth);
   return gs::launch_count(P, means2d, conics, opacities,
                           reinterpret_cast<int32_t*>(base + L.splat_count),
                           reinterpret_cast<int32_t*>(base + L.block_sums),
-                          pair_count, reinterpret_cast<uint32_t*>(base),
-                          (int64_t)(L.ctl_end / sizeof(uint32_t)), s);
+                          pair_count, reinterpret_cast<uint32_t*>(base + z0),
+                          (int64_t)((L.ctl_end - z0) / sizeof(uint32_t)), s);
+}
+
+int gsplat_hip_bin_depth_order(const gsplat_raster_meta* meta,
+                               const float* depths, int32_t* perm,
+                               void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  RasterParams P;
+  int rc = make_params(meta, P);
+  if (rc) return rc;
+  rc = null_check({depths, perm, workspace}, "gsplat_hip_bin_depth_order");
+  if (rc) return rc;
+  const CountLayout L = count_layout(P);
+  if (workspace_bytes < L.total) {
+    gs::set_error("gsplat_hip_bin_depth_order: workspace too small (%zu < %zu)",
+                  workspace_bytes, L.total);
+    return GSPLAT_ERR_WORKSPACE;
+  }
+  if (!gs::radix_size_ok(P.gpb, P.batch)) {
+    gs::set_error("gsplat_hip_bin_depth_order: too many splats per image");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* base = static_cast<char*>(workspace);
+  const gs::RadixCtl depth_ctl = gs::radix_ctl_at(L.depth, base);
+  // stable depth order per image (onesweep LSD over the 32 key bits)
+  rc = gs::launch_zero_u32(reinterpret_cast<uint32_t*>(base),
+                           (int64_t)(gs::radix_ctl_bytes(L.depth) / sizeof(uint32_t)), s);
+  if (!rc) rc = gs::radix_global_hist(L.depth, depth_ctl, nullptr, depths, s);
+  if (!rc)
+    rc = gs::radix_passes(L.depth, depth_ctl, base + L.depth_buffers, nullptr,
+                          nullptr, depths, nullptr,
+                          reinterpret_cast<uint32_t*>(perm), s);
+  return rc;
 }
 
 int gsplat_hip_bin_pack(const gsplat_raster_meta* meta, const float* means2d,
                         const float* conics, const float* colors,
-                        const float* opacities, const float* depths,
-                        int32_t* perm, float* packed, int32_t* splat_offsets,
+                        const float* opacities, const int32_t* perm,
+                        float* packed, int32_t* splat_offsets,
                         void* workspace, size_t workspace_bytes, void* stream) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
-  rc = null_check({means2d, conics, colors, opacities, depths, perm, packed,
+  rc = null_check({means2d, conics, colors, opacities, perm, packed,
                    splat_offsets, workspace},
                   "gsplat_hip_bin_pack");
   if (rc) return rc;
@@ -244,16 +280,8 @@ int gsplat_hip_bin_pack(const gsplat_raster_meta* meta, const float* means2d,
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* base = static_cast<char*>(workspace);
-  const gs::RadixCtl depth_ctl = gs::radix_ctl_at(L.depth, base);
-  // 1. stable depth order per image (onesweep LSD over the 32 key bits)
-  rc = gs::radix_global_hist(L.depth, depth_ctl, nullptr, depths, s);
-  if (!rc)
-    rc = gs::radix_passes(L.depth, depth_ctl, base + L.depth_buffers, nullptr,
-                          nullptr, depths, nullptr,
-                          reinterpret_cast<uint32_t*>(perm), s);
-  // 2. packed records and per-gid pair offsets
-  if (!rc)
-    rc = gs::launch_pack(P, means2d, conics, colors, opacities,
+  // packed records in depth order and per-gid pair offsets
+  rc = gs::launch_pack(P, means2d, conics, colors, opacities,
                          reinterpret_cast<const uint32_t*>(perm),
                          reinterpret_cast<const int32_t*>(base + L.splat_count),
                          packed, splat_offsets,

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("GSPLAT_HIP_LIB", os.path.join(_HERE, "lib", "libgsplat_hip.so"))
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 TILE_SIZE = 16
 RECORD_FLOATS = 12
 
@@ -63,7 +63,8 @@ SIGNATURES = {
     "gsplat_hip_last_error": (ctypes.c_char_p, []),
     "gsplat_hip_bin_count_workspace_bytes": (_sz, [_PM]),
     "gsplat_hip_bin_count": (ctypes.c_int, [_PM] + [_vp] * 4 + [_vp, _sz, _vp]),
-    "gsplat_hip_bin_pack": (ctypes.c_int, [_PM] + [_vp] * 8 + [_vp, _sz, _vp]),
+    "gsplat_hip_bin_depth_order": (ctypes.c_int, [_PM, _vp, _vp, _vp, _sz, _vp]),
+    "gsplat_hip_bin_pack": (ctypes.c_int, [_PM] + [_vp] * 7 + [_vp, _sz, _vp]),
     "gsplat_hip_bin_emit_workspace_bytes": (_sz, [_PM, _i64]),
     "gsplat_hip_bin_emit": (ctypes.c_int, [_PM, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _vp]),
     "gsplat_hip_render_workspace_bytes": (_sz, [_PM, _i64]),

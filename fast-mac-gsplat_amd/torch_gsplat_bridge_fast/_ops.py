@@ -95,16 +95,31 @@ def _empty(n, dtype, device):
     return torch.empty((n,), dtype=dtype, device=device)
 
 
+_side_streams: dict = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for the per-splat count,
+    which runs concurrently with the depth sort."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    st = _side_streams.get(key)
+    if st is None:
+        st = torch.cuda.Stream(device=device)
+        _side_streams[key] = st
+    return st
+
+
 def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
                   opacities: Tensor, depths: Tensor) -> BinState:
     """Tile binning + stable depth order + record packing + pair sort + tile ranges.
 
     Inputs are flat contiguous fp32 [BG,2], [BG,3], [BG,3], [BG], [BG] in the
-    original splat order.  The pair count N (needed on the host to size the
-    pair buffers, like the reference's tile_offsets[-1] read,
-    variants/v8/csrc/metal/gsplat_metal.mm:188) is copied to pinned memory
-    as soon as the per-splat counts exist and read after the depth sort has
-    been enqueued, so the wait overlaps GPU work."""
+    original splat order.  The per-splat tile-hit count runs on a side stream
+    while the depth sort runs on the caller's stream; packing waits for both.
+    The pair count N (needed on the host to size the pair buffers, like the
+    reference's tile_offsets[-1] read, variants/v8/csrc/metal/gsplat_metal.mm:188)
+    is copied to pinned memory right after the count and read after packing
+    has been enqueued, so the wait overlaps GPU work."""
     L = _lib.lib()
     dev = means2d.device
     B, G = meta.batch, meta.gaussians_per_batch
@@ -117,17 +132,26 @@ def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors
     pair_count = _empty(1, torch.int32, dev)
     ws_bytes = L.gsplat_hip_bin_count_workspace_bytes(meta)
     ws = _empty(max(ws_bytes, 1), torch.uint8, dev)
-    s = stream_of(means2d)
-    with _timed("bin_count"):
-        check(L.gsplat_hip_bin_count(meta, ptr(means2d), ptr(conics), ptr(opacities), ptr(pair_count),
-                                     ptr(ws), ws_bytes, s), "gsplat_hip_bin_count")
     n_host = torch.empty((1,), dtype=torch.int32, pin_memory=True)
-    n_host.copy_(pair_count, non_blocking=True)
+    main = torch.cuda.current_stream(dev)
+    side = _side_stream(dev)
+    inputs_ready = torch.cuda.Event()
+    inputs_ready.record(main)
+    side.wait_event(inputs_ready)
     n_ready = torch.cuda.Event()
-    n_ready.record()
+    with torch.cuda.stream(side):
+        with _timed("bin_count"):
+            check(L.gsplat_hip_bin_count(meta, ptr(means2d), ptr(conics), ptr(opacities), ptr(pair_count),
+                                         ptr(ws), ws_bytes, side.cuda_stream), "gsplat_hip_bin_count")
+        n_host.copy_(pair_count, non_blocking=True)
+        n_ready.record(side)
+    s = main.cuda_stream
     with _timed("bin_pack"):
-        check(L.gsplat_hip_bin_pack(meta, ptr(means2d), ptr(conics), ptr(colors), ptr(opacities), ptr(depths),
-                                    ptr(perm), ptr(packed), ptr(splat_offsets), ptr(ws), ws_bytes, s),
+        check(L.gsplat_hip_bin_depth_order(meta, ptr(depths), ptr(perm), ptr(ws), ws_bytes, s),
+              "gsplat_hip_bin_depth_order")
+        main.wait_event(n_ready)
+        check(L.gsplat_hip_bin_pack(meta, ptr(means2d), ptr(conics), ptr(colors), ptr(opacities), ptr(perm),
+                                    ptr(packed), ptr(splat_offsets), ptr(ws), ws_bytes, s),
               "gsplat_hip_bin_pack")
     n_ready.synchronize()
     n = int(n_host[0])

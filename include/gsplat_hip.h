@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 4
+#define GSPLAT_HIP_ABI_VERSION 5
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -83,44 +83,55 @@ const char* gsplat_hip_last_error(void);
  * stable depth argsort + gathers of variants/v8/torch_gsplat_bridge_v8/
  * rasterize.py:465-475 and the per-tile sort (gsplat_v8_kernels.metal:
  * 141-164).  The reference sizes binned_ids with a host read of
- * tile_offsets[-1] (gsplat_metal.mm:188).  Here binning is three calls on one
- * stream sharing one workspace:
- *   gsplat_hip_bin_count  per-splat tile-hit counts; writes the pair count N;
- *   gsplat_hip_bin_pack   stable depth order, packed records, per-splat pair
- *                         offsets;
- *   gsplat_hip_bin_emit   pair emission, the stable sort by tile, and the
- *                         tile ranges/counts extracted from the sorted keys.
- * A caller that needs N on the host (to size binned_ids) can copy it
- * asynchronously after bin_count and wait for it after enqueuing bin_pack,
- * so the read overlaps the depth sort. */
+ * tile_offsets[-1] (gsplat_metal.mm:188).  Here binning is four calls sharing
+ * one workspace:
+ *   gsplat_hip_bin_count        per-splat tile-hit counts; writes the pair
+ *                               count N;
+ *   gsplat_hip_bin_depth_order  stable depth order per image;
+ *   gsplat_hip_bin_pack         packed records in depth order, per-splat pair
+ *                               offsets (after both calls above);
+ *   gsplat_hip_bin_emit         pair emission, the stable sort by tile, and
+ *                               the tile ranges/counts from the sorted keys.
+ * bin_count and bin_depth_order use disjoint parts of the workspace and may
+ * run concurrently on two streams; the caller orders bin_pack after both
+ * (e.g. with an event) and bin_emit after bin_pack.  A caller that needs N on
+ * the host (to size binned_ids) copies it asynchronously after bin_count and
+ * waits for it after enqueuing bin_pack, so the read overlaps GPU work. */
 
-/* Bytes of the binning workspace used by bin_count, bin_pack and bin_emit. */
+/* Bytes of the binning workspace used by all four binning calls. */
 size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta);
 
 /* Inputs (original order): means2d [BG,2], conics [BG,3], opacities [BG].
  * Output: *pair_count (one int32 in device memory) = N, the number of
  * (tile, splat) pairs, or -1 if N does not fit in int32.  The workspace keeps
  * the per-splat tile-hit counts and the zeroed control state that bin_pack
- * and bin_emit consume: pass the same workspace to them, unmodified, on the
- * same stream. */
+ * and bin_emit consume: pass the same workspace to them, unmodified. */
 int gsplat_hip_bin_count(const gsplat_raster_meta* meta,
                          const float* means2d, const float* conics,
                          const float* opacities, int32_t* pair_count,
                          void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* Stable depth order per image (replaces torch.argsort(depths, stable=True),
+ * v8 rasterize.py:466): perm int32 [BG], perm[b*G+r] = original index
+ * (within image b) of the splat of depth rank r; -0.0 sorts as +0.0, NaNs
+ * last.  Input depths [BG] in the original order. */
+int gsplat_hip_bin_depth_order(const gsplat_raster_meta* meta,
+                               const float* depths, int32_t* perm,
+                               void* workspace, size_t workspace_bytes,
+                               void* stream);
+
 /* Inputs (original order): means2d [BG,2], conics [BG,3], colors [BG,3],
- * opacities [BG], depths [BG], and the workspace of bin_count.  Outputs:
- *   perm          int32 [BG]   perm[b*G+r] = original index (within image b)
- *                              of the splat of depth rank r
- *   packed        float [BG*12] packed records in gid order
+ * opacities [BG]; perm from bin_depth_order; the workspace after bin_count.
+ * Outputs (gathers of v8 rasterize.py:467-475):
+ *   packed        float [BG*12] packed records in gid (depth rank) order
  *   splat_offsets int32 [BG+1] exclusive scan of per-gid tile-hit counts */
 int gsplat_hip_bin_pack(const gsplat_raster_meta* meta,
                         const float* means2d, const float* conics,
                         const float* colors, const float* opacities,
-                        const float* depths,
-                        int32_t* perm, float* packed, int32_t* splat_offsets,
-                        void* workspace, size_t workspace_bytes, void* stream);
+                        const int32_t* perm, float* packed,
+                        int32_t* splat_offsets, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
                                            int64_t n_pairs);

@@ -30,7 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 4
+    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 5
 
 
 def _meta(**kw):
@@ -88,8 +88,10 @@ def test_workspace_too_small_rejected():
     rc = L.gsplat_hip_bin_count(_meta(), *([one] * 4), one, 1, None)
     assert rc == 3
     assert "workspace" in L.gsplat_hip_last_error().decode()
-    rc = L.gsplat_hip_bin_pack(_meta(), *([one] * 8), one, 1, None)
+    rc = L.gsplat_hip_bin_pack(_meta(), *([one] * 7), one, 1, None)
     assert rc == 3 and "bin_pack" in L.gsplat_hip_last_error().decode()
+    rc = L.gsplat_hip_bin_depth_order(_meta(), one, one, one, 1, None)
+    assert rc == 3 and "bin_depth_order" in L.gsplat_hip_last_error().decode()
     rc = L.gsplat_hip_bin_emit(_meta(), one, one, 10, one, one, one, one, 1, one, 1, None)
     assert rc == 3
     pm = _lib.make_project_meta(2, 1000, 1e-4)
