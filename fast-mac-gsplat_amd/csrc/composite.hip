@@ -265,10 +265,9 @@ __device__ __forceinline__ int64_t pixel_index(const RasterParams& P,
   return ((int64_t)tc.batch * P.height + y) * P.width + x;
 }
 
-__device__ __forceinline__ float* pixel_out(const RasterParams& P,
-                                           const TileCoord& tc,
-                                           float* out_rgb) {
-  return out_rgb + 3 * pixel_index(P, tc);
+// Segment record of this thread's pixel in its first strip (null if none).
+__device__ __forceinline__ float4* record_at(const HeavyState& H, int slot) {
+  return slot >= 0 ? H.rec + (int64_t)slot * 256 + opaque_tid() : nullptr;
 }
 
 // End of segment `seg` for NP strips per thread: record it in `slot`
@@ -281,11 +280,11 @@ __device__ __forceinline__ void end_segment(const RasterParams& P,
                                             int seg, const bool* valid,
                                             float* cr, float* cg, float* cb,
                                             const float* T) {
-  float* o0 = pixel_out(P, tc, out_rgb);
-  float4* r0 = H.rec + (int64_t)slot * 256 + opaque_tid();
+  float* o0 = out_rgb + 3 * pixel_index(P, tc);
+  float4* r0 = record_at(H, slot);
 #pragma unroll
   for (int k = 0; k < NP; ++k) {
-    if (slot >= 0) r0[64 * k] = make_float4(cr[k], cg[k], cb[k], T[k]);
+    if (r0 != nullptr) r0[64 * k] = make_float4(cr[k], cg[k], cb[k], T[k]);
     if (valid[k]) {
       float* o = o0 + (int64_t)12 * k * P.width;
       if (seg > 0) {
@@ -312,11 +311,11 @@ __device__ __forceinline__ void last_segment(const RasterParams& P,
                                              const bool* valid, float* cr,
                                              float* cg, float* cb,
                                              const float* T) {
-  const float* o0 = pixel_out(P, tc, const_cast<float*>(out_rgb));
-  float4* r0 = H.rec + (int64_t)slot * 256 + opaque_tid();
+  const float* o0 = out_rgb + 3 * pixel_index(P, tc);
+  float4* r0 = record_at(H, slot);
 #pragma unroll
   for (int k = 0; k < NP; ++k) {
-    if (slot >= 0) r0[64 * k] = make_float4(cr[k], cg[k], cb[k], T[k]);
+    if (r0 != nullptr) r0[64 * k] = make_float4(cr[k], cg[k], cb[k], T[k]);
     if (valid[k]) {
       const float* o = o0 + (int64_t)12 * k * P.width;
       cr[k] += o[0];
@@ -334,17 +333,21 @@ __device__ __forceinline__ void composite_one(float Adxdx, float Bdx,
                                               float max_alpha, int idx1,
                                               float& T, float& cr, float& cg,
                                               float& cb, int& last) {
-  if (T > t_thr) {
-    const float p = splat_exponent(Adxdx, Bdx, a1.x, py - my);
-    if (p <= 0.0f && p >= a2.z) {
-      const float alpha = fminf(max_alpha, a1.y * __builtin_amdgcn_exp2f(p));
-      const float w = T * alpha;
-      cr += w * a1.z;
-      cg += w * a1.w;
-      cb += w * a2.x;
-      T *= (1.0f - alpha);
-      last = idx1;
-    }
+  // One combined test (alive and visible): pixels rarely die inside a
+  // batch, so guarding the exponent by T would save little and cost a
+  // second branch.
+  const float p = splat_exponent(Adxdx, Bdx, a1.x, py - my);
+  if ((T > t_thr) & (p <= 0.0f) & (p >= a2.z)) {
+    // min(max_alpha, o 2^p) as one med3: o 2^p >= 0 here (plim is +inf for
+    // o <= 0), so the lower bound 0 never changes the result.
+    const float alpha = __builtin_amdgcn_fmed3f(
+        a1.y * __builtin_amdgcn_exp2f(p), 0.0f, max_alpha);
+    const float w = T * alpha;
+    cr += w * a1.z;
+    cg += w * a1.w;
+    cb += w * a2.x;
+    T *= (1.0f - alpha);
+    last = idx1;
   }
 }
 
@@ -713,10 +716,11 @@ __device__ __forceinline__ void bwd_walk(
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
         if (!((mask >> k) & 1u)) continue;  // scalar branch
-        if (i < Q.lk[k]) {
-          const float dy = Q.py[k] - a0.y;
-          const float p = splat_exponent(Adxdx, Bdx, a1.x, dy);
-          if (p <= 0.0f && p >= a2.z) {
+        // one combined test: composited in the forward (i < last) and visible
+        const float dy = Q.py[k] - a0.y;
+        const float p = splat_exponent(Adxdx, Bdx, a1.x, dy);
+        {
+          if ((i < Q.lk[k]) & (p <= 0.0f) & (p >= a2.z)) {
             contrib = true;
             const float e = __builtin_amdgcn_exp2f(p);
             const float raw = a1.y * e;
