@@ -91,18 +91,19 @@ struct Staged {
   float4 s2[kBatch];  // blue, orig index bits, plim, strip mask bits
 };
 
-__device__ __forceinline__ float conic_q(float a, float b, float c, float dx,
-                                         float dy) {
-  return a * dx * dx + 2.0f * b * dx * dy + c * dy * dy;
-}
-
 // Bit k set unless strip k of the tile at (x0, y0) certainly holds no pixel
-// with p >= plim.  Exact minimum of the conic quadratic q over each strip's
-// pixel-centre rectangle (the centre if inside, else the minima along the
-// four edges), compared with the support radius tau = -2 ln(thr/o) =
-// -2 ln(2) plim enlarged by 2% + 1e-3, which covers the rounding of p's chain
-// and of this test as long as det > 1e-3 a c (|b| < (1 - 5e-4) sqrt(ac)).
-// Conics outside that range are never culled.
+// with p >= plim.  The support ellipse q(dx, dy) = a dx^2 + 2b dx dy + c dy^2
+// <= tc (tau = -2 ln(thr/o) = -2 ln(2) plim, enlarged to tc = 1.02 tau +
+// 1e-3) cut by the tile's slab of pixel-centre columns dx in [dxa, dxb] is
+// convex, so its rows form one interval [dy_lo, dy_hi]: a strip is kept iff
+// its pixel-centre rows meet it.  On column dx the ellipse spans
+//   dy = (-b dx +- sqrt(c tc - det dx^2)) / c,
+// whose upper end is concave in dx with its maximum at the top point
+// dx_t = -b hy / a (hy = sqrt(a tc / det)) and whose lower end is convex with
+// its minimum at -dx_t; clamping those points into the slab gives dy_hi and
+// dy_lo.  The margin of tc covers the rounding of p's chain and of these
+// hardware sqrt / rcp (about 1 ulp) as long as det > 1e-3 a c
+// (|b| < (1 - 5e-4) sqrt(ac)); other conics are never culled.
 __device__ __forceinline__ uint32_t strip_mask(float mx, float my, float a,
                                                float b, float c, float plim,
                                                int x0, int y0) {
@@ -112,19 +113,22 @@ __device__ __forceinline__ uint32_t strip_mask(float mx, float my, float a,
   if (!(a > 0.0f && c > 0.0f && det > 1e-3f * (a * c) && tau < 3.0e38f))
     return 0xFu;
   const float tc = tau * 1.02f + 1e-3f;
-  const float dx0 = ((float)x0 + 0.5f) - mx, dx1 = dx0 + 15.0f;
-  const float kc = -b / c, ka = -b / a;
-  const float ex0 = kc * dx0, ex1 = kc * dx1;  // dy minimising q on x = dx0/dx1
+  const float inv_c = __builtin_amdgcn_rcpf(c);
+  const float hy = __builtin_amdgcn_sqrtf(a * tc * __builtin_amdgcn_rcpf(det));
+  const float dx_t = -b * hy * __builtin_amdgcn_rcpf(a);
+  const float dxa = ((float)x0 + 0.5f) - mx, dxb = dxa + 15.0f;
+  const float ct = c * tc;
+  const float ut = fminf(fmaxf(dx_t, dxa), dxb);
+  const float ub = fminf(fmaxf(-dx_t, dxa), dxb);
+  const float y_hi =
+      my + (-b * ut + __builtin_amdgcn_sqrtf(fmaxf(ct - det * ut * ut, 0.0f))) * inv_c;
+  const float y_lo =
+      my + (-b * ub - __builtin_amdgcn_sqrtf(fmaxf(ct - det * ub * ub, 0.0f))) * inv_c;
   uint32_t m = 0u;
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
-    const float dy0 = ((float)(y0 + 4 * k) + 0.5f) - my, dy1 = dy0 + 3.0f;
-    const bool inside = dx0 <= 0.0f && dx1 >= 0.0f && dy0 <= 0.0f && dy1 >= 0.0f;
-    float q = conic_q(a, b, c, dx0, fminf(fmaxf(ex0, dy0), dy1));
-    q = fminf(q, conic_q(a, b, c, dx1, fminf(fmaxf(ex1, dy0), dy1)));
-    q = fminf(q, conic_q(a, b, c, fminf(fmaxf(ka * dy0, dx0), dx1), dy0));
-    q = fminf(q, conic_q(a, b, c, fminf(fmaxf(ka * dy1, dx0), dx1), dy1));
-    if (inside || q <= tc) m |= 1u << k;
+    const float r0 = (float)(y0 + 4 * k) + 0.5f;  // first and last row centre
+    if (y_lo <= r0 + 3.0f && y_hi >= r0) m |= 1u << k;
   }
   return m;
 }
