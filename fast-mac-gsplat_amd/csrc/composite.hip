@@ -88,7 +88,7 @@ __device__ __forceinline__ int slot_y(const TileCoord& c, int k) {
 struct Staged {
   float4 s0[kBatch];  // mx, my, A, B
   float4 s1[kBatch];  // C, opacity, r, g
-  float4 s2[kBatch];  // blue, orig index bits, plim, strip mask bits
+  float4 s2[kBatch];  // blue, orig index bits, plim, strip mask bits or 1/o
 };
 
 // Bit k set unless strip k of the tile at (x0, y0) certainly holds no pixel
@@ -135,18 +135,23 @@ __device__ __forceinline__ uint32_t strip_mask(float mx, float my, float a,
 
 // Stages records [first, first+n) of the tile range into LDS with the
 // base-2 exponent coefficients and the tile's strip mask.
-__device__ __forceinline__ void stage_batch(const float4* __restrict__ packed,
-                                            const int32_t* __restrict__ binned,
-                                            int first, int n,
-                                            const TileCoord& tc, Staged& S) {
+// Returns this lane's strip mask (0 for lanes past n).  With kMaskInLds the
+// mask also goes to s2.w (kernels whose other wavefronts read it); otherwise
+// s2.w holds 1 / opacity and the wavefront reads each record's mask from
+// the returning lane with readlane.
+template <bool kMaskInLds>
+__device__ __forceinline__ uint32_t stage_batch(
+    const float4* __restrict__ packed, const int32_t* __restrict__ binned,
+    int first, int n, const TileCoord& tc, Staged& S) {
   const int lane = threadIdx.x;
+  uint32_t m = 0u;
   if (lane < n) {
     const int gid = binned[first + lane];
     const float4 p0 = packed[3 * gid + 0];
     const float4 p1 = packed[3 * gid + 1];
     const float4 p2 = packed[3 * gid + 2];
     const float a = p0.z, b = p0.w, c = p1.x;
-    const uint32_t m = strip_mask(p0.x, p0.y, a, b, c, p2.z, tc.x0, tc.y0);
+    m = strip_mask(p0.x, p0.y, a, b, c, p2.z, tc.x0, tc.y0);
     float A, B, C;
     {
 #pragma clang fp contract(off)
@@ -156,8 +161,11 @@ __device__ __forceinline__ void stage_batch(const float4* __restrict__ packed,
     }
     S.s0[lane] = make_float4(p0.x, p0.y, A, B);
     S.s1[lane] = make_float4(C, p1.y, p1.z, p1.w);
-    S.s2[lane] = make_float4(p2.x, p2.y, p2.z, __uint_as_float(m));
+    S.s2[lane] = make_float4(
+        p2.x, p2.y, p2.z,
+        kMaskInLds ? __uint_as_float(m) : __builtin_amdgcn_rcpf(p1.y));
   }
+  return m;
 }
 
 // p = fma(C dy, dy, fma(B dx, dy, (A dx) dx)) with the x-only products
@@ -400,12 +408,12 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     }
     const int n = min(kBatch, end - base);
     __syncthreads();
-    stage_batch(packed, binned, base, n, tc, S);
+    const uint32_t bmask = stage_batch<false>(packed, binned, base, n, tc, S);
     __syncthreads();
     for (int j = 0; j < n; ++j) {
-      const float4 a2 = S.s2[j];
-      const uint32_t mask = uniform_bits(a2.w);
+      const uint32_t mask = __builtin_amdgcn_readlane(bmask, j);
       if (mask == 0u) continue;
+      const float4 a2 = S.s2[j];
       const float4 a0 = S.s0[j];
       const float4 a1 = S.s1[j];
       float Adxdx, Bdx;
@@ -525,7 +533,7 @@ __global__ __launch_bounds__(kLongThreads) void render_fwd_long_kernel(
         ++seg_cur;
       }
       const int n = min(kBatch, end - base);
-      stage_batch(packed, binned, base, n, tc, S);
+      stage_batch<true>(packed, binned, base, n, tc, S);
       __syncthreads();
       for (int j = 0; j < n; ++j) {
         // all three reads issued before the mask test: one LDS round trip
@@ -704,12 +712,13 @@ __device__ __forceinline__ void bwd_walk(
     const int cstart = max(lo, cend - kBatch);
     const int n = cend - cstart;
     __syncthreads();
-    stage_batch(packed, binned, start + cstart, n, tc, S);
+    const uint32_t bmask =
+        stage_batch<false>(packed, binned, start + cstart, n, tc, S);
     __syncthreads();
     for (int j = n - 1; j >= 0; --j) {
-      const float4 a2 = S.s2[j];
-      const uint32_t mask = uniform_bits(a2.w);
+      const uint32_t mask = __builtin_amdgcn_readlane(bmask, j);
       if (mask == 0u) continue;
+      const float4 a2 = S.s2[j];
       const int i = cstart + j;
       const float4 a0 = S.s0[j];
       const float4 a1 = S.s1[j];
@@ -778,7 +787,7 @@ __device__ __forceinline__ void bwd_walk(
           unsafeAtomicAdd(p1, r1 * role.scale1);
           unsafeAtomicAdd(p2, r2 * role.scale2);
           if (threadIdx.x == 48)
-            unsafeAtomicAdd(g_opac + orig, r3 * __builtin_amdgcn_rcpf(a1.y));
+            unsafeAtomicAdd(g_opac + orig, r3 * a2.w);  // a2.w = 1 / opacity
         }
       }
     }
