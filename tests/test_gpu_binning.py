@@ -45,6 +45,7 @@ def test_exclusive_scan_in_place(gpu):
     (4096, 1, 0, 32, 1 << 32),
     (100_003, 1, 0, 13, 37),          # many duplicates, partial digit
     (700_001, 1, 0, 16, 1 << 16),
+    (2_500_003, 1, 0, 32, 1 << 32),   # 32-bit keys, 16 rounds per workgroup
     (65536, 4, 0, 32, 1 << 32),       # segmented
     (10_000, 3, 8, 24, 1 << 32),      # bit window
     (1000, 2, 0, 0, 1 << 32),         # zero passes: copy
