@@ -212,7 +212,7 @@ __device__ __forceinline__ uint32_t uniform_bits(float v) {
 // splats, and T at its end is recorded.
 constexpr int kSegSplats = 128;     // multiple of kBatch
 constexpr int kHandoff = 128;       // multiple of kSegSplats
-constexpr int kLongThreads = 256;   // one wavefront per strip
+constexpr int kLongStrips = 1;      // strips per wavefront of the long kernel
 
 struct HeavyState {      // all null: every tile is walked whole by one wave
   int32_t* counters;     // [0] slots handed out, [1] tiles handed off
@@ -258,28 +258,31 @@ __device__ __forceinline__ int tile_pixel(int k) {
   return 64 * k + (int)threadIdx.x;
 }
 
-// The thread id through an empty asm: addresses derived from it are
-// computed where they are used, so that the compiler does not keep 64-bit
-// addresses for the rare segment boundaries live across the compositing
-// loop.
-__device__ __forceinline__ int opaque_tid() {
-  int t = (int)threadIdx.x;
-  asm volatile("" : "+v"(t));
-  return t;
+// A value through an empty asm: addresses derived from it are computed
+// where they are used, so that the compiler does not keep 64-bit addresses
+// for the rare segment boundaries live across the compositing loop.
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
 }
 
-// Image index of this thread's pixel in its first strip.
+// t0 below is the in-tile index (tile_pixel order, 64 strip + lane) of this
+// thread's pixel in the first strip it walks; its further strips follow at
+// +64 (four rows down).
+
+// Image index of pixel t0 of the tile.
 __device__ __forceinline__ int64_t pixel_index(const RasterParams& P,
-                                               const TileCoord& tc) {
-  const int t = opaque_tid();
+                                               const TileCoord& tc, int t0) {
+  const int t = opaque(t0);
   const int y = tc.y0 + (t >> 4);
   const int x = tc.x0 + (t & 15);
   return ((int64_t)tc.batch * P.height + y) * P.width + x;
 }
 
-// Segment record of this thread's pixel in its first strip (null if none).
-__device__ __forceinline__ float4* record_at(const HeavyState& H, int slot) {
-  return slot >= 0 ? H.rec + (int64_t)slot * 256 + opaque_tid() : nullptr;
+// Segment record entry of pixel t0 (null if no record is kept).
+__device__ __forceinline__ float4* record_at(const HeavyState& H, int slot,
+                                             int t0) {
+  return slot >= 0 ? H.rec + (int64_t)slot * 256 + opaque(t0) : nullptr;
 }
 
 // End of segment `seg` for NP strips per thread: record it in `slot`
@@ -291,9 +294,9 @@ __device__ __forceinline__ void end_segment(const RasterParams& P,
                                             const HeavyState& H, int slot,
                                             int seg, const bool* valid,
                                             float* cr, float* cg, float* cb,
-                                            const float* T) {
-  float* o0 = out_rgb + 3 * pixel_index(P, tc);
-  float4* r0 = record_at(H, slot);
+                                            const float* T, int t0) {
+  float* o0 = out_rgb + 3 * pixel_index(P, tc, t0);
+  float4* r0 = record_at(H, slot, t0);
 #pragma unroll
   for (int k = 0; k < NP; ++k) {
     if (r0 != nullptr) r0[64 * k] = make_float4(cr[k], cg[k], cb[k], T[k]);
@@ -322,9 +325,9 @@ __device__ __forceinline__ void last_segment(const RasterParams& P,
                                              const HeavyState& H, int slot,
                                              const bool* valid, float* cr,
                                              float* cg, float* cb,
-                                             const float* T) {
-  const float* o0 = out_rgb + 3 * pixel_index(P, tc);
-  float4* r0 = record_at(H, slot);
+                                             const float* T, int t0) {
+  const float* o0 = out_rgb + 3 * pixel_index(P, tc, t0);
+  float4* r0 = record_at(H, slot, t0);
 #pragma unroll
   for (int k = 0; k < NP; ++k) {
     if (r0 != nullptr) r0[64 * k] = make_float4(cr[k], cg[k], cb[k], T[k]);
@@ -403,7 +406,8 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
                            (T[3] > t_thr);
     if (!__any(any_alive)) break;
     if (base > start && (base - start) % kSegSplats == 0) {
-      end_segment<kPix>(P, tc, out_rgb, H, -1, seg_cur, valid, cr, cg, cb, T);
+      end_segment<kPix>(P, tc, out_rgb, H, -1, seg_cur, valid, cr, cg, cb, T,
+                        (int)threadIdx.x);
       ++seg_cur;
     }
     const int n = min(kBatch, end - base);
@@ -437,11 +441,12 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
       int tail = -1, slot = -1;  // chain state, meaningful in lane 0
       if (threadIdx.x == 0) slot = next_segment(H, tc.tile, 0, tail);
       slot = __shfl(slot, 0, 64);
-      end_segment<kPix>(P, tc, out_rgb, H, slot, 0, valid, cr, cg, cb, T);
+      end_segment<kPix>(P, tc, out_rgb, H, slot, 0, valid, cr, cg, cb, T,
+                        (int)threadIdx.x);
       int item = 0;
       if (threadIdx.x == 0) item = atomicAdd(H.counters + 1, 1);
       item = __shfl(item, 0, 64);
-      const int64_t pix0 = pixel_index(P, tc);
+      const int64_t pix0 = pixel_index(P, tc, (int)threadIdx.x);
       int tile_max = 0;
 #pragma unroll
       for (int k = 0; k < kPix; ++k) {
@@ -462,7 +467,8 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     }
   }
   if (seg_cur > 0)  // (no workspace: nothing recorded)
-    last_segment<kPix>(P, tc, out_rgb, H, -1, valid, cr, cg, cb, T);
+    last_segment<kPix>(P, tc, out_rgb, H, -1, valid, cr, cg, cb, T,
+                       (int)threadIdx.x);
   int tile_max = 0;
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
@@ -488,11 +494,13 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
 }
 
 // Continuation of the tiles handed off by render_fwd_kernel: a workgroup of
-// four wavefronts per tile, wavefront w walking strip w (one pixel per
-// thread) from the saved state with the same per-pixel operations, so the
-// result is bit for bit the one-wavefront walk's.  Workgroup b takes
-// hand-off items b, b + gridDim.x, ...
-__global__ __launch_bounds__(kLongThreads) void render_fwd_long_kernel(
+// 4 / kSpW wavefronts per tile, wavefront w walking strips kSpW w ..
+// kSpW w + kSpW - 1 (lane l: column l % 16, row 4 strip + l / 16) from the
+// saved state with the same per-pixel operations, so the result is bit for
+// bit the one-wavefront walk's.  Workgroup b takes hand-off items b,
+// b + gridDim.x, ...
+template <int kSpW>
+__global__ __launch_bounds__(256 / kSpW) void render_fwd_long_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ tile_offsets,
     const int32_t* __restrict__ binned, float* __restrict__ out_rgb,
@@ -500,7 +508,9 @@ __global__ __launch_bounds__(kLongThreads) void render_fwd_long_kernel(
     int32_t* __restrict__ out_tile_stop, HeavyState H) {
   __shared__ Staged S;
   __shared__ int sh_slot;
-  const int strip = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = (int)threadIdx.x & 63;
+  const int s0 = __builtin_amdgcn_readfirstlane(((int)threadIdx.x >> 6) * kSpW);
+  const int t0 = 64 * s0 + lane;  // in-tile index of the first strip's pixel
   const int n_items = H.counters[1];
   const float t_thr = P.trans_thr;
   const float max_alpha = fminf(P.max_alpha, 1.0f);
@@ -508,66 +518,87 @@ __global__ __launch_bounds__(kLongThreads) void render_fwd_long_kernel(
     __syncthreads();  // the previous tile's reads of S and sh_slot are done
     const int tile = H.handoff[item];
     int tail = H.handoff_tail[item];  // used by thread 0
-    // tile_coord_of with a 256-thread id: ly = 4 strip + l/16, so slot 0 of
-    // this thread is its pixel of strip `strip`, and tile_pixel(0) its index.
     const TileCoord tc = tile_coord_of(P, tile);
-    const int x = tc.x0 + tc.lx;
-    const int y = slot_y(tc, 0);
-    const float px = (float)x + 0.5f, py = (float)y + 0.5f;
-    bool valid[1] = {(x < P.width) && (y < P.height)};
-    const int64_t pix = ((int64_t)tc.batch * P.height + y) * P.width + x;
-    float T[1] = {H.hand_T[(int64_t)item * 256 + tile_pixel(0)]};
-    int last = (valid[0] && out_last != nullptr) ? out_last[pix] : 0;
-    float cr[1] = {0.0f}, cg[1] = {0.0f}, cb[1] = {0.0f};
+    const int x = tc.x0 + (lane & 15);
+    const float px = (float)x + 0.5f;
+    float py[kSpW], T[kSpW], cr[kSpW], cg[kSpW], cb[kSpW];
+    int last[kSpW];
+    bool valid[kSpW];
+    int64_t pix[kSpW];
+#pragma unroll
+    for (int k = 0; k < kSpW; ++k) {
+      const int y = tc.y0 + 4 * (s0 + k) + (lane >> 4);
+      valid[k] = (x < P.width) && (y < P.height);
+      py[k] = (float)y + 0.5f;
+      pix[k] = ((int64_t)tc.batch * P.height + y) * P.width + x;
+      T[k] = H.hand_T[(int64_t)item * 256 + t0 + 64 * k];
+      last[k] = (valid[k] && out_last != nullptr) ? out_last[pix[k]] : 0;
+      cr[k] = cg[k] = cb[k] = 0.0f;
+    }
     const int start = tile_offsets[tile];
     const int end = tile_offsets[tile + 1];
     int seg_cur = kHandoff / kSegSplats;
     for (int base = start + kHandoff; base < end; base += kBatch) {
-      if (!__syncthreads_or(T[0] > t_thr)) break;  // uniform; frees S
+      bool alive = false;
+#pragma unroll
+      for (int k = 0; k < kSpW; ++k) alive |= T[k] > t_thr;
+      if (!__syncthreads_or(alive)) break;  // uniform; frees S
       // (the boundary at kHandoff was closed by render_fwd_kernel)
       if (base > start + kHandoff && (base - start) % kSegSplats == 0) {
         if (threadIdx.x == 0) sh_slot = next_segment(H, tile, seg_cur, tail);
         __syncthreads();
-        end_segment<1>(P, tc, out_rgb, H, sh_slot, seg_cur, valid, cr, cg, cb,
-                       T);
+        end_segment<kSpW>(P, tc, out_rgb, H, sh_slot, seg_cur, valid, cr, cg,
+                          cb, T, t0);
         ++seg_cur;
       }
       const int n = min(kBatch, end - base);
       stage_batch<true>(packed, binned, base, n, tc, S);
       __syncthreads();
+      // Software pipelined: record j + 1 is read from LDS while record j is
+      // composited, so the walk does not wait for LDS on every splat.
+      float4 n0 = S.s0[0], n1 = S.s1[0], n2 = S.s2[0];
       for (int j = 0; j < n; ++j) {
-        // all three reads issued before the mask test: one LDS round trip
-        float4 a0 = S.s0[j], a1 = S.s1[j], a2 = S.s2[j];
-        asm volatile("" : "+v"(a0.x), "+v"(a0.y), "+v"(a0.z), "+v"(a0.w),
-                     "+v"(a1.x), "+v"(a1.y), "+v"(a1.z), "+v"(a1.w),
-                     "+v"(a2.x), "+v"(a2.z), "+v"(a2.w));
-        const uint32_t mask = uniform_bits(a2.w);
-        if (!((mask >> strip) & 1u)) continue;  // scalar branch
+        const float4 a0 = n0, a1 = n1, a2 = n2;
+        const int jn = min(j + 1, n - 1);
+        n0 = S.s0[jn];
+        n1 = S.s1[jn];
+        n2 = S.s2[jn];
+        const uint32_t mask = uniform_bits(a2.w) >> s0;
+        if (!(mask & ((1u << kSpW) - 1u))) continue;  // scalar branch
         float Adxdx, Bdx;
         x_terms(a0.z, a0.w, px - a0.x, Adxdx, Bdx);
-        composite_one(Adxdx, Bdx, a1, a2, py, a0.y, t_thr, max_alpha,
-                      base - start + j + 1, T[0], cr[0], cg[0], cb[0], last);
+#pragma unroll
+        for (int k = 0; k < kSpW; ++k) {
+          if (!((mask >> k) & 1u)) continue;  // scalar branch
+          composite_one(Adxdx, Bdx, a1, a2, py[k], a0.y, t_thr, max_alpha,
+                        base - start + j + 1, T[k], cr[k], cg[k], cb[k],
+                        last[k]);
+        }
       }
     }
     __syncthreads();  // sh_slot of the last boundary has been read
     if (threadIdx.x == 0) sh_slot = next_segment(H, tile, seg_cur, tail);
     __syncthreads();
-    last_segment<1>(P, tc, out_rgb, H, sh_slot, valid, cr, cg, cb, T);
-    if (valid[0]) {
-      out_rgb[3 * pix + 0] = cr[0] + T[0] * P.bg_r;
-      out_rgb[3 * pix + 1] = cg[0] + T[0] * P.bg_g;
-      out_rgb[3 * pix + 2] = cb[0] + T[0] * P.bg_b;
-      if (out_T != nullptr) {
-        out_T[pix] = T[0];
-        out_last[pix] = last;
+    last_segment<kSpW>(P, tc, out_rgb, H, sh_slot, valid, cr, cg, cb, T, t0);
+    int tile_max = 0;
+#pragma unroll
+    for (int k = 0; k < kSpW; ++k) {
+      if (valid[k]) {
+        out_rgb[3 * pix[k] + 0] = cr[k] + T[k] * P.bg_r;
+        out_rgb[3 * pix[k] + 1] = cg[k] + T[k] * P.bg_g;
+        out_rgb[3 * pix[k] + 2] = cb[k] + T[k] * P.bg_b;
+        if (out_T != nullptr) {
+          out_T[pix[k]] = T[k];
+          out_last[pix[k]] = last[k];
+        }
+        tile_max = max(tile_max, last[k]);
       }
     }
     if (out_tile_stop != nullptr) {
-      int tile_max = valid[0] ? last : 0;
 #pragma unroll
       for (int off = 32; off > 0; off >>= 1)
         tile_max = max(tile_max, __shfl_xor(tile_max, off, 64));
-      if ((threadIdx.x & 63) == 0) atomicMax(out_tile_stop + tile, tile_max);
+      if (lane == 0) atomicMax(out_tile_stop + tile, tile_max);
     }
   }
 }
@@ -855,7 +886,7 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
         float cr[kPix], cg[kPix], cb[kPix];
 #pragma unroll
         for (int k = 0; k < kPix; ++k) cr[k] = cg[k] = cb[k] = 0.0f;
-        const int t = opaque_tid();
+        const int t = opaque((int)threadIdx.x);
         int sl = H.slot_next[m];
         for (int j = kseg + 1;
              j < nseg && (unsigned)sl < (unsigned)H.max_slots; ++j) {
@@ -956,7 +987,8 @@ int launch_render_forward(const RasterParams& P, const float* packed,
   if (rc || H.counters == nullptr) return rc;
   // Workgroups stride over the hand-off list (its length is on the device).
   const unsigned grid = (unsigned)std::min<int64_t>(P.num_tiles, 2048);
-  hipLaunchKernelGGL(render_fwd_long_kernel, dim3(grid), dim3(kLongThreads), 0,
+  hipLaunchKernelGGL(render_fwd_long_kernel<kLongStrips>, dim3(grid),
+                     dim3(256 / kLongStrips), 0,
                      stream, P, pk, tile_offsets, binned_ids, out_rgb, out_T,
                      out_last, out_tile_stop, H);
   return check_launch("render_fwd_long_kernel");
