@@ -196,7 +196,8 @@ __global__ __launch_bounds__(kThreads) void sum_kernel(
 // One thread per depth-sorted splat (gid): gathers the attributes of
 // orig = perm[gid] into the packed 48-byte record and turns the per-gid
 // tile-hit counts into exclusive offsets splat_offsets in the same launch
-// (workgroup scan + decoupled look-back).
+// (workgroup scan + decoupled look-back).  splat_offsets[num_splats] = N, or
+// -1 when N does not fit in int32 (the offsets are then unusable).
 __global__ __launch_bounds__(kThreads) void pack_kernel(
     RasterParams P, const float* __restrict__ means2d,
     const float* __restrict__ conics, const float* __restrict__ colors,
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
     int32_t* __restrict__ splat_offsets, uint64_t* scan_status,
     uint32_t* scan_ticket) {
   __shared__ int wsum[kThreads / 64];
-  __shared__ int s_prefix;
+  __shared__ long long s_prefix;
   const int vb = take_ticket(scan_ticket);
   const int gid = vb * kThreads + threadIdx.x;
   int n = 0;
@@ -254,18 +255,22 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
       if (lane == 0)
         status_store(&scan_status[vb], kFlagInc64 | (prefix + (uint32_t)total));
     }
-    if (lane == 0) s_prefix = (int)prefix;
+    if (lane == 0) s_prefix = (long long)prefix;
   }
   __syncthreads();
-  const int off = s_prefix + pre + inc - n;
-  if (gid < P.num_splats) splat_offsets[gid] = off;
-  if (gid == P.num_splats - 1) splat_offsets[P.num_splats] = off + n;
+  const long long end = s_prefix + pre + inc;
+  if (gid < P.num_splats) splat_offsets[gid] = (int)(end - n);
+  if (gid == P.num_splats - 1)
+    splat_offsets[P.num_splats] = end > 0x7fffffffLL ? -1 : (int)end;
 }
 
+// Pairs are written (and counted in the histograms) only at positions below
+// min(N, capacity), N = splat_offsets[num_splats]: with a capacity below N
+// the output is the first `capacity` pairs, consistently.
 __global__ __launch_bounds__(kThreads) void emit_kernel(
     RasterParams P, const float4* __restrict__ packed,
-    const int32_t* __restrict__ splat_offsets, uint32_t* __restrict__ keys,
-    uint32_t* __restrict__ vals, int pair_passes,
+    const int32_t* __restrict__ splat_offsets, int64_t capacity,
+    uint32_t* __restrict__ keys, uint32_t* __restrict__ vals, int pair_passes,
     uint32_t* __restrict__ hist_partials, uint32_t* pair_status,
     int64_t pair_status_words) {
   __shared__ WalkSlots walk[kWaves];
@@ -286,16 +291,20 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
   const float4 p1 = packed[3 * g + 1];
   const SplatGeom s{p0.x, p0.y, p0.z, p0.w, p1.x, p1.y};
   base[wave][lane] = splat_offsets[g];
+  const int64_t n_eff =
+      min(capacity, (int64_t)max(splat_offsets[P.num_splats], 0));
   WalkSlots& W = walk[wave];
   const int total = walk_setup(P, valid, s, g / P.gpb, W);
   const int gid0 = blockIdx.x * kThreads + wave * 64;
   walk_candidates(P, W, total, [&](int sl, int tile) {
     const int slot = atomicAdd(&W.cnt[sl], 1);
     const int64_t pos = (int64_t)base[wave][sl] + slot;
-    keys[pos] = (uint32_t)tile;
-    vals[pos] = (uint32_t)(gid0 + sl);
-    for (int p = 0; p < pair_passes; ++p)
-      atomicAdd(&h[p][((uint32_t)tile >> (8 * p)) & 255u], 1u);
+    if (pos < n_eff) {  // pos >= 0 whenever n_eff > 0
+      keys[pos] = (uint32_t)tile;
+      vals[pos] = (uint32_t)(gid0 + sl);
+      for (int p = 0; p < pair_passes; ++p)
+        atomicAdd(&h[p][((uint32_t)tile >> (8 * p)) & 255u], 1u);
+    }
   });
   // (3) this workgroup's digit histograms for the pair sort, stored as
   // hist_partials[(p * 256 + d) * nblk + workgroup]
@@ -327,11 +336,14 @@ __global__ __launch_bounds__(kThreads) void hist_reduce_kernel(
 
 // tile_offsets from the sorted tile keys: index i (0 <= i <= n) is the first
 // pair of every tile t with keys[i-1] < t <= keys[i] (keys[-1] = -1,
-// keys[n] = num_tiles), so tile_offsets[num_tiles] = n.
+// keys[n] = num_tiles), so tile_offsets[num_tiles] = n.  With n_dev the key
+// count is min(*n_dev, n).
 __global__ __launch_bounds__(kThreads) void ranges_kernel(
-    const uint32_t* __restrict__ sorted_keys, int64_t n, int num_tiles,
+    const uint32_t* __restrict__ sorted_keys, int64_t n_cap,
+    const int32_t* __restrict__ n_dev, int num_tiles,
     int32_t* __restrict__ tile_offsets) {
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t n = n_dev ? min(n_cap, (int64_t)max(*n_dev, 0)) : n_cap;
   if (i > n) return;
   const int64_t prev = (i == 0) ? -1 : (int64_t)sorted_keys[i - 1];
   const int64_t cur = (i == n) ? (int64_t)num_tiles : (int64_t)sorted_keys[i];
@@ -424,16 +436,16 @@ int emit_blocks(const RasterParams& P) {
 }
 
 int launch_emit(const RasterParams& P, const float* packed,
-                const int32_t* splat_offsets, uint32_t* keys, uint32_t* vals,
-                int pair_passes, uint32_t* hist_partials, uint32_t* pair_ghist,
-                uint32_t* pair_status, int64_t pair_status_words,
-                hipStream_t stream) {
+                const int32_t* splat_offsets, int64_t capacity, uint32_t* keys,
+                uint32_t* vals, int pair_passes, uint32_t* hist_partials,
+                uint32_t* pair_ghist, uint32_t* pair_status,
+                int64_t pair_status_words, hipStream_t stream) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const int nblk = emit_blocks(P);
   hipLaunchKernelGGL(emit_kernel, dim3((unsigned)nblk), dim3(kThreads), 0,
                      stream, P, reinterpret_cast<const float4*>(packed),
-                     splat_offsets, keys, vals, pair_passes, hist_partials,
-                     pair_status, pair_status_words);
+                     splat_offsets, capacity, keys, vals, pair_passes,
+                     hist_partials, pair_status, pair_status_words);
   int rc = check_launch("emit_kernel");
   if (rc || pair_passes == 0) return rc;
   hipLaunchKernelGGL(hist_reduce_kernel, dim3((unsigned)(pair_passes * 256)),
@@ -444,7 +456,7 @@ int launch_emit(const RasterParams& P, const float* packed,
 
 int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        int32_t* tile_offsets, int32_t* tile_counts,
-                       hipStream_t stream) {
+                       hipStream_t stream, const int32_t* n_dev) {
   if (num_tiles <= 0) return GSPLAT_OK;
   int rc;
   if (n == 0) {
@@ -452,8 +464,8 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
   } else {
     hipLaunchKernelGGL(ranges_kernel,
                        dim3((unsigned)((n + 1 + kThreads - 1) / kThreads)),
-                       dim3(kThreads), 0, stream, sorted_keys, n, num_tiles,
-                       tile_offsets);
+                       dim3(kThreads), 0, stream, sorted_keys, n, n_dev,
+                       num_tiles, tile_offsets);
     rc = check_launch("ranges_kernel");
   }
   if (rc || tile_counts == nullptr) return rc;

@@ -314,7 +314,7 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
   rc = null_check({tile_offsets}, "gsplat_hip_bin_emit");
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (n_pairs == 0)
+  if (n_pairs == 0 || P.num_splats == 0)
     return gs::launch_tile_ranges(nullptr, 0, P.num_tiles, tile_offsets,
                                   tile_counts, s);
   rc = null_check({packed, splat_offsets, binned_ids, count_workspace,
@@ -340,19 +340,24 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
   const gs::RadixCtl ctl{reinterpret_cast<uint32_t*>(cbase + C.pair_ghist),
                          reinterpret_cast<uint32_t*>(base + L.status),
                          reinterpret_cast<uint32_t*>(cbase + C.pair_tickets)};
+  // The pair count N is read on the device (splat_offsets[BG], written by
+  // bin_pack); n_pairs is the capacity of the buffers and every stage takes
+  // the first min(N, n_pairs) pairs.
+  const int32_t* n_dev = splat_offsets + P.num_splats;
   // 1. pairs at deterministic per-splat ranges + the sort's histograms
-  rc = gs::launch_emit(P, packed, splat_offsets, keys, vals, L.pairs.passes,
+  rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals,
+                       L.pairs.passes,
                        reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
                        ctl.status, L.pairs.status_words, s);
   // 2. stable sort by tile
   if (!rc)
     rc = gs::radix_passes(L.pairs, ctl, base + L.buffers, keys, vals, nullptr,
                           sorted_keys, reinterpret_cast<uint32_t*>(binned_ids),
-                          s);
+                          s, n_dev);
   // 3. tile ranges and counts from the sorted keys
   if (!rc)
     rc = gs::launch_tile_ranges(sorted_keys, n_pairs, P.num_tiles,
-                                tile_offsets, tile_counts, s);
+                                tile_offsets, tile_counts, s, n_dev);
   return rc;
 }
 

@@ -10,9 +10,9 @@
 // are staged 64 at a time in LDS (each lane gathers one 48-byte record and
 // derives the per-tile constants) and read by all lanes as broadcasts.  A
 // strip is skipped (scalar branch on a per-record bit mask) when the
-// minimum of the splat's quadratic form over the strip's pixel centres
-// exceeds the alpha-support radius by a safety margin, so no pixel that
-// could pass the alpha test is ever skipped.
+// splat's support ellipse, enlarged by a safety margin, spans no row of the
+// strip inside the tile's columns, so no pixel that could pass the alpha
+// test is ever skipped.
 //
 // Alpha test (reference eval_alpha, variants/v8/csrc/metal/gsplat_v8_kernels.metal:121-139):
 // the exponent is evaluated in base 2, p = log2(e) * power, by the fixed

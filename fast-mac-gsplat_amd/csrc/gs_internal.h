@@ -70,11 +70,14 @@ int radix_global_hist(const RadixPlan& L, const RadixCtl& C,
                       const uint32_t* keys, const float* depth_src,
                       hipStream_t stream);
 // One onesweep launch per pass.  depth_src: first pass derives keys from
-// float depths and values from the in-segment index.
+// float depths and values from the in-segment index.  n_dev (one segment
+// only): the sort takes the first min(*n_dev, L.n_seg) elements, L.n_seg
+// being the capacity of the buffers; the histograms must count exactly those.
 int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
                  const uint32_t* keys_in, const uint32_t* vals_in,
                  const float* depth_src, uint32_t* keys_out,
-                 uint32_t* vals_out, hipStream_t stream);
+                 uint32_t* vals_out, hipStream_t stream,
+                 const int32_t* n_dev = nullptr);
 // Self-contained sort (zeroes its control block, computes the histograms).
 int radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in,
                      const float* depth_src, uint32_t* keys_out,
@@ -106,18 +109,19 @@ int count_scan_blocks(const RasterParams& P);
 // emit: writes the (tile, gid) pairs into each splat's range, zeroes
 // pair_status, and fills pair_ghist ([pair_passes][256]) with the pair sort's
 // digit histograms via per-workgroup partials (emit_blocks(P) * 4 * 256
-// words).
+// words).  Only the first min(N, capacity) pairs are written and counted,
+// N = splat_offsets[num_splats] (-1 when N overflowed: nothing is written).
 int emit_blocks(const RasterParams& P);
 int launch_emit(const RasterParams& P, const float* packed,
-                const int32_t* splat_offsets, uint32_t* keys, uint32_t* vals,
-                int pair_passes, uint32_t* hist_partials, uint32_t* pair_ghist,
-                uint32_t* pair_status, int64_t pair_status_words,
-                hipStream_t stream);
+                const int32_t* splat_offsets, int64_t capacity, uint32_t* keys,
+                uint32_t* vals, int pair_passes, uint32_t* hist_partials,
+                uint32_t* pair_ghist, uint32_t* pair_status,
+                int64_t pair_status_words, hipStream_t stream);
 // tile_offsets[0..T] and (unless tile_counts is NULL) tile_counts[0..T)
-// from the n sorted tile keys.
+// from the n sorted tile keys (min(n, *n_dev) of them with n_dev).
 int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        int32_t* tile_offsets, int32_t* tile_counts,
-                       hipStream_t stream);
+                       hipStream_t stream, const int32_t* n_dev = nullptr);
 int launch_zero2(uint32_t* a, int64_t na, uint32_t* b, int64_t nb,
                  hipStream_t stream);
 int launch_fill_i32(int32_t* dst, int32_t value, int64_t n, hipStream_t stream);

@@ -59,7 +59,8 @@ struct PassArgs {
   const float* depth_src;    // keys derived from float depths (kDepthKeys)
   uint32_t* keys_out;        // unused without kKeysOut (last pass)
   uint32_t* vals_out;
-  int64_t n_seg;
+  int64_t n_seg;             // elements per segment (a capacity with n_dev)
+  const int32_t* n_dev;      // one segment: min(*n_dev, n_seg) elements (or null)
   int nblk;                  // workgroups per segment
   int segments;
   int shift;
@@ -148,6 +149,11 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   const int seg = vb / a.nblk;
   const int blk = vb - seg * a.nblk;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  // With the element count on the device, workgroups past it have nothing
+  // to do: none of the workgroups before them looks back at them.
+  const int64_t n_seg =
+      a.n_dev ? min(a.n_seg, (int64_t)max(*a.n_dev, 0)) : a.n_seg;
+  if ((int64_t)blk * kBlockItems >= n_seg) return;
   for (int i = t; i < kWaves * 256; i += kThreads) (&cnt[0][0])[i] = 0u;
 
   const int64_t seg_base = (int64_t)seg * a.n_seg;
@@ -160,7 +166,7 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   uint32_t kreg[kR], vreg[kR], rreg[kR];
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
-    const int64_t src = seg_base + min(lo + r * 64 + lane, a.n_seg - 1);
+    const int64_t src = seg_base + min(lo + r * 64 + lane, n_seg - 1);
     kreg[r] = (kMode & kDepthKeys) ? __float_as_uint(a.depth_src[src])
                                    : a.keys_in[src];
     if (kMode & kValsIn) vreg[r] = a.vals_in[src];
@@ -173,7 +179,7 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
     const int64_t j = lo + r * 64 + lane;
-    const bool valid = j < a.n_seg;
+    const bool valid = j < n_seg;
     if (kMode & kDepthKeys) kreg[r] = depth_key(__uint_as_float(kreg[r]));
     if (!(kMode & kValsIn)) vreg[r] = (uint32_t)j;
     const uint32_t d = (kreg[r] >> a.shift) & dmask;
@@ -220,14 +226,15 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   }
   __syncthreads();
 
-  const int64_t remain = a.n_seg - (int64_t)blk * kBlockItems;
+  const int64_t remain = n_seg - (int64_t)blk * kBlockItems;
   const int count = remain < kBlockItems ? (int)remain : kBlockItems;
   for (int i = t; i < count; i += kThreads) {
     const uint32_t key = sk[i];
     const uint32_t d = (key >> a.shift) & dmask;
-    const int64_t dst = seg_base + (int64_t)gbase[d] + (int64_t)(i - (int)dstart[d]);
-    if (kMode & kKeysOut) a.keys_out[dst] = key;
-    a.vals_out[dst] = sv[i];
+    const int64_t pos = (int64_t)gbase[d] + (int64_t)(i - (int)dstart[d]);
+    if (pos >= n_seg) continue;  // only with histograms inconsistent with the keys
+    if (kMode & kKeysOut) a.keys_out[seg_base + pos] = key;
+    a.vals_out[seg_base + pos] = sv[i];
   }
 }
 
@@ -330,13 +337,18 @@ int radix_global_hist(const RadixPlan& L, const RadixCtl& C,
 int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
                  const uint32_t* keys_in, const uint32_t* vals_in,
                  const float* depth_src, uint32_t* keys_out,
-                 uint32_t* vals_out, hipStream_t stream) {
+                 uint32_t* vals_out, hipStream_t stream,
+                 const int32_t* n_dev) {
   if (L.n_seg == 0 || L.segments == 0) return GSPLAT_OK;
+  if (n_dev != nullptr && L.segments != 1) {
+    set_error("radix sort: a device element count needs one segment");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
   char* base = static_cast<char*>(buffers);
   const int64_t n = L.n_seg * L.segments;
-  if (L.passes == 0) {
+  if (L.passes == 0) {  // copies all L.n_seg elements (in bounds with n_dev)
     PassArgs a{keys_in, vals_in, depth_src, keys_out, vals_out, L.n_seg,
-               L.nblk, L.segments, 0, 0, nullptr, nullptr, nullptr};
+               nullptr, L.nblk, L.segments, 0, 0, nullptr, nullptr, nullptr};
     hipLaunchKernelGGL(rs_copy_kernel, dim3((unsigned)((n + 255) / 256)),
                        dim3(256), 0, stream, a, n);
     return check_launch("rs_copy_kernel");
@@ -355,7 +367,7 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
     const bool last = (p == L.passes - 1);
     uint32_t* out_k = last ? keys_out : bufk[p & 1];
     uint32_t* out_v = last ? vals_out : bufv[p & 1];
-    PassArgs a{cur_k, cur_v, cur_depth, out_k, out_v, L.n_seg, L.nblk,
+    PassArgs a{cur_k, cur_v, cur_depth, out_k, out_v, L.n_seg, n_dev, L.nblk,
                L.segments, shift, bits,
                C.ghist + (int64_t)p * L.segments * 256,
                C.status + p * status_per_pass, C.tickets + p};

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("GSPLAT_HIP_LIB", os.path.join(_HERE, "lib", "libgsplat_hip.so"))
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 TILE_SIZE = 16
 RECORD_FLOATS = 12
 

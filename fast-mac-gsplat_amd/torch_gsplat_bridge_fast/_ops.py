@@ -2,9 +2,12 @@
 
 Each function allocates its outputs with torch's caching allocator on the
 inputs' device, enqueues the HIP work on the current stream and returns the
-tensors.  The only host synchronisation on the raster path is the read of the
-pair count N between binning's count and emit stages (the reference makes the
-same read, variants/v8/csrc/metal/gsplat_metal.mm:188).
+tensors.  The raster path holds one host synchronisation: the pair count N,
+which sizes the pair buffers (the reference reads it before emitting,
+variants/v8/csrc/metal/gsplat_metal.mm:188).  Here the buffers are sized from
+the count of an earlier call of the same shape and N is checked only after
+the compositor has been enqueued (bin_and_render), so the host does not stall
+the GPU between binning stages; the first call of a shape reads N first.
 """
 from __future__ import annotations
 
@@ -72,14 +75,54 @@ class _timed:
         return False
 
 
+# Pair-buffer capacity per (device, B, G, H, W), from the pair counts of
+# earlier calls: binning then needs no host read of N before the compositors
+# are enqueued.
+_capacity: dict = {}
+
+
+def _headroom(n: int) -> int:
+    return n + n // 4 + 4096
+
+
 @dataclass
 class BinState:
     perm: Optional[Tensor]          # int32 [BG]  depth rank -> original index within image
     packed: Tensor                  # float32 [BG, 12]  packed records in gid order
     splat_offsets: Optional[Tensor] # int32 [BG+1]
     tile_offsets: Tensor            # int32 [T+1]
-    binned_ids: Tensor              # int32 [N]
-    n_pairs: int
+    pairs: Tensor                   # int32 [capacity]; the first N entries are the binned gids
+    capacity: int                   # pair capacity the buffers and workspaces were sized for
+    _n_host: Optional[Tensor] = None                 # pinned int32 [1]: N once _n_ready completes
+    _n_ready: Optional[torch.cuda.Event] = None
+    _n: Optional[int] = None
+    _key: Optional[tuple] = None
+
+    @property
+    def n_pairs(self) -> int:
+        """The pair count N (waits for the count stage, which ran first on the GPU)."""
+        if self._n is None:
+            self._n_ready.synchronize()
+            self._n = int(self._n_host[0])
+        return self._n
+
+    def confirm(self) -> bool:
+        """True if all N pairs fit in the buffers.  Otherwise the binning holds only the first
+        `capacity` pairs and must be redone; the capacity for this shape has then been raised, so
+        binning the same inputs again fits.  Raises if N overflowed int32."""
+        n = self.n_pairs
+        if n < 0:
+            raise RuntimeError("pair count overflowed int32")
+        if self._key is not None:
+            cap = _capacity.get(self._key, 0)
+            if n > cap or 2 * _headroom(n) < cap:
+                _capacity[self._key] = _headroom(n)
+        return n <= self.capacity
+
+    @property
+    def binned_ids(self) -> Tensor:
+        """int32 [N] gids grouped by tile, depth order inside each tile."""
+        return self.pairs[: self.n_pairs]
 
     @property
     def num_tiles(self) -> int:
@@ -110,16 +153,39 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
 
 
 def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
-                  opacities: Tensor, depths: Tensor) -> BinState:
+                  opacities: Tensor, depths: Tensor, *, defer_check: bool = False) -> BinState:
     """Tile binning + stable depth order + record packing + pair sort + tile ranges.
 
     Inputs are flat contiguous fp32 [BG,2], [BG,3], [BG,3], [BG], [BG] in the
     original splat order.  The per-splat tile-hit count runs on a side stream
     while the depth sort runs on the caller's stream; packing waits for both.
-    The pair count N (needed on the host to size the pair buffers, like the
-    reference's tile_offsets[-1] read, variants/v8/csrc/metal/gsplat_metal.mm:188)
-    is copied to pinned memory right after the count and read after packing
-    has been enqueued, so the wait overlaps GPU work."""
+    The pair count N is copied to pinned memory right after the count.  The
+    pair buffers are sized from earlier calls of the same shape; the first call
+    reads N before emitting (like the reference's tile_offsets[-1] read,
+    variants/v8/csrc/metal/gsplat_metal.mm:188).  Unless defer_check, N is then
+    checked against the capacity (binning again if it did not fit); with
+    defer_check the caller must call confirm() before using the result."""
+    st = _bin(meta, means2d, conics, colors, opacities, depths)
+    if not defer_check and not st.confirm():
+        st = _bin(meta, means2d, conics, colors, opacities, depths)
+        if not st.confirm():
+            raise RuntimeError("binning: pair count changed between two binnings of the same inputs")
+    return st
+
+
+def bin_and_render(meta: _lib.RasterMeta, flat, *, save_state: bool):
+    """Binning then render_forward with the capacity check after the forward is enqueued, so
+    that the host never waits on the GPU in between.  Returns (BinState, render_forward outputs)."""
+    st = bin_gaussians(meta, *flat, defer_check=True)
+    out = render_forward(meta, st, save_state=save_state)
+    if not st.confirm():
+        st = bin_gaussians(meta, *flat)
+        out = render_forward(meta, st, save_state=save_state)
+    return st, out
+
+
+def _bin(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
+         opacities: Tensor, depths: Tensor) -> BinState:
     L = _lib.lib()
     dev = means2d.device
     B, G = meta.batch, meta.gaussians_per_batch
@@ -153,18 +219,24 @@ def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors
         check(L.gsplat_hip_bin_pack(meta, ptr(means2d), ptr(conics), ptr(colors), ptr(opacities), ptr(perm),
                                     ptr(packed), ptr(splat_offsets), ptr(ws), ws_bytes, s),
               "gsplat_hip_bin_pack")
-    n_ready.synchronize()
-    n = int(n_host[0])
-    if n < 0:
-        raise RuntimeError("pair count overflowed int32")
-    binned = _empty(n, torch.int32, dev)
-    ws2_bytes = L.gsplat_hip_bin_emit_workspace_bytes(meta, n)
+    key = (dev.index, B, G, meta.height, meta.width)
+    cap = _capacity.get(key)
+    n_known = None
+    if cap is None:
+        # first binning of this shape: size the buffers from N itself
+        n_ready.synchronize()
+        n_known = int(n_host[0])
+        if n_known < 0:
+            raise RuntimeError("pair count overflowed int32")
+        cap = n_known
+    pairs = _empty(cap, torch.int32, dev)
+    ws2_bytes = L.gsplat_hip_bin_emit_workspace_bytes(meta, cap)
     ws2 = _empty(max(ws2_bytes, 1), torch.uint8, dev)
     with _timed("bin_emit"):
-        check(L.gsplat_hip_bin_emit(meta, ptr(packed), ptr(splat_offsets), n, ptr(binned), None,
+        check(L.gsplat_hip_bin_emit(meta, ptr(packed), ptr(splat_offsets), cap, ptr(pairs), None,
                                     ptr(tile_offsets), ptr(ws), ws_bytes, ptr(ws2), ws2_bytes, s),
               "gsplat_hip_bin_emit")
-    return BinState(perm, packed, splat_offsets, tile_offsets, binned, n)
+    return BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, n_host, n_ready, n_known, key)
 
 
 def render_forward(meta: _lib.RasterMeta, st: BinState, *, save_state: bool):
@@ -181,11 +253,11 @@ def render_forward(meta: _lib.RasterMeta, st: BinState, *, save_state: bool):
         final_T = torch.empty((B, H, W), dtype=torch.float32, device=dev)
         last = torch.empty((B, H, W), dtype=torch.int32, device=dev)
         tile_stop = _empty(tiles, torch.int32, dev)
-    wsb = L.gsplat_hip_render_workspace_bytes(meta, st.n_pairs)
+    wsb = L.gsplat_hip_render_workspace_bytes(meta, st.capacity)
     ws = _empty(max(wsb, 1), torch.uint8, dev)
     with _timed("render_forward"):
-        check(L.gsplat_hip_render_forward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.binned_ids), ptr(img),
-                                          ptr(final_T), ptr(last), ptr(tile_stop), st.n_pairs, ptr(ws), wsb,
+        check(L.gsplat_hip_render_forward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.pairs), ptr(img),
+                                          ptr(final_T), ptr(last), ptr(tile_stop), st.capacity, ptr(ws), wsb,
                                           stream_of(img)),
               "gsplat_hip_render_forward")
     return img, final_T, last, tile_stop, (ws if save_state else None)
@@ -206,9 +278,9 @@ def render_backward(meta: _lib.RasterMeta, st: BinState, final_T: Tensor, last: 
     g_o = torch.empty((B, G), dtype=torch.float32, device=dev)
     grad_img = grad_img.contiguous()
     with _timed("render_backward"):
-        check(L.gsplat_hip_render_backward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.binned_ids),
+        check(L.gsplat_hip_render_backward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.pairs),
                                            ptr(final_T), ptr(last), ptr(tile_stop), ptr(grad_img), ptr(g_m), ptr(g_q),
-                                           ptr(g_c), ptr(g_o), st.n_pairs, ptr(workspace),
+                                           ptr(g_c), ptr(g_o), st.capacity, ptr(workspace),
                                            0 if workspace is None else workspace.numel(), stream_of(grad_img)),
               "gsplat_hip_render_backward")
     return g_m, g_q, g_c, g_o

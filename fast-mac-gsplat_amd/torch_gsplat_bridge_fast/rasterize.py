@@ -225,10 +225,9 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
         meta = _meta(config, B, G)
         flat = _flat(means2d_b.detach(), conics_b.detach(), colors_b.detach(), opacities_b.detach(),
                      depths_b.detach())
-        st = _ops.bin_gaussians(meta, *flat)
+        st, (img, final_T, last, tile_stop, ws) = _ops.bin_and_render(meta, flat, save_state=True)
         _check_overflow(config, st)
-        img, final_T, last, tile_stop, ws = _ops.render_forward(meta, st, save_state=True)
-        ctx.save_for_backward(st.packed, st.tile_offsets, st.binned_ids, final_T, last, tile_stop, ws)
+        ctx.save_for_backward(st.packed, st.tile_offsets, st.pairs, final_T, last, tile_stop, ws)
         ctx.meta = meta
         ctx.shape = (B, G)
         ctx.depth_shape = depths_b.shape
@@ -236,8 +235,8 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        packed, tile_offsets, binned_ids, final_T, last, tile_stop, ws = ctx.saved_tensors
-        st = _ops.BinState(None, packed, None, tile_offsets, binned_ids, binned_ids.numel())
+        packed, tile_offsets, pairs, final_T, last, tile_stop, ws = ctx.saved_tensors
+        st = _ops.BinState(None, packed, None, tile_offsets, pairs, pairs.numel())
         g_m, g_q, g_c, g_o = _ops.render_backward(ctx.meta, st, final_T, last, tile_stop, grad_out, ws)
         need = ctx.needs_input_grad
         g_depth = torch.zeros(ctx.depth_shape, dtype=torch.float32, device=grad_out.device) if need[4] else None
@@ -252,10 +251,10 @@ def _rasterize_chunk_eval(means2d_b, conics_b, colors_b, opacities_b, depths_b, 
     """Eval path (reference v8 rasterize.py:684-786): no saved state."""
     B, G = means2d_b.shape[:2]
     meta = _meta(config, B, G)
-    st = _ops.bin_gaussians(meta, *_flat(means2d_b, conics_b, colors_b, opacities_b, depths_b))
+    st, out = _ops.bin_and_render(meta, _flat(means2d_b, conics_b, colors_b, opacities_b, depths_b),
+                                  save_state=False)
     _check_overflow(config, st)
-    img = _ops.render_forward(meta, st, save_state=False)[0]
-    return img
+    return out[0]
 
 
 @torch.no_grad()

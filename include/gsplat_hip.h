@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 5
+#define GSPLAT_HIP_ABI_VERSION 6
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -94,9 +94,12 @@ const char* gsplat_hip_last_error(void);
  *                               the tile ranges/counts from the sorted keys.
  * bin_count and bin_depth_order use disjoint parts of the workspace and may
  * run concurrently on two streams; the caller orders bin_pack after both
- * (e.g. with an event) and bin_emit after bin_pack.  A caller that needs N on
- * the host (to size binned_ids) copies it asynchronously after bin_count and
- * waits for it after enqueuing bin_pack, so the read overlaps GPU work. */
+ * (e.g. with an event) and bin_emit after bin_pack.  bin_emit reads N on the
+ * device and takes the capacity of its buffers from the caller, so no host
+ * read of N is needed before the compositors are enqueued: a caller sizes the
+ * buffers from an earlier call (or reads N first, as the reference does),
+ * copies N to the host asynchronously after bin_count and checks it against
+ * the capacity later, binning again with larger buffers if it did not fit. */
 
 /* Bytes of the binning workspace used by all four binning calls. */
 size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta);
@@ -137,14 +140,20 @@ size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
                                            int64_t n_pairs);
 
 /* Emits the N (tile, gid) pairs, sorts them by tile with a stable LSD radix
- * sort (8-bit digits) and extracts the tile ranges.  Outputs:
- *   binned_ids    int32 [N]    gids grouped by tile, ascending gid (= depth
- *                              order) inside each tile range; the sorted
- *                              64-bit key of pair i is
+ * sort (8-bit digits) and extracts the tile ranges.  N is read on the device
+ * (splat_offsets[BG] as bin_pack wrote it); n_pairs is the capacity of
+ * binned_ids and the size the workspace was queried for.  Outputs:
+ *   binned_ids    int32 [n_pairs]  first N entries: gids grouped by tile,
+ *                              ascending gid (= depth order) inside each tile
+ *                              range; the sorted 64-bit key of pair i is
  *                              (tile << 32) | binned_ids[i]
  *   tile_counts   int32 [T]    pairs per tile (may be NULL: not computed)
  *   tile_offsets  int32 [T+1]  tile t's range is [tile_offsets[t],
  *                              tile_offsets[t+1]); tile_offsets[T] = N
+ * With n_pairs < N only the first n_pairs pairs in (gid, tile) order are
+ * binned (tile_offsets[T] = n_pairs): a consistent but incomplete result that
+ * the caller discards and redoes from bin_count with n_pairs >= N.  With
+ * N = -1 (overflow) nothing is binned.
  * count_workspace is the workspace of bin_count / bin_pack.  Replaces
  * emit_binned_ids (variants/v8/csrc/metal/gsplat_v8_kernels.metal:290-327),
  * the reference's tile_counts/tile_offsets (count_tiles :244-288 + the

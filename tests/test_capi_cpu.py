@@ -30,7 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 5
+    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 6
 
 
 def _meta(**kw):
@@ -115,3 +115,24 @@ def test_projection_meta_rejected():
     one = ctypes.c_void_p(1)
     rc = L.gsplat_hip_project_forward(pm, *([one] * 10), None)
     assert rc == 1 and "batch" in L.gsplat_hip_last_error().decode()
+
+
+def test_pair_capacity_policy():
+    """Host bookkeeping of the pair capacity (no GPU): a count above the capacity fails the check and
+    raises the remembered capacity; a much smaller one lowers it; an overflowed count raises."""
+    from torch_gsplat_bridge_fast import _ops
+
+    key = ("cpu-test", 1, 2, 3, 4)
+    _ops._capacity.pop(key, None)
+    st = _ops.BinState(None, None, None, None, None, 1000, _n=900, _key=key)
+    assert st.confirm() and _ops._capacity[key] == _ops._headroom(900)
+    _ops._capacity[key] = 1000
+    st = _ops.BinState(None, None, None, None, None, 1000, _n=1001, _key=key)
+    assert not st.confirm() and _ops._capacity[key] == _ops._headroom(1001) >= 1001
+    _ops._capacity[key] = 10 ** 7
+    st = _ops.BinState(None, None, None, None, None, 10 ** 7, _n=5, _key=key)
+    assert st.confirm() and _ops._capacity[key] == _ops._headroom(5)
+    st = _ops.BinState(None, None, None, None, None, 10, _n=-1, _key=key)
+    with pytest.raises(RuntimeError, match="overflowed"):
+        st.confirm()
+    _ops._capacity.pop(key, None)

@@ -165,3 +165,56 @@ def test_binning_all_culled(gpu):
     st = _gpu_bins(sc, H, W, B, G)
     assert st.n_pairs == 0
     assert int(st.tile_counts.sum()) == 0
+
+
+def _capacity_key(B, G, H, W):
+    return (0, B, G, H, W)
+
+
+def test_binning_from_remembered_capacity(gpu):
+    """The second binning of a shape sizes its pair buffers from the first one's count and reads N
+    only afterwards; the result is bit-identical and the capacity covers N."""
+    B, G, H, W = 2, 3000, 200, 264
+    print(f"capacity B={B} G={G} {H}x{W}", flush=True)
+    sc = make_scene_2d(1, seed=5, G=G, B=B, H=H, W=W)
+    _ops._capacity.pop(_capacity_key(B, G, H, W), None)
+    first = _gpu_bins(sc, H, W, B, G)
+    assert first.capacity == first.n_pairs > 0
+    st = _gpu_bins(sc, H, W, B, G)
+    assert st.capacity > st.n_pairs == first.n_pairs
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    _assert_bins_equal(st, ob, sc, B, G)
+
+
+def test_binning_capacity_too_small(gpu):
+    """With buffers below N the binning holds exactly the first `capacity` pairs (every pair of the
+    gids whose range ends below it, part of the one range that straddles it), confirm() reports it,
+    and binning again fits and is exact."""
+    B, G, H, W = 1, 4000, 256, 256
+    print(f"capacity overflow B={B} G={G} {H}x{W}", flush=True)
+    sc = make_scene_2d(2, seed=9, G=G, B=B, H=H, W=W)
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    n = ob.binned_ids.size
+    key = _capacity_key(B, G, H, W)
+    for cap in (n // 3, n - 1):
+        _ops._capacity[key] = cap
+        dev = torch.device("cuda:0")
+        meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, (0.0, 0.0, 0.0))
+        flat = [sc[k].reshape(B * G, -1).squeeze(-1).contiguous().to(dev) for k in KEYS]
+        st = _ops.bin_gaussians(meta, *flat, defer_check=True)
+        assert st.capacity == cap
+        offsets = st.tile_offsets.cpu().numpy()
+        assert offsets[0] == 0 and offsets[-1] == cap and np.all(np.diff(offsets) >= 0)
+        assert not st.confirm() and st.n_pairs == n
+        assert _ops._capacity[key] >= n
+        # the truncated pairs: tile t holds a depth-ordered subset of the oracle's tile t
+        got = st.pairs[:cap].cpu().numpy()
+        splat_end = st.splat_offsets.cpu().numpy()[1:]
+        for t in range(ob.tile_offsets.size - 1):
+            want = ob.binned_ids[ob.tile_offsets[t]:ob.tile_offsets[t + 1]]
+            have = got[offsets[t]:offsets[t + 1]]
+            assert np.all(np.diff(have) > 0) and np.isin(have, want).all()
+            full = want[splat_end[want] <= cap]
+            assert np.isin(full, have).all()
+        st2 = _ops.bin_gaussians(meta, *flat)
+        _assert_bins_equal(st2, ob, sc, B, G)

@@ -189,6 +189,38 @@ def test_eval_path_matches_train_path(gpu):
     assert torch.equal(ev, tr.detach())
 
 
+def test_forward_rebins_when_pairs_exceed_capacity(gpu):
+    """A pair capacity remembered from a smaller scene is detected after the forward has been
+    enqueued; the forward bins and renders again, giving the same image and gradients."""
+    from torch_gsplat_bridge_fast import _ops
+
+    H, W, B, G = 200, 260, 1, 5000
+    print(f"rebin {H}x{W} G={G}", flush=True)
+    sc0 = make_scene_2d(1, seed=2, G=G, H=H, W=W)
+    sc = {k: sc0[k].to(gpu) for k in KEYS}
+    cfg = RasterConfig(height=H, width=W)
+    wgt = torch.rand(H, W, 3, generator=torch.Generator().manual_seed(3)).to(gpu)
+    key = (0, B, G, H, W)
+    _ops._capacity.pop(key, None)
+    results = []
+    for forced in (None, 100):
+        if forced is not None:
+            _ops._capacity[key] = forced
+        with torch.no_grad():
+            ev = rasterize_projected_gaussians(*[sc[k] for k in KEYS], cfg)
+        if forced is not None:
+            _ops._capacity[key] = forced
+        leaves = [sc[k].clone().requires_grad_(k != "depths") for k in KEYS]
+        img = rasterize_projected_gaussians(*leaves, cfg)
+        (img * wgt).sum().backward()
+        results.append((ev, img.detach(), [leaves[i].grad for i in range(4)]))
+        assert _ops._capacity[key] > 100
+    (ev0, img0, g0), (ev1, img1, g1) = results
+    assert torch.equal(ev0, ev1) and torch.equal(img0, img1) and torch.equal(ev0, img0)
+    for a, b in zip(g0, g1):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-7)
+
+
 def test_unbatched_matches_batched(gpu):
     sc0 = make_scene_2d(3, seed=5, G=3000, B=2, H=64, W=96)
     cfg = RasterConfig(height=64, width=96)
