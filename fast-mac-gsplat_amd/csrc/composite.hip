@@ -632,61 +632,64 @@ __device__ __forceinline__ float wave_sum_row3(float x) {
   return x;
 }
 
-// Sums of four values over the 64 lanes: returns a register whose row r
-// (lanes 16r..16r+15) holds in every lane the total of v[order[r]] with
-// order = {0, 2, 1, 3}.  v_permlane32_swap exchanges the upper half of its
-// first operand with the lower half of its second, v_permlane16_swap the odd
-// rows of the first with the even rows of the second.
-__device__ __forceinline__ float wave_sum4(float v0, float v1, float v2,
-                                           float v3) {
-  const auto s01 = __builtin_amdgcn_permlane32_swap(
-      __float_as_uint(v0), __float_as_uint(v1), false, false);
-  const auto s23 = __builtin_amdgcn_permlane32_swap(
-      __float_as_uint(v2), __float_as_uint(v3), false, false);
-  // rows of h01: v0(rows 0+2), v0(1+3), v1(0+2), v1(1+3); h23 likewise
-  const float h01 = __uint_as_float(s01[0]) + __uint_as_float(s01[1]);
-  const float h23 = __uint_as_float(s23[0]) + __uint_as_float(s23[1]);
-  const auto s = __builtin_amdgcn_permlane16_swap(
-      __float_as_uint(h01), __float_as_uint(h23), false, false);
-  return row_sum_dpp(__uint_as_float(s[0]) + __uint_as_float(s[1]));
+// Sum over each group of eight lanes (8g..8g+7), left in every lane of the
+// group.
+__device__ __forceinline__ float group8_sum_dpp(float x) {
+  x += dpp_src<0xB1>(x);
+  x += dpp_src<0x4E>(x);
+  x += dpp_src<0x141>(x);
+  return x;
 }
 
-// Where lanes 0, 16, 32 and 48 (the row heads) send their reduced values.
-// Register 1 rows hold {V_mx, V_ca, V_my, V_cb}, register 2 rows
-// {V_cc, V_g, V_r, V_b}, and row 3 of register 3 holds S0 (see the backward
-// kernel for the values).  A row's destination is base + orig * stride floats.
-struct AtomicRole {
-  float* base1;
-  float* base2;
-  bool stride3;  // register 1 target has 3 floats per splat (else 2)
-  float scale1, scale2;
+// Orders this wavefront's LDS stores before its later LDS loads of other
+// lanes' data.  The backward's workgroup is one wavefront, so no s_barrier is
+// needed: the fences only keep the compiler from moving the accesses and wait
+// for the stores.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Gradient reduction of the backward walk.  Per splat each lane holds nine
+// partial sums over its pixels.  Eight of them (kGradQ quantities) go through
+// LDS: lane l stores quantity q at red[q][l], then the eight lanes of group q
+// (lanes 8q..8q+7) each add eight of its 64 values (two 16-byte loads) and
+// three DPP steps finish the group's total, which lane 8q adds atomically to
+// the splat's gradient.  The ninth, S0, is summed across the wavefront by
+// DPP.  LDS accesses issue on their own port, so the reduction costs few
+// vector-ALU slots, the compositor's bound.
+constexpr int kGradQ = 8;
+struct BwdShared {
+  Staged S;
+  float red[kGradQ * kLanes];
 };
 
-__device__ __forceinline__ AtomicRole atomic_role(float* g_means2d,
+// Where group q = lane / 8 sends its total: q = 0..7 is
+// {V_mx, V_my, V_ca, V_cb, V_cc, colour r, g, b} (see the backward walk),
+// added at base + orig * stride bytes after scaling.
+struct GradTarget {
+  float* base;
+  uint32_t stride;
+  float scale;
+};
+
+__device__ __forceinline__ GradTarget grad_target(float* g_means2d,
                                                   float* g_conics,
                                                   float* g_colors) {
-  // g_mean = -(2/L) V_m since a = -2A/L, b = -B/L, c = -2C/L.
+  // g_mean = -(2/L) V_m since a = -2A/L, b = -B/L, c = -2C/L;
+  // g_conic = (-V_ca/2, -V_cb, -V_cc/2).
   constexpr float kMeanScale = -2.0f / kLog2e;
-  AtomicRole r;
-  switch (threadIdx.x >> 4) {
-    case 0:
-      r.base1 = g_means2d + 0; r.stride3 = false; r.scale1 = kMeanScale;
-      r.base2 = g_conics + 2; r.scale2 = -0.5f;
-      break;
-    case 1:
-      r.base1 = g_conics + 0; r.stride3 = true; r.scale1 = -0.5f;
-      r.base2 = g_colors + 1; r.scale2 = 1.0f;
-      break;
-    case 2:
-      r.base1 = g_means2d + 1; r.stride3 = false; r.scale1 = kMeanScale;
-      r.base2 = g_colors + 0; r.scale2 = 1.0f;
-      break;
-    default:
-      r.base1 = g_conics + 1; r.stride3 = true; r.scale1 = -1.0f;
-      r.base2 = g_colors + 2; r.scale2 = 1.0f;
-      break;
+  switch (threadIdx.x >> 3) {
+    case 0: return {g_means2d + 0, 8, kMeanScale};
+    case 1: return {g_means2d + 1, 8, kMeanScale};
+    case 2: return {g_conics + 0, 12, -0.5f};
+    case 3: return {g_conics + 1, 12, -1.0f};
+    case 4: return {g_conics + 2, 12, -0.5f};
+    case 5: return {g_colors + 0, 12, 1.0f};
+    case 6: return {g_colors + 1, 12, 1.0f};
+    default: return {g_colors + 2, 12, 1.0f};
   }
-  return r;
 }
 
 // Per-pixel state of the backward walk (4 pixels per lane).
@@ -725,16 +728,37 @@ __device__ __forceinline__ void load_bwd_pixels(
   }
 }
 
+// True when some pixel of the wavefront lies outside the image or stopped
+// early in the forward (T <= transmittance threshold).  Otherwise every pixel
+// composited every splat visible to it, so a splat at index >= last is
+// invisible there and the walk can skip the index test (kCheckLast = false).
+__device__ __forceinline__ bool needs_last_test(const RasterParams& P,
+                                                const TileCoord& tc,
+                                                const BwdPixels& Q) {
+  const int x = tc.x0 + tc.lx;
+  bool need = false;
+#pragma unroll
+  for (int k = 0; k < kPix; ++k)
+    need |= (x >= P.width) | (slot_y(tc, k) >= P.height) |
+            !(Q.Tc[k] > P.trans_thr);
+  return __builtin_amdgcn_ballot_w64(need) != 0;
+}
+
 // Reverse walk over the tile-range indices [lo, hi): gradients of every
 // splat, reduced across the wavefront and added atomically in original order.
+template <bool kCheckLast>
 __device__ __forceinline__ void bwd_walk(
     const RasterParams& P, const float4* __restrict__ packed,
     const int32_t* __restrict__ binned, int start, int lo, int hi,
-    const TileCoord& tc, Staged& S, BwdPixels& Q, float* __restrict__ g_means2d,
-    float* __restrict__ g_conics, float* __restrict__ g_colors,
-    float* __restrict__ g_opac) {
-  const AtomicRole role = atomic_role(g_means2d, g_conics, g_colors);
-  const bool row_head = (threadIdx.x & 15) == 0;
+    const TileCoord& tc, BwdShared& SH, BwdPixels& Q,
+    float* __restrict__ g_means2d, float* __restrict__ g_conics,
+    float* __restrict__ g_colors, float* __restrict__ g_opac) {
+  Staged& S = SH.S;
+  const int lane = threadIdx.x;
+  const GradTarget target = grad_target(g_means2d, g_conics, g_colors);
+  const bool group_head = (lane & 7) == 0;
+  // this lane's eight values of its group's quantity in red
+  const float* red_in = SH.red + (lane >> 3) * kLanes + (lane & 7) * 8;
   const float max_alpha = fminf(P.max_alpha, 1.0f);
   // Per-lane partial sums of the current splat; zero between splats.
   float S0 = 0.f, S1 = 0.f, S2 = 0.f;
@@ -764,7 +788,7 @@ __device__ __forceinline__ void bwd_walk(
         const float dy = Q.py[k] - a0.y;
         const float p = splat_exponent(Adxdx, Bdx, a1.x, dy);
         {
-          if ((i < Q.lk[k]) & (p <= 0.0f) & (p >= a2.z)) {
+          if (((!kCheckLast) | (i < Q.lk[k])) & (p <= 0.0f) & (p >= a2.z)) {
             contrib = true;
             const float e = __builtin_amdgcn_exp2f(p);
             const float raw = a1.y * e;
@@ -781,7 +805,8 @@ __device__ __forceinline__ void bwd_walk(
             acc_r += Q.gr[k] * wgt;
             acc_g += Q.gg[k] * wgt;
             acc_b += Q.gb[k] * wgt;
-            const float g_pow = open ? (T_prev * diff) * raw : 0.0f;
+            // alpha = raw when the gate is open, so T_prev raw = wgt
+            const float g_pow = open ? wgt * diff : 0.0f;
             const float hdy = g_pow * dy;
             S0 += g_pow;
             S1 += hdy;
@@ -791,35 +816,39 @@ __device__ __forceinline__ void bwd_walk(
           }
         }
       }
-      if (__any(contrib)) {
+      if (__builtin_amdgcn_ballot_w64(contrib) != 0) {
         // Per-lane parts of the splat's gradients (a, b, c = -2A/L, -B/L,
         // -2C/L): g_mean = -(2/L) (V_mx, V_my), g_conic = (-V_ca/2, -V_cb,
         // -V_cc/2) with V_cc = S2, and g_opacity = sum g_raw exp(power) =
         // (sum g_power) / o = S0 / o.
         const float X = dx * S0;             // sum g_power dx
         const float hB = 0.5f * a0.w;
-        const float V_mx = a0.z * X + hB * S1;
-        const float V_my = hB * X + a1.x * S1;
-        const float V_ca = dx * X;           // sum g_power dx^2
-        const float V_cb = dx * S1;          // sum g_power dx dy
+        float* red_out = SH.red + lane;
+        red_out[0 * kLanes] = a0.z * X + hB * S1;  // V_mx
+        red_out[1 * kLanes] = hB * X + a1.x * S1;  // V_my
+        red_out[2 * kLanes] = dx * X;              // V_ca = sum g_power dx^2
+        red_out[3 * kLanes] = dx * S1;             // V_cb = sum g_power dx dy
+        red_out[4 * kLanes] = S2;
+        red_out[5 * kLanes] = acc_r;
+        red_out[6 * kLanes] = acc_g;
+        red_out[7 * kLanes] = acc_b;
         const float r3 = wave_sum_row3(S0);
-        const float r1 = wave_sum4(V_mx, V_my, V_ca, V_cb);
-        const float r2 = wave_sum4(S2, acc_r, acc_g, acc_b);
         S0 = S1 = S2 = 0.f;
         acc_r = acc_g = acc_b = 0.f;
-        if (row_head) {
-          const uint32_t orig = uniform_bits(a2.y);
-          const uint64_t off2 = (uint64_t)orig * 8u;   // bytes, 2 floats
-          const uint64_t off3 = (uint64_t)orig * 12u;  // bytes, 3 floats
-          float* p1 = reinterpret_cast<float*>(
-              reinterpret_cast<char*>(role.base1) + (role.stride3 ? off3 : off2));
-          float* p2 = reinterpret_cast<float*>(
-              reinterpret_cast<char*>(role.base2) + off3);
-          unsafeAtomicAdd(p1, r1 * role.scale1);
-          unsafeAtomicAdd(p2, r2 * role.scale2);
-          if (threadIdx.x == 48)
-            unsafeAtomicAdd(g_opac + orig, r3 * a2.w);  // a2.w = 1 / opacity
-        }
+        wave_lds_sync();
+        const float4 u = *reinterpret_cast<const float4*>(red_in);
+        const float4 w = *reinterpret_cast<const float4*>(red_in + 4);
+        const float tot = group8_sum_dpp(((u.x + u.y) + (u.z + u.w)) +
+                                         ((w.x + w.y) + (w.z + w.w)));
+        const uint32_t orig = uniform_bits(a2.y);
+        if (group_head)
+          unsafeAtomicAdd(reinterpret_cast<float*>(
+                              reinterpret_cast<char*>(target.base) +
+                              (uint64_t)orig * target.stride),
+                          tot * target.scale);
+        if (lane == kLanes - 1)
+          unsafeAtomicAdd(g_opac + orig, r3 * a2.w);  // a2.w = 1 / opacity
+        wave_lds_sync();  // loads done before the next splat's stores
       }
     }
   }
@@ -860,7 +889,7 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
     const float* __restrict__ grad_rgb, float* __restrict__ g_means2d,
     float* __restrict__ g_conics, float* __restrict__ g_colors,
     float* __restrict__ g_opac, HeavyState H, int seg_blocks) {
-  __shared__ Staged S;
+  __shared__ BwdShared SH;
   const int bid = (int)blockIdx.x;
   const bool seg = bid < seg_blocks;
   const int m = bid;
@@ -913,8 +942,14 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
         }
       }
     }
-    bwd_walk(P, packed, binned, tile_offsets[tile], lo, hi, tc, S, Q,
-             g_means2d, g_conics, g_colors, g_opac);
+    // Q.Tc holds T_final, or T at the segment's end for pixels alive past it
+    // (T_end > T_final > threshold), so the test sees the final state.
+    if (needs_last_test(P, tc, Q))
+      bwd_walk<true>(P, packed, binned, tile_offsets[tile], lo, hi, tc, SH, Q,
+                     g_means2d, g_conics, g_colors, g_opac);
+    else
+      bwd_walk<false>(P, packed, binned, tile_offsets[tile], lo, hi, tc, SH, Q,
+                      g_means2d, g_conics, g_colors, g_opac);
   }
 }
 
