@@ -218,3 +218,27 @@ def test_binning_capacity_too_small(gpu):
             assert np.isin(full, have).all()
         st2 = _ops.bin_gaussians(meta, *flat)
         _assert_bins_equal(st2, ob, sc, B, G)
+
+
+@pytest.mark.parametrize("B,G", [(3, 70_001), (1, 4_200_001)])
+def test_depth_order_segments_and_large(gpu, B, G):
+    """Stable depth order of bin_depth_order (torch.argsort(stable=True) semantics: ties by index,
+    -0.0 == +0.0) for several images of 1024-element workgroups and for 4.2M splats in one image
+    (4096-element workgroups, more of them than the device holds at once)."""
+    print(f"depth order B={B} G={G}", flush=True)
+    rng = np.random.default_rng(G)
+    d = rng.uniform(0.1, 10.0, size=(B, G)).astype(np.float32)
+    d[:, ::7] = d[:, 3:4]          # ties keep index order
+    d[:, 5] = -0.0
+    d[:, 6] = 0.0
+    meta = _lib.make_raster_meta(64, 64, B, G, 1.0 / 255.0, 1e-4, (0.0, 0.0, 0.0))
+    L = _lib.lib()
+    wsb = L.gsplat_hip_bin_count_workspace_bytes(meta)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    dd = torch.from_numpy(d).to(gpu)
+    perm = torch.empty(B * G, dtype=torch.int32, device=gpu)
+    _lib.check(L.gsplat_hip_bin_depth_order(meta, _lib.ptr(dd), _lib.ptr(perm), _lib.ptr(ws), wsb,
+                                            _lib.stream_of(dd)), "gsplat_hip_bin_depth_order")
+    got = perm.cpu().numpy().reshape(B, G)
+    for b in range(B):
+        np.testing.assert_array_equal(got[b], np.argsort(d[b], kind="stable"))
