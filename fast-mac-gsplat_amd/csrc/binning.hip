@@ -43,19 +43,34 @@ struct SplatGeom {
 
 constexpr int kWaves = kThreads / 64;
 
-// One wavefront's 64 splats, staged for the cooperative tile walk.
+// Splats per wavefront in the tile walk.  A wavefront's 64 lanes test the
+// candidates of kWalkSplats splats together; fewer splats per wavefront
+// than lanes gives each launch more wavefronts (the walk is latency bound)
+// and a shorter slot search.
+constexpr int kWalkSplats = 32;
+constexpr int kWalkBlockSplats = kWaves * kWalkSplats;
+
+// One wavefront's kWalkSplats splats, staged for the cooperative tile walk.
 struct WalkSlots {
-  float4 g0[64];  // mx, my, a, b
-  float4 g1[64];  // c, tau, kc, ka
-  int4 box[64];   // tx0, ty0, tiles per bbox row, first tile of the image
-  int flags[64];  // bit 0: use_c, bit 1: use_a
-  int cend[64];   // inclusive prefix sum of candidate counts
-  int cnt[64];    // hits found so far
+  float4 g0[kWalkSplats];  // mx, my, a, b
+  float4 g1[kWalkSplats];  // c, tau, kc, ka
+  int4 box[kWalkSplats];   // tx0, ty0, tiles per bbox row, first tile of the image
+  int flags[kWalkSplats];  // bit 0: use_c, bit 1: use_a
+  int cend[kWalkSplats];   // inclusive prefix sum of candidate counts
+  int cnt[kWalkSplats];    // hits found so far
 };
 
-// Stages this lane's splat and returns the wavefront's candidate total.
-// Candidate counts fit in int32: tiles per image are limited to 2^24 on the
-// host, so a wavefront has at most 2^30 candidates.
+// Index of this thread's splat in the walk order of count / emit: lanes
+// 0..kWalkSplats-1 of each wavefront take consecutive splats.
+__device__ __forceinline__ int walk_splat_index() {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  return ((int)blockIdx.x * kWaves + wave) * kWalkSplats + lane;
+}
+
+// Stages this lane's splat (lanes below kWalkSplats) and returns the
+// wavefront's candidate total.  Candidate counts fit in int32: tiles per
+// image are limited to 2^24 on the host, so a wavefront has at most 2^28
+// candidates.
 __device__ __forceinline__ int walk_setup(const RasterParams& P, bool valid,
                                           const SplatGeom& s, int batch,
                                           WalkSlots& W) {
@@ -79,24 +94,26 @@ __device__ __forceinline__ int walk_setup(const RasterParams& P, bool valid,
       flags = (k.use_c ? 1 : 0) | (k.use_a ? 2 : 0);
     }
   }
-  W.g0[lane] = make_float4(s.mx, s.my, s.a, s.b);
-  W.g1[lane] = g1;
-  W.box[lane] = box;
-  W.flags[lane] = flags;
-  W.cnt[lane] = 0;
   int inc = ncand;
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
+  for (int off = 1; off < kWalkSplats; off <<= 1) {
     const int y = __shfl_up(inc, off, 64);
     if (lane >= off) inc += y;
   }
-  W.cend[lane] = inc;
+  if (lane < kWalkSplats) {
+    W.g0[lane] = make_float4(s.mx, s.my, s.a, s.b);
+    W.g1[lane] = g1;
+    W.box[lane] = box;
+    W.flags[lane] = flags;
+    W.cnt[lane] = 0;
+    W.cend[lane] = inc;
+  }
   __builtin_amdgcn_wave_barrier();
-  return __shfl(inc, 63, 64);
+  return __shfl(inc, kWalkSplats - 1, 64);
 }
 
 // Tests the wavefront's candidates 64 at a time and calls on_hit(slot, tile)
-// for every hit (slot = 0..63, the splat's lane in walk_setup).
+// for every hit (slot = 0..kWalkSplats-1, the splat's lane in walk_setup).
 template <typename Fn>
 __device__ __forceinline__ void walk_candidates(const RasterParams& P,
                                                 const WalkSlots& W, int total,
@@ -109,7 +126,7 @@ __device__ __forceinline__ void walk_candidates(const RasterParams& P,
       // first slot whose inclusive prefix exceeds c
       int sl = 0;
 #pragma unroll
-      for (int step = 32; step > 0; step >>= 1)
+      for (int step = kWalkSplats / 2; step > 0; step >>= 1)
         if (W.cend[sl + step - 1] <= c) sl += step;
       const int k = c - (sl == 0 ? 0 : W.cend[sl - 1]);
       const int4 bx = W.box[sl];
@@ -145,8 +162,8 @@ __global__ __launch_bounds__(kThreads) void count_kernel(
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_zero_words;
        i += (int64_t)gridDim.x * kThreads)
     zero_words[i] = 0u;
-  const int orig = blockIdx.x * kThreads + threadIdx.x;
-  const bool valid = orig < P.num_splats;
+  const int orig = walk_splat_index();
+  const bool valid = lane < kWalkSplats && orig < P.num_splats;
   const int o = valid ? orig : P.num_splats - 1;
   SplatGeom s;
   s.mx = means2d[2 * o + 0];
@@ -179,8 +196,17 @@ __global__ __launch_bounds__(kThreads) void count_kernel(
 __global__ __launch_bounds__(kThreads) void sum_kernel(
     const int32_t* __restrict__ block_sums, int n, int32_t* pair_count) {
   __shared__ long long part[kThreads];
+  // eight independent loads in flight per thread
+  long long acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int i = threadIdx.x;
+  for (; i + 7 * kThreads < n; i += 8 * kThreads) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] += block_sums[i + u * kThreads];
+  }
+  for (; i < n; i += kThreads) acc[0] += block_sums[i];
   long long v = 0;
-  for (int i = threadIdx.x; i < n; i += kThreads) v += block_sums[i];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) v += acc[u];
   part[threadIdx.x] = v;
   __syncthreads();
   for (int half = kThreads / 2; half > 0; half >>= 1) {
@@ -274,7 +300,7 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
     uint32_t* __restrict__ hist_partials, uint32_t* pair_status,
     int64_t pair_status_words) {
   __shared__ WalkSlots walk[kWaves];
-  __shared__ int base[kWaves][64];
+  __shared__ int base[kWaves][kWalkSplats];
   __shared__ uint32_t h[4][256];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   // (1) zero the pair sort's look-back status (grid-stride)
@@ -284,18 +310,18 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
   for (int i = t; i < 4 * 256; i += kThreads) (&h[0][0])[i] = 0u;
   __syncthreads();
   // (2) pair emission
-  const int gid = blockIdx.x * kThreads + t;
-  const bool valid = gid < P.num_splats;
+  const int gid = walk_splat_index();
+  const bool valid = lane < kWalkSplats && gid < P.num_splats;
   const int g = valid ? gid : P.num_splats - 1;
   const float4 p0 = packed[3 * g + 0];
   const float4 p1 = packed[3 * g + 1];
   const SplatGeom s{p0.x, p0.y, p0.z, p0.w, p1.x, p1.y};
-  base[wave][lane] = splat_offsets[g];
+  if (lane < kWalkSplats) base[wave][lane] = splat_offsets[g];
   const int64_t n_eff =
       min(capacity, (int64_t)max(splat_offsets[P.num_splats], 0));
   WalkSlots& W = walk[wave];
   const int total = walk_setup(P, valid, s, g / P.gpb, W);
-  const int gid0 = blockIdx.x * kThreads + wave * 64;
+  const int gid0 = gid - lane;
   walk_candidates(P, W, total, [&](int sl, int tile) {
     const int slot = atomicAdd(&W.cnt[sl], 1);
     const int64_t pos = (int64_t)base[wave][sl] + slot;
@@ -320,8 +346,17 @@ __global__ __launch_bounds__(kThreads) void hist_reduce_kernel(
     uint32_t* __restrict__ ghist) {
   __shared__ uint32_t part[kThreads / 64];
   const uint32_t* row = hist_partials + (int64_t)blockIdx.x * nblk;
+  // eight independent loads in flight per thread
+  uint32_t acc[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  int b = threadIdx.x;
+  for (; b + 7 * kThreads < nblk; b += 8 * kThreads) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] += row[b + u * kThreads];
+  }
+  for (; b < nblk; b += kThreads) acc[0] += row[b];
   uint32_t v = 0u;
-  for (int b = threadIdx.x; b < nblk; b += kThreads) v += row[b];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) v += acc[u];
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
@@ -393,7 +428,7 @@ __global__ void zero_grads_kernel(float* g_m, float* g_q, float* g_c,
 }  // namespace
 
 int count_blocks(const RasterParams& P) {
-  return (P.num_splats + kThreads - 1) / kThreads;
+  return (P.num_splats + kWalkBlockSplats - 1) / kWalkBlockSplats;
 }
 
 int launch_count(const RasterParams& P, const float* means2d,
@@ -432,7 +467,7 @@ int count_scan_blocks(const RasterParams& P) {
 }
 
 int emit_blocks(const RasterParams& P) {
-  return (P.num_splats + kThreads - 1) / kThreads;
+  return (P.num_splats + kWalkBlockSplats - 1) / kWalkBlockSplats;
 }
 
 int launch_emit(const RasterParams& P, const float* packed,
