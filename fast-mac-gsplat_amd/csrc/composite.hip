@@ -475,12 +475,13 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     if (valid[k]) {
       const int64_t pix =
           ((int64_t)tc.batch * P.height + slot_y(tc, k)) * P.width + x;
-      out_rgb[3 * pix + 0] = cr[k] + T[k] * P.bg_r;
-      out_rgb[3 * pix + 1] = cg[k] + T[k] * P.bg_g;
-      out_rgb[3 * pix + 2] = cb[k] + T[k] * P.bg_b;
+      // streaming stores: the per-pixel outputs are not read again here
+      __builtin_nontemporal_store(cr[k] + T[k] * P.bg_r, out_rgb + 3 * pix + 0);
+      __builtin_nontemporal_store(cg[k] + T[k] * P.bg_g, out_rgb + 3 * pix + 1);
+      __builtin_nontemporal_store(cb[k] + T[k] * P.bg_b, out_rgb + 3 * pix + 2);
       if (out_T) {
-        out_T[pix] = T[k];
-        out_last[pix] = last[k];
+        __builtin_nontemporal_store(T[k], out_T + pix);
+        __builtin_nontemporal_store(last[k], out_last + pix);
       }
       tile_max = max(tile_max, last[k]);
     }
@@ -714,11 +715,12 @@ __device__ __forceinline__ void load_bwd_pixels(
     Q.py[k] = (float)y + 0.5f;
     if (valid) {
       const int64_t pix = ((int64_t)tc.batch * P.height + y) * P.width + x;
-      Q.gr[k] = grad_rgb[3 * pix + 0];
-      Q.gg[k] = grad_rgb[3 * pix + 1];
-      Q.gb[k] = grad_rgb[3 * pix + 2];
-      Q.Tc[k] = final_T[pix];
-      Q.lk[k] = last_in[pix];
+      // streaming loads: each pixel's state is read once
+      Q.gr[k] = __builtin_nontemporal_load(grad_rgb + 3 * pix + 0);
+      Q.gg[k] = __builtin_nontemporal_load(grad_rgb + 3 * pix + 1);
+      Q.gb[k] = __builtin_nontemporal_load(grad_rgb + 3 * pix + 2);
+      Q.Tc[k] = __builtin_nontemporal_load(final_T + pix);
+      Q.lk[k] = __builtin_nontemporal_load(last_in + pix);
     } else {
       Q.gr[k] = Q.gg[k] = Q.gb[k] = 0.0f;
       Q.Tc[k] = 1.0f;
