@@ -759,8 +759,10 @@ __device__ __forceinline__ void bwd_walk(
   const int lane = threadIdx.x;
   const GradTarget target = grad_target(g_means2d, g_conics, g_colors);
   const bool group_head = (lane & 7) == 0;
-  // this lane's eight values of its group's quantity in red
-  const float* red_in = SH.red + (lane >> 3) * kLanes + (lane & 7) * 8;
+  // this lane's eight values of its group's quantity in red: 16-byte chunks
+  // l and l + 8 of the row (l = lane % 8), so that the eight lanes of a
+  // group read 128 consecutive bytes per load (no bank conflict)
+  const float* red_in = SH.red + (lane >> 3) * kLanes + (lane & 7) * 4;
   const float max_alpha = fminf(P.max_alpha, 1.0f);
   // Per-lane partial sums of the current splat; zero between splats.
   float S0 = 0.f, S1 = 0.f, S2 = 0.f;
@@ -839,7 +841,7 @@ __device__ __forceinline__ void bwd_walk(
         acc_r = acc_g = acc_b = 0.f;
         wave_lds_sync();
         const float4 u = *reinterpret_cast<const float4*>(red_in);
-        const float4 w = *reinterpret_cast<const float4*>(red_in + 4);
+        const float4 w = *reinterpret_cast<const float4*>(red_in + 32);
         const float tot = group8_sum_dpp(((u.x + u.y) + (u.z + u.w)) +
                                          ((w.x + w.y) + (w.z + w.w)));
         const uint32_t orig = uniform_bits(a2.y);
