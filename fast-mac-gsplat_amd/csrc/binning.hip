@@ -49,6 +49,9 @@ constexpr int kWaves = kThreads / 64;
 // and a shorter slot search.
 constexpr int kWalkSplats = 32;
 constexpr int kWalkBlockSplats = kWaves * kWalkSplats;
+// Emit launches with at most this many workgroups add their pair-sort
+// histograms atomically instead of through hist_reduce_kernel.
+constexpr int kDirectHistBlocks = 1024;
 
 // One wavefront's kWalkSplats splats, staged for the cooperative tile walk.
 struct WalkSlots {
@@ -297,7 +300,8 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ splat_offsets, int64_t capacity,
     uint32_t* __restrict__ keys, uint32_t* __restrict__ vals, int pair_passes,
-    uint32_t* __restrict__ hist_partials, uint32_t* pair_status,
+    uint32_t* __restrict__ hist_partials, uint32_t* ghist_direct,
+    uint32_t* pair_status,
     int64_t pair_status_words) {
   __shared__ WalkSlots walk[kWaves];
   __shared__ int base[kWaves][kWalkSplats];
@@ -332,11 +336,18 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
         atomicAdd(&h[p][((uint32_t)tile >> (8 * p)) & 255u], 1u);
     }
   });
-  // (3) this workgroup's digit histograms for the pair sort, stored as
-  // hist_partials[(p * 256 + d) * nblk + workgroup]
+  // (3) this workgroup's digit histograms for the pair sort: added to the
+  // zeroed global histograms (ghist_direct, few workgroups) or stored as
+  // hist_partials[(p * 256 + d) * nblk + workgroup] for hist_reduce_kernel
   __syncthreads();
-  for (int p = 0; p < pair_passes; ++p)
-    hist_partials[((int64_t)p * 256 + t) * gridDim.x + blockIdx.x] = h[p][t];
+  for (int p = 0; p < pair_passes; ++p) {
+    const uint32_t c = h[p][t];
+    if (ghist_direct != nullptr) {
+      if (c) atomicAdd(&ghist_direct[p * 256 + t], c);
+    } else {
+      hist_partials[((int64_t)p * 256 + t) * gridDim.x + blockIdx.x] = c;
+    }
+  }
 }
 
 // ghist[p][d] = sum over the emit workgroups of their digit-d counts of pass
@@ -477,12 +488,16 @@ int launch_emit(const RasterParams& P, const float* packed,
                 int64_t pair_status_words, hipStream_t stream) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const int nblk = emit_blocks(P);
+  // Few workgroups add their histograms atomically (pair_ghist is zeroed
+  // by count_kernel), which saves the reduction launch; many would contend.
+  const bool direct = nblk <= kDirectHistBlocks;
   hipLaunchKernelGGL(emit_kernel, dim3((unsigned)nblk), dim3(kThreads), 0,
                      stream, P, reinterpret_cast<const float4*>(packed),
                      splat_offsets, capacity, keys, vals, pair_passes,
-                     hist_partials, pair_status, pair_status_words);
+                     hist_partials, direct ? pair_ghist : nullptr,
+                     pair_status, pair_status_words);
   int rc = check_launch("emit_kernel");
-  if (rc || pair_passes == 0) return rc;
+  if (rc || pair_passes == 0 || direct) return rc;
   hipLaunchKernelGGL(hist_reduce_kernel, dim3((unsigned)(pair_passes * 256)),
                      dim3(kThreads), 0, stream, hist_partials, nblk,
                      pair_ghist);

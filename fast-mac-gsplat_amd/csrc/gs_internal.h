@@ -107,9 +107,9 @@ int launch_pack(const RasterParams& P, const float* means2d,
                 uint32_t* scan_ticket, hipStream_t stream);
 int count_scan_blocks(const RasterParams& P);
 // emit: writes the (tile, gid) pairs into each splat's range, zeroes
-// pair_status, and fills pair_ghist ([pair_passes][256]) with the pair sort's
-// digit histograms via per-workgroup partials (emit_blocks(P) * 4 * 256
-// words).  Only the first min(N, capacity) pairs are written and counted,
+// pair_status, and fills pair_ghist ([pair_passes][256], zero on entry) with
+// the pair sort's digit histograms, atomically or via per-workgroup partials
+// (emit_blocks(P) * 4 * 256 words) and a reduction launch.  Only the first min(N, capacity) pairs are written and counted,
 // N = splat_offsets[num_splats] (-1 when N overflowed: nothing is written).
 int emit_blocks(const RasterParams& P);
 int launch_emit(const RasterParams& P, const float* packed,
