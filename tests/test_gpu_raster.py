@@ -218,7 +218,9 @@ def test_forward_rebins_when_pairs_exceed_capacity(gpu):
     (ev0, img0, g0), (ev1, img1, g1) = results
     assert torch.equal(ev0, ev1) and torch.equal(img0, img1) and torch.equal(ev0, img0)
     for a, b in zip(g0, g1):
-        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-7)
+        # equal up to the order of the float atomics (cancellation makes single sums differ in the
+        # fifth digit)
+        torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-6)
 
 
 def test_unbatched_matches_batched(gpu):
