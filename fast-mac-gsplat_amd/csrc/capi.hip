@@ -107,6 +107,13 @@ int make_params(const gsplat_raster_meta* m, RasterParams& P) {
   return GSPLAT_OK;
 }
 
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return GSPLAT_OK;
+  (void)hipGetLastError();
+  gs::set_error("%s: %s", what, hipGetErrorString(e));
+  return GSPLAT_ERR_HIP;
+}
+
 int null_check(std::initializer_list<const void*> ptrs, const char* what) {
   for (const void* p : ptrs) {
     if (p == nullptr) {
@@ -359,6 +366,89 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
     rc = gs::launch_tile_ranges(sorted_keys, n_pairs, P.num_tiles,
                                 tile_offsets, tile_counts, s, n_dev);
   return rc;
+}
+
+size_t gsplat_hip_bin_workspace_bytes(const gsplat_raster_meta* meta,
+                                      int64_t capacity) {
+  RasterParams P;
+  if (make_params(meta, P) || capacity < 0) return 0;
+  return 256 + gs::align_up(count_layout(P).total, 256) +
+         emit_layout(P, capacity).total;
+}
+
+int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
+                   const float* conics, const float* colors,
+                   const float* opacities, const float* depths,
+                   int64_t capacity, int32_t* perm, float* packed,
+                   int32_t* splat_offsets, int32_t* binned_ids,
+                   int32_t* tile_offsets, int32_t* pair_count_host,
+                   void* workspace, size_t workspace_bytes, void* stream,
+                   void* count_stream, void* inputs_event,
+                   void* count_event) {
+  RasterParams P;
+  int rc = make_params(meta, P);
+  if (rc) return rc;
+  if (capacity < 0 || capacity > 0x7fffffffLL) {
+    gs::set_error("gsplat_hip_bin: invalid capacity %lld", (long long)capacity);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  rc = null_check({means2d, conics, colors, opacities, depths, perm, packed,
+                   splat_offsets, tile_offsets, workspace},
+                  "gsplat_hip_bin");
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipStream_t cs = count_stream ? static_cast<hipStream_t>(count_stream) : s;
+  if (cs != s && (inputs_event == nullptr || count_event == nullptr)) {
+    gs::set_error("gsplat_hip_bin: a count stream needs both events");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  const size_t cbytes = gs::align_up(count_layout(P).total, 256);
+  const size_t need = gsplat_hip_bin_workspace_bytes(meta, capacity);
+  if (workspace_bytes < need) {
+    gs::set_error("gsplat_hip_bin: workspace too small (%zu < %zu)",
+                  workspace_bytes, need);
+    return GSPLAT_ERR_WORKSPACE;
+  }
+  char* base = static_cast<char*>(workspace);
+  int32_t* n_dev = reinterpret_cast<int32_t*>(base);
+  void* cws = base + 256;
+  void* ews = base + 256 + cbytes;
+  const size_t ebytes = workspace_bytes - 256 - cbytes;
+  hipEvent_t ev_in = static_cast<hipEvent_t>(inputs_event);
+  hipEvent_t ev_n = static_cast<hipEvent_t>(count_event);
+  // 1. per-splat hit counts and N on the count stream (after the caller's
+  //    work on `stream`), N copied to the host
+  if (cs != s) {
+    rc = hip_status(hipEventRecord(ev_in, s), "gsplat_hip_bin: event record");
+    if (!rc)
+      rc = hip_status(hipStreamWaitEvent(cs, ev_in, 0),
+                      "gsplat_hip_bin: stream wait");
+    if (rc) return rc;
+  }
+  rc = gsplat_hip_bin_count(meta, means2d, conics, opacities, n_dev, cws,
+                            cbytes, cs);
+  if (!rc && pair_count_host != nullptr)
+    rc = hip_status(hipMemcpyAsync(pair_count_host, n_dev, sizeof(int32_t),
+                                   hipMemcpyDeviceToHost, cs),
+                    "gsplat_hip_bin: pair count copy");
+  if (!rc && ev_n != nullptr)
+    rc = hip_status(hipEventRecord(ev_n, cs), "gsplat_hip_bin: event record");
+  if (rc) return rc;
+  // 2. stable depth order on `stream`, concurrently with the count
+  rc = gsplat_hip_bin_depth_order(meta, depths, perm, cws, cbytes, s);
+  if (rc) return rc;
+  if (cs != s) {
+    rc = hip_status(hipStreamWaitEvent(s, ev_n, 0),
+                    "gsplat_hip_bin: stream wait");
+    if (rc) return rc;
+  }
+  // 3. records and offsets, 4. pairs, pair sort and tile ranges
+  rc = gsplat_hip_bin_pack(meta, means2d, conics, colors, opacities, perm,
+                           packed, splat_offsets, cws, cbytes, s);
+  if (rc) return rc;
+  return gsplat_hip_bin_emit(meta, packed, splat_offsets, capacity,
+                             binned_ids, nullptr, tile_offsets, cws, cbytes,
+                             ews, ebytes, s);
 }
 
 int gsplat_hip_render_forward(const gsplat_raster_meta* meta,

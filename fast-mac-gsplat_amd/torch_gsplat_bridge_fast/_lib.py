@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("GSPLAT_HIP_LIB", os.path.join(_HERE, "lib", "libgsplat_hip.so"))
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 TILE_SIZE = 16
 RECORD_FLOATS = 12
 
@@ -67,6 +67,8 @@ SIGNATURES = {
     "gsplat_hip_bin_pack": (ctypes.c_int, [_PM] + [_vp] * 7 + [_vp, _sz, _vp]),
     "gsplat_hip_bin_emit_workspace_bytes": (_sz, [_PM, _i64]),
     "gsplat_hip_bin_emit": (ctypes.c_int, [_PM, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _vp]),
+    "gsplat_hip_bin_workspace_bytes": (_sz, [_PM, _i64]),
+    "gsplat_hip_bin": (ctypes.c_int, [_PM] + [_vp] * 5 + [_i64] + [_vp] * 7 + [_sz] + [_vp] * 4),
     "gsplat_hip_render_workspace_bytes": (_sz, [_PM, _i64]),
     "gsplat_hip_render_forward": (ctypes.c_int, [_PM] + [_vp] * 7 + [_i64, _vp, _sz, _vp]),
     "gsplat_hip_render_backward": (ctypes.c_int, [_PM] + [_vp] * 11 + [_i64, _vp, _sz, _vp]),

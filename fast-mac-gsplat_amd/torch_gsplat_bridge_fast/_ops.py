@@ -93,17 +93,18 @@ class BinState:
     tile_offsets: Tensor            # int32 [T+1]
     pairs: Tensor                   # int32 [capacity]; the first N entries are the binned gids
     capacity: int                   # pair capacity the buffers and workspaces were sized for
-    _n_host: Optional[Tensor] = None                 # pinned int32 [1]: N once _n_ready completes
+    _n_host: Optional[Tensor] = None                 # pinned int32: N at _n_slot once _n_ready completes
     _n_ready: Optional[torch.cuda.Event] = None
     _n: Optional[int] = None
     _key: Optional[tuple] = None
+    _n_slot: int = 0
 
     @property
     def n_pairs(self) -> int:
         """The pair count N (waits for the count stage, which ran first on the GPU)."""
         if self._n is None:
             self._n_ready.synchronize()
-            self._n = int(self._n_host[0])
+            self._n = int(self._n_host[self._n_slot])
         return self._n
 
     def confirm(self) -> bool:
@@ -184,8 +185,68 @@ def bin_and_render(meta: _lib.RasterMeta, flat, *, save_state: bool):
     return st, out
 
 
+class _DeviceBinState:
+    """Per-device objects reused by every binning call: the two ordering events of gsplat_hip_bin
+    (re-recording them is safe: a stream wait takes the event's state when it is enqueued, and a
+    host wait on a later recording of the count event also covers the earlier copies) and a ring
+    of pinned words for the pair counts."""
+    RING = 64
+
+    def __init__(self, device: torch.device):
+        main = torch.cuda.current_stream(device)
+        self.inputs = torch.cuda.Event()
+        self.count = torch.cuda.Event()
+        for e in (self.inputs, self.count):
+            e.record(main)      # creates the HIP event
+        self.ring = torch.zeros((self.RING,), dtype=torch.int32, pin_memory=True)
+        self.next = 0
+
+    def slot(self) -> int:
+        i = self.next
+        self.next = (i + 1) % self.RING
+        return i
+
+
+_device_bin: dict = {}
+
+
+def _bin_fast(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
+              opacities: Tensor, depths: Tensor, cap: int, key: tuple) -> BinState:
+    """All of binning in one C-ABI call (gsplat_hip_bin) with buffers of the known capacity."""
+    L = _lib.lib()
+    dev = means2d.device
+    B, G = meta.batch, meta.gaussians_per_batch
+    BG = B * G
+    tiles = B * ((meta.height + 15) // 16) * ((meta.width + 15) // 16)
+    d = _device_bin.get(dev.index)
+    if d is None:
+        d = _device_bin[dev.index] = _DeviceBinState(dev)
+    perm = _empty(BG, torch.int32, dev)
+    packed = torch.empty((BG, _lib.RECORD_FLOATS), dtype=torch.float32, device=dev)
+    splat_offsets = _empty(BG + 1, torch.int32, dev)
+    tile_offsets = _empty(tiles + 1, torch.int32, dev)
+    pairs = _empty(cap, torch.int32, dev)
+    ws_bytes = L.gsplat_hip_bin_workspace_bytes(meta, cap)
+    ws = _empty(max(ws_bytes, 1), torch.uint8, dev)
+    slot = d.slot()
+    check(L.gsplat_hip_bin(meta, ptr(means2d), ptr(conics), ptr(colors), ptr(opacities), ptr(depths), cap,
+                           ptr(perm), ptr(packed), ptr(splat_offsets), ptr(pairs), ptr(tile_offsets),
+                           d.ring.data_ptr() + 4 * slot, ptr(ws), ws_bytes,
+                           torch.cuda.current_stream(dev).cuda_stream, _side_stream(dev).cuda_stream,
+                           d.inputs.cuda_event, d.count.cuda_event),
+          "gsplat_hip_bin")
+    return BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, d.ring, d.count, None, key, slot)
+
+
 def _bin(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
          opacities: Tensor, depths: Tensor) -> BinState:
+    dev = means2d.device
+    key = (dev.index, meta.batch, meta.gaussians_per_batch, meta.height, meta.width)
+    cap = _capacity.get(key)
+    staged = _timing is not None and (_timing_ops is None or
+                                      bool(_timing_ops & {"bin_count", "bin_pack", "bin_emit"}))
+    if cap is not None and not staged:
+        return _bin_fast(meta, means2d, conics, colors, opacities, depths, cap, key)
     L = _lib.lib()
     dev = means2d.device
     B, G = meta.batch, meta.gaussians_per_batch
@@ -219,8 +280,6 @@ def _bin(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
         check(L.gsplat_hip_bin_pack(meta, ptr(means2d), ptr(conics), ptr(colors), ptr(opacities), ptr(perm),
                                     ptr(packed), ptr(splat_offsets), ptr(ws), ws_bytes, s),
               "gsplat_hip_bin_pack")
-    key = (dev.index, B, G, meta.height, meta.width)
-    cap = _capacity.get(key)
     n_known = None
     if cap is None:
         # first binning of this shape: size the buffers from N itself

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 6
+#define GSPLAT_HIP_ABI_VERSION 7
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -165,6 +165,30 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
                         int32_t* tile_offsets,
                         void* count_workspace, size_t count_workspace_bytes,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* All four binning calls in one: bin_count on count_stream (NULL: `stream`),
+ * ordered after the work already enqueued on `stream` through inputs_event;
+ * N copied to the pinned host word *pair_count_host (may be NULL) on
+ * count_stream, after which count_event is recorded; bin_depth_order on
+ * `stream` concurrently; then bin_pack (after count_event) and bin_emit with
+ * the pair capacity `capacity` (see bin_emit: n_pairs).  The events are the
+ * caller's (hipEvent_t, required when count_stream differs from stream); the
+ * caller waits for count_event before reading *pair_count_host.  Outputs as
+ * bin_depth_order (perm), bin_pack (packed, splat_offsets) and bin_emit
+ * (binned_ids [capacity], tile_offsets).  One call instead of four keeps the
+ * host's per-step launch overhead small; it replaces the same reference
+ * steps as the four calls. */
+size_t gsplat_hip_bin_workspace_bytes(const gsplat_raster_meta* meta,
+                                      int64_t capacity);
+int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
+                   const float* conics, const float* colors,
+                   const float* opacities, const float* depths,
+                   int64_t capacity, int32_t* perm, float* packed,
+                   int32_t* splat_offsets, int32_t* binned_ids,
+                   int32_t* tile_offsets, int32_t* pair_count_host,
+                   void* workspace, size_t workspace_bytes, void* stream,
+                   void* count_stream, void* inputs_event,
+                   void* count_event);
 
 /* -------------------------------------------------------------- composite
  * Compositor workspace (optional; n_pairs is the N of the binning).  With it

@@ -30,7 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 6
+    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 7
 
 
 def _meta(**kw):
@@ -136,3 +136,21 @@ def test_pair_capacity_policy():
     with pytest.raises(RuntimeError, match="overflowed"):
         st.confirm()
     _ops._capacity.pop(key, None)
+
+
+def test_one_call_binning_validation():
+    """gsplat_hip_bin checks its arguments before launching: NULL inputs, a negative capacity, a count
+    stream without events, a short workspace."""
+    L = _lib.lib()
+    one = ctypes.c_void_p(1)
+    m = _meta()
+    need = L.gsplat_hip_bin_workspace_bytes(m, 1000)
+    assert need > L.gsplat_hip_bin_workspace_bytes(m, 10) > 0
+    rc = L.gsplat_hip_bin(m, *([None] * 5), 10, *([one] * 7), need, None, None, None, None)
+    assert rc == 1 and "NULL" in L.gsplat_hip_last_error().decode()
+    rc = L.gsplat_hip_bin(m, *([one] * 5), -1, *([one] * 7), need, None, None, None, None)
+    assert rc == 1 and "capacity" in L.gsplat_hip_last_error().decode()
+    rc = L.gsplat_hip_bin(m, *([one] * 5), 1000, *([one] * 7), need, one, ctypes.c_void_p(2), None, None)
+    assert rc == 1 and "events" in L.gsplat_hip_last_error().decode()
+    rc = L.gsplat_hip_bin(m, *([one] * 5), 1000, *([one] * 7), need - 1, None, None, None, None)
+    assert rc == 3 and "workspace" in L.gsplat_hip_last_error().decode()
