@@ -188,6 +188,24 @@ __device__ __forceinline__ uint32_t uniform_bits(float v) {
   return __builtin_amdgcn_readfirstlane(__float_as_uint(v));
 }
 
+// Maximum of a non-negative int over the 64 lanes, valid in lanes 48..63:
+// DPP steps within each 16-lane row (quad_perm [1,0,3,2], [2,3,0,1],
+// row_half_mirror, row_mirror), then row_bcast:15 and row_bcast:31 carry the
+// row maxima upward (lanes outside a step's rows read 0).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_src_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, ROW_MASK, 0xF, false);
+}
+__device__ __forceinline__ int wave_max_row3(int x) {
+  x = max(x, dpp_src_i<0xB1>(x));
+  x = max(x, dpp_src_i<0x4E>(x));
+  x = max(x, dpp_src_i<0x141>(x));
+  x = max(x, dpp_src_i<0x140>(x));
+  x = max(x, dpp_src_i<0x142, 0xA>(x));
+  x = max(x, dpp_src_i<0x143, 0xC>(x));
+  return x;
+}
+
 // Long tiles.  A tile range is cut into segments of kSegSplats splats and
 // colour is summed per segment: at each segment boundary a pixel's colour
 // accumulators are added into its output pixel (which holds the sum of the
@@ -262,6 +280,13 @@ __device__ __forceinline__ int tile_pixel(int k) {
 // where they are used, so that the compiler does not keep 64-bit addresses
 // for the rare segment boundaries live across the compositing loop.
 __device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+// The same for a 64-bit pixel index: the other pixels of a lane are then
+// reached by adding multiples of a row stride instead of a full 64-bit
+// index computation each.
+__device__ __forceinline__ int64_t opaque64(int64_t v) {
   asm volatile("" : "+v"(v));
   return v;
 }
@@ -455,11 +480,10 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
           out_last[pix0 + (int64_t)4 * k * P.width] = last[k];
         tile_max = max(tile_max, last[k]);
       }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1)
-        tile_max = max(tile_max, __shfl_xor(tile_max, off, 64));
+      tile_max = wave_max_row3(tile_max);
+      if (threadIdx.x == kLanes - 1 && out_tile_stop != nullptr)
+        out_tile_stop[tc.tile] = tile_max;
       if (threadIdx.x == 0) {
-        if (out_tile_stop != nullptr) out_tile_stop[tc.tile] = tile_max;
         H.handoff[item] = tc.tile;
         H.handoff_tail[item] = tail;
       }
@@ -470,11 +494,14 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     last_segment<kPix>(P, tc, out_rgb, H, -1, valid, cr, cg, cb, T,
                        (int)threadIdx.x);
   int tile_max = 0;
+  // The lane's pixels are 4 rows apart: one 64-bit index, then increments.
+  const int64_t pix0 = opaque64(
+      ((int64_t)tc.batch * P.height + slot_y(tc, 0)) * P.width + x);
+  const int64_t strip = (int64_t)4 * P.width;
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
     if (valid[k]) {
-      const int64_t pix =
-          ((int64_t)tc.batch * P.height + slot_y(tc, k)) * P.width + x;
+      const int64_t pix = pix0 + k * strip;
       // streaming stores: the per-pixel outputs are not read again here
       __builtin_nontemporal_store(cr[k] + T[k] * P.bg_r, out_rgb + 3 * pix + 0);
       __builtin_nontemporal_store(cg[k] + T[k] * P.bg_g, out_rgb + 3 * pix + 1);
@@ -487,10 +514,8 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     }
   }
   if (out_tile_stop) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-      tile_max = max(tile_max, __shfl_xor(tile_max, off, 64));
-    if (threadIdx.x == 0) out_tile_stop[tc.tile] = tile_max;
+    tile_max = wave_max_row3(tile_max);
+    if (threadIdx.x == kLanes - 1) out_tile_stop[tc.tile] = tile_max;
   }
 }
 
@@ -596,10 +621,8 @@ __global__ __launch_bounds__(256 / kSpW) void render_fwd_long_kernel(
       }
     }
     if (out_tile_stop != nullptr) {
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1)
-        tile_max = max(tile_max, __shfl_xor(tile_max, off, 64));
-      if (lane == 0) atomicMax(out_tile_stop + tile, tile_max);
+      tile_max = wave_max_row3(tile_max);
+      if (lane == kLanes - 1) atomicMax(out_tile_stop + tile, tile_max);
     }
   }
 }
@@ -708,13 +731,17 @@ __device__ __forceinline__ void load_bwd_pixels(
     const float* __restrict__ grad_rgb, BwdPixels& Q) {
   const int x = tc.x0 + tc.lx;
   Q.px = (float)x + 0.5f;
+  // The lane's pixels are 4 rows apart: one 64-bit index, then increments.
+  const int64_t pix0 = opaque64(
+      ((int64_t)tc.batch * P.height + slot_y(tc, 0)) * P.width + x);
+  const int64_t strip = (int64_t)4 * P.width;
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
     const int y = slot_y(tc, k);
     const bool valid = (x < P.width) && (y < P.height);
     Q.py[k] = (float)y + 0.5f;
     if (valid) {
-      const int64_t pix = ((int64_t)tc.batch * P.height + y) * P.width + x;
+      const int64_t pix = pix0 + k * strip;
       // streaming loads: each pixel's state is read once
       Q.gr[k] = __builtin_nontemporal_load(grad_rgb + 3 * pix + 0);
       Q.gg[k] = __builtin_nontemporal_load(grad_rgb + 3 * pix + 1);
