@@ -257,9 +257,13 @@ __global__ void zero_u32_kernel(uint32_t* p, int64_t n) {
 }  // namespace
 
 // Rounds (64-element groups per wavefront) of one onesweep workgroup: small
-// segments use smaller workgroups so that more of them run side by side.
+// segments use smaller workgroups so that more of them run side by side;
+// large ones use larger workgroups (8192 elements, two per CU by LDS), which
+// halves the look-back chain and doubles the length of each digit's
+// coalesced run in the scatter (measured 25% faster passes at 1.2e8 pairs).
 int radix_rounds(int64_t n_seg) {
-  return n_seg <= (int64_t(1) << 18) ? 4 : 16;
+  if (n_seg <= (int64_t(1) << 18)) return 4;
+  return n_seg <= (int64_t(1) << 22) ? 16 : 32;
 }
 
 RadixPlan radix_plan(int64_t n_seg, int segments, int begin_bit, int end_bit) {
@@ -327,8 +331,10 @@ int radix_global_hist(const RadixPlan& L, const RadixCtl& C,
                      L.begin_bit, L.end_bit, L.passes, C.ghist)
   if (L.rounds == 4) {
     if (depth_src) GS_HIST_LAUNCH(true, 4); else GS_HIST_LAUNCH(false, 4);
-  } else {
+  } else if (L.rounds == 16) {
     if (depth_src) GS_HIST_LAUNCH(true, 16); else GS_HIST_LAUNCH(false, 16);
+  } else {
+    if (depth_src) GS_HIST_LAUNCH(true, 32); else GS_HIST_LAUNCH(false, 32);
   }
 #undef GS_HIST_LAUNCH
   return check_launch("rs_global_hist_kernel");
@@ -380,7 +386,8 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
     hipLaunchKernelGGL((rs_onesweep_kernel<M, R>), grid, dim3(kThreads), 0, \
                        stream, a);                                          \
     break;
-#define GS_ONESWEEP_MODE(M) GS_ONESWEEP_CASE(M, 4) GS_ONESWEEP_CASE(M, 16)
+#define GS_ONESWEEP_MODE(M) \
+  GS_ONESWEEP_CASE(M, 4) GS_ONESWEEP_CASE(M, 16) GS_ONESWEEP_CASE(M, 32)
       GS_ONESWEEP_MODE(0) GS_ONESWEEP_MODE(1) GS_ONESWEEP_MODE(2)
       GS_ONESWEEP_MODE(3) GS_ONESWEEP_MODE(4) GS_ONESWEEP_MODE(5)
       GS_ONESWEEP_MODE(6) GS_ONESWEEP_MODE(7)

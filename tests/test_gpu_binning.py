@@ -46,6 +46,8 @@ def test_exclusive_scan_in_place(gpu):
     (100_003, 1, 0, 13, 37),          # many duplicates, partial digit
     (700_001, 1, 0, 16, 1 << 16),
     (2_500_003, 1, 0, 32, 1 << 32),   # 32-bit keys, 16 rounds per workgroup
+    (4_200_001, 1, 0, 16, 1 << 16),   # 32 rounds per workgroup (above 2^22 elements)
+    (3_000_000, 2, 0, 24, 1 << 24),   # segmented, 16 rounds
     (65536, 4, 0, 32, 1 << 32),       # segmented
     (10_000, 3, 8, 24, 1 << 32),      # bit window
     (1000, 2, 0, 0, 1 << 32),         # zero passes: copy
