@@ -383,17 +383,36 @@ __global__ __launch_bounds__(kThreads) void hist_reduce_kernel(
 // tile_offsets from the sorted tile keys: index i (0 <= i <= n) is the first
 // pair of every tile t with keys[i-1] < t <= keys[i] (keys[-1] = -1,
 // keys[n] = num_tiles), so tile_offsets[num_tiles] = n.  With n_dev the key
-// count is min(*n_dev, n).
+// count is min(*n_dev, n).  Grid-stride over the indices, kRangeUnroll of
+// them per iteration with all their loads issued first (indices clamped into
+// [0, n_cap), so the loads need no branch), which keeps a launch over 1e8
+// keys to a few thousand workgroups.
+constexpr int kRangeUnroll = 4;
+constexpr int kRangeMaxBlocks = 2048;
 __global__ __launch_bounds__(kThreads) void ranges_kernel(
     const uint32_t* __restrict__ sorted_keys, int64_t n_cap,
     const int32_t* __restrict__ n_dev, int num_tiles,
     int32_t* __restrict__ tile_offsets) {
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   const int64_t n = n_dev ? min(n_cap, (int64_t)max(*n_dev, 0)) : n_cap;
-  if (i > n) return;
-  const int64_t prev = (i == 0) ? -1 : (int64_t)sorted_keys[i - 1];
-  const int64_t cur = (i == n) ? (int64_t)num_tiles : (int64_t)sorted_keys[i];
-  for (int64_t t = prev + 1; t <= cur; ++t) tile_offsets[t] = (int32_t)i;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; i0 <= n;
+       i0 += kRangeUnroll * stride) {
+    uint32_t kp[kRangeUnroll], kc[kRangeUnroll];
+#pragma unroll
+    for (int u = 0; u < kRangeUnroll; ++u) {
+      const int64_t i = min(i0 + u * stride, n);
+      kp[u] = sorted_keys[max(i - 1, (int64_t)0)];
+      kc[u] = sorted_keys[max(min(i, n - 1), (int64_t)0)];
+    }
+#pragma unroll
+    for (int u = 0; u < kRangeUnroll; ++u) {
+      const int64_t i = i0 + u * stride;
+      if (i > n) break;
+      const int64_t prev = (i == 0) ? -1 : (int64_t)kp[u];
+      const int64_t cur = (i == n) ? (int64_t)num_tiles : (int64_t)kc[u];
+      for (int64_t t = prev + 1; t <= cur; ++t) tile_offsets[t] = (int32_t)i;
+    }
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void counts_kernel(
@@ -512,10 +531,11 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
   if (n == 0) {
     rc = launch_fill_i32(tile_offsets, 0, (int64_t)num_tiles + 1, stream);
   } else {
-    hipLaunchKernelGGL(ranges_kernel,
-                       dim3((unsigned)((n + 1 + kThreads - 1) / kThreads)),
-                       dim3(kThreads), 0, stream, sorted_keys, n, n_dev,
-                       num_tiles, tile_offsets);
+    int64_t grid = (n + 1 + kThreads - 1) / kThreads;
+    if (grid > kRangeMaxBlocks) grid = kRangeMaxBlocks;
+    hipLaunchKernelGGL(ranges_kernel, dim3((unsigned)grid), dim3(kThreads), 0,
+                       stream, sorted_keys, n, n_dev, num_tiles,
+                       tile_offsets);
     rc = check_launch("ranges_kernel");
   }
   if (rc || tile_counts == nullptr) return rc;
