@@ -344,6 +344,10 @@ def main() -> int:
             "frac": round(achieved_tflops / PEAK_FP32_TFLOPS, 4),
             "traffic": traffic,
             "work": f"256 * walked_pairs evaluations x {FLOP_PER_EVAL[dom]:.0f} FLOP per launch",
+            # the same launch against the HBM roof (measured bytes per launch
+            # over the live launch time): shows the kernel is not HBM bound
+            "hbm_achieved_gbs": (round(traffic / (comp_ms[dom] * 1e-3) / 1e9, 1) if traffic else None),
+            "hbm_frac": (round(traffic / (comp_ms[dom] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if traffic else None),
         },
     }
     if not args.no_cpu_baseline and not three_d:

@@ -129,8 +129,10 @@ int null_check(std::initializer_list<const void*> ptrs, const char* what) {
 // bin_depth_order; then the pack-scan look-back status and ticket and the
 // pair sort's histograms and tickets, zeroed by bin_count), then the
 // per-splat tile-hit counts (original order), the count workgroups' sums and
-// the depth sort's ping-pong buffers.  bin_count and bin_depth_order touch
-// disjoint parts, so they may run concurrently on two streams.
+// the depth sort's buffers (the onesweep's ping-pong buffers, or the sorted
+// runs and samples of the two-launch sort of small images).  bin_count and
+// bin_depth_order touch disjoint parts, so they may run concurrently on two
+// streams.
 struct CountLayout {
   gs::RadixPlan depth;
   size_t scan_status, scan_ticket, pair_ghist, pair_tickets, ctl_end;
@@ -155,7 +157,10 @@ CountLayout count_layout(const RasterParams& P) {
   L.block_sums = off;
   off += gs::align_up((size_t)gs::count_blocks(P) * sizeof(int32_t), 256);
   L.depth_buffers = off;
-  off += gs::align_up(L.depth.buffer_bytes, 256);
+  size_t depth_bytes = L.depth.buffer_bytes;
+  if (gs::depth_small_ok(P.gpb))
+    depth_bytes = std::max(depth_bytes, gs::depth_small_bytes(P.gpb, P.batch));
+  off += gs::align_up(depth_bytes, 256);
   L.total = off;
   return L;
 }
@@ -255,8 +260,12 @@ int gsplat_hip_bin_depth_order(const gsplat_raster_meta* meta,
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* base = static_cast<char*>(workspace);
+  // stable depth order per image: small images by run sort + merge ranks
+  // (two launches), larger ones by the onesweep LSD over the 32 key bits
+  if (gs::depth_small_ok(P.gpb))
+    return gs::launch_depth_order_small(depths, perm, P.gpb, P.batch,
+                                        base + L.depth_buffers, s);
   const gs::RadixCtl depth_ctl = gs::radix_ctl_at(L.depth, base);
-  // stable depth order per image (onesweep LSD over the 32 key bits)
   rc = gs::launch_zero_u32(reinterpret_cast<uint32_t*>(base),
                            (int64_t)(gs::radix_ctl_bytes(L.depth) / sizeof(uint32_t)), s);
   if (!rc) rc = gs::radix_global_hist(L.depth, depth_ctl, nullptr, depths, s);

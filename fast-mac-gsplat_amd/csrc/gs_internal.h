@@ -35,6 +35,17 @@ int check_launch(const char* what);
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Order-preserving map of a float depth to uint32 (ascending float order ==
+// ascending key).  -0.0 and +0.0 map to the same key (they compare equal in
+// torch.argsort); every NaN maps to 0xffc00000, above +inf (torch sorts NaN
+// last).
+__device__ __forceinline__ uint32_t depth_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if (f == 0.0f) u = 0u;
+  if (!(f == f)) u = 0x7fc00000u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 // ---- scan (scan.hip)
 size_t scan_workspace_bytes(int64_t n);
 // ctl_zeroed: the workspace's look-back status and ticket are already zero
@@ -84,6 +95,13 @@ int radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in,
                      uint32_t* vals_out, int64_t n_per_segment, int segments,
                      int begin_bit, int end_bit, void* ws, size_t ws_bytes,
                      hipStream_t stream);
+// ---- stable depth order of small images (depth_sort.hip)
+// Images of at most 131072 splats: run sort in LDS + merge ranks, two
+// launches.  buffers: depth_small_bytes(G, batch) bytes.
+bool depth_small_ok(int64_t G);
+size_t depth_small_bytes(int64_t G, int batch);
+int launch_depth_order_small(const float* depths, int32_t* perm, int64_t G,
+                             int batch, void* buffers, hipStream_t stream);
 
 // ---- binning (binning.hip)
 // count: per-splat tile-hit counts (original order) into splat_count, the

@@ -26,16 +26,6 @@ constexpr int kWaves = 4;
 // Look-back window: predecessor statuses read per round trip.
 constexpr int kLookbackWindow = 16;
 
-// Order-preserving map of a float depth to uint32 (ascending float order ==
-// ascending key).  -0.0 and +0.0 map to the same key (they compare equal in
-// torch.argsort); every NaN maps above +inf (torch sorts NaN last).
-__device__ __forceinline__ uint32_t depth_key(float f) {
-  uint32_t u = __float_as_uint(f);
-  if (f == 0.0f) u = 0u;
-  if (!(f == f)) u = 0x7fc00000u;
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const unsigned lane = threadIdx.x & 63u;
   return (lane == 0u) ? 0ull : (~0ull >> (64u - lane));

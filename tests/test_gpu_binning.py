@@ -244,3 +244,42 @@ def test_depth_order_segments_and_large(gpu, B, G):
     got = perm.cpu().numpy().reshape(B, G)
     for b in range(B):
         np.testing.assert_array_equal(got[b], np.argsort(d[b], kind="stable"))
+
+
+@pytest.mark.parametrize("B,G,kind", [
+    (1, 1, "uniform"), (1, 37, "few"), (2, 4095, "uniform"), (1, 4096, "equal"),
+    (3, 4097, "few"), (1, 65536, "uniform"), (2, 65536, "special"), (1, 131072, "few"),
+    (2, 131072, "uniform"),     # largest image of the two-launch sort (32 runs)
+    (1, 131073, "special"),     # smallest image of the onesweep path
+])
+def test_depth_order_small_images(gpu, B, G, kind):
+    """Images of up to 131072 splats take the two-launch sort (4096-splat runs sorted in LDS, merge
+    ranks from sampled binary searches): permutation equal to a stable argsort for uniform depths,
+    all-equal depths, few distinct depths and NaN / +-inf / +-0 mixes, at and around the run and
+    path boundaries."""
+    print(f"depth order small B={B} G={G} {kind}", flush=True)
+    rng = np.random.default_rng(G + B)
+    if kind == "uniform":
+        d = rng.uniform(0.1, 10.0, size=(B, G))
+    elif kind == "equal":
+        d = np.full((B, G), 2.5)
+    elif kind == "few":
+        d = rng.integers(0, 4, size=(B, G)) * 0.75 + 1.0
+    else:
+        d = rng.uniform(-5.0, 5.0, size=(B, G))
+        specials = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-30, -1e-30])
+        pick = rng.random((B, G)) < 0.2
+        d[pick] = rng.choice(specials, size=int(pick.sum()))
+    d = d.astype(np.float32)
+    meta = _lib.make_raster_meta(64, 64, B, G, 1.0 / 255.0, 1e-4, (0.0, 0.0, 0.0))
+    L = _lib.lib()
+    wsb = L.gsplat_hip_bin_count_workspace_bytes(meta)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    dd = torch.from_numpy(d).to(gpu)
+    perm = torch.full((B * G,), -1, dtype=torch.int32, device=gpu)
+    _lib.check(L.gsplat_hip_bin_depth_order(meta, _lib.ptr(dd), _lib.ptr(perm), _lib.ptr(ws), wsb,
+                                            _lib.stream_of(dd)), "gsplat_hip_bin_depth_order")
+    got = perm.cpu().numpy().reshape(B, G)
+    for b in range(B):
+        # numpy: -0.0 == +0.0, NaN last, stable
+        np.testing.assert_array_equal(got[b], np.argsort(d[b], kind="stable"))
