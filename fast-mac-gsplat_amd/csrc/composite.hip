@@ -42,11 +42,9 @@
 // (dx is shared by the lane's pixels) and the colour sums are kept (the
 // opacity gradient is sum g_raw exp(power) = S0 / o);
 // the nine per-splat values are formed from them and reduced across the
-// wavefront by a transposed butterfly: two rounds of half-wave register swaps
-// (v_permlane32_swap / v_permlane16_swap) fold eight values into two
-// registers whose four rows each hold one value, four DPP row steps finish
-// them, and lanes 0, 16, 32 and 48 each issue the float atomic for their row
-// into the original splat order (the ninth value uses a plain DPP reduction).
+// wavefront: eight through LDS (each group of eight lanes sums one value's 64
+// partials, then three DPP steps; the group's first lane issues the float
+// atomic into the original splat order) and the ninth by DPP row steps.
 #include "gs_internal.h"
 #include "gs_predicate.h"
 
@@ -133,8 +131,43 @@ __device__ __forceinline__ uint32_t strip_mask(float mx, float my, float a,
   return m;
 }
 
+// Mask bit of a "plain" record: for it the compositors' tests p <= 0 and
+// o 2^p < max_alpha always hold, so they are left out (same results, fewer
+// VALU operations per pixel).  Set only together with a strip bit.
+constexpr uint32_t kPlainBit = 1u << 4;
+
+// True when, for every pixel, the computed exponent p = fma(C dy, dy,
+// fma(B dx, dy, (A dx) dx)) is <= 0 and o 2^p stays below max_alpha:
+//  * -p is the quadratic form a' dx^2 + b' dx dy + c' dy^2 (a' = -A,
+//    b' = -B, c' = -C) whose smallest eigenvalue is at least
+//    (4a'c' - b'^2) / (4 (a' + c')) >= 2^-18 (a' + c') when 4a'c' - b'^2 >=
+//    2^-16 (a' + c')^2, while the rounding of the chain (three roundings
+//    per term, relative 2^-24 each) moves -p by at most 4.6 2^-24 (a' + c')
+//    (dx^2 + dy^2): the sign of p is never flipped.  The bounds on a', c',
+//    |b'| and the centre keep every product of the chain normal and finite
+//    (|dx| and |dy| are 0 or at least 2^-25, and at most 2^33, since pixel
+//    centres are below 2^31); dx = dy = 0 gives p = +-0, which passes p <= 0;
+//  * 2^p <= 1 (hardware exp2, within 1 ulp) and o <= o_plain = max_alpha
+//    (1 - 2^-20) keep the rounded o 2^p below max_alpha, so the clamp and
+//    the gradient gate never act.
+// NaN anywhere fails a comparison and leaves the record on the general path.
+__device__ __forceinline__ bool plain_record(float A, float B, float C,
+                                             float mx, float my, float o,
+                                             float o_plain) {
+  const float a = -A, c = -C, s = a + c;
+  return (o > 0.0f) & (o <= o_plain) & (a >= 0x1p-60f) & (c >= 0x1p-60f) &
+         (a <= 0x1p40f) & (c <= 0x1p40f) & (fabsf(B) <= 0x1p40f) &
+         (4.0f * a * c - B * B >= 0x1p-16f * s * s) &
+         (fabsf(mx) <= 0x1p32f) & (fabsf(my) <= 0x1p32f);
+}
+
+// o_plain of plain_record for a clamp value max_alpha.
+__device__ __forceinline__ float plain_opacity_limit(float max_alpha) {
+  return max_alpha * (1.0f - 0x1p-20f);
+}
+
 // Stages records [first, first+n) of the tile range into LDS with the
-// base-2 exponent coefficients and the tile's strip mask.
+// base-2 exponent coefficients and the tile's strip mask (plus kPlainBit).
 // Returns this lane's strip mask (0 for lanes past n).  With kMaskInLds the
 // mask also goes to s2.w (kernels whose other wavefronts read it); otherwise
 // s2.w holds 1 / opacity and the wavefront reads each record's mask from
@@ -142,7 +175,7 @@ __device__ __forceinline__ uint32_t strip_mask(float mx, float my, float a,
 template <bool kMaskInLds>
 __device__ __forceinline__ uint32_t stage_batch(
     const float4* __restrict__ packed, const int32_t* __restrict__ binned,
-    int first, int n, const TileCoord& tc, Staged& S) {
+    int first, int n, const TileCoord& tc, float o_plain, Staged& S) {
   const int lane = threadIdx.x;
   uint32_t m = 0u;
   if (lane < n) {
@@ -159,6 +192,8 @@ __device__ __forceinline__ uint32_t stage_batch(
       B = (-b) * kLog2e;
       C = (-0.5f * c) * kLog2e;
     }
+    if (m != 0u && plain_record(A, B, C, p0.x, p0.y, p1.y, o_plain))
+      m |= kPlainBit;
     S.s0[lane] = make_float4(p0.x, p0.y, A, B);
     S.s1[lane] = make_float4(C, p1.y, p1.z, p1.w);
     S.s2[lane] = make_float4(
@@ -365,7 +400,9 @@ __device__ __forceinline__ void last_segment(const RasterParams& P,
   }
 }
 
-// Front-to-back compositing of splat j of the staged batch into one pixel.
+// Front-to-back compositing of splat j of the staged batch into one pixel
+// (kPlain: a record with kPlainBit, whose p <= 0 test and clamp never act).
+template <bool kPlain>
 __device__ __forceinline__ void composite_one(float Adxdx, float Bdx,
                                               const float4& a1,
                                               const float4& a2, float py,
@@ -377,17 +414,52 @@ __device__ __forceinline__ void composite_one(float Adxdx, float Bdx,
   // batch, so guarding the exponent by T would save little and cost a
   // second branch.
   const float p = splat_exponent(Adxdx, Bdx, a1.x, py - my);
-  if ((T > t_thr) & (p <= 0.0f) & (p >= a2.z)) {
+  if ((T > t_thr) & (kPlain || p <= 0.0f) & (p >= a2.z)) {
     // min(max_alpha, o 2^p) as one med3: o 2^p >= 0 here (plim is +inf for
     // o <= 0), so the lower bound 0 never changes the result.
-    const float alpha = __builtin_amdgcn_fmed3f(
-        a1.y * __builtin_amdgcn_exp2f(p), 0.0f, max_alpha);
+    // o 2^p rounded once (an fma with +0 is never fused with 1 - alpha, so
+    // both variants round alike)
+    const float raw = __builtin_fmaf(a1.y, __builtin_amdgcn_exp2f(p), 0.0f);
+    const float alpha =
+        kPlain ? raw : __builtin_amdgcn_fmed3f(raw, 0.0f, max_alpha);
     const float w = T * alpha;
     cr += w * a1.z;
     cg += w * a1.w;
     cb += w * a2.x;
     T *= (1.0f - alpha);
     last = idx1;
+  }
+}
+
+// True when every record of the staged batch that reaches a strip carries
+// kPlainBit (m: the staging lane's mask), so the batch is composited without
+// the p <= 0 test and the max_alpha clamp.
+__device__ __forceinline__ bool batch_plain(uint32_t m) {
+  return __builtin_amdgcn_ballot_w64((m != 0u) & !(m & kPlainBit)) == 0;
+}
+
+// Front-to-back compositing of the n staged records of one batch into the
+// lane's kPix pixels (idx1: 1 + tile index of record 0).
+template <bool kPlain>
+__device__ __forceinline__ void fwd_batch(const Staged& S, uint32_t bmask,
+                                          int n, int idx1, float px,
+                                          const float* py, float t_thr,
+                                          float max_alpha, float* T, float* cr,
+                                          float* cg, float* cb, int* last) {
+  for (int j = 0; j < n; ++j) {
+    const uint32_t mask = __builtin_amdgcn_readlane(bmask, j);
+    if (mask == 0u) continue;
+    const float4 a2 = S.s2[j];
+    const float4 a0 = S.s0[j];
+    const float4 a1 = S.s1[j];
+    float Adxdx, Bdx;
+    x_terms(a0.z, a0.w, px - a0.x, Adxdx, Bdx);
+#pragma unroll
+    for (int k = 0; k < kPix; ++k) {
+      if (!((mask >> k) & 1u)) continue;  // scalar branch
+      composite_one<kPlain>(Adxdx, Bdx, a1, a2, py[k], a0.y, t_thr, max_alpha,
+                            idx1 + j, T[k], cr[k], cg[k], cb[k], last[k]);
+    }
   }
 }
 
@@ -405,6 +477,7 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
   // host); pixels outside the image start at T = 0 and are never written.
   const float t_thr = P.trans_thr;
   const float max_alpha = fminf(P.max_alpha, 1.0f);
+  const float o_plain = plain_opacity_limit(max_alpha);
   float py[kPix], T[kPix], cr[kPix], cg[kPix], cb[kPix];
   int last[kPix];
   bool valid[kPix];
@@ -437,24 +510,15 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     }
     const int n = min(kBatch, end - base);
     __syncthreads();
-    const uint32_t bmask = stage_batch<false>(packed, binned, base, n, tc, S);
+    const uint32_t bmask =
+        stage_batch<false>(packed, binned, base, n, tc, o_plain, S);
     __syncthreads();
-    for (int j = 0; j < n; ++j) {
-      const uint32_t mask = __builtin_amdgcn_readlane(bmask, j);
-      if (mask == 0u) continue;
-      const float4 a2 = S.s2[j];
-      const float4 a0 = S.s0[j];
-      const float4 a1 = S.s1[j];
-      float Adxdx, Bdx;
-      x_terms(a0.z, a0.w, px - a0.x, Adxdx, Bdx);
-      const int idx1 = base - start + j + 1;
-#pragma unroll
-      for (int k = 0; k < kPix; ++k) {
-        if (!((mask >> k) & 1u)) continue;  // scalar branch
-        composite_one(Adxdx, Bdx, a1, a2, py[k], a0.y, t_thr, max_alpha, idx1,
-                      T[k], cr[k], cg[k], cb[k], last[k]);
-      }
-    }
+    if (batch_plain(bmask))
+      fwd_batch<true>(S, bmask, n, base - start + 1, px, py, t_thr, max_alpha,
+                      T, cr, cg, cb, last);
+    else
+      fwd_batch<false>(S, bmask, n, base - start + 1, px, py, t_thr,
+                       max_alpha, T, cr, cg, cb, last);
   }
   if (walk_end < end) {
     const bool any_alive = (T[0] > t_thr) | (T[1] > t_thr) | (T[2] > t_thr) |
@@ -519,6 +583,36 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
   }
 }
 
+// The long kernel's walk over the n staged records of one batch for this
+// wavefront's kSpW strips (strips s0 .. s0 + kSpW - 1; strip masks in s2.w).
+// Software pipelined: record j + 1 is read from LDS while record j is
+// composited, so the walk does not wait for LDS on every splat.
+template <int kSpW, bool kPlain>
+__device__ __forceinline__ void long_batch(const Staged& S, int n, int idx1,
+                                           int s0, float px, const float* py,
+                                           float t_thr, float max_alpha,
+                                           float* T, float* cr, float* cg,
+                                           float* cb, int* last) {
+  float4 n0 = S.s0[0], n1 = S.s1[0], n2 = S.s2[0];
+  for (int j = 0; j < n; ++j) {
+    const float4 a0 = n0, a1 = n1, a2 = n2;
+    const int jn = min(j + 1, n - 1);
+    n0 = S.s0[jn];
+    n1 = S.s1[jn];
+    n2 = S.s2[jn];
+    const uint32_t mask = uniform_bits(a2.w) >> s0;
+    if (!(mask & ((1u << kSpW) - 1u))) continue;  // scalar branch
+    float Adxdx, Bdx;
+    x_terms(a0.z, a0.w, px - a0.x, Adxdx, Bdx);
+#pragma unroll
+    for (int k = 0; k < kSpW; ++k) {
+      if (!((mask >> k) & 1u)) continue;  // scalar branch
+      composite_one<kPlain>(Adxdx, Bdx, a1, a2, py[k], a0.y, t_thr, max_alpha,
+                            idx1 + j, T[k], cr[k], cg[k], cb[k], last[k]);
+    }
+  }
+}
+
 // Continuation of the tiles handed off by render_fwd_kernel: a workgroup of
 // 4 / kSpW wavefronts per tile, wavefront w walking strips kSpW w ..
 // kSpW w + kSpW - 1 (lane l: column l % 16, row 4 strip + l / 16) from the
@@ -534,12 +628,14 @@ __global__ __launch_bounds__(256 / kSpW) void render_fwd_long_kernel(
     int32_t* __restrict__ out_tile_stop, HeavyState H) {
   __shared__ Staged S;
   __shared__ int sh_slot;
+  __shared__ int sh_plain;  // batch_plain of the staged batch
   const int lane = (int)threadIdx.x & 63;
   const int s0 = __builtin_amdgcn_readfirstlane(((int)threadIdx.x >> 6) * kSpW);
   const int t0 = 64 * s0 + lane;  // in-tile index of the first strip's pixel
   const int n_items = H.counters[1];
   const float t_thr = P.trans_thr;
   const float max_alpha = fminf(P.max_alpha, 1.0f);
+  const float o_plain = plain_opacity_limit(max_alpha);
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     __syncthreads();  // the previous tile's reads of S and sh_slot are done
     const int tile = H.handoff[item];
@@ -578,29 +674,20 @@ __global__ __launch_bounds__(256 / kSpW) void render_fwd_long_kernel(
         ++seg_cur;
       }
       const int n = min(kBatch, end - base);
-      stage_batch<true>(packed, binned, base, n, tc, S);
-      __syncthreads();
-      // Software pipelined: record j + 1 is read from LDS while record j is
-      // composited, so the walk does not wait for LDS on every splat.
-      float4 n0 = S.s0[0], n1 = S.s1[0], n2 = S.s2[0];
-      for (int j = 0; j < n; ++j) {
-        const float4 a0 = n0, a1 = n1, a2 = n2;
-        const int jn = min(j + 1, n - 1);
-        n0 = S.s0[jn];
-        n1 = S.s1[jn];
-        n2 = S.s2[jn];
-        const uint32_t mask = uniform_bits(a2.w) >> s0;
-        if (!(mask & ((1u << kSpW) - 1u))) continue;  // scalar branch
-        float Adxdx, Bdx;
-        x_terms(a0.z, a0.w, px - a0.x, Adxdx, Bdx);
-#pragma unroll
-        for (int k = 0; k < kSpW; ++k) {
-          if (!((mask >> k) & 1u)) continue;  // scalar branch
-          composite_one(Adxdx, Bdx, a1, a2, py[k], a0.y, t_thr, max_alpha,
-                        base - start + j + 1, T[k], cr[k], cg[k], cb[k],
-                        last[k]);
-        }
+      const uint32_t m =
+          stage_batch<true>(packed, binned, base, n, tc, o_plain, S);
+      if (threadIdx.x < kLanes) {  // wavefront 0 staged the batch
+        const bool all_plain = batch_plain(m);
+        if (threadIdx.x == 0) sh_plain = all_plain;
       }
+      __syncthreads();
+      const bool plain = sh_plain != 0;
+      if (plain)
+        long_batch<kSpW, true>(S, n, base - start + 1, s0, px, py, t_thr,
+                               max_alpha, T, cr, cg, cb, last);
+      else
+        long_batch<kSpW, false>(S, n, base - start + 1, s0, px, py, t_thr,
+                                max_alpha, T, cr, cg, cb, last);
     }
     __syncthreads();  // sh_slot of the last boundary has been read
     if (threadIdx.x == 0) sh_slot = next_segment(H, tile, seg_cur, tail);
@@ -773,8 +860,111 @@ __device__ __forceinline__ bool needs_last_test(const RasterParams& P,
   return __builtin_amdgcn_ballot_w64(need) != 0;
 }
 
-// Reverse walk over the tile-range indices [lo, hi): gradients of every
-// splat, reduced across the wavefront and added atomically in original order.
+// Reverse walk over the n staged records of one batch (tile indices
+// cstart .. cstart + n - 1): each pixel undoes the blend of every splat it
+// composited in the forward (i < last, tested with kCheckLast) and sees,
+// adding its parts of the splat's gradients to the lane's sums, which are
+// reduced across the wavefront and added atomically in original order.
+// kPlain: every record has kPlainBit, so p <= 0 and the max_alpha gate are
+// not tested (they always pass).
+template <bool kCheckLast, bool kPlain>
+__device__ __forceinline__ void bwd_batch(
+    BwdShared& SH, uint32_t bmask, int n, int cstart, float max_alpha,
+    const GradTarget& target, BwdPixels& Q, float* __restrict__ g_opac) {
+  const Staged& S = SH.S;
+  const int lane = threadIdx.x;
+  const bool group_head = (lane & 7) == 0;
+  // this lane's eight values of its group's quantity in red: 16-byte chunks
+  // l and l + 8 of the row (l = lane % 8), so that the eight lanes of a
+  // group read 128 consecutive bytes per load (no bank conflict)
+  const float* red_in = SH.red + (lane >> 3) * kLanes + (lane & 7) * 4;
+  // Per-lane partial sums of the current splat; zero between splats.
+  float S0 = 0.f, S1 = 0.f, S2 = 0.f;
+  float acc_r = 0.f, acc_g = 0.f, acc_b = 0.f;
+  for (int j = n - 1; j >= 0; --j) {
+    const uint32_t mask = __builtin_amdgcn_readlane(bmask, j);
+    if (mask == 0u) continue;
+    const float4 a2 = S.s2[j];
+    const int i = cstart + j;
+    const float4 a0 = S.s0[j];
+    const float4 a1 = S.s1[j];
+    const float dx = Q.px - a0.x;
+    float Adxdx, Bdx;
+    x_terms(a0.z, a0.w, dx, Adxdx, Bdx);
+    bool contrib = false;
+#pragma unroll
+    for (int k = 0; k < kPix; ++k) {
+      if (!((mask >> k) & 1u)) continue;  // scalar branch
+      // one combined test: composited in the forward (i < last) and visible
+      const float dy = Q.py[k] - a0.y;
+      const float p = splat_exponent(Adxdx, Bdx, a1.x, dy);
+      if (((!kCheckLast) | (i < Q.lk[k])) & (kPlain | (p <= 0.0f)) &
+          (p >= a2.z)) {
+        contrib = true;
+        const float e = __builtin_amdgcn_exp2f(p);
+        // o 2^p rounded once (an fma with +0 is never fused with 1 - raw,
+        // so both variants round alike)
+        const float raw = __builtin_fmaf(a1.y, e, 0.0f);
+        const bool open = kPlain || raw < max_alpha;  // gradient gate
+        const float alpha = open ? raw : max_alpha;
+        // 1 - alpha >= 1 - max_alpha >= eps (checked on the host), so the
+        // reference's max(1 - alpha, eps) is 1 - alpha.
+        const float T_prev = Q.Tc[k] * __builtin_amdgcn_rcpf(1.0f - alpha);
+        const float dot_gc = Q.gr[k] * a1.z + Q.gg[k] * a1.w + Q.gb[k] * a2.x;
+        const float diff = dot_gc - Q.gT[k];
+        const float wgt = T_prev * alpha;
+        acc_r += Q.gr[k] * wgt;
+        acc_g += Q.gg[k] * wgt;
+        acc_b += Q.gb[k] * wgt;
+        // alpha = raw when the gate is open, so T_prev raw = wgt
+        const float g_pow = open ? wgt * diff : 0.0f;
+        const float hdy = g_pow * dy;
+        S0 += g_pow;
+        S1 += hdy;
+        S2 += hdy * dy;
+        Q.gT[k] += alpha * diff;
+        Q.Tc[k] = T_prev;
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(contrib) != 0) {
+      // Per-lane parts of the splat's gradients (a, b, c = -2A/L, -B/L,
+      // -2C/L): g_mean = -(2/L) (V_mx, V_my), g_conic = (-V_ca/2, -V_cb,
+      // -V_cc/2) with V_cc = S2, and g_opacity = sum g_raw exp(power) =
+      // (sum g_power) / o = S0 / o.
+      const float X = dx * S0;             // sum g_power dx
+      const float hB = 0.5f * a0.w;
+      float* red_out = SH.red + lane;
+      red_out[0 * kLanes] = a0.z * X + hB * S1;  // V_mx
+      red_out[1 * kLanes] = hB * X + a1.x * S1;  // V_my
+      red_out[2 * kLanes] = dx * X;              // V_ca = sum g_power dx^2
+      red_out[3 * kLanes] = dx * S1;             // V_cb = sum g_power dx dy
+      red_out[4 * kLanes] = S2;
+      red_out[5 * kLanes] = acc_r;
+      red_out[6 * kLanes] = acc_g;
+      red_out[7 * kLanes] = acc_b;
+      const float r3 = wave_sum_row3(S0);
+      S0 = S1 = S2 = 0.f;
+      acc_r = acc_g = acc_b = 0.f;
+      wave_lds_sync();
+      const float4 u = *reinterpret_cast<const float4*>(red_in);
+      const float4 w = *reinterpret_cast<const float4*>(red_in + 32);
+      const float tot = group8_sum_dpp(((u.x + u.y) + (u.z + u.w)) +
+                                       ((w.x + w.y) + (w.z + w.w)));
+      const uint32_t orig = uniform_bits(a2.y);
+      if (group_head)
+        unsafeAtomicAdd(reinterpret_cast<float*>(
+                            reinterpret_cast<char*>(target.base) +
+                            (uint64_t)orig * target.stride),
+                        tot * target.scale);
+      if (lane == kLanes - 1)
+        unsafeAtomicAdd(g_opac + orig, r3 * a2.w);  // a2.w = 1 / opacity
+      wave_lds_sync();  // loads done before the next splat's stores
+    }
+  }
+}
+
+// Reverse walk over the tile-range indices [lo, hi), one staged batch of 64
+// records at a time.
 template <bool kCheckLast>
 __device__ __forceinline__ void bwd_walk(
     const RasterParams& P, const float4* __restrict__ packed,
@@ -782,106 +972,22 @@ __device__ __forceinline__ void bwd_walk(
     const TileCoord& tc, BwdShared& SH, BwdPixels& Q,
     float* __restrict__ g_means2d, float* __restrict__ g_conics,
     float* __restrict__ g_colors, float* __restrict__ g_opac) {
-  Staged& S = SH.S;
-  const int lane = threadIdx.x;
   const GradTarget target = grad_target(g_means2d, g_conics, g_colors);
-  const bool group_head = (lane & 7) == 0;
-  // this lane's eight values of its group's quantity in red: 16-byte chunks
-  // l and l + 8 of the row (l = lane % 8), so that the eight lanes of a
-  // group read 128 consecutive bytes per load (no bank conflict)
-  const float* red_in = SH.red + (lane >> 3) * kLanes + (lane & 7) * 4;
   const float max_alpha = fminf(P.max_alpha, 1.0f);
-  // Per-lane partial sums of the current splat; zero between splats.
-  float S0 = 0.f, S1 = 0.f, S2 = 0.f;
-  float acc_r = 0.f, acc_g = 0.f, acc_b = 0.f;
+  const float o_plain = plain_opacity_limit(max_alpha);
   for (int cend = hi; cend > lo; cend -= kBatch) {
     const int cstart = max(lo, cend - kBatch);
     const int n = cend - cstart;
     __syncthreads();
     const uint32_t bmask =
-        stage_batch<false>(packed, binned, start + cstart, n, tc, S);
+        stage_batch<false>(packed, binned, start + cstart, n, tc, o_plain, SH.S);
     __syncthreads();
-    for (int j = n - 1; j >= 0; --j) {
-      const uint32_t mask = __builtin_amdgcn_readlane(bmask, j);
-      if (mask == 0u) continue;
-      const float4 a2 = S.s2[j];
-      const int i = cstart + j;
-      const float4 a0 = S.s0[j];
-      const float4 a1 = S.s1[j];
-      const float dx = Q.px - a0.x;
-      float Adxdx, Bdx;
-      x_terms(a0.z, a0.w, dx, Adxdx, Bdx);
-      bool contrib = false;
-#pragma unroll
-      for (int k = 0; k < kPix; ++k) {
-        if (!((mask >> k) & 1u)) continue;  // scalar branch
-        // one combined test: composited in the forward (i < last) and visible
-        const float dy = Q.py[k] - a0.y;
-        const float p = splat_exponent(Adxdx, Bdx, a1.x, dy);
-        {
-          if (((!kCheckLast) | (i < Q.lk[k])) & (p <= 0.0f) & (p >= a2.z)) {
-            contrib = true;
-            const float e = __builtin_amdgcn_exp2f(p);
-            const float raw = a1.y * e;
-            const bool open = raw < max_alpha;  // gradient gate
-            const float alpha = open ? raw : max_alpha;
-            // 1 - alpha >= 1 - max_alpha >= eps (checked on the host), so the
-            // reference's max(1 - alpha, eps) is 1 - alpha.
-            const float T_prev =
-                Q.Tc[k] * __builtin_amdgcn_rcpf(1.0f - alpha);
-            const float dot_gc =
-                Q.gr[k] * a1.z + Q.gg[k] * a1.w + Q.gb[k] * a2.x;
-            const float diff = dot_gc - Q.gT[k];
-            const float wgt = T_prev * alpha;
-            acc_r += Q.gr[k] * wgt;
-            acc_g += Q.gg[k] * wgt;
-            acc_b += Q.gb[k] * wgt;
-            // alpha = raw when the gate is open, so T_prev raw = wgt
-            const float g_pow = open ? wgt * diff : 0.0f;
-            const float hdy = g_pow * dy;
-            S0 += g_pow;
-            S1 += hdy;
-            S2 += hdy * dy;
-            Q.gT[k] += alpha * diff;
-            Q.Tc[k] = T_prev;
-          }
-        }
-      }
-      if (__builtin_amdgcn_ballot_w64(contrib) != 0) {
-        // Per-lane parts of the splat's gradients (a, b, c = -2A/L, -B/L,
-        // -2C/L): g_mean = -(2/L) (V_mx, V_my), g_conic = (-V_ca/2, -V_cb,
-        // -V_cc/2) with V_cc = S2, and g_opacity = sum g_raw exp(power) =
-        // (sum g_power) / o = S0 / o.
-        const float X = dx * S0;             // sum g_power dx
-        const float hB = 0.5f * a0.w;
-        float* red_out = SH.red + lane;
-        red_out[0 * kLanes] = a0.z * X + hB * S1;  // V_mx
-        red_out[1 * kLanes] = hB * X + a1.x * S1;  // V_my
-        red_out[2 * kLanes] = dx * X;              // V_ca = sum g_power dx^2
-        red_out[3 * kLanes] = dx * S1;             // V_cb = sum g_power dx dy
-        red_out[4 * kLanes] = S2;
-        red_out[5 * kLanes] = acc_r;
-        red_out[6 * kLanes] = acc_g;
-        red_out[7 * kLanes] = acc_b;
-        const float r3 = wave_sum_row3(S0);
-        S0 = S1 = S2 = 0.f;
-        acc_r = acc_g = acc_b = 0.f;
-        wave_lds_sync();
-        const float4 u = *reinterpret_cast<const float4*>(red_in);
-        const float4 w = *reinterpret_cast<const float4*>(red_in + 32);
-        const float tot = group8_sum_dpp(((u.x + u.y) + (u.z + u.w)) +
-                                         ((w.x + w.y) + (w.z + w.w)));
-        const uint32_t orig = uniform_bits(a2.y);
-        if (group_head)
-          unsafeAtomicAdd(reinterpret_cast<float*>(
-                              reinterpret_cast<char*>(target.base) +
-                              (uint64_t)orig * target.stride),
-                          tot * target.scale);
-        if (lane == kLanes - 1)
-          unsafeAtomicAdd(g_opac + orig, r3 * a2.w);  // a2.w = 1 / opacity
-        wave_lds_sync();  // loads done before the next splat's stores
-      }
-    }
+    if (batch_plain(bmask))
+      bwd_batch<kCheckLast, true>(SH, bmask, n, cstart, max_alpha, target, Q,
+                                  g_opac);
+    else
+      bwd_batch<kCheckLast, false>(SH, bmask, n, cstart, max_alpha, target, Q,
+                                   g_opac);
   }
 }
 

@@ -322,6 +322,59 @@ def test_heavy_tiles_segmented_backward(gpu):
         _grad_close(c.cpu().numpy(), a.cpu().numpy(), name, rtol=1e-5)
 
 
+def test_plain_and_general_batches(gpu):
+    """The compositors drop the p <= 0 test and the max_alpha clamp/gate for a
+    batch whose records are all well-conditioned (positive-definite conic
+    with margin, opacity below max_alpha).  Here the left half of each image
+    also holds records that need the general path -- hair-thin splats
+    (sigma 0.02 x 20 px, conic too ill-conditioned for the shortcut) and a
+    few with opacity 0.995, whose alpha the clamp limits -- so left-half tiles
+    take the general path and right-half tiles the shortcut, in the
+    one-wavefront and the continuation kernels (tiles of several hundred
+    splats) and in the backward.  Checked against the tile oracle, and the
+    forward with and without the continuation kernel bit for bit."""
+    from torch_gsplat_bridge_fast import _lib, _ops
+
+    B, G, H, W = 2, 2500, 48, 80
+    sc = _faint_crowd(33, B, G, H, W)
+    g = torch.Generator().manual_seed(34)
+    left = sc["means2d"][..., 0] < W / 2
+    idx = torch.arange(G).expand(B, G)
+    thin = left & (idx % 5 == 0)
+    sc["conics"][thin] = torch.tensor([1.0 / 0.02 ** 2, 0.0, 1.0 / 20.0 ** 2])
+    bright = left & (idx % 50 == 1)
+    sc["opacities"][bright] = 0.995
+    sc["opacities"][left & (idx % 50 == 2)] = 0.99 * (1.0 - 2.0 ** -21)  # just above the shortcut's bound
+    sc["colors"] = torch.rand(B, G, 3, generator=g)
+    print(f"plain/general batches {W}x{H} B={B} G={G} thin={int(thin.sum())} bright={int(bright.sum())}",
+          flush=True)
+    w = torch.rand(B, H, W, 3, generator=torch.Generator().manual_seed(35))
+    img, grads = _run_gpu(sc, RasterConfig(height=H, width=W), w)
+    oimg, _, _, ostop, ograds, amb, tainted = _oracle_run(sc, H, W, B, G, (0.0, 0.0, 0.0), w)
+    assert int((ostop > 128).sum()) >= 10  # the continuation kernel runs
+    ok = amb.reshape(-1) == 0
+    assert (~ok).mean() <= MAX_AMBIGUOUS_FRACTION
+    np.testing.assert_allclose(img.numpy().reshape(-1, 3)[ok], oimg.reshape(-1, 3)[ok], rtol=1e-4, atol=1e-5)
+    assert tainted.mean() <= 0.10
+    keep = ~tainted
+    for name, gr, r in zip(KEYS[:4], grads, ograds):
+        n = r.shape[0]
+        _grad_close(gr.numpy().reshape(n, -1)[keep], r.reshape(n, -1)[keep], name)
+    meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, (0, 0, 0))
+    flat = [sc[k].reshape(B * G, -1).squeeze(-1).contiguous().to(gpu) for k in KEYS]
+    st = _ops.bin_gaussians(meta, *flat)
+    img_ws, T, last, stop, _ = _ops.render_forward(meta, st, save_state=True)
+    L = _lib.lib()
+    img1 = torch.empty_like(img_ws)
+    T1, last1, stop1 = torch.empty_like(T), torch.empty_like(last), torch.empty_like(stop)
+    _lib.check(L.gsplat_hip_render_forward(meta, _lib.ptr(st.packed), _lib.ptr(st.tile_offsets),
+                                           _lib.ptr(st.binned_ids), _lib.ptr(img1), _lib.ptr(T1), _lib.ptr(last1),
+                                           _lib.ptr(stop1), st.n_pairs, None, 0, _lib.stream_of(img1)),
+               "gsplat_hip_render_forward")
+    torch.cuda.synchronize()
+    assert torch.equal(img1, img_ws) and torch.equal(T1, T) and torch.equal(last1, last)
+
+
 def test_pair_budget_splits_training_launches(gpu):
     """max_pairs_per_launch (reference _choose_batch_slices, v8 rasterize.py:339-391):
     a budget below two images' pairs gives one launch per image; image and
