@@ -27,9 +27,13 @@
 //
 // Forward (reference tile_fast_forward_state, gsplat_v8_kernels.metal:400-476):
 //   C += T*alpha*c; T *= 1-alpha; a pixel stops after the splat that brings
-//   T <= transmittance_threshold.  Saves per pixel the final T and last = 1 +
-//   index of the last composited splat, and per tile the max of last, so the
-//   backward pass needs no forward replay.
+//   T <= transmittance_threshold.  Saves per pixel the final T and last, the
+//   reference's local_stop (:455-467): 1 + index of the splat that stopped
+//   the pixel, or the tile's pair count if it never stops.  The walk records
+//   the index of every blend, so a stopped pixel holds that of its stopping
+//   splat; pixels still alive at the end get the pair count.  Per tile the
+//   max of last (the stop count), so the backward pass needs no forward
+//   replay.
 // Backward (reference tile_fast_backward_saved, :478-608, and the recurrence
 // of docs/v8_critical_theory_notes.md:113-141): walks the tile range in
 // reverse from the tile's max(last); T_prev = T/(1-alpha),
@@ -525,8 +529,8 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
                            (T[3] > t_thr);
     if (__any(any_alive)) {
       // Close segment 0 and hand the rest of the tile to the four-wavefront
-      // kernel: T to the workspace, last to out_last, the colour sum is in
-      // the output.
+      // kernel: T to the workspace, last (of the blends so far) to out_last,
+      // the colour sum is in the output.
       int tail = -1, slot = -1;  // chain state, meaningful in lane 0
       if (threadIdx.x == 0) slot = next_segment(H, tc.tile, 0, tail);
       slot = __shfl(slot, 0, 64);
@@ -565,6 +569,7 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
     if (valid[k]) {
+      if (T[k] > t_thr) last[k] = end - start;  // never stopped: whole list
       const int64_t pix = pix0 + k * strip;
       // streaming stores: the per-pixel outputs are not read again here
       __builtin_nontemporal_store(cr[k] + T[k] * P.bg_r, out_rgb + 3 * pix + 0);
@@ -697,6 +702,7 @@ __global__ __launch_bounds__(256 / kSpW) void render_fwd_long_kernel(
 #pragma unroll
     for (int k = 0; k < kSpW; ++k) {
       if (valid[k]) {
+        if (T[k] > t_thr) last[k] = end - start;  // never stopped: whole list
         out_rgb[3 * pix[k] + 0] = cr[k] + T[k] * P.bg_r;
         out_rgb[3 * pix[k] + 1] = cg[k] + T[k] * P.bg_g;
         out_rgb[3 * pix[k] + 2] = cb[k] + T[k] * P.bg_b;

@@ -206,8 +206,11 @@ size_t gsplat_hip_render_workspace_bytes(const gsplat_raster_meta* meta,
  * 330-476).  out_rgb float [B,H,W,3].  State outputs (all NULL together for
  * the eval path): out_final_T float [B,H,W]
  * transmittance after the last composited splat, out_last int32 [B,H,W] =
- * 1 + index (within the tile range) of the last composited splat (0 if
- * none), out_tile_stop int32 [T] = max of out_last over the tile's pixels. */
+ * the reference's per-pixel stop count (local_stop, gsplat_v8_kernels.metal:
+ * 455-467): 1 + index (within the tile range) of the splat whose blend
+ * brought T to transmittance_threshold, or the tile's pair count if the
+ * pixel never stopped, out_tile_stop int32 [T] = max of out_last over the
+ * tile's pixels (the reference's stop count). */
 int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
                               const float* packed, const int32_t* tile_offsets,
                               const int32_t* binned_ids, float* out_rgb,

@@ -302,8 +302,10 @@ static int eval_alpha(const oracle_meta* M, const splat_t* s, float px, float py
   return 1;
 }
 
-/* out_rgb [B,H,W,3]; out_T [B,H,W]; out_last [B,H,W] = 1 + index of the last
- * composited splat in the tile list (0 if none); tile_stop [T] = max last. */
+/* out_rgb [B,H,W,3]; out_T [B,H,W]; out_last [B,H,W] = the reference's
+ * local_stop (gsplat_v8_kernels.metal:455-467): 1 + index in the tile list of
+ * the splat whose blend brought T to the threshold, or the list length if
+ * the pixel never stopped (every splat iterated); tile_stop [T] = max last. */
 void oracle_render_forward(const oracle_meta* M, const float* means2d, const float* conics,
                            const float* colors, const float* opac, const int32_t* perm,
                            const int32_t* tile_offsets, const int32_t* binned_ids,
@@ -325,6 +327,7 @@ void oracle_render_forward(const oracle_meta* M, const float* means2d, const flo
         int last = 0, amb = 0;
         float errT = 0.0f; /* bound on T's relative deviation from exp2 ulps */
         for (int i = start; i < end; ++i) {
+          last = i - start + 1; /* iterated while alive (reference :457) */
           const splat_t s = load_splat(M, means2d, conics, colors, opac, perm, binned_ids[i]);
           float alpha, raw, dx, dy;
           if (!eval_alpha(M, &s, (float)x + 0.5f, (float)y + 0.5f, &alpha, &raw, &dx, &dy, &amb)) continue;
@@ -334,7 +337,6 @@ void oracle_render_forward(const oracle_meta* M, const float* means2d, const flo
           errT += 2.4e-7f * alpha / (1.0f - alpha);
           if (fabsf(T - M->transmittance_threshold) <= (errT + 1e-6f) * M->transmittance_threshold)
             amb |= AMB_STOP;
-          last = i - start + 1;
           if (T <= M->transmittance_threshold) break;
         }
         const int64_t pix = ((int64_t)b * M->height + y) * M->width + x;

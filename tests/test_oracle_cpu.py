@@ -349,3 +349,40 @@ def test_golden_projection_regression():
                                     i["camera_params"], pc["near_plane"])
     for name, v in zip(("means2d", "conics", "opacities_out", "depths"), out):
         np.testing.assert_allclose(v.numpy(), np.array(pc["outputs"][name]), rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------ stop counts (local_stop)
+def _stop_scene(opacities, sigmas, means):
+    """One 16x16 tile; splats in depth order with isotropic sigmas."""
+    G = len(opacities)
+    s2 = np.asarray(sigmas, dtype=np.float32) ** 2
+    conics = np.stack([1.0 / s2, np.zeros(G, np.float32), 1.0 / s2], axis=1).astype(np.float32)
+    meta = TO.make_meta(16, 16, 1, G)
+    sc = TO.Scene(np.asarray(means, np.float32), conics, np.full((G, 3), 0.5, np.float32),
+                  np.asarray(opacities, np.float32), np.arange(1, G + 1, dtype=np.float32), 1, G)
+    bins = TO.bin_scene(meta, sc)
+    assert int(bins.tile_counts[0]) == G
+    return TO.render_forward(meta, sc, bins)
+
+
+def test_stop_count_of_pixels_that_never_stop_is_the_list_length():
+    """Reference tile_fast_forward_state (gsplat_v8_kernels.metal:455-467) sets
+    local_stop = j + 1 for every splat a live pixel iterates, visible or not:
+    two wide splats (alpha 0.9 each, T = 0.01 > 1e-4 after both) and a small one
+    seen only near the tile's corner.  Every pixel iterates all three."""
+    img, T, last, stop = _stop_scene([0.9, 0.9, 0.5], [1000.0, 1000.0, 1.0],
+                                     [[8.0, 8.0], [8.0, 8.0], [1.5, 1.5]])
+    assert np.all(T > 1e-4)
+    assert np.all(last == 3) and int(stop[0]) == 3
+    # the small splat is invisible at the far corner, so "last composited"
+    # would have been 2 there
+    assert abs(float(T[0, 15, 15]) - 0.01) < 1e-4
+
+
+def test_stop_count_is_one_past_the_stopping_splat():
+    """Five wide splats of alpha ~0.95: T = 0.05, 2.5e-3, 1.25e-4 (> 1e-4), then
+    6.3e-6 <= 1e-4, so every pixel stops at the fourth (local_stop = 4 and the
+    loop breaks, gsplat_v8_kernels.metal:467); the fifth is never iterated."""
+    img, T, last, stop = _stop_scene([0.95] * 5, [1000.0] * 5, [[8.0, 8.0]] * 5)
+    assert np.all((T > 5e-6) & (T < 7e-6))
+    assert np.all(last == 4) and int(stop[0]) == 4
