@@ -87,10 +87,12 @@ __device__ __forceinline__ int slot_y(const TileCoord& c, int k) {
   return c.y0 + 4 * k + c.ly;
 }
 
+// s2 first: the forward reads only its x and z (one ds_read2 whose 8-bit
+// dword offsets reach it from the batch's base address without an add).
 struct Staged {
+  float4 s2[kBatch];  // blue, orig index bits, plim, strip mask bits or 1/o
   float4 s0[kBatch];  // mx, my, A, B
   float4 s1[kBatch];  // C, opacity, r, g
-  float4 s2[kBatch];  // blue, orig index bits, plim, strip mask bits or 1/o
 };
 
 // Bit k set unless strip k of the tile at (x0, y0) certainly holds no pixel
