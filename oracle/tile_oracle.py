@@ -53,11 +53,15 @@ def lib():
         L.oracle_bin_fill.restype = None
         L.oracle_bin_fill.argtypes = [pm, vp, vp, vp, vp, vp, vp]
         L.oracle_render_forward.restype = None
-        L.oracle_render_forward.argtypes = [pm] + [vp] * 12
+        L.oracle_render_forward.argtypes = [pm] + [vp] * 13
         L.oracle_render_backward.restype = None
-        L.oracle_render_backward.argtypes = [pm] + [vp] * 12
-        L.oracle_taint.restype = None
-        L.oracle_taint.argtypes = [pm] + [vp] * 9
+        L.oracle_render_backward.argtypes = [pm] + [vp] * 16
+        L.oracle_render_backward_serial.restype = None
+        L.oracle_render_backward_serial.argtypes = [pm] + [vp] * 12
+        L.oracle_threads.restype = ctypes.c_int
+        L.oracle_threads.argtypes = []
+        L.oracle_set_threads.restype = None
+        L.oracle_set_threads.argtypes = [ctypes.c_int]
         _lib = L
     return _lib
 
@@ -142,47 +146,90 @@ def bin_scene(meta: OracleMeta, s: Scene) -> OracleBins:
     return OracleBins(perm, counts, offsets, ids)
 
 
-AMB_ALPHA, AMB_STOP, AMB_GATE = 1, 2, 4
+AMB_ALPHA, AMB_STOP, AMB_GATE, AMB_FORCED_BAD = 1, 2, 4, 8
+
+# Gradient entries per splat in the bound arrays of render_backward:
+# means2d x, y; conics a, b, c; colors r, g, b; opacity.
+GRAD_SLICES = {"means2d": slice(0, 2), "conics": slice(2, 5), "colors": slice(5, 8), "opacities": slice(8, 9)}
 
 
-def render_forward(meta: OracleMeta, s: Scene, bins: OracleBins, with_ambiguity: bool = False):
+def threads() -> int:
+    """Threads the oracle's parallel loops use (OMP_NUM_THREADS or the core count)."""
+    return int(lib().oracle_threads())
+
+
+def set_threads(n: int) -> None:
+    """Thread count of the oracle's parallel loops (results do not depend on it)."""
+    lib().oracle_set_threads(int(n))
+
+
+def _force(meta: OracleMeta, force_last):
+    if force_last is None:
+        return None
+    f = np.ascontiguousarray(force_last, dtype=np.int32)
+    assert f.shape == (meta.batch, meta.height, meta.width)
+    return f
+
+
+def render_forward(meta: OracleMeta, s: Scene, bins: OracleBins, with_ambiguity: bool = False, force_last=None):
     """Returns (img, final_T, last, tile_stop[, ambiguity]).  ambiguity[b,y,x] is a
     bit mask: AMB_STOP when an early-stop decision of the pixel lies within
     exp's last-ulp window (another implementation with a 1-ulp exp2 may decide
     it the other way), AMB_GATE likewise for the max_alpha gradient gate.  The
-    alpha-threshold decision itself is exact (AMB_ALPHA is never set)."""
+    alpha-threshold decision itself is exact (AMB_ALPHA is never set).
+
+    force_last [B,H,W] int32 (-1 = the oracle decides): walk exactly that many
+    records of the pixel's tile list (another implementation's stop count);
+    AMB_FORCED_BAD marks pixels where that decision lies outside the window."""
     B, H, W = meta.batch, meta.height, meta.width
     img = np.empty((B, H, W, 3), dtype=np.float32)
     T = np.empty((B, H, W), dtype=np.float32)
     last = np.empty((B, H, W), dtype=np.int32)
     stop = np.empty(bins.tile_counts.size, dtype=np.int32)
     amb = np.empty((B, H, W), dtype=np.uint8)
+    f = _force(meta, force_last)
     lib().oracle_render_forward(ctypes.byref(meta), _p(s.means2d), _p(s.conics), _p(s.colors), _p(s.opacities),
-                                _p(bins.perm), _p(bins.tile_offsets), _p(bins.binned_ids), _p(img), _p(T), _p(last),
-                                _p(stop), _p(amb))
+                                _p(bins.perm), _p(bins.tile_offsets), _p(bins.binned_ids), _p(f), _p(img), _p(T),
+                                _p(last), _p(stop), _p(amb))
     if with_ambiguity:
         return img, T, last, stop, amb
     return img, T, last, stop
 
 
-def tainted_splats(meta: OracleMeta, s: Scene, bins: OracleBins, amb: np.ndarray) -> np.ndarray:
-    """Boolean [B*G] (original order): splats visible at some ambiguous pixel.
-    Their gradients may legitimately differ between two exact implementations."""
-    out = np.zeros(s.B * s.G, dtype=np.uint8)
-    a = np.ascontiguousarray(amb, dtype=np.uint8)
-    lib().oracle_taint(ctypes.byref(meta), _p(s.means2d), _p(s.conics), _p(s.colors), _p(s.opacities),
-                       _p(bins.perm), _p(bins.tile_offsets), _p(bins.binned_ids), _p(a), _p(out))
-    return out.astype(bool)
+def render_backward(meta: OracleMeta, s: Scene, bins: OracleBins, grad_img, force_last=None,
+                    with_bounds: bool = False):
+    """Gradients (original order) (g_means2d [BG,2], g_conics [BG,3], g_colors
+    [BG,3], g_opacities [BG]); with_bounds adds a dict of float64 [BG, 9]
+    arrays "mag", "chain" and "slack" (tile_oracle.c: oracle_render_backward)
+    from which parity.grad_bound forms each entry's rounding allowance."""
+    n = s.B * s.G
+    g = _f32(grad_img, (meta.batch, meta.height, meta.width, 3))
+    gm = np.empty((n, 2), dtype=np.float32)
+    gq = np.empty((n, 3), dtype=np.float32)
+    gc = np.empty((n, 3), dtype=np.float32)
+    go = np.empty((n,), dtype=np.float32)
+    bounds = {k: np.empty((n, 9), dtype=np.float64) for k in ("mag", "chain", "slack")} if with_bounds else None
+    f = _force(meta, force_last)
+    lib().oracle_render_backward(ctypes.byref(meta), _p(s.means2d), _p(s.conics), _p(s.colors), _p(s.opacities),
+                                 _p(bins.perm), _p(bins.tile_offsets), _p(bins.binned_ids), _p(f), _p(g), _p(gm),
+                                 _p(gq), _p(gc), _p(go), *(_p(bounds[k]) if bounds else None
+                                                           for k in ("mag", "chain", "slack")))
+    if with_bounds:
+        return (gm, gq, gc, go), bounds
+    return gm, gq, gc, go
 
 
-def render_backward(meta: OracleMeta, s: Scene, bins: OracleBins, grad_img):
+def render_backward_serial(meta: OracleMeta, s: Scene, bins: OracleBins, grad_img):
+    """The same gradients accumulated as the reference kernels do (float32
+    sums in pixel order, one thread): the restatement render_backward is
+    checked against."""
     n = s.B * s.G
     g = _f32(grad_img, (meta.batch, meta.height, meta.width, 3))
     gm = np.zeros((n, 2), dtype=np.float32)
     gq = np.zeros((n, 3), dtype=np.float32)
     gc = np.zeros((n, 3), dtype=np.float32)
     go = np.zeros((n,), dtype=np.float32)
-    lib().oracle_render_backward(ctypes.byref(meta), _p(s.means2d), _p(s.conics), _p(s.colors), _p(s.opacities),
-                                 _p(bins.perm), _p(bins.tile_offsets), _p(bins.binned_ids), _p(g), _p(gm), _p(gq),
-                                 _p(gc), _p(go))
+    lib().oracle_render_backward_serial(ctypes.byref(meta), _p(s.means2d), _p(s.conics), _p(s.colors),
+                                        _p(s.opacities), _p(bins.perm), _p(bins.tile_offsets), _p(bins.binned_ids),
+                                        _p(g), _p(gm), _p(gq), _p(gc), _p(go))
     return gm, gq, gc, go

@@ -20,6 +20,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import parity
 from oracle import tile_oracle as TO
 from oracle.dense_reference import dense_reference, project_pinhole_reference
 from torch_gsplat_bridge_fast.scenes import make_scene_2d
@@ -293,9 +294,14 @@ def test_golden_config0_regression():
     np.testing.assert_allclose(img[0, 200:264, 300:364], g["img_crop"], rtol=1e-6, atol=1e-7)
     np.testing.assert_array_equal(stop, g["tile_stop"])
     w = torch.rand(H, W, 3, generator=torch.Generator().manual_seed(123)).numpy()
-    gm, gq, gc, go = TO.render_backward(meta, s, bins, w[None])
-    for name, v in (("g_means2d", gm), ("g_conics", gq), ("g_colors", gc), ("g_opacities", go)):
+    # the fixture holds the reference-order float32 sums (render_backward_serial)
+    serial = TO.render_backward_serial(meta, s, bins, w[None])
+    for name, v in zip(("g_means2d", "g_conics", "g_colors", "g_opacities"), serial):
         np.testing.assert_allclose(v, g[name], rtol=1e-6, atol=1e-6 * max(1.0, float(np.abs(g[name]).max())))
+    # the parallel double-sum backward agrees with them within its own bounds
+    got, bounds = TO.render_backward(meta, s, bins, w[None], with_bounds=True)
+    fixture = [g[k] for k in ("g_means2d", "g_conics", "g_colors", "g_opacities")]
+    parity.check_grads(fixture, got, bounds, parity.tiles_per_splat(bins, B, G), "config0 fixture")
 
 
 def test_golden_reference_hand_case_values():
