@@ -608,6 +608,44 @@ int gsplat_hip_project_backward(
       workspace, static_cast<hipStream_t>(stream));
 }
 
+int gsplat_hip_project_backward_noalloc(
+    const gsplat_project_meta* meta, const float* grad_means2d,
+    const float* grad_conics, const float* grad_opacities,
+    const float* grad_depths, const float* means3d, const float* scales,
+    const float* quats, const float* opacities, const float* camera_to_world,
+    const float* camera_params, float* g_means3d, float* g_scales,
+    float* g_quats, float* g_opacities, float* g_camera_to_world,
+    float* g_camera_params, void* stream) {
+  gs::ProjectParams P;
+  int rc = make_project_params(meta, P);
+  if (rc) return rc;
+  rc = null_check({grad_means2d, grad_conics, grad_opacities, grad_depths,
+                   means3d, scales, quats, opacities, camera_to_world,
+                   camera_params, g_means3d, g_scales, g_quats, g_opacities,
+                   g_camera_to_world, g_camera_params},
+                  "gsplat_hip_project_backward_noalloc");
+  if (rc) return rc;
+  const size_t need = gs::project_backward_workspace_bytes(P);
+  if (need > GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES) {
+    gs::set_error(
+        "gsplat_hip_project_backward_noalloc: B * ceil(G/256) * 64 bytes = %zu "
+        "exceeds the static scratch of %d bytes (B * ceil(G/256) <= %d); use "
+        "gsplat_hip_project_backward with a workspace",
+        need, GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES,
+        GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES / 64);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* scratch = nullptr;
+  rc = gs::project_noalloc_scratch(s, &scratch);
+  if (rc) return rc;
+  return gs::launch_project_backward(
+      P, grad_means2d, grad_conics, grad_opacities, grad_depths, means3d,
+      scales, quats, opacities, camera_to_world, camera_params, g_means3d,
+      g_scales, g_quats, g_opacities, g_camera_to_world, g_camera_params,
+      scratch, s);
+}
+
 size_t gsplat_hip_project_backward_workspace_bytes(
     const gsplat_project_meta* meta) {
   gs::ProjectParams P;

@@ -184,6 +184,9 @@ int launch_project_backward(const ProjectParams& P, const float* g_means2d,
                             hipStream_t stream);
 // Camera-gradient partial sums: B * ceil(G/256) * 16 floats.
 size_t project_backward_workspace_bytes(const ProjectParams& P);
+// Device address (on the stream's device) of the static scratch array of
+// the allocation-free projection backward; looked up once per device.
+int project_noalloc_scratch(hipStream_t stream, void** out);
 
 // Maps a linear workgroup id onto a linear work index so that the 8 XCDs of
 // an MI355X (which receive workgroups round-robin) each process one

@@ -21,7 +21,17 @@
 // (reference :338-342).  Camera gradients are summed per workgroup (one
 // image per workgroup) into a workspace and reduced by a second launch in a
 // fixed order, without atomics.
+#include <mutex>
+
 #include "gs_internal.h"
+
+// Camera-gradient partial sums of the allocation-free backward
+// (gsplat_hip_project_backward_noalloc): a file-scope device array instead
+// of a caller workspace.  Every GPU the library runs on holds its own copy
+// until the process ends.  In host code `scratch` names a host-side stand-in,
+// not device memory: its device address is looked up once per device
+// (project_noalloc_scratch) and only that address is passed to kernels.
+static __device__ __align__(256) float scratch[GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES / sizeof(float)];
 
 namespace gs {
 namespace {
@@ -402,6 +412,43 @@ int launch_project_forward(const ProjectParams& P, const float* means3d,
                      P, means3d, scales, quats, opacities, c2w, cam,
                      out_means2d, out_conics, out_opac, out_depths);
   return check_launch("project_fwd_kernel");
+}
+
+namespace {
+constexpr int kMaxDevices = 256;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device
+}  // namespace
+
+int project_noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipStreamGetDevice(stream, &dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    set_error("project_backward_noalloc: cannot resolve the stream's device (%s)",
+              e != hipSuccess ? hipGetErrorString(e) : "device index out of range");
+    return GSPLAT_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    // hipGetSymbolAddress resolves the symbol on the current device: make the
+    // stream's device current for the lookup and restore the caller's after.
+    int cur = 0;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      set_error("project_backward_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                e != hipSuccess ? hipGetErrorString(e) : "null address");
+      return GSPLAT_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GSPLAT_OK;
 }
 
 size_t project_backward_workspace_bytes(const ProjectParams& P) {

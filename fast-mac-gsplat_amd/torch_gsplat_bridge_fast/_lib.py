@@ -17,9 +17,10 @@ import torch  # noqa: F401  (must be loaded before the HIP library)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("GSPLAT_HIP_LIB", os.path.join(_HERE, "lib", "libgsplat_hip.so"))
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 TILE_SIZE = 16
 RECORD_FLOATS = 12
+PROJECT_NOALLOC_SCRATCH_BYTES = 1 << 20   # GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -75,6 +76,7 @@ SIGNATURES = {
     "gsplat_hip_project_forward": (ctypes.c_int, [_PP] + [_vp] * 10 + [_vp]),
     "gsplat_hip_project_backward_workspace_bytes": (_sz, [_PP]),
     "gsplat_hip_project_backward": (ctypes.c_int, [_PP] + [_vp] * 16 + [_vp, _sz, _vp]),
+    "gsplat_hip_project_backward_noalloc": (ctypes.c_int, [_PP] + [_vp] * 16 + [_vp]),
     "gsplat_hip_scan_workspace_bytes": (_sz, [_i64]),
     "gsplat_hip_exclusive_scan_i32": (ctypes.c_int, [_vp, _vp, _i64, _vp, _sz, _vp]),
     "gsplat_hip_radix_sort_workspace_bytes": (_sz, [_i64, _i32]),

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 7
+#define GSPLAT_HIP_ABI_VERSION 8
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -278,6 +278,31 @@ int gsplat_hip_project_backward(const gsplat_project_meta* meta,
                                 float* g_camera_params,
                                 void* workspace, size_t workspace_bytes,
                                 void* stream);
+
+/* Allocation-free variant of gsplat_hip_project_backward.  It has no
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, results and kernels as
+ * gsplat_hip_project_backward, without the workspace: the camera-gradient
+ * partial sums go to a static device array of
+ * GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends
+ * and looked up on the stream's device at the first call there.  Limit:
+ * B * ceil(G / 256) * 64 bytes must fit, i.e. B * ceil(G / 256) <= 16384
+ * (B = 1: up to 4,194,304 splats); larger problems return
+ * GSPLAT_ERR_INVALID_ARGUMENT.  Every slot of the array that a call reads
+ * is written earlier by the same call, so nothing is cleared between calls.
+ * All calls on one GPU share the array: calls that overlap on one GPU (on
+ * different streams, or from different threads) race and must be ordered
+ * by the caller.  Calls no hipMalloc, hipFree or allocating routine. */
+#define GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES (1 << 20)
+int gsplat_hip_project_backward_noalloc(
+    const gsplat_project_meta* meta, const float* grad_means2d,
+    const float* grad_conics, const float* grad_opacities,
+    const float* grad_depths, const float* means3d, const float* scales,
+    const float* quats, const float* opacities, const float* camera_to_world,
+    const float* camera_params, float* g_means3d, float* g_scales,
+    float* g_quats, float* g_opacities, float* g_camera_to_world,
+    float* g_camera_params, void* stream);
 
 /* ------------------------------------------------------------- primitives
  * Device-wide building blocks used by the stages above, exported so they can
