@@ -233,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
     const float* __restrict__ opacities, const uint32_t* __restrict__ perm,
     const int32_t* __restrict__ splat_count, float4* __restrict__ packed,
     int32_t* __restrict__ splat_offsets, uint64_t* scan_status,
-    uint32_t* scan_ticket) {
+    uint32_t* scan_ticket, uint32_t* err) {
   __shared__ int wsum[kThreads / 64];
   __shared__ long long s_prefix;
   const int vb = take_ticket(scan_ticket);
@@ -241,7 +241,9 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
   int n = 0;
   if (gid < P.num_splats) {
     const int batch = gid / P.gpb;
-    const int orig = batch * P.gpb + (int)perm[gid];
+    // (perm is in [0, G) unless a look-back of the depth sort gave up; the
+    // clamp keeps the gathers in bounds then, and the status reports it)
+    const int orig = batch * P.gpb + (int)min(perm[gid], (uint32_t)(P.gpb - 1));
     const float mx = means2d[2 * orig + 0];
     const float my = means2d[2 * orig + 1];
     const float a = conics[3 * orig + 0];
@@ -280,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
                                          (uint64_t)(uint32_t)total);
     uint64_t prefix = 0;
     if (vb > 0) {
-      prefix = lookback64_wave(scan_status, vb);
+      prefix = lookback64_wave(scan_status, vb, err);
       if (lane == 0)
         status_store(&scan_status[vb], kFlagInc64 | (prefix + (uint32_t)total));
     }
@@ -389,12 +391,32 @@ __global__ __launch_bounds__(kThreads) void hist_reduce_kernel(
 // keys to a few thousand workgroups.
 constexpr int kRangeUnroll = 4;
 constexpr int kRangeMaxBlocks = 2048;
+struct StatusWords {
+  const uint32_t* err[3];  // give-up status words (null: not used)
+  int32_t* out;            // their OR (null: not reported)
+};
+
 __global__ __launch_bounds__(kThreads) void ranges_kernel(
     const uint32_t* __restrict__ sorted_keys, int64_t n_cap,
     const int32_t* __restrict__ n_dev, int num_tiles,
-    int32_t* __restrict__ tile_offsets) {
-  const int64_t n = n_dev ? min(n_cap, (int64_t)max(*n_dev, 0)) : n_cap;
+    int32_t* __restrict__ tile_offsets, StatusWords sw) {
+  // Every look-back of the binning ran in an earlier launch.  If one gave
+  // up, the pairs may hold unwritten entries: every tile is emptied instead
+  // (the compositors then read no pair), and the status says why.
+  uint32_t e = 0u;
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+    if (sw.err[k] != nullptr) e |= *sw.err[k];
+  if (sw.out != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+    *sw.out = (int32_t)e;
   const int64_t stride = (int64_t)gridDim.x * kThreads;
+  if (e != 0u) {
+    for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+         t <= num_tiles; t += stride)
+      tile_offsets[t] = 0;
+    return;
+  }
+  const int64_t n = n_dev ? min(n_cap, (int64_t)max(*n_dev, 0)) : n_cap;
   for (int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; i0 <= n;
        i0 += kRangeUnroll * stride) {
     uint32_t kp[kRangeUnroll], kc[kRangeUnroll];
@@ -409,7 +431,8 @@ __global__ __launch_bounds__(kThreads) void ranges_kernel(
       const int64_t i = i0 + u * stride;
       if (i > n) break;
       const int64_t prev = (i == 0) ? -1 : (int64_t)kp[u];
-      const int64_t cur = (i == n) ? (int64_t)num_tiles : (int64_t)kc[u];
+      const int64_t cur = (i == n) ? (int64_t)num_tiles
+                                   : min((int64_t)kc[u], (int64_t)num_tiles);
       for (int64_t t = prev + 1; t <= cur; ++t) tile_offsets[t] = (int32_t)i;
     }
   }
@@ -482,13 +505,13 @@ int launch_pack(const RasterParams& P, const float* means2d,
                 const float* opacities, const uint32_t* perm,
                 const int32_t* splat_count, float* packed,
                 int32_t* splat_offsets, uint64_t* scan_status,
-                uint32_t* scan_ticket, hipStream_t stream) {
+                uint32_t* scan_ticket, uint32_t* err, hipStream_t stream) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
   hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(kThreads), 0, stream, P,
                      means2d, conics, colors, opacities, perm, splat_count,
                      reinterpret_cast<float4*>(packed), splat_offsets,
-                     scan_status, scan_ticket);
+                     scan_status, scan_ticket, err);
   return check_launch("pack_kernel");
 }
 
@@ -525,17 +548,22 @@ int launch_emit(const RasterParams& P, const float* packed,
 
 int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        int32_t* tile_offsets, int32_t* tile_counts,
-                       hipStream_t stream, const int32_t* n_dev) {
-  if (num_tiles <= 0) return GSPLAT_OK;
+                       hipStream_t stream, const int32_t* n_dev,
+                       const uint32_t* err0, const uint32_t* err1,
+                       const uint32_t* err2, int32_t* status_out) {
+  if (num_tiles <= 0)
+    return status_out ? launch_fill_i32(status_out, 0, 1, stream) : GSPLAT_OK;
+  const StatusWords sw{{err0, err1, err2}, status_out};
   int rc;
   if (n == 0) {
     rc = launch_fill_i32(tile_offsets, 0, (int64_t)num_tiles + 1, stream);
+    if (!rc && status_out) rc = launch_fill_i32(status_out, 0, 1, stream);
   } else {
     int64_t grid = (n + 1 + kThreads - 1) / kThreads;
     if (grid > kRangeMaxBlocks) grid = kRangeMaxBlocks;
     hipLaunchKernelGGL(ranges_kernel, dim3((unsigned)grid), dim3(kThreads), 0,
                        stream, sorted_keys, n, n_dev, num_tiles,
-                       tile_offsets);
+                       tile_offsets, sw);
     rc = check_launch("ranges_kernel");
   }
   if (rc || tile_counts == nullptr) return rc;

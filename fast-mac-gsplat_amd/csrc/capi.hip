@@ -126,8 +126,9 @@ int null_check(std::initializer_list<const void*> ptrs, const char* what) {
 
 // Binning workspace shared by bin_count, bin_depth_order, bin_pack and
 // bin_emit: a control region (the depth sort's control block, zeroed by
-// bin_depth_order; then the pack-scan look-back status and ticket and the
-// pair sort's histograms and tickets, zeroed by bin_count), then the
+// bin_depth_order; then the pack-scan look-back status, its ticket (word 0)
+// and give-up status (word 1), and the pair sort's histograms, tickets
+// (words 0-3) and give-up status (word 4), zeroed by bin_count), then the
 // per-splat tile-hit counts (original order), the count workgroups' sums and
 // the depth sort's buffers (the onesweep's ping-pong buffers, or the sorted
 // runs and samples of the two-launch sort of small images).  bin_count and
@@ -302,7 +303,9 @@ int gsplat_hip_bin_pack(const gsplat_raster_meta* meta, const float* means2d,
                          reinterpret_cast<const int32_t*>(base + L.splat_count),
                          packed, splat_offsets,
                          reinterpret_cast<uint64_t*>(base + L.scan_status),
-                         reinterpret_cast<uint32_t*>(base + L.scan_ticket), s);
+                         reinterpret_cast<uint32_t*>(base + L.scan_ticket),
+                         reinterpret_cast<uint32_t*>(base + L.scan_ticket) + 1,
+                         s);
   return rc;
 }
 
@@ -316,9 +319,10 @@ size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
 int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
                         const int32_t* splat_offsets, int64_t n_pairs,
                         int32_t* binned_ids, int32_t* tile_counts,
-                        int32_t* tile_offsets, void* count_workspace,
-                        size_t count_workspace_bytes, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+                        int32_t* tile_offsets, int32_t* status,
+                        void* count_workspace, size_t count_workspace_bytes,
+                        void* workspace, size_t workspace_bytes,
+                        void* stream) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -330,14 +334,24 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
   rc = null_check({tile_offsets}, "gsplat_hip_bin_emit");
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // give-up status words of the binning's look-backs (pack scan, pair sort,
+  // and the onesweep depth sort of large images)
+  const CountLayout C = count_layout(P);
+  char* cbase = static_cast<char*>(count_workspace);
+  const uint32_t* err_pack =
+      cbase ? reinterpret_cast<const uint32_t*>(cbase + C.scan_ticket) + 1 : nullptr;
+  const uint32_t* err_pairs =
+      cbase ? reinterpret_cast<const uint32_t*>(cbase + C.pair_tickets) + 4 : nullptr;
+  const uint32_t* err_depth =
+      (cbase && !gs::depth_small_ok(P.gpb)) ? gs::radix_ctl_at(C.depth, cbase).err : nullptr;
   if (n_pairs == 0 || P.num_splats == 0)
     return gs::launch_tile_ranges(nullptr, 0, P.num_tiles, tile_offsets,
-                                  tile_counts, s);
+                                  tile_counts, s, nullptr, err_pack, nullptr,
+                                  err_depth, status);
   rc = null_check({packed, splat_offsets, binned_ids, count_workspace,
                    workspace},
                   "gsplat_hip_bin_emit");
   if (rc) return rc;
-  const CountLayout C = count_layout(P);
   const EmitLayout L = emit_layout(P, n_pairs);
   if (count_workspace_bytes < C.total || workspace_bytes < L.total) {
     gs::set_error("gsplat_hip_bin_emit: workspace too small (%zu < %zu or %zu < %zu)",
@@ -348,14 +362,14 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
     gs::set_error("gsplat_hip_bin_emit: too many pairs");
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
-  char* cbase = static_cast<char*>(count_workspace);
   char* base = static_cast<char*>(workspace);
   uint32_t* keys = reinterpret_cast<uint32_t*>(base + L.keys);
   uint32_t* vals = reinterpret_cast<uint32_t*>(base + L.vals);
   uint32_t* sorted_keys = reinterpret_cast<uint32_t*>(base + L.sorted_keys);
   const gs::RadixCtl ctl{reinterpret_cast<uint32_t*>(cbase + C.pair_ghist),
                          reinterpret_cast<uint32_t*>(base + L.status),
-                         reinterpret_cast<uint32_t*>(cbase + C.pair_tickets)};
+                         reinterpret_cast<uint32_t*>(cbase + C.pair_tickets),
+                         reinterpret_cast<uint32_t*>(cbase + C.pair_tickets) + 4};
   // The pair count N is read on the device (splat_offsets[BG], written by
   // bin_pack); n_pairs is the capacity of the buffers and every stage takes
   // the first min(N, n_pairs) pairs.
@@ -370,10 +384,11 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
     rc = gs::radix_passes(L.pairs, ctl, base + L.buffers, keys, vals, nullptr,
                           sorted_keys, reinterpret_cast<uint32_t*>(binned_ids),
                           s, n_dev);
-  // 3. tile ranges and counts from the sorted keys
+  // 3. tile ranges and counts from the sorted keys, and the look-back status
   if (!rc)
     rc = gs::launch_tile_ranges(sorted_keys, n_pairs, P.num_tiles,
-                                tile_offsets, tile_counts, s, n_dev);
+                                tile_offsets, tile_counts, s, n_dev, err_pack,
+                                err_pairs, err_depth, status);
   return rc;
 }
 
@@ -390,10 +405,10 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
                    const float* opacities, const float* depths,
                    int64_t capacity, int32_t* perm, float* packed,
                    int32_t* splat_offsets, int32_t* binned_ids,
-                   int32_t* tile_offsets, int32_t* pair_count_host,
+                   int32_t* tile_offsets, int32_t* host_words,
                    void* workspace, size_t workspace_bytes, void* stream,
                    void* count_stream, void* inputs_event,
-                   void* count_event) {
+                   void* count_event, void* status_event) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -408,7 +423,7 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipStream_t cs = count_stream ? static_cast<hipStream_t>(count_stream) : s;
   if (cs != s && (inputs_event == nullptr || count_event == nullptr)) {
-    gs::set_error("gsplat_hip_bin: a count stream needs both events");
+    gs::set_error("gsplat_hip_bin: a count stream needs the events");
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
   const size_t cbytes = gs::align_up(count_layout(P).total, 256);
@@ -420,13 +435,15 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
   }
   char* base = static_cast<char*>(workspace);
   int32_t* n_dev = reinterpret_cast<int32_t*>(base);
+  int32_t* status_dev = n_dev + 1;
   void* cws = base + 256;
   void* ews = base + 256 + cbytes;
   const size_t ebytes = workspace_bytes - 256 - cbytes;
   hipEvent_t ev_in = static_cast<hipEvent_t>(inputs_event);
   hipEvent_t ev_n = static_cast<hipEvent_t>(count_event);
+  hipEvent_t ev_st = static_cast<hipEvent_t>(status_event);
   // 1. per-splat hit counts and N on the count stream (after the caller's
-  //    work on `stream`), N copied to the host
+  //    work on `stream`)
   if (cs != s) {
     rc = hip_status(hipEventRecord(ev_in, s), "gsplat_hip_bin: event record");
     if (!rc)
@@ -436,10 +453,6 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
   }
   rc = gsplat_hip_bin_count(meta, means2d, conics, opacities, n_dev, cws,
                             cbytes, cs);
-  if (!rc && pair_count_host != nullptr)
-    rc = hip_status(hipMemcpyAsync(pair_count_host, n_dev, sizeof(int32_t),
-                                   hipMemcpyDeviceToHost, cs),
-                    "gsplat_hip_bin: pair count copy");
   if (!rc && ev_n != nullptr)
     rc = hip_status(hipEventRecord(ev_n, cs), "gsplat_hip_bin: event record");
   if (rc) return rc;
@@ -451,13 +464,22 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
                     "gsplat_hip_bin: stream wait");
     if (rc) return rc;
   }
-  // 3. records and offsets, 4. pairs, pair sort and tile ranges
+  // 3. records and offsets, 4. pairs, pair sort, tile ranges and the
+  //    look-back status (next to N in the workspace header)
   rc = gsplat_hip_bin_pack(meta, means2d, conics, colors, opacities, perm,
                            packed, splat_offsets, cws, cbytes, s);
   if (rc) return rc;
-  return gsplat_hip_bin_emit(meta, packed, splat_offsets, capacity,
-                             binned_ids, nullptr, tile_offsets, cws, cbytes,
-                             ews, ebytes, s);
+  rc = gsplat_hip_bin_emit(meta, packed, splat_offsets, capacity, binned_ids,
+                           nullptr, tile_offsets, status_dev, cws, cbytes, ews,
+                           ebytes, s);
+  if (rc || host_words == nullptr) return rc;
+  // 5. N and the status to the host in one copy
+  rc = hip_status(hipMemcpyAsync(host_words, n_dev, 2 * sizeof(int32_t),
+                                 hipMemcpyDeviceToHost, s),
+                  "gsplat_hip_bin: pair count and status copy");
+  if (!rc && ev_st != nullptr)
+    rc = hip_status(hipEventRecord(ev_st, s), "gsplat_hip_bin: event record");
+  return rc;
 }
 
 int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
@@ -658,8 +680,8 @@ size_t gsplat_hip_scan_workspace_bytes(int64_t n) {
 }
 
 int gsplat_hip_exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n,
-                                  void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+                                  int32_t* status, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
   if (n > 0x7fffffffLL) {
     gs::set_error("exclusive_scan: n too large");
     return GSPLAT_ERR_INVALID_ARGUMENT;
@@ -668,7 +690,27 @@ int gsplat_hip_exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n,
   int rc = null_check({n > 0 ? in : out, out}, "gsplat_hip_exclusive_scan_i32");
   if (rc) return rc;
   return gs::exclusive_scan_i32(in, out, n, workspace, workspace_bytes,
-                                static_cast<hipStream_t>(stream));
+                                static_cast<hipStream_t>(stream), false,
+                                status);
+}
+
+int gsplat_hip_debug_stalled_scan(const int32_t* in, int32_t* out, int64_t n,
+                                  int32_t stalled_blocks, int32_t spin_limit,
+                                  int32_t* status, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  const int64_t blocks = n <= 0 ? 1 : (n + 4095) / 4096;
+  if (n <= 0 || n > 0x7fffffffLL || stalled_blocks < 0 ||
+      stalled_blocks >= blocks || spin_limit < 0) {
+    gs::set_error("gsplat_hip_debug_stalled_scan: need 0 < n, 0 <= "
+                  "stalled_blocks < %lld blocks, spin_limit >= 0",
+                  (long long)blocks);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  int rc = null_check({in, out, status}, "gsplat_hip_debug_stalled_scan");
+  if (rc) return rc;
+  return gs::exclusive_scan_i32(in, out, n, workspace, workspace_bytes,
+                                static_cast<hipStream_t>(stream), false,
+                                status, stalled_blocks, spin_limit);
 }
 
 size_t gsplat_hip_radix_sort_workspace_bytes(int64_t n_per_segment,
@@ -681,12 +723,12 @@ int gsplat_hip_radix_sort_pairs_u32(const uint32_t* keys_in,
                                     uint32_t* keys_out, uint32_t* vals_out,
                                     int64_t n_per_segment, int32_t segments,
                                     int32_t begin_bit, int32_t end_bit,
-                                    void* workspace, size_t workspace_bytes,
-                                    void* stream) {
+                                    int32_t* status, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
   return gs::radix_sort_pairs(keys_in, vals_in, nullptr, keys_out, vals_out,
                               n_per_segment, segments, begin_bit, end_bit,
                               workspace, workspace_bytes,
-                              static_cast<hipStream_t>(stream));
+                              static_cast<hipStream_t>(stream), status);
 }
 
 }  // extern "C"

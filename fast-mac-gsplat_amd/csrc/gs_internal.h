@@ -49,10 +49,15 @@ __device__ __forceinline__ uint32_t depth_key(float f) {
 // ---- scan (scan.hip)
 size_t scan_workspace_bytes(int64_t n);
 // ctl_zeroed: the workspace's look-back status and ticket are already zero
-// (otherwise they are zeroed by an extra launch).
+// (otherwise they are zeroed by an extra launch).  status_out (device int32,
+// may be null): receives 0 or GSPLAT_STATUS_LOOKBACK_TIMEOUT (zeroed by the
+// same launch).  first_ticket > 0 (diagnostic only): workgroup tickets start
+// there, so the first first_ticket blocks are never scanned and their
+// look-back statuses never published; spin_limit bounds each wait.
 int exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n, void* ws,
                        size_t ws_bytes, hipStream_t stream,
-                       bool ctl_zeroed = false);
+                       bool ctl_zeroed = false, int32_t* status_out = nullptr,
+                       int first_ticket = 0, int spin_limit = 1 << 20);
 
 // ---- radix sort (radix_sort.hip)
 // Layout of one sort: a control block (global digit histograms, look-back
@@ -68,7 +73,10 @@ struct RadixPlan {
 struct RadixCtl {
   uint32_t* ghist;    // [4][segments][256]
   uint32_t* status;   // [passes][segments][nblk][256]
-  uint32_t* tickets;  // [4]
+  uint32_t* tickets;  // [4] (ticket_words = 8: the tickets, then the error
+                      // word radix_ctl_at points err at)
+  uint32_t* err;      // look-back give-up status (GSPLAT_STATUS_*), zeroed
+                      // with the control block
 };
 RadixPlan radix_plan(int64_t n_seg, int segments, int begin_bit, int end_bit);
 size_t radix_ctl_bytes(const RadixPlan& L);
@@ -90,11 +98,13 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
                  uint32_t* vals_out, hipStream_t stream,
                  const int32_t* n_dev = nullptr);
 // Self-contained sort (zeroes its control block, computes the histograms).
+// status_out (device int32, may be null): receives 0 or
+// GSPLAT_STATUS_LOOKBACK_TIMEOUT.
 int radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in,
                      const float* depth_src, uint32_t* keys_out,
                      uint32_t* vals_out, int64_t n_per_segment, int segments,
                      int begin_bit, int end_bit, void* ws, size_t ws_bytes,
-                     hipStream_t stream);
+                     hipStream_t stream, int32_t* status_out = nullptr);
 // ---- stable depth order of small images (depth_sort.hip)
 // Images of at most 131072 splats: run sort in LDS + merge ranks, two
 // launches.  buffers: depth_small_bytes(G, batch) bytes.
@@ -117,12 +127,13 @@ int launch_count(const RasterParams& P, const float* means2d,
 // pack: packed records in gid order and splat_offsets[0..BG] (exclusive scan
 // of splat_count[perm]) via a look-back scan whose status
 // (count_scan_blocks(P) words) and ticket must be zero.
+// err: the give-up status word of the look-back (zero before the launch).
 int launch_pack(const RasterParams& P, const float* means2d,
                 const float* conics, const float* colors,
                 const float* opacities, const uint32_t* perm,
                 const int32_t* splat_count, float* packed,
                 int32_t* splat_offsets, uint64_t* scan_status,
-                uint32_t* scan_ticket, hipStream_t stream);
+                uint32_t* scan_ticket, uint32_t* err, hipStream_t stream);
 int count_scan_blocks(const RasterParams& P);
 // emit: writes the (tile, gid) pairs into each splat's range, zeroes
 // pair_status, and fills pair_ghist ([pair_passes][256], zero on entry) with
@@ -136,10 +147,16 @@ int launch_emit(const RasterParams& P, const float* packed,
                 uint32_t* pair_ghist, uint32_t* pair_status,
                 int64_t pair_status_words, hipStream_t stream);
 // tile_offsets[0..T] and (unless tile_counts is NULL) tile_counts[0..T)
-// from the n sorted tile keys (min(n, *n_dev) of them with n_dev).
+// from the n sorted tile keys (min(n, *n_dev) of them with n_dev).  With
+// status_out, the same launch writes there the OR of the (non-null) give-up
+// status words err[0..2] of the binning's look-backs.
 int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        int32_t* tile_offsets, int32_t* tile_counts,
-                       hipStream_t stream, const int32_t* n_dev = nullptr);
+                       hipStream_t stream, const int32_t* n_dev = nullptr,
+                       const uint32_t* err0 = nullptr,
+                       const uint32_t* err1 = nullptr,
+                       const uint32_t* err2 = nullptr,
+                       int32_t* status_out = nullptr);
 int launch_zero2(uint32_t* a, int64_t na, uint32_t* b, int64_t nb,
                  hipStream_t stream);
 int launch_fill_i32(int32_t* dst, int32_t value, int64_t n, hipStream_t stream);

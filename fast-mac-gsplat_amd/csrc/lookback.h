@@ -8,12 +8,16 @@
 // one word, so relaxed device-scope atomics suffice.  Predecessor statuses are
 // read several at a time (independent loads) so the walk costs one memory
 // round trip per window rather than per predecessor.  Waits are bounded:
-// after kMaxSpins polls the wait gives up (results would then be wrong, but
-// every wave terminates).
+// after spin_limit polls (kMaxSpins unless a caller passes less) the wait
+// gives up, ORs GSPLAT_STATUS_LOOKBACK_TIMEOUT into the caller's status word
+// and returns the partial prefix.  Every wave therefore terminates, and the
+// status word (which the host reads back) says that the results are wrong.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "../../include/gsplat_hip.h"
 
 namespace gs {
 
@@ -24,6 +28,10 @@ constexpr uint64_t kFlagAgg64 = 1ull << 62;
 constexpr uint64_t kFlagInc64 = 2ull << 62;
 constexpr uint64_t kVal64 = (1ull << 62) - 1ull;
 constexpr int kMaxSpins = 1 << 20;
+
+__device__ __forceinline__ void report_giveup(uint32_t* err) {
+  if (err != nullptr) atomicOr(err, (uint32_t)GSPLAT_STATUS_LOOKBACK_TIMEOUT);
+}
 
 __device__ __forceinline__ uint32_t status_load(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -42,7 +50,8 @@ __device__ __forceinline__ void status_store(uint64_t* p, uint64_t v) {
 // blk-1, blk-2, ... stored `stride` words apart; one thread, windows of W.
 template <int W>
 __device__ __forceinline__ uint32_t lookback32(const uint32_t* status, int blk,
-                                              int stride) {
+                                              int stride, uint32_t* err,
+                                              int spin_limit = kMaxSpins) {
   uint32_t prefix = 0u;
   int b = blk - 1;
   int spins = 0;
@@ -73,7 +82,10 @@ __device__ __forceinline__ uint32_t lookback32(const uint32_t* status, int blk,
     if (done) break;
     b -= consumed;
     if (wait) {
-      if (++spins > kMaxSpins) break;
+      if (++spins > spin_limit) {
+        report_giveup(err);
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
     }
   }
@@ -90,7 +102,8 @@ __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 // computed by one whole wavefront (64 predecessors per round trip).  Every
 // lane of the calling wave must call it; all lanes receive the result.
 __device__ __forceinline__ uint64_t lookback64_wave(const uint64_t* status,
-                                                    int blk) {
+                                                    int blk, uint32_t* err,
+                                                    int spin_limit = kMaxSpins) {
   const int lane = threadIdx.x & 63;
   uint64_t prefix = 0ull;
   int b = blk - 1;
@@ -105,7 +118,10 @@ __device__ __forceinline__ uint64_t lookback64_wave(const uint64_t* status,
     const uint64_t need =
         first_inc >= 63 ? ~0ull : ((2ull << first_inc) - 1ull);
     if (not_ready & need) {
-      if (++spins > kMaxSpins) break;
+      if (++spins > spin_limit) {
+        if ((threadIdx.x & 63) == 0) report_giveup(err);
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
       continue;
     }

@@ -58,6 +58,7 @@ struct PassArgs {
   const uint32_t* ghist;     // [segments][256] global digit counts of this pass
   uint32_t* status;          // [segments][nblk][256], zeroed
   uint32_t* ticket;          // zeroed
+  uint32_t* err;             // look-back give-up status word
 };
 
 // Kernel variants, chosen on the host, so that the load loops hold no
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   uint32_t prefix = 0u;
   if (blk > 0) {
     prefix = lookback32<kLookbackWindow>(
-        a.status + (int64_t)seg * a.nblk * 256 + t, blk, 256);
+        a.status + (int64_t)seg * a.nblk * 256 + t, blk, 256, a.err);
     status_store(my_status, kFlagInc32 | (prefix + tot));
   }
   dstart[t] = local;
@@ -268,7 +269,7 @@ RadixPlan radix_plan(int64_t n_seg, int segments, int begin_bit, int end_bit) {
   L.nblk = (int)((n_seg + block_items - 1) / block_items);
   L.ghist_words = (int64_t)4 * segments * 256;
   L.status_words = (int64_t)(L.passes > 0 ? L.passes : 1) * segments * L.nblk * 256;
-  L.ticket_words = 4;
+  L.ticket_words = 8;  // four pass tickets, the give-up status word, padding
   const int64_t n = n_seg * (int64_t)segments;
   const size_t vec = align_up((size_t)n * sizeof(uint32_t), 256);
   size_t off = 0;
@@ -292,7 +293,8 @@ size_t radix_ctl_bytes(const RadixPlan& L) {
 
 RadixCtl radix_ctl_at(const RadixPlan& L, void* p) {
   uint32_t* w = static_cast<uint32_t*>(p);
-  return RadixCtl{w, w + L.ghist_words, w + L.ghist_words + L.status_words};
+  uint32_t* tickets = w + L.ghist_words + L.status_words;
+  return RadixCtl{w, w + L.ghist_words, tickets, tickets + 4};
 }
 
 size_t radix_sort_workspace_bytes(int64_t n_per_segment, int segments) {
@@ -344,7 +346,8 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
   const int64_t n = L.n_seg * L.segments;
   if (L.passes == 0) {  // copies all L.n_seg elements (in bounds with n_dev)
     PassArgs a{keys_in, vals_in, depth_src, keys_out, vals_out, L.n_seg,
-               nullptr, L.nblk, L.segments, 0, 0, nullptr, nullptr, nullptr};
+               nullptr, L.nblk, L.segments, 0, 0, nullptr, nullptr, nullptr,
+               nullptr};
     hipLaunchKernelGGL(rs_copy_kernel, dim3((unsigned)((n + 255) / 256)),
                        dim3(256), 0, stream, a, n);
     return check_launch("rs_copy_kernel");
@@ -366,7 +369,7 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
     PassArgs a{cur_k, cur_v, cur_depth, out_k, out_v, L.n_seg, n_dev, L.nblk,
                L.segments, shift, bits,
                C.ghist + (int64_t)p * L.segments * 256,
-               C.status + p * status_per_pass, C.tickets + p};
+               C.status + p * status_per_pass, C.tickets + p, C.err};
     const int mode = (cur_depth ? kDepthKeys : 0) | (cur_v ? kValsIn : 0) |
                      (out_k ? kKeysOut : 0);
     const dim3 grid((unsigned)(L.nblk * (int64_t)L.segments));
@@ -408,13 +411,14 @@ int radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in,
                      const float* depth_src, uint32_t* keys_out,
                      uint32_t* vals_out, int64_t n_seg, int segments,
                      int begin_bit, int end_bit, void* ws, size_t ws_bytes,
-                     hipStream_t stream) {
+                     hipStream_t stream, int32_t* status_out) {
   if (n_seg < 0 || segments < 0 || begin_bit < 0 || end_bit > 32 ||
       (keys_in == nullptr && depth_src == nullptr) || vals_out == nullptr) {
     set_error("radix_sort: invalid arguments");
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
-  if (n_seg == 0 || segments == 0) return GSPLAT_OK;
+  if (n_seg == 0 || segments == 0)
+    return status_out ? launch_fill_i32(status_out, 0, 1, stream) : GSPLAT_OK;
   if (!radix_size_ok(n_seg, segments)) {
     set_error("radix_sort: input too large");
     return GSPLAT_ERR_INVALID_ARGUMENT;
@@ -426,10 +430,16 @@ int radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in,
               ctl + L.buffer_bytes);
     return GSPLAT_ERR_WORKSPACE;
   }
-  const RadixCtl C = radix_ctl_at(L, ws);
+  RadixCtl C = radix_ctl_at(L, ws);
+  if (status_out) C.err = reinterpret_cast<uint32_t*>(status_out);
   if (L.passes > 0) {
-    int rc = launch_zero_u32(C.ghist, (int64_t)(ctl / sizeof(uint32_t)), stream);
+    int rc = launch_zero2(C.ghist, (int64_t)(ctl / sizeof(uint32_t)),
+                          reinterpret_cast<uint32_t*>(status_out),
+                          status_out ? 1 : 0, stream);
     if (!rc) rc = radix_global_hist(L, C, keys_in, depth_src, stream);
+    if (rc) return rc;
+  } else if (status_out) {
+    const int rc = launch_fill_i32(status_out, 0, 1, stream);
     if (rc) return rc;
   }
   return radix_passes(L, C, static_cast<char*>(ws) + ctl, keys_in, vals_in,

@@ -6,14 +6,17 @@ projected-2D API plus the pinhole projection front end.
 from .rasterize import (
     ProjectedGaussianRasterizer,
     RasterConfig,
+    RuntimeShaderConfig,
     get_runtime_shader_config,
     profile_projected_gaussians,
     rasterize_projected_gaussians,
 )
 from .project import project_pinhole_gaussians, rasterize_pinhole_gaussians
+from . import ops  # noqa: F401  (registers torch.ops.gsplat_hip.*)
 
 __all__ = [
     "RasterConfig",
+    "RuntimeShaderConfig",
     "ProjectedGaussianRasterizer",
     "rasterize_projected_gaussians",
     "profile_projected_gaussians",

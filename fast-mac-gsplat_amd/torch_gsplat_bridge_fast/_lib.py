@@ -17,10 +17,11 @@ import torch  # noqa: F401  (must be loaded before the HIP library)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("GSPLAT_HIP_LIB", os.path.join(_HERE, "lib", "libgsplat_hip.so"))
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 TILE_SIZE = 16
 RECORD_FLOATS = 12
 PROJECT_NOALLOC_SCRATCH_BYTES = 1 << 20   # GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES
+STATUS_LOOKBACK_TIMEOUT = 1               # GSPLAT_STATUS_LOOKBACK_TIMEOUT
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -67,9 +68,9 @@ SIGNATURES = {
     "gsplat_hip_bin_depth_order": (ctypes.c_int, [_PM, _vp, _vp, _vp, _sz, _vp]),
     "gsplat_hip_bin_pack": (ctypes.c_int, [_PM] + [_vp] * 7 + [_vp, _sz, _vp]),
     "gsplat_hip_bin_emit_workspace_bytes": (_sz, [_PM, _i64]),
-    "gsplat_hip_bin_emit": (ctypes.c_int, [_PM, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _vp]),
+    "gsplat_hip_bin_emit": (ctypes.c_int, [_PM, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _vp]),
     "gsplat_hip_bin_workspace_bytes": (_sz, [_PM, _i64]),
-    "gsplat_hip_bin": (ctypes.c_int, [_PM] + [_vp] * 5 + [_i64] + [_vp] * 7 + [_sz] + [_vp] * 4),
+    "gsplat_hip_bin": (ctypes.c_int, [_PM] + [_vp] * 5 + [_i64] + [_vp] * 7 + [_sz] + [_vp] * 5),
     "gsplat_hip_render_workspace_bytes": (_sz, [_PM, _i64]),
     "gsplat_hip_render_forward": (ctypes.c_int, [_PM] + [_vp] * 7 + [_i64, _vp, _sz, _vp]),
     "gsplat_hip_render_backward": (ctypes.c_int, [_PM] + [_vp] * 11 + [_i64, _vp, _sz, _vp]),
@@ -78,11 +79,12 @@ SIGNATURES = {
     "gsplat_hip_project_backward": (ctypes.c_int, [_PP] + [_vp] * 16 + [_vp, _sz, _vp]),
     "gsplat_hip_project_backward_noalloc": (ctypes.c_int, [_PP] + [_vp] * 16 + [_vp]),
     "gsplat_hip_scan_workspace_bytes": (_sz, [_i64]),
-    "gsplat_hip_exclusive_scan_i32": (ctypes.c_int, [_vp, _vp, _i64, _vp, _sz, _vp]),
+    "gsplat_hip_exclusive_scan_i32": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _sz, _vp]),
+    "gsplat_hip_debug_stalled_scan": (ctypes.c_int, [_vp, _vp, _i64, _i32, _i32, _vp, _vp, _sz, _vp]),
     "gsplat_hip_radix_sort_workspace_bytes": (_sz, [_i64, _i32]),
     "gsplat_hip_radix_sort_pairs_u32": (
         ctypes.c_int,
-        [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _sz, _vp],
+        [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp, _sz, _vp],
     ),
 }
 

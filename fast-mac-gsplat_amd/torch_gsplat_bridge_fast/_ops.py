@@ -8,6 +8,11 @@ variants/v8/csrc/metal/gsplat_metal.mm:188).  Here the buffers are sized from
 the count of an earlier call of the same shape and N is checked only after
 the compositor has been enqueued (bin_and_render), so the host does not stall
 the GPU between binning stages; the first call of a shape reads N first.
+
+Every binning also reports a status word (GSPLAT_STATUS_*, set when a
+look-back wait gave up, which empties every tile range of that binning).
+It reaches pinned memory in the same transfer as N, and BinState.confirm()
+raises RuntimeError when it is set, so the call that bins fails.
 """
 from __future__ import annotations
 
@@ -80,9 +85,16 @@ class _timed:
 # are enqueued.
 _capacity: dict = {}
 
+# Largest pair count the pair sort takes (radix_size_ok in radix_sort.hip).
+MAX_PAIRS = 1 << 29
+
 
 def _headroom(n: int) -> int:
-    return n + n // 4 + 4096
+    """Capacity remembered for a shape whose last count was n: 25% + 4096 of
+    headroom, but never above the sort's limit when n itself fits it (a
+    larger capacity would make every later call of the shape fail)."""
+    cap = n + n // 4 + 4096
+    return min(cap, MAX_PAIRS) if n <= MAX_PAIRS else cap
 
 
 @dataclass
@@ -93,18 +105,29 @@ class BinState:
     tile_offsets: Tensor            # int32 [T+1]
     pairs: Tensor                   # int32 [capacity]; the first N entries are the binned gids
     capacity: int                   # pair capacity the buffers and workspaces were sized for
-    _n_host: Optional[Tensor] = None                 # pinned int32: N at _n_slot once _n_ready completes
+    _n_host: Optional[Tensor] = None                 # pinned int32: N at _n_index once _n_ready completes
     _n_ready: Optional[torch.cuda.Event] = None
     _n: Optional[int] = None
     _key: Optional[tuple] = None
-    _n_slot: int = 0
+    _n_index: tuple = (0,)
+    _status_host: Optional[Tensor] = None            # pinned int32: the status at _status_index
+    _status_index: tuple = (0,)
+    _status_ready: Optional[torch.cuda.Event] = None
+    _ring: Optional["_DeviceBinState"] = None        # owner of the pinned words (fast path)
+    _generation: int = 0
+
+    def _words_current(self) -> bool:
+        """False if the pinned ring slot has been reused by later binnings."""
+        return self._ring is None or self._ring.calls - self._generation < self._ring.RING
 
     @property
     def n_pairs(self) -> int:
-        """The pair count N (waits for the count stage, which ran first on the GPU)."""
+        """The pair count N (waits for the transfer that carries it)."""
         if self._n is None:
             self._n_ready.synchronize()
-            self._n = int(self._n_host[self._n_slot])
+            if not self._words_current():
+                raise RuntimeError("binning state read after its pinned slot was reused")
+            self._n = int(self._n_host[self._n_index])
         return self._n
 
     def confirm(self) -> bool:
@@ -112,6 +135,7 @@ class BinState:
         `capacity` pairs and must be redone; the capacity for this shape has then been raised, so
         binning the same inputs again fits.  Raises if N overflowed int32."""
         n = self.n_pairs
+        self.check_status()
         if n < 0:
             raise RuntimeError("pair count overflowed int32")
         if self._key is not None:
@@ -119,6 +143,22 @@ class BinState:
             if n > cap or 2 * _headroom(n) < cap:
                 _capacity[self._key] = _headroom(n)
         return n <= self.capacity
+
+    def check_status(self) -> None:
+        """Raises RuntimeError if a look-back wait of this binning gave up (its tile ranges are then
+        all empty).  Waits for the transfer that carries the status; a no-op once read."""
+        if self._status_ready is None:
+            return
+        self._status_ready.synchronize()
+        if not self._words_current():
+            return  # the slot was reused; its status can no longer be read
+        status = int(self._status_host[self._status_index])
+        self._status_ready = None
+        if status & _lib.STATUS_LOOKBACK_TIMEOUT:
+            raise RuntimeError("binning failed: a decoupled look-back wait gave up (a predecessor workgroup "
+                               "did not make progress for ~1 s); the results of this call are invalid")
+        if status:
+            raise RuntimeError(f"binning failed with device status {status:#x}")
 
     @property
     def binned_ids(self) -> Tensor:
@@ -165,18 +205,22 @@ def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors
     reads N before emitting (like the reference's tile_offsets[-1] read,
     variants/v8/csrc/metal/gsplat_metal.mm:188).  Unless defer_check, N is then
     checked against the capacity (binning again if it did not fit); with
-    defer_check the caller must call confirm() before using the result."""
+    defer_check the caller must call confirm() (and check_status()) before using the result;
+    otherwise both run here."""
     st = _bin(meta, means2d, conics, colors, opacities, depths)
-    if not defer_check and not st.confirm():
-        st = _bin(meta, means2d, conics, colors, opacities, depths)
+    if not defer_check:
         if not st.confirm():
-            raise RuntimeError("binning: pair count changed between two binnings of the same inputs")
+            st = _bin(meta, means2d, conics, colors, opacities, depths)
+            if not st.confirm():
+                raise RuntimeError("binning: pair count changed between two binnings of the same inputs")
+        st.check_status()
     return st
 
 
 def bin_and_render(meta: _lib.RasterMeta, flat, *, save_state: bool):
     """Binning then render_forward with the capacity check after the forward is enqueued, so
-    that the host never waits on the GPU in between.  Returns (BinState, render_forward outputs)."""
+    that the host never waits on the GPU in between.  Returns (BinState, render_forward outputs);
+    the caller runs st.check_status() before the results are relied on."""
     st = bin_gaussians(meta, *flat, defer_check=True)
     out = render_forward(meta, st, save_state=save_state)
     if not st.confirm():
@@ -186,24 +230,26 @@ def bin_and_render(meta: _lib.RasterMeta, flat, *, save_state: bool):
 
 
 class _DeviceBinState:
-    """Per-device objects reused by every binning call: the two ordering events of gsplat_hip_bin
+    """Per-device objects reused by every binning call: the three events of gsplat_hip_bin
     (re-recording them is safe: a stream wait takes the event's state when it is enqueued, and a
-    host wait on a later recording of the count event also covers the earlier copies) and a ring
-    of pinned words for the pair counts."""
-    RING = 64
+    host wait on a later recording of an event also covers the earlier copies) and a ring of
+    pinned word pairs (N, status), one pair per call, filled by one transfer at the end of the
+    binning."""
+    RING = 1024
 
     def __init__(self, device: torch.device):
         main = torch.cuda.current_stream(device)
         self.inputs = torch.cuda.Event()
         self.count = torch.cuda.Event()
-        for e in (self.inputs, self.count):
+        self.status = torch.cuda.Event()
+        for e in (self.inputs, self.count, self.status):
             e.record(main)      # creates the HIP event
-        self.ring = torch.zeros((self.RING,), dtype=torch.int32, pin_memory=True)
-        self.next = 0
+        self.ring = torch.zeros((self.RING, 2), dtype=torch.int32, pin_memory=True)
+        self.calls = 0
 
     def slot(self) -> int:
-        i = self.next
-        self.next = (i + 1) % self.RING
+        i = self.calls % self.RING
+        self.calls += 1
         return i
 
 
@@ -229,13 +275,16 @@ def _bin_fast(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Te
     ws_bytes = L.gsplat_hip_bin_workspace_bytes(meta, cap)
     ws = _empty(max(ws_bytes, 1), torch.uint8, dev)
     slot = d.slot()
+    # The side stream's work (the count) is waited for by the launch stream inside the call, so
+    # every later use of these buffers on the launch stream is ordered after it.
     check(L.gsplat_hip_bin(meta, ptr(means2d), ptr(conics), ptr(colors), ptr(opacities), ptr(depths), cap,
                            ptr(perm), ptr(packed), ptr(splat_offsets), ptr(pairs), ptr(tile_offsets),
-                           d.ring.data_ptr() + 4 * slot, ptr(ws), ws_bytes,
+                           d.ring.data_ptr() + 8 * slot, ptr(ws), ws_bytes,
                            torch.cuda.current_stream(dev).cuda_stream, _side_stream(dev).cuda_stream,
-                           d.inputs.cuda_event, d.count.cuda_event),
+                           d.inputs.cuda_event, d.count.cuda_event, d.status.cuda_event),
           "gsplat_hip_bin")
-    return BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, d.ring, d.count, None, key, slot)
+    return BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, d.ring, d.status, None, key, (slot, 0),
+                    d.ring, (slot, 1), d.status, d, d.calls - 1)
 
 
 def _bin(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
@@ -291,11 +340,17 @@ def _bin(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
     pairs = _empty(cap, torch.int32, dev)
     ws2_bytes = L.gsplat_hip_bin_emit_workspace_bytes(meta, cap)
     ws2 = _empty(max(ws2_bytes, 1), torch.uint8, dev)
+    status = _empty(1, torch.int32, dev)
     with _timed("bin_emit"):
         check(L.gsplat_hip_bin_emit(meta, ptr(packed), ptr(splat_offsets), cap, ptr(pairs), None,
-                                    ptr(tile_offsets), ptr(ws), ws_bytes, ptr(ws2), ws2_bytes, s),
+                                    ptr(tile_offsets), ptr(status), ptr(ws), ws_bytes, ptr(ws2), ws2_bytes, s),
               "gsplat_hip_bin_emit")
-    return BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, n_host, n_ready, n_known, key)
+    status_host = torch.empty((1,), dtype=torch.int32, pin_memory=True)
+    status_host.copy_(status, non_blocking=True)
+    status_ready = torch.cuda.Event()
+    status_ready.record(main)
+    return BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, n_host, n_ready, n_known, key, (0,),
+                    status_host, (0,), status_ready)
 
 
 def render_forward(meta: _lib.RasterMeta, st: BinState, *, save_state: bool):
@@ -382,15 +437,24 @@ def project_backward(meta: _lib.ProjectMeta, g_m2, g_cq, g_op, g_dp, means3d, sc
     return gm3, gs, gq, go, gc2w, gcam
 
 
+def _raise_on_status(status: Tensor, what: str) -> None:
+    """Synchronises on the device status word of a primitive call."""
+    v = int(status.item())
+    if v:
+        raise RuntimeError(f"{what}: device status {v:#x} (a decoupled look-back wait gave up)")
+
+
 def exclusive_scan_i32(x: Tensor) -> Tensor:
     """out[0..n]: exclusive prefix sum of int32 x with the total at out[n]."""
     L = _lib.lib()
     n = x.numel()
     out = _empty(n + 1, torch.int32, x.device)
+    status = _empty(1, torch.int32, x.device)
     wsb = L.gsplat_hip_scan_workspace_bytes(n)
     ws = _empty(max(wsb, 1), torch.uint8, x.device)
-    check(L.gsplat_hip_exclusive_scan_i32(ptr(x), ptr(out), n, ptr(ws), wsb, stream_of(x)),
+    check(L.gsplat_hip_exclusive_scan_i32(ptr(x), ptr(out), n, ptr(status), ptr(ws), wsb, stream_of(x)),
           "gsplat_hip_exclusive_scan_i32")
+    _raise_on_status(status, "gsplat_hip_exclusive_scan_i32")
     return out
 
 
@@ -405,7 +469,9 @@ def radix_sort_pairs_u32(keys: Tensor, vals: Optional[Tensor], *, segments: int 
     vo = torch.empty((n,), dtype=torch.int32, device=keys.device)
     wsb = L.gsplat_hip_radix_sort_workspace_bytes(n_seg, segments)
     ws = _empty(max(wsb, 1), torch.uint8, keys.device)
+    status = _empty(1, torch.int32, keys.device)
     check(L.gsplat_hip_radix_sort_pairs_u32(ptr(keys), ptr(vals), ptr(ko), ptr(vo), n_seg, segments, begin_bit,
-                                            end_bit, ptr(ws), wsb, stream_of(keys)),
+                                            end_bit, ptr(status), ptr(ws), wsb, stream_of(keys)),
           "gsplat_hip_radix_sort_pairs_u32")
+    _raise_on_status(status, "gsplat_hip_radix_sort_pairs_u32")
     return ko, vo

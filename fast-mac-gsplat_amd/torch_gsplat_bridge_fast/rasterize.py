@@ -41,10 +41,16 @@ from . import _lib, _ops
 
 @dataclass(frozen=True)
 class RuntimeShaderConfig:
+    """Compiled compositor parameters (reference fields, v8 rasterize.py:17-23):
+    tile_size (pixels per tile side), threads (lanes of a tile's workgroup),
+    chunk_size (splats staged per batch), fast_cap (the max_fast_pairs
+    bound) and simdgroups (hardware execution groups per tile workgroup:
+    64-lane wavefronts here)."""
     tile_size: int
     threads: int
     chunk_size: int
     fast_cap: int
+    simdgroups: int
 
 
 def _env_int(name: str, default: int) -> int:
@@ -55,20 +61,28 @@ def _env_int(name: str, default: int) -> int:
 
 
 def get_runtime_shader_config() -> RuntimeShaderConfig:
-    """Compiled kernel parameters (reference: v8 rasterize.py:33-53).
+    """Compiled kernel parameters (reference: v8 rasterize.py:33-53), with the
+    reference's environment variables and checks.
 
-    The HIP kernels are built for 16x16 tiles with one 64-lane wavefront per
-    tile and 64-splat LDS batches; GSP_TILE_SIZE other than 16 is rejected.
+    The HIP kernels are built for 16x16 tiles walked by one 64-lane wavefront
+    (threads = 64, simdgroups = 1 wavefront) and 64-splat LDS batches;
+    GSP_TILE_SIZE other than 16 and GSP_CHUNK other than 64 are rejected.
     GSP_FAST_CAP bounds ``max_fast_pairs`` as in the reference."""
     tile_size = _env_int("GSP_TILE_SIZE", 16)
+    chunk_size = _env_int("GSP_CHUNK", 64)
     fast_cap = _env_int("GSP_FAST_CAP", 2048)
     if tile_size not in (8, 16, 32):
         raise ValueError(f"GSP_TILE_SIZE must be one of 8, 16, 32; got {tile_size}")
     if tile_size != _lib.TILE_SIZE:
         raise ValueError(f"GSP_TILE_SIZE={tile_size} is not supported: the HIP kernels are built for 16x16 tiles")
+    if chunk_size <= 0:
+        raise ValueError("GSP_CHUNK must be positive")
+    if chunk_size != 64:
+        raise ValueError(f"GSP_CHUNK={chunk_size} is not supported: the HIP kernels stage 64-splat batches")
     if fast_cap <= 0:
         raise ValueError("GSP_FAST_CAP must be positive")
-    return RuntimeShaderConfig(tile_size=tile_size, threads=64, chunk_size=64, fast_cap=fast_cap)
+    return RuntimeShaderConfig(tile_size=tile_size, threads=64, chunk_size=chunk_size, fast_cap=fast_cap,
+                               simdgroups=1)
 
 
 @dataclass(frozen=True)
@@ -228,6 +242,8 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
         st, (img, final_T, last, tile_stop, ws) = _ops.bin_and_render(meta, flat, save_state=True)
         _check_overflow(config, st)
         ctx.save_for_backward(st.packed, st.tile_offsets, st.pairs, final_T, last, tile_stop, ws)
+        # the binning's status is read before the backward (by then the GPU is done with it)
+        ctx.check_status = st.check_status
         ctx.meta = meta
         ctx.shape = (B, G)
         ctx.depth_shape = depths_b.shape
@@ -236,6 +252,7 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         packed, tile_offsets, pairs, final_T, last, tile_stop, ws = ctx.saved_tensors
+        ctx.check_status()
         st = _ops.BinState(None, packed, None, tile_offsets, pairs, pairs.numel())
         g_m, g_q, g_c, g_o = _ops.render_backward(ctx.meta, st, final_T, last, tile_stop, grad_out, ws)
         need = ctx.needs_input_grad
@@ -254,6 +271,7 @@ def _rasterize_chunk_eval(means2d_b, conics_b, colors_b, opacities_b, depths_b, 
     st, out = _ops.bin_and_render(meta, _flat(means2d_b, conics_b, colors_b, opacities_b, depths_b),
                                   save_state=False)
     _check_overflow(config, st)
+    st.check_status()
     return out[0]
 
 

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 8
+#define GSPLAT_HIP_ABI_VERSION 9
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -49,6 +49,14 @@ enum gsplat_status {
   GSPLAT_ERR_HIP = 2,
   GSPLAT_ERR_WORKSPACE = 3
 };
+
+/* Device status words (the `status` outputs below): 0 when every kernel
+ * completed normally.  The scans and sorts obtain earlier workgroups' totals
+ * by decoupled look-back; a wait that exceeds its poll budget (a predecessor
+ * starved for about a second, e.g. by another process on the GPU) gives up so
+ * that every wave terminates, and sets this bit: the outputs of that call are
+ * then wrong and must be discarded. */
+#define GSPLAT_STATUS_LOOKBACK_TIMEOUT 1
 
 /* Static render parameters.  Mirrors the reference's RasterConfig plus the
  * meta packing of variants/v8/torch_gsplat_bridge_v8/rasterize.py:129-173
@@ -154,6 +162,9 @@ size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
  * binned (tile_offsets[T] = n_pairs): a consistent but incomplete result that
  * the caller discards and redoes from bin_count with n_pairs >= N.  With
  * N = -1 (overflow) nothing is binned.
+ * status (device int32, may be NULL): receives the OR of the GSPLAT_STATUS_*
+ * bits of the whole binning (bin_depth_order, bin_pack and this call); when
+ * it is not 0 every tile range is empty (tile_offsets all 0).
  * count_workspace is the workspace of bin_count / bin_pack.  Replaces
  * emit_binned_ids (variants/v8/csrc/metal/gsplat_v8_kernels.metal:290-327),
  * the reference's tile_counts/tile_offsets (count_tiles :244-288 + the
@@ -162,22 +173,26 @@ size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
 int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
                         const int32_t* splat_offsets, int64_t n_pairs,
                         int32_t* binned_ids, int32_t* tile_counts,
-                        int32_t* tile_offsets,
+                        int32_t* tile_offsets, int32_t* status,
                         void* count_workspace, size_t count_workspace_bytes,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* All four binning calls in one: bin_count on count_stream (NULL: `stream`),
- * ordered after the work already enqueued on `stream` through inputs_event;
- * N copied to the pinned host word *pair_count_host (may be NULL) on
- * count_stream, after which count_event is recorded; bin_depth_order on
- * `stream` concurrently; then bin_pack (after count_event) and bin_emit with
- * the pair capacity `capacity` (see bin_emit: n_pairs).  The events are the
- * caller's (hipEvent_t, required when count_stream differs from stream); the
- * caller waits for count_event before reading *pair_count_host.  Outputs as
- * bin_depth_order (perm), bin_pack (packed, splat_offsets) and bin_emit
- * (binned_ids [capacity], tile_offsets).  One call instead of four keeps the
- * host's per-step launch overhead small; it replaces the same reference
- * steps as the four calls. */
+ * ordered after the work already enqueued on `stream` through inputs_event,
+ * after which count_event is recorded; bin_depth_order on `stream`
+ * concurrently; then bin_pack (after count_event) and bin_emit with the pair
+ * capacity `capacity` (see bin_emit: n_pairs).  Finally, on `stream`, the
+ * pair count N and the binning's status word (GSPLAT_STATUS_*) are copied in
+ * one transfer to host_words[0] and host_words[1] (two pinned int32; may be
+ * NULL: nothing copied), after which status_event (may be NULL) is recorded:
+ * the caller waits for it before reading them.  The events are the
+ * caller's (hipEvent_t; inputs_event and count_event are required when
+ * count_stream differs from stream).  If a look-back gave up, every tile
+ * range is empty (the compositors then read no pair) and the status says
+ * so.  Outputs as bin_depth_order (perm), bin_pack (packed, splat_offsets)
+ * and bin_emit (binned_ids [capacity], tile_offsets).  One call instead of
+ * four keeps the host's per-step launch overhead small; it replaces the same
+ * reference steps as the four calls. */
 size_t gsplat_hip_bin_workspace_bytes(const gsplat_raster_meta* meta,
                                       int64_t capacity);
 int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
@@ -185,10 +200,10 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
                    const float* opacities, const float* depths,
                    int64_t capacity, int32_t* perm, float* packed,
                    int32_t* splat_offsets, int32_t* binned_ids,
-                   int32_t* tile_offsets, int32_t* pair_count_host,
+                   int32_t* tile_offsets, int32_t* host_words,
                    void* workspace, size_t workspace_bytes, void* stream,
                    void* count_stream, void* inputs_event,
-                   void* count_event);
+                   void* count_event, void* status_event);
 
 /* -------------------------------------------------------------- composite
  * Compositor workspace (optional; n_pairs is the N of the binning).  With it
@@ -312,10 +327,24 @@ int gsplat_hip_project_backward_noalloc(
 
 size_t gsplat_hip_scan_workspace_bytes(int64_t n);
 /* out[0..n] = exclusive prefix sum of in[0..n-1]; out[n] = total.  In-place
- * (out == in) is allowed. */
+ * (out == in) is allowed.  status (device int32, may be NULL): 0 or
+ * GSPLAT_STATUS_* bits. */
 int gsplat_hip_exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n,
-                                  void* workspace, size_t workspace_bytes,
-                                  void* stream);
+                                  int32_t* status, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
+/* Diagnostic (no counterpart in the reference): the scan above with its
+ * first `stalled_blocks` 4096-element blocks never scanned, so their
+ * look-back statuses are never published, and each look-back wait limited
+ * to spin_limit polls.  The block after them gives up waiting, every kernel
+ * finishes, and *status receives GSPLAT_STATUS_LOOKBACK_TIMEOUT; out holds
+ * prefixes that miss the stalled blocks' totals (elements of the stalled
+ * blocks themselves are not written).  It exists to test that a look-back
+ * give-up reaches the caller; 0 <= stalled_blocks < ceil(n / 4096). */
+int gsplat_hip_debug_stalled_scan(const int32_t* in, int32_t* out, int64_t n,
+                                  int32_t stalled_blocks, int32_t spin_limit,
+                                  int32_t* status, void* workspace,
+                                  size_t workspace_bytes, void* stream);
 
 size_t gsplat_hip_radix_sort_workspace_bytes(int64_t n_per_segment,
                                              int32_t segments);
@@ -323,14 +352,15 @@ size_t gsplat_hip_radix_sort_workspace_bytes(int64_t n_per_segment,
  * [begin_bit, end_bit), 8-bit digits, independently inside each of
  * `segments` contiguous segments of n_per_segment elements.  vals_in may be
  * NULL (values are then the index within the segment); keys_out may be NULL
- * (keys are then not written). */
+ * (keys are then not written).  status (device int32, may be NULL): 0 or
+ * GSPLAT_STATUS_* bits. */
 int gsplat_hip_radix_sort_pairs_u32(const uint32_t* keys_in,
                                     const uint32_t* vals_in,
                                     uint32_t* keys_out, uint32_t* vals_out,
                                     int64_t n_per_segment, int32_t segments,
                                     int32_t begin_bit, int32_t end_bit,
-                                    void* workspace, size_t workspace_bytes,
-                                    void* stream);
+                                    int32_t* status, void* workspace,
+                                    size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -115,3 +115,47 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_pair_capacity_is_clamped_to_the_sort_limit(monkeypatch):
+    """A capacity remembered for a shape never exceeds the pair sort's limit
+    when the count itself fits (a larger one would make every later call of
+    the shape fail); counts above the limit keep their headroom (and fail
+    loudly in the sort)."""
+    from torch_gsplat_bridge_fast import _ops
+
+    monkeypatch.setattr(_ops, "MAX_PAIRS", 1000)
+    assert _ops._headroom(10) == 10 + 2 + 4096 if 10 + 2 + 4096 <= 1000 else _ops._headroom(10) == 1000
+    assert _ops._headroom(900) == 1000
+    assert _ops._headroom(1000) == 1000
+    assert _ops._headroom(1001) == 1001 + 250 + 4096
+    monkeypatch.setattr(_ops, "MAX_PAIRS", 1 << 29)
+    n = 429_493_500                         # 1.25 n + 4096 > 2^29 >= n
+    assert _ops._headroom(n) == 1 << 29
+    assert _ops._headroom(1000) == 1000 + 250 + 4096
+
+
+class _DoneEvent:
+    def synchronize(self):
+        pass
+
+
+def test_binning_status_word_raises():
+    """check_status turns a set status word into RuntimeError (and a zero one
+    into nothing); it waits on the status event first."""
+    import torch
+
+    from torch_gsplat_bridge_fast import _ops
+
+    def state(word):
+        host = torch.tensor([[123, word]], dtype=torch.int32)
+        t = torch.zeros(1)
+        return _ops.BinState(None, t, None, t, t, 1, host, _DoneEvent(), None, None, (0, 0), host, (0, 1),
+                             _DoneEvent())
+
+    state(0).check_status()
+    with pytest.raises(RuntimeError, match="look-back wait gave up"):
+        state(1).check_status()
+    with pytest.raises(RuntimeError, match="device status"):
+        state(4).check_status()
+    assert state(0).n_pairs == 123

@@ -30,7 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 8
+    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 9
 
 
 def _meta(**kw):
@@ -92,7 +92,7 @@ def test_workspace_too_small_rejected():
     assert rc == 3 and "bin_pack" in L.gsplat_hip_last_error().decode()
     rc = L.gsplat_hip_bin_depth_order(_meta(), one, one, one, 1, None)
     assert rc == 3 and "bin_depth_order" in L.gsplat_hip_last_error().decode()
-    rc = L.gsplat_hip_bin_emit(_meta(), one, one, 10, one, one, one, one, 1, one, 1, None)
+    rc = L.gsplat_hip_bin_emit(_meta(), one, one, 10, one, one, one, None, one, 1, one, 1, None)
     assert rc == 3
     pm = _lib.make_project_meta(2, 1000, 1e-4)
     need = L.gsplat_hip_project_backward_workspace_bytes(pm)
@@ -146,11 +146,11 @@ def test_one_call_binning_validation():
     m = _meta()
     need = L.gsplat_hip_bin_workspace_bytes(m, 1000)
     assert need > L.gsplat_hip_bin_workspace_bytes(m, 10) > 0
-    rc = L.gsplat_hip_bin(m, *([None] * 5), 10, *([one] * 7), need, None, None, None, None)
+    rc = L.gsplat_hip_bin(m, *([None] * 5), 10, *([one] * 7), need, None, None, None, None, None)
     assert rc == 1 and "NULL" in L.gsplat_hip_last_error().decode()
-    rc = L.gsplat_hip_bin(m, *([one] * 5), -1, *([one] * 7), need, None, None, None, None)
+    rc = L.gsplat_hip_bin(m, *([one] * 5), -1, *([one] * 7), need, None, None, None, None, None)
     assert rc == 1 and "capacity" in L.gsplat_hip_last_error().decode()
-    rc = L.gsplat_hip_bin(m, *([one] * 5), 1000, *([one] * 7), need, one, ctypes.c_void_p(2), None, None)
+    rc = L.gsplat_hip_bin(m, *([one] * 5), 1000, *([one] * 7), need, one, ctypes.c_void_p(2), None, None, None)
     assert rc == 1 and "events" in L.gsplat_hip_last_error().decode()
-    rc = L.gsplat_hip_bin(m, *([one] * 5), 1000, *([one] * 7), need - 1, None, None, None, None)
+    rc = L.gsplat_hip_bin(m, *([one] * 5), 1000, *([one] * 7), need - 1, None, None, None, None, None)
     assert rc == 3 and "workspace" in L.gsplat_hip_last_error().decode()

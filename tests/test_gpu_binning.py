@@ -34,7 +34,7 @@ def test_exclusive_scan_in_place(gpu):
     L = _lib.lib()
     wsb = L.gsplat_hip_scan_workspace_bytes(300_001)
     ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
-    _lib.check(L.gsplat_hip_exclusive_scan_i32(buf.data_ptr(), buf.data_ptr(), 300_001, ws.data_ptr(), wsb,
+    _lib.check(L.gsplat_hip_exclusive_scan_i32(buf.data_ptr(), buf.data_ptr(), 300_001, None, ws.data_ptr(), wsb,
                                                _lib.stream_of(buf)), "scan")
     np.testing.assert_array_equal(buf.cpu().numpy(), ref)
 
@@ -283,3 +283,53 @@ def test_depth_order_small_images(gpu, B, G, kind):
     for b in range(B):
         # numpy: -0.0 == +0.0, NaN last, stable
         np.testing.assert_array_equal(got[b], np.argsort(d[b], kind="stable"))
+
+
+def test_lookback_giveup_reaches_the_caller(gpu):
+    """A look-back wait whose predecessor never publishes its status (forced
+    from the host: the diagnostic scan never runs its first blocks) gives up
+    after its poll budget, every kernel finishes, and the status word says
+    so; the same scan without a stall reports 0 and is exact."""
+    L = _lib.lib()
+    n = 10 * 4096 + 123
+    x = torch.ones(n, dtype=torch.int32, device=gpu)
+    wsb = L.gsplat_hip_scan_workspace_bytes(n)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    for stalled, spin_limit in ((0, 1 << 20), (3, 64)):
+        print(f"stalled scan: {stalled} stalled blocks, spin limit {spin_limit}", flush=True)
+        out = torch.full((n + 1,), -7, dtype=torch.int32, device=gpu)
+        status = torch.full((1,), -1, dtype=torch.int32, device=gpu)
+        _lib.check(L.gsplat_hip_debug_stalled_scan(x.data_ptr(), out.data_ptr(), n, stalled, spin_limit,
+                                                   status.data_ptr(), ws.data_ptr(), wsb, _lib.stream_of(x)),
+                   "gsplat_hip_debug_stalled_scan")
+        torch.cuda.synchronize()
+        o = out.cpu().numpy()
+        if stalled == 0:
+            assert int(status.item()) == 0
+            np.testing.assert_array_equal(o, np.arange(n + 1, dtype=np.int32))
+        else:
+            assert int(status.item()) == _lib.STATUS_LOOKBACK_TIMEOUT
+            # the stalled blocks were never scanned; the first block after them gave up with an
+            # empty prefix (later ones may give up too: each block is only consistent in itself)
+            assert np.all(o[: stalled * 4096] == -7)
+            assert o[stalled * 4096] == 0
+            for b in range(stalled, (n + 4095) // 4096):
+                blk = o[b * 4096: min((b + 1) * 4096, n)]
+                np.testing.assert_array_equal(np.diff(blk), np.ones(blk.size - 1, dtype=np.int32))
+    # invalid diagnostics are refused before launching
+    rc = L.gsplat_hip_debug_stalled_scan(x.data_ptr(), x.data_ptr(), n, 11, 1, x.data_ptr(), ws.data_ptr(), wsb,
+                                         _lib.stream_of(x))
+    assert rc == 1
+
+
+def test_binning_reports_status_zero(gpu):
+    """The status word of a normal binning (fast path and four-call path) is 0."""
+    sc = make_scene_2d(1, seed=3, G=20000, H=300, W=500)
+    from torch_gsplat_bridge_fast import _ops as ops
+
+    key = (0, 1, 20000, 300, 500)
+    ops._capacity.pop(key, None)
+    for _ in range(2):                      # first call: four-call path; second: one call
+        st = _gpu_bins(sc, 300, 500, 1, 20000)
+        assert st._status_ready is None      # checked by bin_gaussians
+        assert int(st._status_host[st._status_index]) == 0

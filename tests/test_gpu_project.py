@@ -268,3 +268,27 @@ def test_config4_full_workload(gpu):
                           img.detach().cpu().numpy(), [t.grad.cpu().numpy() for t in leaves],
                           colors.grad.cpu().numpy(), "config 4")
     assert bins.binned_ids.size > 100_000_000
+
+
+def test_torch_ops_projection(gpu):
+    """torch.ops.gsplat_hip.project_forward / project_backward (the roles of the
+    reference's project_pinhole_forward / _backward ops) against the
+    running-error reference, as the autograd path above."""
+    B, G = 2, 900
+    m, s, q, o, c2w, cam = (t.float() for t in _scene(B, G, seed=9))
+    dev = torch.device("cuda:0")
+    args = [t.reshape(B * G, -1).squeeze(-1).contiguous().to(dev) for t in (m, s, q, o)] + \
+        [c2w.contiguous().to(dev), cam.contiguous().to(dev)]
+    out = torch.ops.gsplat_hip.project_forward(*args, 1e-4)
+    _check_forward(tuple(t.reshape(B, G, -1).squeeze(-1) for t in out), m, s, q, o, c2w, cam)
+    gen = torch.Generator().manual_seed(19)
+    w = [torch.randn(B * G, 2, generator=gen), torch.randn(B * G, 3, generator=gen) * 1e3,
+         torch.randn(B * G, generator=gen), torch.randn(B * G, generator=gen)]
+    g = torch.ops.gsplat_hip.project_backward(*(x.to(dev) for x in w), *args, 1e-4)
+    torch.cuda.synchronize()
+    r = PB.project_vjp(*(_np(t) for t in (m, s, q, o, c2w, cam)), *(x.reshape(B, G, -1).squeeze(-1).double().numpy()
+                                                                    for x in w))
+    for key, got in zip(KEYS3, g[:4]):
+        PB.assert_close(_np(got).reshape(B * G, -1), r[key], key)
+    PB.assert_close(_np(g[4]).reshape(B, 16), r["camera_to_world"], "camera_to_world")
+    PB.assert_close(_np(g[5]), r["camera_params"], "camera_params")

@@ -471,3 +471,32 @@ def test_recorded_trace_vs_tile_oracle(gpu, tmp_path):
     host = {k: tr[k].cpu() for k in KEYS}
     oracle_parity(host, H, W, 1, G, (0.0, 0.0, 0.0), w.numpy(), img.detach().cpu().numpy(),
                   [t.grad.cpu().numpy() for t in leaves[:4]], "recorded trace")
+
+
+def test_torch_ops_vs_tile_oracle(gpu):
+    """The torch.library operators (torch.ops.gsplat_hip.bin / render_forward /
+    render_backward, the roles of torch.ops.gsplat_metal_v8.bin /
+    render_fast_forward_state / render_fast_backward_saved), composed as the
+    reference's autograd function composes its ops: binning bit-exact, image
+    and gradients at the bar against the tile oracle, and the eval forward
+    bit-identical to the state forward."""
+    B, G, H, W = 2, 5000, 96, 160
+    bg = [0.2, 0.3, 0.4]
+    sc = make_scene_2d(3, seed=6, G=G, B=B, H=H, W=W)
+    flat = [sc[k].reshape(B * G, -1).squeeze(-1).contiguous().to(gpu) for k in KEYS]
+    counts, offsets, ids, packed, perm = torch.ops.gsplat_hip.bin(*flat, H, W, B, 1.0 / 255.0, 1e-4, bg)
+    bins = TO.bin_scene(TO.make_meta(H, W, B, G, background=bg), TO.Scene(*(sc[k].numpy() for k in KEYS), B, G))
+    np.testing.assert_array_equal(perm.cpu().numpy(), bins.perm)
+    np.testing.assert_array_equal(counts.cpu().numpy(), bins.tile_counts)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), bins.tile_offsets)
+    np.testing.assert_array_equal(ids.cpu().numpy(), bins.binned_ids)
+    img, fT, last, stop, ws = torch.ops.gsplat_hip.render_forward(packed, offsets, ids, H, W, B, G, 1.0 / 255.0,
+                                                                  1e-4, bg, True)
+    ev = torch.ops.gsplat_hip.render_forward(packed, offsets, ids, H, W, B, G, 1.0 / 255.0, 1e-4, bg, False)
+    w = torch.rand(B, H, W, 3, generator=torch.Generator().manual_seed(17))
+    grads = torch.ops.gsplat_hip.render_backward(w.to(gpu), packed, offsets, ids, fT, last, stop, ws, H, W, B, G,
+                                                 1.0 / 255.0, 1e-4, bg)
+    torch.cuda.synchronize()
+    assert torch.equal(ev[0], img)
+    oracle_parity(sc, H, W, B, G, tuple(bg), w.numpy(), img.cpu().numpy(), [g.cpu().numpy() for g in grads],
+                  "torch.ops", gpu_last=last.cpu().numpy())
