@@ -9,10 +9,11 @@
 // the tile's pixel-centre rectangle meets the splat's alpha >= threshold
 // ellipse (reference count_tiles / emit_binned_ids,
 // variants/v8/csrc/metal/gsplat_v8_kernels.metal:244-327).  A wavefront takes
-// 64 splats, prefix-sums their candidate counts in registers and then tests
-// 64 candidates per step whatever splats they belong to (each lane finds its
-// candidate's splat by binary search over the prefix sums in LDS), so a splat
-// with thousands of candidate tiles no longer serialises one lane.
+// kWalkSplats (32) splats, prefix-sums their candidate counts in registers
+// and then tests 64 candidates per step whatever splats they belong to (each
+// lane finds its candidate's splat by binary search over the prefix sums in
+// LDS), so a splat with thousands of candidate tiles no longer serialises one
+// lane.
 //
 // count_kernel  original order: per-splat hit counts and per-workgroup sums
 //   (sum_kernel turns them into the pair count N).

@@ -506,10 +506,12 @@ int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
                   (long long)n_pairs);
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
+  // the eval forward (no state outputs) records no segments
+  const int64_t ws_pairs = out_final_T != nullptr ? n_pairs : 0;
   if (workspace != nullptr &&
-      workspace_bytes < gs::render_workspace_bytes(P, n_pairs)) {
+      workspace_bytes < gs::render_workspace_bytes(P, ws_pairs)) {
     gs::set_error("gsplat_hip_render_forward: workspace too small (%zu < %zu)",
-                  workspace_bytes, gs::render_workspace_bytes(P, n_pairs));
+                  workspace_bytes, gs::render_workspace_bytes(P, ws_pairs));
     return GSPLAT_ERR_WORKSPACE;
   }
   return gs::launch_render_forward(P, packed, tile_offsets, binned_ids, out_rgb,

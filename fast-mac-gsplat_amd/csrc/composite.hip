@@ -51,6 +51,8 @@
 // atomic into the original splat order) and the ninth by DPP row steps.
 #include "gs_internal.h"
 #include "gs_predicate.h"
+#define GS_HD __device__ __forceinline__
+#include "gs_strip.h"
 
 namespace gs {
 namespace {
@@ -95,46 +97,20 @@ struct Staged {
   float4 s1[kBatch];  // C, opacity, r, g
 };
 
-// Bit k set unless strip k of the tile at (x0, y0) certainly holds no pixel
-// with p >= plim.  The support ellipse q(dx, dy) = a dx^2 + 2b dx dy + c dy^2
-// <= tc (tau = -2 ln(thr/o) = -2 ln(2) plim, enlarged to tc = 1.02 tau +
-// 1e-3) cut by the tile's slab of pixel-centre columns dx in [dxa, dxb] is
-// convex, so its rows form one interval [dy_lo, dy_hi]: a strip is kept iff
-// its pixel-centre rows meet it.  On column dx the ellipse spans
-//   dy = (-b dx +- sqrt(c tc - det dx^2)) / c,
-// whose upper end is concave in dx with its maximum at the top point
-// dx_t = -b hy / a (hy = sqrt(a tc / det)) and whose lower end is convex with
-// its minimum at -dx_t; clamping those points into the slab gives dy_hi and
-// dy_lo.  The margin of tc covers the rounding of p's chain and of these
-// hardware sqrt / rcp (about 1 ulp) as long as det > 1e-3 a c
-// (|b| < (1 - 5e-4) sqrt(ac)); other conics are never culled.
+// Strip culling (gs_strip.h) with the hardware reciprocal and square root.
+struct HwOps {
+  static __device__ __forceinline__ float rcp(float x) {
+    return __builtin_amdgcn_rcpf(x);
+  }
+  static __device__ __forceinline__ float sqrt(float x) {
+    return __builtin_amdgcn_sqrtf(x);
+  }
+};
+
 __device__ __forceinline__ uint32_t strip_mask(float mx, float my, float a,
                                                float b, float c, float plim,
                                                int x0, int y0) {
-  if (plim > 0.0f) return 0u;  // p <= 0 < plim: invisible everywhere
-  const float tau = -1.38629436f * plim;
-  const float det = a * c - b * b;
-  if (!(a > 0.0f && c > 0.0f && det > 1e-3f * (a * c) && tau < 3.0e38f))
-    return 0xFu;
-  const float tc = tau * 1.02f + 1e-3f;
-  const float inv_c = __builtin_amdgcn_rcpf(c);
-  const float hy = __builtin_amdgcn_sqrtf(a * tc * __builtin_amdgcn_rcpf(det));
-  const float dx_t = -b * hy * __builtin_amdgcn_rcpf(a);
-  const float dxa = ((float)x0 + 0.5f) - mx, dxb = dxa + 15.0f;
-  const float ct = c * tc;
-  const float ut = fminf(fmaxf(dx_t, dxa), dxb);
-  const float ub = fminf(fmaxf(-dx_t, dxa), dxb);
-  const float y_hi =
-      my + (-b * ut + __builtin_amdgcn_sqrtf(fmaxf(ct - det * ut * ut, 0.0f))) * inv_c;
-  const float y_lo =
-      my + (-b * ub - __builtin_amdgcn_sqrtf(fmaxf(ct - det * ub * ub, 0.0f))) * inv_c;
-  uint32_t m = 0u;
-#pragma unroll
-  for (int k = 0; k < kPix; ++k) {
-    const float r0 = (float)(y0 + 4 * k) + 0.5f;  // first and last row centre
-    if (y_lo <= r0 + 3.0f && y_hi >= r0) m |= 1u << k;
-  }
-  return m;
+  return strip_mask_t<HwOps>(mx, my, a, b, c, plim, x0, y0);
 }
 
 // Mask bit of a "plain" record: for it the compositors' tests p <= 0 and
@@ -275,7 +251,8 @@ constexpr int kLongStrips = 1;      // strips per wavefront of the long kernel
 
 struct HeavyState {      // all null: every tile is walked whole by one wave
   int32_t* counters;     // [0] slots handed out, [1] tiles handed off
-                         // (zeroed by the forward)
+                         // (zeroed by the forward), [2] max_slots of the
+                         // forward that recorded segments (-1: none)
   int32_t* tile_slot;    // [T] slot of segment 0, -1: no usable chain
   int32_t* slot_tile;    // [max_slots] tile of each slot
   int32_t* slot_seg;     // [max_slots] segment index of each slot
@@ -499,6 +476,10 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
   const int start = tile_offsets[tc.tile];
   const int end = tile_offsets[tc.tile + 1];
   if (H.rec != nullptr && threadIdx.x == 0) H.tile_slot[tc.tile] = -1;
+  // The workspace's layout follows n_pairs: the backward uses the segment
+  // records only if it was given the same n_pairs (same max_slots).
+  if (H.counters != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+    H.counters[2] = H.rec != nullptr ? H.max_slots : -1;
   // With a workspace a tile longer than kHandoff is walked here only up to
   // kHandoff, so segment boundaries inside this loop (and records) occur
   // only without a workspace.
@@ -999,9 +980,12 @@ __device__ __forceinline__ void bwd_walk(
   }
 }
 
+// True when the backward walks this tile as segments: the forward recorded
+// them (with the same workspace layout) and the tile's stop exceeds one.
 __device__ __forceinline__ bool heavy_backward(const HeavyState& H, int tile,
                                                int nstop) {
-  return H.tile_slot != nullptr && H.tile_slot[tile] >= 0 && nstop > kSegSplats;
+  return H.tile_slot != nullptr && H.counters[2] == H.max_slots &&
+         H.tile_slot[tile] >= 0 && nstop > kSegSplats;
 }
 
 // Decodes segment slot m: tile, segment index k, segment count and the range
@@ -1101,6 +1085,7 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
 // Segment records kept at most: one per segment of every tile in the worst
 // case, capped at T + 1024 (4 KB each: at most 16 B per pixel + 4 MB).
 // Tiles that find the records full are walked whole by the backward.
+// n_pairs = 0 (the eval forward, which records nothing) gives one slot.
 size_t heavy_max_slots(const RasterParams& P, int64_t n_pairs) {
   const int64_t per_seg = n_pairs / kSegSplats;
   const int64_t worst =
@@ -1153,7 +1138,9 @@ int launch_render_forward(const RasterParams& P, const float* packed,
                           int32_t* out_tile_stop, int64_t n_pairs,
                           void* workspace, hipStream_t stream) {
   if (P.num_tiles == 0) return GSPLAT_OK;
-  HeavyState H = heavy_state(P, n_pairs, workspace);
+  // Without the state outputs no segment is recorded: the layout of
+  // n_pairs = 0 (no slot area to speak of) fits the eval workspace.
+  HeavyState H = heavy_state(P, out_T != nullptr ? n_pairs : 0, workspace);
   if (out_T == nullptr) H.rec = nullptr;  // no backward: hand-off only
   const float4* pk = reinterpret_cast<const float4*>(packed);
   if (H.counters != nullptr) {

@@ -367,7 +367,8 @@ def render_forward(meta: _lib.RasterMeta, st: BinState, *, save_state: bool):
         final_T = torch.empty((B, H, W), dtype=torch.float32, device=dev)
         last = torch.empty((B, H, W), dtype=torch.int32, device=dev)
         tile_stop = _empty(tiles, torch.int32, dev)
-    wsb = L.gsplat_hip_render_workspace_bytes(meta, st.capacity)
+    # the eval forward records no segments: its workspace has no record area
+    wsb = L.gsplat_hip_render_workspace_bytes(meta, st.capacity if save_state else 0)
     ws = _empty(max(wsb, 1), torch.uint8, dev)
     with _timed("render_forward"):
         check(L.gsplat_hip_render_forward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.pairs), ptr(img),

@@ -206,13 +206,19 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
                    void* count_event, void* status_event);
 
 /* -------------------------------------------------------------- composite
- * Compositor workspace (optional; n_pairs is the N of the binning).  With it
- * the forward continues a tile that still has live pixels after 128 splats
- * with four wavefronts, and, when the state outputs are given, records the
- * tile's 128-splat segments so that the backward given the same workspace
- * walks them in parallel.  Without it every tile is walked by one wavefront.
- * Images are identical either way; gradients differ only in summation
- * order.  The forward overwrites the workspace; the backward only reads it. */
+ * Compositor workspace (optional).  With it the forward continues a tile
+ * that still has live pixels after 128 splats with four wavefronts, and,
+ * when the state outputs are given, records the tile's 128-splat segments so
+ * that the backward given the same workspace walks them in parallel.
+ * Without it every tile is walked by one wavefront.  Images are identical
+ * either way; gradients differ only in summation order.  The forward
+ * overwrites the workspace; the backward only reads it.  n_pairs sizes the
+ * record area: the pair count N or any capacity >= N (the length of the
+ * binned_ids buffer), and the forward and the backward of one binning must
+ * receive the same value (the layout follows it; a backward given another
+ * n_pairs ignores the records and walks every tile whole).  n_pairs = 0
+ * sizes the smaller workspace of the eval forward (state outputs NULL),
+ * which records no segments. */
 size_t gsplat_hip_render_workspace_bytes(const gsplat_raster_meta* meta,
                                          int64_t n_pairs);
 

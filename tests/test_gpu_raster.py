@@ -500,3 +500,75 @@ def test_torch_ops_vs_tile_oracle(gpu):
     assert torch.equal(ev[0], img)
     oracle_parity(sc, H, W, B, G, tuple(bg), w.numpy(), img.cpu().numpy(), [g.cpu().numpy() for g in grads],
                   "torch.ops", gpu_last=last.cpu().numpy())
+
+
+def _dust(seed, B, G, H, W):
+    """Very small, faint splats: each is visible only near its centre, so every
+    pixel stays alive through the whole tile list (hundreds of thousands of
+    splats per tile are walked)."""
+    g = torch.Generator().manual_seed(seed)
+    m = torch.rand(B, G, 2, generator=g) * torch.tensor([W, H], dtype=torch.float32)
+    sig = 0.2 + 0.1 * torch.rand(B, G, generator=g)
+    inv = 1.0 / sig ** 2
+    return {"means2d": m, "conics": torch.stack([inv, torch.zeros_like(inv), inv], dim=-1),
+            "colors": torch.rand(B, G, 3, generator=g),
+            "opacities": 0.006 + 0.006 * torch.rand(B, G, generator=g),
+            "depths": torch.rand(B, G, generator=g)}
+
+
+def test_segment_records_overflow(gpu):
+    """More 128-splat segments are walked than the workspace holds (T + 1024
+    records for a 2x2-tile image): tiles that find the records full break
+    their chain and are walked whole by the backward.  Checked against the
+    oracle, with the overflow asserted from the workspace's slot counter."""
+    from torch_gsplat_bridge_fast import _lib, _ops
+
+    B, G, H, W = 1, 300_000, 32, 32
+    sc = _dust(41, B, G, H, W)
+    print(f"segment overflow {W}x{H} G={G}", flush=True)
+    T, last, stop, st = gpu_state(sc, H, W, B, G, (0.0, 0.0, 0.0))
+    meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, (0, 0, 0))
+    img, T2, last2, stop2, ws = _ops.render_forward(meta, st, save_state=True)
+    torch.cuda.synchronize()
+    slots_used = int(ws[:4].view(torch.int32).item())
+    max_slots = 4 + 1024
+    assert slots_used > max_slots, slots_used          # the records ran out
+    assert int(stop2.min().item()) > 128 * 300           # every tile walked far past one segment
+    w = torch.rand(B, H, W, 3, generator=torch.Generator().manual_seed(42))
+    grads = _ops.render_backward(meta, st, T2, last2, stop2, w.to(gpu), ws)
+    torch.cuda.synchronize()
+    oracle_parity(sc, H, W, B, G, (0.0, 0.0, 0.0), w.numpy(), img.cpu().numpy(), [g.cpu().numpy() for g in grads],
+                  "segment overflow", gpu_last=last2.cpu().numpy())
+
+
+def test_backward_with_another_n_pairs_ignores_records(gpu):
+    """The compositor workspace's layout follows n_pairs: a backward given
+    another n_pairs than its forward must not read the segment records (it
+    walks every tile whole) and still meets the bar."""
+    from torch_gsplat_bridge_fast import _lib, _ops
+
+    B, G, H, W = 2, 2500, 48, 80
+    sc = _faint_crowd(21, B, G, H, W)
+    T, last, stop, st = gpu_state(sc, H, W, B, G, (0.0, 0.0, 0.0))
+    meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, (0, 0, 0))
+    L = _lib.lib()
+    n1, n2 = st.capacity, st.capacity + 50_000
+    assert L.gsplat_hip_render_workspace_bytes(meta, n2) > L.gsplat_hip_render_workspace_bytes(meta, n1)
+    wsb = L.gsplat_hip_render_workspace_bytes(meta, n2)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=gpu)
+    img = torch.empty((B, H, W, 3), device=gpu)
+    T1, last1 = torch.empty((B, H, W), device=gpu), torch.empty((B, H, W), dtype=torch.int32, device=gpu)
+    stop1 = torch.empty((st.num_tiles,), dtype=torch.int32, device=gpu)
+    _lib.check(L.gsplat_hip_render_forward(meta, _lib.ptr(st.packed), _lib.ptr(st.tile_offsets), _lib.ptr(st.pairs),
+                                           _lib.ptr(img), _lib.ptr(T1), _lib.ptr(last1), _lib.ptr(stop1), n1,
+                                           _lib.ptr(ws), wsb, _lib.stream_of(img)), "forward")
+    w = torch.rand(B, H, W, 3, generator=torch.Generator().manual_seed(8))
+    out = [torch.empty(s, device=gpu) for s in ((B, G, 2), (B, G, 3), (B, G, 3), (B, G))]
+    _lib.check(L.gsplat_hip_render_backward(meta, _lib.ptr(st.packed), _lib.ptr(st.tile_offsets), _lib.ptr(st.pairs),
+                                            _lib.ptr(T1), _lib.ptr(last1), _lib.ptr(stop1), _lib.ptr(w.to(gpu)),
+                                            *[_lib.ptr(t) for t in out], n2, _lib.ptr(ws), wsb,
+                                            _lib.stream_of(img)), "backward")
+    torch.cuda.synchronize()
+    assert int(stop1.max().item()) > 256
+    oracle_parity(sc, H, W, B, G, (0.0, 0.0, 0.0), w.numpy(), img.cpu().numpy(), [t.cpu().numpy() for t in out],
+                  "backward with another n_pairs", gpu_last=last1.cpu().numpy())
