@@ -10,9 +10,10 @@ backward compositing, gradients in the original order.
 Prints ONE JSON line.  `roofline` is for the dominant kernel (the backward
 compositor, which dominates step time): its launch time is measured live with
 HIP events (torch.cuda.Event on the stream the library launches on) over the
-timed steps.  `cpu_baseline` times the CPU oracle (single-threaded C
-restatement of the reference algorithm, oracle/tile_oracle.c) on the same
-scene, forward+backward, once.
+timed steps.  `cpu_baseline` times the CPU oracle (the C
+restatement of the reference algorithm, oracle/tile_oracle.c, on the host's
+threads) on the same scene, forward+backward, once, and the reference's
+dense Torch renderer on config 0.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 2]
     python bench.py --trace FILE --height H --width W [--trace-batch B] [--trace-gaussians G]
@@ -77,7 +78,8 @@ def stage_roofline(op_ms, BG, N, walked, T, P, three_d, depth_passes=4, pair_pas
             out[k] = {"bound": "valu", "achieved": round(a, 2), "unit": "TFLOP/s",
                       "frac": round(a / PEAK_FP32_TFLOPS, 4)}
     return out
-PEAK_HBM_GBS = 8000.0      # MI355X published HBM3E bandwidth
+
+
 # The reference's best published cfg2 forward+backward: 65.754 ms on an Apple
 # M4 (v8_direct; benchmarks/full_rasterizer_benchmark_v8_prior_compare_4k64k.md:34)
 # = 4096*4096 / 65.754 ms = 255.15 Mpix/s.
@@ -98,10 +100,33 @@ def _cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(sc, H, W, B, G, w_np):
-    """Times the CPU oracle (forward + backward) once on the full scene."""
-    from oracle import tile_oracle as TO
+def _host_threads() -> int:
+    """Threads the CPU legs use: OMP_NUM_THREADS (the box's CPU share) or the core count."""
+    raw = os.environ.get("OMP_NUM_THREADS", "")
+    return int(raw) if raw.isdigit() and int(raw) > 0 else (os.cpu_count() or 1)
 
+
+def cpu_baseline(sc, H, W, B, G, w_np):
+    """The CPU baselines, timed on this host (reported beside the GPU figure,
+    not the optimisation target):
+      * value: the C restatement of the reference's tile algorithm
+        (oracle/tile_oracle.c, OpenMP over tiles and splats) on the full
+        workload, one forward + backward (binning, compositing, gradients);
+      * dense_torch_cfg0: the reference's dense Torch renderer torch_direct
+        (benchmarks/benchmark_full_matrix.py:128-152, restated in
+        oracle/dense_reference.py, no early stop) on config 0 (512x512,
+        512 splats), forward + loss.backward(), with torch's CPU threads set
+        to the same count; median of 3 after one warm-up.  The dense
+        renderer's autograd graph does not fit in memory at configs 1-4."""
+    import numpy as np
+    import torch
+
+    from oracle import tile_oracle as TO
+    from oracle.dense_reference import dense_reference
+    from torch_gsplat_bridge_fast.scenes import make_scene_2d
+
+    n = _host_threads()
+    TO.set_threads(n)
     meta = TO.make_meta(H, W, B, G)
     s = TO.Scene(*(sc[k].numpy() for k in KEYS), B, G)
     t0 = time.perf_counter()
@@ -109,14 +134,37 @@ def cpu_baseline(sc, H, W, B, G, w_np):
     TO.render_forward(meta, s, bins)
     TO.render_backward(meta, s, bins, w_np)
     dt = time.perf_counter() - t0
+
+    torch.set_num_threads(n)
+    sc0 = make_scene_2d(0, seed=0)
+    H0, W0 = sc0["H"], sc0["W"]
+    w0 = torch.rand(H0, W0, 3, generator=torch.Generator().manual_seed(123))
+    times = []
+    for _ in range(4):
+        ts = [sc0[k][0].clone().requires_grad_(k != "depths") for k in KEYS]
+        t1 = time.perf_counter()
+        img = dense_reference(*ts, H0, W0, early_stop=False)
+        (img * w0).sum().backward()
+        times.append(time.perf_counter() - t1)
+    dense_s = float(np.median(times[1:]))
     return {
         "value": (B * H * W) / dt / 1e6,
         "unit": "Mpix/s",
         "ms_per_step": dt * 1e3,
-        "cores": 1,
+        "cores": n,
         "kind": "port",
-        "sample": f"full workload ({W}x{H}, B={B}, G={G}), one forward+backward, single thread; "
-                  f"C restatement of the reference tile algorithm; CPU: {_cpu_model()}",
+        "sample": f"full workload ({W}x{H}, B={B}, G={G}), one forward+backward of the C restatement of the "
+                  f"reference tile algorithm on {n} threads (OpenMP); CPU: {_cpu_model()}, "
+                  f"{os.cpu_count()} logical CPUs visible",
+        "dense_torch_cfg0": {
+            "value": H0 * W0 / dense_s / 1e6,
+            "unit": "Mpix/s",
+            "ms_per_step": dense_s * 1e3,
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": "config 0 (512x512, 512 splats): the reference's dense torch_direct renderer restated "
+                      "(oracle/dense_reference.py, no early stop), fp32 forward + loss.backward(), median of 3",
+        },
     }
 
 
