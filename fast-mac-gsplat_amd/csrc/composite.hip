@@ -262,6 +262,8 @@ struct HeavyState {      // all null: every tile is walked whole by one wave
   float* hand_T;         // [T][256] T of each pixel at the hand-off
   float4* rec;           // [max_slots][256] (r, g, b, T at segment end);
                          // null: no records (forward without state)
+  float* acc;            // [num_splats][kAccFloats] gradient sums of the
+                         // backward; null with n_pairs = 0
   int max_slots;
 };
 
@@ -723,12 +725,21 @@ __device__ __forceinline__ float row_sum_dpp(float x) {
   return x;
 }
 
+// x += x of the lane that the DPP control selects, in one v_add_f32_dpp, for
+// the rows of ROW_MASK; the other rows keep x (as x + 0 would).  Written as
+// inline assembly because the compiler splits a partial-row-mask update (and
+// one it sinks into a branch) into a zero move, a DPP move and an add.  The
+// s_nop 1 gives the two wait states a DPP read needs after a VALU write of
+// its source, which the compiler does not insert for inline assembly.
+#define GS_ADD_DPP(x, CTRL)                                                  \
+  asm("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 " CTRL " bank_mask:0xf" : "+v"(x))
+
 // Sum over the 64 lanes, left in every lane of row 3 (lanes 48..63):
 // row sums, then row_bcast:15 and row_bcast:31 carry them upward.
 __device__ __forceinline__ float wave_sum_row3(float x) {
   x = row_sum_dpp(x);
-  x += dpp_src<0x142, 0xA>(x);
-  x += dpp_src<0x143, 0xC>(x);
+  GS_ADD_DPP(x, "row_bcast:15 row_mask:0xa");
+  GS_ADD_DPP(x, "row_bcast:31 row_mask:0xc");
   return x;
 }
 
@@ -737,7 +748,7 @@ __device__ __forceinline__ float wave_sum_row3(float x) {
 __device__ __forceinline__ float group8_sum_dpp(float x) {
   x += dpp_src<0xB1>(x);
   x += dpp_src<0x4E>(x);
-  x += dpp_src<0x141>(x);
+  GS_ADD_DPP(x, "row_half_mirror row_mask:0xf");
   return x;
 }
 
@@ -760,9 +771,25 @@ __device__ __forceinline__ void wave_lds_sync() {
 // DPP.  LDS accesses issue on their own port, so the reduction costs few
 // vector-ALU slots, the compositor's bound.
 constexpr int kGradQ = 8;
+constexpr int kAccFloats = 16;  // floats per accumulator record (64 bytes)
 struct BwdShared {
   Staged S;
   float red[kGradQ * kLanes];
+};
+
+// Where the backward adds its gradients (in original splat order): one
+// accumulator record of kAccFloats floats per splat, or, without one, the
+// four output arrays.  A record holds a splat's nine gradient entries in one
+// 64-byte line, {g_mean x, y, g_conic a, b, c, g_colour r, g, b, g_opacity},
+// so the nine atomics a tile adds for a splat touch one cache line instead
+// of four or five; render_grads_unpack_kernel copies the records to the
+// output arrays.
+struct GradOut {
+  float* g_means2d;
+  float* g_conics;
+  float* g_colors;
+  float* g_opac;
+  float* acc;  // [num_splats][kAccFloats] or null
 };
 
 // Where group q = lane / 8 sends its total: q = 0..7 is
@@ -774,22 +801,32 @@ struct GradTarget {
   float scale;
 };
 
-__device__ __forceinline__ GradTarget grad_target(float* g_means2d,
-                                                  float* g_conics,
-                                                  float* g_colors) {
+__device__ __forceinline__ GradTarget grad_target(const GradOut& G) {
   // g_mean = -(2/L) V_m since a = -2A/L, b = -B/L, c = -2C/L;
   // g_conic = (-V_ca/2, -V_cb, -V_cc/2).
   constexpr float kMeanScale = -2.0f / kLog2e;
-  switch (threadIdx.x >> 3) {
-    case 0: return {g_means2d + 0, 8, kMeanScale};
-    case 1: return {g_means2d + 1, 8, kMeanScale};
-    case 2: return {g_conics + 0, 12, -0.5f};
-    case 3: return {g_conics + 1, 12, -1.0f};
-    case 4: return {g_conics + 2, 12, -0.5f};
-    case 5: return {g_colors + 0, 12, 1.0f};
-    case 6: return {g_colors + 1, 12, 1.0f};
-    default: return {g_colors + 2, 12, 1.0f};
+  const int q = threadIdx.x >> 3;
+  if (G.acc != nullptr) {
+    const float scale =
+        q < 2 ? kMeanScale : q == 3 ? -1.0f : q < 5 ? -0.5f : 1.0f;
+    return {G.acc + q, 4 * kAccFloats, scale};
   }
+  switch (q) {
+    case 0: return {G.g_means2d + 0, 8, kMeanScale};
+    case 1: return {G.g_means2d + 1, 8, kMeanScale};
+    case 2: return {G.g_conics + 0, 12, -0.5f};
+    case 3: return {G.g_conics + 1, 12, -1.0f};
+    case 4: return {G.g_conics + 2, 12, -0.5f};
+    case 5: return {G.g_colors + 0, 12, 1.0f};
+    case 6: return {G.g_colors + 1, 12, 1.0f};
+    default: return {G.g_colors + 2, 12, 1.0f};
+  }
+}
+
+// Where the opacity gradient goes (scale 1).
+__device__ __forceinline__ GradTarget opac_target(const GradOut& G) {
+  if (G.acc != nullptr) return {G.acc + 8, 4 * kAccFloats, 1.0f};
+  return {G.g_opac, 4, 1.0f};
 }
 
 // Per-pixel state of the backward walk (4 pixels per lane).
@@ -859,14 +896,20 @@ __device__ __forceinline__ bool needs_last_test(const RasterParams& P,
 template <bool kCheckLast, bool kPlain>
 __device__ __forceinline__ void bwd_batch(
     BwdShared& SH, uint32_t bmask, int n, int cstart, float max_alpha,
-    const GradTarget& target, BwdPixels& Q, float* __restrict__ g_opac) {
+    const GradTarget& target, const GradTarget& opac, BwdPixels& Q) {
   const Staged& S = SH.S;
   const int lane = threadIdx.x;
   const bool group_head = (lane & 7) == 0;
-  // this lane's eight values of its group's quantity in red: 16-byte chunks
-  // l and l + 8 of the row (l = lane % 8), so that the eight lanes of a
-  // group read 128 consecutive bytes per load (no bank conflict)
-  const float* red_in = SH.red + (lane >> 3) * kLanes + (lane & 7) * 4;
+  // this lane's eight values of its group's quantity q = lane / 8 in red:
+  // 16-byte chunks l and l + 8 of the row (l = lane % 8), so that the eight
+  // lanes of a group read 128 consecutive bytes per load.  Rows are 256 bytes
+  // apart, one turn of the 64 four-byte LDS banks, so odd groups read their
+  // two halves in the other order: each load then spreads over all 64 banks
+  // (no bank conflict).  The sum below adds the two halves' sums, which is
+  // commutative, so the order does not change the result.
+  const int q = lane >> 3;
+  const float* red_in0 = SH.red + q * kLanes + (lane & 7) * 4 + (q & 1) * 32;
+  const float* red_in1 = SH.red + q * kLanes + (lane & 7) * 4 + (~q & 1) * 32;
   // Per-lane partial sums of the current splat; zero between splats.
   float S0 = 0.f, S1 = 0.f, S2 = 0.f;
   float acc_r = 0.f, acc_g = 0.f, acc_b = 0.f;
@@ -935,8 +978,8 @@ __device__ __forceinline__ void bwd_batch(
       S0 = S1 = S2 = 0.f;
       acc_r = acc_g = acc_b = 0.f;
       wave_lds_sync();
-      const float4 u = *reinterpret_cast<const float4*>(red_in);
-      const float4 w = *reinterpret_cast<const float4*>(red_in + 32);
+      const float4 u = *reinterpret_cast<const float4*>(red_in0);
+      const float4 w = *reinterpret_cast<const float4*>(red_in1);
       const float tot = group8_sum_dpp(((u.x + u.y) + (u.z + u.w)) +
                                        ((w.x + w.y) + (w.z + w.w)));
       const uint32_t orig = uniform_bits(a2.y);
@@ -945,8 +988,11 @@ __device__ __forceinline__ void bwd_batch(
                             reinterpret_cast<char*>(target.base) +
                             (uint64_t)orig * target.stride),
                         tot * target.scale);
-      if (lane == kLanes - 1)
-        unsafeAtomicAdd(g_opac + orig, r3 * a2.w);  // a2.w = 1 / opacity
+      if (lane == kLanes - 1)  // a2.w = 1 / opacity
+        unsafeAtomicAdd(reinterpret_cast<float*>(
+                            reinterpret_cast<char*>(opac.base) +
+                            (uint64_t)orig * opac.stride),
+                        r3 * a2.w);
       wave_lds_sync();  // loads done before the next splat's stores
     }
   }
@@ -958,10 +1004,9 @@ template <bool kCheckLast>
 __device__ __forceinline__ void bwd_walk(
     const RasterParams& P, const float4* __restrict__ packed,
     const int32_t* __restrict__ binned, int start, int lo, int hi,
-    const TileCoord& tc, BwdShared& SH, BwdPixels& Q,
-    float* __restrict__ g_means2d, float* __restrict__ g_conics,
-    float* __restrict__ g_colors, float* __restrict__ g_opac) {
-  const GradTarget target = grad_target(g_means2d, g_conics, g_colors);
+    const TileCoord& tc, BwdShared& SH, BwdPixels& Q, const GradOut& G) {
+  const GradTarget target = grad_target(G);
+  const GradTarget opac = opac_target(G);
   const float max_alpha = fminf(P.max_alpha, 1.0f);
   const float o_plain = plain_opacity_limit(max_alpha);
   for (int cend = hi; cend > lo; cend -= kBatch) {
@@ -972,12 +1017,32 @@ __device__ __forceinline__ void bwd_walk(
         stage_batch<false>(packed, binned, start + cstart, n, tc, o_plain, SH.S);
     __syncthreads();
     if (batch_plain(bmask))
-      bwd_batch<kCheckLast, true>(SH, bmask, n, cstart, max_alpha, target, Q,
-                                  g_opac);
+      bwd_batch<kCheckLast, true>(SH, bmask, n, cstart, max_alpha, target,
+                                  opac, Q);
     else
-      bwd_batch<kCheckLast, false>(SH, bmask, n, cstart, max_alpha, target, Q,
-                                   g_opac);
+      bwd_batch<kCheckLast, false>(SH, bmask, n, cstart, max_alpha, target,
+                                   opac, Q);
   }
+}
+
+// Copies the backward's accumulator records (GradOut) to the four gradient
+// arrays: one thread per splat.
+__global__ __launch_bounds__(256) void render_grads_unpack_kernel(GradOut G,
+                                                                  int n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float4* rec = reinterpret_cast<const float4*>(G.acc + i * kAccFloats);
+  const float4 a = rec[0], b = rec[1];
+  const float o = G.acc[i * kAccFloats + 8];
+  G.g_means2d[2 * i + 0] = a.x;
+  G.g_means2d[2 * i + 1] = a.y;
+  G.g_conics[3 * i + 0] = a.z;
+  G.g_conics[3 * i + 1] = a.w;
+  G.g_conics[3 * i + 2] = b.x;
+  G.g_colors[3 * i + 0] = b.y;
+  G.g_colors[3 * i + 1] = b.z;
+  G.g_colors[3 * i + 2] = b.w;
+  G.g_opac[i] = o;
 }
 
 // True when the backward walks this tile as segments: the forward recorded
@@ -1015,9 +1080,8 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
     const int32_t* __restrict__ tile_offsets,
     const int32_t* __restrict__ binned, const float* __restrict__ final_T,
     const int32_t* __restrict__ last_in, const int32_t* __restrict__ tile_stop,
-    const float* __restrict__ grad_rgb, float* __restrict__ g_means2d,
-    float* __restrict__ g_conics, float* __restrict__ g_colors,
-    float* __restrict__ g_opac, HeavyState H, int seg_blocks) {
+    const float* __restrict__ grad_rgb, GradOut G, HeavyState H,
+    int seg_blocks) {
   __shared__ BwdShared SH;
   const int bid = (int)blockIdx.x;
   const bool seg = bid < seg_blocks;
@@ -1075,10 +1139,10 @@ __global__ __launch_bounds__(kLanes) void render_bwd_kernel(
     // (T_end > T_final > threshold), so the test sees the final state.
     if (needs_last_test(P, tc, Q))
       bwd_walk<true>(P, packed, binned, tile_offsets[tile], lo, hi, tc, SH, Q,
-                     g_means2d, g_conics, g_colors, g_opac);
+                     G);
     else
       bwd_walk<false>(P, packed, binned, tile_offsets[tile], lo, hi, tc, SH, Q,
-                      g_means2d, g_conics, g_colors, g_opac);
+                      G);
   }
 }
 
@@ -1095,11 +1159,18 @@ size_t heavy_max_slots(const RasterParams& P, int64_t n_pairs) {
 
 }  // namespace
 
+// The backward's accumulator records (absent from the eval workspace).
+size_t acc_bytes(const RasterParams& P, int64_t n_pairs) {
+  return n_pairs > 0 ? align_up((size_t)P.num_splats * 4 * kAccFloats, 256)
+                     : 0;
+}
+
 size_t render_workspace_bytes(const RasterParams& P, int64_t n_pairs) {
   const size_t slots = heavy_max_slots(P, n_pairs);
   const size_t T = (size_t)P.num_tiles;
   return 256 + 3 * align_up(T * 4, 256) + align_up(T * 256 * 4, 256) +
-         3 * align_up(slots * 4, 256) + align_up(slots * 256 * sizeof(float4), 256);
+         3 * align_up(slots * 4, 256) +
+         align_up(slots * 256 * sizeof(float4), 256) + acc_bytes(P, n_pairs);
 }
 
 namespace {
@@ -1126,6 +1197,8 @@ HeavyState heavy_state(const RasterParams& P, int64_t n_pairs, void* ws) {
   H.slot_next = reinterpret_cast<int32_t*>(p);
   p += align_up(slots * 4, 256);
   H.rec = reinterpret_cast<float4*>(p);
+  p += align_up(slots * 256 * sizeof(float4), 256);
+  H.acc = n_pairs > 0 ? reinterpret_cast<float*>(p) : nullptr;
   H.max_slots = (int)slots;
   return H;
 }
@@ -1169,20 +1242,29 @@ int launch_render_backward(const RasterParams& P, const float* packed,
                            float* g_conics, float* g_colors, float* g_opac,
                            int64_t n_pairs, void* workspace,
                            hipStream_t stream) {
-  int rc = launch_zero_grads(g_means2d, g_conics, g_colors, g_opac,
-                             P.num_splats, stream);
+  const HeavyState H = heavy_state(P, n_pairs, workspace);
+  const GradOut G{g_means2d, g_conics, g_colors, g_opac,
+                  P.num_tiles > 0 ? H.acc : nullptr};
+  int rc = G.acc != nullptr
+               ? launch_fill_f32(G.acc, 0.0f,
+                                 (int64_t)P.num_splats * kAccFloats, stream)
+               : launch_zero_grads(g_means2d, g_conics, g_colors, g_opac,
+                                   P.num_splats, stream);
   if (rc) return rc;
   if (P.num_tiles == 0) return GSPLAT_OK;
-  const HeavyState H = heavy_state(P, n_pairs, workspace);
   const float4* pk = reinterpret_cast<const float4*>(packed);
   // One block per possible slot, rounded to a multiple of 8 (XCD mapping).
   const int seg_blocks = H.counters ? (H.max_slots + 7) & ~7 : 0;
   hipLaunchKernelGGL(render_bwd_kernel,
                      dim3((unsigned)(seg_blocks + P.num_tiles)), dim3(kLanes),
                      0, stream, P, pk, tile_offsets, binned_ids, final_T, last,
-                     tile_stop, grad_rgb, g_means2d, g_conics, g_colors,
-                     g_opac, H, seg_blocks);
-  return check_launch("render_bwd_kernel");
+                     tile_stop, grad_rgb, G, H, seg_blocks);
+  rc = check_launch("render_bwd_kernel");
+  if (rc || G.acc == nullptr || P.num_splats <= 0) return rc;
+  hipLaunchKernelGGL(render_grads_unpack_kernel,
+                     dim3((unsigned)((P.num_splats + 255) / 256)), dim3(256),
+                     0, stream, G, P.num_splats);
+  return check_launch("render_grads_unpack_kernel");
 }
 
 }  // namespace gs

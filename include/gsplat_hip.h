@@ -212,7 +212,11 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
  * that the backward given the same workspace walks them in parallel.
  * Without it every tile is walked by one wavefront.  Images are identical
  * either way; gradients differ only in summation order.  The forward
- * overwrites the workspace; the backward only reads it.  n_pairs sizes the
+ * overwrites the workspace.  The backward reads the forward's part and
+ * uses an area after it as its own scratch: one 64-byte accumulator record
+ * per splat, so that the nine atomic additions a tile makes to a splat's
+ * gradients go to one cache line (without a workspace they go straight to
+ * the four output arrays).  n_pairs sizes the
  * record area: the pair count N or any capacity >= N (the length of the
  * binned_ids buffer), and the forward and the backward of one binning must
  * receive the same value (the layout follows it; a backward given another
@@ -244,8 +248,8 @@ int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
  * (variants/v8/csrc/bindings.cpp:204; kernel gsplat_v8_kernels.metal:
  * 478-608) and the unsort of v8 rasterize.py:676-680: gradients are written
  * in the ORIGINAL splat order using the orig_index stored in each packed
- * record; the four gradient arrays are zeroed by this call.  workspace: the
- * forward's (or NULL). */
+ * record; the four gradient arrays are written in full by this call.
+ * workspace: the forward's (or NULL). */
 int gsplat_hip_render_backward(const gsplat_raster_meta* meta,
                                const float* packed,
                                const int32_t* tile_offsets,
