@@ -12,16 +12,16 @@
 //     lane) = index order, ranks from ballot matching as in the onesweep
 //     kernel), then the sorted keys and in-image indices of the run and
 //     every kSampleStride-th sorted key (the run's samples).
-//   depth_run_rank_kernel  one lane per element of the sorted runs: its
-//     position in the image's order is its position in its own run plus,
-//     for every other run of the image, the number of that run's keys that
-//     precede it (keys < k for later runs, keys <= k for earlier runs, so
-//     equal keys keep index order).  That count is bracketed to a window of
-//     kSampleStride - 1 keys by a search over the run's samples in LDS and
-//     finished by a 6-step binary search over the window in global memory
-//     (the searches of up to kRankGroup runs advance together, so their
-//     loads overlap).
-//     perm[rank] = in-image index.
+//   depth_run_rank_kernel  a workgroup per 256 consecutive elements of a
+//     sorted run, four threads per element: an element's position in the
+//     image's order is its position in its own run plus, for every other
+//     run of the image, the number of that run's keys that precede it (keys
+//     < k for later runs, keys <= k for earlier runs, so equal keys keep
+//     index order).  The run's samples bound those counts, for the whole
+//     chunk, to a window of the other run (about 256 + 128 keys), which the
+//     workgroup loads into LDS; each thread binary-searches its element's
+//     counts in a quarter of the runs there and the four partial positions
+//     are added.  perm[rank] = in-image index.
 //
 // No atomics, look-back or control words: nothing needs zeroing and the two
 // launches are independent of earlier calls.
@@ -37,8 +37,6 @@ constexpr int kRunRounds = kRunItems / kRunThreads;  // 64-element groups per wa
 constexpr int kSampleStride = 64;
 constexpr int kRunSamples = kRunItems / kSampleStride;
 constexpr int kMaxRuns = 32;
-constexpr int kRankThreads = 256;
-constexpr int kRankGroup = 16;   // runs searched together in the rank kernel
 static_assert(kRunRounds * kRunThreads == kRunItems, "run shape");
 
 __device__ __forceinline__ uint64_t lanes_below() {
@@ -159,69 +157,145 @@ __device__ __forceinline__ bool precedes(uint32_t x, uint32_t k,
   return below_or_equal ? (x <= k) : (x < k);
 }
 
-__global__ __launch_bounds__(kRankThreads) void depth_run_rank_kernel(
+// Number of the first n keys of the sorted array a[] (n <= 2^kLog2) that
+// precede k: they form a prefix, found by binary search.
+template <int kLog2, class Load>
+__device__ __forceinline__ int prefix_count(Load a, int n, uint32_t k,
+                                            bool below_or_equal) {
+  int c = 0;
+#pragma unroll
+  for (int step = 1 << kLog2; step > 0; step >>= 1)
+    if (c + step <= n && precedes(a(c + step - 1), k, below_or_equal))
+      c += step;
+  return c;
+}
+
+// Rank kernel: a workgroup takes 256 consecutive elements of one sorted run,
+// four threads per element (thread t: element t % 256, run group t / 256).
+// The element's counts in another run o all lie in a window [L, U) of o that
+// the run's samples bound: L from the samples that precede the chunk's first
+// key, U from those that precede its last key (the chunk's keys ascend).
+// The workgroup loads the other runs' windows into LDS in coalesced reads
+// (kWinKeys keys at most, about 256 + 128 for runs of like key
+// distributions; kLdsRuns runs at a time) and each thread finds its
+// element's counts in its runs (o = group + 4 v) by binary searches there
+// that advance together; a window longer than kWinKeys is searched in global
+// memory.  The four partial ranks are added in LDS.
+constexpr int kRankElems = 256;                  // elements per workgroup
+constexpr int kRankSplit = 4;                    // threads per element
+constexpr int kRankBlock = kRankElems * kRankSplit;
+constexpr int kWinKeys = 512;
+constexpr int kLdsRuns = 16;  // runs whose windows the LDS holds at once
+constexpr int kRunsPerThread = kLdsRuns / kRankSplit;
+constexpr int kLoadsPerThread = kLdsRuns * kWinKeys / kRankBlock;
+static_assert(kRunItems % kRankElems == 0, "a rank workgroup lies in one run");
+static_assert(kMaxRuns % kLdsRuns == 0, "run groups");
+
+__global__ __launch_bounds__(kRankBlock) void depth_run_rank_kernel(
     const uint32_t* __restrict__ run_keys,
     const uint32_t* __restrict__ run_vals,
     const uint32_t* __restrict__ samples, int G, int runs,
     int32_t* __restrict__ perm) {
   __shared__ uint32_t ss[kMaxRuns * kRunSamples];
-  const int blocks_per_seg = (G + kRankThreads - 1) / kRankThreads;
+  __shared__ int wlo[kMaxRuns], wlen[kMaxRuns];
+  __shared__ uint32_t kfl[2];
+  __shared__ uint32_t win[kLdsRuns * kWinKeys];
+  __shared__ int part[kRankSplit][kRankElems];
+  const int t = threadIdx.x;
+  const int el = t % kRankElems, grp = t / kRankElems;
+  const int blocks_per_seg = (G + kRankElems - 1) / kRankElems;
   const int seg = blockIdx.x / blocks_per_seg;
-  const int e = (blockIdx.x - seg * blocks_per_seg) * kRankThreads + threadIdx.x;
+  const int e0 = (blockIdx.x - seg * blocks_per_seg) * kRankElems;
+  const int e = e0 + el;
   const int64_t base = (int64_t)seg * G;
-  for (int i = threadIdx.x; i < runs * kRunSamples; i += kRankThreads)
+  const int r = e0 / kRunItems;  // the chunk's run
+  for (int i = t; i < runs * kRunSamples; i += kRankBlock)
     ss[i] = samples[(int64_t)seg * runs * kRunSamples + i];
+  const int ec = min(e, G - 1);
+  const uint32_t key = run_keys[base + ec];
+  if (t == 0) kfl[0] = key;
+  if (grp == 0 && e == min(e0 + kRankElems, G) - 1) kfl[1] = key;
   __syncthreads();
-  if (e >= G) return;
-  const int r = e / kRunItems;
-  const uint32_t key = run_keys[base + e];
-  const uint32_t val = run_vals[base + e];
-  int rank = e - r * kRunItems;
-  // Runs in groups of kRankGroup; per run o of a group, its count lies in
-  // [lo, hi] and the window search below narrows lo up to it.
-  for (int g0 = 0; g0 < runs; g0 += kRankGroup) {
-    int lo[kRankGroup], hi[kRankGroup];
-#pragma unroll
-    for (int u = 0; u < kRankGroup; ++u) {
-      const int o = g0 + u;
-      lo[u] = hi[u] = 0;
-      if (o < runs && o != r) {  // uniform: a workgroup lies in one run
-        const int len = min(kRunItems, G - o * kRunItems);
-        const int ns = (len + kSampleStride - 1) / kSampleStride;
-        const bool le = o < r;
-        // ws = samples of run o that precede key (a prefix of its samples)
-        int ws = 0;
-#pragma unroll
-        for (int step = kRunSamples; step > 0; step >>= 1)
-          if (ws + step <= ns &&
-              precedes(ss[o * kRunSamples + ws + step - 1], key, le))
-            ws += step;
-        // the key at (ws-1) strides precedes, the one at ws strides does not
-        lo[u] = ws == 0 ? 0 : kSampleStride * (ws - 1) + 1;
-        hi[u] = ws == 0 ? 0 : min(kSampleStride * ws, len);
-      }
+  if (t < runs) {
+    const int o = t;
+    int L = 0, U = 0;
+    if (o != r) {
+      const int len = min(kRunItems, G - o * kRunItems);
+      const int ns = (len + kSampleStride - 1) / kSampleStride;
+      const bool le = o < r;
+      const uint32_t* so = ss + o * kRunSamples;
+      auto ld = [so](int i) { return so[i]; };
+      const int wf = prefix_count<6>(ld, ns, kfl[0], le);
+      const int wl = prefix_count<6>(ld, ns, kfl[1], le);
+      L = wf == 0 ? 0 : kSampleStride * (wf - 1) + 1;
+      U = wl == 0 ? 0 : min(kSampleStride * wl, len);
+      U = max(U, L);
     }
-    // Binary search of [lo, hi) for the group's runs at once: lo becomes
-    // the count.  Loads at clamped indices, results used only in the window.
-#pragma unroll
-    for (int step = kSampleStride / 2; step > 0; step >>= 1) {
-      uint32_t x[kRankGroup];
-#pragma unroll
-      for (int u = 0; u < kRankGroup; ++u) {
-        const int o = min(g0 + u, runs - 1);
-        const int len = min(kRunItems, G - o * kRunItems);
-        const int idx = min(max(lo[u] + step - 1, 0), len - 1);
-        x[u] = run_keys[base + (int64_t)o * kRunItems + idx];
-      }
-#pragma unroll
-      for (int u = 0; u < kRankGroup; ++u)
-        if (lo[u] + step <= hi[u] && precedes(x[u], key, g0 + u < r))
-          lo[u] += step;
-    }
-#pragma unroll
-    for (int u = 0; u < kRankGroup; ++u) rank += lo[u];  // 0 for o == r, o >= runs
+    wlo[o] = L;
+    wlen[o] = U - L;
   }
-  perm[base + rank] = (int32_t)val;
+  __syncthreads();
+  int rank = grp == 0 ? e - r * kRunItems : 0;
+  for (int l0 = 0; l0 < runs; l0 += kLdsRuns) {
+    if (l0 > 0) __syncthreads();  // searches of the previous runs done
+    // Windows of runs l0 .. l0 + kLdsRuns - 1 into LDS: every load in
+    // flight before the first store (loads at clamped, in-run positions).
+    uint32_t x[kLoadsPerThread];
+#pragma unroll
+    for (int k = 0; k < kLoadsPerThread; ++k) {
+      const int f = t + kRankBlock * k;
+      const int o = min(l0 + f / kWinKeys, runs - 1);
+      const int len = min(kRunItems, G - o * kRunItems);
+      const int n = min(wlen[o], kWinKeys);
+      const int i = min(f % kWinKeys, max(n - 1, 0));
+      x[k] = run_keys[base + (int64_t)o * kRunItems + min(wlo[o] + i, len - 1)];
+    }
+#pragma unroll
+    for (int k = 0; k < kLoadsPerThread; ++k) {
+      const int f = t + kRankBlock * k;
+      const int o = l0 + f / kWinKeys;
+      if (o < runs && f % kWinKeys < min(wlen[o], kWinKeys)) win[f] = x[k];
+    }
+    __syncthreads();
+    // This thread's runs o = l0 + grp + kRankSplit v: binary searches that
+    // advance together (n = 0 for runs not searched here).
+    int c[kRunsPerThread], n[kRunsPerThread];
+#pragma unroll
+    for (int v = 0; v < kRunsPerThread; ++v) {
+      const int o = l0 + grp + kRankSplit * v;
+      c[v] = 0;
+      n[v] = (o < runs && o != r && wlen[o] <= kWinKeys) ? wlen[o] : 0;
+    }
+#pragma unroll
+    for (int step = kWinKeys; step > 0; step >>= 1) {
+#pragma unroll
+      for (int v = 0; v < kRunsPerThread; ++v) {
+        const int u = grp + kRankSplit * v;  // run l0 + u
+        const uint32_t x =
+            win[u * kWinKeys + min(c[v] + step - 1, kWinKeys - 1)];
+        if (c[v] + step <= n[v] && precedes(x, key, l0 + u < r)) c[v] += step;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < kRunsPerThread; ++v) {
+      const int o = l0 + grp + kRankSplit * v;
+      if (o < runs && o != r) {
+        if (wlen[o] > kWinKeys) {  // rare: the window is searched in place
+          const uint32_t* w =
+              run_keys + base + (int64_t)o * kRunItems + wlo[o];
+          c[v] = prefix_count<12>([w](int i) { return w[i]; }, wlen[o], key,
+                                  o < r);
+        }
+        rank += wlo[o] + c[v];
+      }
+    }
+  }
+  part[grp][el] = rank;
+  __syncthreads();
+  if (grp == 0 && e < G) {
+    const int pos = part[0][el] + part[1][el] + part[2][el] + part[3][el];
+    perm[base + pos] = (int32_t)run_vals[base + e];
+  }
 }
 
 int runs_of(int64_t G) { return (int)((G + kRunItems - 1) / kRunItems); }
@@ -256,10 +330,10 @@ int launch_depth_order_small(const float* depths, int32_t* perm, int64_t G,
                      vals, smp);
   int rc = check_launch("depth_run_sort_kernel");
   if (rc) return rc;
-  const int blocks_per_seg = (int)((G + kRankThreads - 1) / kRankThreads);
+  const int blocks_per_seg = (int)((G + kRankElems - 1) / kRankElems);
   hipLaunchKernelGGL(depth_run_rank_kernel,
                      dim3((unsigned)((int64_t)batch * blocks_per_seg)),
-                     dim3(kRankThreads), 0, stream, keys, vals, smp, (int)G,
+                     dim3(kRankBlock), 0, stream, keys, vals, smp, (int)G,
                      runs, perm);
   return check_launch("depth_run_rank_kernel");
 }
