@@ -61,8 +61,45 @@ struct WalkSlots {
   int4 box[kWalkSplats];   // tx0, ty0, tiles per bbox row, first tile of the image
   int flags[kWalkSplats];  // bit 0: use_c, bit 1: use_a
   int cend[kWalkSplats];   // inclusive prefix sum of candidate counts
+  int first[kWalkSplats];  // exclusive prefix sum: the splat's first candidate
   int cnt[kWalkSplats];    // hits found so far
+  uint32_t own[64];        // per walk step: splats starting at each position
 };
+
+// Inclusive prefix maximum over the wavefront's 64 lanes (DPP: row shifts by
+// 1, 2, 4, 8, then the row broadcasts carry rows 0 and 2 into rows 1, 3 and
+// row 1 into rows 2, 3).  Lanes without a DPP source see 0, the identity.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_or_zero(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF,
+                                               false);
+}
+__device__ __forceinline__ uint32_t wave_prefix_max(uint32_t x) {
+  x = max(x, dpp_or_zero<0x111>(x));
+  x = max(x, dpp_or_zero<0x112>(x));
+  x = max(x, dpp_or_zero<0x114>(x));
+  x = max(x, dpp_or_zero<0x118>(x));
+  x = max(x, dpp_or_zero<0x142, 0xA>(x));
+  x = max(x, dpp_or_zero<0x143, 0xC>(x));
+  return x;
+}
+
+// k / w for 0 <= k and 1 <= w, both below 2^24: the float quotient is
+// within a few units of the truth for such operands, and the remainder
+// corrects it exactly.
+__device__ __forceinline__ int div_small(int k, int w) {
+  int q = (int)((float)k * __builtin_amdgcn_rcpf((float)w));
+  int r = k - q * w;
+  while (r < 0) {
+    --q;
+    r += w;
+  }
+  while (r >= w) {
+    ++q;
+    r -= w;
+  }
+  return q;
+}
 
 // Index of this thread's splat in the walk order of count / emit: lanes
 // 0..kWalkSplats-1 of each wavefront take consecutive splats.
@@ -111,6 +148,7 @@ __device__ __forceinline__ int walk_setup(const RasterParams& P, bool valid,
     W.flags[lane] = flags;
     W.cnt[lane] = 0;
     W.cend[lane] = inc;
+    W.first[lane] = inc - ncand;
   }
   __builtin_amdgcn_wave_barrier();
   return __shfl(inc, kWalkSplats - 1, 64);
@@ -118,23 +156,35 @@ __device__ __forceinline__ int walk_setup(const RasterParams& P, bool valid,
 
 // Tests the wavefront's candidates 64 at a time and calls on_hit(slot, tile)
 // for every hit (slot = 0..kWalkSplats-1, the splat's lane in walk_setup).
+// A candidate's slot is the last splat whose first candidate is at or
+// before it (a splat without candidates shares its first index with the
+// next one and loses to it): the owner of the step's first candidate is
+// counted with a ballot, the splats that start inside the step mark their
+// position with an LDS max, and a prefix maximum over the lanes spreads the
+// marks -- one LDS round trip per step instead of a binary search.
 template <typename Fn>
 __device__ __forceinline__ void walk_candidates(const RasterParams& P,
-                                                const WalkSlots& W, int total,
+                                                WalkSlots& W, int total,
                                                 Fn&& on_hit) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
+  const int first = lane < kWalkSplats ? W.first[lane] : 0x7fffffff;
   for (int c0 = 0; c0 < total; c0 += 64) {
+    const int owner0 = __popcll(__ballot(first <= c0)) - 1;  // first[0] = 0
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    W.own[lane] = lane == 0 ? (uint32_t)owner0 : 0u;
+    if (first > c0 && first < c0 + 64)
+      atomicMax(&W.own[first - c0], (uint32_t)lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int sl = (int)wave_prefix_max(W.own[lane]);
     const int c = c0 + lane;
     if (c < total) {
-      // first slot whose inclusive prefix exceeds c
-      int sl = 0;
-#pragma unroll
-      for (int step = kWalkSplats / 2; step > 0; step >>= 1)
-        if (W.cend[sl + step - 1] <= c) sl += step;
-      const int k = c - (sl == 0 ? 0 : W.cend[sl - 1]);
+      const int k = c - W.first[sl];
       const int4 bx = W.box[sl];
-      const int dy = k / bx.z;
+      const int dy = div_small(k, bx.z);
       const int tx = bx.x + (k - dy * bx.z), ty = bx.y + dy;
       const float4 g0 = W.g0[sl], g1 = W.g1[sl];
       const int fl = W.flags[sl];

@@ -151,6 +151,13 @@ __device__ __forceinline__ bool ellipse_hits_rect(float mx, float my, float a,
   if (mx >= rx0 && mx <= rx1 && my >= ry0 && my <= ry1) return true;
   const float dx0 = rx0 - mx, dx1 = rx1 - mx;
   const float dy0 = ry0 - my, dy1 = ry1 - my;
+  // The corner nearest the centre first: its quadratic is one of the terms
+  // minimised below, so if it is within tau the minimum is too and the
+  // answer is already known (the same decision, bit for bit).  Tiles inside
+  // a large splat, most of its candidates, end here.
+  const float cx = fabsf(dx0) <= fabsf(dx1) ? dx0 : dx1;
+  const float cy = fabsf(dy0) <= fabsf(dy1) ? dy0 : dy1;
+  if (quad_form(a, b, c, cx, cy) <= tau) return true;
   float q = quad_form(a, b, c, dx0, dy0);
   q = fminf(q, quad_form(a, b, c, dx0, dy1));
   q = fminf(q, quad_form(a, b, c, dx1, dy0));
