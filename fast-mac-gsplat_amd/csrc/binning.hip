@@ -445,6 +445,8 @@ constexpr int kRangeMaxBlocks = 2048;
 struct StatusWords {
   const uint32_t* err[3];  // give-up status words (null: not used)
   int32_t* out;            // their OR (null: not reported)
+  int32_t* host;           // null, or pinned host words that receive
+                           // {N (-1 on overflow), the OR} directly
 };
 
 __global__ __launch_bounds__(kThreads) void ranges_kernel(
@@ -458,8 +460,13 @@ __global__ __launch_bounds__(kThreads) void ranges_kernel(
 #pragma unroll
   for (int k = 0; k < 3; ++k)
     if (sw.err[k] != nullptr) e |= *sw.err[k];
-  if (sw.out != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
-    *sw.out = (int32_t)e;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    if (sw.out != nullptr) *sw.out = (int32_t)e;
+    if (sw.host != nullptr) {
+      sw.host[0] = n_dev ? *n_dev : (int32_t)n_cap;
+      sw.host[1] = (int32_t)e;
+    }
+  }
   const int64_t stride = (int64_t)gridDim.x * kThreads;
   if (e != 0u) {
     for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
@@ -601,10 +608,11 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        int32_t* tile_offsets, int32_t* tile_counts,
                        hipStream_t stream, const int32_t* n_dev,
                        const uint32_t* err0, const uint32_t* err1,
-                       const uint32_t* err2, int32_t* status_out) {
+                       const uint32_t* err2, int32_t* status_out,
+                       int32_t* host_words) {
   if (num_tiles <= 0)
     return status_out ? launch_fill_i32(status_out, 0, 1, stream) : GSPLAT_OK;
-  const StatusWords sw{{err0, err1, err2}, status_out};
+  const StatusWords sw{{err0, err1, err2}, status_out, host_words};
   int rc;
   if (n == 0) {
     rc = launch_fill_i32(tile_offsets, 0, (int64_t)num_tiles + 1, stream);

@@ -316,13 +316,19 @@ size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
   return emit_layout(P, n_pairs).total;
 }
 
-int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
-                        const int32_t* splat_offsets, int64_t n_pairs,
-                        int32_t* binned_ids, int32_t* tile_counts,
-                        int32_t* tile_offsets, int32_t* status,
-                        void* count_workspace, size_t count_workspace_bytes,
-                        void* workspace, size_t workspace_bytes,
-                        void* stream) {
+}  // extern "C"
+
+namespace {
+// bin_emit; with host_words (device-mapped pinned host memory) the tile
+// range launch also writes {N, status} there, which it reports as true
+// through *host_written (false: the caller copies them).
+int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
+                  const int32_t* splat_offsets, int64_t n_pairs,
+                  int32_t* binned_ids, int32_t* tile_counts,
+                  int32_t* tile_offsets, int32_t* status,
+                  void* count_workspace, size_t count_workspace_bytes,
+                  void* workspace, size_t workspace_bytes, void* stream,
+                  int32_t* host_words, bool* host_written) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -388,8 +394,26 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
   if (!rc)
     rc = gs::launch_tile_ranges(sorted_keys, n_pairs, P.num_tiles,
                                 tile_offsets, tile_counts, s, n_dev, err_pack,
-                                err_pairs, err_depth, status);
+                                err_pairs, err_depth, status, host_words);
+  if (!rc && host_written != nullptr)
+    *host_written = host_words != nullptr && P.num_tiles > 0;
   return rc;
+}
+}  // namespace
+
+extern "C" {
+
+int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
+                        const int32_t* splat_offsets, int64_t n_pairs,
+                        int32_t* binned_ids, int32_t* tile_counts,
+                        int32_t* tile_offsets, int32_t* status,
+                        void* count_workspace, size_t count_workspace_bytes,
+                        void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  return bin_emit_impl(meta, packed, splat_offsets, n_pairs, binned_ids,
+                       tile_counts, tile_offsets, status, count_workspace,
+                       count_workspace_bytes, workspace, workspace_bytes,
+                       stream, nullptr, nullptr);
 }
 
 size_t gsplat_hip_bin_workspace_bytes(const gsplat_raster_meta* meta,
@@ -469,14 +493,17 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
   rc = gsplat_hip_bin_pack(meta, means2d, conics, colors, opacities, perm,
                            packed, splat_offsets, cws, cbytes, s);
   if (rc) return rc;
-  rc = gsplat_hip_bin_emit(meta, packed, splat_offsets, capacity, binned_ids,
-                           nullptr, tile_offsets, status_dev, cws, cbytes, ews,
-                           ebytes, s);
+  bool written = false;
+  rc = bin_emit_impl(meta, packed, splat_offsets, capacity, binned_ids,
+                     nullptr, tile_offsets, status_dev, cws, cbytes, ews,
+                     ebytes, s, host_words, &written);
   if (rc || host_words == nullptr) return rc;
-  // 5. N and the status to the host in one copy
-  rc = hip_status(hipMemcpyAsync(host_words, n_dev, 2 * sizeof(int32_t),
-                                 hipMemcpyDeviceToHost, s),
-                  "gsplat_hip_bin: pair count and status copy");
+  // 5. N and the status reach the host: written by the tile range launch
+  //    itself, or else in one copy
+  if (!written)
+    rc = hip_status(hipMemcpyAsync(host_words, n_dev, 2 * sizeof(int32_t),
+                                   hipMemcpyDeviceToHost, s),
+                    "gsplat_hip_bin: pair count and status copy");
   if (!rc && ev_st != nullptr)
     rc = hip_status(hipEventRecord(ev_st, s), "gsplat_hip_bin: event record");
   return rc;

@@ -263,7 +263,9 @@ struct HeavyState {      // all null: every tile is walked whole by one wave
   float4* rec;           // [max_slots][256] (r, g, b, T at segment end);
                          // null: no records (forward without state)
   float* acc;            // [num_splats][kAccFloats] gradient sums of the
-                         // backward; null with n_pairs = 0
+                         // backward (zero outside a backward: the training
+                         // forward zeroes them and the backward's unpack
+                         // leaves them zero); null with n_pairs = 0
   int max_slots;
 };
 
@@ -1026,14 +1028,18 @@ __device__ __forceinline__ void bwd_walk(
 }
 
 // Copies the backward's accumulator records (GradOut) to the four gradient
-// arrays: one thread per splat.
+// arrays and zeroes them: one thread per splat.
 __global__ __launch_bounds__(256) void render_grads_unpack_kernel(GradOut G,
                                                                   int n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
-  const float4* rec = reinterpret_cast<const float4*>(G.acc + i * kAccFloats);
+  float4* rec = reinterpret_cast<float4*>(G.acc + i * kAccFloats);
   const float4 a = rec[0], b = rec[1];
   const float o = G.acc[i * kAccFloats + 8];
+  // leave the record zero for the next backward on this workspace
+  rec[0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  rec[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  G.acc[i * kAccFloats + 8] = 0.0f;
   G.g_means2d[2 * i + 0] = a.x;
   G.g_means2d[2 * i + 1] = a.y;
   G.g_conics[3 * i + 0] = a.z;
@@ -1182,6 +1188,8 @@ HeavyState heavy_state(const RasterParams& P, int64_t n_pairs, void* ws) {
   char* p = static_cast<char*>(ws);
   H.counters = reinterpret_cast<int32_t*>(p);
   p += 256;
+  H.acc = n_pairs > 0 ? reinterpret_cast<float*>(p) : nullptr;
+  p += acc_bytes(P, n_pairs);
   H.tile_slot = reinterpret_cast<int32_t*>(p);
   p += align_up(T * 4, 256);
   H.handoff = reinterpret_cast<int32_t*>(p);
@@ -1197,8 +1205,6 @@ HeavyState heavy_state(const RasterParams& P, int64_t n_pairs, void* ws) {
   H.slot_next = reinterpret_cast<int32_t*>(p);
   p += align_up(slots * 4, 256);
   H.rec = reinterpret_cast<float4*>(p);
-  p += align_up(slots * 256 * sizeof(float4), 256);
-  H.acc = n_pairs > 0 ? reinterpret_cast<float*>(p) : nullptr;
   H.max_slots = (int)slots;
   return H;
 }
@@ -1217,7 +1223,14 @@ int launch_render_forward(const RasterParams& P, const float* packed,
   if (out_T == nullptr) H.rec = nullptr;  // no backward: hand-off only
   const float4* pk = reinterpret_cast<const float4*>(packed);
   if (H.counters != nullptr) {
-    const int rc = launch_fill_i32(H.counters, 0, 2, stream);
+    // The training forward also zeroes the backward's gradient records (the
+    // backward accumulates into them and its unpack leaves them zero again).
+    const int rc =
+        H.acc != nullptr
+            ? launch_zero2(reinterpret_cast<uint32_t*>(H.counters), 2,
+                           reinterpret_cast<uint32_t*>(H.acc),
+                           (int64_t)P.num_splats * kAccFloats, stream)
+            : launch_fill_i32(H.counters, 0, 2, stream);
     if (rc) return rc;
   }
   hipLaunchKernelGGL(render_fwd_kernel, dim3((unsigned)P.num_tiles),
@@ -1245,9 +1258,11 @@ int launch_render_backward(const RasterParams& P, const float* packed,
   const HeavyState H = heavy_state(P, n_pairs, workspace);
   const GradOut G{g_means2d, g_conics, g_colors, g_opac,
                   P.num_tiles > 0 ? H.acc : nullptr};
+  // The gradient records come zeroed from the training forward (or from
+  // the unpack of an earlier backward); without them the outputs are the
+  // accumulators and are zeroed here.
   int rc = G.acc != nullptr
-               ? launch_fill_f32(G.acc, 0.0f,
-                                 (int64_t)P.num_splats * kAccFloats, stream)
+               ? GSPLAT_OK
                : launch_zero_grads(g_means2d, g_conics, g_colors, g_opac,
                                    P.num_splats, stream);
   if (rc) return rc;

@@ -149,14 +149,17 @@ int launch_emit(const RasterParams& P, const float* packed,
 // tile_offsets[0..T] and (unless tile_counts is NULL) tile_counts[0..T)
 // from the n sorted tile keys (min(n, *n_dev) of them with n_dev).  With
 // status_out, the same launch writes there the OR of the (non-null) give-up
-// status words err[0..2] of the binning's look-backs.
+// status words err[0..2] of the binning's look-backs; with host_words
+// (device-mapped pinned host memory, n > 0 only) it also writes
+// {*n_dev, that OR} there.
 int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        int32_t* tile_offsets, int32_t* tile_counts,
                        hipStream_t stream, const int32_t* n_dev = nullptr,
                        const uint32_t* err0 = nullptr,
                        const uint32_t* err1 = nullptr,
                        const uint32_t* err2 = nullptr,
-                       int32_t* status_out = nullptr);
+                       int32_t* status_out = nullptr,
+                       int32_t* host_words = nullptr);
 int launch_zero2(uint32_t* a, int64_t na, uint32_t* b, int64_t nb,
                  hipStream_t stream);
 int launch_fill_i32(int32_t* dst, int32_t value, int64_t n, hipStream_t stream);

@@ -181,11 +181,13 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
  * ordered after the work already enqueued on `stream` through inputs_event,
  * after which count_event is recorded; bin_depth_order on `stream`
  * concurrently; then bin_pack (after count_event) and bin_emit with the pair
- * capacity `capacity` (see bin_emit: n_pairs).  Finally, on `stream`, the
- * pair count N and the binning's status word (GSPLAT_STATUS_*) are copied in
- * one transfer to host_words[0] and host_words[1] (two pinned int32; may be
- * NULL: nothing copied), after which status_event (may be NULL) is recorded:
- * the caller waits for it before reading them.  The events are the
+ * capacity `capacity` (see bin_emit: n_pairs).  Finally the pair count N
+ * and the binning's status word (GSPLAT_STATUS_*) reach host_words[0] and
+ * host_words[1] (two int32 of page-locked host memory mapped for the device,
+ * as hipHostMalloc and torch's pin_memory allocate it; may be NULL): the
+ * tile-range launch on `stream` writes them directly (a capacity of 0 copies
+ * them instead), after which status_event (may be NULL) is recorded on
+ * `stream`: the caller waits for it before reading them.  The events are the
  * caller's (hipEvent_t; inputs_event and count_event are required when
  * count_stream differs from stream).  If a look-back gave up, every tile
  * range is empty (the compositors then read no pair) and the status says
@@ -213,10 +215,12 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
  * Without it every tile is walked by one wavefront.  Images are identical
  * either way; gradients differ only in summation order.  The forward
  * overwrites the workspace.  The backward reads the forward's part and
- * uses an area after it as its own scratch: one 64-byte accumulator record
- * per splat, so that the nine atomic additions a tile makes to a splat's
- * gradients go to one cache line (without a workspace they go straight to
- * the four output arrays).  n_pairs sizes the
+ * accumulates into one 64-byte record per splat, so that the nine atomic
+ * additions a tile makes to a splat's gradients go to one cache line
+ * (without a workspace they go straight to the four output arrays); the
+ * training forward zeroes these records and the backward leaves them zero,
+ * so a backward takes a workspace that a training forward with n_pairs > 0
+ * has filled (repeated backwards on it are fine).  n_pairs sizes the
  * record area: the pair count N or any capacity >= N (the length of the
  * binned_ids buffer), and the forward and the backward of one binning must
  * receive the same value (the layout follows it; a backward given another
