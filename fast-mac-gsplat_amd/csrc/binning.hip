@@ -31,6 +31,7 @@
 //   sorted tile keys (the reference reads them from its atomic counters).
 #include "gs_internal.h"
 #include "gs_predicate.h"
+#include "depth_runs.h"
 #include "lookback.h"
 
 namespace gs {
@@ -202,21 +203,29 @@ __device__ __forceinline__ void walk_candidates(const RasterParams& P,
   }
 }
 
-// Original order: splat_count[orig] = tile hits of splat orig;
-// block_sums[workgroup] = the workgroup's total.
-__global__ __launch_bounds__(kThreads) void count_kernel(
-    RasterParams P, const float* __restrict__ means2d,
+// LDS of a count block of kW wavefronts.
+template <int kW>
+struct CountLds {
+  WalkSlots walk[kW];
+  int wsum[kW];
+};
+
+// Count block vb of nvb (kW wavefronts, kWalkSplats splats each), original
+// order: splat_count[orig] = tile hits of splat orig and, with block_sums,
+// block_sums[vb] = the block's total.  The blocks also zero
+// zero_words[0..n_zero_words) (grid-stride; read only by later launches).
+template <int kW>
+__device__ __forceinline__ void count_block(
+    const RasterParams& P, const float* __restrict__ means2d,
     const float* __restrict__ conics, const float* __restrict__ opacities,
     int32_t* __restrict__ splat_count, int32_t* __restrict__ block_sums,
-    uint32_t* __restrict__ zero_words, int64_t n_zero_words) {
-  __shared__ WalkSlots walk[kWaves];
-  __shared__ int wsum[kWaves];
+    uint32_t* __restrict__ zero_words, int64_t n_zero_words, int vb, int nvb,
+    CountLds<kW>& S) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // zero the binning control block (grid-stride; read only by later launches)
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_zero_words;
-       i += (int64_t)gridDim.x * kThreads)
+  for (int64_t i = (int64_t)vb * (64 * kW) + threadIdx.x; i < n_zero_words;
+       i += (int64_t)nvb * (64 * kW))
     zero_words[i] = 0u;
-  const int orig = walk_splat_index();
+  const int orig = (vb * kW + wave) * kWalkSplats + lane;
   const bool valid = lane < kWalkSplats && orig < P.num_splats;
   const int o = valid ? orig : P.num_splats - 1;
   SplatGeom s;
@@ -226,23 +235,62 @@ __global__ __launch_bounds__(kThreads) void count_kernel(
   s.b = conics[3 * o + 1];
   s.c = conics[3 * o + 2];
   s.o = opacities[o];
-  WalkSlots& W = walk[wave];
+  WalkSlots& W = S.walk[wave];
   const int total = walk_setup(P, valid, s, o / P.gpb, W);
   walk_candidates(P, W, total, [&](int sl, int) { atomicAdd(&W.cnt[sl], 1); });
   __builtin_amdgcn_wave_barrier();
   const int n = valid ? W.cnt[lane] : 0;
   if (valid) splat_count[orig] = n;
+  if (block_sums == nullptr) return;
   int v = n;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  if (lane == 0) wsum[wave] = v;
+  if (lane == 0) S.wsum[wave] = v;
   __syncthreads();
   if (threadIdx.x == 0) {
     int t = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) t += wsum[w];
-    block_sums[blockIdx.x] = t;
+    for (int w = 0; w < kW; ++w) t += S.wsum[w];
+    block_sums[vb] = t;
   }
+}
+
+__global__ __launch_bounds__(kThreads) void count_kernel(
+    RasterParams P, const float* __restrict__ means2d,
+    const float* __restrict__ conics, const float* __restrict__ opacities,
+    int32_t* __restrict__ splat_count, int32_t* __restrict__ block_sums,
+    uint32_t* __restrict__ zero_words, int64_t n_zero_words) {
+  __shared__ CountLds<kWaves> S;
+  count_block<kWaves>(P, means2d, conics, opacities, splat_count, block_sums,
+                      zero_words, n_zero_words, (int)blockIdx.x,
+                      (int)gridDim.x, S);
+}
+
+// The count next to the run step of the small-image depth order, in one
+// launch: workgroups below run_blocks sort one depth run each (a few CUs for
+// most of the launch), the others are count blocks of kRunWaves wavefronts
+// and fill the remaining CUs.  The two parts touch disjoint memory.
+union CountRunsLds {
+  run_step::RunSortLds runs;
+  CountLds<run_step::kRunWaves> count;
+};
+
+__global__ __launch_bounds__(run_step::kRunThreads) void count_depth_runs_kernel(
+    RasterParams P, const float* __restrict__ means2d,
+    const float* __restrict__ conics, const float* __restrict__ opacities,
+    int32_t* __restrict__ splat_count, uint32_t* __restrict__ zero_words,
+    int64_t n_zero_words, const float* __restrict__ depths, int runs,
+    int run_blocks, run_step::RunBuffers runs_out) {
+  __shared__ CountRunsLds S;
+  if ((int)blockIdx.x < run_blocks) {
+    run_step::run_sort_block(depths, P.gpb, runs, (int)blockIdx.x, runs_out,
+                             S.runs);
+    return;
+  }
+  count_block<run_step::kRunWaves>(
+      P, means2d, conics, opacities, splat_count, nullptr, zero_words,
+      n_zero_words, (int)blockIdx.x - run_blocks,
+      (int)gridDim.x - run_blocks, S.count);
 }
 
 // One workgroup: *pair_count = sum of the n block sums (-1 if it does not fit
@@ -556,6 +604,28 @@ int launch_count(const RasterParams& P, const float* means2d,
   hipLaunchKernelGGL(sum_kernel, dim3(1), dim3(kThreads), 0, stream,
                      block_sums, nblk, pair_count);
   return check_launch("sum_kernel");
+}
+
+int launch_count_depth_runs(const RasterParams& P, const float* means2d,
+                            const float* conics, const float* opacities,
+                            int32_t* splat_count, uint32_t* zero_words,
+                            int64_t n_zero_words, const float* depths,
+                            void* depth_buffers, hipStream_t stream) {
+  if (P.num_splats == 0 || !depth_small_ok(P.gpb)) {
+    set_error("count + depth runs: needs 1..131072 splats per image");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  const int runs = run_step::runs_of(P.gpb);
+  const int run_blocks = P.batch * runs;
+  constexpr int kSplatsPerBlock = run_step::kRunWaves * kWalkSplats;
+  const int cblocks = (P.num_splats + kSplatsPerBlock - 1) / kSplatsPerBlock;
+  hipLaunchKernelGGL(count_depth_runs_kernel,
+                     dim3((unsigned)(run_blocks + cblocks)),
+                     dim3(run_step::kRunThreads), 0, stream, P, means2d, conics,
+                     opacities, splat_count, zero_words, n_zero_words, depths,
+                     runs, run_blocks,
+                     run_step::run_buffers(depth_buffers, P.gpb, P.batch));
+  return check_launch("count_depth_runs_kernel");
 }
 
 int launch_pack(const RasterParams& P, const float* means2d,

@@ -466,6 +466,41 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
   hipEvent_t ev_in = static_cast<hipEvent_t>(inputs_event);
   hipEvent_t ev_n = static_cast<hipEvent_t>(count_event);
   hipEvent_t ev_st = static_cast<hipEvent_t>(status_event);
+  // Images of at most 131072 splats whose N goes to host_words: the count
+  // and the run step of the depth order share one launch on `stream` (the
+  // run step leaves most CUs idle), and N is read off the pack scan's total
+  // by the tile-range launch, so the count stream, its events and the sum of
+  // the count workgroups are not used.
+  if (host_words != nullptr && P.num_tiles > 0 && P.num_splats > 0 &&
+      gs::depth_small_ok(P.gpb)) {
+    const CountLayout C = count_layout(P);
+    char* cb = static_cast<char*>(cws);
+    const size_t z0 = gs::radix_ctl_bytes(C.depth);
+    rc = gs::launch_count_depth_runs(
+        P, means2d, conics, opacities,
+        reinterpret_cast<int32_t*>(cb + C.splat_count),
+        reinterpret_cast<uint32_t*>(cb + z0),
+        (int64_t)((C.ctl_end - z0) / sizeof(uint32_t)), depths,
+        cb + C.depth_buffers, s);
+    if (!rc)
+      rc = gs::launch_depth_ranks_small(cb + C.depth_buffers, perm, P.gpb,
+                                        P.batch, s);
+    if (!rc)
+      rc = gsplat_hip_bin_pack(meta, means2d, conics, colors, opacities, perm,
+                               packed, splat_offsets, cws, cbytes, s);
+    bool written = false;
+    if (!rc)
+      rc = bin_emit_impl(meta, packed, splat_offsets, capacity, binned_ids,
+                         nullptr, tile_offsets, status_dev, cws, cbytes, ews,
+                         ebytes, s, host_words, &written);
+    if (!rc && !written) {
+      gs::set_error("gsplat_hip_bin: the tile ranges did not report N");
+      rc = GSPLAT_ERR_INVALID_ARGUMENT;
+    }
+    if (!rc && ev_st != nullptr)
+      rc = hip_status(hipEventRecord(ev_st, s), "gsplat_hip_bin: event record");
+    return rc;
+  }
   // 1. per-splat hit counts and N on the count stream (after the caller's
   //    work on `stream`)
   if (cs != s) {

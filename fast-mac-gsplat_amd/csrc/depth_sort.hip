@@ -25,128 +25,16 @@
 //
 // No atomics, look-back or control words: nothing needs zeroing and the two
 // launches are independent of earlier calls.
-#include "gs_internal.h"
+#include "depth_runs.h"
 
 namespace gs {
+using namespace run_step;
 namespace {
 
-constexpr int kRunItems = 4096;
-constexpr int kRunWaves = 16;
-constexpr int kRunThreads = 64 * kRunWaves;
-constexpr int kRunRounds = kRunItems / kRunThreads;  // 64-element groups per wavefront
-constexpr int kSampleStride = 64;
-constexpr int kRunSamples = kRunItems / kSampleStride;
-constexpr int kMaxRuns = 32;
-static_assert(kRunRounds * kRunThreads == kRunItems, "run shape");
-
-__device__ __forceinline__ uint64_t lanes_below() {
-  const unsigned lane = threadIdx.x & 63u;
-  return (lane == 0u) ? 0ull : (~0ull >> (64u - lane));
-}
-
-// Lanes whose 8-bit digit equals this lane's digit (every lane is active).
-__device__ __forceinline__ uint64_t same_digit_lanes(uint32_t d) {
-  uint64_t m = ~0ull;
-#pragma unroll
-  for (int bit = 0; bit < 8; ++bit) {
-    const bool p = (d >> bit) & 1u;
-    const uint64_t b = __ballot(p);
-    m &= p ? b : ~b;
-  }
-  return m;
-}
-
 __global__ __launch_bounds__(kRunThreads) void depth_run_sort_kernel(
-    const float* __restrict__ depths, int G, int runs,
-    uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_vals,
-    uint32_t* __restrict__ samples) {
-  __shared__ uint32_t cnt[kRunWaves][256];
-  __shared__ uint32_t dstart[256];
-  __shared__ uint32_t wsum[kRunWaves];
-  __shared__ uint32_t sk[kRunItems];
-  __shared__ uint32_t sv[kRunItems];
-  const int seg = blockIdx.x / runs;
-  const int run = blockIdx.x - seg * runs;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int first = run * kRunItems;
-  const int len = min(kRunItems, G - first);
-  const int64_t base = (int64_t)seg * G + first;
-  // Element q = wave * 256 + 64 * round + lane.  Slots past the run's end
-  // get key 0xffffffff, above every depth key (NaN maps to 0xffc00000), so
-  // they sort after the run's elements.
-  uint32_t k[kRunRounds], v[kRunRounds];
-#pragma unroll
-  for (int r = 0; r < kRunRounds; ++r) {
-    const int q = wave * (64 * kRunRounds) + 64 * r + lane;
-    const uint32_t key = depth_key(depths[base + min(q, len - 1)]);
-    k[r] = q < len ? key : 0xffffffffu;
-    v[r] = (uint32_t)(first + q);
-  }
-  const uint64_t lt = lanes_below();
-  for (int shift = 0; shift < 32; shift += 8) {
-    for (int i = t; i < kRunWaves * 256; i += kRunThreads) (&cnt[0][0])[i] = 0u;
-    __syncthreads();
-    uint32_t rank[kRunRounds];
-#pragma unroll
-    for (int r = 0; r < kRunRounds; ++r) {
-      const uint32_t d = (k[r] >> shift) & 255u;
-      const uint64_t peers = same_digit_lanes(d);
-      const uint32_t below = (uint32_t)__popcll(peers & lt);
-      uint32_t old = 0u;
-      if (below == 0u) old = atomicAdd(&cnt[wave][d], (uint32_t)__popcll(peers));
-      old = (uint32_t)__shfl((int)old, __ffsll((long long)peers) - 1, 64);
-      rank[r] = old + below;
-    }
-    __syncthreads();
-    // digit t (threads 0..255): wavefront offsets, then the digit's start
-    uint32_t tot = 0u;
-    if (t < 256) {
-#pragma unroll
-      for (int w = 0; w < kRunWaves; ++w) {
-        const uint32_t c = cnt[w][t];
-        cnt[w][t] = tot;
-        tot += c;
-      }
-    }
-    uint32_t inc = tot;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t y = __shfl_up(inc, off, 64);
-      if (lane >= off) inc += y;
-    }
-    if (lane == 63) wsum[wave] = inc;
-    __syncthreads();
-    if (t < 256) {
-      uint32_t pre = 0u;
-      for (int w = 0; w < wave; ++w) pre += wsum[w];
-      dstart[t] = pre + inc - tot;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kRunRounds; ++r) {
-      const uint32_t d = (k[r] >> shift) & 255u;
-      const uint32_t pos = dstart[d] + cnt[wave][d] + rank[r];
-      sk[pos] = k[r];
-      sv[pos] = v[r];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kRunRounds; ++r) {
-      const int q = wave * (64 * kRunRounds) + 64 * r + lane;
-      k[r] = sk[q];
-      v[r] = sv[q];
-    }
-  }
-  const int64_t sbase = ((int64_t)seg * runs + run) * kRunSamples;
-#pragma unroll
-  for (int r = 0; r < kRunRounds; ++r) {
-    const int q = wave * (64 * kRunRounds) + 64 * r + lane;
-    if (q < len) {
-      run_keys[base + q] = k[r];
-      run_vals[base + q] = v[r];
-      if (q % kSampleStride == 0) samples[sbase + q / kSampleStride] = k[r];
-    }
-  }
+    const float* __restrict__ depths, int G, int runs, RunBuffers out) {
+  __shared__ RunSortLds S;
+  run_sort_block(depths, G, runs, (int)blockIdx.x, out, S);
 }
 
 // Whether a key x of another run precedes key k in the stable order: keys
@@ -298,8 +186,6 @@ __global__ __launch_bounds__(kRankBlock) void depth_run_rank_kernel(
   }
 }
 
-int runs_of(int64_t G) { return (int)((G + kRunItems - 1) / kRunItems); }
-
 }  // namespace
 
 bool depth_small_ok(int64_t G) {
@@ -312,6 +198,22 @@ size_t depth_small_bytes(int64_t G, int batch) {
                                 sizeof(uint32_t), 256);
 }
 
+int launch_depth_ranks_small(void* buffers, int32_t* perm, int64_t G,
+                             int batch, hipStream_t stream) {
+  if (!depth_small_ok(G) || batch < 1) {
+    set_error("depth order: %lld splats per image exceed the two-launch sort",
+              (long long)G);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  const RunBuffers b = run_buffers(buffers, G, batch);
+  const int blocks_per_seg = (int)((G + kRankElems - 1) / kRankElems);
+  hipLaunchKernelGGL(depth_run_rank_kernel,
+                     dim3((unsigned)((int64_t)batch * blocks_per_seg)),
+                     dim3(kRankBlock), 0, stream, b.keys, b.vals, b.samples,
+                     (int)G, runs_of(G), perm);
+  return check_launch("depth_run_rank_kernel");
+}
+
 int launch_depth_order_small(const float* depths, int32_t* perm, int64_t G,
                              int batch, void* buffers, hipStream_t stream) {
   if (!depth_small_ok(G) || batch < 1) {
@@ -320,22 +222,12 @@ int launch_depth_order_small(const float* depths, int32_t* perm, int64_t G,
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
   const int runs = runs_of(G);
-  const size_t vec = align_up((size_t)(G * batch) * sizeof(uint32_t), 256);
-  char* b = static_cast<char*>(buffers);
-  uint32_t* keys = reinterpret_cast<uint32_t*>(b);
-  uint32_t* vals = reinterpret_cast<uint32_t*>(b + vec);
-  uint32_t* smp = reinterpret_cast<uint32_t*>(b + 2 * vec);
   hipLaunchKernelGGL(depth_run_sort_kernel, dim3((unsigned)(batch * runs)),
-                     dim3(kRunThreads), 0, stream, depths, (int)G, runs, keys,
-                     vals, smp);
-  int rc = check_launch("depth_run_sort_kernel");
+                     dim3(kRunThreads), 0, stream, depths, (int)G, runs,
+                     run_buffers(buffers, G, batch));
+  const int rc = check_launch("depth_run_sort_kernel");
   if (rc) return rc;
-  const int blocks_per_seg = (int)((G + kRankElems - 1) / kRankElems);
-  hipLaunchKernelGGL(depth_run_rank_kernel,
-                     dim3((unsigned)((int64_t)batch * blocks_per_seg)),
-                     dim3(kRankBlock), 0, stream, keys, vals, smp, (int)G,
-                     runs, perm);
-  return check_launch("depth_run_rank_kernel");
+  return launch_depth_ranks_small(buffers, perm, G, batch, stream);
 }
 
 }  // namespace gs

@@ -112,6 +112,9 @@ bool depth_small_ok(int64_t G);
 size_t depth_small_bytes(int64_t G, int batch);
 int launch_depth_order_small(const float* depths, int32_t* perm, int64_t G,
                              int batch, void* buffers, hipStream_t stream);
+// The second of those launches alone (the runs are already in buffers).
+int launch_depth_ranks_small(void* buffers, int32_t* perm, int64_t G,
+                             int batch, hipStream_t stream);
 
 // ---- binning (binning.hip)
 // count: per-splat tile-hit counts (original order) into splat_count, the
@@ -124,6 +127,15 @@ int launch_count(const RasterParams& P, const float* means2d,
                  int32_t* splat_count, int32_t* block_sums,
                  int32_t* pair_count, uint32_t* zero_words,
                  int64_t n_zero_words, hipStream_t stream);
+// count_depth_runs: the count (splat_count, zero_words as above; no block
+// sums and no N) and the first launch of the small-image depth order (runs
+// into depth_buffers) as one launch.  Requires P.num_splats > 0 and
+// depth_small_ok(P.gpb); launch_depth_ranks_small completes the order.
+int launch_count_depth_runs(const RasterParams& P, const float* means2d,
+                            const float* conics, const float* opacities,
+                            int32_t* splat_count, uint32_t* zero_words,
+                            int64_t n_zero_words, const float* depths,
+                            void* depth_buffers, hipStream_t stream);
 // pack: packed records in gid order and splat_offsets[0..BG] (exclusive scan
 // of splat_count[perm]) via a look-back scan whose status
 // (count_scan_blocks(P) words) and ticket must be zero.

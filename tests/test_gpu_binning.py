@@ -173,10 +173,12 @@ def _capacity_key(B, G, H, W):
     return (0, B, G, H, W)
 
 
-def test_binning_from_remembered_capacity(gpu):
+@pytest.mark.parametrize("B,G,H,W", [(2, 3000, 200, 264), (1, 70_000, 512, 384), (3, 9_000, 160, 200)])
+def test_binning_from_remembered_capacity(gpu, B, G, H, W):
     """The second binning of a shape sizes its pair buffers from the first one's count and reads N
-    only afterwards; the result is bit-identical and the capacity covers N."""
-    B, G, H, W = 2, 3000, 200, 264
+    only afterwards (one C-ABI call: for these sizes the count and the depth runs share a launch and N
+    comes from the pack scan); the result is bit-identical and the capacity covers N.  Sizes: one
+    depth run per image, 18 runs with a partial last one, three images of three runs."""
     print(f"capacity B={B} G={G} {H}x{W}", flush=True)
     sc = make_scene_2d(1, seed=5, G=G, B=B, H=H, W=W)
     _ops._capacity.pop(_capacity_key(B, G, H, W), None)
