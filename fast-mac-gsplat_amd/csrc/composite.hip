@@ -97,6 +97,21 @@ struct Staged {
   float4 s1[kBatch];  // C, opacity, r, g
 };
 
+// A value through an empty asm: addresses derived from it are computed
+// where they are used, so that the compiler does not keep 64-bit addresses
+// for the rare segment boundaries live across the compositing loop.
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+// The same for a 64-bit pixel index: the other pixels of a lane are then
+// reached by adding multiples of a row stride instead of a full 64-bit
+// index computation each.
+__device__ __forceinline__ int64_t opaque64(int64_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // Strip culling (gs_strip.h) with the hardware reciprocal and square root.
 struct HwOps {
   static __device__ __forceinline__ float rcp(float x) {
@@ -166,7 +181,9 @@ __device__ __forceinline__ uint32_t stage_batch(
     const float4 p1 = packed[3 * gid + 1];
     const float4 p2 = packed[3 * gid + 2];
     const float a = p0.z, b = p0.w, c = p1.x;
-    m = strip_mask(p0.x, p0.y, a, b, c, p2.z, tc.x0, tc.y0);
+    // (the tile corner through opaque(): computed here per batch rather than
+    // kept live in registers across the walk)
+    m = strip_mask(p0.x, p0.y, a, b, c, p2.z, opaque(tc.x0), opaque(tc.y0));
     float A, B, C;
     {
 #pragma clang fp contract(off)
@@ -296,21 +313,6 @@ __device__ int next_segment(const HeavyState& H, int tile, int seg,
 // Pixel index inside the tile used by the per-pixel segment records.
 __device__ __forceinline__ int tile_pixel(int k) {
   return 64 * k + (int)threadIdx.x;
-}
-
-// A value through an empty asm: addresses derived from it are computed
-// where they are used, so that the compiler does not keep 64-bit addresses
-// for the rare segment boundaries live across the compositing loop.
-__device__ __forceinline__ int opaque(int v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
-// The same for a 64-bit pixel index: the other pixels of a lane are then
-// reached by adding multiples of a row stride instead of a full 64-bit
-// index computation each.
-__device__ __forceinline__ int64_t opaque64(int64_t v) {
-  asm volatile("" : "+v"(v));
-  return v;
 }
 
 // t0 below is the in-tile index (tile_pixel order, 64 strip + lane) of this
@@ -1081,7 +1083,11 @@ __device__ __forceinline__ bool seg_item(const RasterParams& P,
 // Work items: block m < seg_blocks walks segment slot m (the longest walks,
 // dispatched first), the other blocks are tiles (tiles walked as segments
 // return at once).
-__global__ __launch_bounds__(kLanes) void render_bwd_kernel(
+// Six wavefronts per SIMD (at most 80 VGPRs): the walk's LDS round trips
+// and atomics need the extra wavefronts to hide their latency more than the
+// few spilled set-up values cost.
+__global__ __launch_bounds__(kLanes) __attribute__((amdgpu_waves_per_eu(6, 8)))
+void render_bwd_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ tile_offsets,
     const int32_t* __restrict__ binned, const float* __restrict__ final_T,
