@@ -494,7 +494,10 @@ struct StatusWords {
   const uint32_t* err[3];  // give-up status words (null: not used)
   int32_t* out;            // their OR (null: not reported)
   int32_t* host;           // null, or pinned host words that receive
-                           // {N (-1 on overflow), the OR} directly
+                           // {N (-1 on overflow), the OR} directly, and
+                           // host[2] = 1 if a tile range is longer than
+                           // kHandoffPairs (left alone otherwise)
+  ZeroSpan zero[2];        // zeroed by the launch on the side
 };
 
 __global__ __launch_bounds__(kThreads) void ranges_kernel(
@@ -516,6 +519,11 @@ __global__ __launch_bounds__(kThreads) void ranges_kernel(
     }
   }
   const int64_t stride = (int64_t)gridDim.x * kThreads;
+#pragma unroll
+  for (int z = 0; z < 2; ++z)
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+         i < sw.zero[z].n; i += stride)
+      sw.zero[z].p[i] = 0u;
   if (e != 0u) {
     for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
          t <= num_tiles; t += stride)
@@ -523,6 +531,7 @@ __global__ __launch_bounds__(kThreads) void ranges_kernel(
     return;
   }
   const int64_t n = n_dev ? min(n_cap, (int64_t)max(*n_dev, 0)) : n_cap;
+  bool long_range = false;  // a range starting here exceeds kHandoffPairs
   for (int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; i0 <= n;
        i0 += kRangeUnroll * stride) {
     uint32_t kp[kRangeUnroll], kc[kRangeUnroll];
@@ -540,8 +549,15 @@ __global__ __launch_bounds__(kThreads) void ranges_kernel(
       const int64_t cur = (i == n) ? (int64_t)num_tiles
                                    : min((int64_t)kc[u], (int64_t)num_tiles);
       for (int64_t t = prev + 1; t <= cur; ++t) tile_offsets[t] = (int32_t)i;
+      // tile cur's range starts at i: longer than kHandoffPairs iff its
+      // key is still there kHandoffPairs places on
+      if (sw.host != nullptr && prev != cur && i + kHandoffPairs < n)
+        long_range |= sorted_keys[i + kHandoffPairs] == kc[u];
     }
   }
+  if (sw.host != nullptr && __ballot(long_range) != 0ull &&
+      (threadIdx.x & 63) == 0)
+    sw.host[2] = 1;
 }
 
 __global__ __launch_bounds__(kThreads) void counts_kernel(
@@ -679,11 +695,18 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        hipStream_t stream, const int32_t* n_dev,
                        const uint32_t* err0, const uint32_t* err1,
                        const uint32_t* err2, int32_t* status_out,
-                       int32_t* host_words) {
+                       int32_t* host_words, const ZeroSpan* zero) {
+  int rc = GSPLAT_OK;
+  if (zero != nullptr && (num_tiles <= 0 || n == 0))
+    rc = launch_zero2(zero[0].p, zero[0].n, zero[1].p, zero[1].n, stream);
+  if (rc) return rc;
   if (num_tiles <= 0)
     return status_out ? launch_fill_i32(status_out, 0, 1, stream) : GSPLAT_OK;
-  const StatusWords sw{{err0, err1, err2}, status_out, host_words};
-  int rc;
+  StatusWords sw{{err0, err1, err2}, status_out, host_words, {}};
+  if (zero != nullptr) {
+    sw.zero[0] = zero[0];
+    sw.zero[1] = zero[1];
+  }
   if (n == 0) {
     rc = launch_fill_i32(tile_offsets, 0, (int64_t)num_tiles + 1, stream);
     if (!rc && status_out) rc = launch_fill_i32(status_out, 0, 1, stream);

@@ -328,7 +328,8 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
                   int32_t* tile_offsets, int32_t* status,
                   void* count_workspace, size_t count_workspace_bytes,
                   void* workspace, size_t workspace_bytes, void* stream,
-                  int32_t* host_words, bool* host_written) {
+                  int32_t* host_words, bool* host_written,
+                  const gs::ZeroSpan* zero = nullptr) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -353,7 +354,7 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
   if (n_pairs == 0 || P.num_splats == 0)
     return gs::launch_tile_ranges(nullptr, 0, P.num_tiles, tile_offsets,
                                   tile_counts, s, nullptr, err_pack, nullptr,
-                                  err_depth, status);
+                                  err_depth, status, nullptr, zero);
   rc = null_check({packed, splat_offsets, binned_ids, count_workspace,
                    workspace},
                   "gsplat_hip_bin_emit");
@@ -394,7 +395,8 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
   if (!rc)
     rc = gs::launch_tile_ranges(sorted_keys, n_pairs, P.num_tiles,
                                 tile_offsets, tile_counts, s, n_dev, err_pack,
-                                err_pairs, err_depth, status, host_words);
+                                err_pairs, err_depth, status, host_words,
+                                zero);
   if (!rc && host_written != nullptr)
     *host_written = host_words != nullptr && P.num_tiles > 0;
   return rc;
@@ -424,15 +426,19 @@ size_t gsplat_hip_bin_workspace_bytes(const gsplat_raster_meta* meta,
          emit_layout(P, capacity).total;
 }
 
-int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
-                   const float* conics, const float* colors,
-                   const float* opacities, const float* depths,
-                   int64_t capacity, int32_t* perm, float* packed,
-                   int32_t* splat_offsets, int32_t* binned_ids,
-                   int32_t* tile_offsets, int32_t* host_words,
-                   void* workspace, size_t workspace_bytes, void* stream,
-                   void* count_stream, void* inputs_event,
-                   void* count_event, void* status_event) {
+}  // extern "C"
+
+namespace {
+// gsplat_hip_bin; zero (may be null): two spans that the tile-range launch
+// zeroes on the side (or a launch of their own where it does not run).
+int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
+             const float* conics, const float* colors, const float* opacities,
+             const float* depths, int64_t capacity, int32_t* perm,
+             float* packed, int32_t* splat_offsets, int32_t* binned_ids,
+             int32_t* tile_offsets, int32_t* host_words, void* workspace,
+             size_t workspace_bytes, void* stream, void* count_stream,
+             void* inputs_event, void* count_event, void* status_event,
+             const gs::ZeroSpan* zero) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -457,6 +463,8 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
                   workspace_bytes, need);
     return GSPLAT_ERR_WORKSPACE;
   }
+  // host_words[2] is set by the tile-range launch if a range is long
+  if (host_words != nullptr) host_words[2] = 0;
   char* base = static_cast<char*>(workspace);
   int32_t* n_dev = reinterpret_cast<int32_t*>(base);
   int32_t* status_dev = n_dev + 1;
@@ -492,7 +500,7 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
     if (!rc)
       rc = bin_emit_impl(meta, packed, splat_offsets, capacity, binned_ids,
                          nullptr, tile_offsets, status_dev, cws, cbytes, ews,
-                         ebytes, s, host_words, &written);
+                         ebytes, s, host_words, &written, zero);
     if (!rc && !written) {
       gs::set_error("gsplat_hip_bin: the tile ranges did not report N");
       rc = GSPLAT_ERR_INVALID_ARGUMENT;
@@ -531,7 +539,7 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
   bool written = false;
   rc = bin_emit_impl(meta, packed, splat_offsets, capacity, binned_ids,
                      nullptr, tile_offsets, status_dev, cws, cbytes, ews,
-                     ebytes, s, host_words, &written);
+                     ebytes, s, host_words, &written, zero);
   if (rc || host_words == nullptr) return rc;
   // 5. N and the status reach the host: written by the tile range launch
   //    itself, or else in one copy
@@ -544,6 +552,65 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
   return rc;
 }
 
+}  // namespace
+
+extern "C" {
+
+int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
+                   const float* conics, const float* colors,
+                   const float* opacities, const float* depths,
+                   int64_t capacity, int32_t* perm, float* packed,
+                   int32_t* splat_offsets, int32_t* binned_ids,
+                   int32_t* tile_offsets, int32_t* host_words,
+                   void* workspace, size_t workspace_bytes, void* stream,
+                   void* count_stream, void* inputs_event,
+                   void* count_event, void* status_event) {
+  return bin_impl(meta, means2d, conics, colors, opacities, depths, capacity,
+                  perm, packed, splat_offsets, binned_ids, tile_offsets,
+                  host_words, workspace, workspace_bytes, stream, count_stream,
+                  inputs_event, count_event, status_event, nullptr);
+}
+
+}  // extern "C"
+
+namespace {
+// Arguments of the forward entry points (`what` names the entry in errors);
+// `in_bin`: the binning's outputs are still to be written by the same call.
+int check_forward(const RasterParams& P, const float* packed,
+                  const int32_t* tile_offsets, const int32_t* binned_ids,
+                  const float* out_rgb, const float* out_final_T,
+                  const int32_t* out_last, const int32_t* out_tile_stop,
+                  int64_t n_pairs, const void* workspace,
+                  size_t workspace_bytes, const char* what) {
+  int rc = null_check({packed, tile_offsets, out_rgb}, what);
+  if (rc) return rc;
+  (void)binned_ids;
+  if ((out_final_T == nullptr) != (out_last == nullptr) ||
+      (out_final_T == nullptr) != (out_tile_stop == nullptr)) {
+    gs::set_error(
+        "%s: out_final_T, out_last and out_tile_stop must all be given or all "
+        "be NULL",
+        what);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  if (n_pairs < 0) {
+    gs::set_error("%s: invalid pair count %lld", what, (long long)n_pairs);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  // the eval forward (no state outputs) records no segments
+  const int64_t ws_pairs = out_final_T != nullptr ? n_pairs : 0;
+  if (workspace != nullptr &&
+      workspace_bytes < gs::render_workspace_bytes(P, ws_pairs)) {
+    gs::set_error("%s: workspace too small (%zu < %zu)", what,
+                  workspace_bytes, gs::render_workspace_bytes(P, ws_pairs));
+    return GSPLAT_ERR_WORKSPACE;
+  }
+  return GSPLAT_OK;
+}
+}  // namespace
+
+extern "C" {
+
 int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
                               const float* packed, const int32_t* tile_offsets,
                               const int32_t* binned_ids, float* out_rgb,
@@ -553,33 +620,74 @@ int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
                               void* stream) {
   RasterParams P;
   int rc = make_params(meta, P);
+  if (!rc)
+    rc = check_forward(P, packed, tile_offsets, binned_ids, out_rgb,
+                       out_final_T, out_last, out_tile_stop, n_pairs,
+                       workspace, workspace_bytes, "gsplat_hip_render_forward");
   if (rc) return rc;
-  rc = null_check({packed, tile_offsets, out_rgb}, "gsplat_hip_render_forward");
-  if (rc) return rc;
-  if ((out_final_T == nullptr) != (out_last == nullptr) ||
-      (out_final_T == nullptr) != (out_tile_stop == nullptr)) {
-    gs::set_error(
-        "gsplat_hip_render_forward: out_final_T, out_last and out_tile_stop "
-        "must all be given or all be NULL");
-    return GSPLAT_ERR_INVALID_ARGUMENT;
-  }
-  if (n_pairs < 0) {
-    gs::set_error("gsplat_hip_render_forward: invalid pair count %lld",
-                  (long long)n_pairs);
-    return GSPLAT_ERR_INVALID_ARGUMENT;
-  }
-  // the eval forward (no state outputs) records no segments
-  const int64_t ws_pairs = out_final_T != nullptr ? n_pairs : 0;
-  if (workspace != nullptr &&
-      workspace_bytes < gs::render_workspace_bytes(P, ws_pairs)) {
-    gs::set_error("gsplat_hip_render_forward: workspace too small (%zu < %zu)",
-                  workspace_bytes, gs::render_workspace_bytes(P, ws_pairs));
-    return GSPLAT_ERR_WORKSPACE;
-  }
   return gs::launch_render_forward(P, packed, tile_offsets, binned_ids, out_rgb,
                                    out_final_T, out_last, out_tile_stop,
                                    n_pairs, workspace,
                                    static_cast<hipStream_t>(stream));
+}
+
+int gsplat_hip_render_forward_long(const gsplat_raster_meta* meta,
+                                   const float* packed,
+                                   const int32_t* tile_offsets,
+                                   const int32_t* binned_ids, float* out_rgb,
+                                   float* out_final_T, int32_t* out_last,
+                                   int32_t* out_tile_stop, int64_t n_pairs,
+                                   void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  RasterParams P;
+  int rc = make_params(meta, P);
+  if (!rc)
+    rc = check_forward(P, packed, tile_offsets, binned_ids, out_rgb,
+                       out_final_T, out_last, out_tile_stop, n_pairs,
+                       workspace, workspace_bytes,
+                       "gsplat_hip_render_forward_long");
+  if (rc) return rc;
+  return gs::launch_render_forward_long(
+      P, packed, tile_offsets, binned_ids, out_rgb, out_final_T, out_last,
+      out_tile_stop, n_pairs, workspace, static_cast<hipStream_t>(stream));
+}
+
+int gsplat_hip_bin_render_forward(
+    const gsplat_raster_meta* meta, const float* means2d, const float* conics,
+    const float* colors, const float* opacities, const float* depths,
+    int64_t capacity, int32_t* perm, float* packed, int32_t* splat_offsets,
+    int32_t* binned_ids, int32_t* tile_offsets, int32_t* host_words,
+    void* bin_workspace, size_t bin_workspace_bytes, float* out_rgb,
+    float* out_final_T, int32_t* out_last, int32_t* out_tile_stop,
+    void* render_workspace, size_t render_workspace_bytes, void* stream,
+    void* count_stream, void* inputs_event, void* count_event,
+    void* status_event) {
+  RasterParams P;
+  int rc = make_params(meta, P);
+  if (!rc)
+    rc = null_check({host_words, render_workspace},
+                    "gsplat_hip_bin_render_forward");
+  if (!rc)
+    rc = check_forward(P, packed, tile_offsets, binned_ids, out_rgb,
+                       out_final_T, out_last, out_tile_stop, capacity,
+                       render_workspace, render_workspace_bytes,
+                       "gsplat_hip_bin_render_forward");
+  if (rc) return rc;
+  // The tile-range launch zeroes what the forward needs zero (hand-off
+  // counters, gradient records), so the forward follows it directly.
+  gs::ZeroSpan zero[2];
+  gs::render_forward_zero_spans(P, capacity, render_workspace,
+                                out_final_T != nullptr, zero);
+  rc = bin_impl(meta, means2d, conics, colors, opacities, depths, capacity,
+                perm, packed, splat_offsets, binned_ids, tile_offsets,
+                host_words, bin_workspace, bin_workspace_bytes, stream,
+                count_stream, inputs_event, count_event, status_event, zero);
+  if (rc) return rc;
+  return gs::launch_render_forward(
+      P, packed, tile_offsets, binned_ids, out_rgb, out_final_T, out_last,
+      out_tile_stop, capacity, render_workspace,
+      static_cast<hipStream_t>(stream),
+      gs::kForwardPreZeroed | gs::kForwardNoLong);
 }
 
 size_t gsplat_hip_render_workspace_bytes(const gsplat_raster_meta* meta,

@@ -263,7 +263,8 @@ __device__ __forceinline__ int wave_max_row3(int x) {
 // the closed form of gT <- alpha <g,c> + (1 - alpha) gT over the later
 // splats, and T at its end is recorded.
 constexpr int kSegSplats = 128;     // multiple of kBatch
-constexpr int kHandoff = 128;       // multiple of kSegSplats
+constexpr int kHandoff = kHandoffPairs;  // multiple of kSegSplats
+static_assert(kHandoff % kSegSplats == 0, "hand-off at a segment boundary");
 constexpr int kLongStrips = 1;      // strips per wavefront of the long kernel
 
 struct HeavyState {      // all null: every tile is walked whole by one wave
@@ -1216,40 +1217,70 @@ HeavyState heavy_state(const RasterParams& P, int64_t n_pairs, void* ws) {
 }
 }  // namespace
 
+void render_forward_zero_spans(const RasterParams& P, int64_t n_pairs,
+                               void* workspace, bool training,
+                               ZeroSpan out[2]) {
+  out[0] = out[1] = ZeroSpan{nullptr, 0};
+  if (P.num_tiles == 0 || workspace == nullptr) return;
+  const HeavyState H = heavy_state(P, training ? n_pairs : 0, workspace);
+  out[0] = ZeroSpan{reinterpret_cast<uint32_t*>(H.counters), 2};
+  // The training forward also zeroes the backward's gradient records (the
+  // backward accumulates into them and its unpack leaves them zero again).
+  if (training && H.acc != nullptr)
+    out[1] = ZeroSpan{reinterpret_cast<uint32_t*>(H.acc),
+                      (int64_t)P.num_splats * kAccFloats};
+}
+
+namespace {
+HeavyState forward_state(const RasterParams& P, int64_t n_pairs,
+                         void* workspace, const float* out_T) {
+  // Without the state outputs no segment is recorded: the layout of
+  // n_pairs = 0 (no slot area to speak of) fits the eval workspace.
+  HeavyState H = heavy_state(P, out_T != nullptr ? n_pairs : 0, workspace);
+  if (out_T == nullptr) H.rec = nullptr;  // no backward: hand-off only
+  return H;
+}
+}  // namespace
+
 int launch_render_forward(const RasterParams& P, const float* packed,
                           const int32_t* tile_offsets,
                           const int32_t* binned_ids, float* out_rgb,
                           float* out_T, int32_t* out_last,
                           int32_t* out_tile_stop, int64_t n_pairs,
-                          void* workspace, hipStream_t stream) {
+                          void* workspace, hipStream_t stream, int flags) {
   if (P.num_tiles == 0) return GSPLAT_OK;
-  // Without the state outputs no segment is recorded: the layout of
-  // n_pairs = 0 (no slot area to speak of) fits the eval workspace.
-  HeavyState H = heavy_state(P, out_T != nullptr ? n_pairs : 0, workspace);
-  if (out_T == nullptr) H.rec = nullptr;  // no backward: hand-off only
+  const HeavyState H = forward_state(P, n_pairs, workspace, out_T);
   const float4* pk = reinterpret_cast<const float4*>(packed);
-  if (H.counters != nullptr) {
-    // The training forward also zeroes the backward's gradient records (the
-    // backward accumulates into them and its unpack leaves them zero again).
-    const int rc =
-        H.acc != nullptr
-            ? launch_zero2(reinterpret_cast<uint32_t*>(H.counters), 2,
-                           reinterpret_cast<uint32_t*>(H.acc),
-                           (int64_t)P.num_splats * kAccFloats, stream)
-            : launch_fill_i32(H.counters, 0, 2, stream);
+  if (H.counters != nullptr && !(flags & kForwardPreZeroed)) {
+    ZeroSpan z[2];
+    render_forward_zero_spans(P, n_pairs, workspace, out_T != nullptr, z);
+    const int rc = launch_zero2(z[0].p, z[0].n, z[1].p, z[1].n, stream);
     if (rc) return rc;
   }
   hipLaunchKernelGGL(render_fwd_kernel, dim3((unsigned)P.num_tiles),
                      dim3(kLanes), 0, stream, P, pk, tile_offsets, binned_ids,
                      out_rgb, out_T, out_last, out_tile_stop, H);
-  int rc = check_launch("render_fwd_kernel");
-  if (rc || H.counters == nullptr) return rc;
+  const int rc = check_launch("render_fwd_kernel");
+  if (rc || (flags & kForwardNoLong)) return rc;
+  return launch_render_forward_long(P, packed, tile_offsets, binned_ids,
+                                    out_rgb, out_T, out_last, out_tile_stop,
+                                    n_pairs, workspace, stream);
+}
+
+int launch_render_forward_long(const RasterParams& P, const float* packed,
+                               const int32_t* tile_offsets,
+                               const int32_t* binned_ids, float* out_rgb,
+                               float* out_T, int32_t* out_last,
+                               int32_t* out_tile_stop, int64_t n_pairs,
+                               void* workspace, hipStream_t stream) {
+  if (P.num_tiles == 0 || workspace == nullptr) return GSPLAT_OK;
+  const HeavyState H = forward_state(P, n_pairs, workspace, out_T);
   // Workgroups stride over the hand-off list (its length is on the device).
   const unsigned grid = (unsigned)std::min<int64_t>(P.num_tiles, 2048);
   hipLaunchKernelGGL(render_fwd_long_kernel<kLongStrips>, dim3(grid),
-                     dim3(256 / kLongStrips), 0,
-                     stream, P, pk, tile_offsets, binned_ids, out_rgb, out_T,
-                     out_last, out_tile_stop, H);
+                     dim3(256 / kLongStrips), 0, stream, P,
+                     reinterpret_cast<const float4*>(packed), tile_offsets,
+                     binned_ids, out_rgb, out_T, out_last, out_tile_stop, H);
   return check_launch("render_fwd_long_kernel");
 }
 

@@ -158,12 +158,24 @@ int launch_emit(const RasterParams& P, const float* packed,
                 uint32_t* vals, int pair_passes, uint32_t* hist_partials,
                 uint32_t* pair_ghist, uint32_t* pair_status,
                 int64_t pair_status_words, hipStream_t stream);
+// Tile ranges longer than this many pairs are walked by the forward's first
+// launch only up to here and continued by its second (render_fwd_long).
+constexpr int kHandoffPairs = GSPLAT_HANDOFF_PAIRS;
+
+// Words that a launch zeroes on the side (n 32-bit words at p).
+struct ZeroSpan {
+  uint32_t* p;
+  int64_t n;
+};
+
 // tile_offsets[0..T] and (unless tile_counts is NULL) tile_counts[0..T)
 // from the n sorted tile keys (min(n, *n_dev) of them with n_dev).  With
 // status_out, the same launch writes there the OR of the (non-null) give-up
 // status words err[0..2] of the binning's look-backs; with host_words
 // (device-mapped pinned host memory, n > 0 only) it also writes
-// {*n_dev, that OR} there.
+// {*n_dev, that OR} to host_words[0..1] and sets host_words[2] to 1 if a
+// tile range is longer than kHandoffPairs (the caller zeroes it before).
+// zero (may be null): two spans that the same launch zeroes.
 int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        int32_t* tile_offsets, int32_t* tile_counts,
                        hipStream_t stream, const int32_t* n_dev = nullptr,
@@ -171,7 +183,8 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        const uint32_t* err1 = nullptr,
                        const uint32_t* err2 = nullptr,
                        int32_t* status_out = nullptr,
-                       int32_t* host_words = nullptr);
+                       int32_t* host_words = nullptr,
+                       const ZeroSpan* zero = nullptr);
 int launch_zero2(uint32_t* a, int64_t na, uint32_t* b, int64_t nb,
                  hipStream_t stream);
 int launch_fill_i32(int32_t* dst, int32_t value, int64_t n, hipStream_t stream);
@@ -183,12 +196,29 @@ int launch_zero_grads(float* g_m, float* g_q, float* g_c, float* g_o,
 // workspace (render_workspace_bytes, may be null): heavy-tile segment state,
 // written by the forward and read by the backward of the same binning.
 size_t render_workspace_bytes(const RasterParams& P, int64_t n_pairs);
+// Forward launches.  flags: kForwardPreZeroed (the words of
+// render_forward_zero_spans are already zero), kForwardNoLong (the tiles
+// handed off are left for launch_render_forward_long, which the caller
+// issues unless no tile range is longer than kHandoffPairs).
+constexpr int kForwardPreZeroed = 1;
+constexpr int kForwardNoLong = 2;
 int launch_render_forward(const RasterParams& P, const float* packed,
                           const int32_t* tile_offsets,
                           const int32_t* binned_ids, float* out_rgb,
                           float* out_T, int32_t* out_last,
                           int32_t* out_tile_stop, int64_t n_pairs,
-                          void* workspace, hipStream_t stream);
+                          void* workspace, hipStream_t stream, int flags = 0);
+int launch_render_forward_long(const RasterParams& P, const float* packed,
+                               const int32_t* tile_offsets,
+                               const int32_t* binned_ids, float* out_rgb,
+                               float* out_T, int32_t* out_last,
+                               int32_t* out_tile_stop, int64_t n_pairs,
+                               void* workspace, hipStream_t stream);
+// The workspace words a forward needs zero before it starts (hand-off
+// counters; with the state outputs also the backward's gradient records).
+void render_forward_zero_spans(const RasterParams& P, int64_t n_pairs,
+                               void* workspace, bool training,
+                               ZeroSpan out[2]);
 int launch_render_backward(const RasterParams& P, const float* packed,
                            const int32_t* tile_offsets,
                            const int32_t* binned_ids, const float* final_T,

@@ -17,11 +17,12 @@ import torch  # noqa: F401  (must be loaded before the HIP library)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("GSPLAT_HIP_LIB", os.path.join(_HERE, "lib", "libgsplat_hip.so"))
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 TILE_SIZE = 16
 RECORD_FLOATS = 12
 PROJECT_NOALLOC_SCRATCH_BYTES = 1 << 20   # GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES
 STATUS_LOOKBACK_TIMEOUT = 1               # GSPLAT_STATUS_LOOKBACK_TIMEOUT
+HANDOFF_PAIRS = 128                       # GSPLAT_HANDOFF_PAIRS
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -73,6 +74,11 @@ SIGNATURES = {
     "gsplat_hip_bin": (ctypes.c_int, [_PM] + [_vp] * 5 + [_i64] + [_vp] * 7 + [_sz] + [_vp] * 5),
     "gsplat_hip_render_workspace_bytes": (_sz, [_PM, _i64]),
     "gsplat_hip_render_forward": (ctypes.c_int, [_PM] + [_vp] * 7 + [_i64, _vp, _sz, _vp]),
+    "gsplat_hip_render_forward_long": (ctypes.c_int, [_PM] + [_vp] * 7 + [_i64, _vp, _sz, _vp]),
+    "gsplat_hip_bin_render_forward": (
+        ctypes.c_int,
+        [_PM] + [_vp] * 5 + [_i64] + [_vp] * 7 + [_sz] + [_vp] * 5 + [_sz] + [_vp] * 5,
+    ),
     "gsplat_hip_render_backward": (ctypes.c_int, [_PM] + [_vp] * 11 + [_i64, _vp, _sz, _vp]),
     "gsplat_hip_project_forward": (ctypes.c_int, [_PP] + [_vp] * 10 + [_vp]),
     "gsplat_hip_project_backward_workspace_bytes": (_sz, [_PP]),

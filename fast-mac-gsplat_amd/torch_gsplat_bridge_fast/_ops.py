@@ -115,6 +115,7 @@ class BinState:
     _status_ready: Optional[torch.cuda.Event] = None
     _ring: Optional["_DeviceBinState"] = None        # owner of the pinned words (fast path)
     _generation: int = 0
+    _long_index: Optional[tuple] = None              # where _n_host holds the long-range flag
 
     def _words_current(self) -> bool:
         """False if the pinned ring slot has been reused by later binnings."""
@@ -143,6 +144,17 @@ class BinState:
             if n > cap or 2 * _headroom(n) < cap:
                 _capacity[self._key] = _headroom(n)
         return n <= self.capacity
+
+    @property
+    def long_tiles(self) -> bool:
+        """Whether some tile range is longer than HANDOFF_PAIRS pairs (the forward then hands tiles
+        to its continuation); True when the binning did not report it.  Waits like n_pairs."""
+        if self._long_index is None:
+            return True
+        self.n_pairs  # the transfer that carries N carries the flag too
+        if not self._words_current():
+            return True
+        return bool(self._n_host[self._long_index])
 
     def check_status(self) -> None:
         """Raises RuntimeError if a look-back wait of this binning gave up (its tile ranges are then
@@ -220,13 +232,34 @@ def bin_gaussians(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors
 def bin_and_render(meta: _lib.RasterMeta, flat, *, save_state: bool):
     """Binning then render_forward with the capacity check after the forward is enqueued, so
     that the host never waits on the GPU in between.  Returns (BinState, render_forward outputs);
-    the caller runs st.check_status() before the results are relied on."""
+    the caller runs st.check_status() before the results are relied on.  With the shape's pair
+    capacity known, both go through one C-ABI call (gsplat_hip_bin_render_forward) and the
+    continuation of long tiles is launched only if the binning reports a tile range longer than
+    HANDOFF_PAIRS."""
+    dev = flat[0].device
+    key = (dev.index, meta.batch, meta.gaussians_per_batch, meta.height, meta.width)
+    cap = _capacity.get(key)
+    if cap is not None and not _staged():
+        st, out, rws = _bin_render_fast(meta, flat, cap, key, save_state)
+        if st.confirm():
+            if st.long_tiles:
+                render_forward_long(meta, st, out, rws)
+            return st, out
+        st = bin_gaussians(meta, *flat)
+        return st, render_forward(meta, st, save_state=save_state)
     st = bin_gaussians(meta, *flat, defer_check=True)
     out = render_forward(meta, st, save_state=save_state)
     if not st.confirm():
         st = bin_gaussians(meta, *flat)
         out = render_forward(meta, st, save_state=save_state)
     return st, out
+
+
+def _staged() -> bool:
+    """True while per-stage timing of the binning or the forward is on: those calls then run one
+    by one, each bracketed by its events."""
+    return _timing is not None and (_timing_ops is None or
+                                    bool(_timing_ops & {"bin_count", "bin_pack", "bin_emit", "render_forward"}))
 
 
 class _DeviceBinState:
@@ -244,7 +277,10 @@ class _DeviceBinState:
         self.status = torch.cuda.Event()
         for e in (self.inputs, self.count, self.status):
             e.record(main)      # creates the HIP event
-        self.ring = torch.zeros((self.RING, 2), dtype=torch.int32, pin_memory=True)
+        # {N, status, long-range flag, unused} per call, read through a numpy view
+        self.ring_t = torch.zeros((self.RING, 4), dtype=torch.int32, pin_memory=True)
+        self.ring = self.ring_t.numpy()
+        self.ring_base = self.ring_t.data_ptr()
         self.calls = 0
 
     def slot(self) -> int:
@@ -279,12 +315,52 @@ def _bin_fast(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Te
     # every later use of these buffers on the launch stream is ordered after it.
     check(L.gsplat_hip_bin(meta, ptr(means2d), ptr(conics), ptr(colors), ptr(opacities), ptr(depths), cap,
                            ptr(perm), ptr(packed), ptr(splat_offsets), ptr(pairs), ptr(tile_offsets),
-                           d.ring.data_ptr() + 8 * slot, ptr(ws), ws_bytes,
+                           d.ring_base + 16 * slot, ptr(ws), ws_bytes,
                            torch.cuda.current_stream(dev).cuda_stream, _side_stream(dev).cuda_stream,
                            d.inputs.cuda_event, d.count.cuda_event, d.status.cuda_event),
           "gsplat_hip_bin")
     return BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, d.ring, d.status, None, key, (slot, 0),
-                    d.ring, (slot, 1), d.status, d, d.calls - 1)
+                    d.ring, (slot, 1), d.status, d, d.calls - 1, (slot, 2))
+
+
+def _bin_render_fast(meta: _lib.RasterMeta, flat, cap: int, key: tuple, save_state: bool):
+    """Binning with buffers of the known capacity and the forward in one C-ABI call
+    (gsplat_hip_bin_render_forward).  Returns (BinState, render_forward outputs, render workspace);
+    the continuation of long tiles is left to the caller."""
+    L = _lib.lib()
+    means2d, conics, colors, opacities, depths = flat
+    dev = means2d.device
+    B, G, H, W = meta.batch, meta.gaussians_per_batch, meta.height, meta.width
+    BG = B * G
+    tiles = B * ((H + 15) // 16) * ((W + 15) // 16)
+    d = _device_bin.get(dev.index)
+    if d is None:
+        d = _device_bin[dev.index] = _DeviceBinState(dev)
+    perm = _empty(BG, torch.int32, dev)
+    packed = torch.empty((BG, _lib.RECORD_FLOATS), dtype=torch.float32, device=dev)
+    splat_offsets = _empty(BG + 1, torch.int32, dev)
+    tile_offsets = _empty(tiles + 1, torch.int32, dev)
+    pairs = _empty(cap, torch.int32, dev)
+    ws_bytes = L.gsplat_hip_bin_workspace_bytes(meta, cap)
+    ws = _empty(max(ws_bytes, 1), torch.uint8, dev)
+    img = torch.empty((B, H, W, 3), dtype=torch.float32, device=dev)
+    final_T = last = tile_stop = None
+    if save_state:
+        final_T = torch.empty((B, H, W), dtype=torch.float32, device=dev)
+        last = torch.empty((B, H, W), dtype=torch.int32, device=dev)
+        tile_stop = _empty(tiles, torch.int32, dev)
+    rws_bytes = L.gsplat_hip_render_workspace_bytes(meta, cap if save_state else 0)
+    rws = _empty(max(rws_bytes, 1), torch.uint8, dev)
+    slot = d.slot()
+    check(L.gsplat_hip_bin_render_forward(
+        meta, ptr(means2d), ptr(conics), ptr(colors), ptr(opacities), ptr(depths), cap, ptr(perm), ptr(packed),
+        ptr(splat_offsets), ptr(pairs), ptr(tile_offsets), d.ring_base + 16 * slot, ptr(ws), ws_bytes, ptr(img),
+        ptr(final_T), ptr(last), ptr(tile_stop), ptr(rws), rws_bytes,
+        torch.cuda.current_stream(dev).cuda_stream, _side_stream(dev).cuda_stream,
+        d.inputs.cuda_event, d.count.cuda_event, d.status.cuda_event), "gsplat_hip_bin_render_forward")
+    st = BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, d.ring, d.status, None, key, (slot, 0),
+                  d.ring, (slot, 1), d.status, d, d.calls - 1, (slot, 2))
+    return st, (img, final_T, last, tile_stop, (rws if save_state else None)), rws
 
 
 def _bin(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Tensor,
@@ -376,6 +452,17 @@ def render_forward(meta: _lib.RasterMeta, st: BinState, *, save_state: bool):
                                           stream_of(img)),
               "gsplat_hip_render_forward")
     return img, final_T, last, tile_stop, (ws if save_state else None)
+
+
+def render_forward_long(meta: _lib.RasterMeta, st: BinState, out, workspace: Tensor) -> None:
+    """Continues the tiles that the forward of gsplat_hip_bin_render_forward handed off (out: its
+    (img, final_T, last, tile_stop, ...) outputs, workspace: its render workspace)."""
+    L = _lib.lib()
+    img, final_T, last, tile_stop = out[:4]
+    check(L.gsplat_hip_render_forward_long(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.pairs), ptr(img),
+                                           ptr(final_T), ptr(last), ptr(tile_stop), st.capacity, ptr(workspace),
+                                           workspace.numel(), stream_of(img)),
+          "gsplat_hip_render_forward_long")
 
 
 def render_backward(meta: _lib.RasterMeta, st: BinState, final_T: Tensor, last: Tensor, tile_stop: Tensor,

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 9
+#define GSPLAT_HIP_ABI_VERSION 10
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -183,11 +183,13 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
  * concurrently; then bin_pack (after count_event) and bin_emit with the pair
  * capacity `capacity` (see bin_emit: n_pairs).  Finally the pair count N
  * and the binning's status word (GSPLAT_STATUS_*) reach host_words[0] and
- * host_words[1] (two int32 of page-locked host memory mapped for the device,
- * as hipHostMalloc and torch's pin_memory allocate it; may be NULL): the
- * tile-range launch on `stream` writes them directly (a capacity of 0 copies
- * them instead), after which status_event (may be NULL) is recorded on
- * `stream`: the caller waits for it before reading them.  The events are the
+ * host_words[1], and host_words[2] is 1 if some tile range is longer than
+ * GSPLAT_HANDOFF_PAIRS pairs, else 0 (host_words: three int32 of page-locked
+ * host memory mapped for the device, as hipHostMalloc and torch's
+ * pin_memory allocate it; may be NULL): the call sets host_words[2] to 0 and
+ * the tile-range launch on `stream` writes the words directly (a capacity of
+ * 0 copies N and the status instead), after which status_event (may be NULL)
+ * is recorded on `stream`: the caller waits for it before reading them.  The events are the
  * caller's (hipEvent_t; inputs_event and count_event are required when
  * count_stream differs from stream).  If a look-back gave up, every tile
  * range is empty (the compositors then read no pair) and the status says
@@ -247,6 +249,50 @@ int gsplat_hip_render_forward(const gsplat_raster_meta* meta,
                               int32_t* out_tile_stop, int64_t n_pairs,
                               void* workspace, size_t workspace_bytes,
                               void* stream);
+
+/* Tile ranges longer than this many pairs are handed from the forward's
+ * one-wavefront walk to a continuation with four wavefronts per tile (with
+ * a workspace). */
+#define GSPLAT_HANDOFF_PAIRS 128
+
+/* The forward compositor in two parts.  gsplat_hip_render_forward is
+ * gsplat_hip_bin_render_forward's forward followed by this call, which
+ * continues the tiles that the forward handed off (nothing without a
+ * workspace, or when no tile range is longer than GSPLAT_HANDOFF_PAIRS).
+ * Same arguments as gsplat_hip_render_forward.  It has no counterpart in
+ * the reference: it is for callers that read host_words[2] of the binning
+ * and skip it when it is 0. */
+int gsplat_hip_render_forward_long(const gsplat_raster_meta* meta,
+                                   const float* packed,
+                                   const int32_t* tile_offsets,
+                                   const int32_t* binned_ids, float* out_rgb,
+                                   float* out_final_T, int32_t* out_last,
+                                   int32_t* out_tile_stop, int64_t n_pairs,
+                                   void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
+/* gsplat_hip_bin (arguments up to status_event, with its workspace as
+ * bin_workspace) followed by gsplat_hip_render_forward on its outputs with
+ * n_pairs = capacity and render_workspace (required, as are host_words),
+ * except that the continuation of long tiles is left to
+ * gsplat_hip_render_forward_long: call it with the same arguments unless
+ * host_words[2] is 0.  The tile-range launch of the binning also zeroes the
+ * forward's workspace words, so the forward follows it without a launch of
+ * its own for that, and status_event is recorded before the forward, so the
+ * host can read host_words while the forward runs.  With N above capacity
+ * (see gsplat_hip_bin) the image is that of the incomplete binning.  It has
+ * no counterpart in the reference (which binds bin and render as two ops):
+ * it is the one-call form of both for the per-step path. */
+int gsplat_hip_bin_render_forward(
+    const gsplat_raster_meta* meta, const float* means2d, const float* conics,
+    const float* colors, const float* opacities, const float* depths,
+    int64_t capacity, int32_t* perm, float* packed, int32_t* splat_offsets,
+    int32_t* binned_ids, int32_t* tile_offsets, int32_t* host_words,
+    void* bin_workspace, size_t bin_workspace_bytes, float* out_rgb,
+    float* out_final_T, int32_t* out_last, int32_t* out_tile_stop,
+    void* render_workspace, size_t render_workspace_bytes, void* stream,
+    void* count_stream, void* inputs_event, void* count_event,
+    void* status_event);
 
 /* Backward compositor.  Replaces render_fast_backward_saved
  * (variants/v8/csrc/bindings.cpp:204; kernel gsplat_v8_kernels.metal:

@@ -572,3 +572,80 @@ def test_backward_with_another_n_pairs_ignores_records(gpu):
     assert int(stop1.max().item()) > 256
     oracle_parity(sc, H, W, B, G, (0.0, 0.0, 0.0), w.numpy(), img.cpu().numpy(), [t.cpu().numpy() for t in out],
                   "backward with another n_pairs", gpu_last=last1.cpu().numpy())
+
+
+def _tile_stack(n, seed, B=1, H=64, W=80, extra=60):
+    """n tiny splats whose supports lie inside tile (1, 1) of every image
+    (that tile's range holds exactly n pairs) plus `extra` small splats
+    spread over the image's right part."""
+    g = torch.Generator().manual_seed(seed)
+    G = n + extra
+    # the others lie right of pixel column 35, clear of tile (1, 1) (supports
+    # reach 4.5 pixels from the centre)
+    m = torch.rand(B, G, 2, generator=g) * torch.tensor([W - 44.0, H - 8.0]) + torch.tensor([40.0, 4.0])
+    m[:, :n] = 23.5 + torch.rand(B, n, 2, generator=g)
+    conics = torch.zeros(B, G, 3)
+    conics[..., 0] = 4.0
+    conics[..., 2] = 4.0
+    conics[:, n:, 0] = 0.5
+    conics[:, n:, 2] = 0.5
+    return {
+        "means2d": m.contiguous(),
+        "conics": conics.contiguous(),
+        "colors": torch.rand(B, G, 3, generator=g),
+        "opacities": 0.1 + 0.5 * torch.rand(B, G, generator=g),
+        "depths": torch.rand(B, G, generator=g) * 10.0,
+    }
+
+
+@pytest.mark.parametrize("kind", ["config1_small", "heavy", "stack128", "stack129"])
+def test_one_call_bin_and_forward(gpu, kind):
+    """With the shape's pair capacity known, bin_and_render bins and composites in one C-ABI call
+    (gsplat_hip_bin_render_forward: the tile-range launch zeroes the forward's workspace words)
+    and continues long tiles (gsplat_hip_render_forward_long) only when the binning reports a
+    tile range longer than HANDOFF_PAIRS.  Checked: the flag against the tile counts (a range of
+    exactly 128 pairs is not long, 129 is), binning, image and state bit-identical to the
+    separate calls of the first binning of the shape, the eval forward's image, and image and
+    gradients of the one-call forward's state against the tile oracle."""
+    from torch_gsplat_bridge_fast import _lib, _ops
+
+    if kind == "config1_small":
+        B, G, H, W = 2, 3000, 200, 264
+        sc = make_scene_2d(1, seed=5, G=G, B=B, H=H, W=W)
+    elif kind == "heavy":
+        B, G, H, W = 2, 2500, 48, 80
+        sc = _faint_crowd(21, B, G, H, W)
+    else:
+        n = 128 if kind == "stack128" else 129
+        B, H, W = 2, 64, 80
+        sc = _tile_stack(n, seed=n, B=B, H=H, W=W)
+        G = sc["opacities"].shape[1]
+    print(f"one-call binning + forward: {kind} B={B} G={G} {W}x{H}", flush=True)
+    meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, (0.0, 0.0, 0.0))
+    flat = [torch.as_tensor(sc[k]).reshape(B * G, -1).squeeze(-1).contiguous().to(gpu) for k in KEYS]
+    _ops._capacity.pop((0, B, G, H, W), None)
+    st0, out0 = _ops.bin_and_render(meta, flat, save_state=True)   # first binning of the shape
+    st1, out1 = _ops.bin_and_render(meta, flat, save_state=True)   # one call
+    st2, out2 = _ops.bin_and_render(meta, flat, save_state=False)  # one call, eval forward
+    assert st0._long_index is None and st1._long_index is not None and st2._long_index is not None
+    st1.check_status()
+    st2.check_status()
+    counts = (st1.tile_offsets[1:] - st1.tile_offsets[:-1]).cpu().numpy()
+    long_expected = bool(counts.max() > _lib.HANDOFF_PAIRS)
+    assert st1.long_tiles == st2.long_tiles == long_expected
+    if kind.startswith("stack"):
+        assert int(counts.max()) == int(kind[5:])
+    n = st0.n_pairs
+    assert st1.n_pairs == n
+    for a, b in [(st0.perm, st1.perm), (st0.packed, st1.packed), (st0.tile_offsets, st1.tile_offsets),
+                 (st0.splat_offsets, st1.splat_offsets), (st0.pairs[:n], st1.pairs[:n])]:
+        assert torch.equal(a, b)
+    for a, b in zip(out0[:4], out1[:4]):
+        assert torch.equal(a, b)
+    assert torch.equal(out2[0], out0[0])
+    w = torch.rand(B, H, W, 3, generator=torch.Generator().manual_seed(3))
+    img, T, last, stop, ws = out1
+    grads = _ops.render_backward(meta, st1, T, last, stop, w.to(gpu), ws)
+    torch.cuda.synchronize()
+    oracle_parity(sc, H, W, B, G, (0.0, 0.0, 0.0), w.numpy(), img.cpu().numpy(),
+                  [g.cpu().numpy() for g in grads], f"one call {kind}", gpu_last=last.cpu().numpy())
