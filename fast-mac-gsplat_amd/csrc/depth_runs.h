@@ -58,15 +58,23 @@ __device__ __forceinline__ uint64_t lanes_below() {
 }
 
 // Lanes whose 8-bit digit equals this lane's digit (every lane is active).
+// Per bit: n = the bit sign-extended (0 or ~0), b = the wavefront's ballot
+// of it; the lanes that agree with this lane are ~(b ^ n), so m &= ~(b ^ n)
+// is one three-input bit operation per 32-bit half (truth table 0x90 for
+// src0 & ~(src1 ^ src2) with the operand patterns 0xF0, 0xCC, 0xAA).
 __device__ __forceinline__ uint64_t same_digit_lanes(uint32_t d) {
-  uint64_t m = ~0ull;
+  uint32_t lo = ~0u, hi = ~0u;
 #pragma unroll
   for (int bit = 0; bit < 8; ++bit) {
-    const bool p = (d >> bit) & 1u;
-    const uint64_t b = __ballot(p);
-    m &= p ? b : ~b;
+    uint32_t n = (uint32_t)__builtin_amdgcn_sbfe((int)d, bit, 1);
+    // (through an empty asm: the ballot then compares n itself instead of
+    // recomputing the bit with a shift)
+    asm volatile("" : "+v"(n));
+    const uint64_t b = __builtin_amdgcn_ballot_w64(n != 0u);
+    lo = __builtin_amdgcn_bitop3_b32(lo, (uint32_t)b, n, 0x90);
+    hi = __builtin_amdgcn_bitop3_b32(hi, (uint32_t)(b >> 32), n, 0x90);
   }
-  return m;
+  return ((uint64_t)hi << 32) | lo;
 }
 
 // Sorts run `block % runs` of image `block / runs` (kRunThreads threads).
@@ -101,9 +109,12 @@ __device__ __forceinline__ void run_sort_block(const float* __restrict__ depths,
       const uint32_t d = (k[r] >> shift) & 255u;
       const uint64_t peers = same_digit_lanes(d);
       const uint32_t below = (uint32_t)__popcll(peers & lt);
-      uint32_t old = 0u;
-      if (below == 0u) old = atomicAdd(&S.cnt[wave][d], (uint32_t)__popcll(peers));
-      old = (uint32_t)__shfl((int)old, __ffsll((long long)peers) - 1, 64);
+      // Every lane of the digit reads its count, then the digit's lowest
+      // lane adds the group's size: one wavefront's LDS accesses take effect
+      // in program order, so all of them see the count before the addition.
+      const uint32_t old = S.cnt[wave][d];
+      __builtin_amdgcn_wave_barrier();  // the read stays before the addition
+      if (below == 0u) atomicAdd(&S.cnt[wave][d], (uint32_t)__popcll(peers));
       rank[r] = old + below;
     }
     __syncthreads();

@@ -31,16 +31,24 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return (lane == 0u) ? 0ull : (~0ull >> (64u - lane));
 }
 
-// Lanes of `active` whose 8-bit digit equals this lane's digit.
+// Lanes of `active` whose 8-bit digit equals this lane's digit.  Per bit:
+// n = the bit sign-extended (0 or ~0), b = the wavefront's ballot of it; the
+// lanes that agree with this lane are ~(b ^ n), so m &= ~(b ^ n) is one
+// three-input bit operation per 32-bit half (truth table 0x90 for
+// src0 & ~(src1 ^ src2) with the operand patterns 0xF0, 0xCC, 0xAA).
 __device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active) {
-  uint64_t m = active;
+  uint32_t lo = (uint32_t)active, hi = (uint32_t)(active >> 32);
 #pragma unroll
   for (int bit = 0; bit < 8; ++bit) {
-    const bool p = (d >> bit) & 1u;
-    const uint64_t b = __ballot(p);
-    m &= p ? b : ~b;
+    uint32_t n = (uint32_t)__builtin_amdgcn_sbfe((int)d, bit, 1);
+    // (through an empty asm: the ballot then compares n itself instead of
+    // recomputing the bit with a shift)
+    asm volatile("" : "+v"(n));
+    const uint64_t b = __builtin_amdgcn_ballot_w64(n != 0u);
+    lo = __builtin_amdgcn_bitop3_b32(lo, (uint32_t)b, n, 0x90);
+    hi = __builtin_amdgcn_bitop3_b32(hi, (uint32_t)(b >> 32), n, 0x90);
   }
-  return m;
+  return ((uint64_t)hi << 32) | lo;
 }
 
 struct PassArgs {
@@ -131,7 +139,7 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   constexpr int kBlockItems = kWaves * kWaveItems;
   __shared__ uint32_t cnt[kWaves][256];
   __shared__ uint32_t dstart[256];
-  __shared__ uint32_t gbase[256];
+  __shared__ uint32_t gdelta[256];  // global position of digit d's LDS slot 0
   __shared__ uint32_t wsum[kWaves];
   __shared__ uint32_t sk[kBlockItems];
   __shared__ uint32_t sv[kBlockItems];
@@ -176,11 +184,12 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
     const uint32_t d = (kreg[r] >> a.shift) & dmask;
     const uint64_t peers = match_digit(d, __ballot(valid));
     const uint32_t below = (uint32_t)__popcll(peers & lt);
-    uint32_t old = 0u;
-    if (valid && below == 0u)
-      old = atomicAdd(&cnt[wave][d], (uint32_t)__popcll(peers));
-    // every lane takes the old count from its digit's lowest lane
-    old = (uint32_t)__shfl((int)old, __ffsll((long long)peers) - 1, 64);
+    // Every lane of the digit reads its count, then the digit's lowest lane
+    // adds the group's size: one wavefront's LDS accesses take effect in
+    // program order, so all of them see the count before the addition.
+    const uint32_t old = cnt[wave][d];
+    __builtin_amdgcn_wave_barrier();  // the read stays before the addition
+    if (valid && below == 0u) atomicAdd(&cnt[wave][d], (uint32_t)__popcll(peers));
     rreg[r] = valid ? ((old + below) | (d << 16)) : 0xffffffffu;
   }
   __syncthreads();
@@ -203,7 +212,8 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
     status_store(my_status, kFlagInc32 | (prefix + tot));
   }
   dstart[t] = local;
-  gbase[t] = dbase + prefix;
+  // (modulo 2^32: the positions themselves are below 2^29)
+  gdelta[t] = dbase + prefix - local;
   __syncthreads();
 
 #pragma unroll
@@ -217,15 +227,22 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   }
   __syncthreads();
 
+  // Unrolled, so that the LDS reads of all kR elements are in flight
+  // together; 32-bit positions (n_seg <= 2^29).
   const int64_t remain = n_seg - (int64_t)blk * kBlockItems;
   const int count = remain < kBlockItems ? (int)remain : kBlockItems;
-  for (int i = t; i < count; i += kThreads) {
-    const uint32_t key = sk[i];
-    const uint32_t d = (key >> a.shift) & dmask;
-    const int64_t pos = (int64_t)gbase[d] + (int64_t)(i - (int)dstart[d]);
-    if (pos >= n_seg) continue;  // only with histograms inconsistent with the keys
-    if (kMode & kKeysOut) a.keys_out[seg_base + pos] = key;
-    a.vals_out[seg_base + pos] = sv[i];
+  const uint32_t n32 = (uint32_t)n_seg;
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    const int i = t + r * kThreads;
+    if (i < count) {
+      const uint32_t key = sk[i];
+      const uint32_t pos = gdelta[(key >> a.shift) & dmask] + (uint32_t)i;
+      if (pos < n32) {  // (fails only with histograms inconsistent with the keys)
+        if (kMode & kKeysOut) a.keys_out[seg_base + pos] = key;
+        a.vals_out[seg_base + pos] = sv[i];
+      }
+    }
   }
 }
 
