@@ -321,6 +321,52 @@ __global__ __launch_bounds__(kThreads) void sum_kernel(
   }
 }
 
+// The packed 48-byte record of splat orig at depth rank gid:
+// {mx, my, a, b}, {c, o, r, g}, {b, orig, plim, 0}.
+__device__ __forceinline__ void pack_record(
+    const RasterParams& P, const float* __restrict__ means2d,
+    const float* __restrict__ conics, const float* __restrict__ colors,
+    const float* __restrict__ opacities, float4* __restrict__ packed, int gid,
+    int orig) {
+  const float mx = means2d[2 * orig + 0];
+  const float my = means2d[2 * orig + 1];
+  const float a = conics[3 * orig + 0];
+  const float b = conics[3 * orig + 1];
+  const float c = conics[3 * orig + 2];
+  const float o = opacities[orig];
+  const float cr = colors[3 * orig + 0];
+  const float cg = colors[3 * orig + 1];
+  const float cb = colors[3 * orig + 2];
+  packed[3 * gid + 0] = make_float4(mx, my, a, b);
+  packed[3 * gid + 1] = make_float4(c, o, cr, cg);
+  packed[3 * gid + 2] =
+      make_float4(cb, __int_as_float(orig),
+                  visibility_limit(o, P.alpha_thr, P.max_alpha), 0.0f);
+}
+
+// Rank step of the small-image depth order with the records packed where
+// the ranks land: perm[gid] = in-image index, the record of gid and
+// gid_count[gid] = splat_count[orig] (the pair offsets are then scanned by
+// emit_kernel<true>).
+__global__ __launch_bounds__(run_step::kRankBlock) void rank_pack_kernel(
+    RasterParams P, const float* __restrict__ means2d,
+    const float* __restrict__ conics, const float* __restrict__ colors,
+    const float* __restrict__ opacities, run_step::RunBuffers runs_in,
+    int runs, const int32_t* __restrict__ splat_count,
+    int32_t* __restrict__ perm, float4* __restrict__ packed,
+    int32_t* __restrict__ gid_count) {
+  __shared__ run_step::RankLds S;
+  run_step::rank_block(
+      runs_in.keys, runs_in.vals, runs_in.samples, P.gpb, runs,
+      (int)blockIdx.x, S, [&](int64_t base, int pos, uint32_t v) {
+        const int gid = (int)base + pos;
+        const int orig = (int)base + (int)v;
+        perm[gid] = (int32_t)v;
+        pack_record(P, means2d, conics, colors, opacities, packed, gid, orig);
+        gid_count[gid] = splat_count[orig];
+      });
+}
+
 // One thread per depth-sorted splat (gid): gathers the attributes of
 // orig = perm[gid] into the packed 48-byte record and turns the per-gid
 // tile-hit counts into exclusive offsets splat_offsets in the same launch
@@ -343,21 +389,8 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
     // (perm is in [0, G) unless a look-back of the depth sort gave up; the
     // clamp keeps the gathers in bounds then, and the status reports it)
     const int orig = batch * P.gpb + (int)min(perm[gid], (uint32_t)(P.gpb - 1));
-    const float mx = means2d[2 * orig + 0];
-    const float my = means2d[2 * orig + 1];
-    const float a = conics[3 * orig + 0];
-    const float b = conics[3 * orig + 1];
-    const float c = conics[3 * orig + 2];
-    const float o = opacities[orig];
-    const float cr = colors[3 * orig + 0];
-    const float cg = colors[3 * orig + 1];
-    const float cb = colors[3 * orig + 2];
+    pack_record(P, means2d, conics, colors, opacities, packed, gid, orig);
     n = splat_count[orig];
-    packed[3 * gid + 0] = make_float4(mx, my, a, b);
-    packed[3 * gid + 1] = make_float4(c, o, cr, cg);
-    packed[3 * gid + 2] =
-        make_float4(cb, __int_as_float(orig),
-                    visibility_limit(o, P.alpha_thr, P.max_alpha), 0.0f);
   }
   // Workgroup exclusive scan of the counts.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -394,38 +427,105 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
     splat_offsets[P.num_splats] = end > 0x7fffffffLL ? -1 : (int)end;
 }
 
+// emit_kernel<true>: the pair offsets are scanned by the emit itself.
+struct EmitScan {
+  const int32_t* gid_count;  // per-gid tile-hit counts
+  int32_t* splat_offsets;    // written: exclusive offsets; [num_splats] = N
+                             // (-1 when N does not fit in int32)
+  uint64_t* status;          // look-back status per workgroup (zero before)
+  uint32_t* ticket;          // workgroup order (zero before)
+  uint32_t* err;             // give-up status word
+};
+
 // Pairs are written (and counted in the histograms) only at positions below
-// min(N, capacity), N = splat_offsets[num_splats]: with a capacity below N
-// the output is the first `capacity` pairs, consistently.
+// min(N, capacity): with a capacity below N the output is the first
+// `capacity` pairs, consistently.  kScan: the workgroups take tickets, scan
+// the per-gid counts with a decoupled look-back and write splat_offsets
+// before walking (the offsets, not N, bound the positions then: every pair
+// lies below N by construction).  Otherwise splat_offsets (and N in
+// splat_offsets[num_splats]) come from pack_kernel.
+template <bool kScan>
 __global__ __launch_bounds__(kThreads) void emit_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ splat_offsets, int64_t capacity,
     uint32_t* __restrict__ keys, uint32_t* __restrict__ vals, int pair_passes,
     uint32_t* __restrict__ hist_partials, uint32_t* ghist_direct,
-    uint32_t* pair_status,
-    int64_t pair_status_words) {
+    uint32_t* pair_status, int64_t pair_status_words, EmitScan sc) {
   __shared__ WalkSlots walk[kWaves];
   __shared__ int base[kWaves][kWalkSplats];
   __shared__ uint32_t h[4][256];
+  __shared__ int wsum[kWaves];
+  __shared__ long long s_prefix;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   // (1) zero the pair sort's look-back status (grid-stride)
   for (int64_t i = (int64_t)blockIdx.x * kThreads + t; i < pair_status_words;
        i += (int64_t)gridDim.x * kThreads)
     pair_status[i] = 0u;
   for (int i = t; i < 4 * 256; i += kThreads) (&h[0][0])[i] = 0u;
-  __syncthreads();
+  // (take_ticket synchronises the workgroup)
+  const int vb = kScan ? take_ticket(sc.ticket) : (int)blockIdx.x;
+  if (!kScan) __syncthreads();
   // (2) pair emission
-  const int gid = walk_splat_index();
+  const int gid = (vb * kWaves + wave) * kWalkSplats + lane;
   const bool valid = lane < kWalkSplats && gid < P.num_splats;
   const int g = valid ? gid : P.num_splats - 1;
   const float4 p0 = packed[3 * g + 0];
   const float4 p1 = packed[3 * g + 1];
   const SplatGeom s{p0.x, p0.y, p0.z, p0.w, p1.x, p1.y};
-  if (lane < kWalkSplats) base[wave][lane] = splat_offsets[g];
-  const int64_t n_eff =
-      min(capacity, (int64_t)max(splat_offsets[P.num_splats], 0));
   WalkSlots& W = walk[wave];
-  const int total = walk_setup(P, valid, s, g / P.gpb, W);
+  int64_t n_eff;
+  int total;
+  if (kScan) {
+    // exclusive offsets of the workgroup's gids: wavefront scans, then the
+    // workgroup's prefix by look-back (64-bit sums).  The workgroup's total
+    // is published first and the walk set up before the look-back waits,
+    // so that the wait overlaps the set-up.
+    const int n = valid ? sc.gid_count[gid] : 0;
+    int inc = n;
+#pragma unroll
+    for (int off = 1; off < kWalkSplats; off <<= 1) {
+      const int y = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += y;
+    }
+    if (lane == kWalkSplats - 1) wsum[wave] = inc;
+    __syncthreads();
+    long long pre = 0, wg_total = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      pre += (w < wave) ? wsum[w] : 0;
+      wg_total += wsum[w];
+    }
+    if (t == 0)
+      status_store(&sc.status[vb], (vb == 0 ? kFlagInc64 : kFlagAgg64) |
+                                       (uint64_t)wg_total);
+    total = walk_setup(P, valid, s, g / P.gpb, W);
+    if (wave == 0) {
+      uint64_t prefix = 0;
+      if (vb > 0) {
+        prefix = lookback64_wave(sc.status, vb, sc.err);
+        if (lane == 0)
+          status_store(&sc.status[vb],
+                       kFlagInc64 | (prefix + (uint64_t)wg_total));
+      }
+      if (lane == 0) s_prefix = (long long)prefix;
+    }
+    __syncthreads();
+    const long long end = s_prefix + pre + inc;
+    if (valid) {
+      sc.splat_offsets[gid] = (int)(end - n);
+      // positions at or above the capacity are not written: clamp there
+      base[wave][lane] = (int)min((long long)capacity, end - n);
+    }
+    // (lanes 32..63 alias the next wavefront's gids: only a valid lane
+    // writes)
+    if (valid && gid == P.num_splats - 1)
+      sc.splat_offsets[P.num_splats] = end > 0x7fffffffLL ? -1 : (int)end;
+    n_eff = capacity;
+  } else {
+    if (lane < kWalkSplats) base[wave][lane] = splat_offsets[g];
+    n_eff = min(capacity, (int64_t)max(splat_offsets[P.num_splats], 0));
+    total = walk_setup(P, valid, s, g / P.gpb, W);
+  }
   const int gid0 = gid - lane;
   walk_candidates(P, W, total, [&](int sl, int tile) {
     const int slot = atomicAdd(&W.cnt[sl], 1);
@@ -644,6 +744,27 @@ int launch_count_depth_runs(const RasterParams& P, const float* means2d,
   return check_launch("count_depth_runs_kernel");
 }
 
+int launch_rank_pack(const RasterParams& P, const float* means2d,
+                     const float* conics, const float* colors,
+                     const float* opacities, void* depth_buffers,
+                     const int32_t* splat_count, int32_t* perm, float* packed,
+                     int32_t* gid_count, hipStream_t stream) {
+  if (P.num_splats == 0 || !depth_small_ok(P.gpb)) {
+    set_error("rank + pack: needs 1..131072 splats per image");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  const int blocks_per_seg =
+      (P.gpb + run_step::kRankElems - 1) / run_step::kRankElems;
+  hipLaunchKernelGGL(rank_pack_kernel,
+                     dim3((unsigned)((int64_t)P.batch * blocks_per_seg)),
+                     dim3(run_step::kRankBlock), 0, stream, P, means2d, conics,
+                     colors, opacities,
+                     run_step::run_buffers(depth_buffers, P.gpb, P.batch),
+                     run_step::runs_of(P.gpb), splat_count, perm,
+                     reinterpret_cast<float4*>(packed), gid_count);
+  return check_launch("rank_pack_kernel");
+}
+
 int launch_pack(const RasterParams& P, const float* means2d,
                 const float* conics, const float* colors,
                 const float* opacities, const uint32_t* perm,
@@ -671,17 +792,29 @@ int launch_emit(const RasterParams& P, const float* packed,
                 const int32_t* splat_offsets, int64_t capacity, uint32_t* keys,
                 uint32_t* vals, int pair_passes, uint32_t* hist_partials,
                 uint32_t* pair_ghist, uint32_t* pair_status,
-                int64_t pair_status_words, hipStream_t stream) {
+                int64_t pair_status_words, hipStream_t stream,
+                const EmitScanArgs* scan) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const int nblk = emit_blocks(P);
   // Few workgroups add their histograms atomically (pair_ghist is zeroed
   // by count_kernel), which saves the reduction launch; many would contend.
   const bool direct = nblk <= kDirectHistBlocks;
-  hipLaunchKernelGGL(emit_kernel, dim3((unsigned)nblk), dim3(kThreads), 0,
-                     stream, P, reinterpret_cast<const float4*>(packed),
-                     splat_offsets, capacity, keys, vals, pair_passes,
-                     hist_partials, direct ? pair_ghist : nullptr,
-                     pair_status, pair_status_words);
+  if (scan != nullptr) {
+    const EmitScan sc{scan->gid_count, scan->splat_offsets, scan->status,
+                      scan->ticket, scan->err};
+    hipLaunchKernelGGL(emit_kernel<true>, dim3((unsigned)nblk), dim3(kThreads),
+                       0, stream, P, reinterpret_cast<const float4*>(packed),
+                       nullptr, capacity, keys, vals, pair_passes,
+                       hist_partials, direct ? pair_ghist : nullptr,
+                       pair_status, pair_status_words, sc);
+  } else {
+    hipLaunchKernelGGL(emit_kernel<false>, dim3((unsigned)nblk),
+                       dim3(kThreads), 0, stream, P,
+                       reinterpret_cast<const float4*>(packed), splat_offsets,
+                       capacity, keys, vals, pair_passes, hist_partials,
+                       direct ? pair_ghist : nullptr, pair_status,
+                       pair_status_words, EmitScan{});
+  }
   int rc = check_launch("emit_kernel");
   if (rc || pair_passes == 0 || direct) return rc;
   hipLaunchKernelGGL(hist_reduce_kernel, dim3((unsigned)(pair_passes * 256)),

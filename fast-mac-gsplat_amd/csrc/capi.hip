@@ -137,15 +137,17 @@ int null_check(std::initializer_list<const void*> ptrs, const char* what) {
 struct CountLayout {
   gs::RadixPlan depth;
   size_t scan_status, scan_ticket, pair_ghist, pair_tickets, ctl_end;
-  size_t splat_count, block_sums, depth_buffers, total;
+  size_t splat_count, block_sums, gid_count, depth_buffers, total;
 };
 
 CountLayout count_layout(const RasterParams& P) {
   CountLayout L{};
   L.depth = gs::radix_plan(P.gpb, P.batch, 0, 32);
   size_t off = gs::radix_ctl_bytes(L.depth);
-  L.scan_status = off;
-  off += gs::align_up((size_t)gs::count_scan_blocks(P) * sizeof(uint64_t), 256);
+  L.scan_status = off;  // the pack scan's, or the emit scan's in gsplat_hip_bin
+  off += gs::align_up((size_t)std::max(gs::count_scan_blocks(P), gs::emit_blocks(P)) *
+                          sizeof(uint64_t),
+                      256);
   L.scan_ticket = off;
   off += 256;
   L.pair_ghist = off;
@@ -157,6 +159,8 @@ CountLayout count_layout(const RasterParams& P) {
   off += gs::align_up((size_t)P.num_splats * sizeof(int32_t), 256);
   L.block_sums = off;
   off += gs::align_up((size_t)gs::count_blocks(P) * sizeof(int32_t), 256);
+  L.gid_count = off;  // per-gid counts of gsplat_hip_bin's small-image path
+  off += gs::align_up((size_t)P.num_splats * sizeof(int32_t), 256);
   L.depth_buffers = off;
   size_t depth_bytes = L.depth.buffer_bytes;
   if (gs::depth_small_ok(P.gpb))
@@ -329,7 +333,8 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
                   void* count_workspace, size_t count_workspace_bytes,
                   void* workspace, size_t workspace_bytes, void* stream,
                   int32_t* host_words, bool* host_written,
-                  const gs::ZeroSpan* zero = nullptr) {
+                  const gs::ZeroSpan* zero = nullptr,
+                  const gs::EmitScanArgs* scan = nullptr) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -385,7 +390,7 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
   rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals,
                        L.pairs.passes,
                        reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
-                       ctl.status, L.pairs.status_words, s);
+                       ctl.status, L.pairs.status_words, s, scan);
   // 2. stable sort by tile
   if (!rc)
     rc = gs::radix_passes(L.pairs, ctl, base + L.buffers, keys, vals, nullptr,
@@ -476,11 +481,12 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
   hipEvent_t ev_st = static_cast<hipEvent_t>(status_event);
   // Images of at most 131072 splats whose N goes to host_words: the count
   // and the run step of the depth order share one launch on `stream` (the
-  // run step leaves most CUs idle), and N is read off the pack scan's total
-  // by the tile-range launch, so the count stream, its events and the sum of
-  // the count workgroups are not used.
-  if (host_words != nullptr && P.num_tiles > 0 && P.num_splats > 0 &&
-      gs::depth_small_ok(P.gpb)) {
+  // run step leaves most CUs idle), the rank step packs the records, and the
+  // emit scans the pair offsets and writes N, which the tile-range launch
+  // reports; the count stream, its events and the sum of the count
+  // workgroups are not used.
+  if (host_words != nullptr && capacity > 0 && P.num_tiles > 0 &&
+      P.num_splats > 0 && gs::depth_small_ok(P.gpb)) {
     const CountLayout C = count_layout(P);
     char* cb = static_cast<char*>(cws);
     const size_t z0 = gs::radix_ctl_bytes(C.depth);
@@ -490,17 +496,24 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
         reinterpret_cast<uint32_t*>(cb + z0),
         (int64_t)((C.ctl_end - z0) / sizeof(uint32_t)), depths,
         cb + C.depth_buffers, s);
+    // ranks with the records packed at them, then the emit scans the pair
+    // offsets itself (the pack launch's look-back words serve it)
+    int32_t* gid_count = reinterpret_cast<int32_t*>(cb + C.gid_count);
     if (!rc)
-      rc = gs::launch_depth_ranks_small(cb + C.depth_buffers, perm, P.gpb,
-                                        P.batch, s);
-    if (!rc)
-      rc = gsplat_hip_bin_pack(meta, means2d, conics, colors, opacities, perm,
-                               packed, splat_offsets, cws, cbytes, s);
+      rc = gs::launch_rank_pack(
+          P, means2d, conics, colors, opacities, cb + C.depth_buffers,
+          reinterpret_cast<const int32_t*>(cb + C.splat_count), perm, packed,
+          gid_count, s);
+    const gs::EmitScanArgs scan{
+        gid_count, splat_offsets,
+        reinterpret_cast<uint64_t*>(cb + C.scan_status),
+        reinterpret_cast<uint32_t*>(cb + C.scan_ticket),
+        reinterpret_cast<uint32_t*>(cb + C.scan_ticket) + 1};
     bool written = false;
     if (!rc)
       rc = bin_emit_impl(meta, packed, splat_offsets, capacity, binned_ids,
                          nullptr, tile_offsets, status_dev, cws, cbytes, ews,
-                         ebytes, s, host_words, &written, zero);
+                         ebytes, s, host_words, &written, zero, &scan);
     if (!rc && !written) {
       gs::set_error("gsplat_hip_bin: the tile ranges did not report N");
       rc = GSPLAT_ERR_INVALID_ARGUMENT;

@@ -169,5 +169,169 @@ __device__ __forceinline__ void run_sort_block(const float* __restrict__ depths,
   }
 }
 
+// Whether a key x of another run precedes key k in the stable order: keys
+// of earlier runs precede when x <= k (below_or_equal), of later runs when
+// x < k.
+__device__ __forceinline__ bool precedes(uint32_t x, uint32_t k,
+                                         bool below_or_equal) {
+  return below_or_equal ? (x <= k) : (x < k);
+}
+
+// Number of the first n keys of the sorted array a[] (n <= 2^kLog2) that
+// precede k: they form a prefix, found by binary search.
+template <int kLog2, class Load>
+__device__ __forceinline__ int prefix_count(Load a, int n, uint32_t k,
+                                            bool below_or_equal) {
+  int c = 0;
+#pragma unroll
+  for (int step = 1 << kLog2; step > 0; step >>= 1)
+    if (c + step <= n && precedes(a(c + step - 1), k, below_or_equal))
+      c += step;
+  return c;
+}
+
+// Rank kernel: a workgroup takes 256 consecutive elements of one sorted run,
+// four threads per element (thread t: element t % 256, run group t / 256).
+// The element's counts in another run o all lie in a window [L, U) of o that
+// the run's samples bound: L from the samples that precede the chunk's first
+// key, U from those that precede its last key (the chunk's keys ascend).
+// The workgroup loads the other runs' windows into LDS in coalesced reads
+// (kWinKeys keys at most, about 256 + 128 for runs of like key
+// distributions; kLdsRuns runs at a time) and each thread finds its
+// element's counts in its runs (o = group + 4 v) by binary searches there
+// that advance together; a window longer than kWinKeys is searched in global
+// memory.  The four partial ranks are added in LDS.
+constexpr int kRankElems = 256;                  // elements per workgroup
+constexpr int kRankSplit = 4;                    // threads per element
+constexpr int kRankBlock = kRankElems * kRankSplit;
+constexpr int kWinKeys = 512;
+constexpr int kLdsRuns = 16;  // runs whose windows the LDS holds at once
+constexpr int kRunsPerThread = kLdsRuns / kRankSplit;
+constexpr int kLoadsPerThread = kLdsRuns * kWinKeys / kRankBlock;
+static_assert(kRunItems % kRankElems == 0, "a rank workgroup lies in one run");
+static_assert(kMaxRuns % kLdsRuns == 0, "run groups");
+
+struct RankLds {
+  uint32_t ss[kMaxRuns * kRunSamples];
+  int wlo[kMaxRuns], wlen[kMaxRuns];
+  uint32_t kfl[2];
+  uint32_t win[kLdsRuns * kWinKeys];
+  int part[kRankSplit][kRankElems];
+};
+
+// Rank step of workgroup `block` (kRankBlock threads): on_rank(base, pos, v)
+// is called once per element, by a thread of group 0, with the image's
+// first index base, the element's position pos in the image's stable order
+// and its in-image index v.
+template <class OnRank>
+__device__ __forceinline__ void rank_block(
+    const uint32_t* __restrict__ run_keys,
+    const uint32_t* __restrict__ run_vals,
+    const uint32_t* __restrict__ samples, int G, int runs, int block,
+    RankLds& S, OnRank&& on_rank) {
+  uint32_t* ss = S.ss;
+  int* wlo = S.wlo;
+  int* wlen = S.wlen;
+  uint32_t* kfl = S.kfl;
+  uint32_t* win = S.win;
+  auto& part = S.part;
+  const int t = threadIdx.x;
+  const int el = t % kRankElems, grp = t / kRankElems;
+  const int blocks_per_seg = (G + kRankElems - 1) / kRankElems;
+  const int seg = block / blocks_per_seg;
+  const int e0 = (block - seg * blocks_per_seg) * kRankElems;
+  const int e = e0 + el;
+  const int64_t base = (int64_t)seg * G;
+  const int r = e0 / kRunItems;  // the chunk's run
+  for (int i = t; i < runs * kRunSamples; i += kRankBlock)
+    ss[i] = samples[(int64_t)seg * runs * kRunSamples + i];
+  const int ec = min(e, G - 1);
+  const uint32_t key = run_keys[base + ec];
+  if (t == 0) kfl[0] = key;
+  if (grp == 0 && e == min(e0 + kRankElems, G) - 1) kfl[1] = key;
+  __syncthreads();
+  if (t < runs) {
+    const int o = t;
+    int L = 0, U = 0;
+    if (o != r) {
+      const int len = min(kRunItems, G - o * kRunItems);
+      const int ns = (len + kSampleStride - 1) / kSampleStride;
+      const bool le = o < r;
+      const uint32_t* so = ss + o * kRunSamples;
+      auto ld = [so](int i) { return so[i]; };
+      const int wf = prefix_count<6>(ld, ns, kfl[0], le);
+      const int wl = prefix_count<6>(ld, ns, kfl[1], le);
+      L = wf == 0 ? 0 : kSampleStride * (wf - 1) + 1;
+      U = wl == 0 ? 0 : min(kSampleStride * wl, len);
+      U = max(U, L);
+    }
+    wlo[o] = L;
+    wlen[o] = U - L;
+  }
+  __syncthreads();
+  int rank = grp == 0 ? e - r * kRunItems : 0;
+  for (int l0 = 0; l0 < runs; l0 += kLdsRuns) {
+    if (l0 > 0) __syncthreads();  // searches of the previous runs done
+    // Windows of runs l0 .. l0 + kLdsRuns - 1 into LDS: every load in
+    // flight before the first store (loads at clamped, in-run positions).
+    uint32_t x[kLoadsPerThread];
+#pragma unroll
+    for (int k = 0; k < kLoadsPerThread; ++k) {
+      const int f = t + kRankBlock * k;
+      const int o = min(l0 + f / kWinKeys, runs - 1);
+      const int len = min(kRunItems, G - o * kRunItems);
+      const int n = min(wlen[o], kWinKeys);
+      const int i = min(f % kWinKeys, max(n - 1, 0));
+      x[k] = run_keys[base + (int64_t)o * kRunItems + min(wlo[o] + i, len - 1)];
+    }
+#pragma unroll
+    for (int k = 0; k < kLoadsPerThread; ++k) {
+      const int f = t + kRankBlock * k;
+      const int o = l0 + f / kWinKeys;
+      if (o < runs && f % kWinKeys < min(wlen[o], kWinKeys)) win[f] = x[k];
+    }
+    __syncthreads();
+    // This thread's runs o = l0 + grp + kRankSplit v: binary searches that
+    // advance together (n = 0 for runs not searched here).
+    int c[kRunsPerThread], n[kRunsPerThread];
+#pragma unroll
+    for (int v = 0; v < kRunsPerThread; ++v) {
+      const int o = l0 + grp + kRankSplit * v;
+      c[v] = 0;
+      n[v] = (o < runs && o != r && wlen[o] <= kWinKeys) ? wlen[o] : 0;
+    }
+#pragma unroll
+    for (int step = kWinKeys; step > 0; step >>= 1) {
+#pragma unroll
+      for (int v = 0; v < kRunsPerThread; ++v) {
+        const int u = grp + kRankSplit * v;  // run l0 + u
+        const uint32_t x =
+            win[u * kWinKeys + min(c[v] + step - 1, kWinKeys - 1)];
+        if (c[v] + step <= n[v] && precedes(x, key, l0 + u < r)) c[v] += step;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < kRunsPerThread; ++v) {
+      const int o = l0 + grp + kRankSplit * v;
+      if (o < runs && o != r) {
+        if (wlen[o] > kWinKeys) {  // rare: the window is searched in place
+          const uint32_t* w =
+              run_keys + base + (int64_t)o * kRunItems + wlo[o];
+          c[v] = prefix_count<12>([w](int i) { return w[i]; }, wlen[o], key,
+                                  o < r);
+        }
+        rank += wlo[o] + c[v];
+      }
+    }
+  }
+  part[grp][el] = rank;
+  __syncthreads();
+  if (grp == 0 && e < G) {
+    const int pos = part[0][el] + part[1][el] + part[2][el] + part[3][el];
+    on_rank(base, pos, run_vals[base + e]);
+  }
+}
+
+
 }  // namespace run_step
 }  // namespace gs

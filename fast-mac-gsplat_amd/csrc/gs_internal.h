@@ -153,11 +153,31 @@ int count_scan_blocks(const RasterParams& P);
 // (emit_blocks(P) * 4 * 256 words) and a reduction launch.  Only the first min(N, capacity) pairs are written and counted,
 // N = splat_offsets[num_splats] (-1 when N overflowed: nothing is written).
 int emit_blocks(const RasterParams& P);
+// With scan, the emit scans the per-gid counts itself (decoupled look-back,
+// status words emit_blocks(P) and ticket zero before the launch) and writes
+// splat_offsets[0..BG] there; splat_offsets is then not read.
+struct EmitScanArgs {
+  const int32_t* gid_count;
+  int32_t* splat_offsets;
+  uint64_t* status;
+  uint32_t* ticket;
+  uint32_t* err;
+};
 int launch_emit(const RasterParams& P, const float* packed,
                 const int32_t* splat_offsets, int64_t capacity, uint32_t* keys,
                 uint32_t* vals, int pair_passes, uint32_t* hist_partials,
                 uint32_t* pair_ghist, uint32_t* pair_status,
-                int64_t pair_status_words, hipStream_t stream);
+                int64_t pair_status_words, hipStream_t stream,
+                const EmitScanArgs* scan = nullptr);
+// rank_pack: the second launch of the small-image depth order (runs in
+// depth_buffers, as launch_count_depth_runs leaves them) with the records
+// packed at the ranks: perm, packed and gid_count[gid] = splat_count[orig]
+// (the pair offsets then come from launch_emit with scan).
+int launch_rank_pack(const RasterParams& P, const float* means2d,
+                     const float* conics, const float* colors,
+                     const float* opacities, void* depth_buffers,
+                     const int32_t* splat_count, int32_t* perm, float* packed,
+                     int32_t* gid_count, hipStream_t stream);
 // Tile ranges longer than this many pairs are walked by the forward's first
 // launch only up to here and continued by its second (render_fwd_long).
 constexpr int kHandoffPairs = GSPLAT_HANDOFF_PAIRS;
