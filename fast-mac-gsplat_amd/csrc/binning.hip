@@ -63,7 +63,6 @@ struct WalkSlots {
   int flags[kWalkSplats];  // bit 0: use_c, bit 1: use_a
   int cend[kWalkSplats];   // inclusive prefix sum of candidate counts
   int first[kWalkSplats];  // exclusive prefix sum: the splat's first candidate
-  int cnt[kWalkSplats];    // hits found so far
   uint32_t own[64];        // per walk step: splats starting at each position
 };
 
@@ -147,7 +146,6 @@ __device__ __forceinline__ int walk_setup(const RasterParams& P, bool valid,
     W.g1[lane] = g1;
     W.box[lane] = box;
     W.flags[lane] = flags;
-    W.cnt[lane] = 0;
     W.cend[lane] = inc;
     W.first[lane] = inc - ncand;
   }
@@ -163,10 +161,18 @@ __device__ __forceinline__ int walk_setup(const RasterParams& P, bool valid,
 // counted with a ballot, the splats that start inside the step mark their
 // position with an LDS max, and a prefix maximum over the lanes spreads the
 // marks -- one LDS round trip per step instead of a binary search.
+//
+// on_step(hm, hit, sl, tile, c0) is called by every lane once per step, hm
+// being the step's ballot of hits (hit, sl and tile: this lane's
+// candidate's; sl and tile mean nothing without the hit).  Candidates are enumerated splat by
+// splat, so the wavefront's hits arrive in splat order: the hits before a
+// position are counted with one running total and a lane-masked popcount,
+// without per-splat counters (whose atomics would serialise the lanes of one
+// splat on one LDS address).
 template <typename Fn>
 __device__ __forceinline__ void walk_candidates(const RasterParams& P,
                                                 WalkSlots& W, int total,
-                                                Fn&& on_hit) {
+                                                Fn&& on_step) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int first = lane < kWalkSplats ? W.first[lane] : 0x7fffffff;
@@ -182,6 +188,8 @@ __device__ __forceinline__ void walk_candidates(const RasterParams& P,
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int sl = (int)wave_prefix_max(W.own[lane]);
     const int c = c0 + lane;
+    bool hit = false;
+    int tile = 0;
     if (c < total) {
       const int k = c - W.first[sl];
       const int4 bx = W.box[sl];
@@ -196,11 +204,17 @@ __device__ __forceinline__ void walk_candidates(const RasterParams& P,
       ks.use_a = (fl & 2) != 0;
       float rx0, ry0, rx1, ry1;
       tile_rect(tx, ty, P.width, P.height, rx0, ry0, rx1, ry1);
-      if (ellipse_hits_rect(g0.x, g0.y, g0.z, g0.w, g1.x, ks, g1.y, rx0, ry0,
-                            rx1, ry1))
-        on_hit(sl, bx.w + ty * P.tiles_x + tx);
+      hit = ellipse_hits_rect(g0.x, g0.y, g0.z, g0.w, g1.x, ks, g1.y, rx0, ry0,
+                              rx1, ry1);
+      tile = bx.w + ty * P.tiles_x + tx;
     }
+    on_step(__ballot(hit), hit, sl, tile, c0);
   }
+}
+
+// Hits among the lanes below `rel` of a step's hit ballot hm (rel in 0..64).
+__device__ __forceinline__ int hits_below(uint64_t hm, int rel) {
+  return __popcll(rel >= 64 ? hm : (hm & ((1ull << rel) - 1ull)));
 }
 
 // LDS of a count block of kW wavefronts.
@@ -237,9 +251,19 @@ __device__ __forceinline__ void count_block(
   s.o = opacities[o];
   WalkSlots& W = S.walk[wave];
   const int total = walk_setup(P, valid, s, o / P.gpb, W);
-  walk_candidates(P, W, total, [&](int sl, int) { atomicAdd(&W.cnt[sl], 1); });
-  __builtin_amdgcn_wave_barrier();
-  const int n = valid ? W.cnt[lane] : 0;
+  // Hits before the end of this lane's splat's candidates (lanes below
+  // kWalkSplats): the running total of the steps before plus the hits below
+  // the end inside its step; a splat's count is the difference to the
+  // previous lane's.
+  const int my_end = lane < kWalkSplats ? W.cend[lane] : 0;
+  int run = 0, hits_to_end = 0;
+  walk_candidates(P, W, total, [&](uint64_t hm, bool, int, int, int c0) {
+    const int rel = my_end - c0;
+    if (rel > 0 && rel <= 64) hits_to_end = run + hits_below(hm, rel);
+    run += __popcll(hm);
+  });
+  const int prev_end = __shfl_up(hits_to_end, 1, 64);
+  const int n = valid ? hits_to_end - (lane == 0 ? 0 : prev_end) : 0;
   if (valid) splat_count[orig] = n;
   if (block_sums == nullptr) return;
   int v = n;
@@ -527,10 +551,16 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
     total = walk_setup(P, valid, s, g / P.gpb, W);
   }
   const int gid0 = gid - lane;
-  walk_candidates(P, W, total, [&](int sl, int tile) {
-    const int slot = atomicAdd(&W.cnt[sl], 1);
-    const int64_t pos = (int64_t)base[wave][sl] + slot;
-    if (pos < n_eff) {  // pos >= 0 whenever n_eff > 0
+  // The wavefront's splats own consecutive ranges starting at the first
+  // one's offset and its hits arrive in splat order: a hit's position is
+  // that offset plus the hits before it (running total + lanes below).
+  const int64_t wave_base = base[wave][0];
+  int64_t run = 0;
+  walk_candidates(P, W, total, [&](uint64_t hm, bool hit, int sl, int tile,
+                                   int) {
+    const int64_t pos = wave_base + run + hits_below(hm, lane);
+    run += __popcll(hm);
+    if (hit && pos < n_eff) {  // pos >= 0 whenever n_eff > 0
       keys[pos] = (uint32_t)tile;
       vals[pos] = (uint32_t)(gid0 + sl);
       for (int p = 0; p < pair_passes; ++p)
