@@ -54,6 +54,8 @@ constexpr int kWalkBlockSplats = kWaves * kWalkSplats;
 // Emit launches with at most this many workgroups add their pair-sort
 // histograms atomically instead of through hist_reduce_kernel.
 constexpr int kDirectHistBlocks = 1024;
+// Copies of the emit's digit histograms (see emit_kernel).
+constexpr int kHistCopies = 4;
 
 // One wavefront's kWalkSplats splats, staged for the cooperative tile walk.
 struct WalkSlots {
@@ -477,7 +479,11 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
     uint32_t* pair_status, int64_t pair_status_words, EmitScan sc) {
   __shared__ WalkSlots walk[kWaves];
   __shared__ int base[kWaves][kWalkSplats];
-  __shared__ uint32_t h[4][256];
+  // the pair sort's digit histograms in kHistCopies copies (lane l adds to
+  // copy l % kHistCopies; rows 257 words apart, so that one digit's copies
+  // lie in different LDS banks): hits of one tile row share the row's
+  // digit, and a copy per lane group divides their serialisation
+  __shared__ uint32_t h[4][kHistCopies][257];
   __shared__ int wsum[kWaves];
   __shared__ long long s_prefix;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -485,7 +491,7 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
   for (int64_t i = (int64_t)blockIdx.x * kThreads + t; i < pair_status_words;
        i += (int64_t)gridDim.x * kThreads)
     pair_status[i] = 0u;
-  for (int i = t; i < 4 * 256; i += kThreads) (&h[0][0])[i] = 0u;
+  for (int i = t; i < 4 * kHistCopies * 257; i += kThreads) (&h[0][0][0])[i] = 0u;
   // (take_ticket synchronises the workgroup)
   const int vb = kScan ? take_ticket(sc.ticket) : (int)blockIdx.x;
   if (!kScan) __syncthreads();
@@ -564,7 +570,8 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
       keys[pos] = (uint32_t)tile;
       vals[pos] = (uint32_t)(gid0 + sl);
       for (int p = 0; p < pair_passes; ++p)
-        atomicAdd(&h[p][((uint32_t)tile >> (8 * p)) & 255u], 1u);
+        atomicAdd(&h[p][lane % kHistCopies][((uint32_t)tile >> (8 * p)) & 255u],
+                  1u);
     }
   });
   // (3) this workgroup's digit histograms for the pair sort: added to the
@@ -572,7 +579,9 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
   // hist_partials[(p * 256 + d) * nblk + workgroup] for hist_reduce_kernel
   __syncthreads();
   for (int p = 0; p < pair_passes; ++p) {
-    const uint32_t c = h[p][t];
+    uint32_t c = 0u;
+#pragma unroll
+    for (int q = 0; q < kHistCopies; ++q) c += h[p][q][t];
     if (ghist_direct != nullptr) {
       if (c) atomicAdd(&ghist_direct[p * 256 + t], c);
     } else {
