@@ -632,10 +632,9 @@ constexpr int kRangeMaxBlocks = 2048;
 struct StatusWords {
   const uint32_t* err[3];  // give-up status words (null: not used)
   int32_t* out;            // their OR (null: not reported)
-  int32_t* host;           // null, or pinned host words that receive
-                           // {N (-1 on overflow), the OR} directly, and
-                           // host[2] = 1 if a tile range is longer than
-                           // kHandoffPairs (left alone otherwise)
+  int32_t* long_flag;      // null, or a device word (zero before the
+                           // launch) set to 1 if a tile range is longer
+                           // than kHandoffPairs
   ZeroSpan zero[2];        // zeroed by the launch on the side
 };
 
@@ -650,13 +649,8 @@ __global__ __launch_bounds__(kThreads) void ranges_kernel(
 #pragma unroll
   for (int k = 0; k < 3; ++k)
     if (sw.err[k] != nullptr) e |= *sw.err[k];
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    if (sw.out != nullptr) *sw.out = (int32_t)e;
-    if (sw.host != nullptr) {
-      sw.host[0] = n_dev ? *n_dev : (int32_t)n_cap;
-      sw.host[1] = (int32_t)e;
-    }
-  }
+  if (blockIdx.x == 0 && threadIdx.x == 0 && sw.out != nullptr)
+    *sw.out = (int32_t)e;
   const int64_t stride = (int64_t)gridDim.x * kThreads;
 #pragma unroll
   for (int z = 0; z < 2; ++z)
@@ -690,13 +684,17 @@ __global__ __launch_bounds__(kThreads) void ranges_kernel(
       for (int64_t t = prev + 1; t <= cur; ++t) tile_offsets[t] = (int32_t)i;
       // tile cur's range starts at i: longer than kHandoffPairs iff its
       // key is still there kHandoffPairs places on
-      if (sw.host != nullptr && prev != cur && i + kHandoffPairs < n)
+      if (sw.long_flag != nullptr && prev != cur && i + kHandoffPairs < n)
         long_range |= sorted_keys[i + kHandoffPairs] == kc[u];
     }
   }
-  if (sw.host != nullptr && __ballot(long_range) != 0ull &&
+  if (sw.long_flag != nullptr && __ballot(long_range) != 0ull &&
       (threadIdx.x & 63) == 0)
-    sw.host[2] = 1;
+    *sw.long_flag = 1;
+}
+
+__global__ void host_report_kernel(HostReport R) {
+  if (threadIdx.x == 0) write_host_report(R);
 }
 
 __global__ __launch_bounds__(kThreads) void counts_kernel(
@@ -867,14 +865,14 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        hipStream_t stream, const int32_t* n_dev,
                        const uint32_t* err0, const uint32_t* err1,
                        const uint32_t* err2, int32_t* status_out,
-                       int32_t* host_words, const ZeroSpan* zero) {
+                       int32_t* long_flag, const ZeroSpan* zero) {
   int rc = GSPLAT_OK;
   if (zero != nullptr && (num_tiles <= 0 || n == 0))
     rc = launch_zero2(zero[0].p, zero[0].n, zero[1].p, zero[1].n, stream);
   if (rc) return rc;
   if (num_tiles <= 0)
     return status_out ? launch_fill_i32(status_out, 0, 1, stream) : GSPLAT_OK;
-  StatusWords sw{{err0, err1, err2}, status_out, host_words, {}};
+  StatusWords sw{{err0, err1, err2}, status_out, long_flag, {}};
   if (zero != nullptr) {
     sw.zero[0] = zero[0];
     sw.zero[1] = zero[1];
@@ -896,6 +894,11 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                      dim3(kThreads), 0, stream, tile_offsets, num_tiles,
                      tile_counts);
   return check_launch("counts_kernel");
+}
+
+int launch_host_report(const HostReport& R, hipStream_t stream) {
+  hipLaunchKernelGGL(host_report_kernel, dim3(1), dim3(64), 0, stream, R);
+  return check_launch("host_report_kernel");
 }
 
 int launch_zero2(uint32_t* a, int64_t na, uint32_t* b, int64_t nb,

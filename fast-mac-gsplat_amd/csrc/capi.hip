@@ -323,17 +323,16 @@ size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
 }  // extern "C"
 
 namespace {
-// bin_emit; with host_words (device-mapped pinned host memory) the tile
-// range launch also writes {N, status} there, which it reports as true
-// through *host_written (false: the caller copies them).
+// bin_emit; with long_flag (a device word that is zero before the call) the
+// tile range launch sets it to 1 if a tile range is longer than
+// kHandoffPairs.
 int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
                   const int32_t* splat_offsets, int64_t n_pairs,
                   int32_t* binned_ids, int32_t* tile_counts,
                   int32_t* tile_offsets, int32_t* status,
                   void* count_workspace, size_t count_workspace_bytes,
                   void* workspace, size_t workspace_bytes, void* stream,
-                  int32_t* host_words, bool* host_written,
-                  const gs::ZeroSpan* zero = nullptr,
+                  int32_t* long_flag, const gs::ZeroSpan* zero = nullptr,
                   const gs::EmitScanArgs* scan = nullptr) {
   RasterParams P;
   int rc = make_params(meta, P);
@@ -400,10 +399,8 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
   if (!rc)
     rc = gs::launch_tile_ranges(sorted_keys, n_pairs, P.num_tiles,
                                 tile_offsets, tile_counts, s, n_dev, err_pack,
-                                err_pairs, err_depth, status, host_words,
+                                err_pairs, err_depth, status, long_flag,
                                 zero);
-  if (!rc && host_written != nullptr)
-    *host_written = host_words != nullptr && P.num_tiles > 0;
   return rc;
 }
 }  // namespace
@@ -436,6 +433,9 @@ size_t gsplat_hip_bin_workspace_bytes(const gsplat_raster_meta* meta,
 namespace {
 // gsplat_hip_bin; zero (may be null): two spans that the tile-range launch
 // zeroes on the side (or a launch of their own where it does not run).
+// With report_out the report of host_words is left to the caller's next
+// launch (*report_out says what to copy) and status_event is not recorded;
+// otherwise a launch of its own writes it.
 int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
              const float* conics, const float* colors, const float* opacities,
              const float* depths, int64_t capacity, int32_t* perm,
@@ -443,7 +443,7 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
              int32_t* tile_offsets, int32_t* host_words, void* workspace,
              size_t workspace_bytes, void* stream, void* count_stream,
              void* inputs_event, void* count_event, void* status_event,
-             const gs::ZeroSpan* zero) {
+             const gs::ZeroSpan* zero, gs::HostReport* report_out) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -468,17 +468,35 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
                   workspace_bytes, need);
     return GSPLAT_ERR_WORKSPACE;
   }
-  // host_words[2] is set by the tile-range launch if a range is long
-  if (host_words != nullptr) host_words[2] = 0;
+  // host_words[3] turns 1 once host_words[0..2] hold the report
+  if (host_words != nullptr) host_words[3] = 0;
   char* base = static_cast<char*>(workspace);
   int32_t* n_dev = reinterpret_cast<int32_t*>(base);
   int32_t* status_dev = n_dev + 1;
   void* cws = base + 256;
+  // the long-range flag: a control word of the count workspace, zeroed by
+  // the count launch like the pair sort's tickets
+  int32_t* long_dev = reinterpret_cast<int32_t*>(
+                          static_cast<char*>(cws) + count_layout(P).pair_tickets) +
+                      8;
+  // the report of host_words, after the tile ranges
+  auto report = [&](const int32_t* n_src) -> int {
+    const gs::HostReport R{n_src, status_dev, long_dev, host_words};
+    int r = GSPLAT_OK;
+    if (report_out != nullptr) {
+      *report_out = R;
+      return r;
+    }
+    r = gs::launch_host_report(R, s);
+    if (!r && status_event != nullptr)
+      r = hip_status(hipEventRecord(static_cast<hipEvent_t>(status_event), s),
+                     "gsplat_hip_bin: event record");
+    return r;
+  };
   void* ews = base + 256 + cbytes;
   const size_t ebytes = workspace_bytes - 256 - cbytes;
   hipEvent_t ev_in = static_cast<hipEvent_t>(inputs_event);
   hipEvent_t ev_n = static_cast<hipEvent_t>(count_event);
-  hipEvent_t ev_st = static_cast<hipEvent_t>(status_event);
   // Images of at most 131072 splats whose N goes to host_words: the count
   // and the run step of the depth order share one launch on `stream` (the
   // run step leaves most CUs idle), the rank step packs the records, and the
@@ -509,18 +527,12 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
         reinterpret_cast<uint64_t*>(cb + C.scan_status),
         reinterpret_cast<uint32_t*>(cb + C.scan_ticket),
         reinterpret_cast<uint32_t*>(cb + C.scan_ticket) + 1};
-    bool written = false;
     if (!rc)
       rc = bin_emit_impl(meta, packed, splat_offsets, capacity, binned_ids,
                          nullptr, tile_offsets, status_dev, cws, cbytes, ews,
-                         ebytes, s, host_words, &written, zero, &scan);
-    if (!rc && !written) {
-      gs::set_error("gsplat_hip_bin: the tile ranges did not report N");
-      rc = GSPLAT_ERR_INVALID_ARGUMENT;
-    }
-    if (!rc && ev_st != nullptr)
-      rc = hip_status(hipEventRecord(ev_st, s), "gsplat_hip_bin: event record");
-    return rc;
+                         ebytes, s, long_dev, zero, &scan);
+    // N is written by the emit's scan
+    return rc ? rc : report(splat_offsets + P.num_splats);
   }
   // 1. per-splat hit counts and N on the count stream (after the caller's
   //    work on `stream`)
@@ -549,20 +561,13 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
   rc = gsplat_hip_bin_pack(meta, means2d, conics, colors, opacities, perm,
                            packed, splat_offsets, cws, cbytes, s);
   if (rc) return rc;
-  bool written = false;
   rc = bin_emit_impl(meta, packed, splat_offsets, capacity, binned_ids,
                      nullptr, tile_offsets, status_dev, cws, cbytes, ews,
-                     ebytes, s, host_words, &written, zero);
+                     ebytes, s, host_words != nullptr ? long_dev : nullptr,
+                     zero);
   if (rc || host_words == nullptr) return rc;
-  // 5. N and the status reach the host: written by the tile range launch
-  //    itself, or else in one copy
-  if (!written)
-    rc = hip_status(hipMemcpyAsync(host_words, n_dev, 2 * sizeof(int32_t),
-                                   hipMemcpyDeviceToHost, s),
-                    "gsplat_hip_bin: pair count and status copy");
-  if (!rc && ev_st != nullptr)
-    rc = hip_status(hipEventRecord(ev_st, s), "gsplat_hip_bin: event record");
-  return rc;
+  // 5. N (from the count), the status and the long-range flag to the host
+  return report(n_dev);
 }
 
 }  // namespace
@@ -581,7 +586,7 @@ int gsplat_hip_bin(const gsplat_raster_meta* meta, const float* means2d,
   return bin_impl(meta, means2d, conics, colors, opacities, depths, capacity,
                   perm, packed, splat_offsets, binned_ids, tile_offsets,
                   host_words, workspace, workspace_bytes, stream, count_stream,
-                  inputs_event, count_event, status_event, nullptr);
+                  inputs_event, count_event, status_event, nullptr, nullptr);
 }
 
 }  // extern "C"
@@ -691,16 +696,25 @@ int gsplat_hip_bin_render_forward(
   gs::ZeroSpan zero[2];
   gs::render_forward_zero_spans(P, capacity, render_workspace,
                                 out_final_T != nullptr, zero);
+  // The forward's first workgroup writes the binning's report to
+  // host_words as it starts; status_event follows the forward.
+  gs::HostReport report{};
   rc = bin_impl(meta, means2d, conics, colors, opacities, depths, capacity,
                 perm, packed, splat_offsets, binned_ids, tile_offsets,
                 host_words, bin_workspace, bin_workspace_bytes, stream,
-                count_stream, inputs_event, count_event, status_event, zero);
+                count_stream, inputs_event, count_event, nullptr, zero,
+                &report);
   if (rc) return rc;
-  return gs::launch_render_forward(
-      P, packed, tile_offsets, binned_ids, out_rgb, out_final_T, out_last,
-      out_tile_stop, capacity, render_workspace,
-      static_cast<hipStream_t>(stream),
-      gs::kForwardPreZeroed | gs::kForwardNoLong);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = gs::launch_render_forward(P, packed, tile_offsets, binned_ids, out_rgb,
+                                 out_final_T, out_last, out_tile_stop,
+                                 capacity, render_workspace, s,
+                                 gs::kForwardPreZeroed | gs::kForwardNoLong,
+                                 &report);
+  if (!rc && status_event != nullptr)
+    rc = hip_status(hipEventRecord(static_cast<hipEvent_t>(status_event), s),
+                    "gsplat_hip_bin_render_forward: event record");
+  return rc;
 }
 
 size_t gsplat_hip_render_workspace_bytes(const gsplat_raster_meta* meta,

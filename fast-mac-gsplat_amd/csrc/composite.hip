@@ -458,8 +458,11 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     const int32_t* __restrict__ tile_offsets,
     const int32_t* __restrict__ binned, float* __restrict__ out_rgb,
     float* __restrict__ out_T, int32_t* __restrict__ out_last,
-    int32_t* __restrict__ out_tile_stop, HeavyState H) {
+    int32_t* __restrict__ out_tile_stop, HeavyState H, HostReport R) {
   __shared__ Staged S;
+  // The binning's report reaches the host as the forward starts.
+  if (R.host != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+    write_host_report(R);
   const TileCoord tc = tile_coord(P);
   const int x = tc.x0 + tc.lx;
   const float px = (float)x + 0.5f;
@@ -1247,8 +1250,10 @@ int launch_render_forward(const RasterParams& P, const float* packed,
                           const int32_t* binned_ids, float* out_rgb,
                           float* out_T, int32_t* out_last,
                           int32_t* out_tile_stop, int64_t n_pairs,
-                          void* workspace, hipStream_t stream, int flags) {
-  if (P.num_tiles == 0) return GSPLAT_OK;
+                          void* workspace, hipStream_t stream, int flags,
+                          const HostReport* report) {
+  if (P.num_tiles == 0)
+    return report != nullptr ? launch_host_report(*report, stream) : GSPLAT_OK;
   const HeavyState H = forward_state(P, n_pairs, workspace, out_T);
   const float4* pk = reinterpret_cast<const float4*>(packed);
   if (H.counters != nullptr && !(flags & kForwardPreZeroed)) {
@@ -1259,7 +1264,8 @@ int launch_render_forward(const RasterParams& P, const float* packed,
   }
   hipLaunchKernelGGL(render_fwd_kernel, dim3((unsigned)P.num_tiles),
                      dim3(kLanes), 0, stream, P, pk, tile_offsets, binned_ids,
-                     out_rgb, out_T, out_last, out_tile_stop, H);
+                     out_rgb, out_T, out_last, out_tile_stop, H,
+                     report != nullptr ? *report : HostReport{});
   const int rc = check_launch("render_fwd_kernel");
   if (rc || (flags & kForwardNoLong)) return rc;
   return launch_render_forward_long(P, packed, tile_offsets, binned_ids,

@@ -191,10 +191,9 @@ struct ZeroSpan {
 // tile_offsets[0..T] and (unless tile_counts is NULL) tile_counts[0..T)
 // from the n sorted tile keys (min(n, *n_dev) of them with n_dev).  With
 // status_out, the same launch writes there the OR of the (non-null) give-up
-// status words err[0..2] of the binning's look-backs; with host_words
-// (device-mapped pinned host memory, n > 0 only) it also writes
-// {*n_dev, that OR} to host_words[0..1] and sets host_words[2] to 1 if a
-// tile range is longer than kHandoffPairs (the caller zeroes it before).
+// status words err[0..2] of the binning's look-backs; with long_flag (a
+// device word that is zero before the launch, n > 0 only) it sets
+// *long_flag to 1 if a tile range is longer than kHandoffPairs.
 // zero (may be null): two spans that the same launch zeroes.
 int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        int32_t* tile_offsets, int32_t* tile_counts,
@@ -203,8 +202,29 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        const uint32_t* err1 = nullptr,
                        const uint32_t* err2 = nullptr,
                        int32_t* status_out = nullptr,
-                       int32_t* host_words = nullptr,
+                       int32_t* long_flag = nullptr,
                        const ZeroSpan* zero = nullptr);
+
+// The binning's results for the host: device words {N, status, long-range
+// flag} copied to pinned host words host[0..2], then host[3] = 1.  Every
+// store is a system-scope store, and host[3] is a release store, so a host
+// thread that reads host[3] == 1 then reads the final host[0..2] without a
+// HIP event or stream synchronisation.
+struct HostReport {
+  const int32_t* n;
+  const int32_t* status;
+  const int32_t* long_flag;
+  int32_t* host;
+};
+__device__ inline void write_host_report(const HostReport& R) {
+  const int32_t v0 = *R.n, v1 = *R.status, v2 = *R.long_flag;
+  __hip_atomic_store(R.host + 0, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store(R.host + 1, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store(R.host + 2, v2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store(R.host + 3, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+// One workgroup that writes the report (when no forward launch carries it).
+int launch_host_report(const HostReport& R, hipStream_t stream);
 int launch_zero2(uint32_t* a, int64_t na, uint32_t* b, int64_t nb,
                  hipStream_t stream);
 int launch_fill_i32(int32_t* dst, int32_t value, int64_t n, hipStream_t stream);
@@ -222,12 +242,16 @@ size_t render_workspace_bytes(const RasterParams& P, int64_t n_pairs);
 // issues unless no tile range is longer than kHandoffPairs).
 constexpr int kForwardPreZeroed = 1;
 constexpr int kForwardNoLong = 2;
+// report (may be null): the binning's host report, written by the forward's
+// first workgroup as it starts (or by launch_host_report if the forward has
+// no workgroup).
 int launch_render_forward(const RasterParams& P, const float* packed,
                           const int32_t* tile_offsets,
                           const int32_t* binned_ids, float* out_rgb,
                           float* out_T, int32_t* out_last,
                           int32_t* out_tile_stop, int64_t n_pairs,
-                          void* workspace, hipStream_t stream, int flags = 0);
+                          void* workspace, hipStream_t stream, int flags = 0,
+                          const HostReport* report = nullptr);
 int launch_render_forward_long(const RasterParams& P, const float* packed,
                                const int32_t* tile_offsets,
                                const int32_t* binned_ids, float* out_rgb,

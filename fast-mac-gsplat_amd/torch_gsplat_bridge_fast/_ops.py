@@ -16,6 +16,7 @@ raises RuntimeError when it is set, so the call that bins fails.
 """
 from __future__ import annotations
 
+import time
 from dataclasses import dataclass
 from typing import Optional
 
@@ -29,17 +30,22 @@ from ._lib import check, ptr, stream_of
 # Optional per-op timing: when enabled, the C-ABI calls below (all, or those
 # named in `ops`) are bracketed by timing events recorded on the stream the
 # work is enqueued on.  The events come from a pool created up front, so a
-# timed call costs two event records and no event creation.
+# timed call costs two event records and no event creation.  With every = k
+# only every k-th of those calls is bracketed (each event record costs the
+# stream a few microseconds, so a sample keeps that out of most steps).
 _timing: Optional[list] = None
 _timing_ops: Optional[set] = None
 _pool: list = []
+_every = 1
+_seen = 0
 
 
-def set_timing(enabled: bool, ops=None, pool: int = 0) -> None:
+def set_timing(enabled: bool, ops=None, pool: int = 0, every: int = 1) -> None:
     """Starts (or stops) recording; `pool` events are created now and used first."""
-    global _timing, _timing_ops, _pool
+    global _timing, _timing_ops, _pool, _every, _seen
     _timing = [] if enabled else None
     _timing_ops = set(ops) if ops is not None else None
+    _every, _seen = max(1, int(every)), 0
     _pool = []
     if enabled and pool:
         _pool = [torch.cuda.Event(enable_timing=True) for _ in range(pool)]
@@ -63,8 +69,12 @@ def pop_timing() -> list:
 
 class _timed:
     def __init__(self, name):
+        global _seen
         self.name = name
         self.on = _timing is not None and (_timing_ops is None or name in _timing_ops)
+        if self.on:
+            self.on = _seen % _every == _every - 1
+            _seen += 1
 
     def __enter__(self):
         if self.on:
@@ -106,13 +116,13 @@ class BinState:
     pairs: Tensor                   # int32 [capacity]; the first N entries are the binned gids
     capacity: int                   # pair capacity the buffers and workspaces were sized for
     _n_host: Optional[Tensor] = None                 # pinned int32: N at _n_index once _n_ready completes
-    _n_ready: Optional[torch.cuda.Event] = None
+    _n_ready: Optional[object] = None                 # torch.cuda.Event or _ReportReady (synchronize())
     _n: Optional[int] = None
     _key: Optional[tuple] = None
     _n_index: tuple = (0,)
     _status_host: Optional[Tensor] = None            # pinned int32: the status at _status_index
     _status_index: tuple = (0,)
-    _status_ready: Optional[torch.cuda.Event] = None
+    _status_ready: Optional[object] = None
     _ring: Optional["_DeviceBinState"] = None        # owner of the pinned words (fast path)
     _generation: int = 0
     _long_index: Optional[tuple] = None              # where _n_host holds the long-range flag
@@ -263,21 +273,20 @@ def _staged() -> bool:
 
 
 class _DeviceBinState:
-    """Per-device objects reused by every binning call: the three events of gsplat_hip_bin
-    (re-recording them is safe: a stream wait takes the event's state when it is enqueued, and a
-    host wait on a later recording of an event also covers the earlier copies) and a ring of
-    pinned word pairs (N, status), one pair per call, filled by one transfer at the end of the
-    binning."""
+    """Per-device objects reused by every binning call: the two events that order gsplat_hip_bin's
+    count stream (re-recording them is safe: a stream wait takes the event's state when it is
+    enqueued) and a ring of pinned host words, one row per call, that the device fills with the
+    binning's report (N, status, long-range flag, then the ready word)."""
     RING = 1024
 
     def __init__(self, device: torch.device):
         main = torch.cuda.current_stream(device)
+        self.device = device
         self.inputs = torch.cuda.Event()
         self.count = torch.cuda.Event()
-        self.status = torch.cuda.Event()
-        for e in (self.inputs, self.count, self.status):
+        for e in (self.inputs, self.count):
             e.record(main)      # creates the HIP event
-        # {N, status, long-range flag, unused} per call, read through a numpy view
+        # {N, status, long-range flag, ready} per call, read through a numpy view
         self.ring_t = torch.zeros((self.RING, 4), dtype=torch.int32, pin_memory=True)
         self.ring = self.ring_t.numpy()
         self.ring_base = self.ring_t.data_ptr()
@@ -287,6 +296,36 @@ class _DeviceBinState:
         i = self.calls % self.RING
         self.calls += 1
         return i
+
+
+class _ReportReady:
+    """Host wait for the binning's report in one ring row: the device writes words 0-2 and then
+    word 3 = 1, with system-scope stores in that order, so the host reads the row once word 3 is
+    set.  The wait polls the pinned word (no HIP event, no stream synchronisation).  A wait that
+    lasts over a second synchronises the device instead (which raises if the device failed) and
+    then requires the word to be set."""
+    __slots__ = ("row", "device")
+    POLL_S = 1.0
+
+    def __init__(self, row, device: torch.device):
+        self.row = row
+        self.device = device
+
+    def synchronize(self) -> None:
+        row = self.row
+        spins = 0
+        limit = None
+        while not row[3]:
+            spins += 1
+            if spins & 4095 == 0:
+                now = time.perf_counter()
+                if limit is None:
+                    limit = now + self.POLL_S
+                elif now > limit:
+                    torch.cuda.synchronize(self.device)
+                    if not row[3]:
+                        raise RuntimeError("binning: the device did not write its report to the host words")
+                    return
 
 
 _device_bin: dict = {}
@@ -317,10 +356,11 @@ def _bin_fast(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Te
                            ptr(perm), ptr(packed), ptr(splat_offsets), ptr(pairs), ptr(tile_offsets),
                            d.ring_base + 16 * slot, ptr(ws), ws_bytes,
                            torch.cuda.current_stream(dev).cuda_stream, _side_stream(dev).cuda_stream,
-                           d.inputs.cuda_event, d.count.cuda_event, d.status.cuda_event),
+                           d.inputs.cuda_event, d.count.cuda_event, None),
           "gsplat_hip_bin")
-    return BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, d.ring, d.status, None, key, (slot, 0),
-                    d.ring, (slot, 1), d.status, d, d.calls - 1, (slot, 2))
+    ready = _ReportReady(d.ring[slot], dev)
+    return BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, d.ring, ready, None, key, (slot, 0),
+                    d.ring, (slot, 1), ready, d, d.calls - 1, (slot, 2))
 
 
 def _bin_render_fast(meta: _lib.RasterMeta, flat, cap: int, key: tuple, save_state: bool):
@@ -357,9 +397,10 @@ def _bin_render_fast(meta: _lib.RasterMeta, flat, cap: int, key: tuple, save_sta
         ptr(splat_offsets), ptr(pairs), ptr(tile_offsets), d.ring_base + 16 * slot, ptr(ws), ws_bytes, ptr(img),
         ptr(final_T), ptr(last), ptr(tile_stop), ptr(rws), rws_bytes,
         torch.cuda.current_stream(dev).cuda_stream, _side_stream(dev).cuda_stream,
-        d.inputs.cuda_event, d.count.cuda_event, d.status.cuda_event), "gsplat_hip_bin_render_forward")
-    st = BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, d.ring, d.status, None, key, (slot, 0),
-                  d.ring, (slot, 1), d.status, d, d.calls - 1, (slot, 2))
+        d.inputs.cuda_event, d.count.cuda_event, None), "gsplat_hip_bin_render_forward")
+    ready = _ReportReady(d.ring[slot], dev)
+    st = BinState(perm, packed, splat_offsets, tile_offsets, pairs, cap, d.ring, ready, None, key, (slot, 0),
+                  d.ring, (slot, 1), ready, d, d.calls - 1, (slot, 2))
     return st, (img, final_T, last, tile_stop, (rws if save_state else None)), rws
 
 

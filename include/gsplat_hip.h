@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 10
+#define GSPLAT_HIP_ABI_VERSION 11
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -181,15 +181,18 @@ int gsplat_hip_bin_emit(const gsplat_raster_meta* meta, const float* packed,
  * ordered after the work already enqueued on `stream` through inputs_event,
  * after which count_event is recorded; bin_depth_order on `stream`
  * concurrently; then bin_pack (after count_event) and bin_emit with the pair
- * capacity `capacity` (see bin_emit: n_pairs).  Finally the pair count N
- * and the binning's status word (GSPLAT_STATUS_*) reach host_words[0] and
- * host_words[1], and host_words[2] is 1 if some tile range is longer than
- * GSPLAT_HANDOFF_PAIRS pairs, else 0 (host_words: three int32 of page-locked
- * host memory mapped for the device, as hipHostMalloc and torch's
- * pin_memory allocate it; may be NULL): the call sets host_words[2] to 0 and
- * the tile-range launch on `stream` writes the words directly (a capacity of
- * 0 copies N and the status instead), after which status_event (may be NULL)
- * is recorded on `stream`: the caller waits for it before reading them.  The events are the
+ * capacity `capacity` (see bin_emit: n_pairs).  Finally a launch on
+ * `stream` reports the binning to host_words (four int32 of page-locked host
+ * memory mapped for the device, as hipHostMalloc and torch's pin_memory
+ * allocate it; may be NULL): host_words[0] = the pair count N,
+ * host_words[1] = the binning's status word (GSPLAT_STATUS_*),
+ * host_words[2] = 1 if some tile range is longer than GSPLAT_HANDOFF_PAIRS
+ * pairs, else 0, and then host_words[3] = 1.  The call sets host_words[3]
+ * to 0 before it launches anything; the device writes it last, with
+ * system-scope stores (release order), so a host thread that reads 1 there
+ * may read words 0-2 without further synchronisation.  status_event (may be
+ * NULL) is recorded on `stream` after the report: waiting for it is the
+ * other way to know the words are final.  The events are the
  * caller's (hipEvent_t; inputs_event and count_event are required when
  * count_stream differs from stream).  If a look-back gave up, every tile
  * range is empty (the compositors then read no pair) and the status says
@@ -278,8 +281,10 @@ int gsplat_hip_render_forward_long(const gsplat_raster_meta* meta,
  * gsplat_hip_render_forward_long: call it with the same arguments unless
  * host_words[2] is 0.  The tile-range launch of the binning also zeroes the
  * forward's workspace words, so the forward follows it without a launch of
- * its own for that, and status_event is recorded before the forward, so the
- * host can read host_words while the forward runs.  With N above capacity
+ * its own for that.  The binning's report (see gsplat_hip_bin) is written
+ * by the forward's first workgroup as it starts, so the host can poll
+ * host_words[3] and read the words while the forward runs; status_event
+ * (may be NULL) is recorded after the forward.  With N above capacity
  * (see gsplat_hip_bin) the image is that of the incomplete binning.  It has
  * no counterpart in the reference (which binds bin and render as two ops):
  * it is the one-call form of both for the per-step path. */

@@ -190,6 +190,80 @@ def test_binning_from_remembered_capacity(gpu, B, G, H, W):
     _assert_bins_equal(st, ob, sc, B, G)
 
 
+def _wait_word(words, timeout_s=5.0):
+    """Polls pinned host word 3 (set by the device after words 0-2), bounded in time."""
+    import time
+    t_end = time.perf_counter() + timeout_s
+    while words[3] == 0:
+        if time.perf_counter() > t_end:
+            torch.cuda.synchronize()
+            break
+    return [int(v) for v in words]
+
+
+@pytest.mark.parametrize("cfg,G,H,W,B", [(1, 3000, 200, 264, 1), (3, 150_000, 256, 256, 1)])
+def test_host_report_words(gpu, cfg, G, H, W, B):
+    """gsplat_hip_bin and gsplat_hip_bin_render_forward report {N, status, long-range flag} to four
+    pinned host words with word 3 set last.  The words read after polling word 3 (no event, no
+    synchronisation) and after waiting for status_event hold the oracle's N, status 0 and whether some
+    tile range exceeds HANDOFF_PAIRS; word 3 is cleared by the call before it launches.  Sizes: the
+    one-stream small-image path and the two-stream path above 131,072 splats."""
+    print(f"host report cfg={cfg} G={G} {H}x{W}", flush=True)
+    dev = torch.device("cuda:0")
+    sc = make_scene_2d(cfg, seed=11, G=G, B=B, H=H, W=W)
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    n = int(ob.binned_ids.size)
+    long_ref = int(np.max(np.diff(ob.tile_offsets)) > _lib.HANDOFF_PAIRS)
+    L = _lib.lib()
+    meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, (0.0, 0.0, 0.0))
+    flat = [sc[k].reshape(B * G, -1).squeeze(-1).contiguous().to(dev) for k in KEYS]
+    BG, T = B * G, B * ((H + 15) // 16) * ((W + 15) // 16)
+    cap = n + 1000
+    perm = torch.empty(BG, dtype=torch.int32, device=dev)
+    packed = torch.empty((BG, _lib.RECORD_FLOATS), dtype=torch.float32, device=dev)
+    offs = torch.empty(BG + 1, dtype=torch.int32, device=dev)
+    tiles = torch.empty(T + 1, dtype=torch.int32, device=dev)
+    pairs = torch.empty(cap, dtype=torch.int32, device=dev)
+    wsb = L.gsplat_hip_bin_workspace_bytes(meta, cap)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    words = torch.full((4,), 7, dtype=torch.int32, pin_memory=True)
+    host = words.numpy()
+    main = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(device=dev)
+    ev_in, ev_n, ev_st = torch.cuda.Event(), torch.cuda.Event(), torch.cuda.Event()
+    for e in (ev_in, ev_n, ev_st):
+        e.record(main)
+    torch.cuda.synchronize()
+    args = [_lib.ptr(t) for t in flat] + [cap, perm.data_ptr(), packed.data_ptr(), offs.data_ptr(),
+                                         pairs.data_ptr(), tiles.data_ptr(), words.data_ptr(),
+                                         ws.data_ptr(), wsb]
+    streams = [main.cuda_stream, side.cuda_stream, ev_in.cuda_event, ev_n.cuda_event]
+    expect = [n, 0, long_ref, 1]
+    # standalone binning, polled
+    _lib.check(L.gsplat_hip_bin(meta, *args, *streams, None), "gsplat_hip_bin")
+    assert _wait_word(host) == expect
+    np.testing.assert_array_equal(tiles.cpu().numpy(), ob.tile_offsets)
+    # standalone binning, waited for through status_event
+    host[:] = 7
+    _lib.check(L.gsplat_hip_bin(meta, *args, *streams, ev_st.cuda_event), "gsplat_hip_bin")
+    ev_st.synchronize()
+    assert [int(v) for v in host] == expect
+    # binning + forward: the forward's first workgroup reports
+    img = torch.empty((B, H, W, 3), dtype=torch.float32, device=dev)
+    rwsb = L.gsplat_hip_render_workspace_bytes(meta, 0)
+    rws = torch.empty(max(rwsb, 1), dtype=torch.uint8, device=dev)
+    for ev in (None, ev_st.cuda_event):
+        host[:] = 7
+        _lib.check(L.gsplat_hip_bin_render_forward(meta, *args, img.data_ptr(), None, None, None, rws.data_ptr(),
+                                                   rwsb, *streams, ev), "gsplat_hip_bin_render_forward")
+        if ev is None:
+            assert _wait_word(host) == expect
+        else:
+            ev_st.synchronize()
+            assert [int(v) for v in host] == expect
+    torch.cuda.synchronize()
+
+
 def test_binning_capacity_too_small(gpu):
     """With buffers below N the binning holds exactly the first `capacity` pairs (every pair of the
     gids whose range ends below it, part of the one range that straddles it), confirm() reports it,
