@@ -18,7 +18,7 @@
 // the exponent is evaluated in base 2, p = log2(e) * power, by the fixed
 // rounding chain
 //   A = (-a/2)*L, B = (-b)*L, C = (-c/2)*L  (L = log2(e) rounded to float),
-//   p = fma(C*dy, dy, fma(B*dx, dy, (A*dx)*dx)),
+//   p = fma(fma(C, dy, B*dx), dy, (A*dx)*dx),
 // and a pixel sees the splat iff p <= 0 and p >= plim, where plim (stored in
 // the packed record by binning) is the exponent at which o * 2^p equals the
 // alpha threshold.  Both decisions are therefore exact functions of the
@@ -133,14 +133,18 @@ __device__ __forceinline__ uint32_t strip_mask(float mx, float my, float a,
 // VALU operations per pixel).  Set only together with a strip bit.
 constexpr uint32_t kPlainBit = 1u << 4;
 
-// True when, for every pixel, the computed exponent p = fma(C dy, dy,
-// fma(B dx, dy, (A dx) dx)) is <= 0 and o 2^p stays below max_alpha:
+// True when, for every pixel, the computed exponent p = fma(fma(C, dy,
+// B dx), dy, (A dx) dx) is <= 0 and o 2^p stays below max_alpha:
 //  * -p is the quadratic form a' dx^2 + b' dx dy + c' dy^2 (a' = -A,
 //    b' = -B, c' = -C) whose smallest eigenvalue is at least
 //    (4a'c' - b'^2) / (4 (a' + c')) >= 2^-18 (a' + c') when 4a'c' - b'^2 >=
-//    2^-16 (a' + c')^2, while the rounding of the chain (three roundings
-//    per term, relative 2^-24 each) moves -p by at most 4.6 2^-24 (a' + c')
-//    (dx^2 + dy^2): the sign of p is never flipped.  The bounds on a', c',
+//    2^-16 (a' + c')^2.  The chain computes (1 + d5) times c' dy^2 (1 + d2)
+//    + b' dx dy (1 + d1)(1 + d2) + a' dx^2 (1 + d3)(1 + d4) (|di| <= 2^-24;
+//    the last rounding only scales), which is off the quadratic form by at
+//    most 2.0001 2^-24 (a' dx^2 + |b' dx dy| + c' dy^2) <= 3.0002 2^-24
+//    (a' + c') (dx^2 + dy^2): the sign of p is never flipped.  Where the
+//    inner fma cancels to a subnormal its absolute error, 2^-150 |dy|, is
+//    below 2^-78 dy^2 for |dy| >= 2^-25.  The bounds on a', c',
 //    |b'| and the centre keep every product of the chain normal and finite
 //    (|dx| and |dy| are 0 or at least 2^-25, and at most 2^33, since pixel
 //    centres are below 2^31); dx = dy = 0 gives p = +-0, which passes p <= 0;
@@ -202,13 +206,14 @@ __device__ __forceinline__ uint32_t stage_batch(
   return m;
 }
 
-// p = fma(C dy, dy, fma(B dx, dy, (A dx) dx)) with the x-only products
-// Adxdx = (A dx) dx and Bdx = B dx precomputed; contraction stays off so the
-// chain of roundings is exactly the one the CPU oracle evaluates.
+// p = fma(fma(C, dy, B dx), dy, (A dx) dx) (Horner in dy) with the x-only
+// products Adxdx = (A dx) dx and Bdx = B dx precomputed: two fmas per pixel
+// after dy.  Contraction stays off so the chain of roundings is exactly the
+// one the CPU oracle evaluates.
 __device__ __forceinline__ float splat_exponent(float Adxdx, float Bdx, float C,
                                                 float dy) {
 #pragma clang fp contract(off)
-  return __builtin_fmaf(C * dy, dy, __builtin_fmaf(Bdx, dy, Adxdx));
+  return __builtin_fmaf(__builtin_fmaf(C, dy, Bdx), dy, Adxdx);
 }
 
 __device__ __forceinline__ void x_terms(float A, float B, float dx,

@@ -347,7 +347,7 @@ static splat_t* gather_splats(const oracle_meta* M, const float* means2d, const 
  * power = -0.5*(a dx^2 + 2 b dx dy + c dy^2) and alpha = min(max_alpha,
  * o exp(power)).  Evaluated in base 2 by a fixed chain of roundings,
  *   A = (-a/2) L, B = (-b) L, C = (-c/2) L   (L = log2(e) rounded to float)
- *   p = fma(C dy, dy, fma(B dx, dy, (A dx) dx))
+ *   p = fma(fma(C, dy, B dx), dy, (A dx) dx)
  * with the visibility decision p <= 0 and p >= plim (oracle_plim), which the
  * HIP compositor takes bit for bit the same way.  2^p is rounded once from
  * double; the hardware exp2 is within 1 ulp, so later decisions that depend
@@ -362,7 +362,7 @@ static splat_t* gather_splats(const oracle_meta* M, const float* means2d, const 
 static float splat_exponent(const splat_t* s, float dx, float dy) {
   const float A = (-0.5f * s->a) * LOG2E_F, B = (-s->b) * LOG2E_F;
   const float C = (-0.5f * s->c) * LOG2E_F;
-  return fmaf(C * dy, dy, fmaf(B * dx, dy, (A * dx) * dx));
+  return fmaf(fmaf(C, dy, B * dx), dy, (A * dx) * dx);
 }
 
 static int eval_alpha(const oracle_meta* M, const splat_t* s, float px, float py,

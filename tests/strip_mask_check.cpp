@@ -21,13 +21,13 @@ struct PerturbedOps {
 };
 
 // The compositors' exponent chain (composite.hip splat_exponent / x_terms):
-// A = (-a/2) L, B = (-b) L, C = (-c/2) L, p = fma(C dy, dy, fma(B dx, dy,
-// (A dx) dx)); a pixel sees the splat iff p <= 0 and p >= plim.
+// A = (-a/2) L, B = (-b) L, C = (-c/2) L, p = fma(fma(C, dy, B dx), dy,
+// (A dx) dx); a pixel sees the splat iff p <= 0 and p >= plim.
 bool visible(float mx, float my, float a, float b, float c, float plim, float px, float py) {
   const float L = 1.44269502f;
   const float A = (-0.5f * a) * L, B = (-b) * L, C = (-0.5f * c) * L;
   const float dx = px - mx, dy = py - my;
-  const float p = fmaf(C * dy, dy, fmaf(B * dx, dy, (A * dx) * dx));
+  const float p = fmaf(fmaf(C, dy, B * dx), dy, (A * dx) * dx);
   return p <= 0.0f && p >= plim;
 }
 
