@@ -475,8 +475,9 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ splat_offsets, int64_t capacity,
     uint32_t* __restrict__ keys, uint32_t* __restrict__ vals, int pair_passes,
-    uint32_t* __restrict__ hist_partials, uint32_t* ghist_direct,
-    uint32_t* pair_status, int64_t pair_status_words, EmitScan sc) {
+    int hist_shift, uint32_t* __restrict__ hist_partials,
+    uint32_t* ghist_direct, uint32_t* pair_status, int64_t pair_status_words,
+    EmitScan sc) {
   __shared__ WalkSlots walk[kWaves];
   __shared__ int base[kWaves][kWalkSplats];
   // the pair sort's digit histograms in kHistCopies copies (lane l adds to
@@ -570,7 +571,8 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
       keys[pos] = (uint32_t)tile;
       vals[pos] = (uint32_t)(gid0 + sl);
       for (int p = 0; p < pair_passes; ++p)
-        atomicAdd(&h[p][lane % kHistCopies][((uint32_t)tile >> (8 * p)) & 255u],
+        atomicAdd(&h[p][lane % kHistCopies]
+                     [((uint32_t)tile >> (hist_shift + 8 * p)) & 255u],
                   1u);
     }
   });
@@ -695,6 +697,183 @@ __global__ __launch_bounds__(kThreads) void ranges_kernel(
 
 __global__ void host_report_kernel(HostReport R) {
   if (threadIdx.x == 0) write_host_report(R);
+}
+
+// Bucket counting sort (launch_bucket_sort): one workgroup per bucket of
+// 2^low_bits tiles, whose pairs the onesweep pass on the higher tile bits
+// left contiguous and in gid order.  A pass takes up to kBucketChunk of the
+// bucket's pairs: wavefront w the pairs [w*64*R, (w+1)*64*R) of the pass,
+// round r of it the 64 from w*64*R + r*64 (R = kBucketRounds), so that the
+// order (pass, wavefront, round, lane) is the pairs' order in the bucket.
+// A pair's output index is its digit's start, plus the pairs of that digit
+// in earlier passes, in earlier wavefronts of its pass, in the lane's earlier
+// rounds and in lower lanes of its round (ballot match): a stable sort.  The
+// digit starts are the scan of the digit counts: counted by the single pass
+// of a bucket of at most kBucketChunk pairs, else by a counting sweep first.
+constexpr int kBucketWaves = 16;
+constexpr int kBucketThreads = kBucketWaves * 64;
+constexpr int kBucketRounds = kBucketChunk / kBucketThreads;
+
+struct BucketLds {
+  uint32_t cnt[kBucketWaves][256];  // per-wavefront digit counts, then the
+                                    // digit's output index for the wavefront
+  uint32_t run[256];                // digit's next output index (sweeps)
+  uint32_t wsum[kBucketWaves];
+};
+
+// Exclusive scan of v over threads 0..255 of the workgroup (0 elsewhere);
+// every thread calls it (it synchronises the workgroup).
+__device__ __forceinline__ uint32_t bucket_digit_scan(uint32_t v,
+                                                      BucketLds& S) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  uint32_t inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += y;
+  }
+  if (lane == 63 && wave < 4) S.wsum[wave] = inc;
+  __syncthreads();
+  uint32_t pre = 0u;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) pre += (w < wave) ? S.wsum[w] : 0u;
+  __syncthreads();  // wsum is read before it is written again
+  return pre + inc - v;
+}
+
+__global__ __launch_bounds__(kBucketThreads) void bucket_sort_kernel(
+    BucketSortArgs A) {
+  __shared__ BucketLds S;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int b = blockIdx.x;
+  const int ndig = 1 << A.low_bits;
+  const uint32_t dmask = (uint32_t)ndig - 1u;
+  const int tile0 = b << A.low_bits;
+  uint32_t e = 0u;
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+    if (A.err[k] != nullptr) e |= *A.err[k];
+  if (b == 0 && t == 0 && A.status_out != nullptr) *A.status_out = (int32_t)e;
+  const int64_t n =
+      A.n_dev ? min(A.n, (int64_t)max(*A.n_dev, 0)) : A.n;
+  // the bucket's first index, the sizes of buckets 0..b-1 (b < 256), summed
+  // by every wavefront (no workgroup barrier)
+  uint32_t before = 0u;
+#pragma unroll
+  for (int i = lane; i < 256; i += 64) before += (i < b) ? A.bucket_sizes[i] : 0u;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) before += __shfl_xor(before, off, 64);
+  const uint32_t base = before;
+  // (the sizes add up to n by construction; the clamp keeps every access
+  // inside the first n pairs regardless)
+  const uint32_t size = (uint32_t)min(
+      (int64_t)A.bucket_sizes[b], max((int64_t)0, n - (int64_t)base));
+  for (int i = t; i < kBucketWaves * 256; i += kBucketThreads)
+    (&S.cnt[0][0])[i] = 0u;
+  const int64_t stride = (int64_t)gridDim.x * kBucketThreads;
+#pragma unroll
+  for (int z = 0; z < 2; ++z)
+    for (int64_t i = (int64_t)b * kBucketThreads + t; i < A.zero[z].n;
+         i += stride)
+      A.zero[z].p[i] = 0u;
+  // A look-back of the binning gave up: every tile range is empty (as in
+  // ranges_kernel).
+  if (e != 0u) {
+    for (int d = t; d < ndig; d += kBucketThreads) {
+      if (tile0 + d >= A.num_tiles) break;
+      A.tile_offsets[tile0 + d] = 0;
+      if (A.tile_counts != nullptr) A.tile_counts[tile0 + d] = 0;
+    }
+    if (b == 0 && t == 0) A.tile_offsets[A.num_tiles] = 0;
+    return;
+  }
+  if (b == 0 && t == 0) A.tile_offsets[A.num_tiles] = (int32_t)n;
+  const bool sweep = size > (uint32_t)kBucketChunk;
+  bool long_range = false;
+  if (sweep) {
+    // counting sweep, then the digit starts
+    if (t < 256) S.run[t] = 0u;
+    __syncthreads();
+    for (uint32_t i = t; i < size; i += kBucketThreads)
+      atomicAdd(&S.run[A.keys[base + i] & dmask], 1u);
+    __syncthreads();
+    const uint32_t tot = t < 256 ? S.run[t] : 0u;
+    const uint32_t first = base + bucket_digit_scan(tot, S);
+    if (t < ndig && tile0 + t < A.num_tiles) {
+      A.tile_offsets[tile0 + t] = (int32_t)first;
+      if (A.tile_counts != nullptr) A.tile_counts[tile0 + t] = (int32_t)tot;
+      long_range = tot > (uint32_t)kHandoffPairs;
+    }
+    if (t < 256) S.run[t] = first;
+    __syncthreads();
+  }
+  const uint64_t lt = run_step::lanes_below();
+  for (uint32_t c0 = 0; c0 < size; c0 += kBucketChunk) {
+    uint32_t d[kBucketRounds], v[kBucketRounds], rank[kBucketRounds];
+    bool ok[kBucketRounds];
+#pragma unroll
+    for (int r = 0; r < kBucketRounds; ++r) {
+      const uint32_t li =
+          c0 + (uint32_t)(wave * 64 * kBucketRounds + r * 64 + lane);
+      ok[r] = li < size;
+      d[r] = ok[r] ? (A.keys[base + li] & dmask) : 0u;
+      v[r] = ok[r] ? A.vals[base + li] : 0u;
+    }
+    __syncthreads();  // the counts are zero
+#pragma unroll
+    for (int r = 0; r < kBucketRounds; ++r) {
+      const uint64_t peers =
+          run_step::same_digit_lanes(d[r]) & __builtin_amdgcn_ballot_w64(ok[r]);
+      const uint32_t below = (uint32_t)__popcll(peers & lt);
+      // every lane of the digit reads the count, then its lowest lane adds
+      // the group's size (one wavefront's LDS accesses take effect in
+      // program order)
+      const uint32_t old = S.cnt[wave][d[r]];
+      __builtin_amdgcn_wave_barrier();
+      if (ok[r] && below == 0u)
+        S.cnt[wave][d[r]] = old + (uint32_t)__popcll(peers);
+      rank[r] = old + below;
+    }
+    __syncthreads();
+    // digit t: its wavefronts' output indices
+    uint32_t tot = 0u;
+    if (t < 256) {
+#pragma unroll
+      for (int w = 0; w < kBucketWaves; ++w) tot += S.cnt[w][t];
+    }
+    uint32_t first;
+    if (sweep) {
+      first = t < 256 ? S.run[t] : 0u;
+    } else {
+      first = base + bucket_digit_scan(tot, S);
+      if (t < ndig && tile0 + t < A.num_tiles) {
+        A.tile_offsets[tile0 + t] = (int32_t)first;
+        if (A.tile_counts != nullptr) A.tile_counts[tile0 + t] = (int32_t)tot;
+        long_range = tot > (uint32_t)kHandoffPairs;
+      }
+    }
+    if (t < 256) {
+      uint32_t o = first;
+#pragma unroll
+      for (int w = 0; w < kBucketWaves; ++w) {
+        const uint32_t c = S.cnt[w][t];
+        S.cnt[w][t] = o;
+        o += c;
+      }
+      if (sweep) S.run[t] = o;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kBucketRounds; ++r)
+      if (ok[r]) A.binned_ids[S.cnt[wave][d[r]] + rank[r]] = v[r];
+    if (c0 + kBucketChunk < size) {
+      __syncthreads();  // the indices are read before they are cleared
+      for (int i = t; i < kBucketWaves * 256; i += kBucketThreads)
+        (&S.cnt[0][0])[i] = 0u;
+    }
+  }
+  if (A.long_flag != nullptr && __ballot(long_range) != 0ull && lane == 0)
+    *A.long_flag = 1;
 }
 
 __global__ __launch_bounds__(kThreads) void counts_kernel(
@@ -830,7 +1009,7 @@ int launch_emit(const RasterParams& P, const float* packed,
                 uint32_t* vals, int pair_passes, uint32_t* hist_partials,
                 uint32_t* pair_ghist, uint32_t* pair_status,
                 int64_t pair_status_words, hipStream_t stream,
-                const EmitScanArgs* scan) {
+                const EmitScanArgs* scan, int hist_shift) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const int nblk = emit_blocks(P);
   // Few workgroups add their histograms atomically (pair_ghist is zeroed
@@ -841,15 +1020,16 @@ int launch_emit(const RasterParams& P, const float* packed,
                       scan->ticket, scan->err};
     hipLaunchKernelGGL(emit_kernel<true>, dim3((unsigned)nblk), dim3(kThreads),
                        0, stream, P, reinterpret_cast<const float4*>(packed),
-                       nullptr, capacity, keys, vals, pair_passes,
+                       nullptr, capacity, keys, vals, pair_passes, hist_shift,
                        hist_partials, direct ? pair_ghist : nullptr,
                        pair_status, pair_status_words, sc);
   } else {
     hipLaunchKernelGGL(emit_kernel<false>, dim3((unsigned)nblk),
                        dim3(kThreads), 0, stream, P,
                        reinterpret_cast<const float4*>(packed), splat_offsets,
-                       capacity, keys, vals, pair_passes, hist_partials,
-                       direct ? pair_ghist : nullptr, pair_status,
+                       capacity, keys, vals, pair_passes, hist_shift,
+                       hist_partials, direct ? pair_ghist : nullptr,
+                       pair_status,
                        pair_status_words, EmitScan{});
   }
   int rc = check_launch("emit_kernel");
@@ -894,6 +1074,22 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                      dim3(kThreads), 0, stream, tile_offsets, num_tiles,
                      tile_counts);
   return check_launch("counts_kernel");
+}
+
+int launch_bucket_sort(const BucketSortArgs& A, hipStream_t stream) {
+  if (A.num_tiles <= 0 || A.low_bits < 1 || A.low_bits > 8) {
+    set_error("bucket sort: needs tiles and 1..8 low bits");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  const int64_t buckets =
+      ((int64_t)A.num_tiles + (1 << A.low_bits) - 1) >> A.low_bits;
+  if (buckets > 256) {
+    set_error("bucket sort: more than 256 buckets");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  hipLaunchKernelGGL(bucket_sort_kernel, dim3((unsigned)buckets),
+                     dim3(kBucketThreads), 0, stream, A);
+  return check_launch("bucket_sort_kernel");
 }
 
 int launch_host_report(const HostReport& R, hipStream_t stream) {

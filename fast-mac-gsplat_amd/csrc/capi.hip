@@ -385,6 +385,52 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
   // bin_pack); n_pairs is the capacity of the buffers and every stage takes
   // the first min(N, n_pairs) pairs.
   const int32_t* n_dev = splat_offsets + P.num_splats;
+  // Images of 2^9..2^16 tiles whose buffers hold at most kBucketChunk pairs
+  // per bucket on average: the sort is one onesweep pass on the tile bits
+  // above the low ones (bits - 8 of them: 2^(bits-8) tiles per bucket, at
+  // most 256 buckets), then a counting sort per bucket that also writes the
+  // tile ranges.
+  const int tile_bits = bits_for((int64_t)P.num_tiles - 1);
+  const int low_bits = tile_bits - 8;
+  const int64_t buckets =
+      low_bits > 0 ? (((int64_t)P.num_tiles + (1 << low_bits) - 1) >> low_bits)
+                   : 0;
+  if (low_bits >= 1 && tile_bits <= 16 &&
+      n_pairs <= buckets * (int64_t)gs::kBucketChunk) {
+    const gs::RadixPlan high = gs::radix_plan(n_pairs, 1, low_bits, tile_bits);
+    uint32_t* high_vals =
+        reinterpret_cast<uint32_t*>(base + L.buffers + L.pairs.a_vals);
+    rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals, 1,
+                         reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
+                         ctl.status, L.pairs.status_words, s, scan, low_bits);
+    if (!rc)
+      rc = gs::radix_passes(high, ctl, base + L.buffers, keys, vals, nullptr,
+                            sorted_keys, high_vals, s, n_dev);
+    if (!rc) {
+      gs::BucketSortArgs A{};
+      A.keys = sorted_keys;
+      A.vals = high_vals;
+      A.bucket_sizes = ctl.ghist;
+      A.n = n_pairs;
+      A.n_dev = n_dev;
+      A.num_tiles = P.num_tiles;
+      A.low_bits = low_bits;
+      A.tile_offsets = tile_offsets;
+      A.tile_counts = tile_counts;
+      A.binned_ids = reinterpret_cast<uint32_t*>(binned_ids);
+      A.err[0] = err_pack;
+      A.err[1] = err_pairs;
+      A.err[2] = err_depth;
+      A.status_out = status;
+      A.long_flag = long_flag;
+      if (zero != nullptr) {
+        A.zero[0] = zero[0];
+        A.zero[1] = zero[1];
+      }
+      rc = gs::launch_bucket_sort(A, s);
+    }
+    return rc;
+  }
   // 1. pairs at deterministic per-splat ranges + the sort's histograms
   rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals,
                        L.pairs.passes,

@@ -147,9 +147,16 @@ int launch_pack(const RasterParams& P, const float* means2d,
                 int32_t* splat_offsets, uint64_t* scan_status,
                 uint32_t* scan_ticket, uint32_t* err, hipStream_t stream);
 int count_scan_blocks(const RasterParams& P);
+// Words that a launch zeroes on the side (n 32-bit words at p).
+struct ZeroSpan {
+  uint32_t* p;
+  int64_t n;
+};
+
 // emit: writes the (tile, gid) pairs into each splat's range, zeroes
 // pair_status, and fills pair_ghist ([pair_passes][256], zero on entry) with
-// the pair sort's digit histograms, atomically or via per-workgroup partials
+// the pair sort's digit histograms (digit p = bits hist_shift + 8p .. +7 of
+// the tile), atomically or via per-workgroup partials
 // (emit_blocks(P) * 4 * 256 words) and a reduction launch.  Only the first min(N, capacity) pairs are written and counted,
 // N = splat_offsets[num_splats] (-1 when N overflowed: nothing is written).
 int emit_blocks(const RasterParams& P);
@@ -168,7 +175,32 @@ int launch_emit(const RasterParams& P, const float* packed,
                 uint32_t* vals, int pair_passes, uint32_t* hist_partials,
                 uint32_t* pair_ghist, uint32_t* pair_status,
                 int64_t pair_status_words, hipStream_t stream,
-                const EmitScanArgs* scan = nullptr);
+                const EmitScanArgs* scan = nullptr, int hist_shift = 0);
+// Second half of the pair sort when one onesweep pass has ordered the pairs
+// by the tile bits above low_bits (a bucket = 2^low_bits consecutive tiles;
+// at most 256 buckets): one workgroup per bucket sorts its pairs stably on
+// the low bits and writes binned_ids, the bucket's tile_offsets (and
+// tile_counts unless NULL), tile_offsets[num_tiles] = min(n, *n_dev), the
+// status OR and the long-range flag as launch_tile_ranges does, and zeroes
+// the two spans.  bucket_sizes: the pass's digit histogram.  Any bucket size
+// is sorted correctly; one of at most kBucketChunk pairs takes one pass.
+constexpr int kBucketChunk = 4096;
+struct BucketSortArgs {
+  const uint32_t* keys;
+  const uint32_t* vals;
+  const uint32_t* bucket_sizes;
+  int64_t n;
+  const int32_t* n_dev;
+  int num_tiles, low_bits;
+  int32_t* tile_offsets;
+  int32_t* tile_counts;
+  uint32_t* binned_ids;
+  const uint32_t* err[3];
+  int32_t* status_out;
+  int32_t* long_flag;
+  ZeroSpan zero[2];
+};
+int launch_bucket_sort(const BucketSortArgs& A, hipStream_t stream);
 // rank_pack: the second launch of the small-image depth order (runs in
 // depth_buffers, as launch_count_depth_runs leaves them) with the records
 // packed at the ranks: perm, packed and gid_count[gid] = splat_count[orig]
@@ -182,11 +214,6 @@ int launch_rank_pack(const RasterParams& P, const float* means2d,
 // launch only up to here and continued by its second (render_fwd_long).
 constexpr int kHandoffPairs = GSPLAT_HANDOFF_PAIRS;
 
-// Words that a launch zeroes on the side (n 32-bit words at p).
-struct ZeroSpan {
-  uint32_t* p;
-  int64_t n;
-};
 
 // tile_offsets[0..T] and (unless tile_counts is NULL) tile_counts[0..T)
 // from the n sorted tile keys (min(n, *n_dev) of them with n_dev).  With

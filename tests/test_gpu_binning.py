@@ -128,6 +128,39 @@ def test_binning_bit_exact(gpu, cfg_id, kw):
     _assert_bins_equal(st, ob, sc, B, G)
 
 
+def test_bucket_sort_skewed(gpu):
+    """The pair sort of images of 2^9..2^16 tiles ends in one counting sort per bucket of
+    2^(bits-8) tiles.  Here 1024x1024 (4096 tiles: 256 buckets of 16) with most splats packed into
+    a 128x96-pixel patch, so that a few buckets hold tens of thousands of pairs (counted in a sweep,
+    then sorted 4096 at a time) while the others hold few: sorted ids, ranges and counts bit-exact,
+    on the first binning of the shape and on the one sized from it."""
+    rng = np.random.default_rng(21)
+    B, H, W = 1, 1024, 1024
+    G_hot, G_rest = 24_000, 6_000
+    G = G_hot + G_rest
+    m = np.concatenate([rng.uniform([300, 500], [428, 596], size=(G_hot, 2)),
+                        rng.uniform(-20, 1044, size=(G_rest, 2))]).astype(np.float32)
+    sig = rng.uniform(2.0, 14.0, size=(G, 2))
+    th = rng.uniform(0, np.pi, size=G)
+    c, s_ = np.cos(th), np.sin(th)
+    ix, iy = 1 / sig[:, 0] ** 2, 1 / sig[:, 1] ** 2
+    q = np.stack([c * c * ix + s_ * s_ * iy, c * s_ * (ix - iy), s_ * s_ * ix + c * c * iy], -1).astype(np.float32)
+    perm = rng.permutation(G)
+    sc = dict(means2d=m[perm][None], conics=q[perm][None],
+              colors=rng.uniform(0, 1, size=(1, G, 3)).astype(np.float32),
+              opacities=rng.uniform(0.05, 1, size=(1, G)).astype(np.float32),
+              depths=rng.uniform(0.5, 20, size=(1, G)).astype(np.float32))
+    sc = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in sc.items()}
+    print(f"bucket sort skewed {W}x{H} G={G}", flush=True)
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    per_bucket = np.add.reduceat(np.diff(ob.tile_offsets), np.arange(0, 4096, 16))
+    assert per_bucket.max() > 4 * 4096 and ob.binned_ids.size <= 256 * 4096
+    _ops._capacity.pop(_capacity_key(B, G, H, W), None)
+    for _ in range(2):
+        st = _gpu_bins(sc, H, W, B, G)
+        _assert_bins_equal(st, ob, sc, B, G)
+
+
 def test_binning_edge_cases(gpu):
     """Off-screen, zero/threshold opacity, degenerate and huge conics, depth ties, -0/+0, NaN depth."""
     rng = np.random.default_rng(5)
