@@ -367,7 +367,8 @@ __device__ __forceinline__ void pack_record(
   packed[3 * gid + 1] = make_float4(c, o, cr, cg);
   packed[3 * gid + 2] =
       make_float4(cb, __int_as_float(orig),
-                  visibility_limit(o, P.alpha_thr, P.max_alpha), 0.0f);
+                  visibility_limit(o, P.alpha_thr, P.max_alpha),
+                  opacity_log2(o));
 }
 
 // Rank step of the small-image depth order with the records packed where

@@ -15,15 +15,15 @@
 // test is ever skipped.
 //
 // Alpha test (reference eval_alpha, variants/v8/csrc/metal/gsplat_v8_kernels.metal:121-139):
-// the exponent is evaluated in base 2, p = log2(e) * power, by the fixed
-// rounding chain
+// the exponent is evaluated in base 2, by the fixed rounding chain
 //   A = (-a/2)*L, B = (-b)*L, C = (-c/2)*L  (L = log2(e) rounded to float),
-//   p = fma(fma(C, dy, B*dx), dy, (A*dx)*dx),
-// and a pixel sees the splat iff p <= 0 and p >= plim, where plim (stored in
-// the packed record by binning) is the exponent at which o * 2^p equals the
-// alpha threshold.  Both decisions are therefore exact functions of the
-// inputs that the CPU oracle reproduces; alpha = min(max_alpha, o * 2^p) with
-// the hardware exp2 (within 1 ulp).
+//   t = fma(C, dy, B*dx),  e = fma(t, dy, (A*dx)*dx)         (L * power),
+//   p = fma(t, dy, (A*dx)*dx + lo)                 (L * power + log2(o)),
+// where lo = L * ln(o) and plim, the base-2 exponent at which o * 2^power
+// equals the alpha threshold, come with the packed record from binning.  A
+// pixel sees the splat iff e <= 0 and p >= q = plim + lo.  Both decisions are
+// therefore exact functions of the inputs that the CPU oracle reproduces;
+// alpha = min(max_alpha, 2^p) with the hardware exp2 (within 1 ulp).
 //
 // Forward (reference tile_fast_forward_state, gsplat_v8_kernels.metal:400-476):
 //   C += T*alpha*c; T *= 1-alpha; a pixel stops after the splat that brings
@@ -92,9 +92,9 @@ __device__ __forceinline__ int slot_y(const TileCoord& c, int k) {
 // s2 first: the forward reads only its x and z (one ds_read2 whose 8-bit
 // dword offsets reach it from the batch's base address without an add).
 struct Staged {
-  float4 s2[kBatch];  // blue, orig index bits, plim, strip mask bits or 1/o
+  float4 s2[kBatch];  // blue, orig index bits, q, strip mask bits or 1/o
   float4 s0[kBatch];  // mx, my, A, B
-  float4 s1[kBatch];  // C, opacity, r, g
+  float4 s1[kBatch];  // C, lo, r, g
 };
 
 // A value through an empty asm: addresses derived from it are computed
@@ -128,13 +128,14 @@ __device__ __forceinline__ uint32_t strip_mask(float mx, float my, float a,
   return strip_mask_t<HwOps>(mx, my, a, b, c, plim, x0, y0);
 }
 
-// Mask bit of a "plain" record: for it the compositors' tests p <= 0 and
-// o 2^p < max_alpha always hold, so they are left out (same results, fewer
+// Mask bit of a "plain" record: for it the compositors' tests e <= 0 and
+// 2^p < max_alpha always hold, so they are left out (same results, fewer
 // VALU operations per pixel).  Set only together with a strip bit.
 constexpr uint32_t kPlainBit = 1u << 4;
 
-// True when, for every pixel, the computed exponent p = fma(fma(C, dy,
-// B dx), dy, (A dx) dx) is <= 0 and o 2^p stays below max_alpha:
+// True when, for every pixel, the computed exponent e = fma(fma(C, dy,
+// B dx), dy, (A dx) dx) is <= 0 and 2^p (p = fma(t, dy, (A dx) dx + lo))
+// stays below max_alpha:
 //  * -p is the quadratic form a' dx^2 + b' dx dy + c' dy^2 (a' = -A,
 //    b' = -B, c' = -C) whose smallest eigenvalue is at least
 //    (4a'c' - b'^2) / (4 (a' + c')) >= 2^-18 (a' + c') when 4a'c' - b'^2 >=
@@ -147,16 +148,21 @@ constexpr uint32_t kPlainBit = 1u << 4;
 //    below 2^-78 dy^2 for |dy| >= 2^-25.  The bounds on a', c',
 //    |b'| and the centre keep every product of the chain normal and finite
 //    (|dx| and |dy| are 0 or at least 2^-25, and at most 2^33, since pixel
-//    centres are below 2^31); dx = dy = 0 gives p = +-0, which passes p <= 0;
-//  * 2^p <= 1 (hardware exp2, within 1 ulp) and o <= o_plain = max_alpha
-//    (1 - 2^-20) keep the rounded o 2^p below max_alpha, so the clamp and
-//    the gradient gate never act.
+//    centres are below 2^31); dx = dy = 0 gives e = +-0, which passes e <= 0;
+//  * the unrounded t dy + (A dx) dx is <= 0 by the same bound, and the
+//    rounding of (A dx) dx + lo adds at most 2^-24 (|(A dx) dx| + |lo|),
+//    where 2^-24 |(A dx) dx| <= 2^-6 of the bound's margin, so p <= lo +
+//    2^-23 |lo|.  lo is within 7 2^-24 |lo| of log2(o) (ln within 4 ulp, the
+//    rounding of log2(e) and of the product), so 2^p <= o 2^(9 2^-24 |lo|),
+//    which for 2^-20 <= o <= o_plain = max_alpha (1 - 2^-16) (|lo| <= 20)
+//    and the hardware exp2 (within 1 ulp) stays below max_alpha: the clamp
+//    and the gradient gate never act.
 // NaN anywhere fails a comparison and leaves the record on the general path.
 __device__ __forceinline__ bool plain_record(float A, float B, float C,
                                              float mx, float my, float o,
                                              float o_plain) {
   const float a = -A, c = -C, s = a + c;
-  return (o > 0.0f) & (o <= o_plain) & (a >= 0x1p-60f) & (c >= 0x1p-60f) &
+  return (o >= 0x1p-20f) & (o <= o_plain) & (a >= 0x1p-60f) & (c >= 0x1p-60f) &
          (a <= 0x1p40f) & (c <= 0x1p40f) & (fabsf(B) <= 0x1p40f) &
          (4.0f * a * c - B * B >= 0x1p-16f * s * s) &
          (fabsf(mx) <= 0x1p32f) & (fabsf(my) <= 0x1p32f);
@@ -164,7 +170,7 @@ __device__ __forceinline__ bool plain_record(float A, float B, float C,
 
 // o_plain of plain_record for a clamp value max_alpha.
 __device__ __forceinline__ float plain_opacity_limit(float max_alpha) {
-  return max_alpha * (1.0f - 0x1p-20f);
+  return max_alpha * (1.0f - 0x1p-16f);
 }
 
 // Stages records [first, first+n) of the tile range into LDS with the
@@ -198,29 +204,49 @@ __device__ __forceinline__ uint32_t stage_batch(
     if (m != 0u && plain_record(A, B, C, p0.x, p0.y, p1.y, o_plain))
       m |= kPlainBit;
     S.s0[lane] = make_float4(p0.x, p0.y, A, B);
-    S.s1[lane] = make_float4(C, p1.y, p1.z, p1.w);
+    S.s1[lane] = make_float4(C, p2.w, p1.z, p1.w);
     S.s2[lane] = make_float4(
-        p2.x, p2.y, p2.z,
+        p2.x, p2.y, p2.z + p2.w,
         kMaskInLds ? __uint_as_float(m) : __builtin_amdgcn_rcpf(p1.y));
   }
   return m;
 }
 
-// p = fma(fma(C, dy, B dx), dy, (A dx) dx) (Horner in dy) with the x-only
-// products Adxdx = (A dx) dx and Bdx = B dx precomputed: two fmas per pixel
-// after dy.  Contraction stays off so the chain of roundings is exactly the
-// one the CPU oracle evaluates.
-__device__ __forceinline__ float splat_exponent(float Adxdx, float Bdx, float C,
-                                                float dy) {
+// The x-only parts of the exponents, once per splat and lane: a0 = (A dx) dx,
+// a = a0 + lo, b = B dx.
+struct XTerms {
+  float a0, a, b;
+};
+__device__ __forceinline__ XTerms x_terms(float A, float B, float dx,
+                                          float lo) {
 #pragma clang fp contract(off)
-  return __builtin_fmaf(__builtin_fmaf(C, dy, Bdx), dy, Adxdx);
+  XTerms X;
+  X.a0 = (A * dx) * dx;
+  X.a = X.a0 + lo;
+  X.b = B * dx;
+  return X;
 }
 
-__device__ __forceinline__ void x_terms(float A, float B, float dx,
-                                        float& Adxdx, float& Bdx) {
+// One pixel's exponents, Horner in dy (after dy two fmas, a third for the
+// power <= 0 test): t = fma(C, dy, B dx), p = fma(t, dy, a), e = fma(t, dy,
+// a0).  Contraction stays off so the chain of roundings is exactly the one
+// the CPU oracle evaluates.
+struct Exponents {
+  float t, p;
+};
+__device__ __forceinline__ Exponents exponents(const XTerms& X, float C,
+                                               float dy) {
 #pragma clang fp contract(off)
-  Adxdx = (A * dx) * dx;
-  Bdx = B * dx;
+  Exponents E;
+  E.t = __builtin_fmaf(C, dy, X.b);
+  E.p = __builtin_fmaf(E.t, dy, X.a);
+  return E;
+}
+// e <= 0: power <= 0 (the reference's test; always true for plain records)
+__device__ __forceinline__ bool power_nonpositive(const Exponents& E,
+                                                  const XTerms& X, float dy) {
+#pragma clang fp contract(off)
+  return __builtin_fmaf(E.t, dy, X.a0) <= 0.0f;
 }
 
 __device__ __forceinline__ uint32_t uniform_bits(float v) {
@@ -396,9 +422,9 @@ __device__ __forceinline__ void last_segment(const RasterParams& P,
 }
 
 // Front-to-back compositing of splat j of the staged batch into one pixel
-// (kPlain: a record with kPlainBit, whose p <= 0 test and clamp never act).
+// (kPlain: a record with kPlainBit, whose e <= 0 test and clamp never act).
 template <bool kPlain>
-__device__ __forceinline__ void composite_one(float Adxdx, float Bdx,
+__device__ __forceinline__ void composite_one(const XTerms& X,
                                               const float4& a1,
                                               const float4& a2, float py,
                                               float my, float t_thr,
@@ -408,13 +434,12 @@ __device__ __forceinline__ void composite_one(float Adxdx, float Bdx,
   // One combined test (alive and visible): pixels rarely die inside a
   // batch, so guarding the exponent by T would save little and cost a
   // second branch.
-  const float p = splat_exponent(Adxdx, Bdx, a1.x, py - my);
-  if ((T > t_thr) & (kPlain || p <= 0.0f) & (p >= a2.z)) {
-    // min(max_alpha, o 2^p) as one med3: o 2^p >= 0 here (plim is +inf for
-    // o <= 0), so the lower bound 0 never changes the result.
-    // o 2^p rounded once (an fma with +0 is never fused with 1 - alpha, so
-    // both variants round alike)
-    const float raw = __builtin_fmaf(a1.y, __builtin_amdgcn_exp2f(p), 0.0f);
+  const float dy = py - my;
+  const Exponents E = exponents(X, a1.x, dy);
+  if ((T > t_thr) & (kPlain || power_nonpositive(E, X, dy)) & (E.p >= a2.z)) {
+    // min(max_alpha, 2^p) as one med3: 2^p >= 0, so the lower bound 0 never
+    // changes the result.
+    const float raw = __builtin_amdgcn_exp2f(E.p);
     const float alpha =
         kPlain ? raw : __builtin_amdgcn_fmed3f(raw, 0.0f, max_alpha);
     const float w = T * alpha;
@@ -428,7 +453,7 @@ __device__ __forceinline__ void composite_one(float Adxdx, float Bdx,
 
 // True when every record of the staged batch that reaches a strip carries
 // kPlainBit (m: the staging lane's mask), so the batch is composited without
-// the p <= 0 test and the max_alpha clamp.
+// the e <= 0 test and the max_alpha clamp.
 __device__ __forceinline__ bool batch_plain(uint32_t m) {
   return __builtin_amdgcn_ballot_w64((m != 0u) & !(m & kPlainBit)) == 0;
 }
@@ -447,12 +472,11 @@ __device__ __forceinline__ void fwd_batch(const Staged& S, uint32_t bmask,
     const float4 a2 = S.s2[j];
     const float4 a0 = S.s0[j];
     const float4 a1 = S.s1[j];
-    float Adxdx, Bdx;
-    x_terms(a0.z, a0.w, px - a0.x, Adxdx, Bdx);
+    const XTerms xt = x_terms(a0.z, a0.w, px - a0.x, a1.y);
 #pragma unroll
     for (int k = 0; k < kPix; ++k) {
       if (!((mask >> k) & 1u)) continue;  // scalar branch
-      composite_one<kPlain>(Adxdx, Bdx, a1, a2, py[k], a0.y, t_thr, max_alpha,
+      composite_one<kPlain>(xt, a1, a2, py[k], a0.y, t_thr, max_alpha,
                             idx1 + j, T[k], cr[k], cg[k], cb[k], last[k]);
     }
   }
@@ -605,12 +629,11 @@ __device__ __forceinline__ void long_batch(const Staged& S, int n, int idx1,
     n2 = S.s2[jn];
     const uint32_t mask = uniform_bits(a2.w) >> s0;
     if (!(mask & ((1u << kSpW) - 1u))) continue;  // scalar branch
-    float Adxdx, Bdx;
-    x_terms(a0.z, a0.w, px - a0.x, Adxdx, Bdx);
+    const XTerms xt = x_terms(a0.z, a0.w, px - a0.x, a1.y);
 #pragma unroll
     for (int k = 0; k < kSpW; ++k) {
       if (!((mask >> k) & 1u)) continue;  // scalar branch
-      composite_one<kPlain>(Adxdx, Bdx, a1, a2, py[k], a0.y, t_thr, max_alpha,
+      composite_one<kPlain>(xt, a1, a2, py[k], a0.y, t_thr, max_alpha,
                             idx1 + j, T[k], cr[k], cg[k], cb[k], last[k]);
     }
   }
@@ -904,7 +927,7 @@ __device__ __forceinline__ bool needs_last_test(const RasterParams& P,
 // composited in the forward (i < last, tested with kCheckLast) and sees,
 // adding its parts of the splat's gradients to the lane's sums, which are
 // reduced across the wavefront and added atomically in original order.
-// kPlain: every record has kPlainBit, so p <= 0 and the max_alpha gate are
+// kPlain: every record has kPlainBit, so e <= 0 and the max_alpha gate are
 // not tested (they always pass).
 template <bool kCheckLast, bool kPlain>
 __device__ __forceinline__ void bwd_batch(
@@ -934,22 +957,18 @@ __device__ __forceinline__ void bwd_batch(
     const float4 a0 = S.s0[j];
     const float4 a1 = S.s1[j];
     const float dx = Q.px - a0.x;
-    float Adxdx, Bdx;
-    x_terms(a0.z, a0.w, dx, Adxdx, Bdx);
+    const XTerms xt = x_terms(a0.z, a0.w, dx, a1.y);
     bool contrib = false;
 #pragma unroll
     for (int k = 0; k < kPix; ++k) {
       if (!((mask >> k) & 1u)) continue;  // scalar branch
       // one combined test: composited in the forward (i < last) and visible
       const float dy = Q.py[k] - a0.y;
-      const float p = splat_exponent(Adxdx, Bdx, a1.x, dy);
-      if (((!kCheckLast) | (i < Q.lk[k])) & (kPlain | (p <= 0.0f)) &
-          (p >= a2.z)) {
+      const Exponents E = exponents(xt, a1.x, dy);
+      if (((!kCheckLast) | (i < Q.lk[k])) &
+          (kPlain || power_nonpositive(E, xt, dy)) & (E.p >= a2.z)) {
         contrib = true;
-        const float e = __builtin_amdgcn_exp2f(p);
-        // o 2^p rounded once (an fma with +0 is never fused with 1 - raw,
-        // so both variants round alike)
-        const float raw = __builtin_fmaf(a1.y, e, 0.0f);
+        const float raw = __builtin_amdgcn_exp2f(E.p);
         const bool open = kPlain || raw < max_alpha;  // gradient gate
         const float alpha = open ? raw : max_alpha;
         // 1 - alpha >= 1 - max_alpha >= eps (checked on the host), so the

@@ -89,6 +89,13 @@ __device__ __forceinline__ float visibility_limit(float opacity, float thr,
   return kLog2e * gs_logf(ratio);
 }
 
+// Base-2 logarithm of the opacity, kLog2e * ln(o) by gs_logf (-inf for
+// o = 0, NaN for o < 0 or NaN): the compositors evaluate o * 2^p as
+// 2^(p + lo) and test visibility as p + lo >= plim + lo.
+__device__ __forceinline__ float opacity_log2(float o) {
+  return kLog2e * gs_logf(o);
+}
+
 __device__ __forceinline__ int clamp_to_int(float v) {
   // Saturating float->int for the bbox corners (NaN -> 0).  Values that
   // matter are small integers already.

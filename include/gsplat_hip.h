@@ -21,13 +21,15 @@
  *          image b's depths (ascending, ties by original index); ascending gid
  *          within a tile is front-to-back order.
  *   packed splat record: 12 floats per gid,
- *          {mx, my, a, b, c, opacity, r, g, b, orig_index(bits), plim, 0}
+ *          {mx, my, a, b, c, opacity, r, g, b, orig_index(bits), plim, lo}
  *          with the conic (a,b,c) meaning power = -0.5*(a dx^2 + 2 b dx dy + c dy^2)
  *          and plim the base-2 exponent limit of the alpha test:
  *          log2(e)_f32 * ln(max(alpha_threshold / opacity, FLT_MIN)), with
  *          ln evaluated by a fixed sequence of correctly rounded float
  *          operations (+inf if opacity <= 0 or max_alpha < alpha_threshold,
- *          -inf if alpha_threshold <= 0).
+ *          -inf if alpha_threshold <= 0), and lo = log2(e)_f32 * ln(opacity)
+ *          by the same ln (-inf for 0, NaN for a negative or NaN opacity):
+ *          the compositors evaluate opacity * 2^p as 2^(p + lo).
  */
 #ifndef GSPLAT_HIP_H
 #define GSPLAT_HIP_H

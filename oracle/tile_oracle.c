@@ -303,6 +303,8 @@ void oracle_bin_fill(const oracle_meta* M, const float* means2d, const float* co
 typedef struct {
   float mx, my, a, b, c, o, r, g, bl;
   float plim; /* base-2 exponent limit of the alpha test (oracle_plim) */
+  float lo;   /* log2 of the opacity (oracle_opacity_log2) */
+  float q;    /* plim + lo: the limit of the exponent with lo folded in */
   int64_t orig;
 } splat_t;
 
@@ -322,6 +324,11 @@ float oracle_plim(float o, float thr, float max_alpha) {
   return LOG2E_F * oracle_logf(ratio);
 }
 
+/* log2(e)_f32 * ln(o) with oracle_logf (-inf for o = 0, NaN for o < 0 or
+ * NaN): the compositors evaluate o * 2^p as 2^(p + lo); the packed records
+ * written by binning carry this exact value. */
+float oracle_opacity_log2(float o) { return LOG2E_F * oracle_logf(o); }
+
 /* Depth-ordered splat records (index gid), gathered once. */
 static splat_t* gather_splats(const oracle_meta* M, const float* means2d, const float* conics,
                               const float* colors, const float* opac, const int32_t* perm) {
@@ -337,6 +344,8 @@ static splat_t* gather_splats(const oracle_meta* M, const float* means2d, const 
     s.r = colors[3 * o]; s.g = colors[3 * o + 1]; s.bl = colors[3 * o + 2];
     s.o = opac[o];
     s.plim = oracle_plim(s.o, M->alpha_threshold, M->max_alpha);
+    s.lo = oracle_opacity_log2(s.o);
+    s.q = s.plim + s.lo;
     s.orig = o;
     sp[gid] = s;
   }
@@ -347,31 +356,38 @@ static splat_t* gather_splats(const oracle_meta* M, const float* means2d, const 
  * power = -0.5*(a dx^2 + 2 b dx dy + c dy^2) and alpha = min(max_alpha,
  * o exp(power)).  Evaluated in base 2 by a fixed chain of roundings,
  *   A = (-a/2) L, B = (-b) L, C = (-c/2) L   (L = log2(e) rounded to float)
- *   p = fma(fma(C, dy, B dx), dy, (A dx) dx)
- * with the visibility decision p <= 0 and p >= plim (oracle_plim), which the
- * HIP compositor takes bit for bit the same way.  2^p is rounded once from
- * double; the hardware exp2 is within 1 ulp, so later decisions that depend
- * on the value of alpha (early stop on T, the max_alpha gradient gate) can
- * differ in their last-ulp window, reported through the ambiguity flags. */
+ *   t = fma(C, dy, B dx)
+ *   e = fma(t, dy, (A dx) dx)            (L power)
+ *   p = fma(t, dy, (A dx) dx + lo)       (L power + log2(o))
+ * with the visibility decision e <= 0 and p >= q = plim + lo (oracle_plim,
+ * oracle_opacity_log2), which the HIP compositor takes bit for bit the same
+ * way, and alpha = min(max_alpha, 2^p).  2^p is rounded once from double; the
+ * hardware exp2 is within 1 ulp, so later decisions that depend on the value
+ * of alpha (early stop on T, the max_alpha gradient gate) can differ in their
+ * last-ulp window, reported through the ambiguity flags. */
 #define AMB_ALPHA 1  /* unused: the alpha-threshold decision is exact */
 #define AMB_STOP 2   /* T within rounding of transmittance_threshold */
 #define AMB_GATE 4   /* raw alpha within rounding of max_alpha (gradient gate) */
 #define AMB_FORCED_BAD 8 /* a forced stop lies outside the ambiguity window */
 #define AMB_REL 4e-7f
 
-static float splat_exponent(const splat_t* s, float dx, float dy) {
+static void splat_exponents(const splat_t* s, float dx, float dy, float* e, float* p) {
   const float A = (-0.5f * s->a) * LOG2E_F, B = (-s->b) * LOG2E_F;
   const float C = (-0.5f * s->c) * LOG2E_F;
-  return fmaf(fmaf(C, dy, B * dx), dy, (A * dx) * dx);
+  const float t = fmaf(C, dy, B * dx);
+  const float a0 = (A * dx) * dx;
+  *e = fmaf(t, dy, a0);
+  *p = fmaf(t, dy, a0 + s->lo);
 }
 
 static int eval_alpha(const oracle_meta* M, const splat_t* s, float px, float py,
                       float* alpha, float* raw, float* dx, float* dy, int* amb) {
   *dx = px - s->mx;
   *dy = py - s->my;
-  const float p = splat_exponent(s, *dx, *dy);
-  if (!(p <= 0.0f && p >= s->plim)) return 0;
-  *raw = s->o * (float)exp2((double)p);
+  float e, p;
+  splat_exponents(s, *dx, *dy, &e, &p);
+  if (!(e <= 0.0f && p >= s->q)) return 0;
+  *raw = (float)exp2((double)p);
   *alpha = fminf(M->max_alpha, *raw);
   if (amb && fabsf(*raw - M->max_alpha) <= AMB_REL * M->max_alpha) *amb |= AMB_GATE;
   return 1;

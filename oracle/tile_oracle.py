@@ -46,6 +46,8 @@ def lib():
         L.oracle_logf.argtypes = [ctypes.c_float]
         L.oracle_plim.restype = ctypes.c_float
         L.oracle_plim.argtypes = [ctypes.c_float] * 3
+        L.oracle_opacity_log2.restype = ctypes.c_float
+        L.oracle_opacity_log2.argtypes = [ctypes.c_float]
         L.oracle_depth_order.restype = None
         L.oracle_depth_order.argtypes = [vp, ctypes.c_int32, ctypes.c_int32, vp]
         L.oracle_bin_count.restype = ctypes.c_int64
@@ -96,6 +98,12 @@ def plim(opacity: float, alpha_threshold: float, max_alpha: float) -> float:
     """Base-2 exponent limit of the alpha test (float32 value as a Python float)."""
     return float(lib().oracle_plim(ctypes.c_float(opacity), ctypes.c_float(alpha_threshold),
                                    ctypes.c_float(max_alpha)))
+
+
+def opacity_log2(opacity: float) -> float:
+    """log2(e)_f32 * oracle_logf(opacity): the packed record's lo (the compositors evaluate
+    o * 2^p as 2^(p + lo))."""
+    return float(lib().oracle_opacity_log2(ctypes.c_float(opacity)))
 
 
 @dataclass

@@ -20,15 +20,20 @@ struct PerturbedOps {
   static float sqrt(float x) { return scale(sqrtf(x)); }
 };
 
-// The compositors' exponent chain (composite.hip splat_exponent / x_terms):
-// A = (-a/2) L, B = (-b) L, C = (-c/2) L, p = fma(fma(C, dy, B dx), dy,
-// (A dx) dx); a pixel sees the splat iff p <= 0 and p >= plim.
-bool visible(float mx, float my, float a, float b, float c, float plim, float px, float py) {
+// The compositors' exponent chain (composite.hip x_terms / exponents):
+// A = (-a/2) L, B = (-b) L, C = (-c/2) L, t = fma(C, dy, B dx),
+// e = fma(t, dy, (A dx) dx), p = fma(t, dy, (A dx) dx + lo); a pixel sees the
+// splat iff e <= 0 and p >= plim + lo.
+bool visible(float mx, float my, float a, float b, float c, float plim, float lo, float px,
+             float py) {
   const float L = 1.44269502f;
   const float A = (-0.5f * a) * L, B = (-b) * L, C = (-0.5f * c) * L;
   const float dx = px - mx, dy = py - my;
-  const float p = fmaf(fmaf(C, dy, B * dx), dy, (A * dx) * dx);
-  return p <= 0.0f && p >= plim;
+  const float t = fmaf(C, dy, B * dx);
+  const float a0 = (A * dx) * dx;
+  const float e = fmaf(t, dy, a0);
+  const float p = fmaf(t, dy, a0 + lo);
+  return e <= 0.0f && p >= plim + lo;
 }
 
 }  // namespace
@@ -36,7 +41,7 @@ bool visible(float mx, float my, float a, float b, float c, float plim, float px
 extern "C" int strip_mask_check(const float* splats, const float* plims, const int32_t* tiles, int n,
                                 uint32_t* masks, uint32_t* needed) {
   for (int i = 0; i < n; ++i) {
-    const float* s = splats + 6 * i;  // mx, my, a, b, c, (unused)
+    const float* s = splats + 6 * i;  // mx, my, a, b, c, lo
     const int x0 = tiles[2 * i], y0 = tiles[2 * i + 1];
     const float mx = s[0], my = s[1], a = s[2], b = s[3], c = s[4], plim = plims[i];
     masks[3 * i + 0] = gs::strip_mask_t<PerturbedOps<-1>>(mx, my, a, b, c, plim, x0, y0);
@@ -46,7 +51,8 @@ extern "C" int strip_mask_check(const float* splats, const float* plims, const i
     for (int k = 0; k < 4; ++k)
       for (int r = 0; r < 4; ++r)
         for (int col = 0; col < 16; ++col)
-          if (visible(mx, my, a, b, c, plim, (float)(x0 + col) + 0.5f, (float)(y0 + 4 * k + r) + 0.5f))
+          if (visible(mx, my, a, b, c, plim, s[5], (float)(x0 + col) + 0.5f,
+                      (float)(y0 + 4 * k + r) + 0.5f))
             need |= 1u << k;
     needed[i] = need;
   }

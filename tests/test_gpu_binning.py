@@ -106,6 +106,8 @@ def _assert_bins_equal(st, ob, scene, B, G):
     want = np.array([TO.plim(float(v), meta.alpha_threshold, meta.max_alpha) for v in o[orig]],
                     dtype=np.float32)
     np.testing.assert_array_equal(packed[:, 10].view(np.uint32), want.view(np.uint32), err_msg="plim")
+    want = np.array([TO.opacity_log2(float(v)) for v in o[orig]], dtype=np.float32)
+    np.testing.assert_array_equal(packed[:, 11].view(np.uint32), want.view(np.uint32), err_msg="lo")
     # sorted 64-bit keys (tile << 32 | gid) strictly increase
     keys = ob.sorted_keys()
     assert np.all(keys[1:] > keys[:-1])

@@ -74,6 +74,22 @@ def test_plim_is_the_alpha_threshold_exponent():
     assert TO.plim(float(thr), float(thr), 0.99) == 0.0
 
 
+def test_opacity_log2_is_log2_of_the_opacity():
+    """lo = log2(e)_f32 * ln(o) within a few float ulps of log2(o) (closed form), so 2^(p + lo) is
+    o * 2^p; plim + lo is the exponent limit with lo folded in, log2(threshold) up to rounding."""
+    rng = np.random.default_rng(6)
+    thr = np.float32(THR)
+    for o in np.concatenate([10.0 ** rng.uniform(-6, 0, 2000), [1.0, 0.5, 0.25, 0.99, float(thr)]]).astype(np.float32):
+        lo = TO.opacity_log2(float(o))
+        exact = math.log2(float(o))
+        assert abs(lo - exact) <= 8 * abs(_ulp(exact if exact != 0 else 1.0)), (o, lo, exact)
+        q = np.float32(TO.plim(float(o), float(thr), 0.99)) + np.float32(lo)
+        assert abs(float(q) - math.log2(float(thr))) <= 1e-5, (o, q)
+    assert TO.opacity_log2(1.0) == 0.0 and TO.opacity_log2(0.5) == -1.0
+    assert TO.opacity_log2(0.0) == -math.inf
+    assert math.isnan(TO.opacity_log2(-0.5)) and math.isnan(TO.opacity_log2(float("nan")))
+
+
 def test_plim_special_cases():
     assert TO.plim(0.0, THR, 0.99) == math.inf            # nothing visible
     assert TO.plim(-0.5, THR, 0.99) == math.inf

@@ -3,8 +3,8 @@
 A host build of gs::strip_mask_t (fast-mac-gsplat_amd/csrc/gs_strip.h, the
 same source the compositors compile) is compared with brute force over the
 64 pixels of each strip: every strip holding a pixel where the splat passes
-the alpha test (the compositors' exact exponent chain, p <= 0 and p >= plim,
-plim from the oracle) must keep its bit.  The masks are taken with the
+the alpha test (the compositors' exact exponent chain, e <= 0 and
+p >= plim + lo, plim and lo from the oracle) must keep its bit.  The masks are taken with the
 reciprocal and square root rounded 2 ulp down, to nearest and 2 ulp up (the
 hardware operations are within 1 ulp), in builds with and without FP
 contraction, on random splats around a tile: sizes from 0.3 to 40 px, any
@@ -65,6 +65,7 @@ def test_strip_mask_keeps_every_visible_strip(helper, degenerate):
     sp[:, 0] += tiles[:, 0]
     sp[:, 1] += tiles[:, 1]
     plims = np.array([TO.plim(float(v), THR, 0.99) for v in o], np.float32)
+    sp[:, 5] = [TO.opacity_log2(float(v)) for v in o]
     masks = np.zeros((n, 3), np.uint32)
     needed = np.zeros(n, np.uint32)
     helper.strip_mask_check(sp.ctypes.data, plims.ctypes.data, tiles.ctypes.data, n, masks.ctypes.data,
