@@ -315,10 +315,10 @@ def main() -> int:
     dom = max(compositors, key=lambda k: warm_ms.get(k, 0.0))
 
     # Timed region: wall clock over exactly `steps` steps.  Inside it the
-    # dominant compositor call of every 4th step is bracketed by HIP events
-    # (created up front, recorded on the launch stream) for the roofline
-    # figure; the other calls and steps are not instrumented, since each
-    # event record costs the stream a few microseconds.
+    # dominant compositor of every 4th step is timed by HIP events (created
+    # up front) that its kernel launch records (the kernel's own duration)
+    # for the roofline figure; the other calls and steps are not
+    # instrumented, since a launch with events costs the stream ~12 us.
     _ops.set_timing(True, ops=(dom,), pool=2 * args.steps, every=min(TIMED_SAMPLE, max(args.steps, 1)))
     torch.cuda.synchronize()
     t0 = time.perf_counter()

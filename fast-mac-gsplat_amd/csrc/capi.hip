@@ -13,6 +13,19 @@ namespace gs {
 
 namespace {
 thread_local char g_err[1024] = "";
+// armed launch timing (kTimeForward, kTimeBackward): start, stop
+thread_local hipEvent_t g_timing[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
+}
+
+void set_launch_timing(int which, hipEvent_t start, hipEvent_t stop) {
+  g_timing[which][0] = start;
+  g_timing[which][1] = stop;
+}
+
+void take_launch_timing(int which, hipEvent_t& start, hipEvent_t& stop) {
+  start = g_timing[which][0];
+  stop = g_timing[which][1];
+  g_timing[which][0] = g_timing[which][1] = nullptr;
 }
 
 void set_error(const char* fmt, ...) {
@@ -210,6 +223,17 @@ size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta) {
   RasterParams P;
   if (make_params(meta, P)) return 0;
   return count_layout(P).total;
+}
+
+int gsplat_hip_time_next_launch(int which, void* start_event,
+                                void* stop_event) {
+  if (which != gs::kTimeForward && which != gs::kTimeBackward) {
+    gs::set_error("gsplat_hip_time_next_launch: unknown launch %d", which);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  gs::set_launch_timing(which, static_cast<hipEvent_t>(start_event),
+                        static_cast<hipEvent_t>(stop_event));
+  return GSPLAT_OK;
 }
 
 int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,

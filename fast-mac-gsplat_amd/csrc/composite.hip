@@ -49,6 +49,8 @@
 // wavefront: eight through LDS (each group of eight lanes sums one value's 64
 // partials, then three DPP steps; the group's first lane issues the float
 // atomic into the original splat order) and the ninth by DPP row steps.
+#include <hip/hip_ext.h>
+
 #include "gs_internal.h"
 #include "gs_predicate.h"
 #define GS_HD __device__ __forceinline__
@@ -1269,6 +1271,17 @@ HeavyState forward_state(const RasterParams& P, int64_t n_pairs,
 }
 }  // namespace
 
+// A launch with the timing events start/stop (either may be null).
+template <typename F, typename... Args>
+void launch_timed(F kernel, dim3 grid, dim3 block, hipStream_t stream,
+                  hipEvent_t start, hipEvent_t stop, Args... args) {
+  if (start != nullptr || stop != nullptr)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0,
+                          args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+}
+
 int launch_render_forward(const RasterParams& P, const float* packed,
                           const int32_t* tile_offsets,
                           const int32_t* binned_ids, float* out_rgb,
@@ -1276,6 +1289,8 @@ int launch_render_forward(const RasterParams& P, const float* packed,
                           int32_t* out_tile_stop, int64_t n_pairs,
                           void* workspace, hipStream_t stream, int flags,
                           const HostReport* report) {
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  take_launch_timing(kTimeForward, t0, t1);
   if (P.num_tiles == 0)
     return report != nullptr ? launch_host_report(*report, stream) : GSPLAT_OK;
   const HeavyState H = forward_state(P, n_pairs, workspace, out_T);
@@ -1286,15 +1301,17 @@ int launch_render_forward(const RasterParams& P, const float* packed,
     const int rc = launch_zero2(z[0].p, z[0].n, z[1].p, z[1].n, stream);
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(render_fwd_kernel, dim3((unsigned)P.num_tiles),
-                     dim3(kLanes), 0, stream, P, pk, tile_offsets, binned_ids,
-                     out_rgb, out_T, out_last, out_tile_stop, H,
-                     report != nullptr ? *report : HostReport{});
+  // the continuation follows in this call: it ends the timed span
+  const bool more = !(flags & kForwardNoLong) && workspace != nullptr;
+  launch_timed(render_fwd_kernel, dim3((unsigned)P.num_tiles), dim3(kLanes),
+               stream, t0, more ? nullptr : t1, P, pk, tile_offsets,
+               binned_ids, out_rgb, out_T, out_last, out_tile_stop, H,
+               report != nullptr ? *report : HostReport{});
   const int rc = check_launch("render_fwd_kernel");
-  if (rc || (flags & kForwardNoLong)) return rc;
+  if (rc || !more) return rc;
   return launch_render_forward_long(P, packed, tile_offsets, binned_ids,
                                     out_rgb, out_T, out_last, out_tile_stop,
-                                    n_pairs, workspace, stream);
+                                    n_pairs, workspace, stream, t1);
 }
 
 int launch_render_forward_long(const RasterParams& P, const float* packed,
@@ -1302,15 +1319,16 @@ int launch_render_forward_long(const RasterParams& P, const float* packed,
                                const int32_t* binned_ids, float* out_rgb,
                                float* out_T, int32_t* out_last,
                                int32_t* out_tile_stop, int64_t n_pairs,
-                               void* workspace, hipStream_t stream) {
+                               void* workspace, hipStream_t stream,
+                               hipEvent_t stop) {
   if (P.num_tiles == 0 || workspace == nullptr) return GSPLAT_OK;
   const HeavyState H = forward_state(P, n_pairs, workspace, out_T);
   // Workgroups stride over the hand-off list (its length is on the device).
   const unsigned grid = (unsigned)std::min<int64_t>(P.num_tiles, 2048);
-  hipLaunchKernelGGL(render_fwd_long_kernel<kLongStrips>, dim3(grid),
-                     dim3(256 / kLongStrips), 0, stream, P,
-                     reinterpret_cast<const float4*>(packed), tile_offsets,
-                     binned_ids, out_rgb, out_T, out_last, out_tile_stop, H);
+  launch_timed(render_fwd_long_kernel<kLongStrips>, dim3(grid),
+               dim3(256 / kLongStrips), stream, nullptr, stop, P,
+               reinterpret_cast<const float4*>(packed), tile_offsets,
+               binned_ids, out_rgb, out_T, out_last, out_tile_stop, H);
   return check_launch("render_fwd_long_kernel");
 }
 
@@ -1337,10 +1355,12 @@ int launch_render_backward(const RasterParams& P, const float* packed,
   const float4* pk = reinterpret_cast<const float4*>(packed);
   // One block per possible slot, rounded to a multiple of 8 (XCD mapping).
   const int seg_blocks = H.counters ? (H.max_slots + 7) & ~7 : 0;
-  hipLaunchKernelGGL(render_bwd_kernel,
-                     dim3((unsigned)(seg_blocks + P.num_tiles)), dim3(kLanes),
-                     0, stream, P, pk, tile_offsets, binned_ids, final_T, last,
-                     tile_stop, grad_rgb, G, H, seg_blocks);
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  take_launch_timing(kTimeBackward, t0, t1);
+  launch_timed(render_bwd_kernel,
+               dim3((unsigned)(seg_blocks + P.num_tiles)), dim3(kLanes),
+               stream, t0, t1, P, pk, tile_offsets, binned_ids, final_T, last,
+               tile_stop, grad_rgb, G, H, seg_blocks);
   rc = check_launch("render_bwd_kernel");
   if (rc || G.acc == nullptr || P.num_splats <= 0) return rc;
   hipLaunchKernelGGL(render_grads_unpack_kernel,

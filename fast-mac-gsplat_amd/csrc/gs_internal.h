@@ -259,6 +259,16 @@ int launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream);
 int launch_zero_grads(float* g_m, float* g_q, float* g_c, float* g_o,
                       int64_t n, hipStream_t stream);
 
+// Per-thread, one-shot timing of the compositors' launches with the
+// caller's events (created with timing): kTimeForward brackets the forward
+// (render_fwd_kernel, through the long-tile continuation when the same call
+// issues it), kTimeBackward render_bwd_kernel alone.  The next such launch
+// on the thread takes the pair.
+constexpr int kTimeForward = 0;
+constexpr int kTimeBackward = 1;
+void set_launch_timing(int which, hipEvent_t start, hipEvent_t stop);
+void take_launch_timing(int which, hipEvent_t& start, hipEvent_t& stop);
+
 // ---- compositing (composite.hip)
 // workspace (render_workspace_bytes, may be null): heavy-tile segment state,
 // written by the forward and read by the backward of the same binning.
@@ -284,7 +294,8 @@ int launch_render_forward_long(const RasterParams& P, const float* packed,
                                const int32_t* binned_ids, float* out_rgb,
                                float* out_T, int32_t* out_last,
                                int32_t* out_tile_stop, int64_t n_pairs,
-                               void* workspace, hipStream_t stream);
+                               void* workspace, hipStream_t stream,
+                               hipEvent_t stop = nullptr);
 // The workspace words a forward needs zero before it starts (hand-off
 // counters; with the state outputs also the backward's gradient records).
 void render_forward_zero_spans(const RasterParams& P, int64_t n_pairs,

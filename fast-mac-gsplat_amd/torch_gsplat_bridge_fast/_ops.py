@@ -29,8 +29,10 @@ from ._lib import check, ptr, stream_of
 
 # Optional per-op timing: when enabled, the C-ABI calls below (all, or those
 # named in `ops`) are bracketed by timing events recorded on the stream the
-# work is enqueued on.  The events come from a pool created up front, so a
-# timed call costs two event records and no event creation.  With every = k
+# work is enqueued on; the compositor calls instead hand the events to their
+# kernel launch (gsplat_hip_time_next_launch), which times the compositing
+# kernels themselves and adds no stream command.  The events come from a pool
+# created up front, so a timed call creates no event.  With every = k
 # only every k-th of those calls is bracketed (each event record costs the
 # stream a few microseconds, so a sample keeps that out of most steps).
 _timing: Optional[list] = None
@@ -67,6 +69,9 @@ def pop_timing() -> list:
     return out
 
 
+_LAUNCH_TIMED = {"render_forward": _lib.TIME_FORWARD, "render_backward": _lib.TIME_BACKWARD}
+
+
 class _timed:
     def __init__(self, name):
         global _seen
@@ -79,14 +84,28 @@ class _timed:
     def __enter__(self):
         if self.on:
             self.e0 = _event()
-            self.e0.record()
+            self.which = _LAUNCH_TIMED.get(self.name)
+            if self.which is None:
+                self.e0.record()
+            else:
+                self.e1 = _event()
+                for e in (self.e0, self.e1):
+                    if not e.cuda_event:
+                        e.record()   # creates the HIP event
+                check(_lib.lib().gsplat_hip_time_next_launch(self.which, self.e0.cuda_event, self.e1.cuda_event),
+                      "gsplat_hip_time_next_launch")
         return self
 
     def __exit__(self, *exc):
-        if self.on and exc[0] is None:
-            e1 = _event()
-            e1.record()
-            _timing.append((self.name, self.e0, e1))
+        if self.on:
+            if self.which is None:
+                e1 = _event()
+                e1.record()
+            else:
+                e1 = self.e1
+                _lib.lib().gsplat_hip_time_next_launch(self.which, None, None)   # disarm if unused
+            if exc[0] is None:
+                _timing.append((self.name, self.e0, e1))
         return False
 
 

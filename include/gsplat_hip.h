@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 11
+#define GSPLAT_HIP_ABI_VERSION 12
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -86,6 +86,20 @@ typedef struct gsplat_project_meta {
 
 int gsplat_hip_abi_version(void);
 const char* gsplat_hip_last_error(void);
+
+/* Timing of the next compositor launch on the calling thread (one-shot):
+ * which = GSPLAT_TIME_FORWARD brackets the next forward (its first kernel
+ * through the long-tile continuation when the same call issues it),
+ * GSPLAT_TIME_BACKWARD the next backward's compositing kernel alone (not the
+ * copy of its gradient records), with the caller's events (hipEvent_t
+ * created with timing; both may be NULL to disarm), recorded by the launch
+ * itself rather than as separate stream commands.  It has no counterpart in
+ * the reference: it is for callers that measure the compositors' kernel
+ * time, such as a benchmark's roofline figure. */
+#define GSPLAT_TIME_FORWARD 0
+#define GSPLAT_TIME_BACKWARD 1
+int gsplat_hip_time_next_launch(int which, void* start_event,
+                                void* stop_event);
 
 /* ---------------------------------------------------------------- binning
  * Replaces torch.ops.gsplat_metal_v8.bin (variants/v8/csrc/bindings.cpp:201,
