@@ -759,11 +759,18 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_sort_kernel(
       A.n_dev ? min(A.n, (int64_t)max(*A.n_dev, 0)) : A.n;
   // the bucket's first index, the sizes of buckets 0..b-1 (b < 256), summed
   // by every wavefront (no workgroup barrier)
-  uint32_t before = 0u;
+  uint32_t before = 0u, all = 0u;
 #pragma unroll
-  for (int i = lane; i < 256; i += 64) before += (i < b) ? A.bucket_sizes[i] : 0u;
+  for (int i = lane; i < 256; i += 64) {
+    const uint32_t v = A.bucket_sizes[i];
+    before += (i < b) ? v : 0u;
+    all += v;
+  }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) before += __shfl_xor(before, off, 64);
+  for (int off = 32; off > 0; off >>= 1) {
+    before += __shfl_xor(before, off, 64);
+    all += __shfl_xor(all, off, 64);
+  }
   const uint32_t base = before;
   // (the sizes add up to n by construction; the clamp keeps every access
   // inside the first n pairs regardless)
@@ -788,7 +795,10 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_sort_kernel(
     if (b == 0 && t == 0) A.tile_offsets[A.num_tiles] = 0;
     return;
   }
-  if (b == 0 && t == 0) A.tile_offsets[A.num_tiles] = (int32_t)n;
+  // the end of the last range: the pairs the buckets hold (n by
+  // construction), so that no range reaches past the sorted pairs
+  if (b == 0 && t == 0)
+    A.tile_offsets[A.num_tiles] = (int32_t)min(n, (int64_t)all);
   const bool sweep = size > (uint32_t)kBucketChunk;
   bool long_range = false;
   if (sweep) {

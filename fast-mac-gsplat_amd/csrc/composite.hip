@@ -184,11 +184,13 @@ __device__ __forceinline__ float plain_opacity_limit(float max_alpha) {
 template <bool kMaskInLds>
 __device__ __forceinline__ uint32_t stage_batch(
     const float4* __restrict__ packed, const int32_t* __restrict__ binned,
-    int first, int n, const TileCoord& tc, float o_plain, Staged& S) {
+    int first, int n, const TileCoord& tc, float o_plain, uint32_t max_gid,
+    Staged& S) {
   const int lane = threadIdx.x;
   uint32_t m = 0u;
   if (lane < n) {
-    const int gid = binned[first + lane];
+    // (clamped: a corrupt pair list cannot make the gather leave the records)
+    const uint32_t gid = min((uint32_t)binned[first + lane], max_gid);
     const float4 p0 = packed[3 * gid + 0];
     const float4 p1 = packed[3 * gid + 1];
     const float4 p2 = packed[3 * gid + 2];
@@ -539,7 +541,8 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     const int n = min(kBatch, end - base);
     __syncthreads();
     const uint32_t bmask =
-        stage_batch<false>(packed, binned, base, n, tc, o_plain, S);
+        stage_batch<false>(packed, binned, base, n, tc, o_plain,
+                           (uint32_t)P.num_splats - 1u, S);
     __syncthreads();
     if (batch_plain(bmask))
       fwd_batch<true>(S, bmask, n, base - start + 1, px, py, t_thr, max_alpha,
@@ -703,7 +706,8 @@ __global__ __launch_bounds__(256 / kSpW) void render_fwd_long_kernel(
       }
       const int n = min(kBatch, end - base);
       const uint32_t m =
-          stage_batch<true>(packed, binned, base, n, tc, o_plain, S);
+          stage_batch<true>(packed, binned, base, n, tc, o_plain,
+                            (uint32_t)P.num_splats - 1u, S);
       if (threadIdx.x < kLanes) {  // wavefront 0 staged the batch
         const bool all_plain = batch_plain(m);
         if (threadIdx.x == 0) sh_plain = all_plain;
@@ -1048,7 +1052,8 @@ __device__ __forceinline__ void bwd_walk(
     const int n = cend - cstart;
     __syncthreads();
     const uint32_t bmask =
-        stage_batch<false>(packed, binned, start + cstart, n, tc, o_plain, SH.S);
+        stage_batch<false>(packed, binned, start + cstart, n, tc, o_plain,
+                           (uint32_t)P.num_splats - 1u, SH.S);
     __syncthreads();
     if (batch_plain(bmask))
       bwd_batch<kCheckLast, true>(SH, bmask, n, cstart, max_alpha, target,
