@@ -525,19 +525,27 @@ def render_forward_long(meta: _lib.RasterMeta, st: BinState, out, workspace: Ten
           "gsplat_hip_render_forward_long")
 
 
+def gradient_buffers(B: int, G: int, device) -> tuple:
+    """The four gradient outputs of render_backward, [B,G,2], [B,G,3], [B,G,3], [B,G] (allocated
+    ahead, e.g. by the forward before it waits on the binning, to keep them off the path from the
+    forward's return to the backward's launch)."""
+    return (torch.empty((B, G, 2), dtype=torch.float32, device=device),
+            torch.empty((B, G, 3), dtype=torch.float32, device=device),
+            torch.empty((B, G, 3), dtype=torch.float32, device=device),
+            torch.empty((B, G), dtype=torch.float32, device=device))
+
+
 def render_backward(meta: _lib.RasterMeta, st: BinState, final_T: Tensor, last: Tensor, tile_stop: Tensor,
-                    grad_img: Tensor, workspace: Optional[Tensor] = None):
+                    grad_img: Tensor, workspace: Optional[Tensor] = None, out: Optional[tuple] = None):
     """Returns (g_means2d [B,G,2], g_conics [B,G,3], g_colors [B,G,3], g_opacities [B,G]) in ORIGINAL
     order.  They are allocated in the leaves' batched shapes (not as views of flat buffers) so that
-    autograd can hand them to .grad without a copy.  workspace: the one render_forward returned for
-    the same binning (heavy tiles are then split into segments), or None."""
+    autograd can hand them to .grad without a copy; out: such buffers from gradient_buffers (written
+    in full), or None.  workspace: the one render_forward returned for the same binning (heavy tiles
+    are then split into segments), or None."""
     L = _lib.lib()
     dev = st.packed.device
     B, G = meta.batch, meta.gaussians_per_batch
-    g_m = torch.empty((B, G, 2), dtype=torch.float32, device=dev)
-    g_q = torch.empty((B, G, 3), dtype=torch.float32, device=dev)
-    g_c = torch.empty((B, G, 3), dtype=torch.float32, device=dev)
-    g_o = torch.empty((B, G), dtype=torch.float32, device=dev)
+    g_m, g_q, g_c, g_o = out if out is not None else gradient_buffers(B, G, dev)
     grad_img = grad_img.contiguous()
     with _timed("render_backward"):
         check(L.gsplat_hip_render_backward(meta, ptr(st.packed), ptr(st.tile_offsets), ptr(st.pairs),

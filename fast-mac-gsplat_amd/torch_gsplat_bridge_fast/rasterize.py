@@ -239,6 +239,8 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
         meta = _meta(config, B, G)
         flat = _flat(means2d_b.detach(), conics_b.detach(), colors_b.detach(), opacities_b.detach(),
                      depths_b.detach())
+        # the first backward's outputs, allocated before the host waits on the binning
+        ctx.grad_bufs = _ops.gradient_buffers(B, G, means2d_b.device)
         st, (img, final_T, last, tile_stop, ws) = _ops.bin_and_render(meta, flat, save_state=True)
         _check_overflow(config, st)
         ctx.save_for_backward(st.packed, st.tile_offsets, st.pairs, final_T, last, tile_stop, ws)
@@ -254,7 +256,8 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
         packed, tile_offsets, pairs, final_T, last, tile_stop, ws = ctx.saved_tensors
         ctx.check_status()
         st = _ops.BinState(None, packed, None, tile_offsets, pairs, pairs.numel())
-        g_m, g_q, g_c, g_o = _ops.render_backward(ctx.meta, st, final_T, last, tile_stop, grad_out, ws)
+        bufs, ctx.grad_bufs = ctx.grad_bufs, None   # a second backward (retain_graph) allocates anew
+        g_m, g_q, g_c, g_o = _ops.render_backward(ctx.meta, st, final_T, last, tile_stop, grad_out, ws, out=bufs)
         need = ctx.needs_input_grad
         g_depth = torch.zeros(ctx.depth_shape, dtype=torch.float32, device=grad_out.device) if need[4] else None
         return (g_m if need[0] else None,

@@ -250,6 +250,23 @@ def test_depth_gradient_is_zero(gpu):
     assert torch.count_nonzero(ts[4].grad) == 0
 
 
+def test_backward_twice_with_retained_graph(gpu):
+    """The forward allocates the first backward's gradient buffers ahead; a second backward of the
+    same graph (retain_graph) writes fresh ones, so the leaves' .grad ends at twice one backward."""
+    sc = make_scene_2d(1, seed=4, G=2000, H=96, W=128)
+    H, W = sc["H"], sc["W"]
+    print(f"retain_graph {W}x{H}", flush=True)
+    leaves = [sc[k].to(gpu).requires_grad_(k != "depths") for k in KEYS]
+    w = torch.rand((1, H, W, 3), generator=torch.Generator().manual_seed(3)).to(gpu)
+    img = rasterize_projected_gaussians(*leaves, RasterConfig(height=H, width=W))
+    img.backward(w, retain_graph=True)
+    once = [t.grad.clone() for t in leaves[:4]]
+    img.backward(w)
+    for t, g in zip(leaves[:4], once):
+        # (the two backwards add their atomics in different orders)
+        torch.testing.assert_close(t.grad, 2 * g, rtol=1e-4, atol=1e-5 * float(g.abs().max()) + 1e-6)
+
+
 def _faint_crowd(seed, B, G, H, W):
     """Many large, faint splats: every tile holds several hundred pairs and
     few pixels reach the early-stop threshold, so tile stops exceed 256."""
