@@ -375,14 +375,23 @@ __device__ __forceinline__ void pack_record(
 // the ranks land: perm[gid] = in-image index, the record of gid and
 // gid_count[gid] = splat_count[orig] (the pair offsets are then scanned by
 // emit_kernel<true>).
+// Emit workgroups whose totals a rank_pack workgroup adds in LDS first (its
+// 256 gids are increasing and usually span a few dozen of them).
+constexpr int kAggBlocks = 128;
+
 __global__ __launch_bounds__(run_step::kRankBlock) void rank_pack_kernel(
     RasterParams P, const float* __restrict__ means2d,
     const float* __restrict__ conics, const float* __restrict__ colors,
     const float* __restrict__ opacities, run_step::RunBuffers runs_in,
     int runs, const int32_t* __restrict__ splat_count,
     int32_t* __restrict__ perm, float4* __restrict__ packed,
-    int32_t* __restrict__ gid_count) {
+    int32_t* __restrict__ gid_count, uint32_t* __restrict__ block_totals) {
   __shared__ run_step::RankLds S;
+  __shared__ uint32_t agg[kAggBlocks];
+  __shared__ int agg_first;
+  const int t = threadIdx.x;
+  if (t < kAggBlocks) agg[t] = 0u;  // (rank_block synchronises before use)
+  int my_gid = -1, my_n = 0;
   run_step::rank_block(
       runs_in.keys, runs_in.vals, runs_in.samples, P.gpb, runs,
       (int)blockIdx.x, S, [&](int64_t base, int pos, uint32_t v) {
@@ -390,8 +399,26 @@ __global__ __launch_bounds__(run_step::kRankBlock) void rank_pack_kernel(
         const int orig = (int)base + (int)v;
         perm[gid] = (int32_t)v;
         pack_record(P, means2d, conics, colors, opacities, packed, gid, orig);
-        gid_count[gid] = splat_count[orig];
+        my_n = splat_count[orig];
+        gid_count[gid] = my_n;
+        my_gid = gid;
       });
+  // Each gid's count goes to its emit workgroup's total (the emit's later
+  // workgroups start from these): the chunk's element 0 has its smallest
+  // gid, so workgroups first .. first + kAggBlocks - 1 are summed in LDS,
+  // any further one directly.
+  if (t == 0) agg_first = my_gid / kWalkBlockSplats;
+  __syncthreads();
+  const int first = agg_first;
+  if (my_gid >= 0 && my_n != 0) {
+    const int wb = my_gid / kWalkBlockSplats;
+    if (wb - first < kAggBlocks)
+      atomicAdd(&agg[wb - first], (uint32_t)my_n);
+    else
+      atomicAdd(&block_totals[wb], (uint32_t)my_n);
+  }
+  __syncthreads();
+  if (t < kAggBlocks && agg[t] != 0u) atomicAdd(&block_totals[first + t], agg[t]);
 }
 
 // One thread per depth-sorted splat (gid): gathers the attributes of
@@ -456,20 +483,20 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
 
 // emit_kernel<true>: the pair offsets are scanned by the emit itself.
 struct EmitScan {
-  const int32_t* gid_count;  // per-gid tile-hit counts
-  int32_t* splat_offsets;    // written: exclusive offsets; [num_splats] = N
-                             // (-1 when N does not fit in int32)
-  uint64_t* status;          // look-back status per workgroup (zero before)
-  uint32_t* ticket;          // workgroup order (zero before)
-  uint32_t* err;             // give-up status word
+  const int32_t* gid_count;     // per-gid tile-hit counts
+  int32_t* splat_offsets;       // written: exclusive offsets; [num_splats] = N
+                                // (-1 when N does not fit in int32)
+  const uint32_t* block_totals; // per emit workgroup: the sum of its gids'
+                                // counts (added by rank_pack_kernel)
 };
 
 // Pairs are written (and counted in the histograms) only at positions below
 // min(N, capacity): with a capacity below N the output is the first
-// `capacity` pairs, consistently.  kScan: the workgroups take tickets, scan
-// the per-gid counts with a decoupled look-back and write splat_offsets
-// before walking (the offsets, not N, bound the positions then: every pair
-// lies below N by construction).  Otherwise splat_offsets (and N in
+// `capacity` pairs, consistently.  kScan: each workgroup scans its gids'
+// counts, starting from the totals of the workgroups before it (their sum:
+// no look-back, no order among workgroups), and writes splat_offsets before
+// walking (the offsets, not N, bound the positions then: every pair lies
+// below N by construction).  Otherwise splat_offsets (and N in
 // splat_offsets[num_splats]) come from pack_kernel.
 template <bool kScan>
 __global__ __launch_bounds__(kThreads) void emit_kernel(
@@ -487,16 +514,15 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
   // digit, and a copy per lane group divides their serialisation
   __shared__ uint32_t h[4][kHistCopies][257];
   __shared__ int wsum[kWaves];
-  __shared__ long long s_prefix;
+  __shared__ long long wbefore[kWaves];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   // (1) zero the pair sort's look-back status (grid-stride)
   for (int64_t i = (int64_t)blockIdx.x * kThreads + t; i < pair_status_words;
        i += (int64_t)gridDim.x * kThreads)
     pair_status[i] = 0u;
   for (int i = t; i < 4 * kHistCopies * 257; i += kThreads) (&h[0][0][0])[i] = 0u;
-  // (take_ticket synchronises the workgroup)
-  const int vb = kScan ? take_ticket(sc.ticket) : (int)blockIdx.x;
-  if (!kScan) __syncthreads();
+  const int vb = (int)blockIdx.x;
+  __syncthreads();
   // (2) pair emission
   const int gid = (vb * kWaves + wave) * kWalkSplats + lane;
   const bool valid = lane < kWalkSplats && gid < P.num_splats;
@@ -508,11 +534,12 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
   int64_t n_eff;
   int total;
   if (kScan) {
-    // exclusive offsets of the workgroup's gids: wavefront scans, then the
-    // workgroup's prefix by look-back (64-bit sums).  The workgroup's total
-    // is published first and the walk set up before the look-back waits,
-    // so that the wait overlaps the set-up.
+    // exclusive offsets of the workgroup's gids: wavefront scans, the
+    // workgroup's scan, and the totals of the workgroups before it (loaded
+    // first, summed after the walk set-up, which overlaps their latency).
     const int n = valid ? sc.gid_count[gid] : 0;
+    long long before = 0;
+    for (int j = t; j < vb; j += kThreads) before += sc.block_totals[j];
     int inc = n;
 #pragma unroll
     for (int off = 1; off < kWalkSplats; off <<= 1) {
@@ -520,29 +547,18 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
       if (lane >= off) inc += y;
     }
     if (lane == kWalkSplats - 1) wsum[wave] = inc;
+    total = walk_setup(P, valid, s, g / P.gpb, W);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) before += __shfl_xor(before, off, 64);
+    if (lane == 0) wbefore[wave] = before;
     __syncthreads();
-    long long pre = 0, wg_total = 0;
+    long long pre = 0, wg_before = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
       pre += (w < wave) ? wsum[w] : 0;
-      wg_total += wsum[w];
+      wg_before += wbefore[w];
     }
-    if (t == 0)
-      status_store(&sc.status[vb], (vb == 0 ? kFlagInc64 : kFlagAgg64) |
-                                       (uint64_t)wg_total);
-    total = walk_setup(P, valid, s, g / P.gpb, W);
-    if (wave == 0) {
-      uint64_t prefix = 0;
-      if (vb > 0) {
-        prefix = lookback64_wave(sc.status, vb, sc.err);
-        if (lane == 0)
-          status_store(&sc.status[vb],
-                       kFlagInc64 | (prefix + (uint64_t)wg_total));
-      }
-      if (lane == 0) s_prefix = (long long)prefix;
-    }
-    __syncthreads();
-    const long long end = s_prefix + pre + inc;
+    const long long end = wg_before + pre + inc;
     if (valid) {
       sc.splat_offsets[gid] = (int)(end - n);
       // positions at or above the capacity are not written: clamp there
@@ -975,7 +991,8 @@ int launch_rank_pack(const RasterParams& P, const float* means2d,
                      const float* conics, const float* colors,
                      const float* opacities, void* depth_buffers,
                      const int32_t* splat_count, int32_t* perm, float* packed,
-                     int32_t* gid_count, hipStream_t stream) {
+                     int32_t* gid_count, uint32_t* block_totals,
+                     hipStream_t stream) {
   if (P.num_splats == 0 || !depth_small_ok(P.gpb)) {
     set_error("rank + pack: needs 1..131072 splats per image");
     return GSPLAT_ERR_INVALID_ARGUMENT;
@@ -988,7 +1005,8 @@ int launch_rank_pack(const RasterParams& P, const float* means2d,
                      colors, opacities,
                      run_step::run_buffers(depth_buffers, P.gpb, P.batch),
                      run_step::runs_of(P.gpb), splat_count, perm,
-                     reinterpret_cast<float4*>(packed), gid_count);
+                     reinterpret_cast<float4*>(packed), gid_count,
+                     block_totals);
   return check_launch("rank_pack_kernel");
 }
 
@@ -1027,8 +1045,8 @@ int launch_emit(const RasterParams& P, const float* packed,
   // by count_kernel), which saves the reduction launch; many would contend.
   const bool direct = nblk <= kDirectHistBlocks;
   if (scan != nullptr) {
-    const EmitScan sc{scan->gid_count, scan->splat_offsets, scan->status,
-                      scan->ticket, scan->err};
+    const EmitScan sc{scan->gid_count, scan->splat_offsets,
+                      scan->block_totals};
     hipLaunchKernelGGL(emit_kernel<true>, dim3((unsigned)nblk), dim3(kThreads),
                        0, stream, P, reinterpret_cast<const float4*>(packed),
                        nullptr, capacity, keys, vals, pair_passes, hist_shift,

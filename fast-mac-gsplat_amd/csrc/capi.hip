@@ -585,18 +585,17 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
         (int64_t)((C.ctl_end - z0) / sizeof(uint32_t)), depths,
         cb + C.depth_buffers, s);
     // ranks with the records packed at them, then the emit scans the pair
-    // offsets itself (the pack launch's look-back words serve it)
+    // offsets itself
     int32_t* gid_count = reinterpret_cast<int32_t*>(cb + C.gid_count);
+    // per emit workgroup totals (in the zeroed status words of the pack
+    // scan, which this path does not run)
+    uint32_t* block_totals = reinterpret_cast<uint32_t*>(cb + C.scan_status);
     if (!rc)
       rc = gs::launch_rank_pack(
           P, means2d, conics, colors, opacities, cb + C.depth_buffers,
           reinterpret_cast<const int32_t*>(cb + C.splat_count), perm, packed,
-          gid_count, s);
-    const gs::EmitScanArgs scan{
-        gid_count, splat_offsets,
-        reinterpret_cast<uint64_t*>(cb + C.scan_status),
-        reinterpret_cast<uint32_t*>(cb + C.scan_ticket),
-        reinterpret_cast<uint32_t*>(cb + C.scan_ticket) + 1};
+          gid_count, block_totals, s);
+    const gs::EmitScanArgs scan{gid_count, splat_offsets, block_totals};
     if (!rc)
       rc = bin_emit_impl(meta, packed, splat_offsets, capacity, binned_ids,
                          nullptr, tile_offsets, status_dev, cws, cbytes, ews,

@@ -160,15 +160,15 @@ struct ZeroSpan {
 // (emit_blocks(P) * 4 * 256 words) and a reduction launch.  Only the first min(N, capacity) pairs are written and counted,
 // N = splat_offsets[num_splats] (-1 when N overflowed: nothing is written).
 int emit_blocks(const RasterParams& P);
-// With scan, the emit scans the per-gid counts itself (decoupled look-back,
-// status words emit_blocks(P) and ticket zero before the launch) and writes
-// splat_offsets[0..BG] there; splat_offsets is then not read.
+// With scan, the emit scans the per-gid counts itself, each workgroup from
+// the sum of block_totals (emit_blocks(P) words: per emit workgroup the sum
+// of its gids' counts, as launch_rank_pack adds them) over the workgroups
+// before it, and writes splat_offsets[0..BG] there; splat_offsets is then
+// not read.
 struct EmitScanArgs {
   const int32_t* gid_count;
   int32_t* splat_offsets;
-  uint64_t* status;
-  uint32_t* ticket;
-  uint32_t* err;
+  const uint32_t* block_totals;
 };
 int launch_emit(const RasterParams& P, const float* packed,
                 const int32_t* splat_offsets, int64_t capacity, uint32_t* keys,
@@ -203,13 +203,16 @@ struct BucketSortArgs {
 int launch_bucket_sort(const BucketSortArgs& A, hipStream_t stream);
 // rank_pack: the second launch of the small-image depth order (runs in
 // depth_buffers, as launch_count_depth_runs leaves them) with the records
-// packed at the ranks: perm, packed and gid_count[gid] = splat_count[orig]
-// (the pair offsets then come from launch_emit with scan).
+// packed at the ranks: perm, packed, gid_count[gid] = splat_count[orig], and
+// each gid's count added to block_totals[gid / gids per emit workgroup]
+// (zero before the launch; the pair offsets then come from launch_emit with
+// scan).
 int launch_rank_pack(const RasterParams& P, const float* means2d,
                      const float* conics, const float* colors,
                      const float* opacities, void* depth_buffers,
                      const int32_t* splat_count, int32_t* perm, float* packed,
-                     int32_t* gid_count, hipStream_t stream);
+                     int32_t* gid_count, uint32_t* block_totals,
+                     hipStream_t stream);
 // Tile ranges longer than this many pairs are walked by the forward's first
 // launch only up to here and continued by its second (render_fwd_long).
 constexpr int kHandoffPairs = GSPLAT_HANDOFF_PAIRS;
