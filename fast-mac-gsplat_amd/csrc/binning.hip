@@ -15,6 +15,7 @@
 // LDS), so a splat with thousands of candidate tiles no longer serialises one
 // lane.
 //
+// Staged path (one launch per step, also the separate C-ABI steps):
 // count_kernel  original order: per-splat hit counts and per-workgroup sums
 //   (sum_kernel turns them into the pair count N).
 // pack_kernel   one thread per depth-sorted splat (gid): packed 48-byte
@@ -29,6 +30,22 @@
 //   whatever order the slots inside a splat's range were claimed in.
 // ranges_kernel / counts_kernel  tile_offsets and tile_counts from the
 //   sorted tile keys (the reference reads them from its atomic counters).
+//
+// Images of at most 131,072 splats whose pair count goes to host memory
+// (the per-step path) take fewer launches:
+// count_depth_runs_kernel  the count blocks above beside the depth sort's
+//   run-sorting blocks, in one launch.
+// rank_pack_kernel  the depth sort's rank step, packing each record where
+//   its rank lands and adding each gid's hit count to the total of the emit
+//   workgroup that holds the gid.
+// emit_kernel<true>  scans its gids' counts from the sum of the totals of
+//   the workgroups before it (no look-back), then emits as above.
+// bucket_sort_kernel  after one onesweep pass on the high tile bits, a
+//   counting sort of each bucket of 2^(bits-8) tiles on the low bits that
+//   also writes the tile ranges (images of 2^9..2^16 tiles whose pair
+//   buffer holds at most 4096 pairs per bucket on average).
+// host_report_kernel  the binning's report to host memory where the
+//   forward compositor does not write it.
 #include "gs_internal.h"
 #include "gs_predicate.h"
 #include "depth_runs.h"
