@@ -5,7 +5,9 @@ rasterizer at 4096x4096, 65,536 splats, B=1 on one MI355X.
 A step is one call of rasterize_projected_gaussians on GPU-resident inputs
 followed by backward with loss = sum(image * w) (w fixed, seeded), i.e. the
 whole public-API path: depth sort, binning, pair sort, forward compositing,
-backward compositing, gradients in the original order.
+backward compositing, gradients in the original order.  Before the warmup
+steps, untimed steps run for --clock-ramp seconds (0.25) so that the timed
+steps run at the GPU's working clocks (reported as `clock_ramp`).
 
 Prints ONE JSON line.  `roofline` is for the dominant kernel (the backward
 compositor, which dominates step time): its launch time is measured live with
@@ -15,7 +17,7 @@ restatement of the reference algorithm, oracle/tile_oracle.c, on the host's
 threads) on the same scene, forward+backward, once, and the reference's
 dense Torch renderer on config 0.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 2]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 2] [--clock-ramp 0.25]
     python bench.py --trace FILE --height H --width W [--trace-batch B] [--trace-gaussians G]
         a recorded scene (torch.save dict of means2d/conics/colors/opacities/depths,
         the reference's real-trace format) instead of a synthetic config
@@ -89,6 +91,14 @@ REFERENCE_MPIX_S = {2: 4096 * 4096 / 65.754e-3 / 1e6}
 FLOP_PER_EVAL = {"render_forward": 24.0, "render_backward": 60.0}
 # The dominant call's duration is sampled on every TIMED_SAMPLE-th timed step.
 TIMED_SAMPLE = 4
+# Untimed steps for this long come before the warmup steps.  The GPU raises
+# its clocks over the first ~20-30 ms of continuous work, and an idle of
+# ~50 ms lowers them again: after 5 warmup steps the next 20 cfg2 steps took
+# 334 us on average and steps 50-300 took 295 us; after 200 steps of
+# continuous work the next 20 took 292 us.  Without the ramp a short timed
+# region (20 steps of 0.3 ms) would measure the clock transition, not the
+# step.
+CLOCK_RAMP_S = 0.25
 
 
 def _cpu_model() -> str:
@@ -235,6 +245,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--clock-ramp", type=float, default=CLOCK_RAMP_S,
+                    help="seconds of untimed steps before the warmup (0: none)")
     ap.add_argument("--config", type=int, default=2, help="scene config id (torch_gsplat_bridge_fast.scenes)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--trace", default="", help="recorded scene file (real-trace case)")
@@ -304,6 +316,15 @@ def main() -> int:
             img = rasterize_projected_gaussians(*leaves, cfg)
         img.backward(w)
 
+    # Clock ramp (untimed, uninstrumented): continuous steps for
+    # args.clock_ramp seconds (at least one step when positive).
+    ramp_steps = 0
+    r0 = time.perf_counter()
+    while args.clock_ramp > 0 and (ramp_steps == 0 or time.perf_counter() - r0 < args.clock_ramp):
+        step()
+        ramp_steps += 1
+    ramp_s = time.perf_counter() - r0
+
     # Warm-up (untimed), with the compositor calls bracketed to find the
     # dominant one.
     compositors = ("render_forward", "render_backward")
@@ -366,6 +387,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_ramp": {"steps": ramp_steps, "seconds": round(ramp_s, 3)},
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
