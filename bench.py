@@ -316,14 +316,18 @@ def main() -> int:
             img = rasterize_projected_gaussians(*leaves, cfg)
         img.backward(w)
 
-    # Clock ramp (untimed, uninstrumented): continuous steps for
-    # args.clock_ramp seconds (at least one step when positive).
+    # Clock ramp (untimed, uninstrumented): one step, whose launches may
+    # still load kernels, then continuous steps for args.clock_ramp seconds.
     ramp_steps = 0
-    r0 = time.perf_counter()
-    while args.clock_ramp > 0 and (ramp_steps == 0 or time.perf_counter() - r0 < args.clock_ramp):
+    ramp_s = 0.0
+    if args.clock_ramp > 0:
         step()
-        ramp_steps += 1
-    ramp_s = time.perf_counter() - r0
+        ramp_steps = 1
+        r0 = time.perf_counter()
+        while time.perf_counter() - r0 < args.clock_ramp:
+            step()
+            ramp_steps += 1
+        ramp_s = time.perf_counter() - r0
 
     # Warm-up (untimed), with the compositor calls bracketed to find the
     # dominant one.
