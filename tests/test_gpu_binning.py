@@ -236,6 +236,33 @@ def _wait_word(words, timeout_s=5.0):
     return [int(v) for v in words]
 
 
+def test_report_ring_wraps(gpu):
+    """The Python layer's binnings report N through a ring of pinned host rows, one row per call,
+    reused every RING calls.  RING + 8 binnings alternating between two scenes of different pair
+    counts each read their own N (the oracle's) across the wrap, and the last binning of each scene
+    equals the oracle's."""
+    H, W, B, G = 64, 96, 1, 500
+    dev = torch.device("cuda:0")
+    meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, (0.0, 0.0, 0.0))
+    scenes, flats, obs = [], [], []
+    for seed in (21, 22):
+        sc = make_scene_2d(1, seed=seed, G=G, B=B, H=H, W=W)
+        scenes.append(sc)
+        flats.append([sc[k].reshape(B * G, -1).squeeze(-1).contiguous().to(dev) for k in KEYS])
+        obs.append(_oracle_bins(sc, H, W, B, G)[2])
+    n_ref = [int(ob.binned_ids.size) for ob in obs]
+    assert n_ref[0] != n_ref[1]
+    calls = _ops._DeviceBinState.RING + 8
+    print(f"report ring: {calls} binnings, N = {n_ref}", flush=True)
+    last = [None, None]
+    for i in range(calls):
+        st = _ops.bin_gaussians(meta, *flats[i % 2])
+        assert st.n_pairs == n_ref[i % 2], f"call {i}"
+        last[i % 2] = st
+    for k in range(2):
+        _assert_bins_equal(last[k], obs[k], scenes[k], B, G)
+
+
 @pytest.mark.parametrize("cfg,G,H,W,B", [(1, 3000, 200, 264, 1), (3, 150_000, 256, 256, 1)])
 def test_host_report_words(gpu, cfg, G, H, W, B):
     """gsplat_hip_bin and gsplat_hip_bin_render_forward report {N, status, long-range flag} to four
