@@ -130,6 +130,27 @@ def test_binning_bit_exact(gpu, cfg_id, kw):
     _assert_bins_equal(st, ob, sc, B, G)
 
 
+@pytest.mark.parametrize("B,G,H,W", [
+    (1, 2000, 256, 256),     # 256 tiles: 8 tile bits, one onesweep pass
+    (1, 2000, 16, 4112),     # 257 tiles: 9 bits, buckets of 2 tiles, a last bucket of one
+    (1, 2000, 100, 1000),    # 441 tiles: 9 bits, ragged rows
+    (1, 3000, 4096, 4096),   # 65,536 tiles: 16 bits, 256 buckets of 256 tiles
+    (2, 3000, 4096, 4096),   # 131,072 tiles: 17 bits, two onesweep passes and the range launch
+])
+def test_pair_sort_path_boundaries(gpu, B, G, H, W):
+    """The pair sort takes one onesweep pass for images of at most 2^8 tiles, a pass on the high
+    bits plus a counting sort per bucket of 2^(bits-8) tiles for 2^9..2^16 tiles, and two passes
+    plus the tile-range launch above 2^16: binnings at both sides of each boundary (the first of a
+    shape, which reads N before emitting, and the second, with the remembered capacity) are bit-exact
+    against the oracle."""
+    print(f"pair sort path B={B} G={G} {H}x{W}", flush=True)
+    sc = make_scene_2d(1, seed=31, G=G, B=B, H=H, W=W)
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    _ops._capacity.pop(_capacity_key(B, G, H, W), None)
+    for _ in range(2):
+        _assert_bins_equal(_gpu_bins(sc, H, W, B, G), ob, sc, B, G)
+
+
 def test_bucket_sort_skewed(gpu):
     """The pair sort of images of 2^9..2^16 tiles ends in one counting sort per bucket of
     2^(bits-8) tiles.  Here 1024x1024 (4096 tiles: 256 buckets of 16) with most splats packed into
