@@ -11,9 +11,9 @@
 // variants/v8/csrc/metal/gsplat_v8_kernels.metal:244-327).  A wavefront takes
 // kWalkSplats (32) splats, prefix-sums their candidate counts in registers
 // and then tests 64 candidates per step whatever splats they belong to (each
-// lane finds its candidate's splat by binary search over the prefix sums in
-// LDS), so a splat with thousands of candidate tiles no longer serialises one
-// lane.
+// lane finds its candidate's splat from LDS marks of the splats that start
+// inside the step, spread by a DPP prefix maximum; see walk_candidates), so a
+// splat with thousands of candidate tiles does not serialise one lane.
 //
 // Staged path (one launch per step, also the separate C-ABI steps):
 // count_kernel  original order: per-splat hit counts and per-workgroup sums
@@ -832,6 +832,21 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_sort_kernel(
   // construction), so that no range reaches past the sorted pairs
   if (b == 0 && t == 0)
     A.tile_offsets[A.num_tiles] = (int32_t)min(n, (int64_t)all);
+  // An empty bucket (no pairs, or none left below n): its tiles' ranges are
+  // empty and start at the bucket's first index (at most n, so that the
+  // offsets stay monotone when the buffers hold fewer pairs than the
+  // buckets).  The chunk loop below writes the ranges of the other buckets;
+  // it does not run for size 0.  (size is the same for the whole workgroup,
+  // so no thread waits at a barrier that the others skip.)
+  if (size == 0u) {
+    const int32_t start = (int32_t)min((int64_t)base, n);
+    for (int d = t; d < ndig; d += kBucketThreads) {
+      if (tile0 + d >= A.num_tiles) break;
+      A.tile_offsets[tile0 + d] = start;
+      if (A.tile_counts != nullptr) A.tile_counts[tile0 + d] = 0;
+    }
+    return;
+  }
   const bool sweep = size > (uint32_t)kBucketChunk;
   bool long_range = false;
   if (sweep) {

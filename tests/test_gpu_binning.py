@@ -184,6 +184,141 @@ def test_bucket_sort_skewed(gpu):
         _assert_bins_equal(st, ob, sc, B, G)
 
 
+SENTINEL = -123_456_789
+
+
+def _banded_scene(seed, G, H, W, bands):
+    """Config-1 style splats (sigma U(0.5,6) px, support radius at most ~20 px) whose centres lie in
+    the given pixel-row bands only, 40 px clear of each band's edges."""
+    sc = make_scene_2d(1, seed=seed, G=G, B=1, H=H, W=W)
+    rng = np.random.default_rng(seed)
+    lo = np.array([b[0] + 40 for b in bands], dtype=np.float64)
+    hi = np.array([b[1] - 40 for b in bands], dtype=np.float64)
+    pick = rng.choice(len(bands), size=G, p=(hi - lo) / (hi - lo).sum())
+    y = rng.uniform(lo[pick], hi[pick]).astype(np.float32)
+    sc["means2d"][0, :, 1] = torch.from_numpy(y)
+    return sc
+
+
+def _bin_capi_sentinel(sc, H, W, B, G, cap, staged):
+    """Binning through the C ABI with tile_offsets pre-filled with SENTINEL: the one-call
+    gsplat_hip_bin, or the four staged calls (count, depth order, pack, emit)."""
+    dev = torch.device("cuda:0")
+    L = _lib.lib()
+    meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, (0.0, 0.0, 0.0))
+    flat = [sc[k].reshape(B * G, -1).squeeze(-1).contiguous().to(dev) for k in KEYS]
+    BG, T = B * G, B * ((H + 15) // 16) * ((W + 15) // 16)
+    perm = torch.empty(BG, dtype=torch.int32, device=dev)
+    packed = torch.empty((BG, _lib.RECORD_FLOATS), dtype=torch.float32, device=dev)
+    offs = torch.empty(BG + 1, dtype=torch.int32, device=dev)
+    tiles = torch.full((T + 1,), SENTINEL, dtype=torch.int32, device=dev)
+    pairs = torch.full((cap,), SENTINEL, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    if staged:
+        wsb = L.gsplat_hip_bin_count_workspace_bytes(meta)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        n_dev = torch.empty(1, dtype=torch.int32, device=dev)
+        _lib.check(L.gsplat_hip_bin_count(meta, _lib.ptr(flat[0]), _lib.ptr(flat[1]), _lib.ptr(flat[3]),
+                                          n_dev.data_ptr(), ws.data_ptr(), wsb, s), "bin_count")
+        _lib.check(L.gsplat_hip_bin_depth_order(meta, _lib.ptr(flat[4]), perm.data_ptr(), ws.data_ptr(), wsb, s),
+                   "bin_depth_order")
+        _lib.check(L.gsplat_hip_bin_pack(meta, *[_lib.ptr(t) for t in flat[:4]], perm.data_ptr(),
+                                         packed.data_ptr(), offs.data_ptr(), ws.data_ptr(), wsb, s), "bin_pack")
+        ws2b = L.gsplat_hip_bin_emit_workspace_bytes(meta, cap)
+        ws2 = torch.empty(max(ws2b, 1), dtype=torch.uint8, device=dev)
+        counts = torch.full((T,), SENTINEL, dtype=torch.int32, device=dev)
+        status = torch.full((1,), SENTINEL, dtype=torch.int32, device=dev)
+        _lib.check(L.gsplat_hip_bin_emit(meta, packed.data_ptr(), offs.data_ptr(), cap, pairs.data_ptr(),
+                                         counts.data_ptr(), tiles.data_ptr(), status.data_ptr(), ws.data_ptr(), wsb,
+                                         ws2.data_ptr(), ws2b, s), "bin_emit")
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0
+        return perm, tiles, pairs, counts
+    wsb = L.gsplat_hip_bin_workspace_bytes(meta, cap)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    words = torch.zeros((4,), dtype=torch.int32, pin_memory=True)
+    ev_st = torch.cuda.Event()
+    ev_st.record(torch.cuda.current_stream(dev))
+    _lib.check(L.gsplat_hip_bin(meta, *[_lib.ptr(t) for t in flat], cap, perm.data_ptr(), packed.data_ptr(),
+                                offs.data_ptr(), pairs.data_ptr(), tiles.data_ptr(), words.data_ptr(),
+                                ws.data_ptr(), wsb, s, None, None, None, ev_st.cuda_event), "gsplat_hip_bin")
+    ev_st.synchronize()
+    assert int(words[1]) == 0 and int(words[3]) == 1
+    return perm, tiles, pairs, None
+
+
+@pytest.mark.parametrize("H,W,G,bands,empty", [
+    # 4096 tiles: 256 buckets of 16 tiles (a quarter tile row each)
+    (1024, 1024, 6000, [(0, 512)], "last"),                  # splats in the top half only
+    (1024, 1024, 6000, [(512, 1024)], "first"),              # bottom half only
+    (1024, 1024, 6000, [(100, 400), (600, 900)], "both"),    # empty first, middle and last buckets
+    # 65,536 tiles: 256 buckets of one tile row each
+    (4096, 4096, 8000, [(300, 1800), (2500, 3900)], "both"),
+])
+def test_bucket_sort_empty_buckets(gpu, H, W, G, bands, empty):
+    """The bucket counting sort writes the tile ranges of buckets that hold no pair (an image band
+    with no splats): every such tile's range is empty and starts where the next non-empty one does.
+    tile_offsets, tile counts and the sorted ids are pre-filled with a sentinel and compared
+    bit-exact with the oracle, for the one-call binning, the four staged calls and binning +
+    forward (whose image must be the background exactly on the empty tiles)."""
+    B = 1
+    print(f"bucket sort empty buckets {W}x{H} G={G} bands={bands}", flush=True)
+    sc = _banded_scene(41, G, H, W, bands)
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    n = int(ob.binned_ids.size)
+    T = ob.tile_offsets.size - 1
+    low = (T - 1).bit_length() - 8
+    per_bucket = np.add.reduceat(np.diff(ob.tile_offsets), np.arange(0, T, 1 << low))
+    assert per_bucket.size == 256 and n <= 256 * 4096
+    if empty in ("first", "both"):
+        assert per_bucket[0] == 0
+    if empty in ("last", "both"):
+        assert per_bucket[-1] == 0
+    assert (per_bucket > 0).any() and (per_bucket == 0).sum() >= 16
+    for staged in (False, True):
+        for cap in (n, n + 777):
+            perm, tiles, pairs, counts = _bin_capi_sentinel(sc, H, W, B, G, cap, staged)
+            np.testing.assert_array_equal(perm.cpu().numpy(), ob.perm)
+            np.testing.assert_array_equal(tiles.cpu().numpy(), ob.tile_offsets, err_msg=f"ranges staged={staged}")
+            np.testing.assert_array_equal(pairs[:n].cpu().numpy(), ob.binned_ids, err_msg="sorted pair ids")
+            if counts is not None:
+                np.testing.assert_array_equal(counts.cpu().numpy(), np.diff(ob.tile_offsets), err_msg="counts")
+    # binning + forward in one call: empty tiles show the background
+    dev = torch.device("cuda:0")
+    L = _lib.lib()
+    bg = (0.25, 0.5, 0.75)
+    meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, bg)
+    flat = [sc[k].reshape(B * G, -1).squeeze(-1).contiguous().to(dev) for k in KEYS]
+    cap = n + 100
+    perm = torch.empty(G, dtype=torch.int32, device=dev)
+    packed = torch.empty((G, _lib.RECORD_FLOATS), dtype=torch.float32, device=dev)
+    offs = torch.empty(G + 1, dtype=torch.int32, device=dev)
+    tiles = torch.full((T + 1,), SENTINEL, dtype=torch.int32, device=dev)
+    pairs = torch.empty(cap, dtype=torch.int32, device=dev)
+    wsb = L.gsplat_hip_bin_workspace_bytes(meta, cap)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    img = torch.full((B, H, W, 3), -1.0, dtype=torch.float32, device=dev)
+    rwsb = L.gsplat_hip_render_workspace_bytes(meta, 0)
+    rws = torch.empty(max(rwsb, 1), dtype=torch.uint8, device=dev)
+    words = torch.zeros((4,), dtype=torch.int32, pin_memory=True)
+    ev_st = torch.cuda.Event()
+    ev_st.record(torch.cuda.current_stream(dev))
+    _lib.check(L.gsplat_hip_bin_render_forward(
+        meta, *[_lib.ptr(t) for t in flat], cap, perm.data_ptr(), packed.data_ptr(), offs.data_ptr(),
+        pairs.data_ptr(), tiles.data_ptr(), words.data_ptr(), ws.data_ptr(), wsb, img.data_ptr(), None, None, None,
+        rws.data_ptr(), rwsb, torch.cuda.current_stream(dev).cuda_stream, None, None, None, ev_st.cuda_event),
+        "gsplat_hip_bin_render_forward")
+    ev_st.synchronize()
+    assert [int(v) for v in words] == [n, 0, int(np.max(np.diff(ob.tile_offsets)) > _lib.HANDOFF_PAIRS), 1]
+    np.testing.assert_array_equal(tiles.cpu().numpy(), ob.tile_offsets)
+    tiles_x = (W + 15) // 16
+    im = img[0].cpu().numpy()
+    for t in np.flatnonzero(np.diff(ob.tile_offsets) == 0)[::7]:
+        ty, tx = divmod(int(t), tiles_x)
+        blk = im[16 * ty:16 * ty + 16, 16 * tx:16 * tx + 16]
+        np.testing.assert_array_equal(blk, np.broadcast_to(np.array(bg, np.float32), blk.shape))
+
+
 def test_binning_edge_cases(gpu):
     """Off-screen, zero/threshold opacity, degenerate and huge conics, depth ties, -0/+0, NaN depth."""
     rng = np.random.default_rng(5)
