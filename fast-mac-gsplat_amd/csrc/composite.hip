@@ -22,8 +22,12 @@
 // where lo = L * ln(o) and plim, the base-2 exponent at which o * 2^power
 // equals the alpha threshold, come with the packed record from binning.  A
 // pixel sees the splat iff e <= 0 and p >= q = plim + lo.  Both decisions are
-// therefore exact functions of the inputs that the CPU oracle reproduces;
-// alpha = min(max_alpha, 2^p) with the hardware exp2 (within 1 ulp).
+// therefore exact functions of the inputs that the CPU oracle reproduces:
+// exact for this base-2 form.  The reference's own form, min(max_alpha,
+// o*exp(power)) >= threshold with power rounded in another order, decides
+// the same way except where alpha lies within a few ulps of the threshold
+// (a handful of pixels per 4K image).  alpha = min(max_alpha, 2^p) with the
+// hardware exp2 (within 1 ulp).
 //
 // Forward (reference tile_fast_forward_state, gsplat_v8_kernels.metal:400-476):
 //   C += T*alpha*c; T *= 1-alpha; a pixel stops after the splat that brings

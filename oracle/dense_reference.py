@@ -23,36 +23,50 @@ import torch
 
 
 def dense_reference(means2d, conics, colors, opacities, depths, height, width, *, background=(0.0, 0.0, 0.0),
-                    alpha_threshold=1.0 / 255.0, max_alpha=0.99, early_stop=False, transmittance_threshold=1e-4):
-    """[G,..] -> [H,W,3] or [B,G,..] -> [B,H,W,3]."""
+                    alpha_threshold=1.0 / 255.0, max_alpha=0.99, early_stop=False, transmittance_threshold=1e-4,
+                    x0=0, y0=0):
+    """[G,..] -> [H,W,3] or [B,G,..] -> [B,H,W,3].  Output pixel (y, x) of image b is pixel
+    (y0 + y, x0 + x) of a larger image, centre (x0 + x + 0.5, y0 + y + 0.5): x0 / y0 are ints or
+    int sequences of length B (one crop origin per image), and a crop is evaluated exactly as in
+    the whole image.  The images of the batch are evaluated together, each with the same
+    operations in the same order as alone."""
     squeeze = means2d.ndim == 2
     if squeeze:
         means2d, conics, colors, opacities, depths = (t.unsqueeze(0) for t in
                                                       (means2d, conics, colors, opacities, depths))
     dt, dev = means2d.dtype, means2d.device
+    Bn = means2d.shape[0]
     bg = torch.tensor(background, dtype=dt, device=dev)
-    ys = torch.arange(height, dtype=dt, device=dev) + 0.5
-    xs = torch.arange(width, dtype=dt, device=dev) + 0.5
-    yy, xx = torch.meshgrid(ys, xs, indexing="ij")
-    outs = []
-    for b in range(means2d.shape[0]):
-        perm = torch.argsort(depths[b].detach(), stable=True)
-        m, q, c, o = means2d[b][perm], conics[b][perm], colors[b][perm], opacities[b][perm]
-        out = torch.zeros(height, width, 3, dtype=dt, device=dev)
-        T = torch.ones(height, width, dtype=dt, device=dev)
-        for i in range(m.shape[0]):
-            dx = xx - m[i, 0]
-            dy = yy - m[i, 1]
-            power = -0.5 * (q[i, 0] * dx * dx + 2.0 * q[i, 1] * dx * dy + q[i, 2] * dy * dy)
-            alpha = torch.clamp(o[i] * torch.exp(power), max=max_alpha)
-            keep = (power <= 0.0) & (alpha >= alpha_threshold)
-            if early_stop:
-                keep = keep & (T > transmittance_threshold)
-            alpha = torch.where(keep, alpha, torch.zeros_like(alpha))
-            out = out + (T * alpha)[..., None] * c[i]
-            T = T * (1.0 - alpha)
-        outs.append(out + T[..., None] * bg)
-    out = torch.stack(outs, dim=0)
+    ox = torch.as_tensor(x0, dtype=dt, device=dev).reshape(-1, 1, 1)
+    oy = torch.as_tensor(y0, dtype=dt, device=dev).reshape(-1, 1, 1)
+    ys = torch.arange(height, dtype=dt, device=dev).reshape(1, -1, 1)
+    xs = torch.arange(width, dtype=dt, device=dev).reshape(1, 1, -1)
+    # integer-valued floats below 2^24: (origin + index) + 0.5 is exact
+    yy = ((ys + oy) + 0.5).expand(-1, height, width)
+    xx = ((xs + ox) + 0.5).expand(-1, height, width)
+    perm = torch.argsort(depths.detach(), dim=1, stable=True)
+
+    def gather(t):
+        if t.ndim == 2:
+            return torch.gather(t, 1, perm)
+        return torch.gather(t, 1, perm[..., None].expand(-1, -1, t.shape[-1]))
+
+    m, q, c, o = gather(means2d), gather(conics), gather(colors), gather(opacities)
+    out = torch.zeros(Bn, height, width, 3, dtype=dt, device=dev)
+    T = torch.ones(Bn, height, width, dtype=dt, device=dev)
+    for i in range(m.shape[1]):
+        dx = xx - m[:, i, 0, None, None]
+        dy = yy - m[:, i, 1, None, None]
+        power = -0.5 * (q[:, i, 0, None, None] * dx * dx + 2.0 * q[:, i, 1, None, None] * dx * dy
+                        + q[:, i, 2, None, None] * dy * dy)
+        alpha = torch.clamp(o[:, i, None, None] * torch.exp(power), max=max_alpha)
+        keep = (power <= 0.0) & (alpha >= alpha_threshold)
+        if early_stop:
+            keep = keep & (T > transmittance_threshold)
+        alpha = torch.where(keep, alpha, torch.zeros_like(alpha))
+        out = out + (T * alpha)[..., None] * c[:, i, None, None, :]
+        T = T * (1.0 - alpha)
+    out = out + T[..., None] * bg
     return out[0] if squeeze else out
 
 

@@ -102,7 +102,12 @@ def gpu_decisions(meta, s, bins, gpu_last, max_ambiguous_fraction=MAX_AMBIGUOUS_
     them with the GPU's count.  Asserts that every other pixel's count
     matches the GPU's exactly, that the forced decisions lie inside the
     window, and that at most max_ambiguous_fraction of the pixels are
-    ambiguous.  Returns (force_last or None, forward outputs, report)."""
+    ambiguous.  Returns (force_last or None, forward outputs, report); the
+    report also counts the pixels where the reference's own form of the
+    alpha test lies within rounding of the threshold (alpha_flagged_pixels)
+    or decides differently from the base-2 form the GPU and the oracle share
+    (alpha_flipped_pixels): there the GPU matches the oracle, and the
+    reference may differ by up to T * alpha_threshold * |colour - bg|."""
     img, T, last, stop, amb = TO.render_forward(meta, s, bins, with_ambiguity=True)
     gpu_last = np.asarray(gpu_last, dtype=np.int32).reshape(last.shape)
     ambiguous = (amb & (TO.AMB_STOP | TO.AMB_GATE)) != 0
@@ -111,7 +116,9 @@ def gpu_decisions(meta, s, bins, gpu_last, max_ambiguous_fraction=MAX_AMBIGUOUS_
     clear = differ & ~((amb & TO.AMB_STOP) != 0)
     assert not clear.any(), (f"{int(clear.sum())} pixels stop differently although their decision is clear; "
                              f"first at {tuple(np.argwhere(clear)[0])}: gpu {gpu_last[clear][0]} oracle {last[clear][0]}")
-    report = {"ambiguous_pixels": int(ambiguous.sum()), "forced_pixels": int(differ.sum())}
+    report = {"ambiguous_pixels": int(ambiguous.sum()), "forced_pixels": int(differ.sum()),
+              "alpha_flagged_pixels": int(((amb & TO.AMB_ALPHA) != 0).sum()),
+              "alpha_flipped_pixels": int(((amb & TO.AMB_ALPHA_FLIP) != 0).sum())}
     if not differ.any():
         return None, (img, T, last, stop), report
     force = np.where(differ, gpu_last, -1).astype(np.int32)

@@ -361,15 +361,24 @@ static splat_t* gather_splats(const oracle_meta* M, const float* means2d, const 
  *   p = fma(t, dy, (A dx) dx + lo)       (L power + log2(o))
  * with the visibility decision e <= 0 and p >= q = plim + lo (oracle_plim,
  * oracle_opacity_log2), which the HIP compositor takes bit for bit the same
- * way, and alpha = min(max_alpha, 2^p).  2^p is rounded once from double; the
- * hardware exp2 is within 1 ulp, so later decisions that depend on the value
- * of alpha (early stop on T, the max_alpha gradient gate) can differ in their
- * last-ulp window, reported through the ambiguity flags. */
-#define AMB_ALPHA 1  /* unused: the alpha-threshold decision is exact */
+ * way, and alpha = min(max_alpha, 2^p).  The decision is exact for this
+ * base-2 form, not for the reference's own form (below), which rounds power
+ * differently and takes exp: the two can disagree where alpha lies within
+ * rounding of alpha_threshold, flagged AMB_ALPHA.  2^p is rounded once from
+ * double; the hardware exp2 is within 1 ulp, so later decisions that depend
+ * on the value of alpha (early stop on T, the max_alpha gradient gate) can
+ * differ in their last-ulp window, reported through the ambiguity flags. */
+#define AMB_ALPHA 1  /* the reference's form may decide the alpha test otherwise */
 #define AMB_STOP 2   /* T within rounding of transmittance_threshold */
 #define AMB_GATE 4   /* raw alpha within rounding of max_alpha (gradient gate) */
 #define AMB_FORCED_BAD 8 /* a forced stop lies outside the ambiguity window */
+#define AMB_ALPHA_FLIP 16 /* ... and does: the two forms' decisions differ */
 #define AMB_REL 4e-7f
+/* AMB_ALPHA window: the reference's raw alpha within this many float ulps
+ * (2^-24 relative) of alpha_threshold.  Its exp is libm's here, torch's in
+ * the dense reference and Metal's in the reference kernels (a few ulps
+ * apart). */
+#define AMB_ALPHA_ULPS 16.0f
 
 static void splat_exponents(const splat_t* s, float dx, float dy, float* e, float* p) {
   const float A = (-0.5f * s->a) * LOG2E_F, B = (-s->b) * LOG2E_F;
@@ -380,13 +389,46 @@ static void splat_exponents(const splat_t* s, float dx, float dy, float* e, floa
   *p = fmaf(t, dy, a0 + s->lo);
 }
 
+/* The reference's own visibility decision (gsplat_v8_kernels.metal:129-138;
+ * the dense Torch reference computes the same expression): float32, left to
+ * right, no contraction (this file is built with -ffp-contract=off), exp
+ * from libm.  *raw_ref = o exp(power) (0 when power > 0). */
+static int ref_form_visible(const oracle_meta* M, const splat_t* s, float dx, float dy, float* raw_ref) {
+  const float power = -0.5f * (s->a * dx * dx + 2.0f * s->b * dx * dy + s->c * dy * dy);
+  if (power > 0.0f) {
+    *raw_ref = 0.0f;
+    return 0;
+  }
+  *raw_ref = s->o * expf(power);
+  return fminf(M->max_alpha, *raw_ref) >= M->alpha_threshold;
+}
+
 static int eval_alpha(const oracle_meta* M, const splat_t* s, float px, float py,
                       float* alpha, float* raw, float* dx, float* dy, int* amb) {
   *dx = px - s->mx;
   *dy = py - s->my;
   float e, p;
   splat_exponents(s, *dx, *dy, &e, &p);
-  if (!(e <= 0.0f && p >= s->q)) return 0;
+  const int vis = e <= 0.0f && p >= s->q;
+  if (amb) {
+    /* Near either threshold of the base-2 form (p - q and e in log2 units):
+     * compare with the reference's form.  The two forms' distances to the
+     * threshold differ by the rounding of power (a few ulps of m, the sum of
+     * the magnitudes of its terms), of lo and plim (ulps of |log2 thr|) and
+     * of exp: far below this margin, so no disagreement lies outside it. */
+    const float m = 0.5f * (fabsf(s->a) * *dx * *dx + 2.0f * fabsf(s->b * *dx * *dy) + fabsf(s->c) * *dy * *dy);
+    const float near = 0x1p-10f + 0x1p-16f * m;
+    if (fabsf(p - s->q) <= near || fabsf(e) <= near) {
+      float raw_ref;
+      const int vis_ref = ref_form_visible(M, s, *dx, *dy, &raw_ref);
+      if (vis_ref != vis)
+        *amb |= AMB_ALPHA | AMB_ALPHA_FLIP;
+      else if (raw_ref > 0.0f &&
+               fabsf(raw_ref - M->alpha_threshold) <= AMB_ALPHA_ULPS * 0x1p-24f * M->alpha_threshold)
+        *amb |= AMB_ALPHA;
+    }
+  }
+  if (!vis) return 0;
   *raw = (float)exp2((double)p);
   *alpha = fminf(M->max_alpha, *raw);
   if (amb && fabsf(*raw - M->max_alpha) <= AMB_REL * M->max_alpha) *amb |= AMB_GATE;

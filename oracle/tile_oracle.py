@@ -154,7 +154,7 @@ def bin_scene(meta: OracleMeta, s: Scene) -> OracleBins:
     return OracleBins(perm, counts, offsets, ids)
 
 
-AMB_ALPHA, AMB_STOP, AMB_GATE, AMB_FORCED_BAD = 1, 2, 4, 8
+AMB_ALPHA, AMB_STOP, AMB_GATE, AMB_FORCED_BAD, AMB_ALPHA_FLIP = 1, 2, 4, 8, 16
 
 # Gradient entries per splat in the bound arrays of render_backward:
 # means2d x, y; conics a, b, c; colors r, g, b; opacity.
@@ -184,7 +184,14 @@ def render_forward(meta: OracleMeta, s: Scene, bins: OracleBins, with_ambiguity:
     bit mask: AMB_STOP when an early-stop decision of the pixel lies within
     exp's last-ulp window (another implementation with a 1-ulp exp2 may decide
     it the other way), AMB_GATE likewise for the max_alpha gradient gate.  The
-    alpha-threshold decision itself is exact (AMB_ALPHA is never set).
+    alpha-threshold decision is exact for the base-2 form the oracle and the
+    HIP compositors share (tile_oracle.c: eval_alpha), not for the reference's
+    own form min(max_alpha, o exp(power)) >= alpha_threshold
+    (gsplat_v8_kernels.metal:121-139): AMB_ALPHA marks pixels where, before
+    the pixel stopped, the reference's form was within AMB_ALPHA_ULPS ulps of
+    the threshold or decided otherwise, and AMB_ALPHA_FLIP those where it
+    decided otherwise.  Such pixels may differ from the reference by up to
+    T * alpha_threshold * |colour - background| per flagged evaluation.
 
     force_last [B,H,W] int32 (-1 = the oracle decides): walk exactly that many
     records of the pixel's tile list (another implementation's stop count);
