@@ -498,6 +498,18 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
     splat_offsets[P.num_splats] = end > 0x7fffffffLL ? -1 : (int)end;
 }
 
+// The records of splats already in depth order (orig = gid), for callers
+// that hold the depth-sorted flat attribute arrays themselves (the
+// reference's op roles take those arrays, not packed records).
+__global__ __launch_bounds__(kThreads) void pack_records_kernel(
+    RasterParams P, const float* __restrict__ means2d,
+    const float* __restrict__ conics, const float* __restrict__ colors,
+    const float* __restrict__ opacities, float4* __restrict__ packed) {
+  const int gid = (int)blockIdx.x * kThreads + (int)threadIdx.x;
+  if (gid < P.num_splats)
+    pack_record(P, means2d, conics, colors, opacities, packed, gid, gid);
+}
+
 // emit_kernel<true>: the pair offsets are scanned by the emit itself.
 struct EmitScan {
   const int32_t* gid_count;     // per-gid tile-hit counts
@@ -1055,6 +1067,18 @@ int launch_pack(const RasterParams& P, const float* means2d,
                      reinterpret_cast<float4*>(packed), splat_offsets,
                      scan_status, scan_ticket, err);
   return check_launch("pack_kernel");
+}
+
+int launch_pack_records(const RasterParams& P, const float* means2d,
+                        const float* conics, const float* colors,
+                        const float* opacities, float* packed,
+                        hipStream_t stream) {
+  if (P.num_splats == 0) return GSPLAT_OK;
+  const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
+  hipLaunchKernelGGL(pack_records_kernel, dim3(grid), dim3(kThreads), 0,
+                     stream, P, means2d, conics, colors, opacities,
+                     reinterpret_cast<float4*>(packed));
+  return check_launch("pack_records_kernel");
 }
 
 int count_scan_blocks(const RasterParams& P) {

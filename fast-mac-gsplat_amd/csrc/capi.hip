@@ -305,6 +305,20 @@ int gsplat_hip_bin_depth_order(const gsplat_raster_meta* meta,
   return rc;
 }
 
+int gsplat_hip_pack_records(const gsplat_raster_meta* meta,
+                            const float* means2d, const float* conics,
+                            const float* colors, const float* opacities,
+                            float* packed, void* stream) {
+  RasterParams P;
+  int rc = make_params(meta, P);
+  if (rc) return rc;
+  rc = null_check({means2d, conics, colors, opacities, packed},
+                  "gsplat_hip_pack_records");
+  if (rc) return rc;
+  return gs::launch_pack_records(P, means2d, conics, colors, opacities, packed,
+                                 static_cast<hipStream_t>(stream));
+}
+
 int gsplat_hip_bin_pack(const gsplat_raster_meta* meta, const float* means2d,
                         const float* conics, const float* colors,
                         const float* opacities, const int32_t* perm,

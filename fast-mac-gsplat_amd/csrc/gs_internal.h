@@ -147,6 +147,12 @@ int launch_pack(const RasterParams& P, const float* means2d,
                 int32_t* splat_offsets, uint64_t* scan_status,
                 uint32_t* scan_ticket, uint32_t* err, hipStream_t stream);
 int count_scan_blocks(const RasterParams& P);
+// pack_records: the packed records of splats already in depth order
+// (record gid from attributes gid, orig = gid).
+int launch_pack_records(const RasterParams& P, const float* means2d,
+                        const float* conics, const float* colors,
+                        const float* opacities, float* packed,
+                        hipStream_t stream);
 // Words that a launch zeroes on the side (n 32-bit words at p).
 struct ZeroSpan {
   uint32_t* p;

@@ -13,6 +13,7 @@ from .rasterize import (
 )
 from .project import project_pinhole_gaussians, rasterize_pinhole_gaussians
 from . import ops  # noqa: F401  (registers torch.ops.gsplat_hip.*)
+from . import v8_ops  # noqa: F401  (registers the reference's torch.ops.gsplat_metal_v8.*)
 
 __all__ = [
     "RasterConfig",

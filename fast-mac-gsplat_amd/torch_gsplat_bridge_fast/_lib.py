@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("GSPLAT_HIP_LIB", os.path.join(_HERE, "lib", "libgsplat_hip.so"))
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 TILE_SIZE = 16
 RECORD_FLOATS = 12
 PROJECT_NOALLOC_SCRATCH_BYTES = 1 << 20   # GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES
@@ -70,6 +70,7 @@ SIGNATURES = {
     "gsplat_hip_bin_count": (ctypes.c_int, [_PM] + [_vp] * 4 + [_vp, _sz, _vp]),
     "gsplat_hip_bin_depth_order": (ctypes.c_int, [_PM, _vp, _vp, _vp, _sz, _vp]),
     "gsplat_hip_bin_pack": (ctypes.c_int, [_PM] + [_vp] * 7 + [_vp, _sz, _vp]),
+    "gsplat_hip_pack_records": (ctypes.c_int, [_PM] + [_vp] * 5 + [_vp]),
     "gsplat_hip_bin_emit_workspace_bytes": (_sz, [_PM, _i64]),
     "gsplat_hip_bin_emit": (ctypes.c_int, [_PM, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _vp]),
     "gsplat_hip_bin_workspace_bytes": (_sz, [_PM, _i64]),

@@ -24,7 +24,9 @@ same):
     ``stop_count_mode`` and ``stop_count_dense_threshold`` are validated like
     the reference but do not change the computation: empty tiles cost one
     early-exiting wavefront, and backward always uses exact per-pixel stop
-    state saved by forward.  ``max_pairs_per_launch`` splits training batches
+    state saved by forward.  profile_projected_gaussians reports the
+    reference's active-tile decision and its stop counts (0 for tiles above
+    max_fast_pairs).  ``max_pairs_per_launch`` splits training batches
     into launches of at most that many tile pairs, as the reference does.
 """
 from __future__ import annotations
@@ -144,6 +146,22 @@ def _effective_active_policy(config: RasterConfig) -> str:
     if config.active_policy == "off" and config.use_active_tiles:
         return "on"
     return config.active_policy
+
+
+def _resolve_active_tile_use(policy: str, active_fraction: float, overflow_tiles: int, max_pairs: int,
+                             max_fast_pairs: int) -> bool:
+    """The reference's choice between its active-tile and its fast kernels for one launch
+    (v8 rasterize.py:401-424): "on" / "off" as given; "auto" takes the active-tile kernels for
+    sparse images (under 10% of the tiles occupied), when a tile overflows max_fast_pairs or one
+    holds more than twice that, and never when over 75% of the tiles are occupied with no
+    overflow.  Here both kernel sets are one compositor; the choice is reported only."""
+    if policy == "off":
+        return False
+    if policy == "on":
+        return True
+    if active_fraction > 0.75 and overflow_tiles == 0:
+        return False
+    return active_fraction < 0.10 or overflow_tiles > 0 or max_pairs > 2 * max_fast_pairs
 
 
 def _meta(config: RasterConfig, batch_size: int, gaussians_per_batch: int) -> _lib.RasterMeta:
@@ -344,7 +362,11 @@ def rasterize_projected_gaussians(means2d: Tensor, conics: Tensor, colors: Tenso
 def profile_projected_gaussians(means2d: Tensor, conics: Tensor, colors: Tensor, opacities: Tensor,
                                 depths: Tensor, config: RasterConfig, *, run_forward: bool = False,
                                 return_image: bool = False) -> Dict[str, Any]:
-    """Tile statistics with the reference's keys (v8 rasterize.py:860-1014)."""
+    """Tile statistics with the reference's keys and meaning (v8 rasterize.py:860-1014).  The stop
+    count statistics are those of the reference's fast kernels: a tile above max_fast_pairs (left
+    to the reference's overflow path) or without pairs counts as 0 (gsplat_v8_kernels.metal:
+    423-431); resolved_use_active_tiles / resolved_active_chunks report the reference's policy
+    decision per launch."""
     _check_inputs(means2d, conics, colors, opacities, depths)
     means2d_b, conics_b, colors_b, opacities_b, depths_b, was_batched = _normalize_inputs(
         means2d, conics, colors, opacities, depths)
@@ -354,30 +376,40 @@ def profile_projected_gaussians(means2d: Tensor, conics: Tensor, colors: Tensor,
     chunk_b = _choose_batch_chunk_size(config, B, G, tiles_per_image)
     slices = _choose_batch_slices(means2d_b, conics_b, colors_b, opacities_b, depths_b, config,
                                   train_mode=True, tiles_per_image=tiles_per_image)
-    counts_all, stops_all, images = [], [], []
+    mfp = int(config.max_fast_pairs)
+    counts_all, stops_all, images, chunk_rows = [], [], [], []
     for b0, b1 in slices:
         args = _flat(means2d_b[b0:b1], conics_b[b0:b1], colors_b[b0:b1], opacities_b[b0:b1], depths_b[b0:b1])
         meta = _meta(config, b1 - b0, G)
         st = _ops.bin_gaussians(meta, *args)
-        counts_all.append(st.tile_counts)
+        cnt = st.tile_counts
+        counts_all.append(cnt)
+        # per launch: occupied fraction, overflowing tiles, largest tile (the policy's inputs)
+        chunk_rows.append(torch.stack([(cnt > 0).sum().to(torch.float32) / max(cnt.numel(), 1),
+                                       (cnt > mfp).sum().to(torch.float32), cnt.max().to(torch.float32)]))
         if run_forward or return_image:
             img, _, _, tile_stop, _ = _ops.render_forward(meta, st, save_state=True)
-            stops_all.append(tile_stop)
+            # the reference's fast kernels report 0 for the tiles they leave to the overflow path
+            stops_all.append(torch.where(cnt <= mfp, tile_stop, torch.zeros_like(tile_stop)))
             if return_image:
                 images.append(img)
     # The statistics are reduced on the device; one small vector comes back.
     counts = torch.cat(counts_all).to(torch.float32)
     n = counts.numel()
     occupied = counts > 0
-    fast = occupied & (counts <= int(config.max_fast_pairs))
+    fast = occupied & (counts <= mfp)
     dense = counts >= int(config.stop_count_dense_threshold)
     if n:
-        vec = torch.stack([counts.sum(), counts.mean(), torch.quantile(counts, 0.95), counts.max(),
-                           (counts > int(config.max_fast_pairs)).sum().to(torch.float32),
-                           fast.sum().to(torch.float32), occupied.sum().to(torch.float32),
-                           (fast & dense).sum().to(torch.float32)]).tolist()
+        vec = torch.cat([torch.stack([counts.sum(), counts.mean(), torch.quantile(counts, 0.95), counts.max(),
+                                      (counts > mfp).sum().to(torch.float32),
+                                      fast.sum().to(torch.float32), occupied.sum().to(torch.float32),
+                                      (fast & dense).sum().to(torch.float32)])]
+                        + chunk_rows).tolist()
     else:
         vec = [0.0] * 8
+    policy = _effective_active_policy(config)
+    resolved = [_resolve_active_tile_use(policy, vec[8 + 3 * k], int(vec[9 + 3 * k]), int(vec[10 + 3 * k]), mfp)
+                for k in range(len(chunk_rows))] if n else [False for _ in slices]
     stats: Dict[str, Any] = {
         "batch_size": int(B),
         "gaussians_per_batch": int(G),
@@ -396,9 +428,9 @@ def profile_projected_gaussians(means2d: Tensor, conics: Tensor, colors: Tensor,
         "chosen_batch_chunk": int(chunk_b),
         "chosen_batch_chunks": [int(b1 - b0) for b0, b1 in slices],
         "max_pairs_per_launch": int(config.max_pairs_per_launch),
-        "active_policy": _effective_active_policy(config),
-        "resolved_use_active_tiles": False,
-        "resolved_active_chunks": [False for _ in slices],
+        "active_policy": policy,
+        "resolved_use_active_tiles": bool(any(resolved)),
+        "resolved_active_chunks": [bool(x) for x in resolved],
         "stop_count_mode": config.stop_count_mode,
     }
     if stops_all and n:

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 12
+#define GSPLAT_HIP_ABI_VERSION 13
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -159,6 +159,20 @@ int gsplat_hip_bin_pack(const gsplat_raster_meta* meta,
                         const int32_t* perm, float* packed,
                         int32_t* splat_offsets, void* workspace,
                         size_t workspace_bytes, void* stream);
+
+/* Packed records of splats that are already in depth order (record i from
+ * attributes i: gradients of the compositor come back in this same order).
+ * Inputs: means2d [BG,2], conics [BG,3], colors [BG,3], opacities [BG];
+ * output packed float [BG*12].  The reference's compositor ops take the
+ * depth-sorted flat arrays themselves and read them by binned id
+ * (torch.ops.gsplat_metal_v8.render_* with the gathers of v8 rasterize.py:
+ * 466-475 done by the caller; load_chunk_params in gsplat_v8_kernels.metal):
+ * a caller that holds those arrays packs them with this call before
+ * gsplat_hip_render_forward / _backward. */
+int gsplat_hip_pack_records(const gsplat_raster_meta* meta,
+                            const float* means2d, const float* conics,
+                            const float* colors, const float* opacities,
+                            float* packed, void* stream);
 
 size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
                                            int64_t n_pairs);

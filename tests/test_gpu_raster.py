@@ -433,15 +433,21 @@ def test_eval_path_vs_tile_oracle(gpu):
                   "eval path")
 
 
-def test_profile_statistics_match_oracle(gpu):
+@pytest.mark.parametrize("policy,strategy", [("auto", "serial"), ("off", "auto")])
+def test_profile_statistics_match_oracle(gpu, policy, strategy):
     """profile_projected_gaussians (reference v8 rasterize.py:860-1014) reduces
     its statistics on the device; they equal the statistics of the tile
-    oracle's tile counts and stop counts."""
+    oracle's tile counts and stop counts, with the reference's meaning: a tile
+    above max_fast_pairs (the reference's overflow path) or without pairs has a
+    stop count of 0 (gsplat_v8_kernels.metal:423-431), and
+    resolved_active_chunks is the reference's policy decision per launch
+    (v8 rasterize.py:401-424), here per image (serial launches) or for the
+    whole batch."""
     from torch_gsplat_bridge_fast import profile_projected_gaussians
 
-    B, G, H, W = 2, 4000, 128, 192
+    B, G, H, W, mfp = 2, 4000, 128, 192, 300
     sc = make_scene_2d(3, seed=1, G=G, B=B, H=H, W=W)
-    cfg = RasterConfig(height=H, width=W, max_fast_pairs=300)
+    cfg = RasterConfig(height=H, width=W, max_fast_pairs=mfp, active_policy=policy, batch_strategy=strategy)
     with torch.no_grad():
         out = profile_projected_gaussians(*[sc[k].to(gpu) for k in KEYS], cfg, run_forward=True, return_image=True)
     st_ = out["stats"]
@@ -451,12 +457,13 @@ def test_profile_statistics_match_oracle(gpu):
     _, (oimg, _, _, ostop), _ = parity.gpu_decisions(meta, s, bins, gpu_state(sc, H, W, B, G, (0, 0, 0))[1])
     parity.check_image(out["image"].cpu().numpy(), oimg, "profile image")
     c = bins.tile_counts.astype(np.float64)
-    stop = ostop.astype(np.float64)
+    assert (c > mfp).sum() > 0 and (ostop[c > mfp] > 0).all()      # overflow tiles with real stops
+    stop = np.where(c <= mfp, ostop, 0).astype(np.float64)
     assert st_["tiles"] == c.size and st_["total_pairs"] == int(c.sum())
     assert st_["max_pairs_per_tile"] == int(c.max()) and st_["max_stop_count"] == int(stop.max())
-    assert st_["overflow_tile_count"] == int((c > 300).sum())
-    assert st_["active_tile_count"] == int(((c > 0) & (c <= 300)).sum())
-    assert st_["dense_active_tile_count"] == int(((c > 0) & (c <= 300) & (c >= 64)).sum())
+    assert st_["overflow_tile_count"] == int((c > mfp).sum())
+    assert st_["active_tile_count"] == int(((c > 0) & (c <= mfp)).sum())
+    assert st_["dense_active_tile_count"] == int(((c > 0) & (c <= mfp) & (c >= 64)).sum())
     np.testing.assert_allclose(st_["active_tile_fraction"], (c > 0).mean(), rtol=1e-6)
     np.testing.assert_allclose(st_["mean_pairs_per_tile"], c.mean(), rtol=1e-5)
     np.testing.assert_allclose(st_["p95_pairs_per_tile"], np.quantile(c, 0.95), rtol=1e-5)
@@ -465,6 +472,21 @@ def test_profile_statistics_match_oracle(gpu):
     ratio = np.where(c > 0, stop / np.maximum(c, 1), 0)
     np.testing.assert_allclose(st_["mean_stop_ratio"], ratio.mean(), rtol=1e-5)
     np.testing.assert_allclose(st_["p95_stop_ratio"], np.quantile(ratio, 0.95), rtol=1e-5)
+    # the reference's policy per launch, restated
+    launches = [c[b * (c.size // B):(b + 1) * (c.size // B)] for b in range(B)] if strategy == "serial" else [c]
+    want = []
+    for lc in launches:
+        frac, over, mx = (lc > 0).mean(), int((lc > mfp).sum()), int(lc.max())
+        if policy == "off":
+            want.append(False)
+        elif frac > 0.75 and over == 0:
+            want.append(False)
+        else:
+            want.append(bool(frac < 0.10 or over > 0 or mx > 2 * mfp))
+    assert st_["resolved_active_chunks"] == want and st_["resolved_use_active_tiles"] == any(want)
+    assert st_["chosen_batch_chunks"] == ([1] * B if strategy == "serial" else [B])
+    if policy == "auto":
+        assert any(want)
 
 
 def test_recorded_trace_vs_tile_oracle(gpu, tmp_path):
