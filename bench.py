@@ -12,7 +12,9 @@ steps run at the GPU's working clocks (reported as `clock_ramp`).
 Prints ONE JSON line.  `roofline` is for the dominant kernel (the backward
 compositor, which dominates step time): its launch time is measured live with
 HIP events (torch.cuda.Event on the stream the library launches on) over the
-timed steps.  `cpu_baseline` times the CPU oracle (the C
+timed steps.  `stage_ms` / `stage_roofline` give every kernel of the step, timed
+by events attached to each launch over a few untimed steps after the timed
+region (the same path; gsplat_hip_trace_launches).  `cpu_baseline` times the CPU oracle (the C
 restatement of the reference algorithm, oracle/tile_oracle.c, on the host's
 threads) on the same scene, forward+backward, once, and the reference's
 dense Torch renderer on config 0.
@@ -50,35 +52,62 @@ PEAK_FP32_TFLOPS = 157.3   # MI355X published fp32 peak
 PEAK_HBM_GBS = 8000.0      # MI355X published HBM3E bandwidth
 
 
-def stage_roofline(op_ms, BG, N, walked, T, P, three_d, depth_passes=4, pair_passes=2):
-    """Achieved fraction of each stage against its bound, from the per-unit
-    algorithmic work of the survey's measurement table: bytes for the
-    binning and projection stages (HBM), FLOP for the compositors (VALU)
-    over the `walked` pairs (each tile's list up to its stop).  A stage's
-    time is the mean of its C-ABI call over the breakdown pass."""
-    work = {
-        "project_forward": ("hbm", 72.0 * BG),
-        "project_backward": ("hbm", 116.0 * BG),
-        "bin_count": ("hbm", 28.0 * BG),
-        # depth sort (24 B per splat and pass) + packing (48 B records + 36 B gathered)
-        "bin_pack": ("hbm", 24.0 * BG * depth_passes + 84.0 * BG),
-        # emit (24 B/splat + 12 B/pair), pair sort (24 B/pair/pass), ranges (8 B/pair + 8 B/tile)
-        "bin_emit": ("hbm", 24.0 * BG + 12.0 * N + 24.0 * N * pair_passes + 8.0 * N + 8.0 * T),
-        "render_forward": ("valu", 256.0 * walked * FLOP_PER_EVAL["render_forward"]),
-        "render_backward": ("valu", 256.0 * walked * FLOP_PER_EVAL["render_backward"]),
+# Algorithmic work of one launch of each kernel the step runs, from the
+# per-unit figures of the measurement plan: (bound, bytes or FLOP, what is
+# counted), in BG splats, N tile pairs, T tiles and `walked` pairs (each tile's
+# list up to its stop).  Bytes are those a kernel must move (reads + writes);
+# FLOP for the compositors are per (pixel, walked pair) evaluation.
+def kernel_work(name, BG, N, walked, T):
+    table = {
+        "count_depth_runs_kernel": ("hbm", 40.0 * BG,
+                                    "40 B/splat: count 24 read + 4 written, depth runs 4 read + 8 written"),
+        "rank_pack_kernel": ("hbm", 104.0 * BG, "104 B/splat: run keys+values 8, attributes 36, count 4 read; "
+                                                "record 48, perm 4, count 4 written"),
+        "emit_kernel<true>": ("hbm", 32.0 * BG + 8.0 * N, "32 B/splat (record 24, count 4 read, offset 4 written) "
+                                                         "+ 8 B/pair (key, value)"),
+        "emit_kernel<false>": ("hbm", 28.0 * BG + 8.0 * N, "28 B/splat (record 24, offset 4) + 8 B/pair"),
+        "count_kernel": ("hbm", 28.0 * BG, "28 B/splat: means 8, conic 12, opacity 4 read, count 4 written"),
+        "depth_run_sort_kernel": ("hbm", 12.0 * BG, "12 B/splat: depth 4 read, run key + value 8 written"),
+        "depth_run_rank_kernel": ("hbm", 12.0 * BG, "12 B/splat: run key + value 8 read, perm 4 written"),
+        "pack_kernel": ("hbm", 96.0 * BG, "96 B/splat: perm 4, attributes 36, count 4 read; record 48, offset 4 "
+                                          "written"),
+        "rs_global_hist_kernel(depth)": ("hbm", 4.0 * BG, "4 B/splat (depth keys read)"),
+        "rs_global_hist_kernel(keys)": ("hbm", 4.0 * N, "4 B/pair (keys read)"),
+        "rs_onesweep_kernel(depth)": ("hbm", 16.0 * BG, "16 B/splat per pass (key + value read and written)"),
+        "rs_onesweep_kernel(keys)": ("hbm", 16.0 * N, "16 B/pair per pass (key + value read and written)"),
+        "ranges_kernel": ("hbm", 4.0 * N + 4.0 * T, "4 B/pair (sorted keys read) + 4 B/tile (offsets written)"),
+        "bucket_sort_kernel": ("hbm", 12.0 * N + 4.0 * T + 64.0 * BG,
+                               "12 B/pair (key, value read; id written) + 4 B/tile + 64 B/splat (gradient record "
+                               "zeroed)"),
+        "render_grads_unpack_kernel": ("hbm", 164.0 * BG, "164 B/splat: record 64 read, gradients 36 written, "
+                                                          "record 64 zeroed"),
+        "project_fwd_kernel": ("hbm", 72.0 * BG, "72 B/splat: 44 read + 28 written"),
+        "project_bwd_kernel": ("hbm", 116.0 * BG, "116 B/splat: 72 read + 44 written"),
+        "render_fwd_kernel": ("valu", 256.0 * walked * FLOP_PER_EVAL["render_forward"],
+                              "256 x walked pairs x 24 FLOP"),
+        "render_bwd_kernel": ("valu", 256.0 * walked * FLOP_PER_EVAL["render_backward"],
+                              "256 x walked pairs x 60 FLOP"),
     }
+    return table.get(name)
+
+
+def stage_roofline(stage_ms, BG, N, walked, T):
+    """Achieved fraction of each kernel's roof: its algorithmic work per launch (kernel_work) over
+    its mean traced launch time."""
     out = {}
-    for k, ms in op_ms.items():
-        if k not in work or ms <= 0:
+    for name, ms in stage_ms.items():
+        w = kernel_work(name, BG, N, walked, T)
+        if w is None or ms <= 0:
             continue
-        bound, units = work[k]
+        bound, units, what = w
         if bound == "hbm":
             a = units / (ms * 1e-3) / 1e9
-            out[k] = {"bound": "hbm", "achieved": round(a, 1), "unit": "GB/s", "frac": round(a / PEAK_HBM_GBS, 4)}
+            out[name] = {"bound": "hbm", "achieved": round(a, 1), "unit": "GB/s", "frac": round(a / PEAK_HBM_GBS, 4),
+                         "work": what}
         else:
             a = units / (ms * 1e-3) / 1e12
-            out[k] = {"bound": "valu", "achieved": round(a, 2), "unit": "TFLOP/s",
-                      "frac": round(a / PEAK_FP32_TFLOPS, 4)}
+            out[name] = {"bound": "valu", "achieved": round(a, 2), "unit": "TFLOP/s",
+                         "frac": round(a / PEAK_FP32_TFLOPS, 4), "work": what}
     return out
 
 
@@ -354,13 +383,20 @@ def main() -> int:
     comp_ms = op_means(_ops.pop_timing())
     ms_per_step = (t1 - t0) * 1e3 / args.steps
 
-    # Per-stage breakdown, after the timed region: every C-ABI call bracketed.
+    # Per-kernel breakdown, after the timed region: every kernel launch of
+    # n_stage untimed steps of the same path carries HIP events attached to
+    # the launch itself (gsplat_hip_trace_launches), so each figure is that
+    # kernel's own duration in the step's own launch sequence.
     n_stage = max(1, min(args.steps, 5))
-    _ops.set_timing(True, pool=24 * n_stage)
-    for _ in range(n_stage):
-        step()
-    torch.cuda.synchronize()
-    op_ms = op_means(_ops.pop_timing())
+    trace = _ops.LaunchTrace(capacity=min(1024, 64 * n_stage))
+    with trace:
+        for _ in range(n_stage):
+            step()
+    per_kernel = {}
+    for name, ms in trace.launches:
+        per_kernel.setdefault(name, []).append(ms)
+    stage_ms = {k: float(np.mean(v)) for k, v in per_kernel.items()}
+    stage_launches = {k: len(v) / n_stage for k, v in per_kernel.items()}
 
     with torch.no_grad():
         if three_d:
@@ -408,9 +444,11 @@ def main() -> int:
             "loss": "sum(image * w), w ~ U(0,1) seed 123",
             "parallelism": "single GPU",
         },
-        "stage_ms": {k: round(v, 4) for k, v in op_ms.items()},
-        "stage_roofline": stage_roofline(op_ms, B * G, n_pairs, walked, n_tiles, B * H * W, three_d,
-                                         pair_passes=(max(n_tiles - 1, 0).bit_length() + 7) // 8),
+        "stage_source": f"kernel trace of {n_stage} untimed steps after the timed region (events attached to "
+                        "each launch, gsplat_hip_trace_launches): mean ms per launch, launches per step",
+        "stage_ms": {k: round(v, 4) for k, v in sorted(stage_ms.items(), key=lambda kv: -kv[1])},
+        "stage_launches_per_step": stage_launches,
+        "stage_roofline": stage_roofline(stage_ms, B * G, n_pairs, walked, n_tiles),
         "roofline": {
             "kernel": f"{dom} ({'render_bwd_kernel' if dom == 'render_backward' else 'render_fwd_kernel'})",
             "launch_us": round(comp_ms[dom] * 1e3, 2),

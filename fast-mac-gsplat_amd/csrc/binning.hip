@@ -999,13 +999,13 @@ int launch_count(const RasterParams& P, const float* means2d,
                  int32_t* pair_count, uint32_t* zero_words,
                  int64_t n_zero_words, hipStream_t stream) {
   const int nblk = count_blocks(P);
-  hipLaunchKernelGGL(count_kernel, dim3((unsigned)nblk), dim3(kThreads), 0,
-                     stream, P, means2d, conics, opacities, splat_count,
-                     block_sums, zero_words, n_zero_words);
+  launch_traced("count_kernel", count_kernel, dim3((unsigned)nblk),
+                dim3(kThreads), 0, stream, P, means2d, conics, opacities,
+                splat_count, block_sums, zero_words, n_zero_words);
   int rc = check_launch("count_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(sum_kernel, dim3(1), dim3(kThreads), 0, stream,
-                     block_sums, nblk, pair_count);
+  launch_traced("sum_kernel", sum_kernel, dim3(1), dim3(kThreads), 0, stream,
+                block_sums, nblk, pair_count);
   return check_launch("sum_kernel");
 }
 
@@ -1022,12 +1022,12 @@ int launch_count_depth_runs(const RasterParams& P, const float* means2d,
   const int run_blocks = P.batch * runs;
   constexpr int kSplatsPerBlock = run_step::kRunWaves * kWalkSplats;
   const int cblocks = (P.num_splats + kSplatsPerBlock - 1) / kSplatsPerBlock;
-  hipLaunchKernelGGL(count_depth_runs_kernel,
-                     dim3((unsigned)(run_blocks + cblocks)),
-                     dim3(run_step::kRunThreads), 0, stream, P, means2d, conics,
-                     opacities, splat_count, zero_words, n_zero_words, depths,
-                     runs, run_blocks,
-                     run_step::run_buffers(depth_buffers, P.gpb, P.batch));
+  launch_traced("count_depth_runs_kernel", count_depth_runs_kernel,
+                dim3((unsigned)(run_blocks + cblocks)),
+                dim3(run_step::kRunThreads), 0, stream, P, means2d, conics,
+                opacities, splat_count, zero_words, n_zero_words, depths, runs,
+                run_blocks,
+                run_step::run_buffers(depth_buffers, P.gpb, P.batch));
   return check_launch("count_depth_runs_kernel");
 }
 
@@ -1043,14 +1043,13 @@ int launch_rank_pack(const RasterParams& P, const float* means2d,
   }
   const int blocks_per_seg =
       (P.gpb + run_step::kRankElems - 1) / run_step::kRankElems;
-  hipLaunchKernelGGL(rank_pack_kernel,
-                     dim3((unsigned)((int64_t)P.batch * blocks_per_seg)),
-                     dim3(run_step::kRankBlock), 0, stream, P, means2d, conics,
-                     colors, opacities,
-                     run_step::run_buffers(depth_buffers, P.gpb, P.batch),
-                     run_step::runs_of(P.gpb), splat_count, perm,
-                     reinterpret_cast<float4*>(packed), gid_count,
-                     block_totals);
+  launch_traced("rank_pack_kernel", rank_pack_kernel,
+                dim3((unsigned)((int64_t)P.batch * blocks_per_seg)),
+                dim3(run_step::kRankBlock), 0, stream, P, means2d, conics,
+                colors, opacities,
+                run_step::run_buffers(depth_buffers, P.gpb, P.batch),
+                run_step::runs_of(P.gpb), splat_count, perm,
+                reinterpret_cast<float4*>(packed), gid_count, block_totals);
   return check_launch("rank_pack_kernel");
 }
 
@@ -1062,10 +1061,10 @@ int launch_pack(const RasterParams& P, const float* means2d,
                 uint32_t* scan_ticket, uint32_t* err, hipStream_t stream) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
-  hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(kThreads), 0, stream, P,
-                     means2d, conics, colors, opacities, perm, splat_count,
-                     reinterpret_cast<float4*>(packed), splat_offsets,
-                     scan_status, scan_ticket, err);
+  launch_traced("pack_kernel", pack_kernel, dim3(grid), dim3(kThreads), 0,
+                stream, P, means2d, conics, colors, opacities, perm,
+                splat_count, reinterpret_cast<float4*>(packed), splat_offsets,
+                scan_status, scan_ticket, err);
   return check_launch("pack_kernel");
 }
 
@@ -1075,9 +1074,9 @@ int launch_pack_records(const RasterParams& P, const float* means2d,
                         hipStream_t stream) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
-  hipLaunchKernelGGL(pack_records_kernel, dim3(grid), dim3(kThreads), 0,
-                     stream, P, means2d, conics, colors, opacities,
-                     reinterpret_cast<float4*>(packed));
+  launch_traced("pack_records_kernel", pack_records_kernel, dim3(grid),
+                dim3(kThreads), 0, stream, P, means2d, conics, colors,
+                opacities, reinterpret_cast<float4*>(packed));
   return check_launch("pack_records_kernel");
 }
 
@@ -1103,25 +1102,25 @@ int launch_emit(const RasterParams& P, const float* packed,
   if (scan != nullptr) {
     const EmitScan sc{scan->gid_count, scan->splat_offsets,
                       scan->block_totals};
-    hipLaunchKernelGGL(emit_kernel<true>, dim3((unsigned)nblk), dim3(kThreads),
-                       0, stream, P, reinterpret_cast<const float4*>(packed),
-                       nullptr, capacity, keys, vals, pair_passes, hist_shift,
-                       hist_partials, direct ? pair_ghist : nullptr,
-                       pair_status, pair_status_words, sc);
+    launch_traced("emit_kernel<true>", emit_kernel<true>, dim3((unsigned)nblk),
+                  dim3(kThreads), 0, stream, P,
+                  reinterpret_cast<const float4*>(packed), nullptr, capacity,
+                  keys, vals, pair_passes, hist_shift, hist_partials,
+                  direct ? pair_ghist : nullptr, pair_status, pair_status_words,
+                  sc);
   } else {
-    hipLaunchKernelGGL(emit_kernel<false>, dim3((unsigned)nblk),
-                       dim3(kThreads), 0, stream, P,
-                       reinterpret_cast<const float4*>(packed), splat_offsets,
-                       capacity, keys, vals, pair_passes, hist_shift,
-                       hist_partials, direct ? pair_ghist : nullptr,
-                       pair_status,
-                       pair_status_words, EmitScan{});
+    launch_traced("emit_kernel<false>", emit_kernel<false>,
+                  dim3((unsigned)nblk), dim3(kThreads), 0, stream, P,
+                  reinterpret_cast<const float4*>(packed), splat_offsets,
+                  capacity, keys, vals, pair_passes, hist_shift, hist_partials,
+                  direct ? pair_ghist : nullptr, pair_status, pair_status_words,
+                  EmitScan{});
   }
   int rc = check_launch("emit_kernel");
   if (rc || pair_passes == 0 || direct) return rc;
-  hipLaunchKernelGGL(hist_reduce_kernel, dim3((unsigned)(pair_passes * 256)),
-                     dim3(kThreads), 0, stream, hist_partials, nblk,
-                     pair_ghist);
+  launch_traced("hist_reduce_kernel", hist_reduce_kernel,
+                dim3((unsigned)(pair_passes * 256)), dim3(kThreads), 0, stream,
+                hist_partials, nblk, pair_ghist);
   return check_launch("hist_reduce_kernel");
 }
 
@@ -1148,16 +1147,16 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
   } else {
     int64_t grid = (n + 1 + kThreads - 1) / kThreads;
     if (grid > kRangeMaxBlocks) grid = kRangeMaxBlocks;
-    hipLaunchKernelGGL(ranges_kernel, dim3((unsigned)grid), dim3(kThreads), 0,
-                       stream, sorted_keys, n, n_dev, num_tiles,
-                       tile_offsets, sw);
+    launch_traced("ranges_kernel", ranges_kernel, dim3((unsigned)grid),
+                  dim3(kThreads), 0, stream, sorted_keys, n, n_dev, num_tiles,
+                  tile_offsets, sw);
     rc = check_launch("ranges_kernel");
   }
   if (rc || tile_counts == nullptr) return rc;
-  hipLaunchKernelGGL(counts_kernel,
-                     dim3((unsigned)((num_tiles + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, stream, tile_offsets, num_tiles,
-                     tile_counts);
+  launch_traced("counts_kernel", counts_kernel,
+                dim3((unsigned)((num_tiles + kThreads - 1) / kThreads)),
+                dim3(kThreads), 0, stream, tile_offsets, num_tiles,
+                tile_counts);
   return check_launch("counts_kernel");
 }
 
@@ -1172,13 +1171,14 @@ int launch_bucket_sort(const BucketSortArgs& A, hipStream_t stream) {
     set_error("bucket sort: more than 256 buckets");
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
-  hipLaunchKernelGGL(bucket_sort_kernel, dim3((unsigned)buckets),
-                     dim3(kBucketThreads), 0, stream, A);
+  launch_traced("bucket_sort_kernel", bucket_sort_kernel,
+                dim3((unsigned)buckets), dim3(kBucketThreads), 0, stream, A);
   return check_launch("bucket_sort_kernel");
 }
 
 int launch_host_report(const HostReport& R, hipStream_t stream) {
-  hipLaunchKernelGGL(host_report_kernel, dim3(1), dim3(64), 0, stream, R);
+  launch_traced("host_report_kernel", host_report_kernel, dim3(1), dim3(64), 0,
+                stream, R);
   return check_launch("host_report_kernel");
 }
 
@@ -1188,8 +1188,8 @@ int launch_zero2(uint32_t* a, int64_t na, uint32_t* b, int64_t nb,
   if (n <= 0) return GSPLAT_OK;
   int64_t grid = (n + 255) / 256;
   if (grid > 4096) grid = 4096;
-  hipLaunchKernelGGL(zero2_kernel, dim3((unsigned)grid), dim3(256), 0, stream,
-                     a, na, b, nb);
+  launch_traced("zero2_kernel", zero2_kernel, dim3((unsigned)grid), dim3(256),
+                0, stream, a, na, b, nb);
   return check_launch("zero2_kernel");
 }
 
@@ -1197,8 +1197,8 @@ int launch_fill_i32(int32_t* dst, int32_t value, int64_t n,
                     hipStream_t stream) {
   if (n <= 0) return GSPLAT_OK;
   const int64_t grid = (n + 255) / 256;
-  hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)grid), dim3(256), 0,
-                     stream, dst, value, n);
+  launch_traced("fill_i32_kernel", fill_i32_kernel, dim3((unsigned)grid),
+                dim3(256), 0, stream, dst, value, n);
   return check_launch("fill_i32_kernel");
 }
 
@@ -1206,16 +1206,16 @@ int launch_zero_grads(float* g_m, float* g_q, float* g_c, float* g_o,
                       int64_t n, hipStream_t stream) {
   if (n <= 0) return GSPLAT_OK;
   const int64_t grid = (3 * n + 255) / 256;
-  hipLaunchKernelGGL(zero_grads_kernel, dim3((unsigned)grid), dim3(256), 0,
-                     stream, g_m, g_q, g_c, g_o, n);
+  launch_traced("zero_grads_kernel", zero_grads_kernel, dim3((unsigned)grid),
+                dim3(256), 0, stream, g_m, g_q, g_c, g_o, n);
   return check_launch("zero_grads_kernel");
 }
 
 int launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream) {
   if (n <= 0) return GSPLAT_OK;
   const int64_t grid = (n + 255) / 256;
-  hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)grid), dim3(256), 0,
-                     stream, dst, value, n);
+  launch_traced("fill_f32_kernel", fill_f32_kernel, dim3((unsigned)grid),
+                dim3(256), 0, stream, dst, value, n);
   return check_launch("fill_f32_kernel");
 }
 

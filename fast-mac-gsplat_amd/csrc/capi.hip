@@ -7,6 +7,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+
 #include "gs_internal.h"
 
 namespace gs {
@@ -26,6 +28,27 @@ void take_launch_timing(int which, hipEvent_t& start, hipEvent_t& stop) {
   start = g_timing[which][0];
   stop = g_timing[which][1];
   g_timing[which][0] = g_timing[which][1] = nullptr;
+}
+
+namespace {
+// The launch trace: process-wide, so that launches from any host thread
+// (e.g. the autograd engine's device thread) are seen.  Slots are taken
+// with one atomic add; g_trace_cap = 0 means disarmed.
+hipEvent_t g_trace_ev[2 * kTraceMax];
+const char* g_trace_name[kTraceMax];
+std::atomic<int> g_trace_next{0};
+std::atomic<int> g_trace_cap{0};
+}  // namespace
+
+void trace_take(const char* name, hipEvent_t& start, hipEvent_t& stop) {
+  start = stop = nullptr;
+  const int cap = g_trace_cap.load(std::memory_order_acquire);
+  if (cap == 0) return;
+  const int k = g_trace_next.fetch_add(1, std::memory_order_relaxed);
+  if (k >= cap) return;
+  g_trace_name[k] = name;
+  start = g_trace_ev[2 * k];
+  stop = g_trace_ev[2 * k + 1];
 }
 
 void set_error(const char* fmt, ...) {
@@ -223,6 +246,38 @@ size_t gsplat_hip_bin_count_workspace_bytes(const gsplat_raster_meta* meta) {
   RasterParams P;
   if (make_params(meta, P)) return 0;
   return count_layout(P).total;
+}
+
+int gsplat_hip_trace_launches(void* const* events, int n) {
+  if (n < 0 || n > gs::kTraceMax || (n > 0 && events == nullptr)) {
+    gs::set_error("gsplat_hip_trace_launches: n must lie in [0, %d] with "
+                  "2n events",
+                  gs::kTraceMax);
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  gs::g_trace_cap.store(0, std::memory_order_release);
+  for (int k = 0; k < 2 * n; ++k) {
+    if (events[k] == nullptr) {
+      gs::set_error("gsplat_hip_trace_launches: event %d is null", k);
+      return GSPLAT_ERR_INVALID_ARGUMENT;
+    }
+    gs::g_trace_ev[k] = static_cast<hipEvent_t>(events[k]);
+  }
+  for (int k = 0; k < n; ++k) gs::g_trace_name[k] = nullptr;
+  gs::g_trace_next.store(0, std::memory_order_relaxed);
+  gs::g_trace_cap.store(n, std::memory_order_release);
+  return GSPLAT_OK;
+}
+
+int gsplat_hip_trace_count(void) {
+  const int cap = gs::g_trace_cap.load(std::memory_order_acquire);
+  const int next = gs::g_trace_next.load(std::memory_order_relaxed);
+  return next < cap ? next : cap;
+}
+
+const char* gsplat_hip_trace_name(int k) {
+  if (k < 0 || k >= gsplat_hip_trace_count()) return nullptr;
+  return gs::g_trace_name[k];
 }
 
 int gsplat_hip_time_next_launch(int which, void* start_event,

@@ -1280,15 +1280,17 @@ HeavyState forward_state(const RasterParams& P, int64_t n_pairs,
 }
 }  // namespace
 
-// A launch with the timing events start/stop (either may be null).
-template <typename F, typename... Args>
-void launch_timed(F kernel, dim3 grid, dim3 block, hipStream_t stream,
-                  hipEvent_t start, hipEvent_t stop, Args... args) {
+// A launch with the one-shot timing events start/stop (gsplat_hip_time_next_
+// launch; either may be null), else a traced launch.
+template <typename... KArgs, typename... Args>
+void launch_timed(const char* name, void (*kernel)(KArgs...), dim3 grid,
+                  dim3 block, hipStream_t stream, hipEvent_t start,
+                  hipEvent_t stop, Args... args) {
   if (start != nullptr || stop != nullptr)
     hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0,
-                          args...);
+                          static_cast<KArgs>(args)...);
   else
-    hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+    launch_traced(name, kernel, grid, block, 0, stream, args...);
 }
 
 int launch_render_forward(const RasterParams& P, const float* packed,
@@ -1312,7 +1314,7 @@ int launch_render_forward(const RasterParams& P, const float* packed,
   }
   // the continuation follows in this call: it ends the timed span
   const bool more = !(flags & kForwardNoLong) && workspace != nullptr;
-  launch_timed(render_fwd_kernel, dim3((unsigned)P.num_tiles), dim3(kLanes),
+  launch_timed("render_fwd_kernel", render_fwd_kernel, dim3((unsigned)P.num_tiles), dim3(kLanes),
                stream, t0, more ? nullptr : t1, P, pk, tile_offsets,
                binned_ids, out_rgb, out_T, out_last, out_tile_stop, H,
                report != nullptr ? *report : HostReport{});
@@ -1334,7 +1336,7 @@ int launch_render_forward_long(const RasterParams& P, const float* packed,
   const HeavyState H = forward_state(P, n_pairs, workspace, out_T);
   // Workgroups stride over the hand-off list (its length is on the device).
   const unsigned grid = (unsigned)std::min<int64_t>(P.num_tiles, 2048);
-  launch_timed(render_fwd_long_kernel<kLongStrips>, dim3(grid),
+  launch_timed("render_fwd_long_kernel", render_fwd_long_kernel<kLongStrips>, dim3(grid),
                dim3(256 / kLongStrips), stream, nullptr, stop, P,
                reinterpret_cast<const float4*>(packed), tile_offsets,
                binned_ids, out_rgb, out_T, out_last, out_tile_stop, H);
@@ -1366,15 +1368,15 @@ int launch_render_backward(const RasterParams& P, const float* packed,
   const int seg_blocks = H.counters ? (H.max_slots + 7) & ~7 : 0;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   take_launch_timing(kTimeBackward, t0, t1);
-  launch_timed(render_bwd_kernel,
+  launch_timed("render_bwd_kernel", render_bwd_kernel,
                dim3((unsigned)(seg_blocks + P.num_tiles)), dim3(kLanes),
                stream, t0, t1, P, pk, tile_offsets, binned_ids, final_T, last,
                tile_stop, grad_rgb, G, H, seg_blocks);
   rc = check_launch("render_bwd_kernel");
   if (rc || G.acc == nullptr || P.num_splats <= 0) return rc;
-  hipLaunchKernelGGL(render_grads_unpack_kernel,
-                     dim3((unsigned)((P.num_splats + 255) / 256)), dim3(256),
-                     0, stream, G, P.num_splats);
+  launch_traced("render_grads_unpack_kernel", render_grads_unpack_kernel,
+                dim3((unsigned)((P.num_splats + 255) / 256)), dim3(256), 0,
+                stream, G, P.num_splats);
   return check_launch("render_grads_unpack_kernel");
 }
 

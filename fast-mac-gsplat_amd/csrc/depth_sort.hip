@@ -70,10 +70,10 @@ int launch_depth_ranks_small(void* buffers, int32_t* perm, int64_t G,
   }
   const RunBuffers b = run_buffers(buffers, G, batch);
   const int blocks_per_seg = (int)((G + kRankElems - 1) / kRankElems);
-  hipLaunchKernelGGL(depth_run_rank_kernel,
-                     dim3((unsigned)((int64_t)batch * blocks_per_seg)),
-                     dim3(kRankBlock), 0, stream, b.keys, b.vals, b.samples,
-                     (int)G, runs_of(G), perm);
+  launch_traced("depth_run_rank_kernel", depth_run_rank_kernel,
+                dim3((unsigned)((int64_t)batch * blocks_per_seg)),
+                dim3(kRankBlock), 0, stream, b.keys, b.vals, b.samples, (int)G,
+                runs_of(G), perm);
   return check_launch("depth_run_rank_kernel");
 }
 
@@ -85,9 +85,9 @@ int launch_depth_order_small(const float* depths, int32_t* perm, int64_t G,
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
   const int runs = runs_of(G);
-  hipLaunchKernelGGL(depth_run_sort_kernel, dim3((unsigned)(batch * runs)),
-                     dim3(kRunThreads), 0, stream, depths, (int)G, runs,
-                     run_buffers(buffers, G, batch));
+  launch_traced("depth_run_sort_kernel", depth_run_sort_kernel,
+                dim3((unsigned)(batch * runs)), dim3(kRunThreads), 0, stream,
+                depths, (int)G, runs, run_buffers(buffers, G, batch));
   const int rc = check_launch("depth_run_sort_kernel");
   if (rc) return rc;
   return launch_depth_ranks_small(buffers, perm, G, batch, stream);

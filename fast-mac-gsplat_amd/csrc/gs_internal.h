@@ -1,6 +1,7 @@
 // gs_internal.h -- declarations shared by the library's translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -277,6 +278,31 @@ constexpr int kTimeForward = 0;
 constexpr int kTimeBackward = 1;
 void set_launch_timing(int which, hipEvent_t start, hipEvent_t stop);
 void take_launch_timing(int which, hipEvent_t& start, hipEvent_t& stop);
+
+// Launch trace (gsplat_hip_trace_launches): while armed, each kernel launch
+// of the library, on any thread, takes the next of the caller's event pairs
+// and records its kernel's name; start = stop = null when the trace is not
+// armed or is full.
+constexpr int kTraceMax = 1024;  // GSPLAT_TRACE_MAX
+void trace_take(const char* name, hipEvent_t& start, hipEvent_t& stop);
+
+// Every kernel launch of the library: with the trace's events when the
+// trace is armed (hipExtLaunchKernelGGL records them at the kernel's own
+// start and end, so they time the kernel alone).  The arguments are
+// converted to the kernel's parameter types.
+template <typename... KArgs, typename... Args>
+inline void launch_traced(const char* name, void (*kernel)(KArgs...),
+                          dim3 grid, dim3 block, size_t shmem,
+                          hipStream_t stream, Args&&... args) {
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  trace_take(name, t0, t1);
+  if (t0 != nullptr)
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)shmem, stream, t0, t1,
+                          0, static_cast<KArgs>(args)...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, shmem, stream,
+                       static_cast<KArgs>(args)...);
+}
 
 // ---- compositing (composite.hip)
 // workspace (render_workspace_bytes, may be null): heavy-tile segment state,

@@ -408,9 +408,9 @@ int launch_project_forward(const ProjectParams& P, const float* means3d,
                            float* out_depths, hipStream_t stream) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
-  hipLaunchKernelGGL(project_fwd_kernel, dim3(grid), dim3(kThreads), 0, stream,
-                     P, means3d, scales, quats, opacities, c2w, cam,
-                     out_means2d, out_conics, out_opac, out_depths);
+  launch_traced("project_fwd_kernel", project_fwd_kernel, dim3(grid),
+                dim3(kThreads), 0, stream, P, means3d, scales, quats, opacities,
+                c2w, cam, out_means2d, out_conics, out_opac, out_depths);
   return check_launch("project_fwd_kernel");
 }
 
@@ -472,14 +472,16 @@ int launch_project_backward(const ProjectParams& P, const float* g_means2d,
   }
   const int nbx = (P.gpb + kThreads - 1) / kThreads;
   float* partials = static_cast<float*>(workspace);
-  hipLaunchKernelGGL(project_bwd_kernel, dim3((unsigned)nbx, (unsigned)P.batch),
-                     dim3(kThreads), 0, stream, P, g_means2d, g_conics,
-                     g_opac_out, g_depths, means3d, scales, quats, opacities,
-                     c2w, cam, g_means3d, g_scales, g_quats, g_opac, partials);
+  launch_traced("project_bwd_kernel", project_bwd_kernel,
+                dim3((unsigned)nbx, (unsigned)P.batch), dim3(kThreads), 0,
+                stream, P, g_means2d, g_conics, g_opac_out, g_depths, means3d,
+                scales, quats, opacities, c2w, cam, g_means3d, g_scales,
+                g_quats, g_opac, partials);
   int rc = check_launch("project_bwd_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(project_cam_reduce_kernel, dim3((unsigned)P.batch),
-                     dim3(kThreads), 0, stream, partials, nbx, g_c2w, g_cam);
+  launch_traced("project_cam_reduce_kernel", project_cam_reduce_kernel,
+                dim3((unsigned)P.batch), dim3(kThreads), 0, stream, partials,
+                nbx, g_c2w, g_cam);
   return check_launch("project_cam_reduce_kernel");
 }
 

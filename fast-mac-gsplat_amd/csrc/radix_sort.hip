@@ -324,8 +324,8 @@ int launch_zero_u32(uint32_t* p, int64_t n, hipStream_t stream) {
   if (n <= 0) return GSPLAT_OK;
   int64_t grid = (n + 255) / 256;
   if (grid > 2048) grid = 2048;
-  hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)grid), dim3(256), 0,
-                     stream, p, n);
+  launch_traced("zero_u32_kernel", zero_u32_kernel, dim3((unsigned)grid),
+                dim3(256), 0, stream, p, n);
   return check_launch("zero_u32_kernel");
 }
 
@@ -335,9 +335,11 @@ int radix_global_hist(const RadixPlan& L, const RadixCtl& C,
   if (L.passes == 0 || L.n_seg == 0 || L.segments == 0) return GSPLAT_OK;
   const dim3 grid((unsigned)(L.nblk * (int64_t)L.segments));
 #define GS_HIST_LAUNCH(D, R)                                                   \
-  hipLaunchKernelGGL((rs_global_hist_kernel<D, R>), grid, dim3(kThreads), 0,  \
-                     stream, keys, depth_src, L.n_seg, L.nblk, L.segments,    \
-                     L.begin_bit, L.end_bit, L.passes, C.ghist)
+  launch_traced(depth_src != nullptr ? "rs_global_hist_kernel(depth)"      \
+                                     : "rs_global_hist_kernel(keys)",       \
+                (rs_global_hist_kernel<D, R>), grid, dim3(kThreads), 0,       \
+                stream, keys, depth_src, L.n_seg, L.nblk, L.segments,         \
+                L.begin_bit, L.end_bit, L.passes, C.ghist)
   if (L.rounds == 4) {
     if (depth_src) GS_HIST_LAUNCH(true, 4); else GS_HIST_LAUNCH(false, 4);
   } else if (L.rounds == 16) {
@@ -365,8 +367,9 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
     PassArgs a{keys_in, vals_in, depth_src, keys_out, vals_out, L.n_seg,
                nullptr, L.nblk, L.segments, 0, 0, nullptr, nullptr, nullptr,
                nullptr};
-    hipLaunchKernelGGL(rs_copy_kernel, dim3((unsigned)((n + 255) / 256)),
-                       dim3(256), 0, stream, a, n);
+    launch_traced("rs_copy_kernel", rs_copy_kernel,
+                  dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a,
+                  n);
     return check_launch("rs_copy_kernel");
   }
   uint32_t* bufk[2] = {reinterpret_cast<uint32_t*>(base + L.a_keys),
@@ -374,6 +377,9 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
   uint32_t* bufv[2] = {reinterpret_cast<uint32_t*>(base + L.a_vals),
                        reinterpret_cast<uint32_t*>(base + L.b_vals)};
   const int64_t status_per_pass = (int64_t)L.segments * L.nblk * 256;
+  // trace name: the depth sort (float depth keys) or a sort of given keys
+  const char* pass_name = depth_src != nullptr ? "rs_onesweep_kernel(depth)"
+                                               : "rs_onesweep_kernel(keys)";
   const uint32_t* cur_k = keys_in;
   const uint32_t* cur_v = vals_in;
   const float* cur_depth = depth_src;
@@ -393,8 +399,8 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
     switch (mode * 32 + L.rounds) {
 #define GS_ONESWEEP_CASE(M, R)                                              \
   case M * 32 + R:                                                          \
-    hipLaunchKernelGGL((rs_onesweep_kernel<M, R>), grid, dim3(kThreads), 0, \
-                       stream, a);                                          \
+    launch_traced(pass_name, (rs_onesweep_kernel<M, R>), grid, dim3(kThreads), \
+                  0, stream, a);                                            \
     break;
 #define GS_ONESWEEP_MODE(M) \
   GS_ONESWEEP_CASE(M, 4) GS_ONESWEEP_CASE(M, 16) GS_ONESWEEP_CASE(M, 32)

@@ -135,8 +135,9 @@ int exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n, void* ws,
                                    first_ticket, 1, stream);
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(scan_lookback_kernel, dim3((unsigned)nb), dim3(kThreads),
-                     0, stream, in, out, n, status, ticket, err, spin_limit);
+  launch_traced("scan_lookback_kernel", scan_lookback_kernel,
+                dim3((unsigned)nb), dim3(kThreads), 0, stream, in, out, n,
+                status, ticket, err, spin_limit);
   return check_launch("scan_lookback_kernel");
 }
 

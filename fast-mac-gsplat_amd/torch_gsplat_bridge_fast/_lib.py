@@ -17,13 +17,14 @@ import torch  # noqa: F401  (must be loaded before the HIP library)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("GSPLAT_HIP_LIB", os.path.join(_HERE, "lib", "libgsplat_hip.so"))
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 TILE_SIZE = 16
 RECORD_FLOATS = 12
 PROJECT_NOALLOC_SCRATCH_BYTES = 1 << 20   # GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES
 STATUS_LOOKBACK_TIMEOUT = 1               # GSPLAT_STATUS_LOOKBACK_TIMEOUT
 HANDOFF_PAIRS = 128                       # GSPLAT_HANDOFF_PAIRS
 TIME_FORWARD, TIME_BACKWARD = 0, 1        # GSPLAT_TIME_FORWARD / _BACKWARD
+TRACE_MAX = 1024                          # GSPLAT_TRACE_MAX
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -66,6 +67,9 @@ SIGNATURES = {
     "gsplat_hip_abi_version": (ctypes.c_int, []),
     "gsplat_hip_last_error": (ctypes.c_char_p, []),
     "gsplat_hip_time_next_launch": (ctypes.c_int, [ctypes.c_int, _vp, _vp]),
+    "gsplat_hip_trace_launches": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int]),
+    "gsplat_hip_trace_count": (ctypes.c_int, []),
+    "gsplat_hip_trace_name": (ctypes.c_char_p, [ctypes.c_int]),
     "gsplat_hip_bin_count_workspace_bytes": (_sz, [_PM]),
     "gsplat_hip_bin_count": (ctypes.c_int, [_PM] + [_vp] * 4 + [_vp, _sz, _vp]),
     "gsplat_hip_bin_depth_order": (ctypes.c_int, [_PM, _vp, _vp, _vp, _sz, _vp]),

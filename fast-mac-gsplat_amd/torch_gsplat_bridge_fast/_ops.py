@@ -16,6 +16,7 @@ raises RuntimeError when it is set, so the call that bins fails.
 """
 from __future__ import annotations
 
+import ctypes
 import time
 from dataclasses import dataclass
 from typing import Optional
@@ -67,6 +68,40 @@ def pop_timing() -> list:
     out = _timing or []
     _timing = None
     return out
+
+
+class LaunchTrace:
+    """Kernel-level timing of everything the library launches inside a `with` block
+    (gsplat_hip_trace_launches): each of the first `capacity` launches, from any thread (the
+    autograd engine runs backward launches on its own), records a pair of this object's HIP
+    events at its kernel's start and end.  After the block, `launches` holds
+    [(kernel name, ms)] in launch order.  Traced launches cost the stream ~10 us each, so a
+    trace never brackets a timed region."""
+
+    def __init__(self, capacity: int = 128):
+        if not 0 < capacity <= _lib.TRACE_MAX:
+            raise ValueError(f"capacity must lie in [1, {_lib.TRACE_MAX}]")
+        self.capacity = capacity
+        self._events = [torch.cuda.Event(enable_timing=True) for _ in range(2 * capacity)]
+        for e in self._events:   # creates the underlying HIP events
+            e.record()
+        torch.cuda.synchronize()
+        self._handles = (ctypes.c_void_p * (2 * capacity))(*[e.cuda_event for e in self._events])
+        self.launches: list = []
+
+    def __enter__(self):
+        torch.cuda.synchronize()
+        check(_lib.lib().gsplat_hip_trace_launches(self._handles, self.capacity), "gsplat_hip_trace_launches")
+        return self
+
+    def __exit__(self, *exc):
+        L = _lib.lib()
+        torch.cuda.synchronize()
+        n = int(L.gsplat_hip_trace_count())
+        names = [L.gsplat_hip_trace_name(k).decode() for k in range(n)]
+        check(L.gsplat_hip_trace_launches(None, 0), "gsplat_hip_trace_launches")
+        self.launches = [(names[k], self._events[2 * k].elapsed_time(self._events[2 * k + 1])) for k in range(n)]
+        return False
 
 
 _LAUNCH_TIMED = {"render_forward": _lib.TIME_FORWARD, "render_backward": _lib.TIME_BACKWARD}

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 13
+#define GSPLAT_HIP_ABI_VERSION 14
 #define GSPLAT_TILE_SIZE 16
 #define GSPLAT_RECORD_FLOATS 12
 
@@ -100,6 +100,25 @@ const char* gsplat_hip_last_error(void);
 #define GSPLAT_TIME_BACKWARD 1
 int gsplat_hip_time_next_launch(int which, void* start_event,
                                 void* stop_event);
+
+/* Launch trace (instrumentation; no counterpart in the reference: it is for
+ * callers that measure every kernel of a step, such as a benchmark's
+ * per-stage breakdown).  Arms a process-wide trace of the next n kernel
+ * launches of the library (n <= GSPLAT_TRACE_MAX), on any host thread:
+ * launch k is bracketed by events[2k] and events[2k+1] (the caller's
+ * hipEvent_t, created with timing), which the launch itself records at the
+ * kernel's start and end (hipExtLaunchKernelGGL), so their elapsed time is
+ * the kernel's.  Launches after the n-th run untraced.  n = 0 disarms.
+ * gsplat_hip_trace_count() gives the launches traced since the trace was
+ * armed (at most n), gsplat_hip_trace_name(k) the k-th one's kernel name
+ * (static storage; NULL for k out of range).  A traced launch costs the
+ * stream ~10 us more than an untraced one; do not arm it around a timed
+ * region.  Arm and read it while no other thread launches work of the
+ * library. */
+#define GSPLAT_TRACE_MAX 1024
+int gsplat_hip_trace_launches(void* const* events, int n);
+int gsplat_hip_trace_count(void);
+const char* gsplat_hip_trace_name(int k);
 
 /* ---------------------------------------------------------------- binning
  * Replaces torch.ops.gsplat_metal_v8.bin (variants/v8/csrc/bindings.cpp:201,

@@ -30,7 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 13
+    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 14
 
 
 def _meta(**kw):
@@ -154,3 +154,18 @@ def test_one_call_binning_validation():
     assert rc == 1 and "events" in L.gsplat_hip_last_error().decode()
     rc = L.gsplat_hip_bin(m, *([one] * 5), 1000, *([one] * 7), need - 1, None, None, None, None, None)
     assert rc == 3 and "workspace" in L.gsplat_hip_last_error().decode()
+
+
+def test_launch_trace_arguments():
+    """gsplat_hip_trace_launches: n outside [0, GSPLAT_TRACE_MAX] or null events are refused;
+    n = 0 disarms; nothing is traced while disarmed (no GPU needed: no launch happens)."""
+    L = _lib.lib()
+    assert L.gsplat_hip_trace_launches(None, -1) != 0
+    assert L.gsplat_hip_trace_launches(None, _lib.TRACE_MAX + 1) != 0
+    assert L.gsplat_hip_trace_launches(None, 4) != 0
+    events = (ctypes.c_void_p * 8)(*([None] * 8))
+    assert L.gsplat_hip_trace_launches(events, 4) != 0
+    assert "null" in L.gsplat_hip_last_error().decode()
+    assert L.gsplat_hip_trace_launches(None, 0) == 0
+    assert L.gsplat_hip_trace_count() == 0
+    assert L.gsplat_hip_trace_name(0) is None

@@ -688,3 +688,37 @@ def test_one_call_bin_and_forward(gpu, kind):
     torch.cuda.synchronize()
     oracle_parity(sc, H, W, B, G, (0.0, 0.0, 0.0), w.numpy(), img.cpu().numpy(),
                   [g.cpu().numpy() for g in grads], f"one call {kind}", gpu_last=last.cpu().numpy())
+
+
+def test_launch_trace_sees_every_kernel_of_a_step(gpu):
+    """gsplat_hip_trace_launches (the benchmark's per-kernel breakdown): a traced forward +
+    backward through the public API, after a first call that sizes the pair buffers, lists the
+    kernels of the one-call path in launch order (the backward's from the autograd engine's
+    thread too), each with a positive duration; tracing changes no result."""
+    from torch_gsplat_bridge_fast import _ops
+
+    H, W, G = 512, 512, 8000
+    sc = make_scene_2d(2, seed=3, G=G, H=H, W=W)
+    cfg = RasterConfig(height=H, width=W)
+    w = torch.rand(1, H, W, 3, generator=torch.Generator().manual_seed(4)).to(gpu)
+
+    def step():
+        leaves = [sc[k].to(gpu).clone().requires_grad_(k != "depths") for k in KEYS]
+        img = rasterize_projected_gaussians(*leaves, cfg)
+        img.backward(w)
+        return img.detach(), [t.grad for t in leaves[:4]]
+
+    ref_img, ref_grads = step()
+    trace = _ops.LaunchTrace(capacity=64)
+    with trace:
+        img, grads = step()
+    names = [n for n, _ in trace.launches]
+    print("traced launches:", trace.launches, flush=True)
+    want = ["count_depth_runs_kernel", "rank_pack_kernel", "emit_kernel<true>", "rs_onesweep_kernel(keys)",
+            "bucket_sort_kernel", "render_fwd_kernel", "render_bwd_kernel", "render_grads_unpack_kernel"]
+    pos = [names.index(k) for k in want]
+    assert pos == sorted(pos), names
+    assert all(ms > 0 for _, ms in trace.launches)
+    assert torch.equal(img, ref_img)
+    for g, r in zip(grads, ref_grads):   # equal up to the order of the gradient atomics
+        torch.testing.assert_close(g, r, rtol=1e-4, atol=1e-5 * float(r.abs().max()))
