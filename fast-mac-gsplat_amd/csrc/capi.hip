@@ -570,6 +570,11 @@ size_t gsplat_hip_bin_workspace_bytes(const gsplat_raster_meta* meta,
 }  // extern "C"
 
 namespace {
+// Largest number of emit workgroups (128 splats each) of the small-image
+// one-call binning: 4096 (524,288 splats in the batch), where an emit
+// workgroup adds at most 4096 totals (16 per thread).
+constexpr int kScanEmitMaxBlocks = 4096;
+
 // gsplat_hip_bin; zero (may be null): two spans that the tile-range launch
 // zeroes on the side (or a launch of their own where it does not run).
 // With report_out the report of host_words is left to the caller's next
@@ -641,9 +646,13 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
   // run step leaves most CUs idle), the rank step packs the records, and the
   // emit scans the pair offsets and writes N, which the tile-range launch
   // reports; the count stream, its events and the sum of the count
-  // workgroups are not used.
+  // workgroups are not used.  Each emit workgroup there adds the totals of
+  // all workgroups before it, work that grows with the square of their
+  // count, so batches of more than kScanEmitMaxBlocks emit workgroups take
+  // the look-back path below.
   if (host_words != nullptr && capacity > 0 && P.num_tiles > 0 &&
-      P.num_splats > 0 && gs::depth_small_ok(P.gpb)) {
+      P.num_splats > 0 && gs::depth_small_ok(P.gpb) &&
+      gs::emit_blocks(P) <= kScanEmitMaxBlocks) {
     const CountLayout C = count_layout(P);
     char* cb = static_cast<char*>(cws);
     const size_t z0 = gs::radix_ctl_bytes(C.depth);

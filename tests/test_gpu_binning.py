@@ -364,12 +364,15 @@ def _capacity_key(B, G, H, W):
     return (0, B, G, H, W)
 
 
-@pytest.mark.parametrize("B,G,H,W", [(2, 3000, 200, 264), (1, 70_000, 512, 384), (3, 9_000, 160, 200)])
+@pytest.mark.parametrize("B,G,H,W", [(2, 3000, 200, 264), (1, 70_000, 512, 384), (3, 9_000, 160, 200),
+                                     (4, 131_072, 64, 96), (5, 104_858, 64, 96)])
 def test_binning_from_remembered_capacity(gpu, B, G, H, W):
     """The second binning of a shape sizes its pair buffers from the first one's count and reads N
     only afterwards (one C-ABI call: for these sizes the count and the depth runs share a launch and N
     comes from the pack scan); the result is bit-identical and the capacity covers N.  Sizes: one
-    depth run per image, 18 runs with a partial last one, three images of three runs."""
+    depth run per image, 18 runs with a partial last one, three images of three runs, and both sides
+    of the bound on the emit workgroups of that path (4096 x 128 splats in the batch: at it the
+    path above, one splat more and the one-call binning takes the look-back path)."""
     print(f"capacity B={B} G={G} {H}x{W}", flush=True)
     sc = make_scene_2d(1, seed=5, G=G, B=B, H=H, W=W)
     _ops._capacity.pop(_capacity_key(B, G, H, W), None)
