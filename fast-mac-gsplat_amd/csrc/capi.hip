@@ -958,10 +958,11 @@ int gsplat_hip_project_backward(
   gs::ProjectParams P;
   int rc = make_project_params(meta, P);
   if (rc) return rc;
-  rc = null_check({grad_means2d, grad_conics, grad_opacities, grad_depths,
-                   means3d, scales, quats, opacities, camera_to_world,
-                   camera_params, g_means3d, g_scales, g_quats, g_opacities,
-                   g_camera_to_world, g_camera_params, workspace},
+  // (grad_depths may be null: a zero depth gradient)
+  rc = null_check({grad_means2d, grad_conics, grad_opacities, means3d, scales,
+                   quats, opacities, camera_to_world, camera_params, g_means3d,
+                   g_scales, g_quats, g_opacities, g_camera_to_world,
+                   g_camera_params, workspace},
                   "gsplat_hip_project_backward");
   if (rc) return rc;
   if (workspace_bytes < gs::project_backward_workspace_bytes(P)) {
@@ -987,10 +988,10 @@ int gsplat_hip_project_backward_noalloc(
   gs::ProjectParams P;
   int rc = make_project_params(meta, P);
   if (rc) return rc;
-  rc = null_check({grad_means2d, grad_conics, grad_opacities, grad_depths,
-                   means3d, scales, quats, opacities, camera_to_world,
-                   camera_params, g_means3d, g_scales, g_quats, g_opacities,
-                   g_camera_to_world, g_camera_params},
+  rc = null_check({grad_means2d, grad_conics, grad_opacities, means3d, scales,
+                   quats, opacities, camera_to_world, camera_params, g_means3d,
+                   g_scales, g_quats, g_opacities, g_camera_to_world,
+                   g_camera_params},
                   "gsplat_hip_project_backward_noalloc");
   if (rc) return rc;
   const size_t need = gs::project_backward_workspace_bytes(P);

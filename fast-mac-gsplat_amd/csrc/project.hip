@@ -246,7 +246,7 @@ __global__ __launch_bounds__(kThreads) void project_bwd_kernel(
   // ---- J, mean2d -> camera-space mean and intrinsics
   const float gmx = g_means2d[2 * g + 0];
   const float gmy = g_means2d[2 * g + 1];
-  float gxc[3] = {0.0f, 0.0f, g_depths[g]};
+  float gxc[3] = {0.0f, 0.0f, g_depths != nullptr ? g_depths[g] : 0.0f};
   float g_fx = 0.0f, g_fy = 0.0f;
   const float g_cx = gmx, g_cy = gmy;
   if (S.front) {
@@ -375,21 +375,36 @@ __global__ __launch_bounds__(kThreads) void project_bwd_kernel(
 // One workgroup per image: sums the nbx workgroup partials of each of the 16
 // camera-gradient values (fixed order, no atomics) and writes
 // g_camera_to_world [B,4,4] (rotation 3x3, translation column, zero last row)
-// and g_camera_params [B,4].
-__global__ __launch_bounds__(kThreads) void project_cam_reduce_kernel(
+// and g_camera_params [B,4].  64 slots of 16 threads read rows slot, slot +
+// 64, ... with four independent sums (so four loads are in flight per
+// thread), then a fixed tree over the slots.
+constexpr int kReduceThreads = 1024;
+constexpr int kReduceSlots = kReduceThreads / 16;
+__global__ __launch_bounds__(kReduceThreads) void project_cam_reduce_kernel(
     const float* __restrict__ cam_partials, int nbx, float* __restrict__ g_c2w,
     float* __restrict__ g_cam) {
-  __shared__ float red[kThreads];
+  __shared__ float red[kReduceThreads];
   const int b = blockIdx.x;
-  const int v = threadIdx.x & 15, slot = threadIdx.x >> 4;  // 16 slots
-  float sum = 0.0f;
-  for (int x = slot; x < nbx; x += kThreads / 16)
-    sum += cam_partials[((int64_t)b * nbx + x) * 16 + v];
-  red[threadIdx.x] = sum;
+  const int v = threadIdx.x & 15, slot = threadIdx.x >> 4;
+  const float* rows = cam_partials + (int64_t)b * nbx * 16 + v;
+  float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+  int x = slot;
+  for (; x + 3 * kReduceSlots < nbx; x += 4 * kReduceSlots) {
+    s0 += rows[(int64_t)x * 16];
+    s1 += rows[(int64_t)(x + kReduceSlots) * 16];
+    s2 += rows[(int64_t)(x + 2 * kReduceSlots) * 16];
+    s3 += rows[(int64_t)(x + 3 * kReduceSlots) * 16];
+  }
+  for (; x < nbx; x += kReduceSlots) s0 += rows[(int64_t)x * 16];
+  red[threadIdx.x] = (s0 + s1) + (s2 + s3);
   __syncthreads();
+#pragma unroll
+  for (int w = kReduceSlots / 2; w >= 1; w >>= 1) {
+    if (slot < w) red[threadIdx.x] += red[threadIdx.x + 16 * w];
+    __syncthreads();
+  }
   if (threadIdx.x < 16) {
-    float total = 0.0f;
-    for (int k = 0; k < kThreads / 16; ++k) total += red[k * 16 + v];
+    const float total = red[v];
     float* gc2w = g_c2w + 16 * b;
     if (v < 9) gc2w[4 * (v / 3) + (v % 3)] = total;        // rotation
     else if (v < 12) gc2w[4 * (v - 9) + 3] = total;         // translation
@@ -480,8 +495,8 @@ int launch_project_backward(const ProjectParams& P, const float* g_means2d,
   int rc = check_launch("project_bwd_kernel");
   if (rc) return rc;
   launch_traced("project_cam_reduce_kernel", project_cam_reduce_kernel,
-                dim3((unsigned)P.batch), dim3(kThreads), 0, stream, partials,
-                nbx, g_c2w, g_cam);
+                dim3((unsigned)P.batch), dim3(kReduceThreads), 0, stream,
+                partials, nbx, g_c2w, g_cam);
   return check_launch("project_cam_reduce_kernel");
 }
 

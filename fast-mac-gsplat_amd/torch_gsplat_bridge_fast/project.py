@@ -116,8 +116,10 @@ class _ProjectPinholeGaussians(torch.autograd.Function):
         def z(g, shape):
             return torch.zeros(shape, dtype=torch.float32, device=dev) if g is None else g.reshape(shape).contiguous()
 
+        # a depth gradient of None (the rasterizer's) is zero: the C ABI takes a null pointer for it
+        g_dp = None if g_dp is None else g_dp.reshape(B * G).contiguous()
         grads = _ops.project_backward(ctx.meta, z(g_m2, (B * G, 2)), z(g_cq, (B * G, 3)), z(g_op, (B * G,)),
-                                      z(g_dp, (B * G,)), means3d, scales, quats, opacities, c2w, cam)
+                                      g_dp, means3d, scales, quats, opacities, c2w, cam)
         gm3, gs, gq, go, gc2w, gcam = grads
         out = [gm3.view(B, G, 3), gs.view(B, G, 3), gq.view(B, G, 4), go.view(B, G), gc2w, gcam]
         for i, need in enumerate(ctx.needs_input_grad[:6]):
@@ -126,16 +128,33 @@ class _ProjectPinholeGaussians(torch.autograd.Function):
         return (*out, None)
 
 
-def _project_pinhole_gaussians_batched(means3d_b, scales_b, quats_b, opacities_b, fx, fy, cx, cy, camera_to_world,
-                                       near_plane):
-    B = means3d_b.shape[0]
-    dev, dt = means3d_b.device, means3d_b.dtype
-    camera_params = torch.stack([
+_scalar_cams: dict = {}
+
+
+def _camera_params(fx, fy, cx, cy, B, dev, dt):
+    """[B,4] (fx, fy, cx, cy).  For Python numbers the device tensor is kept per value and device
+    (at most 64 entries), so a training loop with fixed intrinsics builds it once; it is only read."""
+    if not any(torch.is_tensor(v) for v in (fx, fy, cx, cy)):
+        key = (float(fx), float(fy), float(cx), float(cy), B, str(dev), dt)
+        t = _scalar_cams.get(key)
+        if t is None:
+            if len(_scalar_cams) >= 64:
+                _scalar_cams.clear()
+            t = _scalar_cams[key] = torch.tensor([[key[0], key[1], key[2], key[3]]] * B, dtype=dt).to(dev)
+        return t
+    return torch.stack([
         _camera_scalar_batch(fx, B, dev, dt, "fx"),
         _camera_scalar_batch(fy, B, dev, dt, "fy"),
         _camera_scalar_batch(cx, B, dev, dt, "cx"),
         _camera_scalar_batch(cy, B, dev, dt, "cy"),
     ], dim=1).contiguous()
+
+
+def _project_pinhole_gaussians_batched(means3d_b, scales_b, quats_b, opacities_b, fx, fy, cx, cy, camera_to_world,
+                                       near_plane):
+    B = means3d_b.shape[0]
+    dev, dt = means3d_b.device, means3d_b.dtype
+    camera_params = _camera_params(fx, fy, cx, cy, B, dev, dt)
     c2w_b = _camera_to_world_batch(camera_to_world, B, dev, dt)
     return _ProjectPinholeGaussians.apply(means3d_b, scales_b, quats_b, opacities_b, c2w_b, camera_params,
                                           float(near_plane))
@@ -170,5 +189,5 @@ def rasterize_pinhole_gaussians(means3d: Tensor, scales: Tensor, quats: Tensor, 
     means2d, conics, opac, depths = _project_pinhole_gaussians_batched(
         m_b.contiguous(), s_b.contiguous(), q_b.contiguous(), o_b.contiguous(), fx, fy, cx, cy, camera_to_world,
         near_plane)
-    out = _rasterize_batched(means2d, conics, colors_b.contiguous(), opac, depths, config)
+    out = _rasterize_batched(means2d, conics, colors_b.contiguous(), opac, depths, config, depth_grad=False)
     return out if was_batched else out[0]

@@ -252,7 +252,8 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
     original splat order, so no unsort is needed."""
 
     @staticmethod
-    def forward(ctx, means2d_b, conics_b, colors_b, opacities_b, depths_b, config: RasterConfig):
+    def forward(ctx, means2d_b, conics_b, colors_b, opacities_b, depths_b, config: RasterConfig,
+                depth_grad: bool = True):
         B, G = means2d_b.shape[:2]
         meta = _meta(config, B, G)
         flat = _flat(means2d_b.detach(), conics_b.detach(), colors_b.detach(), opacities_b.detach(),
@@ -267,6 +268,7 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
         ctx.meta = meta
         ctx.shape = (B, G)
         ctx.depth_shape = depths_b.shape
+        ctx.depth_grad = depth_grad
         return img
 
     @staticmethod
@@ -277,12 +279,16 @@ class _RasterizeProjectedGaussians(torch.autograd.Function):
         bufs, ctx.grad_bufs = ctx.grad_bufs, None   # a second backward (retain_graph) allocates anew
         g_m, g_q, g_c, g_o = _ops.render_backward(ctx.meta, st, final_T, last, tile_stop, grad_out, ws, out=bufs)
         need = ctx.needs_input_grad
-        g_depth = torch.zeros(ctx.depth_shape, dtype=torch.float32, device=grad_out.device) if need[4] else None
+        # The depth gradient is zero (the reference returns zeros, v8 rasterize.py:680).  For depths
+        # computed by the projection (depth_grad False) it is returned as None, which autograd
+        # propagates as zero without a zero-filled tensor.
+        g_depth = (torch.zeros(ctx.depth_shape, dtype=torch.float32, device=grad_out.device)
+                   if need[4] and ctx.depth_grad else None)
         return (g_m if need[0] else None,
                 g_q if need[1] else None,
                 g_c if need[2] else None,
                 g_o if need[3] else None,
-                g_depth, None)
+                g_depth, None, None)
 
 
 def _rasterize_chunk_eval(means2d_b, conics_b, colors_b, opacities_b, depths_b, config: RasterConfig) -> Tensor:
@@ -327,7 +333,10 @@ def _choose_batch_slices(means2d_b, conics_b, colors_b, opacities_b, depths_b, c
     return out
 
 
-def _rasterize_batched(means2d_b, conics_b, colors_b, opacities_b, depths_b, config: RasterConfig) -> Tensor:
+def _rasterize_batched(means2d_b, conics_b, colors_b, opacities_b, depths_b, config: RasterConfig,
+                       depth_grad: bool = True) -> Tensor:
+    """depth_grad False: depths are an intermediate result whose (zero) gradient need not be
+    materialised."""
     B, G = means2d_b.shape[:2]
     tiles_per_image = ((config.height + 15) // 16) * ((config.width + 15) // 16)
     train_mode = _should_use_training_path(means2d_b, conics_b, colors_b, opacities_b)
@@ -341,7 +350,7 @@ def _rasterize_batched(means2d_b, conics_b, colors_b, opacities_b, depths_b, con
         else:
             args = (means2d_b[b0:b1], conics_b[b0:b1], colors_b[b0:b1], opacities_b[b0:b1], depths_b[b0:b1])
         if train_mode:
-            outs.append(_RasterizeProjectedGaussians.apply(*args, config))
+            outs.append(_RasterizeProjectedGaussians.apply(*args, config, depth_grad))
         else:
             with torch.no_grad():
                 outs.append(_rasterize_chunk_eval(*args, config))

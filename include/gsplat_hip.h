@@ -388,8 +388,10 @@ int gsplat_hip_project_forward(const gsplat_project_meta* meta,
 size_t gsplat_hip_project_backward_workspace_bytes(
     const gsplat_project_meta* meta);
 
-/* Vector-Jacobian product of gsplat_hip_project_forward.  Per-splat grads are
- * written directly; g_camera_to_world [B,4,4] (last row zero) and
+/* Vector-Jacobian product of gsplat_hip_project_forward.  grad_depths may be
+ * NULL, meaning a zero depth gradient (the rasterizer's, whose depth gradient
+ * is zero).  Per-splat grads are written directly; g_camera_to_world [B,4,4]
+ * (last row zero) and
  * g_camera_params [B,4] are overwritten with the camera gradients, summed
  * per workgroup into the workspace and then in a fixed order (no atomics). */
 int gsplat_hip_project_backward(const gsplat_project_meta* meta,
