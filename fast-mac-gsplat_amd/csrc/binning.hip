@@ -18,7 +18,7 @@
 // Staged path (one launch per step, also the separate C-ABI steps):
 // count_kernel  original order: per-splat hit counts and per-workgroup sums
 //   (sum_kernel turns them into the pair count N).
-// pack_kernel   one thread per depth-sorted splat (gid): packed 48-byte
+// pack_kernel   one thread per depth-sorted splat (gid): packed 64-byte
 //   record and exclusive per-gid pair offsets (workgroup scan + decoupled
 //   look-back in the same launch).
 // emit_kernel   gid order: each hit claims a slot in its splat's range
@@ -48,6 +48,8 @@
 //   forward compositor does not write it.
 #include "gs_internal.h"
 #include "gs_predicate.h"
+#define GS_HD __device__ __forceinline__
+#include "gs_strip.h"
 #include "depth_runs.h"
 #include "lookback.h"
 
@@ -364,8 +366,20 @@ __global__ __launch_bounds__(kThreads) void sum_kernel(
   }
 }
 
-// The packed 48-byte record of splat orig at depth rank gid:
-// {mx, my, a, b}, {c, o, r, g}, {b, orig, plim, 0}.
+// Divisions and square roots of the per-splat strip constants: correctly
+// rounded (this file is built with -fhip-fp32-correctly-rounded-divide-sqrt).
+struct IeeeOps {
+  static __device__ __forceinline__ float div(float x, float y) { return x / y; }
+  static __device__ __forceinline__ float sqrt(float x) {
+    return __builtin_sqrtf(x);
+  }
+};
+
+// The packed 64-byte record of splat orig at depth rank gid:
+// {mx, my, a, b}, {c, o, r, g}, {b, orig | plain << 31, q, lo},
+// {dxt, beta, gamma, delta}: lo = log2(o), q = plim + lo (the compositors'
+// visibility bound on p + lo), plain = plain_record of the compositors'
+// exponent coefficients, and the strip-culling constants (gs_strip.h).
 __device__ __forceinline__ void pack_record(
     const RasterParams& P, const float* __restrict__ means2d,
     const float* __restrict__ conics, const float* __restrict__ colors,
@@ -380,12 +394,18 @@ __device__ __forceinline__ void pack_record(
   const float cr = colors[3 * orig + 0];
   const float cg = colors[3 * orig + 1];
   const float cb = colors[3 * orig + 2];
-  packed[3 * gid + 0] = make_float4(mx, my, a, b);
-  packed[3 * gid + 1] = make_float4(c, o, cr, cg);
-  packed[3 * gid + 2] =
-      make_float4(cb, __int_as_float(orig),
-                  visibility_limit(o, P.alpha_thr, P.max_alpha),
-                  opacity_log2(o));
+  const float plim = visibility_limit(o, P.alpha_thr, P.max_alpha);
+  const float lo = opacity_log2(o);
+  const bool plain = plain_record(
+      (-0.5f * a) * kLog2e, (-b) * kLog2e, (-0.5f * c) * kLog2e, mx, my, o,
+      plain_opacity_limit(fminf(P.max_alpha, 1.0f)));
+  const StripConsts k = strip_consts_t<IeeeOps>(a, b, c, plim);
+  float4* r = packed + (int64_t)kRecordVec4 * gid;
+  r[0] = make_float4(mx, my, a, b);
+  r[1] = make_float4(c, o, cr, cg);
+  r[2] = make_float4(cb, __uint_as_float((uint32_t)orig | (plain ? 0x80000000u : 0u)),
+                     plim + lo, lo);
+  r[3] = make_float4(k.dxt, k.beta, k.gamma, k.delta);
 }
 
 // Rank step of the small-image depth order with the records packed where
@@ -439,7 +459,7 @@ __global__ __launch_bounds__(run_step::kRankBlock) void rank_pack_kernel(
 }
 
 // One thread per depth-sorted splat (gid): gathers the attributes of
-// orig = perm[gid] into the packed 48-byte record and turns the per-gid
+// orig = perm[gid] into the packed 64-byte record and turns the per-gid
 // tile-hit counts into exclusive offsets splat_offsets in the same launch
 // (workgroup scan + decoupled look-back).  splat_offsets[num_splats] = N, or
 // -1 when N does not fit in int32 (the offsets are then unusable).
@@ -556,8 +576,8 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
   const int gid = (vb * kWaves + wave) * kWalkSplats + lane;
   const bool valid = lane < kWalkSplats && gid < P.num_splats;
   const int g = valid ? gid : P.num_splats - 1;
-  const float4 p0 = packed[3 * g + 0];
-  const float4 p1 = packed[3 * g + 1];
+  const float4 p0 = packed[kRecordVec4 * (int64_t)g + 0];
+  const float4 p1 = packed[kRecordVec4 * (int64_t)g + 1];
   const SplatGeom s{p0.x, p0.y, p0.z, p0.w, p1.x, p1.y};
   WalkSlots& W = walk[wave];
   int64_t n_eff;

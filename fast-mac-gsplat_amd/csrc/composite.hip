@@ -7,12 +7,13 @@
 // share their x coordinate (and the x-only part of the Gaussian exponent),
 // every splat record is read once per wave and reused for four pixels, and no
 // barrier spans more than one wavefront.  Splat records of the tile's range
-// are staged 64 at a time in LDS (each lane gathers one 48-byte record and
+// are staged 64 at a time in LDS (each lane gathers one 64-byte record and
 // derives the per-tile constants) and read by all lanes as broadcasts.  A
 // strip is skipped (scalar branch on a per-record bit mask) when the
 // splat's support ellipse, enlarged by a safety margin, spans no row of the
 // strip inside the tile's columns, so no pixel that could pass the alpha
-// test is ever skipped.
+// test is ever skipped; the record carries the splat's part of that test
+// (gs_strip.h), so a lane only clamps and compares per tile.
 //
 // Alpha test (reference eval_alpha, variants/v8/csrc/metal/gsplat_v8_kernels.metal:121-139):
 // the exponent is evaluated in base 2, by the fixed rounding chain
@@ -118,66 +119,19 @@ __device__ __forceinline__ int64_t opaque64(int64_t v) {
   return v;
 }
 
-// Strip culling (gs_strip.h) with the hardware reciprocal and square root.
+// Strip culling (gs_strip.h) with the hardware square root.
 struct HwOps {
-  static __device__ __forceinline__ float rcp(float x) {
-    return __builtin_amdgcn_rcpf(x);
-  }
   static __device__ __forceinline__ float sqrt(float x) {
     return __builtin_amdgcn_sqrtf(x);
   }
 };
 
-__device__ __forceinline__ uint32_t strip_mask(float mx, float my, float a,
-                                               float b, float c, float plim,
-                                               int x0, int y0) {
-  return strip_mask_t<HwOps>(mx, my, a, b, c, plim, x0, y0);
-}
-
-// Mask bit of a "plain" record: for it the compositors' tests e <= 0 and
-// 2^p < max_alpha always hold, so they are left out (same results, fewer
-// VALU operations per pixel).  Set only together with a strip bit.
+// Mask bit of a "plain" record (plain_record of gs_strip.h, flagged by
+// binning in bit 31 of the record's orig word): for it the compositors'
+// tests e <= 0 and 2^p < max_alpha always hold, so they are left out (same
+// results, fewer VALU operations per pixel).  Set only together with a
+// strip bit.
 constexpr uint32_t kPlainBit = 1u << 4;
-
-// True when, for every pixel, the computed exponent e = fma(fma(C, dy,
-// B dx), dy, (A dx) dx) is <= 0 and 2^p (p = fma(t, dy, (A dx) dx + lo))
-// stays below max_alpha:
-//  * -p is the quadratic form a' dx^2 + b' dx dy + c' dy^2 (a' = -A,
-//    b' = -B, c' = -C) whose smallest eigenvalue is at least
-//    (4a'c' - b'^2) / (4 (a' + c')) >= 2^-18 (a' + c') when 4a'c' - b'^2 >=
-//    2^-16 (a' + c')^2.  The chain computes (1 + d5) times c' dy^2 (1 + d2)
-//    + b' dx dy (1 + d1)(1 + d2) + a' dx^2 (1 + d3)(1 + d4) (|di| <= 2^-24;
-//    the last rounding only scales), which is off the quadratic form by at
-//    most 2.0001 2^-24 (a' dx^2 + |b' dx dy| + c' dy^2) <= 3.0002 2^-24
-//    (a' + c') (dx^2 + dy^2): the sign of p is never flipped.  Where the
-//    inner fma cancels to a subnormal its absolute error, 2^-150 |dy|, is
-//    below 2^-78 dy^2 for |dy| >= 2^-25.  The bounds on a', c',
-//    |b'| and the centre keep every product of the chain normal and finite
-//    (|dx| and |dy| are 0 or at least 2^-25, and at most 2^33, since pixel
-//    centres are below 2^31); dx = dy = 0 gives e = +-0, which passes e <= 0;
-//  * the unrounded t dy + (A dx) dx is <= 0 by the same bound, and the
-//    rounding of (A dx) dx + lo adds at most 2^-24 (|(A dx) dx| + |lo|),
-//    where 2^-24 |(A dx) dx| <= 2^-6 of the bound's margin, so p <= lo +
-//    2^-23 |lo|.  lo is within 7 2^-24 |lo| of log2(o) (ln within 4 ulp, the
-//    rounding of log2(e) and of the product), so 2^p <= o 2^(9 2^-24 |lo|),
-//    which for 2^-20 <= o <= o_plain = max_alpha (1 - 2^-16) (|lo| <= 20)
-//    and the hardware exp2 (within 1 ulp) stays below max_alpha: the clamp
-//    and the gradient gate never act.
-// NaN anywhere fails a comparison and leaves the record on the general path.
-__device__ __forceinline__ bool plain_record(float A, float B, float C,
-                                             float mx, float my, float o,
-                                             float o_plain) {
-  const float a = -A, c = -C, s = a + c;
-  return (o >= 0x1p-20f) & (o <= o_plain) & (a >= 0x1p-60f) & (c >= 0x1p-60f) &
-         (a <= 0x1p40f) & (c <= 0x1p40f) & (fabsf(B) <= 0x1p40f) &
-         (4.0f * a * c - B * B >= 0x1p-16f * s * s) &
-         (fabsf(mx) <= 0x1p32f) & (fabsf(my) <= 0x1p32f);
-}
-
-// o_plain of plain_record for a clamp value max_alpha.
-__device__ __forceinline__ float plain_opacity_limit(float max_alpha) {
-  return max_alpha * (1.0f - 0x1p-16f);
-}
 
 // Stages records [first, first+n) of the tile range into LDS with the
 // base-2 exponent coefficients and the tile's strip mask (plus kPlainBit).
@@ -188,33 +142,34 @@ __device__ __forceinline__ float plain_opacity_limit(float max_alpha) {
 template <bool kMaskInLds>
 __device__ __forceinline__ uint32_t stage_batch(
     const float4* __restrict__ packed, const int32_t* __restrict__ binned,
-    int first, int n, const TileCoord& tc, float o_plain, uint32_t max_gid,
-    Staged& S) {
+    int first, int n, const TileCoord& tc, uint32_t max_gid, Staged& S) {
   const int lane = threadIdx.x;
   uint32_t m = 0u;
   if (lane < n) {
     // (clamped: a corrupt pair list cannot make the gather leave the records)
     const uint32_t gid = min((uint32_t)binned[first + lane], max_gid);
-    const float4 p0 = packed[3 * gid + 0];
-    const float4 p1 = packed[3 * gid + 1];
-    const float4 p2 = packed[3 * gid + 2];
-    const float a = p0.z, b = p0.w, c = p1.x;
+    const float4* r = packed + (uint64_t)kRecordVec4 * gid;
+    const float4 p0 = r[0];
+    const float4 p1 = r[1];
+    const float4 p2 = r[2];
+    const float4 p3 = r[3];
     // (the tile corner through opaque(): computed here per batch rather than
     // kept live in registers across the walk)
-    m = strip_mask(p0.x, p0.y, a, b, c, p2.z, opaque(tc.x0), opaque(tc.y0));
+    m = strip_mask_t<HwOps>(StripConsts{p3.x, p3.y, p3.z, p3.w}, p0.x, p0.y,
+                            opaque(tc.x0), opaque(tc.y0));
+    const uint32_t ob = __float_as_uint(p2.y);
+    if (m != 0u && (int32_t)ob < 0) m |= kPlainBit;
     float A, B, C;
     {
 #pragma clang fp contract(off)
-      A = (-0.5f * a) * kLog2e;
-      B = (-b) * kLog2e;
-      C = (-0.5f * c) * kLog2e;
+      A = (-0.5f * p0.z) * kLog2e;
+      B = (-p0.w) * kLog2e;
+      C = (-0.5f * p1.x) * kLog2e;
     }
-    if (m != 0u && plain_record(A, B, C, p0.x, p0.y, p1.y, o_plain))
-      m |= kPlainBit;
     S.s0[lane] = make_float4(p0.x, p0.y, A, B);
     S.s1[lane] = make_float4(C, p2.w, p1.z, p1.w);
     S.s2[lane] = make_float4(
-        p2.x, p2.y, p2.z + p2.w,
+        p2.x, __uint_as_float(ob & 0x7fffffffu), p2.z,
         kMaskInLds ? __uint_as_float(m) : __builtin_amdgcn_rcpf(p1.y));
   }
   return m;
@@ -507,7 +462,6 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
   // host); pixels outside the image start at T = 0 and are never written.
   const float t_thr = P.trans_thr;
   const float max_alpha = fminf(P.max_alpha, 1.0f);
-  const float o_plain = plain_opacity_limit(max_alpha);
   float py[kPix], T[kPix], cr[kPix], cg[kPix], cb[kPix];
   int last[kPix];
   bool valid[kPix];
@@ -545,7 +499,7 @@ __global__ __launch_bounds__(kLanes) void render_fwd_kernel(
     const int n = min(kBatch, end - base);
     __syncthreads();
     const uint32_t bmask =
-        stage_batch<false>(packed, binned, base, n, tc, o_plain,
+        stage_batch<false>(packed, binned, base, n, tc,
                            (uint32_t)P.num_splats - 1u, S);
     __syncthreads();
     if (batch_plain(bmask))
@@ -673,7 +627,6 @@ __global__ __launch_bounds__(256 / kSpW) void render_fwd_long_kernel(
   const int n_items = H.counters[1];
   const float t_thr = P.trans_thr;
   const float max_alpha = fminf(P.max_alpha, 1.0f);
-  const float o_plain = plain_opacity_limit(max_alpha);
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     __syncthreads();  // the previous tile's reads of S and sh_slot are done
     const int tile = H.handoff[item];
@@ -713,7 +666,7 @@ __global__ __launch_bounds__(256 / kSpW) void render_fwd_long_kernel(
       }
       const int n = min(kBatch, end - base);
       const uint32_t m =
-          stage_batch<true>(packed, binned, base, n, tc, o_plain,
+          stage_batch<true>(packed, binned, base, n, tc,
                             (uint32_t)P.num_splats - 1u, S);
       if (threadIdx.x < kLanes) {  // wavefront 0 staged the batch
         const bool all_plain = batch_plain(m);
@@ -1053,13 +1006,12 @@ __device__ __forceinline__ void bwd_walk(
   const GradTarget target = grad_target(G);
   const GradTarget opac = opac_target(G);
   const float max_alpha = fminf(P.max_alpha, 1.0f);
-  const float o_plain = plain_opacity_limit(max_alpha);
   for (int cend = hi; cend > lo; cend -= kBatch) {
     const int cstart = max(lo, cend - kBatch);
     const int n = cend - cstart;
     __syncthreads();
     const uint32_t bmask =
-        stage_batch<false>(packed, binned, start + cstart, n, tc, o_plain,
+        stage_batch<false>(packed, binned, start + cstart, n, tc,
                            (uint32_t)P.num_splats - 1u, SH.S);
     __syncthreads();
     if (batch_plain(bmask))

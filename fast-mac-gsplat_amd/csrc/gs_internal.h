@@ -10,6 +10,10 @@
 
 namespace gs {
 
+// float4 words of one packed splat record (GSPLAT_RECORD_FLOATS floats).
+constexpr int kRecordVec4 = GSPLAT_RECORD_FLOATS / 4;
+static_assert(GSPLAT_RECORD_FLOATS == 16, "record layout of pack_record");
+
 // Render parameters passed by value to every raster kernel (the HIP analogue
 // of the reference's MetaI32/MetaF32 constant buffers,
 // variants/v8/csrc/metal/gsplat_v8_kernels.metal:23-48).

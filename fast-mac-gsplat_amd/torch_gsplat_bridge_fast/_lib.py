@@ -17,9 +17,9 @@ import torch  # noqa: F401  (must be loaded before the HIP library)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("GSPLAT_HIP_LIB", os.path.join(_HERE, "lib", "libgsplat_hip.so"))
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 TILE_SIZE = 16
-RECORD_FLOATS = 12
+RECORD_FLOATS = 16
 PROJECT_NOALLOC_SCRATCH_BYTES = 1 << 20   # GSPLAT_PROJECT_NOALLOC_SCRATCH_BYTES
 STATUS_LOOKBACK_TIMEOUT = 1               # GSPLAT_STATUS_LOOKBACK_TIMEOUT
 HANDOFF_PAIRS = 128                       # GSPLAT_HANDOFF_PAIRS

@@ -41,9 +41,9 @@
 extern "C" {
 #endif
 
-#define GSPLAT_HIP_ABI_VERSION 14
+#define GSPLAT_HIP_ABI_VERSION 15
 #define GSPLAT_TILE_SIZE 16
-#define GSPLAT_RECORD_FLOATS 12
+#define GSPLAT_RECORD_FLOATS 16
 
 enum gsplat_status {
   GSPLAT_OK = 0,
@@ -170,7 +170,7 @@ int gsplat_hip_bin_depth_order(const gsplat_raster_meta* meta,
 /* Inputs (original order): means2d [BG,2], conics [BG,3], colors [BG,3],
  * opacities [BG]; perm from bin_depth_order; the workspace after bin_count.
  * Outputs (gathers of v8 rasterize.py:467-475):
- *   packed        float [BG*12] packed records in gid (depth rank) order
+ *   packed        float [BG*16] packed records in gid (depth rank) order
  *   splat_offsets int32 [BG+1] exclusive scan of per-gid tile-hit counts */
 int gsplat_hip_bin_pack(const gsplat_raster_meta* meta,
                         const float* means2d, const float* conics,
@@ -182,7 +182,7 @@ int gsplat_hip_bin_pack(const gsplat_raster_meta* meta,
 /* Packed records of splats that are already in depth order (record i from
  * attributes i: gradients of the compositor come back in this same order).
  * Inputs: means2d [BG,2], conics [BG,3], colors [BG,3], opacities [BG];
- * output packed float [BG*12].  The reference's compositor ops take the
+ * output packed float [BG*16].  The reference's compositor ops take the
  * depth-sorted flat arrays themselves and read them by binned id
  * (torch.ops.gsplat_metal_v8.render_* with the gathers of v8 rasterize.py:
  * 466-475 done by the caller; load_chunk_params in gsplat_v8_kernels.metal):

@@ -106,6 +106,52 @@ def opacity_log2(opacity: float) -> float:
     return float(lib().oracle_opacity_log2(ctypes.c_float(opacity)))
 
 
+def strip_consts(a, b, c, plim) -> np.ndarray:
+    """float32 [n, 4] (dxt, beta, gamma, delta): the per-splat strip-culling constants of a packed
+    record, restating strip_consts_t of fast-mac-gsplat_amd/csrc/gs_strip.h with correctly rounded
+    float32 operations in its order (numpy fuses nothing).  Invisible splats (plim > 0) get
+    (0, NaN, inf, 0), never-culled ones (0, 0, inf, 0).  The strips these constants select have no
+    reference counterpart (they only skip work; tests/test_strip_mask_cpu.py checks on the C source
+    that no strip with a visible pixel is skipped); this restatement pins the device's arithmetic
+    to that source bit for bit."""
+    f = np.float32
+    a, b, c, plim = (np.asarray(x, np.float32).reshape(-1) for x in (a, b, c, plim))
+    out = np.zeros((a.size, 4), np.float32)
+    out[:, 2] = np.inf
+    with np.errstate(all="ignore"):
+        tau = f(-1.38629436) * plim
+        det = a * c - b * b
+        ok = (a > 0) & (c > 0) & (det > f(1e-3) * (a * c)) & (tau < f(3.0e38)) & ~(plim > 0)
+        tc = tau * f(1.02) + f(1e-3)
+        hy = np.sqrt((a * tc) / det)
+        vals = np.stack([(-b * hy) / a, (-b) / c, tc / c, det / (c * c)], axis=1).astype(np.float32)
+    out[ok] = vals[ok]
+    out[plim > 0, 1] = np.float32(np.nan)
+    return out
+
+
+def plain_flags(a, b, c, mx, my, o, max_alpha) -> np.ndarray:
+    """bool [n]: the packed record's plain flag, restating plain_record of gs_strip.h on the
+    compositors' base-2 coefficients A = (-a/2) L, B = (-b) L, C = (-c/2) L (float32, L = log2(e)
+    rounded), with o_plain = min(max_alpha, 1) (1 - 2^-16).  The flag only selects a shorter but
+    equivalent evaluation of the same alpha test (the bound is proved in gs_strip.h and exercised by
+    the plain/general GPU tests); this restatement pins the device's flag bit for bit."""
+    f = np.float32
+    a, b, c, mx, my, o = (np.asarray(x, np.float32).reshape(-1) for x in (a, b, c, mx, my, o))
+    L = f(1.44269502)
+    with np.errstate(all="ignore"):
+        A = (f(-0.5) * a) * L
+        B = (-b) * L
+        C = (f(-0.5) * c) * L
+        aa, cc = -A, -C
+        s = aa + cc
+        o_plain = np.minimum(f(max_alpha), f(1.0)) * f(1.0 - 2.0 ** -16)
+        big, tiny, lim = f(2.0 ** 40), f(2.0 ** -60), f(2.0 ** 32)
+        return ((o >= f(2.0 ** -20)) & (o <= o_plain) & (aa >= tiny) & (cc >= tiny) & (aa <= big) & (cc <= big)
+                & (B <= big) & (B >= -big) & (f(4.0) * aa * cc - B * B >= f(2.0 ** -16) * s * s)
+                & (mx <= lim) & (mx >= -lim) & (my <= lim) & (my >= -lim))
+
+
 @dataclass
 class OracleBins:
     perm: np.ndarray         # int32 [BG]

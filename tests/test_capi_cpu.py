@@ -30,7 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 14
+    assert _lib.lib().gsplat_hip_abi_version() == _lib.ABI_VERSION == 15
 
 
 def _meta(**kw):

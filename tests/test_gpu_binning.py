@@ -100,14 +100,21 @@ def _assert_bins_equal(st, ob, scene, B, G):
     np.testing.assert_array_equal(packed[:, 2:5], q[orig])
     np.testing.assert_array_equal(packed[:, 5], o[orig])
     np.testing.assert_array_equal(packed[:, 6:9], c[orig])
-    np.testing.assert_array_equal(packed[:, 9].view(np.int32), orig.astype(np.int32))
-    # the alpha-test exponent limit is bit-exact with the oracle's
     meta = TO.make_meta(8, 8, 1, 1)
-    want = np.array([TO.plim(float(v), meta.alpha_threshold, meta.max_alpha) for v in o[orig]],
-                    dtype=np.float32)
-    np.testing.assert_array_equal(packed[:, 10].view(np.uint32), want.view(np.uint32), err_msg="plim")
-    want = np.array([TO.opacity_log2(float(v)) for v in o[orig]], dtype=np.float32)
-    np.testing.assert_array_equal(packed[:, 11].view(np.uint32), want.view(np.uint32), err_msg="lo")
+    qm, om, mm = q[orig], o[orig], m[orig]
+    word = packed[:, 9].view(np.uint32)
+    np.testing.assert_array_equal((word & np.uint32(0x7FFFFFFF)).astype(np.int32), orig.astype(np.int32))
+    # bit 31: the plain flag, bit-exact with its restatement (and not vacuous on these scenes)
+    plain = TO.plain_flags(qm[:, 0], qm[:, 1], qm[:, 2], mm[:, 0], mm[:, 1], om, meta.max_alpha)
+    np.testing.assert_array_equal((word >> np.uint32(31)).astype(bool), plain, err_msg="plain flag")
+    # the alpha test's bounds are bit-exact with the oracle's: q = plim + lo and lo
+    plim = np.array([TO.plim(float(v), meta.alpha_threshold, meta.max_alpha) for v in om], dtype=np.float32)
+    lo = np.array([TO.opacity_log2(float(v)) for v in om], dtype=np.float32)
+    np.testing.assert_array_equal(packed[:, 10].view(np.uint32), (plim + lo).view(np.uint32), err_msg="q")
+    np.testing.assert_array_equal(packed[:, 11].view(np.uint32), lo.view(np.uint32), err_msg="lo")
+    # the strip-culling constants, bit-exact with their restatement
+    want = TO.strip_consts(qm[:, 0], qm[:, 1], qm[:, 2], plim)
+    np.testing.assert_array_equal(packed[:, 12:16].view(np.uint32), want.view(np.uint32), err_msg="strip constants")
     # sorted 64-bit keys (tile << 32 | gid) strictly increase
     keys = ob.sorted_keys()
     assert np.all(keys[1:] > keys[:-1])

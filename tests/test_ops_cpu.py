@@ -42,7 +42,7 @@ def test_fake_implementations_shapes():
         counts, offsets, ids, packed, perm = torch.ops.gsplat_hip.bin(m2, q, c, o, d, H, W, B, 1 / 255, 1e-4,
                                                                       [0.0, 0.0, 0.0])
         assert counts.shape == (T,) and offsets.shape == (T + 1,) and counts.dtype == torch.int32
-        assert packed.shape == (B * G, 12) and perm.shape == (B * G,) and ids.dtype == torch.int32
+        assert packed.shape == (B * G, 16) and perm.shape == (B * G,) and ids.dtype == torch.int32
         assert not isinstance(ids.shape[0], int)          # data-dependent pair count
         ids = f(500, dtype=torch.int32)
         img, fT, last, stop, ws = torch.ops.gsplat_hip.render_forward(packed, offsets, ids, H, W, B, G, 1 / 255,

@@ -62,8 +62,11 @@ def test_strip_mask_keeps_every_visible_strip(helper, degenerate):
     n = 40_000
     sp, o = _splats(rng, n, degenerate)
     tiles = rng.integers(-2, 3, size=(n, 2)).astype(np.int32) * 16   # tile origins around the splats' frame
-    sp[:, 0] += tiles[:, 0]
-    sp[:, 1] += tiles[:, 1]
+    # half of the sample far from the origin (up to 2^13 px), where the centre's rounding is coarser
+    far = (rng.integers(0, 2, size=(n, 1)) * rng.integers(0, 512, size=(n, 2)) * 16).astype(np.int32)
+    tiles += far
+    sp[:, 0] = (sp[:, 0] + tiles[:, 0]).astype(np.float32)
+    sp[:, 1] = (sp[:, 1] + tiles[:, 1]).astype(np.float32)
     plims = np.array([TO.plim(float(v), THR, 0.99) for v in o], np.float32)
     sp[:, 5] = [TO.opacity_log2(float(v)) for v in o]
     masks = np.zeros((n, 3), np.uint32)
