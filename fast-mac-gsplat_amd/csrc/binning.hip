@@ -46,6 +46,8 @@
 //   buffer holds at most 4096 pairs per bucket on average).
 // host_report_kernel  the binning's report to host memory where the
 //   forward compositor does not write it.
+#include <algorithm>
+
 #include "gs_internal.h"
 #include "gs_predicate.h"
 #define GS_HD __device__ __forceinline__
@@ -761,6 +763,37 @@ __global__ __launch_bounds__(kThreads) void ranges_kernel(
     *sw.long_flag = 1;
 }
 
+// After radix_pair_sort_ranges wrote every tile_offsets entry: the
+// binning's status, empty ranges (all zero) when a look-back gave up or no
+// pair was emitted, the long-range flag and the zero spans, as ranges_kernel
+// does beside its ranges.
+__global__ __launch_bounds__(kThreads) void ranges_finish_kernel(
+    int64_t n_cap, const int32_t* __restrict__ n_dev, int num_tiles,
+    int32_t* __restrict__ tile_offsets, StatusWords sw) {
+  uint32_t e = 0u;
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+    if (sw.err[k] != nullptr) e |= *sw.err[k];
+  if (blockIdx.x == 0 && threadIdx.x == 0 && sw.out != nullptr)
+    *sw.out = (int32_t)e;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  const int64_t first = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+#pragma unroll
+  for (int z = 0; z < 2; ++z)
+    for (int64_t i = first; i < sw.zero[z].n; i += stride) sw.zero[z].p[i] = 0u;
+  const int64_t n = n_dev ? min(n_cap, (int64_t)max(*n_dev, 0)) : n_cap;
+  if (e != 0u || n == 0) {
+    for (int64_t t = first; t <= num_tiles; t += stride) tile_offsets[t] = 0;
+    return;
+  }
+  bool long_range = false;
+  for (int64_t t = first; t < num_tiles; t += stride)
+    long_range |= tile_offsets[t + 1] - tile_offsets[t] > kHandoffPairs;
+  if (sw.long_flag != nullptr && __ballot(long_range) != 0ull &&
+      (threadIdx.x & 63) == 0)
+    *sw.long_flag = 1;
+}
+
 __global__ void host_report_kernel(HostReport R) {
   if (threadIdx.x == 0) write_host_report(R);
 }
@@ -1172,6 +1205,38 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                   tile_offsets, sw);
     rc = check_launch("ranges_kernel");
   }
+  if (rc || tile_counts == nullptr) return rc;
+  launch_traced("counts_kernel", counts_kernel,
+                dim3((unsigned)((num_tiles + kThreads - 1) / kThreads)),
+                dim3(kThreads), 0, stream, tile_offsets, num_tiles,
+                tile_counts);
+  return check_launch("counts_kernel");
+}
+
+int launch_ranges_finish(int64_t n, int num_tiles, int32_t* tile_offsets,
+                         int32_t* tile_counts, hipStream_t stream,
+                         const int32_t* n_dev, const uint32_t* err0,
+                         const uint32_t* err1, const uint32_t* err2,
+                         int32_t* status_out, int32_t* long_flag,
+                         const ZeroSpan* zero) {
+  if (num_tiles <= 0 || n == 0)
+    return launch_tile_ranges(nullptr, 0, num_tiles, tile_offsets, tile_counts,
+                              stream, n_dev, err0, err1, err2, status_out,
+                              long_flag, zero);
+  StatusWords sw{{err0, err1, err2}, status_out, long_flag, {}};
+  if (zero != nullptr) {
+    sw.zero[0] = zero[0];
+    sw.zero[1] = zero[1];
+  }
+  // (sized for the zero spans too)
+  int64_t work = (int64_t)num_tiles + 1;
+  for (int z = 0; z < 2; ++z) work = std::max(work, sw.zero[z].n);
+  int64_t grid = (work + kThreads - 1) / kThreads;
+  if (grid > kRangeMaxBlocks) grid = kRangeMaxBlocks;
+  launch_traced("ranges_finish_kernel", ranges_finish_kernel,
+                dim3((unsigned)grid), dim3(kThreads), 0, stream, n, n_dev,
+                num_tiles, tile_offsets, sw);
+  int rc = check_launch("ranges_finish_kernel");
   if (rc || tile_counts == nullptr) return rc;
   launch_traced("counts_kernel", counts_kernel,
                 dim3((unsigned)((num_tiles + kThreads - 1) / kThreads)),

@@ -529,6 +529,21 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
                        L.pairs.passes,
                        reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
                        ctl.status, L.pairs.status_words, s, scan);
+  // 2-3. Tiles below 2^16 and gids below 2^24: two passes over packed words,
+  // the second of which writes the tile ranges
+  if (gs::radix_pair_ranges_ok(L.pairs, P.num_splats)) {
+    if (!rc)
+      rc = gs::radix_pair_sort_ranges(
+          L.pairs, ctl, base + L.buffers, keys, vals,
+          reinterpret_cast<uint32_t*>(binned_ids), tile_offsets, P.num_tiles,
+          s, n_dev);
+    if (!rc)
+      rc = gs::launch_ranges_finish(n_pairs, P.num_tiles, tile_offsets,
+                                    tile_counts, s, n_dev, err_pack,
+                                    err_pairs, err_depth, status, long_flag,
+                                    zero);
+    return rc;
+  }
   // 2. stable sort by tile
   if (!rc)
     rc = gs::radix_passes(L.pairs, ctl, base + L.buffers, keys, vals, nullptr,

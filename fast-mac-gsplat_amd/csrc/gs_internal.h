@@ -102,6 +102,17 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
                  const float* depth_src, uint32_t* keys_out,
                  uint32_t* vals_out, hipStream_t stream,
                  const int32_t* n_dev = nullptr);
+// The tile-pair sort as two passes over packed words (keys below 2^16,
+// values below 2^24: radix_pair_ranges_ok), whose second pass also writes
+// tile_offsets[0..num_tiles] (every entry; workgroup 0 writes
+// tile_offsets[num_tiles] = n).  Nothing is written for n = 0.  Uses the
+// plan's first ping-pong value buffer; ghist holds both passes' counts.
+bool radix_pair_ranges_ok(const RadixPlan& L, int64_t num_values);
+int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
+                           void* buffers, const uint32_t* keys_in,
+                           const uint32_t* vals_in, uint32_t* vals_out,
+                           int32_t* tile_offsets, int num_tiles,
+                           hipStream_t stream, const int32_t* n_dev);
 // Self-contained sort (zeroes its control block, computes the histograms).
 // status_out (device int32, may be null): receives 0 or
 // GSPLAT_STATUS_LOOKBACK_TIMEOUT.
@@ -245,6 +256,15 @@ int launch_tile_ranges(const uint32_t* sorted_keys, int64_t n, int num_tiles,
                        int32_t* status_out = nullptr,
                        int32_t* long_flag = nullptr,
                        const ZeroSpan* zero = nullptr);
+// After radix_pair_sort_ranges: status, emptied ranges on a look-back
+// give-up or n = 0, the long-range flag, zero spans and tile_counts (may be
+// null), as launch_tile_ranges does from sorted keys.
+int launch_ranges_finish(int64_t n, int num_tiles, int32_t* tile_offsets,
+                         int32_t* tile_counts, hipStream_t stream,
+                         const int32_t* n_dev, const uint32_t* err0,
+                         const uint32_t* err1, const uint32_t* err2,
+                         int32_t* status_out, int32_t* long_flag,
+                         const ZeroSpan* zero);
 
 // The binning's results for the host: device words {N, status, long-range
 // flag} copied to pinned host words host[0..2], then host[3] = 1.  Every

@@ -67,13 +67,42 @@ struct PassArgs {
   uint32_t* status;          // [segments][nblk][256], zeroed
   uint32_t* ticket;          // zeroed
   uint32_t* err;             // look-back give-up status word
+  // The tile-pair sort in two passes (kPackHi, then kPairRanges; one
+  // segment): the first pass's global digit counts, and the tile ranges the
+  // second pass writes.
+  const uint32_t* ghist_a;
+  int32_t* tile_offsets;     // [num_tiles + 1]
+  int num_tiles;
 };
 
 // Kernel variants, chosen on the host, so that the load loops hold no
 // data-dependent branches: every load of a lane is in flight before the first
 // one is used (a branch between a load and its use makes the compiler wait
 // for that load before the next is issued).
-enum : int { kDepthKeys = 1, kValsIn = 2, kKeysOut = 4 };
+//
+// The tile-pair sort of tile keys below 2^16 and values (gids) below 2^24 runs
+// as two passes that move 4 bytes less per element each:
+//  kPackHi      (first pass, digit = key bits 0-7): writes the element as one
+//               word, (key >> 8) << 24 | value, and no key;
+//  kPairRanges  (second pass, on those words: digit = word >> 24): writes the
+//               values (word & 0xffffff) and the tile ranges.  Its input is
+//               ordered by the low key byte, which is the first pass's digit:
+//               the elements with low byte below lo are exactly those before
+//               position P[lo] (the scan of the first pass's digit counts).
+//               So the first pair of tile (hi << 8 | lo) lies at dbase[hi] +
+//               (elements of digit hi before position P[lo]), and the
+//               workgroup whose block holds position P[lo] knows that count
+//               from its look-back prefix and its own elements before P[lo]:
+//               it writes tile_offsets[(hi << 8) | lo] for every hi.  Every
+//               entry is written once (empty tiles included); P[lo] = n is
+//               left to workgroup 0, which also writes tile_offsets[T] = n.
+enum : int {
+  kDepthKeys = 1,
+  kValsIn = 2,
+  kKeysOut = 4,
+  kPackHi = 8,
+  kPairRanges = 16
+};
 
 // Exclusive scan of one value per thread over the 256-thread block.
 __device__ __forceinline__ uint32_t block_excl_scan256(uint32_t v,
@@ -142,7 +171,12 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   __shared__ uint32_t gdelta[256];  // global position of digit d's LDS slot 0
   __shared__ uint32_t wsum[kWaves];
   __shared__ uint32_t sk[kBlockItems];
+  // (kPairRanges: the value is the key word's low 24 bits, so this holds the
+  // block's digits in input order instead, one byte each)
   __shared__ uint32_t sv[kBlockItems];
+  constexpr bool kRanges = (kMode & kPairRanges) != 0;
+  __shared__ uint32_t pstart[kRanges ? 256 : 1];  // P[lo] (kPairRanges)
+  __shared__ uint32_t hist[kRanges ? 256 : 1];    // digits before P[lo]
 
   const int vb = take_ticket(a.ticket);
   const int seg = vb / a.nblk;
@@ -154,6 +188,16 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
       a.n_dev ? min(a.n_seg, (int64_t)max(*a.n_dev, 0)) : a.n_seg;
   if ((int64_t)blk * kBlockItems >= n_seg) return;
   for (int i = t; i < kWaves * 256; i += kThreads) (&cnt[0][0])[i] = 0u;
+  // kPairRanges: does this block hold a position P[lo]?
+  const int64_t blk_lo = (int64_t)blk * kBlockItems;
+  const int64_t blk_hi = min(n_seg, blk_lo + kBlockItems);
+  bool boundaries = false;
+  if (kRanges) {
+    const uint32_t pl = block_excl_scan256(a.ghist_a[t], wsum);
+    pstart[t] = pl;
+    hist[t] = 0u;
+    boundaries = __syncthreads_or((int64_t)pl >= blk_lo && (int64_t)pl < blk_hi);
+  }
 
   const int64_t seg_base = (int64_t)seg * a.n_seg;
   const int64_t lo = (int64_t)blk * kBlockItems + (int64_t)wave * kWaveItems;
@@ -180,8 +224,14 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
     const int64_t j = lo + r * 64 + lane;
     const bool valid = j < n_seg;
     if (kMode & kDepthKeys) kreg[r] = depth_key(__uint_as_float(kreg[r]));
-    if (!(kMode & kValsIn)) vreg[r] = (uint32_t)j;
+    if (kRanges)
+      vreg[r] = kreg[r] & 0xffffffu;
+    else if (!(kMode & kValsIn))
+      vreg[r] = (uint32_t)j;
     const uint32_t d = (kreg[r] >> a.shift) & dmask;
+    if (kRanges && boundaries && valid)
+      reinterpret_cast<uint8_t*>(sv)[wave * kWaveItems + r * 64 + lane] =
+          (uint8_t)d;
     const uint64_t peers = match_digit(d, __ballot(valid));
     const uint32_t below = (uint32_t)__popcll(peers & lt);
     // Every lane of the digit reads its count, then the digit's lowest lane
@@ -216,13 +266,53 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   gdelta[t] = dbase + prefix - local;
   __syncthreads();
 
+  if (kRanges) {
+    // Tile ranges at the positions P[lo] inside this block, in increasing
+    // order (P is nondecreasing): hist counts the block's digits before the
+    // current one, each element added once.  Thread t writes the entry of
+    // digit t (hi = t).
+    const bool hi_ok = t < (1 << a.digit_bits);
+    if (boundaries) {
+      // (low bytes without pairs share their position with the next one:
+      // hist is brought up to each distinct position once)
+      uint32_t q_prev = 0u;
+      for (int lo = 0; lo < 256; ++lo) {
+        const int64_t p = pstart[lo];
+        if (p < blk_lo || p >= blk_hi) continue;  // uniform
+        const uint32_t q = (uint32_t)(p - blk_lo);
+        if (q != q_prev) {  // uniform
+          __syncthreads();  // the reads of hist at q_prev are done
+          for (uint32_t i = q_prev + t; i < q; i += kThreads)
+            atomicAdd(&hist[reinterpret_cast<const uint8_t*>(sv)[i]], 1u);
+          q_prev = q;
+          __syncthreads();
+        }
+        const int tile = (t << 8) | lo;
+        if (hi_ok && tile < a.num_tiles)
+          a.tile_offsets[tile] = (int32_t)(dbase + prefix + hist[t]);
+      }
+      __syncthreads();  // before the scatter below reuses LDS
+    }
+    if (blk == 0) {
+      // P[lo] = n: every pair of digit hi lies before (hi << 8 | lo)
+      for (int lo = 0; lo < 256; ++lo) {
+        if ((int64_t)pstart[lo] != n_seg) continue;  // uniform
+        const int tile = (t << 8) | lo;
+        if (hi_ok && tile < a.num_tiles)
+          a.tile_offsets[tile] = (int32_t)(dbase + gh);
+      }
+      if (t == 0) a.tile_offsets[a.num_tiles] = (int32_t)n_seg;
+    }
+  }
+
+  // (kPairRanges: sv, read above, is not written here)
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
     if (rreg[r] != 0xffffffffu) {
       const uint32_t d = rreg[r] >> 16;
       const uint32_t pos = dstart[d] + cnt[wave][d] + (rreg[r] & 0xffffu);
       sk[pos] = kreg[r];
-      sv[pos] = vreg[r];
+      if (!kRanges) sv[pos] = vreg[r];
     }
   }
   __syncthreads();
@@ -240,7 +330,12 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
       const uint32_t pos = gdelta[(key >> a.shift) & dmask] + (uint32_t)i;
       if (pos < n32) {  // (fails only with histograms inconsistent with the keys)
         if (kMode & kKeysOut) a.keys_out[seg_base + pos] = key;
-        a.vals_out[seg_base + pos] = sv[i];
+        if (kRanges)
+          a.vals_out[seg_base + pos] = key & 0xffffffu;
+        else if (kMode & kPackHi)
+          a.vals_out[seg_base + pos] = ((key >> 8) << 24) | sv[i];
+        else
+          a.vals_out[seg_base + pos] = sv[i];
       }
     }
   }
@@ -421,6 +516,57 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
     cur_depth = nullptr;
   }
   return GSPLAT_OK;
+}
+
+// Buffers of fewer pairs sort them in two passes of keys and values and
+// take the tile ranges from the sorted keys (one launch more): below about
+// 2^23 pairs the low-byte ranges are short enough that many of them start in
+// one sort block, whose second pass then walks them one after another.
+constexpr int64_t kPairRangesMinPairs = int64_t(1) << 23;
+
+bool radix_pair_ranges_ok(const RadixPlan& L, int64_t num_values) {
+  return L.segments == 1 && L.passes == 2 && L.begin_bit == 0 &&
+         L.end_bit > 8 && L.end_bit <= 16 && num_values <= (int64_t(1) << 24) &&
+         L.n_seg >= kPairRangesMinPairs;
+}
+
+int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
+                           void* buffers, const uint32_t* keys_in,
+                           const uint32_t* vals_in, uint32_t* vals_out,
+                           int32_t* tile_offsets, int num_tiles,
+                           hipStream_t stream, const int32_t* n_dev) {
+  if (L.segments != 1 || L.passes != 2 || L.begin_bit != 0 ||
+      L.end_bit <= 8 || L.end_bit > 16 || num_tiles > (1 << L.end_bit)) {
+    set_error("radix sort: the two-pass tile sort needs 9..16 key bits");
+    return GSPLAT_ERR_INVALID_ARGUMENT;
+  }
+  if (L.n_seg == 0) return GSPLAT_OK;
+  uint32_t* words =
+      reinterpret_cast<uint32_t*>(static_cast<char*>(buffers) + L.a_vals);
+  const int64_t status_per_pass = (int64_t)L.nblk * 256;
+  const dim3 grid((unsigned)L.nblk);
+  PassArgs a{keys_in, vals_in, nullptr, nullptr, words, L.n_seg, n_dev,
+             L.nblk, 1, 0, 8, C.ghist, C.status, C.tickets, C.err,
+             nullptr, nullptr, 0};
+  PassArgs b{words, nullptr, nullptr, nullptr, vals_out, L.n_seg, n_dev,
+             L.nblk, 1, 24, L.end_bit - 8, C.ghist + 256,
+             C.status + status_per_pass, C.tickets + 1, C.err,
+             C.ghist, tile_offsets, num_tiles};
+  constexpr int kA = kValsIn | kPackHi, kB = kPairRanges;
+#define GS_PAIR_PASSES(R)                                                    \
+  launch_traced("rs_onesweep_kernel(pairs:lo)", (rs_onesweep_kernel<kA, R>), \
+                grid, dim3(kThreads), 0, stream, a);                         \
+  launch_traced("rs_onesweep_kernel(pairs:hi)", (rs_onesweep_kernel<kB, R>), \
+                grid, dim3(kThreads), 0, stream, b);
+  if (L.rounds == 4) {
+    GS_PAIR_PASSES(4)
+  } else if (L.rounds == 16) {
+    GS_PAIR_PASSES(16)
+  } else {
+    GS_PAIR_PASSES(32)
+  }
+#undef GS_PAIR_PASSES
+  return check_launch("rs_onesweep_kernel(pairs)");
 }
 
 bool radix_size_ok(int64_t n_seg, int segments) {

@@ -158,6 +158,73 @@ def test_pair_sort_path_boundaries(gpu, B, G, H, W):
         _assert_bins_equal(_gpu_bins(sc, H, W, B, G), ob, sc, B, G)
 
 
+@pytest.mark.parametrize("B,G,H,W,cap", [
+    (1, 3000, 512, 512, 9_000_000),     # 1,024 tiles (10 bits), few pairs in a large buffer: many
+                                        # low-byte boundaries inside the first sort blocks
+    (1, 40_000, 512, 512, None),        # above 2^23 pairs: this path from the binning's own count
+    (1, 2000, 16, 4112, 9_000_000),     # 257 tiles: 9 bits, one bit in the second pass
+    (2, 3000, 2048, 4096, 9_000_000),   # 65,536 tiles in two images: 16 bits
+    (3, 5000, 300, 520, 9_000_000),     # 3 x 19 x 33 = 1,881 tiles: 11 bits, ragged rows
+])
+def test_two_pass_pair_sort(gpu, B, G, H, W, cap):
+    """Images of 2^9..2^16 tiles whose pair buffer holds at least 2^23 pairs (and more than 4096 per
+    bucket) sort the pairs in two passes over packed words (low tile byte, then the high bits, with
+    gids below 2^24), the second of which writes every tile range from the first pass's digit
+    boundaries: bit-exact against the oracle, with the boundaries sparse (a large count) or dense (a
+    buffer far larger than the pairs, so that many low-byte ranges start inside one sort block)."""
+    print(f"two-pass pair sort B={B} G={G} {H}x{W} cap={cap}", flush=True)
+    sc = make_scene_2d(1, seed=37, G=G, B=B, H=H, W=W)
+    if cap is None:   # splats 18 times larger: about 1.2e7 pairs
+        sc["conics"] = sc["conics"] / 324.0
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    if cap is None:
+        assert ob.binned_ids.size > (1 << 23)
+    key = _capacity_key(B, G, H, W)
+    _ops._capacity.pop(key, None)
+    if cap is not None:
+        _ops._capacity[key] = cap
+    for _ in range(2):
+        _assert_bins_equal(_gpu_bins(sc, H, W, B, G), ob, sc, B, G)
+
+
+def test_two_pass_pair_sort_empty_and_short(gpu):
+    """The two-pass sort with no pair at all (every splat culled, a large remembered buffer) leaves
+    every range empty, and with a buffer below N keeps exactly the first `capacity` pairs."""
+    B, G, H, W = 1, 80_000, 512, 512
+    print(f"two-pass pair sort: empty and short buffers B={B} G={G} {H}x{W}", flush=True)
+    sc = make_scene_2d(1, seed=41, G=G, B=B, H=H, W=W)
+    sc["conics"] = sc["conics"] / 324.0
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    n = ob.binned_ids.size
+    assert n // 2 >= (1 << 23)
+    key = _capacity_key(B, G, H, W)
+    dev = torch.device("cuda:0")
+    meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, (0.0, 0.0, 0.0))
+    # a buffer below N (still at least 2^23 pairs): the first `cap` pairs, consistent ranges
+    cap = n // 2
+    _ops._capacity[key] = cap
+    flat = [sc[k].reshape(B * G, -1).squeeze(-1).contiguous().to(dev) for k in KEYS]
+    st = _ops.bin_gaussians(meta, *flat, defer_check=True)
+    assert st.capacity == cap
+    offsets = st.tile_offsets.cpu().numpy()
+    assert offsets[0] == 0 and offsets[-1] == cap and np.all(np.diff(offsets) >= 0)
+    assert not st.confirm() and st.n_pairs == n
+    got = st.pairs[:cap].cpu().numpy()
+    splat_end = st.splat_offsets.cpu().numpy()[1:]
+    for t in range(ob.tile_offsets.size - 1):
+        want = ob.binned_ids[ob.tile_offsets[t]:ob.tile_offsets[t + 1]]
+        have = got[offsets[t]:offsets[t + 1]]
+        assert np.all(np.diff(have) > 0) and np.isin(have, want).all()
+        assert np.isin(want[splat_end[want] <= cap], have).all()
+    # every splat culled, the buffer remembered from above
+    _ops._capacity[key] = 2 * n
+    sc0 = dict(sc)
+    sc0["opacities"] = torch.zeros_like(sc["opacities"])
+    st = _gpu_bins(sc0, H, W, B, G)
+    assert st.n_pairs == 0
+    assert not st.tile_offsets.cpu().numpy().any() and int(st.tile_counts.sum()) == 0
+
+
 def test_bucket_sort_skewed(gpu):
     """The pair sort of images of 2^9..2^16 tiles ends in one counting sort per bucket of
     2^(bits-8) tiles.  Here 1024x1024 (4096 tiles: 256 buckets of 16) with most splats packed into
