@@ -247,14 +247,83 @@ struct CountLds {
   int wsum[kW];
 };
 
+// Divisions and square roots of the per-splat strip constants: correctly
+// rounded (this file is built with -fhip-fp32-correctly-rounded-divide-sqrt).
+struct IeeeOps {
+  static __device__ __forceinline__ float div(float x, float y) { return x / y; }
+  static __device__ __forceinline__ float sqrt(float x) {
+    return __builtin_sqrtf(x);
+  }
+};
+
+// The packed 64-byte record of splat orig:
+// {mx, my, a, b}, {c, o, r, g}, {b, slot | plain << 31, q, lo},
+// {dxt, beta, gamma, delta}: lo = log2(o), q = plim + lo (the compositors'
+// visibility bound on p + lo), plain = plain_record of the compositors'
+// exponent coefficients, and the strip-culling constants (gs_strip.h).  The
+// slot holds orig in the records of the compositors (pack_record) and the
+// splat's tile-hit count in the original-order records of the count.
+struct Record {
+  float4 v[kRecordVec4];
+};
+__device__ __forceinline__ Record record_of(
+    const RasterParams& P, const float* __restrict__ means2d,
+    const float* __restrict__ conics, const float* __restrict__ colors,
+    const float* __restrict__ opacities, int orig, uint32_t slot) {
+  const float mx = means2d[2 * orig + 0];
+  const float my = means2d[2 * orig + 1];
+  const float a = conics[3 * orig + 0];
+  const float b = conics[3 * orig + 1];
+  const float c = conics[3 * orig + 2];
+  const float o = opacities[orig];
+  const float cr = colors[3 * orig + 0];
+  const float cg = colors[3 * orig + 1];
+  const float cb = colors[3 * orig + 2];
+  const float plim = visibility_limit(o, P.alpha_thr, P.max_alpha);
+  const float lo = opacity_log2(o);
+  const bool plain = plain_record(
+      (-0.5f * a) * kLog2e, (-b) * kLog2e, (-0.5f * c) * kLog2e, mx, my, o,
+      plain_opacity_limit(fminf(P.max_alpha, 1.0f)));
+  const StripConsts k = strip_consts_t<IeeeOps>(a, b, c, plim);
+  Record r;
+  r.v[0] = make_float4(mx, my, a, b);
+  r.v[1] = make_float4(c, o, cr, cg);
+  r.v[2] = make_float4(cb, __uint_as_float(slot | (plain ? 0x80000000u : 0u)),
+                       plim + lo, lo);
+  r.v[3] = make_float4(k.dxt, k.beta, k.gamma, k.delta);
+  return r;
+}
+
+__device__ __forceinline__ void store_record(float4* __restrict__ dst,
+                                             int64_t i, const Record& r) {
+  float4* d = dst + (int64_t)kRecordVec4 * i;
+#pragma unroll
+  for (int k = 0; k < kRecordVec4; ++k) d[k] = r.v[k];
+}
+
+// The record of splat orig at depth rank gid.
+__device__ __forceinline__ void pack_record(
+    const RasterParams& P, const float* __restrict__ means2d,
+    const float* __restrict__ conics, const float* __restrict__ colors,
+    const float* __restrict__ opacities, float4* __restrict__ packed, int gid,
+    int orig) {
+  store_record(packed, gid,
+               record_of(P, means2d, conics, colors, opacities, orig,
+                         (uint32_t)orig));
+}
+
 // Count block vb of nvb (kW wavefronts, kWalkSplats splats each), original
 // order: splat_count[orig] = tile hits of splat orig and, with block_sums,
-// block_sums[vb] = the block's total.  The blocks also zero
-// zero_words[0..n_zero_words) (grid-stride; read only by later launches).
+// block_sums[vb] = the block's total; with rec_orig also the splat's record
+// in original order, its count in the slot (pack_kernel then copies one
+// 64-byte record per splat instead of gathering five attribute arrays).
+// The blocks also zero zero_words[0..n_zero_words) (grid-stride; read only
+// by later launches).
 template <int kW>
 __device__ __forceinline__ void count_block(
     const RasterParams& P, const float* __restrict__ means2d,
     const float* __restrict__ conics, const float* __restrict__ opacities,
+    const float* __restrict__ colors, float4* __restrict__ rec_orig,
     int32_t* __restrict__ splat_count, int32_t* __restrict__ block_sums,
     uint32_t* __restrict__ zero_words, int64_t n_zero_words, int vb, int nvb,
     CountLds<kW>& S) {
@@ -288,6 +357,11 @@ __device__ __forceinline__ void count_block(
   const int prev_end = __shfl_up(hits_to_end, 1, 64);
   const int n = valid ? hits_to_end - (lane == 0 ? 0 : prev_end) : 0;
   if (valid) splat_count[orig] = n;
+  // (the attributes are read again here rather than kept across the walk)
+  if (valid && rec_orig != nullptr)
+    store_record(rec_orig, orig,
+                 record_of(P, means2d, conics, colors, opacities, orig,
+                           (uint32_t)n));
   if (block_sums == nullptr) return;
   int v = n;
 #pragma unroll
@@ -305,12 +379,13 @@ __device__ __forceinline__ void count_block(
 __global__ __launch_bounds__(kThreads) void count_kernel(
     RasterParams P, const float* __restrict__ means2d,
     const float* __restrict__ conics, const float* __restrict__ opacities,
+    const float* __restrict__ colors, float4* __restrict__ rec_orig,
     int32_t* __restrict__ splat_count, int32_t* __restrict__ block_sums,
     uint32_t* __restrict__ zero_words, int64_t n_zero_words) {
   __shared__ CountLds<kWaves> S;
-  count_block<kWaves>(P, means2d, conics, opacities, splat_count, block_sums,
-                      zero_words, n_zero_words, (int)blockIdx.x,
-                      (int)gridDim.x, S);
+  count_block<kWaves>(P, means2d, conics, opacities, colors, rec_orig,
+                      splat_count, block_sums, zero_words, n_zero_words,
+                      (int)blockIdx.x, (int)gridDim.x, S);
 }
 
 // The count next to the run step of the small-image depth order, in one
@@ -335,7 +410,8 @@ __global__ __launch_bounds__(run_step::kRunThreads) void count_depth_runs_kernel
     return;
   }
   count_block<run_step::kRunWaves>(
-      P, means2d, conics, opacities, splat_count, nullptr, zero_words,
+      P, means2d, conics, opacities, nullptr, nullptr, splat_count, nullptr,
+      zero_words,
       n_zero_words, (int)blockIdx.x - run_blocks,
       (int)gridDim.x - run_blocks, S.count);
 }
@@ -366,48 +442,6 @@ __global__ __launch_bounds__(kThreads) void sum_kernel(
     const long long total = part[0];
     *pair_count = total > 0x7fffffffLL ? -1 : (int32_t)total;
   }
-}
-
-// Divisions and square roots of the per-splat strip constants: correctly
-// rounded (this file is built with -fhip-fp32-correctly-rounded-divide-sqrt).
-struct IeeeOps {
-  static __device__ __forceinline__ float div(float x, float y) { return x / y; }
-  static __device__ __forceinline__ float sqrt(float x) {
-    return __builtin_sqrtf(x);
-  }
-};
-
-// The packed 64-byte record of splat orig at depth rank gid:
-// {mx, my, a, b}, {c, o, r, g}, {b, orig | plain << 31, q, lo},
-// {dxt, beta, gamma, delta}: lo = log2(o), q = plim + lo (the compositors'
-// visibility bound on p + lo), plain = plain_record of the compositors'
-// exponent coefficients, and the strip-culling constants (gs_strip.h).
-__device__ __forceinline__ void pack_record(
-    const RasterParams& P, const float* __restrict__ means2d,
-    const float* __restrict__ conics, const float* __restrict__ colors,
-    const float* __restrict__ opacities, float4* __restrict__ packed, int gid,
-    int orig) {
-  const float mx = means2d[2 * orig + 0];
-  const float my = means2d[2 * orig + 1];
-  const float a = conics[3 * orig + 0];
-  const float b = conics[3 * orig + 1];
-  const float c = conics[3 * orig + 2];
-  const float o = opacities[orig];
-  const float cr = colors[3 * orig + 0];
-  const float cg = colors[3 * orig + 1];
-  const float cb = colors[3 * orig + 2];
-  const float plim = visibility_limit(o, P.alpha_thr, P.max_alpha);
-  const float lo = opacity_log2(o);
-  const bool plain = plain_record(
-      (-0.5f * a) * kLog2e, (-b) * kLog2e, (-0.5f * c) * kLog2e, mx, my, o,
-      plain_opacity_limit(fminf(P.max_alpha, 1.0f)));
-  const StripConsts k = strip_consts_t<IeeeOps>(a, b, c, plim);
-  float4* r = packed + (int64_t)kRecordVec4 * gid;
-  r[0] = make_float4(mx, my, a, b);
-  r[1] = make_float4(c, o, cr, cg);
-  r[2] = make_float4(cb, __uint_as_float((uint32_t)orig | (plain ? 0x80000000u : 0u)),
-                     plim + lo, lo);
-  r[3] = make_float4(k.dxt, k.beta, k.gamma, k.delta);
 }
 
 // Rank step of the small-image depth order with the records packed where
@@ -469,7 +503,8 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
     RasterParams P, const float* __restrict__ means2d,
     const float* __restrict__ conics, const float* __restrict__ colors,
     const float* __restrict__ opacities, const uint32_t* __restrict__ perm,
-    const int32_t* __restrict__ splat_count, float4* __restrict__ packed,
+    const int32_t* __restrict__ splat_count,
+    const float4* __restrict__ rec_orig, float4* __restrict__ packed,
     int32_t* __restrict__ splat_offsets, uint64_t* scan_status,
     uint32_t* scan_ticket, uint32_t* err) {
   __shared__ int wsum[kThreads / 64];
@@ -482,8 +517,19 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
     // (perm is in [0, G) unless a look-back of the depth sort gave up; the
     // clamp keeps the gathers in bounds then, and the status reports it)
     const int orig = batch * P.gpb + (int)min(perm[gid], (uint32_t)(P.gpb - 1));
-    pack_record(P, means2d, conics, colors, opacities, packed, gid, orig);
-    n = splat_count[orig];
+    if (rec_orig != nullptr) {  // the count's record: orig replaces the count
+      Record r;
+#pragma unroll
+      for (int k = 0; k < kRecordVec4; ++k)
+        r.v[k] = rec_orig[(int64_t)kRecordVec4 * orig + k];
+      const uint32_t slot = __float_as_uint(r.v[2].y);
+      n = (int)(slot & 0x7fffffffu);
+      r.v[2].y = __uint_as_float((uint32_t)orig | (slot & 0x80000000u));
+      store_record(packed, gid, r);
+    } else {
+      pack_record(P, means2d, conics, colors, opacities, packed, gid, orig);
+      n = splat_count[orig];
+    }
   }
   // Workgroup exclusive scan of the counts.
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1050,11 +1096,13 @@ int launch_count(const RasterParams& P, const float* means2d,
                  const float* conics, const float* opacities,
                  int32_t* splat_count, int32_t* block_sums,
                  int32_t* pair_count, uint32_t* zero_words,
-                 int64_t n_zero_words, hipStream_t stream) {
+                 int64_t n_zero_words, hipStream_t stream,
+                 const float* colors, float* rec_orig) {
   const int nblk = count_blocks(P);
   launch_traced("count_kernel", count_kernel, dim3((unsigned)nblk),
                 dim3(kThreads), 0, stream, P, means2d, conics, opacities,
-                splat_count, block_sums, zero_words, n_zero_words);
+                colors, reinterpret_cast<float4*>(rec_orig), splat_count,
+                block_sums, zero_words, n_zero_words);
   int rc = check_launch("count_kernel");
   if (rc) return rc;
   launch_traced("sum_kernel", sum_kernel, dim3(1), dim3(kThreads), 0, stream,
@@ -1111,13 +1159,15 @@ int launch_pack(const RasterParams& P, const float* means2d,
                 const float* opacities, const uint32_t* perm,
                 const int32_t* splat_count, float* packed,
                 int32_t* splat_offsets, uint64_t* scan_status,
-                uint32_t* scan_ticket, uint32_t* err, hipStream_t stream) {
+                uint32_t* scan_ticket, uint32_t* err, hipStream_t stream,
+                const float* rec_orig) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
   launch_traced("pack_kernel", pack_kernel, dim3(grid), dim3(kThreads), 0,
                 stream, P, means2d, conics, colors, opacities, perm,
-                splat_count, reinterpret_cast<float4*>(packed), splat_offsets,
-                scan_status, scan_ticket, err);
+                splat_count, reinterpret_cast<const float4*>(rec_orig),
+                reinterpret_cast<float4*>(packed), splat_offsets, scan_status,
+                scan_ticket, err);
   return check_launch("pack_kernel");
 }
 

@@ -173,7 +173,7 @@ int null_check(std::initializer_list<const void*> ptrs, const char* what) {
 struct CountLayout {
   gs::RadixPlan depth;
   size_t scan_status, scan_ticket, pair_ghist, pair_tickets, ctl_end;
-  size_t splat_count, block_sums, gid_count, depth_buffers, total;
+  size_t splat_count, block_sums, gid_count, depth_buffers, rec_orig, total;
 };
 
 CountLayout count_layout(const RasterParams& P) {
@@ -202,6 +202,9 @@ CountLayout count_layout(const RasterParams& P) {
   if (gs::depth_small_ok(P.gpb))
     depth_bytes = std::max(depth_bytes, gs::depth_small_bytes(P.gpb, P.batch));
   off += gs::align_up(depth_bytes, 256);
+  L.rec_orig = off;  // the count's original-order records (gsplat_hip_bin)
+  off += gs::align_up((size_t)P.num_splats * GSPLAT_RECORD_FLOATS * sizeof(float),
+                      256);
   L.total = off;
   return L;
 }
@@ -291,10 +294,15 @@ int gsplat_hip_time_next_launch(int which, void* start_event,
   return GSPLAT_OK;
 }
 
-int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
-                         const float* conics, const float* opacities,
-                         int32_t* pair_count, void* workspace,
-                         size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+// gsplat_hip_bin_count; with colors the count also writes the
+// original-order records that bin_pack_impl copies (use_records).
+int bin_count_impl(const gsplat_raster_meta* meta, const float* means2d,
+                   const float* conics, const float* opacities,
+                   const float* colors, int32_t* pair_count, void* workspace,
+                   size_t workspace_bytes, void* stream) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -320,7 +328,22 @@ int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
                           reinterpret_cast<int32_t*>(base + L.splat_count),
                           reinterpret_cast<int32_t*>(base + L.block_sums),
                           pair_count, reinterpret_cast<uint32_t*>(base + z0),
-                          (int64_t)((L.ctl_end - z0) / sizeof(uint32_t)), s);
+                          (int64_t)((L.ctl_end - z0) / sizeof(uint32_t)), s,
+                          colors,
+                          colors != nullptr
+                              ? reinterpret_cast<float*>(base + L.rec_orig)
+                              : nullptr);
+}
+}  // namespace
+
+extern "C" {
+
+int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
+                         const float* conics, const float* opacities,
+                         int32_t* pair_count, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  return bin_count_impl(meta, means2d, conics, opacities, nullptr, pair_count,
+                        workspace, workspace_bytes, stream);
 }
 
 int gsplat_hip_bin_depth_order(const gsplat_raster_meta* meta,
@@ -374,11 +397,16 @@ int gsplat_hip_pack_records(const gsplat_raster_meta* meta,
                                  static_cast<hipStream_t>(stream));
 }
 
-int gsplat_hip_bin_pack(const gsplat_raster_meta* meta, const float* means2d,
-                        const float* conics, const float* colors,
-                        const float* opacities, const int32_t* perm,
-                        float* packed, int32_t* splat_offsets,
-                        void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+// gsplat_hip_bin_pack; use_records: copy the count's original-order records
+// (bin_count_impl with colors) instead of gathering the attributes.
+int bin_pack_impl(const gsplat_raster_meta* meta, const float* means2d,
+                  const float* conics, const float* colors,
+                  const float* opacities, const int32_t* perm, float* packed,
+                  int32_t* splat_offsets, void* workspace,
+                  size_t workspace_bytes, void* stream, bool use_records) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -402,8 +430,24 @@ int gsplat_hip_bin_pack(const gsplat_raster_meta* meta, const float* means2d,
                          reinterpret_cast<uint64_t*>(base + L.scan_status),
                          reinterpret_cast<uint32_t*>(base + L.scan_ticket),
                          reinterpret_cast<uint32_t*>(base + L.scan_ticket) + 1,
-                         s);
+                         s,
+                         use_records
+                             ? reinterpret_cast<const float*>(base + L.rec_orig)
+                             : nullptr);
   return rc;
+}
+}  // namespace
+
+extern "C" {
+
+int gsplat_hip_bin_pack(const gsplat_raster_meta* meta, const float* means2d,
+                        const float* conics, const float* colors,
+                        const float* opacities, const int32_t* perm,
+                        float* packed, int32_t* splat_offsets,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  return bin_pack_impl(meta, means2d, conics, colors, opacities, perm, packed,
+                       splat_offsets, workspace, workspace_bytes, stream,
+                       false);
 }
 
 size_t gsplat_hip_bin_emit_workspace_bytes(const gsplat_raster_meta* meta,
@@ -705,8 +749,8 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
                       "gsplat_hip_bin: stream wait");
     if (rc) return rc;
   }
-  rc = gsplat_hip_bin_count(meta, means2d, conics, opacities, n_dev, cws,
-                            cbytes, cs);
+  rc = bin_count_impl(meta, means2d, conics, opacities, colors, n_dev, cws,
+                      cbytes, cs);
   if (!rc && ev_n != nullptr)
     rc = hip_status(hipEventRecord(ev_n, cs), "gsplat_hip_bin: event record");
   if (rc) return rc;
@@ -720,8 +764,8 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
   }
   // 3. records and offsets, 4. pairs, pair sort, tile ranges and the
   //    look-back status (next to N in the workspace header)
-  rc = gsplat_hip_bin_pack(meta, means2d, conics, colors, opacities, perm,
-                           packed, splat_offsets, cws, cbytes, s);
+  rc = bin_pack_impl(meta, means2d, conics, colors, opacities, perm, packed,
+                     splat_offsets, cws, cbytes, s, true);
   if (rc) return rc;
   rc = bin_emit_impl(meta, packed, splat_offsets, capacity, binned_ids,
                      nullptr, tile_offsets, status_dev, cws, cbytes, ews,

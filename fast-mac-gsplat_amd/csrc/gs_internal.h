@@ -138,11 +138,15 @@ int launch_depth_ranks_small(void* buffers, int32_t* perm, int64_t G,
 // N into *pair_count (-1 if N does not fit in int32); the same launch zeroes
 // zero_words[0..n_zero_words).  Requires P.num_splats > 0.
 int count_blocks(const RasterParams& P);
+// With colors and rec_orig (float [BG*16]) the count also writes each
+// splat's packed record in original order with its hit count in the orig
+// slot, for launch_pack's rec_orig.
 int launch_count(const RasterParams& P, const float* means2d,
                  const float* conics, const float* opacities,
                  int32_t* splat_count, int32_t* block_sums,
                  int32_t* pair_count, uint32_t* zero_words,
-                 int64_t n_zero_words, hipStream_t stream);
+                 int64_t n_zero_words, hipStream_t stream,
+                 const float* colors = nullptr, float* rec_orig = nullptr);
 // count_depth_runs: the count (splat_count, zero_words as above; no block
 // sums and no N) and the first launch of the small-image depth order (runs
 // into depth_buffers) as one launch.  Requires P.num_splats > 0 and
@@ -161,7 +165,8 @@ int launch_pack(const RasterParams& P, const float* means2d,
                 const float* opacities, const uint32_t* perm,
                 const int32_t* splat_count, float* packed,
                 int32_t* splat_offsets, uint64_t* scan_status,
-                uint32_t* scan_ticket, uint32_t* err, hipStream_t stream);
+                uint32_t* scan_ticket, uint32_t* err, hipStream_t stream,
+                const float* rec_orig = nullptr);
 int count_scan_blocks(const RasterParams& P);
 // pack_records: the packed records of splats already in depth order
 // (record gid from attributes gid, orig = gid).
