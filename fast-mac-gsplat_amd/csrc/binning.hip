@@ -76,16 +76,19 @@ constexpr int kWalkBlockSplats = kWaves * kWalkSplats;
 // histograms atomically instead of through hist_reduce_kernel.
 constexpr int kDirectHistBlocks = 1024;
 // Copies of the emit's digit histograms (see emit_kernel).
-constexpr int kHistCopies = 4;
+constexpr int kHistCopies = 2;
 
 // One wavefront's kWalkSplats splats, staged for the cooperative tile walk.
 struct WalkSlots {
   float4 g0[kWalkSplats];  // mx, my, a, b
   float4 g1[kWalkSplats];  // c, tau, kc, ka
   int4 box[kWalkSplats];   // tx0, ty0, tiles per bbox row, first tile of the image
+  int4 inner[kWalkSplats]; // the certain hits (inner_tiles): x, y relative to
+                           // the box corner, width, height
   int flags[kWalkSplats];  // bit 0: use_c, bit 1: use_a
   int cend[kWalkSplats];   // inclusive prefix sum of candidate counts
   int first[kWalkSplats];  // exclusive prefix sum: the splat's first candidate
+  int ni_incl[kWalkSplats];  // inclusive prefix sum of the certain hits
   uint32_t own[64];        // per walk step: splats starting at each position
 };
 
@@ -131,17 +134,71 @@ __device__ __forceinline__ int walk_splat_index() {
   return ((int)blockIdx.x * kWaves + wave) * kWalkSplats + lane;
 }
 
+// Smallest number of certain hits (inner_tiles) taken out of the walk: the
+// emit writes a splat's certain hits with the wavefront's 64 lanes.
+constexpr int kMinCertainHits = 64;
+
+// Tiles of the box [tx0, tx1] x [ty0, ty1] that certainly pass
+// ellipse_hits_rect: those whose pixel-centre rectangle lies in the
+// rectangle |dx| <= u, |dy| <= v around the centre, with u = k s hx,
+// v = k s hy, s^2 = tau / (a hx^2 + c hy^2 + 2|b| hx hy) and k = 1 - 2^-10.
+// The quadratic q = a dx^2 + 2b dx dy + c dy^2 is convex, so on that
+// rectangle it is at most its largest corner value a u^2 + c v^2 + 2|b| u v
+// = k^2 s^2 (...) <= tau (1 - 2^-9) (s rounded within a few ulp).  A tile
+// there has its centre inside (a hit at once) or its nearest corner inside
+// the rectangle, where the predicate's rounded q, whose operands dx, dy are
+// each one rounded subtraction (relative error 2^-24) and whose three
+// terms sum to at most 2 (a dx^2 + c dy^2) <= 2 tau in magnitude (b^2 < ac),
+// exceeds the exact one by less than 16 2^-24 tau: below tau.  The tile
+// range is computed from u and v less an absolute margin far above the
+// rounding of mx +- u and my +- v.  Returns {x, y relative to (tx0, ty0),
+// width, height}, all 0 when there is no such tile or any quantity is not
+// finite, or when they are fewer than kMinCertainHits.  hx, hy only shape
+// the rectangle (the box's half extents).
+__device__ __forceinline__ int4 inner_tiles(float mx, float my, float a,
+                                            float b, float c, float tau,
+                                            int tx0, int ty0, int tx1,
+                                            int ty1) {
+#pragma clang fp contract(off)
+  const float det = a * c - b * b;
+  if (!(a > 0.0f && c > 0.0f && det > 0.0f)) return make_int4(0, 0, 0, 0);
+  const float hx = __builtin_sqrtf(tau * c / det);
+  const float hy = __builtin_sqrtf(tau * a / det);
+  const float den = a * hx * hx + c * hy * hy + 2.0f * fabsf(b) * hx * hy;
+  const float sk = __builtin_sqrtf(tau / den) * (1.0f - 0x1p-10f);
+  const float margin =
+      (fabsf(mx) + fabsf(my) + hx + hy) * 0x1p-20f + 0x1p-20f;
+  const float u = sk * hx - margin, v = sk * hy - margin;
+  if (!(u > 0.0f && v > 0.0f && u < 0x1p30f && v < 0x1p30f &&
+        fabsf(mx) < 0x1p30f && fabsf(my) < 0x1p30f))
+    return make_int4(0, 0, 0, 0);
+  // tiles t with 16 t + 0.5 >= mx - u and 16 t + 15.5 <= mx + u
+  const float fx0 = fmaxf(ceilf((mx - u - 0.5f) * 0.0625f), (float)tx0);
+  const float fx1 = fminf(floorf((mx + u - 15.5f) * 0.0625f), (float)tx1);
+  const float fy0 = fmaxf(ceilf((my - v - 0.5f) * 0.0625f), (float)ty0);
+  const float fy1 = fminf(floorf((my + v - 15.5f) * 0.0625f), (float)ty1);
+  if (!(fx0 <= fx1 && fy0 <= fy1)) return make_int4(0, 0, 0, 0);
+  const int ix0 = (int)fx0, iy0 = (int)fy0;
+  const int iw = (int)fx1 - ix0 + 1, ih = (int)fy1 - iy0 + 1;
+  // (fewer tiles are cheaper to walk than to write in a loop of their own)
+  if (iw * ih < kMinCertainHits) return make_int4(0, 0, 0, 0);
+  return make_int4(ix0 - tx0, iy0 - ty0, iw, ih);
+}
+
 // Stages this lane's splat (lanes below kWalkSplats) and returns the
-// wavefront's candidate total.  Candidate counts fit in int32: tiles per
-// image are limited to 2^24 on the host, so a wavefront has at most 2^28
-// candidates.
+// wavefront's candidate total: the tiles of each splat's box outside its
+// certain hits (inner_tiles), whose count goes to n_inner.  Candidate
+// counts fit in int32: tiles per image are limited to 2^24 on the host, so
+// a wavefront has at most 2^28 candidates.
 __device__ __forceinline__ int walk_setup(const RasterParams& P, bool valid,
                                           const SplatGeom& s, int batch,
-                                          WalkSlots& W) {
+                                          WalkSlots& W, int& n_inner) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   int ncand = 0;
   int4 box = make_int4(0, 0, 1, 0);
+  int4 inner = make_int4(0, 0, 0, 0);
+  n_inner = 0;
   float4 g1 = make_float4(s.c, 0.0f, 0.0f, 0.0f);
   int flags = 0;
   float tau;
@@ -152,25 +209,37 @@ __device__ __forceinline__ int walk_setup(const RasterParams& P, bool valid,
       const int tx0 = bb.x0 >> 4, tx1 = bb.x1 >> 4;
       const int ty0 = bb.y0 >> 4, ty1 = bb.y1 >> 4;
       box = make_int4(tx0, ty0, tx1 - tx0 + 1, batch * P.tiles_per_image);
-      ncand = box.z * (ty1 - ty0 + 1);
+      // (the inscribed rectangle is at most 2/pi of the ellipse's box)
+      if (box.z * (ty1 - ty0 + 1) >= 2 * kMinCertainHits) {
+        inner =
+            inner_tiles(s.mx, s.my, s.a, s.b, s.c, tau, tx0, ty0, tx1, ty1);
+        n_inner = inner.z * inner.w;
+      }
+      ncand = box.z * (ty1 - ty0 + 1) - n_inner;
       const ConicSlopes k = conic_slopes(s.a, s.b, s.c);
       g1 = make_float4(s.c, tau, k.kc, k.ka);
       flags = (k.use_c ? 1 : 0) | (k.use_a ? 2 : 0);
     }
   }
-  int inc = ncand;
+  int inc = ncand, inc_i = n_inner;
 #pragma unroll
   for (int off = 1; off < kWalkSplats; off <<= 1) {
     const int y = __shfl_up(inc, off, 64);
-    if (lane >= off) inc += y;
+    const int yi = __shfl_up(inc_i, off, 64);
+    if (lane >= off) {
+      inc += y;
+      inc_i += yi;
+    }
   }
   if (lane < kWalkSplats) {
     W.g0[lane] = make_float4(s.mx, s.my, s.a, s.b);
     W.g1[lane] = g1;
     W.box[lane] = box;
+    W.inner[lane] = inner;
     W.flags[lane] = flags;
     W.cend[lane] = inc;
     W.first[lane] = inc - ncand;
+    W.ni_incl[lane] = inc_i;
   }
   __builtin_amdgcn_wave_barrier();
   return __shfl(inc, kWalkSplats - 1, 64);
@@ -199,6 +268,8 @@ __device__ __forceinline__ void walk_candidates(const RasterParams& P,
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int first = lane < kWalkSplats ? W.first[lane] : 0x7fffffff;
+  // (without certain hits in the wavefront every box is walked whole)
+  const bool any_inner = W.ni_incl[kWalkSplats - 1] != 0;
   for (int c0 = 0; c0 < total; c0 += 64) {
     const int owner0 = __popcll(__ballot(first <= c0)) - 1;  // first[0] = 0
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -214,10 +285,31 @@ __device__ __forceinline__ void walk_candidates(const RasterParams& P,
     bool hit = false;
     int tile = 0;
     if (c < total) {
+      // Candidate k of the splat's box less its certain hits (an inner
+      // rectangle at (ix, iy), iw x ih, in box coordinates): the rows above
+      // it in full, then ih rows of bw - iw tiles, then the rows below in
+      // full.
       const int k = c - W.first[sl];
       const int4 bx = W.box[sl];
-      const int dy = div_small(k, bx.z);
-      const int tx = bx.x + (k - dy * bx.z), ty = bx.y + dy;
+      int tx, ty;
+      if (any_inner) {
+        const int4 in = W.inner[sl];
+        const int top = bx.z * in.y;
+        const int mid_w = bx.z - in.z;
+        const int mid = mid_w * in.w;
+        const bool in_mid = k >= top && k < top + mid;
+        const bool below = k >= top + mid;
+        const int kk = below ? k - top - mid : (in_mid ? k - top : k);
+        const int w = in_mid ? mid_w : bx.z;
+        const int q = div_small(kk, w);
+        const int j = kk - q * w;
+        tx = bx.x + ((in_mid && j >= in.x) ? j + in.z : j);
+        ty = bx.y + q + (below ? in.y + in.w : (in_mid ? in.y : 0));
+      } else {
+        const int q = div_small(k, bx.z);
+        tx = bx.x + (k - q * bx.z);
+        ty = bx.y + q;
+      }
       const float4 g0 = W.g0[sl], g1 = W.g1[sl];
       const int fl = W.flags[sl];
       ConicSlopes ks;
@@ -342,7 +434,8 @@ __device__ __forceinline__ void count_block(
   s.c = conics[3 * o + 2];
   s.o = opacities[o];
   WalkSlots& W = S.walk[wave];
-  const int total = walk_setup(P, valid, s, o / P.gpb, W);
+  int n_inner;
+  const int total = walk_setup(P, valid, s, o / P.gpb, W, n_inner);
   // Hits before the end of this lane's splat's candidates (lanes below
   // kWalkSplats): the running total of the steps before plus the hits below
   // the end inside its step; a splat's count is the difference to the
@@ -355,7 +448,8 @@ __device__ __forceinline__ void count_block(
     run += __popcll(hm);
   });
   const int prev_end = __shfl_up(hits_to_end, 1, 64);
-  const int n = valid ? hits_to_end - (lane == 0 ? 0 : prev_end) : 0;
+  const int n =
+      valid ? hits_to_end - (lane == 0 ? 0 : prev_end) + n_inner : 0;
   if (valid) splat_count[orig] = n;
   // (the attributes are read again here rather than kept across the walk)
   if (valid && rec_orig != nullptr)
@@ -629,7 +723,7 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
   const SplatGeom s{p0.x, p0.y, p0.z, p0.w, p1.x, p1.y};
   WalkSlots& W = walk[wave];
   int64_t n_eff;
-  int total;
+  int total, n_inner;
   if (kScan) {
     // exclusive offsets of the workgroup's gids: wavefront scans, the
     // workgroup's scan, and the totals of the workgroups before it (loaded
@@ -644,7 +738,7 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
       if (lane >= off) inc += y;
     }
     if (lane == kWalkSplats - 1) wsum[wave] = inc;
-    total = walk_setup(P, valid, s, g / P.gpb, W);
+    total = walk_setup(P, valid, s, g / P.gpb, W, n_inner);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) before += __shfl_xor(before, off, 64);
     if (lane == 0) wbefore[wave] = before;
@@ -669,17 +763,21 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
   } else {
     if (lane < kWalkSplats) base[wave][lane] = splat_offsets[g];
     n_eff = min(capacity, (int64_t)max(splat_offsets[P.num_splats], 0));
-    total = walk_setup(P, valid, s, g / P.gpb, W);
+    total = walk_setup(P, valid, s, g / P.gpb, W, n_inner);
   }
   const int gid0 = gid - lane;
   // The wavefront's splats own consecutive ranges starting at the first
-  // one's offset and its hits arrive in splat order: a hit's position is
-  // that offset plus the hits before it (running total + lanes below).
+  // one's offset; each range starts with the splat's certain hits
+  // (inner_tiles, written below) and the walk's hits follow, arriving in
+  // splat order: a walk hit's position is that offset plus the hits before
+  // it (running total + lanes below) plus the certain hits of the splats up
+  // to its own.
   const int64_t wave_base = base[wave][0];
   int64_t run = 0;
   walk_candidates(P, W, total, [&](uint64_t hm, bool hit, int sl, int tile,
                                    int) {
-    const int64_t pos = wave_base + run + hits_below(hm, lane);
+    const int64_t pos =
+        wave_base + run + hits_below(hm, lane) + (hit ? W.ni_incl[sl] : 0);
     run += __popcll(hm);
     if (hit && pos < n_eff) {  // pos >= 0 whenever n_eff > 0
       keys[pos] = (uint32_t)tile;
@@ -690,6 +788,29 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
                   1u);
     }
   });
+  // The certain hits of each splat, row by row at the start of its range.
+  uint64_t with_inner = __ballot(lane < kWalkSplats && n_inner > 0);
+  for (; with_inner != 0ull; with_inner &= with_inner - 1ull) {
+    const int sl = (int)__builtin_ctzll(with_inner);
+    const int4 in = W.inner[sl];
+    const int ni = in.z * in.w;
+    const int4 bx = W.box[sl];
+    const int64_t off = base[wave][sl];
+    for (int i = lane; i < ni; i += 64) {
+      const int dy = div_small(i, in.z);
+      const int tile = bx.w + (bx.y + in.y + dy) * P.tiles_x +
+                       (bx.x + in.x + (i - dy * in.z));
+      const int64_t pos = off + i;
+      if (pos < n_eff) {
+        keys[pos] = (uint32_t)tile;
+        vals[pos] = (uint32_t)(gid0 + sl);
+        for (int p = 0; p < pair_passes; ++p)
+          atomicAdd(&h[p][lane % kHistCopies]
+                       [((uint32_t)tile >> (hist_shift + 8 * p)) & 255u],
+                    1u);
+      }
+    }
+  }
   // (3) this workgroup's digit histograms for the pair sort: added to the
   // zeroed global histograms (ghist_direct, few workgroups) or stored as
   // hist_partials[(p * 256 + d) * nblk + workgroup] for hist_reduce_kernel

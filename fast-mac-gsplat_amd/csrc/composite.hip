@@ -445,7 +445,11 @@ __device__ __forceinline__ void fwd_batch(const Staged& S, uint32_t bmask,
   }
 }
 
-__global__ __launch_bounds__(kLanes) void render_fwd_kernel(
+// Eight wavefronts per SIMD (at most 64 VGPRs, a few values spilled): the
+// walk is bound by the latency of each wavefront's loads and LDS round
+// trips, so more resident wavefronts shorten it (7% at 1860 pairs per tile).
+__global__ __launch_bounds__(kLanes) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void render_fwd_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ tile_offsets,
     const int32_t* __restrict__ binned, float* __restrict__ out_rgb,
@@ -1077,11 +1081,14 @@ __device__ __forceinline__ bool seg_item(const RasterParams& P,
 // Work items: block m < seg_blocks walks segment slot m (the longest walks,
 // dispatched first), the other blocks are tiles (tiles walked as segments
 // return at once).
-// Six wavefronts per SIMD (at most 80 VGPRs): the walk's LDS round trips
-// and atomics need the extra wavefronts to hide their latency more than the
-// few spilled set-up values cost.
-__global__ __launch_bounds__(kLanes) __attribute__((amdgpu_waves_per_eu(6, 8)))
-void render_bwd_kernel(
+// kWaves wavefronts per SIMD at least: 6 (at most 80 VGPRs) for tiles of
+// many pairs, whose walk's LDS round trips and atomics need the extra
+// wavefronts more than the few spilled set-up values cost, and 7 (72 VGPRs,
+// more values spilled) for tiles of few pairs, whose time goes to the
+// per-tile set-up and the loads of the pixel state.
+template <int kWaves>
+__global__ __launch_bounds__(kLanes)
+__attribute__((amdgpu_waves_per_eu(kWaves, 8))) void render_bwd_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ tile_offsets,
     const int32_t* __restrict__ binned, const float* __restrict__ final_T,
@@ -1323,7 +1330,11 @@ int launch_render_backward(const RasterParams& P, const float* packed,
   const int seg_blocks = H.counters ? (H.max_slots + 7) & ~7 : 0;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   take_launch_timing(kTimeBackward, t0, t1);
-  launch_timed("render_bwd_kernel", render_bwd_kernel,
+  // (the pair buffer's size stands for the pair count: up to 64 pairs per
+  // tile on average the short-tile variant is faster)
+  const bool short_tiles = n_pairs <= (int64_t)64 * P.num_tiles;
+  launch_timed("render_bwd_kernel",
+               short_tiles ? render_bwd_kernel<7> : render_bwd_kernel<6>,
                dim3((unsigned)(seg_blocks + P.num_tiles)), dim3(kLanes),
                stream, t0, t1, P, pk, tile_offsets, binned_ids, final_T, last,
                tile_stop, grad_rgb, G, H, seg_blocks);

@@ -425,6 +425,38 @@ def test_binning_edge_cases(gpu):
         np.testing.assert_array_equal(ob.perm[b * G:(b + 1) * G], np.argsort(d[b], kind="stable"))
 
 
+@pytest.mark.parametrize("seed,H,W,G,elong", [
+    (51, 640, 1000, 2000, False),   # large round splats, centres also off-screen
+    (52, 512, 8192, 1500, True),    # elongated and rotated, far from the origin (x up to 8k)
+    (53, 300, 300, 800, True),
+])
+def test_binning_large_splats(gpu, seed, H, W, G, elong):
+    """Splats of 10-150 px, round or thin (axis ratio down to 0.02) at any angle, opacities from
+    just above the threshold (small support) to 1: most of their candidate tiles lie in the
+    rectangle of certain hits that the walk skips (counted and written without the test), the rest
+    are tested.  The binning is bit-exact against the oracle, which tests every tile."""
+    rng = np.random.default_rng(seed)
+    print(f"large splats seed={seed} {W}x{H} G={G} elongated={elong}", flush=True)
+    m = np.stack([rng.uniform(-200, W + 200, G), rng.uniform(-200, H + 200, G)], -1)
+    s1 = np.exp(rng.uniform(np.log(10.0), np.log(150.0), G))
+    s2 = s1 * (rng.uniform(0.02, 1.0, G) if elong else rng.uniform(0.5, 1.0, G))
+    th = rng.uniform(0, np.pi, G)
+    c, s = np.cos(th), np.sin(th)
+    ix, iy = 1 / s1 ** 2, 1 / s2 ** 2
+    q = np.stack([c * c * ix + s * s * iy, c * s * (ix - iy), s * s * ix + c * c * iy], -1)
+    o = np.exp(rng.uniform(np.log(1.0 / 255.0 * 1.001), 0.0, G))
+    o[: G // 10] = 1.0 / 255.0 * (1 + rng.uniform(1e-4, 1e-2, G // 10))   # tiny support
+    sc = {k: torch.from_numpy(np.asarray(v, np.float32)[None]) for k, v in dict(
+        means2d=m, conics=q, colors=rng.uniform(0, 1, (G, 3)), opacities=o,
+        depths=rng.uniform(0.1, 10, G)).items()}
+    _, _, ob = _oracle_bins(sc, H, W, 1, G)
+    print(f"  pairs {ob.binned_ids.size}", flush=True)
+    key = _capacity_key(1, G, H, W)
+    _ops._capacity.pop(key, None)
+    for _ in range(2):   # the four-call binning, then the one-call path with the remembered buffer
+        _assert_bins_equal(_gpu_bins(sc, H, W, 1, G), ob, sc, 1, G)
+
+
 def test_binning_all_culled(gpu):
     B, G, H, W = 1, 100, 32, 32
     sc = make_scene_2d(0, seed=1, G=G, H=H, W=W)
