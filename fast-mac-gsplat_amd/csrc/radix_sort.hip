@@ -23,8 +23,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-// Look-back window: predecessor statuses read per round trip.
-constexpr int kLookbackWindow = 16;
+// Look-back window: predecessor statuses read per round trip (8 measured
+// faster than 4, 16, 32 or 64 on 1.2e8-pair sorts).
+constexpr int kLookbackWindow = 8;
 
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const unsigned lane = threadIdx.x & 63u;
