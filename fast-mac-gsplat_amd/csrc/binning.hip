@@ -681,6 +681,24 @@ struct EmitScan {
                                 // counts (added by rank_pack_kernel)
 };
 
+// One pair: (tile, gid) into keys and vals, or, for the two-pass sort of
+// tiles below 2^16 and gids below 2^24 (key_bytes), the word
+// (tile >> 8) << 24 | gid into keys and the tile's low byte into key_bytes
+// (5 bytes instead of 8).
+__device__ __forceinline__ void put_pair(uint32_t* __restrict__ keys,
+                                         uint32_t* __restrict__ vals,
+                                         uint8_t* __restrict__ key_bytes,
+                                         int64_t pos, uint32_t tile,
+                                         uint32_t gid) {
+  if (key_bytes != nullptr) {
+    keys[pos] = ((tile >> 8) << 24) | gid;
+    key_bytes[pos] = (uint8_t)tile;
+  } else {
+    keys[pos] = tile;
+    vals[pos] = gid;
+  }
+}
+
 // Pairs are written (and counted in the histograms) only at positions below
 // min(N, capacity): with a capacity below N the output is the first
 // `capacity` pairs, consistently.  kScan: each workgroup scans its gids'
@@ -693,8 +711,9 @@ template <bool kScan>
 __global__ __launch_bounds__(kThreads) void emit_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ splat_offsets, int64_t capacity,
-    uint32_t* __restrict__ keys, uint32_t* __restrict__ vals, int pair_passes,
-    int hist_shift, uint32_t* __restrict__ hist_partials,
+    uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
+    uint8_t* __restrict__ key_bytes, int pair_passes, int hist_shift,
+    uint32_t* __restrict__ hist_partials,
     uint32_t* ghist_direct, uint32_t* pair_status, int64_t pair_status_words,
     EmitScan sc) {
   __shared__ WalkSlots walk[kWaves];
@@ -780,8 +799,8 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
         wave_base + run + hits_below(hm, lane) + (hit ? W.ni_incl[sl] : 0);
     run += __popcll(hm);
     if (hit && pos < n_eff) {  // pos >= 0 whenever n_eff > 0
-      keys[pos] = (uint32_t)tile;
-      vals[pos] = (uint32_t)(gid0 + sl);
+      put_pair(keys, vals, key_bytes, pos, (uint32_t)tile,
+               (uint32_t)(gid0 + sl));
       for (int p = 0; p < pair_passes; ++p)
         atomicAdd(&h[p][lane % kHistCopies]
                      [((uint32_t)tile >> (hist_shift + 8 * p)) & 255u],
@@ -802,8 +821,8 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
                        (bx.x + in.x + (i - dy * in.z));
       const int64_t pos = off + i;
       if (pos < n_eff) {
-        keys[pos] = (uint32_t)tile;
-        vals[pos] = (uint32_t)(gid0 + sl);
+        put_pair(keys, vals, key_bytes, pos, (uint32_t)tile,
+                 (uint32_t)(gid0 + sl));
         for (int p = 0; p < pair_passes; ++p)
           atomicAdd(&h[p][lane % kHistCopies]
                        [((uint32_t)tile >> (hist_shift + 8 * p)) & 255u],
@@ -1317,7 +1336,8 @@ int launch_emit(const RasterParams& P, const float* packed,
                 uint32_t* vals, int pair_passes, uint32_t* hist_partials,
                 uint32_t* pair_ghist, uint32_t* pair_status,
                 int64_t pair_status_words, hipStream_t stream,
-                const EmitScanArgs* scan, int hist_shift) {
+                const EmitScanArgs* scan, int hist_shift,
+                uint8_t* key_bytes) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const int nblk = emit_blocks(P);
   // Few workgroups add their histograms atomically (pair_ghist is zeroed
@@ -1329,14 +1349,15 @@ int launch_emit(const RasterParams& P, const float* packed,
     launch_traced("emit_kernel<true>", emit_kernel<true>, dim3((unsigned)nblk),
                   dim3(kThreads), 0, stream, P,
                   reinterpret_cast<const float4*>(packed), nullptr, capacity,
-                  keys, vals, pair_passes, hist_shift, hist_partials,
+                  keys, vals, key_bytes, pair_passes, hist_shift, hist_partials,
                   direct ? pair_ghist : nullptr, pair_status, pair_status_words,
                   sc);
   } else {
     launch_traced("emit_kernel<false>", emit_kernel<false>,
                   dim3((unsigned)nblk), dim3(kThreads), 0, stream, P,
                   reinterpret_cast<const float4*>(packed), splat_offsets,
-                  capacity, keys, vals, pair_passes, hist_shift, hist_partials,
+                  capacity, keys, vals, key_bytes, pair_passes, hist_shift,
+                  hist_partials,
                   direct ? pair_ghist : nullptr, pair_status, pair_status_words,
                   EmitScan{});
   }

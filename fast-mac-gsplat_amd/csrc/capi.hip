@@ -568,17 +568,20 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
     }
     return rc;
   }
-  // 1. pairs at deterministic per-splat ranges + the sort's histograms
-  rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals,
-                       L.pairs.passes,
-                       reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
-                       ctl.status, L.pairs.status_words, s, scan);
-  // 2-3. Tiles below 2^16 and gids below 2^24: two passes over packed words,
-  // the second of which writes the tile ranges
+  // 1. pairs at deterministic per-splat ranges + the sort's histograms;
+  // 2-3. tiles below 2^16 and gids below 2^24: the emit writes the pairs as
+  // words and low bytes (the sorted keys' buffer holds the bytes) for two
+  // passes over packed words, the second of which writes the tile ranges
   if (gs::radix_pair_ranges_ok(L.pairs, P.num_splats)) {
+    uint8_t* key_bytes = reinterpret_cast<uint8_t*>(sorted_keys);
+    rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals,
+                         L.pairs.passes,
+                         reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
+                         ctl.status, L.pairs.status_words, s, scan, 0,
+                         key_bytes);
     if (!rc)
       rc = gs::radix_pair_sort_ranges(
-          L.pairs, ctl, base + L.buffers, keys, vals,
+          L.pairs, ctl, base + L.buffers, key_bytes, keys,
           reinterpret_cast<uint32_t*>(binned_ids), tile_offsets, P.num_tiles,
           s, n_dev);
     if (!rc)
@@ -588,6 +591,10 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
                                     zero);
     return rc;
   }
+  rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals,
+                       L.pairs.passes,
+                       reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
+                       ctl.status, L.pairs.status_words, s, scan);
   // 2. stable sort by tile
   if (!rc)
     rc = gs::radix_passes(L.pairs, ctl, base + L.buffers, keys, vals, nullptr,

@@ -108,9 +108,11 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
 // tile_offsets[num_tiles] = n).  Nothing is written for n = 0.  Uses the
 // plan's first ping-pong value buffer; ghist holds both passes' counts.
 bool radix_pair_ranges_ok(const RadixPlan& L, int64_t num_values);
+// Its input is the emit's key_bytes form: key_bytes (the tiles' low bytes)
+// and words ((tile >> 8) << 24 | gid).
 int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
-                           void* buffers, const uint32_t* keys_in,
-                           const uint32_t* vals_in, uint32_t* vals_out,
+                           void* buffers, const uint8_t* key_bytes,
+                           const uint32_t* words, uint32_t* vals_out,
                            int32_t* tile_offsets, int num_tiles,
                            hipStream_t stream, const int32_t* n_dev);
 // Self-contained sort (zeroes its control block, computes the histograms).
@@ -202,7 +204,8 @@ int launch_emit(const RasterParams& P, const float* packed,
                 uint32_t* vals, int pair_passes, uint32_t* hist_partials,
                 uint32_t* pair_ghist, uint32_t* pair_status,
                 int64_t pair_status_words, hipStream_t stream,
-                const EmitScanArgs* scan = nullptr, int hist_shift = 0);
+                const EmitScanArgs* scan = nullptr, int hist_shift = 0,
+                uint8_t* key_bytes = nullptr);
 // Second half of the pair sort when one onesweep pass has ordered the pairs
 // by the tile bits above low_bits (a bucket = 2^low_bits consecutive tiles;
 // at most 256 buckets): one workgroup per bucket sorts its pairs stably on

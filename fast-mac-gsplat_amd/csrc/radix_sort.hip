@@ -83,8 +83,11 @@ struct PassArgs {
 //
 // The tile-pair sort of tile keys below 2^16 and values (gids) below 2^24 runs
 // as two passes that move 4 bytes less per element each:
-//  kPackHi      (first pass, digit = key bits 0-7): writes the element as one
-//               word, (key >> 8) << 24 | value, and no key;
+//  kKeyBytes    (first pass): the keys are the tiles' low bytes (uint8) and
+//               the values the words (key >> 8) << 24 | gid, written by the
+//               emit in that form; the pass moves the words;
+//  kPackHi      (a first pass on 32-bit keys and values instead): writes each
+//               element as one word, (key >> 8) << 24 | value, and no key;
 //  kPairRanges  (second pass, on those words: digit = word >> 24): writes the
 //               values (word & 0xffffff) and the tile ranges.  Its input is
 //               ordered by the low key byte, which is the first pass's digit:
@@ -102,7 +105,8 @@ enum : int {
   kValsIn = 2,
   kKeysOut = 4,
   kPackHi = 8,
-  kPairRanges = 16
+  kPairRanges = 16,
+  kKeyBytes = 32
 };
 
 // Exclusive scan of one value per thread over the 256-thread block.
@@ -211,8 +215,11 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
     const int64_t src = seg_base + min(lo + r * 64 + lane, n_seg - 1);
-    kreg[r] = (kMode & kDepthKeys) ? __float_as_uint(a.depth_src[src])
-                                   : a.keys_in[src];
+    if (kMode & kKeyBytes)
+      kreg[r] = reinterpret_cast<const uint8_t*>(a.keys_in)[src];
+    else
+      kreg[r] = (kMode & kDepthKeys) ? __float_as_uint(a.depth_src[src])
+                                     : a.keys_in[src];
     if (kMode & kValsIn) vreg[r] = a.vals_in[src];
   }
   // this pass's global digit count of digit t (digit bases below)
@@ -532,8 +539,8 @@ bool radix_pair_ranges_ok(const RadixPlan& L, int64_t num_values) {
 }
 
 int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
-                           void* buffers, const uint32_t* keys_in,
-                           const uint32_t* vals_in, uint32_t* vals_out,
+                           void* buffers, const uint8_t* key_bytes,
+                           const uint32_t* words_in, uint32_t* vals_out,
                            int32_t* tile_offsets, int num_tiles,
                            hipStream_t stream, const int32_t* n_dev) {
   if (L.segments != 1 || L.passes != 2 || L.begin_bit != 0 ||
@@ -546,14 +553,14 @@ int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
       reinterpret_cast<uint32_t*>(static_cast<char*>(buffers) + L.a_vals);
   const int64_t status_per_pass = (int64_t)L.nblk * 256;
   const dim3 grid((unsigned)L.nblk);
-  PassArgs a{keys_in, vals_in, nullptr, nullptr, words, L.n_seg, n_dev,
-             L.nblk, 1, 0, 8, C.ghist, C.status, C.tickets, C.err,
-             nullptr, nullptr, 0};
+  PassArgs a{reinterpret_cast<const uint32_t*>(key_bytes), words_in, nullptr,
+             nullptr, words, L.n_seg, n_dev, L.nblk, 1, 0, 8, C.ghist,
+             C.status, C.tickets, C.err, nullptr, nullptr, 0};
   PassArgs b{words, nullptr, nullptr, nullptr, vals_out, L.n_seg, n_dev,
              L.nblk, 1, 24, L.end_bit - 8, C.ghist + 256,
              C.status + status_per_pass, C.tickets + 1, C.err,
              C.ghist, tile_offsets, num_tiles};
-  constexpr int kA = kValsIn | kPackHi, kB = kPairRanges;
+  constexpr int kA = kValsIn | kKeyBytes, kB = kPairRanges;
 #define GS_PAIR_PASSES(R)                                                    \
   launch_traced("rs_onesweep_kernel(pairs:lo)", (rs_onesweep_kernel<kA, R>), \
                 grid, dim3(kThreads), 0, stream, a);                         \
