@@ -20,16 +20,23 @@
  *   "gid"  flat index b*G + r where r is the splat's rank in a stable sort of
  *          image b's depths (ascending, ties by original index); ascending gid
  *          within a tile is front-to-back order.
- *   packed splat record: 12 floats per gid,
- *          {mx, my, a, b, c, opacity, r, g, b, orig_index(bits), plim, lo}
- *          with the conic (a,b,c) meaning power = -0.5*(a dx^2 + 2 b dx dy + c dy^2)
- *          and plim the base-2 exponent limit of the alpha test:
+ *   packed splat record: 16 floats per gid (GSPLAT_RECORD_FLOATS),
+ *          {mx, my, a, b}, {c, opacity, r, g}, {b, orig_index | plain << 31,
+ *          q, lo}, {dxt, beta, gamma, delta}
+ *          with the conic (a,b,c) meaning power = -0.5*(a dx^2 + 2 b dx dy + c dy^2);
+ *          lo = log2(e)_f32 * ln(opacity) and q = plim + lo, where plim is
+ *          the base-2 exponent limit of the alpha test,
  *          log2(e)_f32 * ln(max(alpha_threshold / opacity, FLT_MIN)), with
  *          ln evaluated by a fixed sequence of correctly rounded float
- *          operations (+inf if opacity <= 0 or max_alpha < alpha_threshold,
- *          -inf if alpha_threshold <= 0), and lo = log2(e)_f32 * ln(opacity)
- *          by the same ln (-inf for 0, NaN for a negative or NaN opacity):
- *          the compositors evaluate opacity * 2^p as 2^(p + lo).
+ *          operations (plim = +inf if opacity <= 0 or max_alpha <
+ *          alpha_threshold, -inf if alpha_threshold <= 0; lo = -inf for 0,
+ *          NaN for a negative or NaN opacity): the compositors evaluate
+ *          opacity * 2^p as 2^(p + lo) and test p + lo >= q.  plain (bit 31
+ *          of the orig word) marks a splat whose alpha test never needs the
+ *          power <= 0 test or the max_alpha clamp; the last four floats are
+ *          the splat's constants of the compositors' strip culling.
+ *   sizes  at most 2^24 tiles per image, 2^31 - 1 tiles in the batch and
+ *          fewer than 2^40 / 3 pixels in the batch.
  */
 #ifndef GSPLAT_HIP_H
 #define GSPLAT_HIP_H
