@@ -1244,7 +1244,7 @@ int launch_count(const RasterParams& P, const float* means2d,
                 colors, reinterpret_cast<float4*>(rec_orig), splat_count,
                 block_sums, zero_words, n_zero_words);
   int rc = check_launch("count_kernel");
-  if (rc) return rc;
+  if (rc || pair_count == nullptr) return rc;
   launch_traced("sum_kernel", sum_kernel, dim3(1), dim3(kThreads), 0, stream,
                 block_sums, nblk, pair_count);
   return check_launch("sum_kernel");

@@ -298,7 +298,9 @@ int gsplat_hip_time_next_launch(int which, void* start_event,
 
 namespace {
 // gsplat_hip_bin_count; with colors the count also writes the
-// original-order records that bin_pack_impl copies (use_records).
+// original-order records that bin_pack_impl copies (use_records).  A null
+// pair_count skips the total (the one-call binning reports N from the pack
+// scan instead, which computes the same value).
 int bin_count_impl(const gsplat_raster_meta* meta, const float* means2d,
                    const float* conics, const float* opacities,
                    const float* colors, int32_t* pair_count, void* workspace,
@@ -306,7 +308,7 @@ int bin_count_impl(const gsplat_raster_meta* meta, const float* means2d,
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
-  rc = null_check({means2d, conics, opacities, pair_count, workspace},
+  rc = null_check({means2d, conics, opacities, workspace},
                   "gsplat_hip_bin_count");
   if (rc) return rc;
   const CountLayout L = count_layout(P);
@@ -326,7 +328,9 @@ int bin_count_impl(const gsplat_raster_meta* meta, const float* means2d,
   const size_t z0 = gs::radix_ctl_bytes(L.depth);
   return gs::launch_count(P, means2d, conics, opacities,
                           reinterpret_cast<int32_t*>(base + L.splat_count),
-                          reinterpret_cast<int32_t*>(base + L.block_sums),
+                          pair_count != nullptr
+                              ? reinterpret_cast<int32_t*>(base + L.block_sums)
+                              : nullptr,
                           pair_count, reinterpret_cast<uint32_t*>(base + z0),
                           (int64_t)((L.ctl_end - z0) / sizeof(uint32_t)), s,
                           colors,
@@ -342,6 +346,8 @@ int gsplat_hip_bin_count(const gsplat_raster_meta* meta, const float* means2d,
                          const float* conics, const float* opacities,
                          int32_t* pair_count, void* workspace,
                          size_t workspace_bytes, void* stream) {
+  const int rc = null_check({pair_count}, "gsplat_hip_bin_count");
+  if (rc) return rc;
   return bin_count_impl(meta, means2d, conics, opacities, nullptr, pair_count,
                         workspace, workspace_bytes, stream);
 }
@@ -681,8 +687,8 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
   // host_words[3] turns 1 once host_words[0..2] hold the report
   if (host_words != nullptr) host_words[3] = 0;
   char* base = static_cast<char*>(workspace);
-  int32_t* n_dev = reinterpret_cast<int32_t*>(base);
-  int32_t* status_dev = n_dev + 1;
+  // (header words: 0 unused, 1 the binning's status)
+  int32_t* status_dev = reinterpret_cast<int32_t*>(base) + 1;
   void* cws = base + 256;
   // the long-range flag: a control word of the count workspace, zeroed by
   // the count launch like the pair sort's tickets
@@ -747,8 +753,8 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
     // N is written by the emit's scan
     return rc ? rc : report(splat_offsets + P.num_splats);
   }
-  // 1. per-splat hit counts and N on the count stream (after the caller's
-  //    work on `stream`)
+  // 1. per-splat hit counts on the count stream (after the caller's work on
+  //    `stream`)
   if (cs != s) {
     rc = hip_status(hipEventRecord(ev_in, s), "gsplat_hip_bin: event record");
     if (!rc)
@@ -756,7 +762,7 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
                       "gsplat_hip_bin: stream wait");
     if (rc) return rc;
   }
-  rc = bin_count_impl(meta, means2d, conics, opacities, colors, n_dev, cws,
+  rc = bin_count_impl(meta, means2d, conics, opacities, colors, nullptr, cws,
                       cbytes, cs);
   if (!rc && ev_n != nullptr)
     rc = hip_status(hipEventRecord(ev_n, cs), "gsplat_hip_bin: event record");
@@ -779,8 +785,8 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
                      ebytes, s, host_words != nullptr ? long_dev : nullptr,
                      zero);
   if (rc || host_words == nullptr) return rc;
-  // 5. N (from the count), the status and the long-range flag to the host
-  return report(n_dev);
+  // 5. N (from the pack scan), the status and the long-range flag to the host
+  return report(splat_offsets + P.num_splats);
 }
 
 }  // namespace
