@@ -61,21 +61,28 @@ def kernel_work(name, BG, N, walked, T):
     table = {
         "count_depth_runs_kernel": ("hbm", 40.0 * BG,
                                     "40 B/splat: count 24 read + 4 written, depth runs 4 read + 8 written"),
-        "rank_pack_kernel": ("hbm", 104.0 * BG, "104 B/splat: run keys+values 8, attributes 36, count 4 read; "
-                                                "record 48, perm 4, count 4 written"),
+        "rank_pack_kernel": ("hbm", 120.0 * BG, "120 B/splat: run keys+values 8, attributes 36, count 4 read; "
+                                                "record 64, perm 4, count 4 written"),
         "emit_kernel<true>": ("hbm", 32.0 * BG + 8.0 * N, "32 B/splat (record 24, count 4 read, offset 4 written) "
                                                          "+ 8 B/pair (key, value)"),
-        "emit_kernel<false>": ("hbm", 28.0 * BG + 8.0 * N, "28 B/splat (record 24, offset 4) + 8 B/pair"),
-        "count_kernel": ("hbm", 28.0 * BG, "28 B/splat: means 8, conic 12, opacity 4 read, count 4 written"),
+        "emit_kernel<false>": ("hbm", 28.0 * BG + (5.0 if N >= 1 << 23 else 8.0) * N,
+                               "28 B/splat (record 24, offset 4) + 8 B/pair (key, value), or 5 B/pair (packed word "
+                               "+ low tile byte) for the two-pass sort of 2^23+ pairs"),
+        "count_kernel": ("hbm", 104.0 * BG, "104 B/splat (one-call path): means 8, conic 12, opacity 4, colours 12 "
+                                            "read, count 4 and the 64-B record written"),
         "depth_run_sort_kernel": ("hbm", 12.0 * BG, "12 B/splat: depth 4 read, run key + value 8 written"),
         "depth_run_rank_kernel": ("hbm", 12.0 * BG, "12 B/splat: run key + value 8 read, perm 4 written"),
-        "pack_kernel": ("hbm", 96.0 * BG, "96 B/splat: perm 4, attributes 36, count 4 read; record 48, offset 4 "
-                                          "written"),
+        "pack_kernel": ("hbm", 136.0 * BG, "136 B/splat: perm 4 and the count's 64-B record read; record 64, "
+                                           "offset 4 written (one-call path)"),
         "rs_global_hist_kernel(depth)": ("hbm", 4.0 * BG, "4 B/splat (depth keys read)"),
         "rs_global_hist_kernel(keys)": ("hbm", 4.0 * N, "4 B/pair (keys read)"),
         "rs_onesweep_kernel(depth)": ("hbm", 16.0 * BG, "16 B/splat per pass (key + value read and written)"),
         "rs_onesweep_kernel(keys)": ("hbm", 16.0 * N, "16 B/pair per pass (key + value read and written)"),
         "ranges_kernel": ("hbm", 4.0 * N + 4.0 * T, "4 B/pair (sorted keys read) + 4 B/tile (offsets written)"),
+        "rs_onesweep_kernel(pairs:lo)": ("hbm", 9.0 * N, "9 B/pair: low tile byte + packed word read, word written"),
+        "rs_onesweep_kernel(pairs:hi)": ("hbm", 8.0 * N + 4.0 * T, "8 B/pair: word read, gid written; 4 B/tile"),
+        "ranges_finish_kernel": ("hbm", 8.0 * T + 64.0 * BG, "8 B/tile (offsets read) + 64 B/splat (gradient "
+                                                            "records zeroed)"),
         "bucket_sort_kernel": ("hbm", 12.0 * N + 4.0 * T + 64.0 * BG,
                                "12 B/pair (key, value read; id written) + 4 B/tile + 64 B/splat (gradient record "
                                "zeroed)"),
