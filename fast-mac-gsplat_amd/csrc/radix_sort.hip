@@ -52,6 +52,42 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// match_digit for two rounds at once: the two dependency chains interleave.
+__device__ __forceinline__ void match_digit2(uint32_t d0, uint32_t d1,
+                                             uint64_t act0, uint64_t act1,
+                                             uint64_t& m0, uint64_t& m1) {
+  uint32_t lo0 = (uint32_t)act0, hi0 = (uint32_t)(act0 >> 32);
+  uint32_t lo1 = (uint32_t)act1, hi1 = (uint32_t)(act1 >> 32);
+#pragma unroll
+  for (int bit = 0; bit < 8; ++bit) {
+    uint32_t n0 = (uint32_t)__builtin_amdgcn_sbfe((int)d0, bit, 1);
+    uint32_t n1 = (uint32_t)__builtin_amdgcn_sbfe((int)d1, bit, 1);
+    asm volatile("" : "+v"(n0), "+v"(n1));
+    const uint64_t b0 = __builtin_amdgcn_ballot_w64(n0 != 0u);
+    const uint64_t b1 = __builtin_amdgcn_ballot_w64(n1 != 0u);
+    lo0 = __builtin_amdgcn_bitop3_b32(lo0, (uint32_t)b0, n0, 0x90);
+    hi0 = __builtin_amdgcn_bitop3_b32(hi0, (uint32_t)(b0 >> 32), n0, 0x90);
+    lo1 = __builtin_amdgcn_bitop3_b32(lo1, (uint32_t)b1, n1, 0x90);
+    hi1 = __builtin_amdgcn_bitop3_b32(hi1, (uint32_t)(b1 >> 32), n1, 0x90);
+  }
+  m0 = ((uint64_t)hi0 << 32) | lo0;
+  m1 = ((uint64_t)hi1 << 32) | lo1;
+}
+
+// Element i of the array at base, addressed as a uniform base plus a 32-bit
+// byte offset (i * sizeof(T) < 2^32 for every caller: segments hold at most
+// 2^29 elements), which loads and stores take as one register.
+template <class T>
+__device__ __forceinline__ const T& at32(const T* base, uint32_t i) {
+  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) +
+                                     i * (uint32_t)sizeof(T));
+}
+template <class T>
+__device__ __forceinline__ T& at32(T* base, uint32_t i) {
+  return *reinterpret_cast<T*>(reinterpret_cast<char*>(base) +
+                               i * (uint32_t)sizeof(T));
+}
+
 struct PassArgs {
   const uint32_t* keys_in;   // unused with kDepthKeys
   const uint32_t* vals_in;   // unused without kValsIn (values = in-segment index)
@@ -109,9 +145,9 @@ enum : int {
   kKeyBytes = 32
 };
 
-// Exclusive scan of one value per thread over the 256-thread block.
-__device__ __forceinline__ uint32_t block_excl_scan256(uint32_t v,
-                                                       uint32_t* wsum) {
+// Exclusive scan of one value per thread over a block of kW wavefronts.
+template <int kW = kWaves>
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* wsum) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   uint32_t inc = v;
 #pragma unroll
@@ -167,21 +203,94 @@ __global__ __launch_bounds__(kThreads) void rs_global_hist_kernel(
   }
 }
 
-template <int kMode, int kR>
-__global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
-  constexpr int kWaveItems = 64 * kR;
-  constexpr int kBlockItems = kWaves * kWaveItems;
-  __shared__ uint32_t cnt[kWaves][256];
-  __shared__ uint32_t dstart[256];
-  __shared__ uint32_t gdelta[256];  // global position of digit d's LDS slot 0
-  __shared__ uint32_t wsum[kWaves];
-  __shared__ uint32_t sk[kBlockItems];
-  // (kPairRanges: the value is the key word's low 24 bits, so this holds the
-  // block's digits in input order instead, one byte each)
-  __shared__ uint32_t sv[kBlockItems];
+// Ranks the wavefront's kR rounds of 64 elements: rreg[r] = the element's
+// rank among the wavefront's elements of its digit | digit << 16 (all ones
+// for lanes past the segment's end), counting in wcnt (the wavefront's digit
+// counters).  Two rounds at a time: their matches interleave; the count
+// updates stay in round order.  kFull: every element of the block is valid
+// (no per-round masks).  kPairRanges with boundaries: the digits are also
+// kept in input order as bytes at dig8.
+template <int kMode, int kR, bool kFull>
+__device__ __forceinline__ void rank_rounds(uint32_t (&kreg)[kR],
+                                            uint32_t (&vreg)[kR],
+                                            uint32_t (&rreg)[kR],
+                                            uint32_t* wcnt, uint8_t* dig8,
+                                            uint32_t lo, uint32_t n32,
+                                            int shift, uint32_t dmask,
+                                            bool boundaries) {
   constexpr bool kRanges = (kMode & kPairRanges) != 0;
-  __shared__ uint32_t pstart[kRanges ? 256 : 1];  // P[lo] (kPairRanges)
-  __shared__ uint32_t hist[kRanges ? 256 : 1];    // digits before P[lo]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t lt = lanemask_lt();
+#pragma unroll
+  for (int r = 0; r < kR; r += 2) {
+    uint32_t d[2];
+    bool valid[2];
+    uint64_t act[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t j = lo + (uint32_t)((r + u) * 64 + lane);
+      valid[u] = kFull || j < n32;
+      if (kMode & kDepthKeys) kreg[r + u] = depth_key(__uint_as_float(kreg[r + u]));
+      if (kRanges)
+        vreg[r + u] = kreg[r + u] & 0xffffffu;
+      else if (!(kMode & kValsIn))
+        vreg[r + u] = j;
+      d[u] = (kreg[r + u] >> shift) & dmask;
+      if (kRanges && boundaries && valid[u])
+        dig8[wave * (64 * kR) + (r + u) * 64 + lane] = (uint8_t)d[u];
+      act[u] = kFull ? ~0ull : __ballot(valid[u]);
+    }
+    uint64_t peers[2];
+    match_digit2(d[0], d[1], act[0], act[1], peers[0], peers[1]);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t below = (uint32_t)__popcll(peers[u] & lt);
+      // Every lane of the digit reads its count, then the digit's lowest
+      // lane adds the group's size: one wavefront's LDS accesses take effect
+      // in program order, so all of them see the count before the addition.
+      const uint32_t old = wcnt[d[u]];
+      __builtin_amdgcn_wave_barrier();  // the read stays before the addition
+      if (valid[u] && below == 0u)
+        atomicAdd(&wcnt[d[u]], (uint32_t)__popcll(peers[u]));
+      rreg[r + u] = valid[u] ? ((old + below) | (d[u] << 16)) : 0xffffffffu;
+    }
+  }
+}
+
+// A block of 256 kR elements is ranked by onesweep_waves(kR) wavefronts of
+// onesweep_rounds(kR) rounds each: blocks of 8192 elements use eight
+// wavefronts of 16 rounds, which halves the registers that hold a lane's
+// elements (four wavefronts per SIMD instead of two).
+constexpr int onesweep_waves(int rounds) { return rounds == 32 ? 8 : kWaves; }
+constexpr int onesweep_rounds(int rounds) { return rounds == 32 ? 16 : rounds; }
+
+template <int kMode, int kBlockRounds>
+__global__ __launch_bounds__(64 * onesweep_waves(kBlockRounds))
+void rs_onesweep_kernel(PassArgs a) {
+  constexpr int kW = onesweep_waves(kBlockRounds);
+  constexpr int kR = onesweep_rounds(kBlockRounds);
+  constexpr int kT = 64 * kW;
+  constexpr int kWaveItems = 64 * kR;
+  constexpr int kBlockItems = kW * kWaveItems;
+  constexpr bool kRanges = (kMode & kPairRanges) != 0;
+  constexpr bool kBytes = (kMode & kKeyBytes) != 0;
+  __shared__ uint32_t cnt[kW][256];
+  // dstart: digit d's first slot in the block's sorted order; gdelta: the
+  // global position of that slot.  (kPairRanges: they are written after the
+  // tile ranges and hold P[lo] and the digit counts before it until then.)
+  __shared__ uint32_t dstart[256];
+  __shared__ uint32_t gdelta[256];
+  __shared__ uint32_t wsum[kW];
+  // The block in sorted order: keys (one byte each with kKeyBytes; with
+  // kPairRanges the key is the word and, before the scatter, the block's
+  // digits in input order are kept here, one byte each) and values (none
+  // with kPairRanges: the value is the word's low 24 bits).  Sizes are
+  // per mode so that more workgroups fit in a CU's LDS.
+  __shared__ uint32_t sk[kBytes ? kBlockItems / 4 : kBlockItems];
+  __shared__ uint32_t sv[kRanges ? 1 : kBlockItems];
+  uint32_t* const pstart = dstart;  // P[lo] (kPairRanges)
+  uint32_t* const hist = gdelta;    // digits before P[lo] (kPairRanges)
+  uint8_t* const dig8 = reinterpret_cast<uint8_t*>(sk);
 
   const int vb = take_ticket(a.ticket);
   const int seg = vb / a.nblk;
@@ -192,87 +301,80 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
   const int64_t n_seg =
       a.n_dev ? min(a.n_seg, (int64_t)max(*a.n_dev, 0)) : a.n_seg;
   if ((int64_t)blk * kBlockItems >= n_seg) return;
-  for (int i = t; i < kWaves * 256; i += kThreads) (&cnt[0][0])[i] = 0u;
+  const uint32_t n32 = (uint32_t)n_seg;  // (segments hold at most 2^29)
+  for (int i = t; i < kW * 256; i += kT) (&cnt[0][0])[i] = 0u;
   // kPairRanges: does this block hold a position P[lo]?
-  const int64_t blk_lo = (int64_t)blk * kBlockItems;
-  const int64_t blk_hi = min(n_seg, blk_lo + kBlockItems);
+  const uint32_t blk_lo = (uint32_t)blk * kBlockItems;
+  const uint32_t blk_hi = min(n32, blk_lo + kBlockItems);
   bool boundaries = false;
   if (kRanges) {
-    const uint32_t pl = block_excl_scan256(a.ghist_a[t], wsum);
-    pstart[t] = pl;
-    hist[t] = 0u;
-    boundaries = __syncthreads_or((int64_t)pl >= blk_lo && (int64_t)pl < blk_hi);
+    const uint32_t pl = block_excl_scan<kW>(t < 256 ? a.ghist_a[t] : 0u, wsum);
+    if (t < 256) {
+      pstart[t] = pl;
+      hist[t] = 0u;
+    }
+    boundaries = __syncthreads_or(t < 256 && pl >= blk_lo && pl < blk_hi);
   }
 
   const int64_t seg_base = (int64_t)seg * a.n_seg;
-  const int64_t lo = (int64_t)blk * kBlockItems + (int64_t)wave * kWaveItems;
+  const uint32_t lo = blk_lo + (uint32_t)(wave * kWaveItems);
   const uint32_t dmask = (1u << a.digit_bits) - 1u;
 
   // Issue every load of this lane's kR elements before ranking any of them
   // (indices clamped into the segment; lanes past its end are masked out of
   // the ranking below).
   uint32_t kreg[kR], vreg[kR], rreg[kR];
+  {
+    const uint8_t* kin8 = reinterpret_cast<const uint8_t*>(a.keys_in) + seg_base;
+    const uint32_t* kin = a.keys_in + seg_base;
+    const float* din = a.depth_src + seg_base;
+    const uint32_t* vin = a.vals_in + seg_base;
 #pragma unroll
-  for (int r = 0; r < kR; ++r) {
-    const int64_t src = seg_base + min(lo + r * 64 + lane, n_seg - 1);
-    if (kMode & kKeyBytes)
-      kreg[r] = reinterpret_cast<const uint8_t*>(a.keys_in)[src];
-    else
-      kreg[r] = (kMode & kDepthKeys) ? __float_as_uint(a.depth_src[src])
-                                     : a.keys_in[src];
-    if (kMode & kValsIn) vreg[r] = a.vals_in[src];
+    for (int r = 0; r < kR; ++r) {
+      const uint32_t src = min(lo + (uint32_t)(r * 64 + lane), n32 - 1u);
+      if (kBytes)
+        kreg[r] = at32(kin8, src);
+      else
+        kreg[r] = (kMode & kDepthKeys) ? __float_as_uint(at32(din, src))
+                                       : at32(kin, src);
+      if (kMode & kValsIn) vreg[r] = at32(vin, src);
+    }
   }
   // this pass's global digit count of digit t (digit bases below)
-  const uint32_t gh = a.ghist[(int64_t)seg * 256 + t];
+  const uint32_t gh = t < 256 ? a.ghist[(int64_t)seg * 256 + t] : 0u;
   __syncthreads();
 
-  const uint64_t lt = lanemask_lt();
-#pragma unroll
-  for (int r = 0; r < kR; ++r) {
-    const int64_t j = lo + r * 64 + lane;
-    const bool valid = j < n_seg;
-    if (kMode & kDepthKeys) kreg[r] = depth_key(__uint_as_float(kreg[r]));
-    if (kRanges)
-      vreg[r] = kreg[r] & 0xffffffu;
-    else if (!(kMode & kValsIn))
-      vreg[r] = (uint32_t)j;
-    const uint32_t d = (kreg[r] >> a.shift) & dmask;
-    if (kRanges && boundaries && valid)
-      reinterpret_cast<uint8_t*>(sv)[wave * kWaveItems + r * 64 + lane] =
-          (uint8_t)d;
-    const uint64_t peers = match_digit(d, __ballot(valid));
-    const uint32_t below = (uint32_t)__popcll(peers & lt);
-    // Every lane of the digit reads its count, then the digit's lowest lane
-    // adds the group's size: one wavefront's LDS accesses take effect in
-    // program order, so all of them see the count before the addition.
-    const uint32_t old = cnt[wave][d];
-    __builtin_amdgcn_wave_barrier();  // the read stays before the addition
-    if (valid && below == 0u) atomicAdd(&cnt[wave][d], (uint32_t)__popcll(peers));
-    rreg[r] = valid ? ((old + below) | (d << 16)) : 0xffffffffu;
-  }
+  if (blk_hi - blk_lo == (uint32_t)kBlockItems)
+    rank_rounds<kMode, kR, true>(kreg, vreg, rreg, cnt[wave], dig8, lo, n32,
+                                 a.shift, dmask, boundaries);
+  else
+    rank_rounds<kMode, kR, false>(kreg, vreg, rreg, cnt[wave], dig8, lo, n32,
+                                  a.shift, dmask, boundaries);
   __syncthreads();
 
-  // Thread t owns digit t.
-  const uint32_t c0 = cnt[0][t], c1 = cnt[1][t], c2 = cnt[2][t], c3 = cnt[3][t];
-  const uint32_t tot = c0 + c1 + c2 + c3;
+  // Thread t < 256 owns digit t: its count in the block, and each
+  // wavefront's first slot among the block's elements of the digit.
+  uint32_t tot = 0u;
   uint32_t* my_status = a.status + ((int64_t)seg * a.nblk + blk) * 256 + t;
-  status_store(my_status, (blk == 0 ? kFlagInc32 : kFlagAgg32) | tot);
-  cnt[0][t] = 0u;
-  cnt[1][t] = c0;
-  cnt[2][t] = c0 + c1;
-  cnt[3][t] = c0 + c1 + c2;
-  const uint32_t dbase = block_excl_scan256(gh, wsum);
-  const uint32_t local = block_excl_scan256(tot, wsum);
+  if (t < 256) {
+    uint32_t c[kW];
+#pragma unroll
+    for (int w = 0; w < kW; ++w) c[w] = cnt[w][t];
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+      cnt[w][t] = tot;
+      tot += c[w];
+    }
+    status_store(my_status, (blk == 0 ? kFlagInc32 : kFlagAgg32) | tot);
+  }
+  const uint32_t dbase = block_excl_scan<kW>(gh, wsum);
+  const uint32_t local = block_excl_scan<kW>(tot, wsum);
   uint32_t prefix = 0u;
-  if (blk > 0) {
+  if (blk > 0 && t < 256) {
     prefix = lookback32<kLookbackWindow>(
         a.status + (int64_t)seg * a.nblk * 256 + t, blk, 256, a.err);
     status_store(my_status, kFlagInc32 | (prefix + tot));
   }
-  dstart[t] = local;
-  // (modulo 2^32: the positions themselves are below 2^29)
-  gdelta[t] = dbase + prefix - local;
-  __syncthreads();
 
   if (kRanges) {
     // Tile ranges at the positions P[lo] inside this block, in increasing
@@ -284,66 +386,74 @@ __global__ __launch_bounds__(kThreads) void rs_onesweep_kernel(PassArgs a) {
       // (low bytes without pairs share their position with the next one:
       // hist is brought up to each distinct position once)
       uint32_t q_prev = 0u;
-      for (int lo = 0; lo < 256; ++lo) {
-        const int64_t p = pstart[lo];
+      for (int l = 0; l < 256; ++l) {
+        const uint32_t p = pstart[l];
         if (p < blk_lo || p >= blk_hi) continue;  // uniform
-        const uint32_t q = (uint32_t)(p - blk_lo);
+        const uint32_t q = p - blk_lo;
         if (q != q_prev) {  // uniform
           __syncthreads();  // the reads of hist at q_prev are done
-          for (uint32_t i = q_prev + t; i < q; i += kThreads)
-            atomicAdd(&hist[reinterpret_cast<const uint8_t*>(sv)[i]], 1u);
+          for (uint32_t i = q_prev + t; i < q; i += kT)
+            atomicAdd(&hist[dig8[i]], 1u);
           q_prev = q;
           __syncthreads();
         }
-        const int tile = (t << 8) | lo;
+        const int tile = (t << 8) | l;
         if (hi_ok && tile < a.num_tiles)
           a.tile_offsets[tile] = (int32_t)(dbase + prefix + hist[t]);
       }
-      __syncthreads();  // before the scatter below reuses LDS
     }
     if (blk == 0) {
       // P[lo] = n: every pair of digit hi lies before (hi << 8 | lo)
-      for (int lo = 0; lo < 256; ++lo) {
-        if ((int64_t)pstart[lo] != n_seg) continue;  // uniform
-        const int tile = (t << 8) | lo;
+      for (int l = 0; l < 256; ++l) {
+        if (pstart[l] != n32) continue;  // uniform
+        const int tile = (t << 8) | l;
         if (hi_ok && tile < a.num_tiles)
           a.tile_offsets[tile] = (int32_t)(dbase + gh);
       }
       if (t == 0) a.tile_offsets[a.num_tiles] = (int32_t)n_seg;
     }
+    __syncthreads();  // pstart, hist and the digit bytes are read
   }
+  if (t < 256) {
+    dstart[t] = local;
+    // (modulo 2^32: the positions themselves are below 2^29)
+    gdelta[t] = dbase + prefix - local;
+  }
+  __syncthreads();
 
-  // (kPairRanges: sv, read above, is not written here)
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
     if (rreg[r] != 0xffffffffu) {
       const uint32_t d = rreg[r] >> 16;
       const uint32_t pos = dstart[d] + cnt[wave][d] + (rreg[r] & 0xffffu);
-      sk[pos] = kreg[r];
+      if (kBytes)
+        dig8[pos] = (uint8_t)d;  // the key byte is the digit
+      else
+        sk[pos] = kreg[r];
       if (!kRanges) sv[pos] = vreg[r];
     }
   }
   __syncthreads();
 
   // Unrolled, so that the LDS reads of all kR elements are in flight
-  // together; 32-bit positions (n_seg <= 2^29).
-  const int64_t remain = n_seg - (int64_t)blk * kBlockItems;
-  const int count = remain < kBlockItems ? (int)remain : kBlockItems;
-  const uint32_t n32 = (uint32_t)n_seg;
+  // together.
+  const uint32_t count = blk_hi - blk_lo;
+  uint32_t* kout = a.keys_out + seg_base;
+  uint32_t* vout = a.vals_out + seg_base;
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
-    const int i = t + r * kThreads;
+    const uint32_t i = (uint32_t)(t + r * kT);
     if (i < count) {
-      const uint32_t key = sk[i];
-      const uint32_t pos = gdelta[(key >> a.shift) & dmask] + (uint32_t)i;
+      const uint32_t key = kBytes ? (uint32_t)dig8[i] : sk[i];
+      const uint32_t pos = gdelta[(key >> a.shift) & dmask] + i;
       if (pos < n32) {  // (fails only with histograms inconsistent with the keys)
-        if (kMode & kKeysOut) a.keys_out[seg_base + pos] = key;
+        if (kMode & kKeysOut) at32(kout, pos) = key;
         if (kRanges)
-          a.vals_out[seg_base + pos] = key & 0xffffffu;
+          at32(vout, pos) = key & 0xffffffu;
         else if (kMode & kPackHi)
-          a.vals_out[seg_base + pos] = ((key >> 8) << 24) | sv[i];
+          at32(vout, pos) = ((key >> 8) << 24) | sv[i];
         else
-          a.vals_out[seg_base + pos] = sv[i];
+          at32(vout, pos) = sv[i];
       }
     }
   }
@@ -502,7 +612,8 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
     switch (mode * 32 + L.rounds) {
 #define GS_ONESWEEP_CASE(M, R)                                              \
   case M * 32 + R:                                                          \
-    launch_traced(pass_name, (rs_onesweep_kernel<M, R>), grid, dim3(kThreads), \
+    launch_traced(pass_name, (rs_onesweep_kernel<M, R>), grid,               \
+                  dim3(64 * onesweep_waves(R)),                             \
                   0, stream, a);                                            \
     break;
 #define GS_ONESWEEP_MODE(M) \
@@ -563,9 +674,9 @@ int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
   constexpr int kA = kValsIn | kKeyBytes, kB = kPairRanges;
 #define GS_PAIR_PASSES(R)                                                    \
   launch_traced("rs_onesweep_kernel(pairs:lo)", (rs_onesweep_kernel<kA, R>), \
-                grid, dim3(kThreads), 0, stream, a);                         \
+                grid, dim3(64 * onesweep_waves(R)), 0, stream, a);           \
   launch_traced("rs_onesweep_kernel(pairs:hi)", (rs_onesweep_kernel<kB, R>), \
-                grid, dim3(kThreads), 0, stream, b);
+                grid, dim3(64 * onesweep_waves(R)), 0, stream, b);
   if (L.rounds == 4) {
     GS_PAIR_PASSES(4)
   } else if (L.rounds == 16) {
