@@ -578,13 +578,15 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
   // 2-3. tiles below 2^16 and gids below 2^24: the emit writes the pairs as
   // words and low bytes (the sorted keys' buffer holds the bytes) for two
   // passes over packed words, the second of which writes the tile ranges
+  // (the emit zeroes the sort's control words that must start at zero)
   if (gs::radix_pair_ranges_ok(L.pairs, P.num_splats)) {
     uint8_t* key_bytes = reinterpret_cast<uint8_t*>(sorted_keys);
+    int64_t zero_words = 0;
+    uint32_t* zero_span = gs::radix_pair_zero_span(L.pairs, ctl, &zero_words);
     rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals,
                          L.pairs.passes,
                          reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
-                         ctl.status, L.pairs.status_words, s, scan, 0,
-                         key_bytes);
+                         zero_span, zero_words, s, scan, 0, key_bytes);
     if (!rc)
       rc = gs::radix_pair_sort_ranges(
           L.pairs, ctl, base + L.buffers, key_bytes, keys,

@@ -109,7 +109,10 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
 // plan's first ping-pong value buffer; ghist holds both passes' counts.
 bool radix_pair_ranges_ok(const RadixPlan& L, int64_t num_values);
 // Its input is the emit's key_bytes form: key_bytes (the tiles' low bytes)
-// and words ((tile >> 8) << 24 | gid).
+// and words ((tile >> 8) << 24 | gid).  The control words that
+// radix_pair_zero_span returns (*words of them) must be zero before it.
+uint32_t* radix_pair_zero_span(const RadixPlan& L, const RadixCtl& C,
+                               int64_t* words);
 int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
                            void* buffers, const uint8_t* key_bytes,
                            const uint32_t* words, uint32_t* vals_out,

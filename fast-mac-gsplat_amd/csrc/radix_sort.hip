@@ -136,13 +136,22 @@ struct PassArgs {
 //               it writes tile_offsets[(hi << 8) | lo] for every hi.  Every
 //               entry is written once (empty tiles included); P[lo] = n is
 //               left to workgroup 0, which also writes tile_offsets[T] = n.
+//  kPreCounts   (with either): every block's prefix (the elements of each
+//               digit in the blocks before it) is already in its status
+//               words, from rs_block_counts_kernel and rs_block_scan_kernel
+//               launched before the pass; the pass reads it instead of
+//               looking back.  A decoupled look-back serialises the
+//               workgroups (each one's prefix waits for a predecessor's,
+//               a few memory round trips per window of predecessors), which
+//               at 2^23+ elements bounds the pass more than its work does.
 enum : int {
   kDepthKeys = 1,
   kValsIn = 2,
   kKeysOut = 4,
   kPackHi = 8,
   kPairRanges = 16,
-  kKeyBytes = 32
+  kKeyBytes = 32,
+  kPreCounts = 64
 };
 
 // Exclusive scan of one value per thread over a block of kW wavefronts.
@@ -257,6 +266,122 @@ __device__ __forceinline__ void rank_rounds(uint32_t (&kreg)[kR],
   }
 }
 
+// Blocks per chunk of the block-count scan, and thread groups per digit in
+// its workgroups.
+constexpr int kScanChunk = 128;
+constexpr int kScanQ = 4;
+// Blocks counted per workgroup of rs_block_counts_kernel: kSub blocks of
+// bytes (8 KB each) are read together, so that each workgroup has enough
+// loads in flight.
+constexpr int counts_sub(bool bytes) { return bytes ? 4 : 1; }
+
+// Digit counts of every block of 256 kBlockRounds elements of a pass
+// (kPreCounts): status[b][d] = count, and each count added to its chunk's
+// total, chunk_tot[b / kScanChunk][d] (zeroed before).  Keys are bytes
+// (kBytes: the tile-pair sort's low tile bytes) or words (digit = (word >>
+// shift) & dmask).  Workgroup g counts blocks kSub g .. kSub g + kSub - 1;
+// elements past the count are not counted.
+template <bool kBytes, int kBlockRounds>
+__global__ __launch_bounds__(kThreads) void rs_block_counts_kernel(
+    const uint32_t* keys, int64_t n_cap, const int32_t* n_dev, int shift,
+    uint32_t dmask, uint32_t* status, uint32_t* chunk_tot) {
+  constexpr int kSub = counts_sub(kBytes);
+  constexpr int kItems = kThreads * kBlockRounds;
+  constexpr int kLoads = kBytes ? kBlockRounds / 4 : kBlockRounds;
+  __shared__ uint32_t h[kSub][kWaves][256];
+  const int t = threadIdx.x, wave = t >> 6;
+  const int64_t n = n_dev ? min(n_cap, (int64_t)max(*n_dev, 0)) : n_cap;
+  const int blk0 = blockIdx.x * kSub;
+  if ((int64_t)blk0 * kItems >= n) return;
+  const uint32_t n32 = (uint32_t)n;
+  // word j holds elements (kBytes ? 4 : 1) * j onwards
+  const uint32_t words_end = kBytes ? (n32 + 3u) / 4u : n32;
+  constexpr uint32_t kBlockWords = kBytes ? kItems / 4 : kItems;
+  uint32_t v[kSub][kLoads];
+#pragma unroll
+  for (int sb = 0; sb < kSub; ++sb)
+#pragma unroll
+    for (int r = 0; r < kLoads; ++r)
+      v[sb][r] = at32(keys, min((uint32_t)(blk0 + sb) * kBlockWords +
+                                    (uint32_t)(r * kThreads + t),
+                                words_end - 1u));
+  for (int i = t; i < kSub * kWaves * 256; i += kThreads) (&h[0][0][0])[i] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int sb = 0; sb < kSub; ++sb)
+#pragma unroll
+    for (int r = 0; r < kLoads; ++r) {
+      const uint32_t w = (uint32_t)(blk0 + sb) * kBlockWords + (uint32_t)(r * kThreads + t);
+      if (kBytes) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (w * 4u + k < n32)
+            atomicAdd(&h[sb][wave][(v[sb][r] >> (8 * k)) & 255u], 1u);
+      } else if (w < n32) {
+        atomicAdd(&h[sb][wave][(v[sb][r] >> shift) & dmask], 1u);
+      }
+    }
+  __syncthreads();
+#pragma unroll
+  for (int sb = 0; sb < kSub; ++sb) {
+    const int blk = blk0 + sb;
+    if ((int64_t)blk * kItems >= n) break;
+    uint32_t c = 0u;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) c += h[sb][w][t];
+    status[(int64_t)blk * 256 + t] = c;
+    if (c != 0u) atomicAdd(&chunk_tot[(int64_t)(blk / kScanChunk) * 256 + t], c);
+  }
+}
+
+// The counts of rs_block_counts_kernel replaced by their exclusive prefix
+// over the blocks, per digit.  Workgroup c (kScanQ groups of 256 threads,
+// thread t of a group for digit t) takes chunk c: group q sums the totals of
+// every kScanQ-th chunk before it from q on (no order among workgroups) and
+// the counts of the chunk's rows q kRows .. q kRows + kRows - 1; the groups
+// combine their sums in LDS, then each scans its rows.
+template <int kBlockRounds>
+__global__ __launch_bounds__(256 * kScanQ) void rs_block_scan_kernel(
+    uint32_t* status, const uint32_t* chunk_tot, int64_t n_cap,
+    const int32_t* n_dev) {
+  constexpr int64_t kItems = (int64_t)kThreads * kBlockRounds;
+  constexpr int kRows = kScanChunk / kScanQ;
+  __shared__ uint32_t part[kScanQ][256];
+  __shared__ uint32_t before[kScanQ][256];
+  const int t = threadIdx.x & 255, q = threadIdx.x >> 8;
+  const int64_t n = n_dev ? min(n_cap, (int64_t)max(*n_dev, 0)) : n_cap;
+  const int nblk = (int)((n + kItems - 1) / kItems);
+  const int c = blockIdx.x;
+  const int b0 = c * kScanChunk;
+  if (b0 >= nblk) return;
+  const int nb = min(kScanChunk, nblk - b0);
+  uint32_t v[kRows];
+#pragma unroll
+  for (int k = 0; k < kRows; ++k) {
+    const int row = q * kRows + k;
+    const uint32_t x = status[(int64_t)(b0 + min(row, nb - 1)) * 256 + t];
+    v[k] = row < nb ? x : 0u;
+  }
+  uint32_t pre = 0u;
+#pragma unroll 8
+  for (int j = q; j < c; j += kScanQ) pre += chunk_tot[(int64_t)j * 256 + t];
+  uint32_t sum = 0u;
+#pragma unroll
+  for (int k = 0; k < kRows; ++k) sum += v[k];
+  part[q][t] = sum;
+  before[q][t] = pre;
+  __syncthreads();
+  uint32_t run = 0u;
+#pragma unroll
+  for (int i = 0; i < kScanQ; ++i) run += before[i][t] + (i < q ? part[i][t] : 0u);
+#pragma unroll
+  for (int k = 0; k < kRows; ++k) {
+    const int row = q * kRows + k;
+    if (row < nb) status[(int64_t)(b0 + row) * 256 + t] = run;
+    run += v[k];
+  }
+}
+
 // A block of 256 kR elements is ranked by onesweep_waves(kR) wavefronts of
 // onesweep_rounds(kR) rounds each: blocks of 8192 elements use eight
 // wavefronts of 16 rounds, which halves the registers that hold a lane's
@@ -342,6 +467,20 @@ void rs_onesweep_kernel(PassArgs a) {
   }
   // this pass's global digit count of digit t (digit bases below)
   const uint32_t gh = t < 256 ? a.ghist[(int64_t)seg * 256 + t] : 0u;
+  constexpr bool kPre = (kMode & kPreCounts) != 0;
+  uint32_t* my_status = a.status + ((int64_t)seg * a.nblk + blk) * 256 + t;
+  uint32_t tot = 0u, prefix = 0u, dbase = 0u, local = 0u;
+  if (kPre) {
+    // the block's prefix and count (the next block's prefix, or the
+    // digit's total after the last block), while the loads fly
+    if (t < 256) {
+      prefix = *my_status;
+      const uint32_t last = (n32 - 1u) / kBlockItems;
+      tot = ((uint32_t)blk < last ? my_status[256] : gh) - prefix;
+    }
+    dbase = block_excl_scan<kW>(gh, wsum);
+    local = block_excl_scan<kW>(tot, wsum);
+  }
   __syncthreads();
 
   if (blk_hi - blk_lo == (uint32_t)kBlockItems)
@@ -354,26 +493,29 @@ void rs_onesweep_kernel(PassArgs a) {
 
   // Thread t < 256 owns digit t: its count in the block, and each
   // wavefront's first slot among the block's elements of the digit.
-  uint32_t tot = 0u;
-  uint32_t* my_status = a.status + ((int64_t)seg * a.nblk + blk) * 256 + t;
   if (t < 256) {
     uint32_t c[kW];
 #pragma unroll
     for (int w = 0; w < kW; ++w) c[w] = cnt[w][t];
+    uint32_t run = 0u;
 #pragma unroll
     for (int w = 0; w < kW; ++w) {
-      cnt[w][t] = tot;
-      tot += c[w];
+      cnt[w][t] = run;
+      run += c[w];
     }
-    status_store(my_status, (blk == 0 ? kFlagInc32 : kFlagAgg32) | tot);
+    if (!kPre) {
+      tot = run;
+      status_store(my_status, (blk == 0 ? kFlagInc32 : kFlagAgg32) | tot);
+    }
   }
-  const uint32_t dbase = block_excl_scan<kW>(gh, wsum);
-  const uint32_t local = block_excl_scan<kW>(tot, wsum);
-  uint32_t prefix = 0u;
-  if (blk > 0 && t < 256) {
-    prefix = lookback32<kLookbackWindow>(
-        a.status + (int64_t)seg * a.nblk * 256 + t, blk, 256, a.err);
-    status_store(my_status, kFlagInc32 | (prefix + tot));
+  if (!kPre) {
+    dbase = block_excl_scan<kW>(gh, wsum);
+    local = block_excl_scan<kW>(tot, wsum);
+    if (blk > 0 && t < 256) {
+      prefix = lookback32<kLookbackWindow>(
+          a.status + (int64_t)seg * a.nblk * 256 + t, blk, 256, a.err);
+      status_store(my_status, kFlagInc32 | (prefix + tot));
+    }
   }
 
   if (kRanges) {
@@ -498,7 +640,11 @@ RadixPlan radix_plan(int64_t n_seg, int segments, int begin_bit, int end_bit) {
   const int64_t block_items = (int64_t)kThreads * L.rounds;
   L.nblk = (int)((n_seg + block_items - 1) / block_items);
   L.ghist_words = (int64_t)4 * segments * 256;
-  L.status_words = (int64_t)(L.passes > 0 ? L.passes : 1) * segments * L.nblk * 256;
+  // the passes' statuses, then per-chunk digit totals of each pass (the
+  // two-pass tile-pair sort's block-count scan)
+  const int64_t pw = L.passes > 0 ? L.passes : 1;
+  L.status_words = pw * segments * L.nblk * 256 +
+                   pw * ((L.nblk + kScanChunk - 1) / kScanChunk) * 256;
   L.ticket_words = 8;  // four pass tickets, the give-up status word, padding
   const int64_t n = n_seg * (int64_t)segments;
   const size_t vec = align_up((size_t)n * sizeof(uint32_t), 256);
@@ -643,6 +789,14 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
 // one sort block, whose second pass then walks them one after another.
 constexpr int64_t kPairRangesMinPairs = int64_t(1) << 23;
 
+uint32_t* radix_pair_zero_span(const RadixPlan& L, const RadixCtl& C,
+                               int64_t* words) {
+  // the second pass's statuses, then the first pass's chunk totals
+  const int64_t nchunks = (L.nblk + kScanChunk - 1) / kScanChunk;
+  if (words) *words = (int64_t)L.nblk * 256 + nchunks * 256;
+  return C.status + (int64_t)L.nblk * 256;
+}
+
 bool radix_pair_ranges_ok(const RadixPlan& L, int64_t num_values) {
   return L.segments == 1 && L.passes == 2 && L.begin_bit == 0 &&
          L.end_bit > 8 && L.end_bit <= 16 && num_values <= (int64_t(1) << 24) &&
@@ -671,8 +825,22 @@ int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
              L.nblk, 1, 24, L.end_bit - 8, C.ghist + 256,
              C.status + status_per_pass, C.tickets + 1, C.err,
              C.ghist, tile_offsets, num_tiles};
-  constexpr int kA = kValsIn | kKeyBytes, kB = kPairRanges;
+  // The first pass takes its block prefixes from a count and a scan of the
+  // key bytes (1 B/pair read); the second looks back (its counts would cost
+  // a read of the 4-byte words, more than its look-back does).
+  constexpr int kA = kValsIn | kKeyBytes | kPreCounts;
+  constexpr int kB = kPairRanges;
+  uint32_t* chunk_a = C.status + 2 * (int64_t)L.nblk * 256;
+  const dim3 chunks((unsigned)((L.nblk + kScanChunk - 1) / kScanChunk));
+  const dim3 grid_lo((unsigned)((L.nblk + counts_sub(true) - 1) / counts_sub(true)));
 #define GS_PAIR_PASSES(R)                                                    \
+  launch_traced("rs_block_counts_kernel(pairs:lo)",                          \
+                (rs_block_counts_kernel<true, R>), grid_lo, dim3(kThreads), 0, \
+                stream, a.keys_in, L.n_seg, n_dev, 0, 255u, a.status,        \
+                chunk_a);                                                    \
+  launch_traced("rs_block_scan_kernel(pairs:lo)", (rs_block_scan_kernel<R>), \
+                chunks, dim3(256 * kScanQ), 0, stream, a.status, chunk_a,     \
+                L.n_seg, n_dev);                                             \
   launch_traced("rs_onesweep_kernel(pairs:lo)", (rs_onesweep_kernel<kA, R>), \
                 grid, dim3(64 * onesweep_waves(R)), 0, stream, a);           \
   launch_traced("rs_onesweep_kernel(pairs:hi)", (rs_onesweep_kernel<kB, R>), \
