@@ -79,6 +79,11 @@ def kernel_work(name, BG, N, walked, T):
         "rs_onesweep_kernel(depth)": ("hbm", 16.0 * BG, "16 B/splat per pass (key + value read and written)"),
         "rs_onesweep_kernel(keys)": ("hbm", 16.0 * N, "16 B/pair per pass (key + value read and written)"),
         "ranges_kernel": ("hbm", 4.0 * N + 4.0 * T, "4 B/pair (sorted keys read) + 4 B/tile (offsets written)"),
+        "rs_block_counts_kernel(pairs:lo)": ("hbm", 1.0 * N + 1024.0 * -(-N // 8192),
+                                             "1 B/pair (low tile bytes read) + 1 KB per 8192-pair block (counts "
+                                             "written)"),
+        "rs_block_scan_kernel(pairs:lo)": ("hbm", 2048.0 * -(-N // 8192),
+                                           "2 KB per 8192-pair block (counts read, prefixes written)"),
         "rs_onesweep_kernel(pairs:lo)": ("hbm", 9.0 * N, "9 B/pair: low tile byte + packed word read, word written"),
         "rs_onesweep_kernel(pairs:hi)": ("hbm", 8.0 * N + 4.0 * T, "8 B/pair: word read, gid written; 4 B/tile"),
         "ranges_finish_kernel": ("hbm", 8.0 * T + 64.0 * BG, "8 B/tile (offsets read) + 64 B/splat (gradient "

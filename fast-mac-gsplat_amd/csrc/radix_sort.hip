@@ -270,68 +270,52 @@ __device__ __forceinline__ void rank_rounds(uint32_t (&kreg)[kR],
 // its workgroups.
 constexpr int kScanChunk = 128;
 constexpr int kScanQ = 4;
-// Blocks counted per workgroup of rs_block_counts_kernel: kSub blocks of
-// bytes (8 KB each) are read together, so that each workgroup has enough
-// loads in flight.
-constexpr int counts_sub(bool bytes) { return bytes ? 4 : 1; }
 
 // Digit counts of every block of 256 kBlockRounds elements of a pass
 // (kPreCounts): status[b][d] = count, and each count added to its chunk's
 // total, chunk_tot[b / kScanChunk][d] (zeroed before).  Keys are bytes
 // (kBytes: the tile-pair sort's low tile bytes) or words (digit = (word >>
-// shift) & dmask).  Workgroup g counts blocks kSub g .. kSub g + kSub - 1;
-// elements past the count are not counted.
+// shift) & dmask).  One workgroup per block (four blocks per workgroup were
+// slower); elements past the count are not counted.
 template <bool kBytes, int kBlockRounds>
 __global__ __launch_bounds__(kThreads) void rs_block_counts_kernel(
     const uint32_t* keys, int64_t n_cap, const int32_t* n_dev, int shift,
     uint32_t dmask, uint32_t* status, uint32_t* chunk_tot) {
-  constexpr int kSub = counts_sub(kBytes);
   constexpr int kItems = kThreads * kBlockRounds;
   constexpr int kLoads = kBytes ? kBlockRounds / 4 : kBlockRounds;
-  __shared__ uint32_t h[kSub][kWaves][256];
+  __shared__ uint32_t h[kWaves][256];
   const int t = threadIdx.x, wave = t >> 6;
   const int64_t n = n_dev ? min(n_cap, (int64_t)max(*n_dev, 0)) : n_cap;
-  const int blk0 = blockIdx.x * kSub;
-  if ((int64_t)blk0 * kItems >= n) return;
+  const int blk = blockIdx.x;
+  if ((int64_t)blk * kItems >= n) return;
   const uint32_t n32 = (uint32_t)n;
   // word j holds elements (kBytes ? 4 : 1) * j onwards
   const uint32_t words_end = kBytes ? (n32 + 3u) / 4u : n32;
   constexpr uint32_t kBlockWords = kBytes ? kItems / 4 : kItems;
-  uint32_t v[kSub][kLoads];
+  uint32_t v[kLoads];
 #pragma unroll
-  for (int sb = 0; sb < kSub; ++sb)
-#pragma unroll
-    for (int r = 0; r < kLoads; ++r)
-      v[sb][r] = at32(keys, min((uint32_t)(blk0 + sb) * kBlockWords +
-                                    (uint32_t)(r * kThreads + t),
-                                words_end - 1u));
-  for (int i = t; i < kSub * kWaves * 256; i += kThreads) (&h[0][0][0])[i] = 0u;
+  for (int r = 0; r < kLoads; ++r)
+    v[r] = at32(keys, min((uint32_t)blk * kBlockWords + (uint32_t)(r * kThreads + t),
+                          words_end - 1u));
+  for (int i = t; i < kWaves * 256; i += kThreads) (&h[0][0])[i] = 0u;
   __syncthreads();
 #pragma unroll
-  for (int sb = 0; sb < kSub; ++sb)
+  for (int r = 0; r < kLoads; ++r) {
+    const uint32_t w = (uint32_t)blk * kBlockWords + (uint32_t)(r * kThreads + t);
+    if (kBytes) {
 #pragma unroll
-    for (int r = 0; r < kLoads; ++r) {
-      const uint32_t w = (uint32_t)(blk0 + sb) * kBlockWords + (uint32_t)(r * kThreads + t);
-      if (kBytes) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          if (w * 4u + k < n32)
-            atomicAdd(&h[sb][wave][(v[sb][r] >> (8 * k)) & 255u], 1u);
-      } else if (w < n32) {
-        atomicAdd(&h[sb][wave][(v[sb][r] >> shift) & dmask], 1u);
-      }
+      for (int k = 0; k < 4; ++k)
+        if (w * 4u + k < n32) atomicAdd(&h[wave][(v[r] >> (8 * k)) & 255u], 1u);
+    } else if (w < n32) {
+      atomicAdd(&h[wave][(v[r] >> shift) & dmask], 1u);
     }
-  __syncthreads();
-#pragma unroll
-  for (int sb = 0; sb < kSub; ++sb) {
-    const int blk = blk0 + sb;
-    if ((int64_t)blk * kItems >= n) break;
-    uint32_t c = 0u;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) c += h[sb][w][t];
-    status[(int64_t)blk * 256 + t] = c;
-    if (c != 0u) atomicAdd(&chunk_tot[(int64_t)(blk / kScanChunk) * 256 + t], c);
   }
+  __syncthreads();
+  uint32_t c = 0u;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) c += h[w][t];
+  status[(int64_t)blk * 256 + t] = c;
+  if (c != 0u) atomicAdd(&chunk_tot[(int64_t)(blk / kScanChunk) * 256 + t], c);
 }
 
 // The counts of rs_block_counts_kernel replaced by their exclusive prefix
@@ -832,10 +816,9 @@ int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
   constexpr int kB = kPairRanges;
   uint32_t* chunk_a = C.status + 2 * (int64_t)L.nblk * 256;
   const dim3 chunks((unsigned)((L.nblk + kScanChunk - 1) / kScanChunk));
-  const dim3 grid_lo((unsigned)((L.nblk + counts_sub(true) - 1) / counts_sub(true)));
 #define GS_PAIR_PASSES(R)                                                    \
   launch_traced("rs_block_counts_kernel(pairs:lo)",                          \
-                (rs_block_counts_kernel<true, R>), grid_lo, dim3(kThreads), 0, \
+                (rs_block_counts_kernel<true, R>), grid, dim3(kThreads), 0,  \
                 stream, a.keys_in, L.n_seg, n_dev, 0, 255u, a.status,        \
                 chunk_a);                                                    \
   launch_traced("rs_block_scan_kernel(pairs:lo)", (rs_block_scan_kernel<R>), \
