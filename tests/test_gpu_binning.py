@@ -45,9 +45,11 @@ def test_exclusive_scan_in_place(gpu):
     (4096, 1, 0, 32, 1 << 32),
     (100_003, 1, 0, 13, 37),          # many duplicates, partial digit
     (700_001, 1, 0, 16, 1 << 16),
-    (2_500_003, 1, 0, 32, 1 << 32),   # 32-bit keys, 16 rounds per workgroup
-    (4_200_001, 1, 0, 16, 1 << 16),   # 32 rounds per workgroup (above 2^22 elements)
-    (3_000_000, 2, 0, 24, 1 << 24),   # segmented, 16 rounds
+    (1_048_576, 1, 0, 32, 1 << 32),   # 4096-element blocks (at 2^20 elements)
+    (1_048_577, 1, 0, 20, 1 << 20),   # 8192-element blocks (above 2^20), a last block of one element
+    (2_500_003, 1, 0, 32, 1 << 32),   # 32-bit keys, 8192-element blocks
+    (4_200_001, 1, 0, 16, 1 << 16),   # 8192-element blocks above 2^22 elements
+    (3_000_000, 2, 0, 24, 1 << 24),   # segmented, 8192-element blocks
     (65536, 4, 0, 32, 1 << 32),       # segmented
     (10_000, 3, 8, 24, 1 << 32),      # bit window
     (1000, 2, 0, 0, 1 << 32),         # zero passes: copy
