@@ -1,13 +1,16 @@
 // lookback.h -- decoupled look-back: a workgroup obtains the exclusive prefix
 // of per-workgroup totals without a separate scan launch.
 //
-// Every workgroup takes a ticket (atomic counter) when it starts, so a
-// workgroup only ever waits for workgroups with smaller tickets, which are
-// already running.  A workgroup publishes its own total (flag AGG) before it
-// looks back, then its inclusive prefix (flag INC).  Payload and flag share
-// one word, so relaxed device-scope atomics suffice.  Predecessor statuses are
-// read several at a time (independent loads) so the walk costs one memory
-// round trip per window rather than per predecessor.  Waits are bounded:
+// Workgroups are ordered by a ticket (atomic counter) taken when they start,
+// so that a workgroup only ever waits for workgroups with smaller tickets,
+// which are already running (the scans), or by their index (radix_sort.hip,
+// where the dispatch order gives the same property and the ticket's round
+// trip was measured to cost more).  A workgroup publishes its own total
+// (flag AGG) before it looks back, then its inclusive prefix (flag INC).
+// Payload and flag share one word, so relaxed device-scope atomics suffice.
+// Predecessor statuses are read several at a time (independent loads) so the
+// walk costs one memory round trip per window rather than per predecessor.
+// Waits are bounded:
 // after spin_limit polls (kMaxSpins unless a caller passes less) the wait
 // gives up, ORs GSPLAT_STATUS_LOOKBACK_TIMEOUT into the caller's status word
 // and returns the partial prefix.  Every wave therefore terminates, and the

@@ -102,7 +102,6 @@ struct PassArgs {
   int digit_bits;
   const uint32_t* ghist;     // [segments][256] global digit counts of this pass
   uint32_t* status;          // [segments][nblk][256], zeroed
-  uint32_t* ticket;          // zeroed
   uint32_t* err;             // look-back give-up status word
   // The tile-pair sort in two passes (kPackHi, then kPairRanges; one
   // segment): the first pass's global digit counts, and the tile ranges the
@@ -401,10 +400,17 @@ void rs_onesweep_kernel(PassArgs a) {
   uint32_t* const hist = gdelta;    // digits before P[lo] (kPairRanges)
   uint8_t* const dig8 = reinterpret_cast<uint8_t*>(sk);
 
-  // (kPreCounts: no look-back, so no order among workgroups is needed, and
-  // the ticket's atomic on one word would delay every workgroup's loads:
-  // first pair pass 365 -> 330 us at 1.2e8 pairs)
-  const int vb = (kMode & kPreCounts) ? (int)blockIdx.x : take_ticket(a.ticket);
+  // Block = workgroup index.  A workgroup looks back only at blocks of
+  // smaller index, and workgroups are dispatched to the XCDs round-robin by
+  // index and, within an XCD, in index order: a block that has not started
+  // shares its XCD only with running blocks of smaller index, which do not
+  // wait for it, so it starts once one of them ends.  (The bounded waits of
+  // the look-back report a give-up instead of hanging should that order
+  // ever not hold.)  An atomic ticket per workgroup, the usual way to get an
+  // order that holds by construction, delays every workgroup's loads by its
+  // round trip: pair passes at 1.2e8 pairs 365 -> 330 and 503 -> 479 us
+  // without it.
+  const int vb = (int)blockIdx.x;
   const int seg = vb / a.nblk;
   const int blk = vb - seg * a.nblk;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -739,7 +745,7 @@ int radix_passes(const RadixPlan& L, const RadixCtl& C, void* buffers,
     PassArgs a{cur_k, cur_v, cur_depth, out_k, out_v, L.n_seg, n_dev, L.nblk,
                L.segments, shift, bits,
                C.ghist + (int64_t)p * L.segments * 256,
-               C.status + p * status_per_pass, C.tickets + p, C.err};
+               C.status + p * status_per_pass, C.err};
     const int mode = (cur_depth ? kDepthKeys : 0) | (cur_v ? kValsIn : 0) |
                      (out_k ? kKeysOut : 0);
     const dim3 grid((unsigned)(L.nblk * (int64_t)L.segments));
@@ -808,10 +814,10 @@ int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
   const dim3 grid((unsigned)L.nblk);
   PassArgs a{reinterpret_cast<const uint32_t*>(key_bytes), words_in, nullptr,
              nullptr, words, L.n_seg, n_dev, L.nblk, 1, 0, 8, C.ghist,
-             C.status, C.tickets, C.err, nullptr, nullptr, 0};
+             C.status, C.err, nullptr, nullptr, 0};
   PassArgs b{words, nullptr, nullptr, nullptr, vals_out, L.n_seg, n_dev,
              L.nblk, 1, 24, L.end_bit - 8, C.ghist + 256,
-             C.status + status_per_pass, C.tickets + 1, C.err,
+             C.status + status_per_pass, C.err,
              C.ghist, tile_offsets, num_tiles};
   // The first pass takes its block prefixes from a count and a scan of the
   // key bytes (1 B/pair read); the second looks back (its counts would cost
