@@ -410,7 +410,12 @@ __device__ __forceinline__ void pack_record(
 // in original order, its count in the slot (pack_kernel then copies one
 // 64-byte record per splat instead of gathering five attribute arrays).
 // The blocks also zero zero_words[0..n_zero_words) (grid-stride; read only
-// by later launches).
+// by later launches).  With lds_hist (2 x 257 words of LDS) the block also
+// counts its hits' tile digits ((tile >> hist_shift) & 255) and writes them
+// to hist_row[0..255]: the pair sort's histogram, in partials that a later
+// launch sums (it counts every hit, the emit only those below its capacity:
+// the two differ only when the capacity is short, and then the binning is
+// redone).
 template <int kW>
 __device__ __forceinline__ void count_block(
     const RasterParams& P, const float* __restrict__ means2d,
@@ -418,11 +423,16 @@ __device__ __forceinline__ void count_block(
     const float* __restrict__ colors, float4* __restrict__ rec_orig,
     int32_t* __restrict__ splat_count, int32_t* __restrict__ block_sums,
     uint32_t* __restrict__ zero_words, int64_t n_zero_words, int vb, int nvb,
-    CountLds<kW>& S) {
+    CountLds<kW>& S, uint32_t* lds_hist = nullptr,
+    uint32_t* __restrict__ hist_row = nullptr, int hist_shift = 0) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int64_t i = (int64_t)vb * (64 * kW) + threadIdx.x; i < n_zero_words;
        i += (int64_t)nvb * (64 * kW))
     zero_words[i] = 0u;
+  if (lds_hist != nullptr) {
+    for (int i = threadIdx.x; i < 2 * 257; i += 64 * kW) lds_hist[i] = 0u;
+    __syncthreads();
+  }
   const int orig = (vb * kW + wave) * kWalkSplats + lane;
   const bool valid = lane < kWalkSplats && orig < P.num_splats;
   const int o = valid ? orig : P.num_splats - 1;
@@ -442,11 +452,34 @@ __device__ __forceinline__ void count_block(
   // previous lane's.
   const int my_end = lane < kWalkSplats ? W.cend[lane] : 0;
   int run = 0, hits_to_end = 0;
-  walk_candidates(P, W, total, [&](uint64_t hm, bool, int, int, int c0) {
+  walk_candidates(P, W, total, [&](uint64_t hm, bool hit, int, int tile,
+                                   int c0) {
     const int rel = my_end - c0;
     if (rel > 0 && rel <= 64) hits_to_end = run + hits_below(hm, rel);
     run += __popcll(hm);
+    if (lds_hist != nullptr && hit)
+      atomicAdd(&lds_hist[(lane & 1) * 257 + (((uint32_t)tile >> hist_shift) & 255u)], 1u);
   });
+  if (lds_hist != nullptr) {
+    // the certain hits: each row of the splat's inner rectangle, cut where
+    // the digit changes
+    if (lane < kWalkSplats && n_inner > 0) {
+      const int4 in = W.inner[lane];
+      const int4 bx = W.box[lane];
+      for (int r = 0; r < in.w; ++r) {
+        uint32_t t0 = (uint32_t)(bx.w + (bx.y + in.y + r) * P.tiles_x + bx.x + in.x);
+        const uint32_t t1 = t0 + (uint32_t)in.z;
+        while (t0 < t1) {
+          const uint32_t seg = min(t1, ((t0 >> hist_shift) + 1u) << hist_shift);
+          atomicAdd(&lds_hist[(lane & 1) * 257 + ((t0 >> hist_shift) & 255u)], seg - t0);
+          t0 = seg;
+        }
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < 256)
+      hist_row[threadIdx.x] = lds_hist[threadIdx.x] + lds_hist[257 + threadIdx.x];
+  }
   const int prev_end = __shfl_up(hits_to_end, 1, 64);
   const int n =
       valid ? hits_to_end - (lane == 0 ? 0 : prev_end) + n_inner : 0;
@@ -496,18 +529,20 @@ __global__ __launch_bounds__(run_step::kRunThreads) void count_depth_runs_kernel
     const float* __restrict__ conics, const float* __restrict__ opacities,
     int32_t* __restrict__ splat_count, uint32_t* __restrict__ zero_words,
     int64_t n_zero_words, const float* __restrict__ depths, int runs,
-    int run_blocks, run_step::RunBuffers runs_out) {
+    int run_blocks, run_step::RunBuffers runs_out, CountHist H) {
   __shared__ CountRunsLds S;
+  __shared__ uint32_t hist[2 * 257];
   if ((int)blockIdx.x < run_blocks) {
     run_step::run_sort_block(depths, P.gpb, runs, (int)blockIdx.x, runs_out,
                              S.runs);
     return;
   }
+  const int vb = (int)blockIdx.x - run_blocks;
   count_block<run_step::kRunWaves>(
       P, means2d, conics, opacities, nullptr, nullptr, splat_count, nullptr,
-      zero_words,
-      n_zero_words, (int)blockIdx.x - run_blocks,
-      (int)gridDim.x - run_blocks, S.count);
+      zero_words, n_zero_words, vb, (int)gridDim.x - run_blocks, S.count,
+      H.parts != nullptr ? hist : nullptr,
+      H.parts != nullptr ? H.parts + (int64_t)vb * 256 : nullptr, H.shift);
 }
 
 // One workgroup: *pair_count = sum of the n block sums (-1 if it does not fit
@@ -552,11 +587,30 @@ __global__ __launch_bounds__(run_step::kRankBlock) void rank_pack_kernel(
     const float* __restrict__ opacities, run_step::RunBuffers runs_in,
     int runs, const int32_t* __restrict__ splat_count,
     int32_t* __restrict__ perm, float4* __restrict__ packed,
-    int32_t* __restrict__ gid_count, uint32_t* __restrict__ block_totals) {
+    int32_t* __restrict__ gid_count, uint32_t* __restrict__ block_totals,
+    CountHist H) {
   __shared__ run_step::RankLds S;
   __shared__ uint32_t agg[kAggBlocks];
   __shared__ int agg_first;
   const int t = threadIdx.x;
+  if (H.parts != nullptr && blockIdx.x == gridDim.x - 1) {
+    // the extra workgroup: the pair sort's histogram from the count blocks'
+    // partials (kRankSplit thread groups per digit, then their sums in LDS)
+    constexpr int kGroups = run_step::kRankBlock / 256;
+    uint32_t* red = reinterpret_cast<uint32_t*>(&S);
+    const int d = t & 255, g = t >> 8;
+    uint32_t v = 0u;
+    for (int r = g; r < H.nparts; r += kGroups) v += H.parts[(int64_t)r * 256 + d];
+    red[g * 256 + d] = v;
+    __syncthreads();
+    if (t < 256) {
+      uint32_t sum = 0u;
+#pragma unroll
+      for (int k = 0; k < kGroups; ++k) sum += red[k * 256 + t];
+      H.ghist[t] = sum;
+    }
+    return;
+  }
   if (t < kAggBlocks) agg[t] = 0u;  // (rank_block synchronises before use)
   int my_gid = -1, my_n = 0;
   run_step::rank_block(
@@ -1250,25 +1304,30 @@ int launch_count(const RasterParams& P, const float* means2d,
   return check_launch("sum_kernel");
 }
 
+int count_depth_runs_blocks(const RasterParams& P) {
+  constexpr int kSplatsPerBlock = run_step::kRunWaves * kWalkSplats;
+  return (P.num_splats + kSplatsPerBlock - 1) / kSplatsPerBlock;
+}
+
 int launch_count_depth_runs(const RasterParams& P, const float* means2d,
                             const float* conics, const float* opacities,
                             int32_t* splat_count, uint32_t* zero_words,
                             int64_t n_zero_words, const float* depths,
-                            void* depth_buffers, hipStream_t stream) {
+                            void* depth_buffers, hipStream_t stream,
+                            const CountHist& H) {
   if (P.num_splats == 0 || !depth_small_ok(P.gpb)) {
     set_error("count + depth runs: needs 1..131072 splats per image");
     return GSPLAT_ERR_INVALID_ARGUMENT;
   }
   const int runs = run_step::runs_of(P.gpb);
   const int run_blocks = P.batch * runs;
-  constexpr int kSplatsPerBlock = run_step::kRunWaves * kWalkSplats;
-  const int cblocks = (P.num_splats + kSplatsPerBlock - 1) / kSplatsPerBlock;
+  const int cblocks = count_depth_runs_blocks(P);
   launch_traced("count_depth_runs_kernel", count_depth_runs_kernel,
                 dim3((unsigned)(run_blocks + cblocks)),
                 dim3(run_step::kRunThreads), 0, stream, P, means2d, conics,
                 opacities, splat_count, zero_words, n_zero_words, depths, runs,
                 run_blocks,
-                run_step::run_buffers(depth_buffers, P.gpb, P.batch));
+                run_step::run_buffers(depth_buffers, P.gpb, P.batch), H);
   return check_launch("count_depth_runs_kernel");
 }
 
@@ -1277,7 +1336,7 @@ int launch_rank_pack(const RasterParams& P, const float* means2d,
                      const float* opacities, void* depth_buffers,
                      const int32_t* splat_count, int32_t* perm, float* packed,
                      int32_t* gid_count, uint32_t* block_totals,
-                     hipStream_t stream) {
+                     hipStream_t stream, const CountHist& H) {
   if (P.num_splats == 0 || !depth_small_ok(P.gpb)) {
     set_error("rank + pack: needs 1..131072 splats per image");
     return GSPLAT_ERR_INVALID_ARGUMENT;
@@ -1285,12 +1344,13 @@ int launch_rank_pack(const RasterParams& P, const float* means2d,
   const int blocks_per_seg =
       (P.gpb + run_step::kRankElems - 1) / run_step::kRankElems;
   launch_traced("rank_pack_kernel", rank_pack_kernel,
-                dim3((unsigned)((int64_t)P.batch * blocks_per_seg)),
+                dim3((unsigned)((int64_t)P.batch * blocks_per_seg +
+                                (H.parts != nullptr ? 1 : 0))),
                 dim3(run_step::kRankBlock), 0, stream, P, means2d, conics,
                 colors, opacities,
                 run_step::run_buffers(depth_buffers, P.gpb, P.batch),
                 run_step::runs_of(P.gpb), splat_count, perm,
-                reinterpret_cast<float4*>(packed), gid_count, block_totals);
+                reinterpret_cast<float4*>(packed), gid_count, block_totals, H);
   return check_launch("rank_pack_kernel");
 }
 

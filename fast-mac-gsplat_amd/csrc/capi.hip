@@ -469,6 +469,23 @@ namespace {
 // bin_emit; with long_flag (a device word that is zero before the call) the
 // tile range launch sets it to 1 if a tile range is longer than
 // kHandoffPairs.
+// The low tile bits of the one-pass-and-bucket form of the pair sort for
+// buffers of n_pairs pairs (images of 2^9..2^16 tiles with at most
+// kBucketChunk pairs per bucket on average), or -1 for the other forms.
+int bucket_low_bits(const RasterParams& P, int64_t n_pairs) {
+  const int tile_bits = bits_for((int64_t)P.num_tiles - 1);
+  const int low_bits = tile_bits - 8;
+  const int64_t buckets =
+      low_bits > 0 ? (((int64_t)P.num_tiles + (1 << low_bits) - 1) >> low_bits)
+                   : 0;
+  return (low_bits >= 1 && tile_bits <= 16 &&
+          n_pairs <= buckets * (int64_t)gs::kBucketChunk)
+             ? low_bits
+             : -1;
+}
+
+// hist_counted: the bucket form's histogram is already in the control block
+// (counted by the count launch, summed by the rank launch).
 int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
                   const int32_t* splat_offsets, int64_t n_pairs,
                   int32_t* binned_ids, int32_t* tile_counts,
@@ -476,7 +493,8 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
                   void* count_workspace, size_t count_workspace_bytes,
                   void* workspace, size_t workspace_bytes, void* stream,
                   int32_t* long_flag, const gs::ZeroSpan* zero = nullptr,
-                  const gs::EmitScanArgs* scan = nullptr) {
+                  const gs::EmitScanArgs* scan = nullptr,
+                  bool hist_counted = false) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -534,16 +552,13 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
   // most 256 buckets), then a counting sort per bucket that also writes the
   // tile ranges.
   const int tile_bits = bits_for((int64_t)P.num_tiles - 1);
-  const int low_bits = tile_bits - 8;
-  const int64_t buckets =
-      low_bits > 0 ? (((int64_t)P.num_tiles + (1 << low_bits) - 1) >> low_bits)
-                   : 0;
-  if (low_bits >= 1 && tile_bits <= 16 &&
-      n_pairs <= buckets * (int64_t)gs::kBucketChunk) {
+  const int low_bits = bucket_low_bits(P, n_pairs);
+  if (low_bits >= 1) {
     const gs::RadixPlan high = gs::radix_plan(n_pairs, 1, low_bits, tile_bits);
     uint32_t* high_vals =
         reinterpret_cast<uint32_t*>(base + L.buffers + L.pairs.a_vals);
-    rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals, 1,
+    rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals,
+                         hist_counted ? 0 : 1,
                          reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
                          ctl.status, L.pairs.status_words, s, scan, low_bits);
     if (!rc)
@@ -730,12 +745,25 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
     const CountLayout C = count_layout(P);
     char* cb = static_cast<char*>(cws);
     const size_t z0 = gs::radix_ctl_bytes(C.depth);
+    // The bucket form's histogram is counted by the count blocks, which
+    // finish well before the depth run step they share the launch with, and
+    // summed by an extra rank workgroup; the emit's workgroups would
+    // otherwise add it atomically, all at their end (cfg2: ~5 us of emit).
+    gs::CountHist hist;
+    const int low_bits = bucket_low_bits(P, capacity);
+    if (low_bits >= 1) {
+      hist.parts = reinterpret_cast<uint32_t*>(static_cast<char*>(ews) +
+                                               emit_layout(P, capacity).hist);
+      hist.shift = low_bits;
+      hist.nparts = gs::count_depth_runs_blocks(P);
+      hist.ghist = reinterpret_cast<uint32_t*>(cb + C.pair_ghist);
+    }
     rc = gs::launch_count_depth_runs(
         P, means2d, conics, opacities,
         reinterpret_cast<int32_t*>(cb + C.splat_count),
         reinterpret_cast<uint32_t*>(cb + z0),
         (int64_t)((C.ctl_end - z0) / sizeof(uint32_t)), depths,
-        cb + C.depth_buffers, s);
+        cb + C.depth_buffers, s, hist);
     // ranks with the records packed at them, then the emit scans the pair
     // offsets itself
     int32_t* gid_count = reinterpret_cast<int32_t*>(cb + C.gid_count);
@@ -746,12 +774,12 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
       rc = gs::launch_rank_pack(
           P, means2d, conics, colors, opacities, cb + C.depth_buffers,
           reinterpret_cast<const int32_t*>(cb + C.splat_count), perm, packed,
-          gid_count, block_totals, s);
+          gid_count, block_totals, s, hist);
     const gs::EmitScanArgs scan{gid_count, splat_offsets, block_totals};
     if (!rc)
       rc = bin_emit_impl(meta, packed, splat_offsets, capacity, binned_ids,
                          nullptr, tile_offsets, status_dev, cws, cbytes, ews,
-                         ebytes, s, long_dev, zero, &scan);
+                         ebytes, s, long_dev, zero, &scan, low_bits >= 1);
     // N is written by the emit's scan
     return rc ? rc : report(splat_offsets + P.num_splats);
   }

@@ -156,11 +156,24 @@ int launch_count(const RasterParams& P, const float* means2d,
 // sums and no N) and the first launch of the small-image depth order (runs
 // into depth_buffers) as one launch.  Requires P.num_splats > 0 and
 // depth_small_ok(P.gpb); launch_depth_ranks_small completes the order.
+// The pair sort's one-pass histogram counted by the count blocks of
+// launch_count_depth_runs (digit (tile >> shift) & 255 of every hit, one
+// row of 256 partial counts per count block in parts) and summed into
+// ghist[0..255] by an extra workgroup of launch_rank_pack; parts null: not
+// counted there.
+struct CountHist {
+  uint32_t* parts = nullptr;
+  int shift = 0;
+  int nparts = 0;
+  uint32_t* ghist = nullptr;
+};
+int count_depth_runs_blocks(const RasterParams& P);
 int launch_count_depth_runs(const RasterParams& P, const float* means2d,
                             const float* conics, const float* opacities,
                             int32_t* splat_count, uint32_t* zero_words,
                             int64_t n_zero_words, const float* depths,
-                            void* depth_buffers, hipStream_t stream);
+                            void* depth_buffers, hipStream_t stream,
+                            const CountHist& H = CountHist{});
 // pack: packed records in gid order and splat_offsets[0..BG] (exclusive scan
 // of splat_count[perm]) via a look-back scan whose status
 // (count_scan_blocks(P) words) and ticket must be zero.
@@ -245,7 +258,7 @@ int launch_rank_pack(const RasterParams& P, const float* means2d,
                      const float* opacities, void* depth_buffers,
                      const int32_t* splat_count, int32_t* perm, float* packed,
                      int32_t* gid_count, uint32_t* block_totals,
-                     hipStream_t stream);
+                     hipStream_t stream, const CountHist& H = CountHist{});
 // Tile ranges longer than this many pairs are walked by the forward's first
 // launch only up to here and continued by its second (render_fwd_long).
 constexpr int kHandoffPairs = GSPLAT_HANDOFF_PAIRS;
