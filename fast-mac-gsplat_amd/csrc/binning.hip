@@ -599,8 +599,17 @@ __global__ __launch_bounds__(run_step::kRankBlock) void rank_pack_kernel(
     constexpr int kGroups = run_step::kRankBlock / 256;
     uint32_t* red = reinterpret_cast<uint32_t*>(&S);
     const int d = t & 255, g = t >> 8;
+    // (eight independent loads in flight per thread)
+    uint32_t acc[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    int r = g;
+    for (; r + 7 * kGroups < H.nparts; r += 8 * kGroups) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[u] += H.parts[(int64_t)(r + u * kGroups) * 256 + d];
+    }
+    for (; r < H.nparts; r += kGroups) acc[0] += H.parts[(int64_t)r * 256 + d];
     uint32_t v = 0u;
-    for (int r = g; r < H.nparts; r += kGroups) v += H.parts[(int64_t)r * 256 + d];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v += acc[u];
     red[g * 256 + d] = v;
     __syncthreads();
     if (t < 256) {
