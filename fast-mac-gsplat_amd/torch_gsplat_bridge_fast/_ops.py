@@ -417,6 +417,22 @@ def _bin_fast(meta: _lib.RasterMeta, means2d: Tensor, conics: Tensor, colors: Te
                     d.ring, (slot, 1), ready, d, d.calls - 1, (slot, 2))
 
 
+_fast_ws_bytes: dict = {}
+
+
+def _fast_workspace_bytes(L, meta: _lib.RasterMeta, cap: int, key: tuple, save_state: bool) -> tuple:
+    """(binning, render) workspace bytes of the one-call path for a shape key and capacity."""
+    k = (key, cap, save_state)
+    v = _fast_ws_bytes.get(k)
+    if v is None:
+        v = (L.gsplat_hip_bin_workspace_bytes(meta, cap),
+             L.gsplat_hip_render_workspace_bytes(meta, cap if save_state else 0))
+        if len(_fast_ws_bytes) > 256:
+            _fast_ws_bytes.clear()
+        _fast_ws_bytes[k] = v
+    return v
+
+
 def _bin_render_fast(meta: _lib.RasterMeta, flat, cap: int, key: tuple, save_state: bool):
     """Binning with buffers of the known capacity and the forward in one C-ABI call
     (gsplat_hip_bin_render_forward).  Returns (BinState, render_forward outputs, render workspace);
@@ -435,7 +451,7 @@ def _bin_render_fast(meta: _lib.RasterMeta, flat, cap: int, key: tuple, save_sta
     splat_offsets = _empty(BG + 1, torch.int32, dev)
     tile_offsets = _empty(tiles + 1, torch.int32, dev)
     pairs = _empty(cap, torch.int32, dev)
-    ws_bytes = L.gsplat_hip_bin_workspace_bytes(meta, cap)
+    ws_bytes, rws_bytes = _fast_workspace_bytes(L, meta, cap, key, save_state)
     ws = _empty(max(ws_bytes, 1), torch.uint8, dev)
     img = torch.empty((B, H, W, 3), dtype=torch.float32, device=dev)
     final_T = last = tile_stop = None
@@ -443,7 +459,6 @@ def _bin_render_fast(meta: _lib.RasterMeta, flat, cap: int, key: tuple, save_sta
         final_T = torch.empty((B, H, W), dtype=torch.float32, device=dev)
         last = torch.empty((B, H, W), dtype=torch.int32, device=dev)
         tile_stop = _empty(tiles, torch.int32, dev)
-    rws_bytes = L.gsplat_hip_render_workspace_bytes(meta, cap if save_state else 0)
     rws = _empty(max(rws_bytes, 1), torch.uint8, dev)
     slot = d.slot()
     check(L.gsplat_hip_bin_render_forward(

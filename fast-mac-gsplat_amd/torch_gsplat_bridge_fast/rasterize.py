@@ -112,8 +112,28 @@ _EPS = 1e-8
 _MAX_ALPHA = 0.99
 
 
+_validated: dict = {}
+
+
 def _runtime_validate(config: RasterConfig) -> RuntimeShaderConfig:
-    """Same checks and messages as v8 rasterize.py:85-107."""
+    """Same checks and messages as v8 rasterize.py:85-107.  A config that passed once with the same
+    environment is not checked again (RasterConfig is frozen)."""
+    env = (os.environ.get("GSP_TILE_SIZE"), os.environ.get("GSP_CHUNK"), os.environ.get("GSP_FAST_CAP"))
+    key = (config, env)
+    try:
+        rt = _validated.get(key)
+    except TypeError:   # a field that is not hashable (e.g. a list background): no cache
+        return _runtime_validate_uncached(config)
+    if rt is not None:
+        return rt
+    rt = _runtime_validate_uncached(config)
+    if len(_validated) > 256:
+        _validated.clear()
+    _validated[key] = rt
+    return rt
+
+
+def _runtime_validate_uncached(config: RasterConfig) -> RuntimeShaderConfig:
     rt = get_runtime_shader_config()
     if config.tile_size != rt.tile_size:
         raise ValueError(
@@ -164,10 +184,25 @@ def _resolve_active_tile_use(policy: str, active_fraction: float, overflow_tiles
     return active_fraction < 0.10 or overflow_tiles > 0 or max_pairs > 2 * max_fast_pairs
 
 
+_metas: dict = {}
+
+
 def _meta(config: RasterConfig, batch_size: int, gaussians_per_batch: int) -> _lib.RasterMeta:
-    return _lib.make_raster_meta(
-        config.height, config.width, batch_size, gaussians_per_batch, config.alpha_threshold,
-        config.transmittance_threshold, config.background, _EPS, _MAX_ALPHA)
+    """The C-ABI meta struct, built once per (config, B, G): it is only read by the calls."""
+    key = (config, batch_size, gaussians_per_batch)
+    try:
+        m = _metas.get(key)
+    except TypeError:   # a field that is not hashable (e.g. a list background): no cache
+        key, m = None, None
+    if m is None:
+        m = _lib.make_raster_meta(
+            config.height, config.width, batch_size, gaussians_per_batch, config.alpha_threshold,
+            config.transmittance_threshold, config.background, _EPS, _MAX_ALPHA)
+        if key is not None:
+            if len(_metas) > 256:
+                _metas.clear()
+            _metas[key] = m
+    return m
 
 
 def _normalize_inputs(means2d, conics, colors, opacities, depths):
@@ -302,7 +337,6 @@ def _rasterize_chunk_eval(means2d_b, conics_b, colors_b, opacities_b, depths_b, 
     return out[0]
 
 
-@torch.no_grad()
 def _choose_batch_slices(means2d_b, conics_b, colors_b, opacities_b, depths_b, config: RasterConfig, *,
                          train_mode: bool, tiles_per_image: int) -> List[Tuple[int, int]]:
     """Batch slices per launch (reference _choose_batch_slices, v8 rasterize.py:339-391): contiguous
@@ -314,6 +348,14 @@ def _choose_batch_slices(means2d_b, conics_b, colors_b, opacities_b, depths_b, c
     base = [(b0, min(B, b0 + chunk_b)) for b0 in range(0, B, chunk_b)]
     if not train_mode or config.batch_strategy != "auto" or config.max_pairs_per_launch <= 0 or B <= 1:
         return base
+    return _split_by_pair_budget(means2d_b, conics_b, colors_b, opacities_b, depths_b, config, base,
+                                 tiles_per_image)
+
+
+@torch.no_grad()
+def _split_by_pair_budget(means2d_b, conics_b, colors_b, opacities_b, depths_b, config: RasterConfig,
+                          base: List[Tuple[int, int]], tiles_per_image: int) -> List[Tuple[int, int]]:
+    G = means2d_b.shape[1]
     budget = int(config.max_pairs_per_launch)
     out: List[Tuple[int, int]] = []
     for b0, b1 in base:
