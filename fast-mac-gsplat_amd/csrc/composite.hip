@@ -96,6 +96,19 @@ __device__ __forceinline__ int slot_y(const TileCoord& c, int k) {
   return c.y0 + 4 * k + c.ly;
 }
 
+// This lane's index (workgroups of one wavefront), recomputed where it is
+// used instead of kept in a register across the walk: the forward's
+// register budget spills whatever long-lived value it cannot hold, and each
+// wave's spill store and reload went through the caches to HBM (~45 MB more
+// writes per launch at 4096^2).
+__device__ __forceinline__ int lane_now() {
+  int v;
+  asm volatile(
+      "v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0"
+      : "=v"(v));
+  return v;
+}
+
 // s2 first: the forward reads only its x and z (one ds_read2 whose 8-bit
 // dword offsets reach it from the batch's base address without an add).
 struct Staged {
@@ -551,9 +564,12 @@ void render_fwd_kernel(
     last_segment<kPix>(P, tc, out_rgb, H, -1, valid, cr, cg, cb, T,
                        (int)threadIdx.x);
   int tile_max = 0;
-  // The lane's pixels are 4 rows apart: one 64-bit index, then increments.
+  // The lane's pixels are 4 rows apart: one 64-bit index, then increments
+  // (the lane's column and row from a fresh lane index).
+  const int lane_end = lane_now();
   const int64_t pix0 = opaque64(
-      ((int64_t)tc.batch * P.height + slot_y(tc, 0)) * P.width + x);
+      ((int64_t)tc.batch * P.height + tc.y0 + (lane_end >> 4)) * P.width +
+      tc.x0 + (lane_end & 15));
   const int64_t strip = (int64_t)4 * P.width;
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
