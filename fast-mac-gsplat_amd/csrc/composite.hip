@@ -801,11 +801,12 @@ struct BwdShared {
 
 // Where the backward adds its gradients (in original splat order): one
 // accumulator record of kAccFloats floats per splat, or, without one, the
-// four output arrays.  A record holds a splat's nine gradient entries in one
-// 64-byte line, {g_mean x, y, g_conic a, b, c, g_colour r, g, b, g_opacity},
-// so the nine atomics a tile adds for a splat touch one cache line instead
-// of four or five; render_grads_unpack_kernel copies the records to the
-// output arrays.
+// four output arrays.  A record holds a splat's nine gradient sums in one
+// 64-byte line, {V_mx, V_my, V_ca, V_cb, V_cc, colour r, g, b, g_opacity}
+// (the walk's sums before their scales), so the nine atomics a tile adds
+// for a splat touch one cache line instead of four or five, at a uniform
+// address plus the lane's entry; render_grads_unpack_kernel scales them
+// into the output arrays.
 struct GradOut {
   float* g_means2d;
   float* g_conics;
@@ -814,7 +815,7 @@ struct GradOut {
   float* acc;  // [num_splats][kAccFloats] or null
 };
 
-// Where group q = lane / 8 sends its total: q = 0..7 is
+// Without records, where group q = lane / 8 sends its total: q = 0..7 is
 // {V_mx, V_my, V_ca, V_cb, V_cc, colour r, g, b} (see the backward walk),
 // added at base + orig * stride bytes after scaling.
 struct GradTarget {
@@ -823,17 +824,12 @@ struct GradTarget {
   float scale;
 };
 
+// g_mean = -(2/L) V_m since a = -2A/L, b = -B/L, c = -2C/L;
+// g_conic = (-V_ca/2, -V_cb, -V_cc/2).
+constexpr float kMeanScale = -2.0f / kLog2e;
+
 __device__ __forceinline__ GradTarget grad_target(const GradOut& G) {
-  // g_mean = -(2/L) V_m since a = -2A/L, b = -B/L, c = -2C/L;
-  // g_conic = (-V_ca/2, -V_cb, -V_cc/2).
-  constexpr float kMeanScale = -2.0f / kLog2e;
-  const int q = threadIdx.x >> 3;
-  if (G.acc != nullptr) {
-    const float scale =
-        q < 2 ? kMeanScale : q == 3 ? -1.0f : q < 5 ? -0.5f : 1.0f;
-    return {G.acc + q, 4 * kAccFloats, scale};
-  }
-  switch (q) {
+  switch (threadIdx.x >> 3) {
     case 0: return {G.g_means2d + 0, 8, kMeanScale};
     case 1: return {G.g_means2d + 1, 8, kMeanScale};
     case 2: return {G.g_conics + 0, 12, -0.5f};
@@ -845,9 +841,8 @@ __device__ __forceinline__ GradTarget grad_target(const GradOut& G) {
   }
 }
 
-// Where the opacity gradient goes (scale 1).
+// Where the opacity gradient goes without records (scale 1).
 __device__ __forceinline__ GradTarget opac_target(const GradOut& G) {
-  if (G.acc != nullptr) return {G.acc + 8, 4 * kAccFloats, 1.0f};
   return {G.g_opac, 4, 1.0f};
 }
 
@@ -914,11 +909,13 @@ __device__ __forceinline__ bool needs_last_test(const RasterParams& P,
 // adding its parts of the splat's gradients to the lane's sums, which are
 // reduced across the wavefront and added atomically in original order.
 // kPlain: every record has kPlainBit, so e <= 0 and the max_alpha gate are
-// not tested (they always pass).
-template <bool kCheckLast, bool kPlain>
+// not tested (they always pass).  kAcc: the totals go to the records at acc,
+// else to target and opac.
+template <bool kCheckLast, bool kPlain, bool kAcc>
 __device__ __forceinline__ void bwd_batch(
     BwdShared& SH, uint32_t bmask, int n, int cstart, float max_alpha,
-    const GradTarget& target, const GradTarget& opac, BwdPixels& Q) {
+    float* acc, const GradTarget& target, const GradTarget& opac,
+    BwdPixels& Q) {
   const Staged& S = SH.S;
   const int lane = threadIdx.x;
   const bool group_head = (lane & 7) == 0;
@@ -944,16 +941,23 @@ __device__ __forceinline__ void bwd_batch(
     const float4 a1 = S.s1[j];
     const float dx = Q.px - a0.x;
     const XTerms xt = x_terms(a0.z, a0.w, dx, a1.y);
-    bool contrib = false;
+    // lanes with a contribution, from the comparisons' own lane masks
+    // (uniform; a ballot of the combined test would be materialised per lane)
+    uint64_t hits = 0;
 #pragma unroll
     for (int k = 0; k < kPix; ++k) {
       if (!((mask >> k) & 1u)) continue;  // scalar branch
       // one combined test: composited in the forward (i < last) and visible
       const float dy = Q.py[k] - a0.y;
       const Exponents E = exponents(xt, a1.x, dy);
-      if (((!kCheckLast) | (i < Q.lk[k])) &
-          (kPlain || power_nonpositive(E, xt, dy)) & (E.p >= a2.z)) {
-        contrib = true;
+      const bool c_last = (!kCheckLast) | (i < Q.lk[k]);
+      const bool c_e = kPlain || power_nonpositive(E, xt, dy);
+      const bool c_p = E.p >= a2.z;
+      uint64_t hk = __builtin_amdgcn_ballot_w64(c_p);
+      if (kCheckLast) hk &= __builtin_amdgcn_ballot_w64(c_last);
+      if (!kPlain) hk &= __builtin_amdgcn_ballot_w64(c_e);
+      hits |= hk;
+      if (c_last & c_e & c_p) {
         const float raw = __builtin_amdgcn_exp2f(E.p);
         const bool open = kPlain || raw < max_alpha;  // gradient gate
         const float alpha = open ? raw : max_alpha;
@@ -976,7 +980,7 @@ __device__ __forceinline__ void bwd_batch(
         Q.Tc[k] = T_prev;
       }
     }
-    if (__builtin_amdgcn_ballot_w64(contrib) != 0) {
+    if (hits != 0) {
       // Per-lane parts of the splat's gradients (a, b, c = -2A/L, -B/L,
       // -2C/L): g_mean = -(2/L) (V_mx, V_my), g_conic = (-V_ca/2, -V_cb,
       // -V_cc/2) with V_cc = S2, and g_opacity = sum g_raw exp(power) =
@@ -1001,16 +1005,22 @@ __device__ __forceinline__ void bwd_batch(
       const float tot = group8_sum_dpp(((u.x + u.y) + (u.z + u.w)) +
                                        ((w.x + w.y) + (w.z + w.w)));
       const uint32_t orig = uniform_bits(a2.y);
-      if (group_head)
-        unsafeAtomicAdd(reinterpret_cast<float*>(
-                            reinterpret_cast<char*>(target.base) +
-                            (uint64_t)orig * target.stride),
-                        tot * target.scale);
-      if (lane == kLanes - 1)  // a2.w = 1 / opacity
-        unsafeAtomicAdd(reinterpret_cast<float*>(
-                            reinterpret_cast<char*>(opac.base) +
-                            (uint64_t)orig * opac.stride),
-                        r3 * a2.w);
+      if (kAcc) {
+        float* rec = acc + (size_t)orig * kAccFloats;  // uniform
+        if (group_head) unsafeAtomicAdd(rec + q, tot);
+        if (lane == kLanes - 1) unsafeAtomicAdd(rec + 8, r3 * a2.w);
+      } else {
+        if (group_head)
+          unsafeAtomicAdd(reinterpret_cast<float*>(
+                              reinterpret_cast<char*>(target.base) +
+                              (uint64_t)orig * target.stride),
+                          tot * target.scale);
+        if (lane == kLanes - 1)  // a2.w = 1 / opacity
+          unsafeAtomicAdd(reinterpret_cast<float*>(
+                              reinterpret_cast<char*>(opac.base) +
+                              (uint64_t)orig * opac.stride),
+                          r3 * a2.w);
+      }
       wave_lds_sync();  // loads done before the next splat's stores
     }
   }
@@ -1018,13 +1028,13 @@ __device__ __forceinline__ void bwd_batch(
 
 // Reverse walk over the tile-range indices [lo, hi), one staged batch of 64
 // records at a time.
-template <bool kCheckLast>
+template <bool kCheckLast, bool kAcc>
 __device__ __forceinline__ void bwd_walk(
     const RasterParams& P, const float4* __restrict__ packed,
     const int32_t* __restrict__ binned, int start, int lo, int hi,
     const TileCoord& tc, BwdShared& SH, BwdPixels& Q, const GradOut& G) {
-  const GradTarget target = grad_target(G);
-  const GradTarget opac = opac_target(G);
+  const GradTarget target = kAcc ? GradTarget{} : grad_target(G);
+  const GradTarget opac = kAcc ? GradTarget{} : opac_target(G);
   const float max_alpha = fminf(P.max_alpha, 1.0f);
   for (int cend = hi; cend > lo; cend -= kBatch) {
     const int cstart = max(lo, cend - kBatch);
@@ -1035,16 +1045,17 @@ __device__ __forceinline__ void bwd_walk(
                            (uint32_t)P.num_splats - 1u, SH.S);
     __syncthreads();
     if (batch_plain(bmask))
-      bwd_batch<kCheckLast, true>(SH, bmask, n, cstart, max_alpha, target,
-                                  opac, Q);
+      bwd_batch<kCheckLast, true, kAcc>(SH, bmask, n, cstart, max_alpha,
+                                        G.acc, target, opac, Q);
     else
-      bwd_batch<kCheckLast, false>(SH, bmask, n, cstart, max_alpha, target,
-                                   opac, Q);
+      bwd_batch<kCheckLast, false, kAcc>(SH, bmask, n, cstart, max_alpha,
+                                         G.acc, target, opac, Q);
   }
 }
 
 // Copies the backward's accumulator records (GradOut) to the four gradient
-// arrays and zeroes them: one thread per splat.
+// arrays with their scales (as grad_target's) and zeroes them: one thread
+// per splat.
 __global__ __launch_bounds__(256) void render_grads_unpack_kernel(GradOut G,
                                                                   int n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -1056,11 +1067,11 @@ __global__ __launch_bounds__(256) void render_grads_unpack_kernel(GradOut G,
   rec[0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   rec[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   G.acc[i * kAccFloats + 8] = 0.0f;
-  G.g_means2d[2 * i + 0] = a.x;
-  G.g_means2d[2 * i + 1] = a.y;
-  G.g_conics[3 * i + 0] = a.z;
-  G.g_conics[3 * i + 1] = a.w;
-  G.g_conics[3 * i + 2] = b.x;
+  G.g_means2d[2 * i + 0] = kMeanScale * a.x;
+  G.g_means2d[2 * i + 1] = kMeanScale * a.y;
+  G.g_conics[3 * i + 0] = -0.5f * a.z;
+  G.g_conics[3 * i + 1] = -a.w;
+  G.g_conics[3 * i + 2] = -0.5f * b.x;
   G.g_colors[3 * i + 0] = b.y;
   G.g_colors[3 * i + 1] = b.z;
   G.g_colors[3 * i + 2] = b.w;
@@ -1101,8 +1112,9 @@ __device__ __forceinline__ bool seg_item(const RasterParams& P,
 // many pairs, whose walk's LDS round trips and atomics need the extra
 // wavefronts more than the few spilled set-up values cost, and 7 (72 VGPRs,
 // more values spilled) for tiles of few pairs, whose time goes to the
-// per-tile set-up and the loads of the pixel state.
-template <int kWaves>
+// per-tile set-up and the loads of the pixel state.  kAcc: G has the
+// gradient records (the workspace path).
+template <int kWaves, bool kAcc>
 __global__ __launch_bounds__(kLanes)
 __attribute__((amdgpu_waves_per_eu(kWaves, 8))) void render_bwd_kernel(
     RasterParams P, const float4* __restrict__ packed,
@@ -1167,11 +1179,11 @@ __attribute__((amdgpu_waves_per_eu(kWaves, 8))) void render_bwd_kernel(
     // Q.Tc holds T_final, or T at the segment's end for pixels alive past it
     // (T_end > T_final > threshold), so the test sees the final state.
     if (needs_last_test(P, tc, Q))
-      bwd_walk<true>(P, packed, binned, tile_offsets[tile], lo, hi, tc, SH, Q,
-                     G);
+      bwd_walk<true, kAcc>(P, packed, binned, tile_offsets[tile], lo, hi, tc,
+                           SH, Q, G);
     else
-      bwd_walk<false>(P, packed, binned, tile_offsets[tile], lo, hi, tc, SH, Q,
-                      G);
+      bwd_walk<false, kAcc>(P, packed, binned, tile_offsets[tile], lo, hi, tc,
+                            SH, Q, G);
   }
 }
 
@@ -1350,7 +1362,9 @@ int launch_render_backward(const RasterParams& P, const float* packed,
   // tile on average the short-tile variant is faster)
   const bool short_tiles = n_pairs <= (int64_t)64 * P.num_tiles;
   launch_timed("render_bwd_kernel",
-               short_tiles ? render_bwd_kernel<7> : render_bwd_kernel<6>,
+               G.acc == nullptr ? render_bwd_kernel<6, false>
+               : short_tiles    ? render_bwd_kernel<7, true>
+                                : render_bwd_kernel<6, true>,
                dim3((unsigned)(seg_blocks + P.num_tiles)), dim3(kLanes),
                stream, t0, t1, P, pk, tile_offsets, binned_ids, final_T, last,
                tile_stop, grad_rgb, G, H, seg_blocks);
