@@ -958,7 +958,8 @@ int gsplat_hip_bin_render_forward(
   rc = gs::launch_render_forward(P, packed, tile_offsets, binned_ids, out_rgb,
                                  out_final_T, out_last, out_tile_stop,
                                  capacity, render_workspace, s,
-                                 gs::kForwardPreZeroed | gs::kForwardNoLong,
+                                 gs::kForwardPreZeroed | gs::kForwardNoLong |
+                                     gs::kForwardStoppedLast,
                                  &report);
   if (!rc && status_event != nullptr)
     rc = hip_status(hipEventRecord(static_cast<hipEvent_t>(status_event), s),

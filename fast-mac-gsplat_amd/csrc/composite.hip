@@ -458,16 +458,20 @@ __device__ __forceinline__ void fwd_batch(const Staged& S, uint32_t bmask,
   }
 }
 
-// Eight wavefronts per SIMD (at most 64 VGPRs, a few values spilled): the
-// walk is bound by the latency of each wavefront's loads and LDS round
-// trips, so more resident wavefronts shorten it (7% at 1860 pairs per tile).
+// Eight wavefronts per SIMD (at most 64 VGPRs): the walk is bound by the
+// latency of each wavefront's loads and LDS round trips, so more resident
+// wavefronts shorten it (7% at 1860 pairs per tile).  all_last: out_last
+// for every tile, else only for the tiles where a pixel stopped
+// (T <= threshold; the others composited their whole tile range, and the
+// backward reads last only where a pixel stopped).
 __global__ __launch_bounds__(kLanes) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void render_fwd_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ tile_offsets,
     const int32_t* __restrict__ binned, float* __restrict__ out_rgb,
     float* __restrict__ out_T, int32_t* __restrict__ out_last,
-    int32_t* __restrict__ out_tile_stop, HeavyState H, HostReport R) {
+    int32_t* __restrict__ out_tile_stop, HeavyState H, HostReport R,
+    bool all_last) {
   __shared__ Staged S;
   // The binning's report reaches the host as the forward starts.
   if (R.host != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
@@ -571,6 +575,12 @@ void render_fwd_kernel(
       ((int64_t)tc.batch * P.height + tc.y0 + (lane_end >> 4)) * P.width +
       tc.x0 + (lane_end & 15));
   const int64_t strip = (int64_t)4 * P.width;
+  // the whole tile's last or none of it (whole 64-byte rows: lines that the
+  // neighbouring tile also writes are written back whole)
+  bool stop = false;
+#pragma unroll
+  for (int k = 0; k < kPix; ++k) stop |= valid[k] && !(T[k] > t_thr);
+  const bool put_last = all_last || __builtin_amdgcn_ballot_w64(stop) != 0;
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
     if (valid[k]) {
@@ -585,7 +595,7 @@ void render_fwd_kernel(
       out_rgb[3 * pix + 2] = cb[k] + T[k] * P.bg_b;
       if (out_T) {
         out_T[pix] = T[k];
-        out_last[pix] = last[k];
+        if (put_last) out_last[pix] = last[k];
       }
       tile_max = max(tile_max, last[k]);
     }
@@ -854,7 +864,11 @@ struct BwdPixels {
 };
 
 // Loads grad and saved state; T and gT start at final_T and the background
-// term.  Pixels outside the image get lk = 0 (never processed).
+// term.  Pixels outside the image get lk = 0 (never processed).  last is
+// read only for the pixels that stopped (T <= threshold), and only by the
+// wavefronts that have one: a pixel above the threshold composited its whole
+// tile range (lk = 2^31 - 1), and the one-call forward stores last only for
+// the pixels that stopped.
 __device__ __forceinline__ void load_bwd_pixels(
     const RasterParams& P, const TileCoord& tc,
     const float* __restrict__ final_T, const int32_t* __restrict__ last_in,
@@ -865,6 +879,7 @@ __device__ __forceinline__ void load_bwd_pixels(
   const int64_t pix0 = opaque64(
       ((int64_t)tc.batch * P.height + slot_y(tc, 0)) * P.width + x);
   const int64_t strip = (int64_t)4 * P.width;
+  bool stopped[kPix];
 #pragma unroll
   for (int k = 0; k < kPix; ++k) {
     const int y = slot_y(tc, k);
@@ -877,13 +892,22 @@ __device__ __forceinline__ void load_bwd_pixels(
       Q.gg[k] = __builtin_nontemporal_load(grad_rgb + 3 * pix + 1);
       Q.gb[k] = __builtin_nontemporal_load(grad_rgb + 3 * pix + 2);
       Q.Tc[k] = __builtin_nontemporal_load(final_T + pix);
-      Q.lk[k] = __builtin_nontemporal_load(last_in + pix);
     } else {
       Q.gr[k] = Q.gg[k] = Q.gb[k] = 0.0f;
       Q.Tc[k] = 1.0f;
-      Q.lk[k] = 0;
     }
     Q.gT[k] = Q.gr[k] * P.bg_r + Q.gg[k] * P.bg_g + Q.gb[k] * P.bg_b;
+    stopped[k] = valid && !(Q.Tc[k] > P.trans_thr);
+    Q.lk[k] = valid ? 0x7fffffff : 0;
+  }
+  bool any = false;
+#pragma unroll
+  for (int k = 0; k < kPix; ++k) any |= stopped[k];
+  if (__builtin_amdgcn_ballot_w64(any) != 0) {
+#pragma unroll
+    for (int k = 0; k < kPix; ++k)
+      if (stopped[k])
+        Q.lk[k] = __builtin_nontemporal_load(last_in + pix0 + k * strip);
   }
 }
 
@@ -1307,7 +1331,8 @@ int launch_render_forward(const RasterParams& P, const float* packed,
   launch_timed("render_fwd_kernel", render_fwd_kernel, dim3((unsigned)P.num_tiles), dim3(kLanes),
                stream, t0, more ? nullptr : t1, P, pk, tile_offsets,
                binned_ids, out_rgb, out_T, out_last, out_tile_stop, H,
-               report != nullptr ? *report : HostReport{});
+               report != nullptr ? *report : HostReport{},
+               !(flags & kForwardStoppedLast));
   const int rc = check_launch("render_fwd_kernel");
   if (rc || !more) return rc;
   return launch_render_forward_long(P, packed, tile_offsets, binned_ids,

@@ -359,9 +359,14 @@ size_t render_workspace_bytes(const RasterParams& P, int64_t n_pairs);
 // Forward launches.  flags: kForwardPreZeroed (the words of
 // render_forward_zero_spans are already zero), kForwardNoLong (the tiles
 // handed off are left for launch_render_forward_long, which the caller
-// issues unless no tile range is longer than kHandoffPairs).
+// issues unless no tile range is longer than kHandoffPairs),
+// kForwardStoppedLast (the one-wavefront kernel stores out_last only for
+// the tiles where a pixel stopped, final T <= transmittance threshold: the
+// backward reads last only for such pixels, and the other tiles' stores
+// were most of 67 MB per launch at 4096x4096).
 constexpr int kForwardPreZeroed = 1;
 constexpr int kForwardNoLong = 2;
+constexpr int kForwardStoppedLast = 4;
 // report (may be null): the binning's host report, written by the forward's
 // first workgroup as it starts (or by launch_host_report if the forward has
 // no workgroup).

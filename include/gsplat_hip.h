@@ -341,9 +341,13 @@ int gsplat_hip_render_forward_long(const gsplat_raster_meta* meta,
  * by the forward's first workgroup as it starts, so the host can poll
  * host_words[3] and read the words while the forward runs; status_event
  * (may be NULL) is recorded after the forward.  With N above capacity
- * (see gsplat_hip_bin) the image is that of the incomplete binning.  It has
- * no counterpart in the reference (which binds bin and render as two ops):
- * it is the one-call form of both for the per-step path. */
+ * (see gsplat_hip_bin) the image is that of the incomplete binning.
+ * out_last is written only for the tiles where a pixel stopped
+ * (out_final_T <= transmittance_threshold); the other entries are left as
+ * they were, since gsplat_hip_render_backward reads last only where the
+ * pixel stopped.  It
+ * has no counterpart in the reference (which binds bin and render as two
+ * ops): it is the one-call form of both for the per-step path. */
 int gsplat_hip_bin_render_forward(
     const gsplat_raster_meta* meta, const float* means2d, const float* conics,
     const float* colors, const float* opacities, const float* depths,
@@ -360,6 +364,8 @@ int gsplat_hip_bin_render_forward(
  * 478-608) and the unsort of v8 rasterize.py:676-680: gradients are written
  * in the ORIGINAL splat order using the orig_index stored in each packed
  * record; the four gradient arrays are written in full by this call.
+ * last is read only for pixels with final_T <= transmittance_threshold
+ * (a pixel above it composited its whole tile range).
  * workspace: the forward's (or NULL). */
 int gsplat_hip_render_backward(const gsplat_raster_meta* meta,
                                const float* packed,

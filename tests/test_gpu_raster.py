@@ -644,8 +644,9 @@ def test_one_call_bin_and_forward(gpu, kind):
     and continues long tiles (gsplat_hip_render_forward_long) only when the binning reports a
     tile range longer than HANDOFF_PAIRS.  Checked: the flag against the tile counts (a range of
     exactly 128 pairs is not long, 129 is), binning, image and state bit-identical to the
-    separate calls of the first binning of the shape, the eval forward's image, and image and
-    gradients of the one-call forward's state against the tile oracle."""
+    separate calls of the first binning of the shape (last where the pixel stopped: the one-call
+    forward stores it only in such tiles), the eval forward's image, and image and gradients of the
+    one-call forward's state, its other last entries zeroed, against the tile oracle."""
     from torch_gsplat_bridge_fast import _lib, _ops
 
     if kind == "config1_small":
@@ -679,15 +680,21 @@ def test_one_call_bin_and_forward(gpu, kind):
     for a, b in [(st0.perm, st1.perm), (st0.packed, st1.packed), (st0.tile_offsets, st1.tile_offsets),
                  (st0.splat_offsets, st1.splat_offsets), (st0.pairs[:n], st1.pairs[:n])]:
         assert torch.equal(a, b)
-    for a, b in zip(out0[:4], out1[:4]):
-        assert torch.equal(a, b)
+    for i in (0, 1, 3):  # image, final_T, tile stops
+        assert torch.equal(out0[i], out1[i])
+    # the one-call forward stores last only in the tiles where a pixel stopped (T <= threshold)
+    T = out1[1]
+    stopped = ~(T > meta.transmittance_threshold)
+    assert torch.equal(out0[2][stopped], out1[2][stopped])
     assert torch.equal(out2[0], out0[0])
     w = torch.rand(B, H, W, 3, generator=torch.Generator().manual_seed(3))
-    img, T, last, stop, ws = out1
+    img, _, last, stop, ws = out1
+    # the backward must not read the other entries: zero them (a read would skip every splat there)
+    last = torch.where(stopped, last, torch.zeros_like(last))
     grads = _ops.render_backward(meta, st1, T, last, stop, w.to(gpu), ws)
     torch.cuda.synchronize()
     oracle_parity(sc, H, W, B, G, (0.0, 0.0, 0.0), w.numpy(), img.cpu().numpy(),
-                  [g.cpu().numpy() for g in grads], f"one call {kind}", gpu_last=last.cpu().numpy())
+                  [g.cpu().numpy() for g in grads], f"one call {kind}", gpu_last=out0[2].cpu().numpy())
 
 
 def test_launch_trace_sees_every_kernel_of_a_step(gpu):
