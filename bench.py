@@ -68,12 +68,17 @@ def kernel_work(name, BG, N, walked, T):
         "emit_kernel<false>": ("hbm", 28.0 * BG + (5.0 if N >= 1 << 23 else 8.0) * N,
                                "28 B/splat (record 24, offset 4) + 8 B/pair (key, value), or 5 B/pair (packed word "
                                "+ low tile byte) for the two-pass sort of 2^23+ pairs"),
-        "count_kernel": ("hbm", 104.0 * BG, "104 B/splat (one-call path): means 8, conic 12, opacity 4, colours 12 "
-                                            "read, count 4 and the 64-B record written"),
+        "emit_kernel<orig>": ("hbm", 44.0 * BG + (5.0 if N >= 1 << 23 else 8.0) * N + N / 8.0,
+                              "44 B/splat (the count's record 36, offset + gid 8) + 5 or 8 B/pair as "
+                              "emit_kernel<false> + the count's hit ballots (1 bit per candidate, at least one "
+                              "per pair)"),
+        "count_kernel": ("hbm", 104.0 * BG + N / 8.0, "104 B/splat (one-call path): means 8, conic 12, opacity 4, "
+                                                      "colours 12 read, count 4 and the 64-B record written; "
+                                                      "+ the hit ballots (1 bit per candidate, at least one per pair)"),
         "depth_run_sort_kernel": ("hbm", 12.0 * BG, "12 B/splat: depth 4 read, run key + value 8 written"),
         "depth_run_rank_kernel": ("hbm", 12.0 * BG, "12 B/splat: run key + value 8 read, perm 4 written"),
-        "pack_kernel": ("hbm", 136.0 * BG, "136 B/splat: perm 4 and the count's 64-B record read; record 64, "
-                                           "offset 4 written (one-call path)"),
+        "pack_kernel": ("hbm", 144.0 * BG, "144 B/splat: perm 4 and the count's 64-B record read; record 64, "
+                                           "offset 4 and the original-order offset + gid 8 written (one-call path)"),
         "rs_global_hist_kernel(depth)": ("hbm", 4.0 * BG, "4 B/splat (depth keys read)"),
         "rs_global_hist_kernel(keys)": ("hbm", 4.0 * N, "4 B/pair (keys read)"),
         "rs_onesweep_kernel(depth)": ("hbm", 16.0 * BG, "16 B/splat per pass (key + value read and written)"),

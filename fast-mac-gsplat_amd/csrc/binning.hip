@@ -127,6 +127,14 @@ __device__ __forceinline__ int div_small(int k, int w) {
   return q;
 }
 
+// A 64-bit value of lane l (l uniform).
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi =
+      (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 // Index of this thread's splat in the walk order of count / emit: lanes
 // 0..kWalkSplats-1 of each wavefront take consecutive splats.
 __device__ __forceinline__ int walk_splat_index() {
@@ -261,16 +269,32 @@ __device__ __forceinline__ int walk_setup(const RasterParams& P, bool valid,
 // position are counted with one running total and a lane-masked popcount,
 // without per-splat counters (whose atomics would serialise the lanes of one
 // splat on one LDS address).
+//
+// rec (may be null): the wavefront's recorded ballots (kHitSlab words, step
+// k's ballot at rec[k], as count_block records them for the same splats):
+// the steps they cover take their hits from there instead of the exact
+// test, and steps without a hit are skipped (on_step is not called).
 template <typename Fn>
 __device__ __forceinline__ void walk_candidates(const RasterParams& P,
                                                 WalkSlots& W, int total,
+                                                const uint64_t* __restrict__ rec,
                                                 Fn&& on_step) {
 #pragma clang fp contract(off)
+  static_assert(kHitSlab % 64 == 0, "a slab is loaded 64 words at a time");
   const int lane = threadIdx.x & 63;
   const int first = lane < kWalkSplats ? W.first[lane] : 0x7fffffff;
   // (without certain hits in the wavefront every box is walked whole)
   const bool any_inner = W.ni_incl[kWalkSplats - 1] != 0;
+  uint64_t chunk = 0ull;  // lane l: the recorded ballot of step 64 (k / 64) + l
   for (int c0 = 0; c0 < total; c0 += 64) {
+    const int step = c0 >> 6;
+    const bool recorded = rec != nullptr && step < kHitSlab;
+    uint64_t hm = 0ull;
+    if (recorded) {
+      if ((step & 63) == 0) chunk = rec[step + lane];  // < kHitSlab
+      hm = readlane64(chunk, step & 63);
+      if (hm == 0ull) continue;  // no hit among these candidates
+    }
     const int owner0 = __popcll(__ballot(first <= c0)) - 1;  // first[0] = 0
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -310,20 +334,25 @@ __device__ __forceinline__ void walk_candidates(const RasterParams& P,
         tx = bx.x + (k - q * bx.z);
         ty = bx.y + q;
       }
-      const float4 g0 = W.g0[sl], g1 = W.g1[sl];
-      const int fl = W.flags[sl];
-      ConicSlopes ks;
-      ks.kc = g1.z;
-      ks.ka = g1.w;
-      ks.use_c = (fl & 1) != 0;
-      ks.use_a = (fl & 2) != 0;
-      float rx0, ry0, rx1, ry1;
-      tile_rect(tx, ty, P.width, P.height, rx0, ry0, rx1, ry1);
-      hit = ellipse_hits_rect(g0.x, g0.y, g0.z, g0.w, g1.x, ks, g1.y, rx0, ry0,
-                              rx1, ry1);
+      if (recorded) {
+        hit = ((hm >> lane) & 1ull) != 0ull;
+      } else {
+        const float4 g0 = W.g0[sl], g1 = W.g1[sl];
+        const int fl = W.flags[sl];
+        ConicSlopes ks;
+        ks.kc = g1.z;
+        ks.ka = g1.w;
+        ks.use_c = (fl & 1) != 0;
+        ks.use_a = (fl & 2) != 0;
+        float rx0, ry0, rx1, ry1;
+        tile_rect(tx, ty, P.width, P.height, rx0, ry0, rx1, ry1);
+        hit = ellipse_hits_rect(g0.x, g0.y, g0.z, g0.w, g1.x, ks, g1.y, rx0,
+                                ry0, rx1, ry1);
+      }
       tile = bx.w + ty * P.tiles_x + tx;
     }
-    on_step(__ballot(hit), hit, sl, tile, c0);
+    if (!recorded) hm = __ballot(hit);
+    on_step(hm, hit, sl, tile, c0);
   }
 }
 
@@ -415,7 +444,9 @@ __device__ __forceinline__ void pack_record(
 // to hist_row[0..255]: the pair sort's histogram, in partials that a later
 // launch sums (it counts every hit, the emit only those below its capacity:
 // the two differ only when the capacity is short, and then the binning is
-// redone).
+// redone).  With hit_bits the block records each wavefront's first kHitSlab
+// step ballots at hit_bits[w * kHitSlab + step] (w = vb * kW + wavefront:
+// the splats' index / kWalkSplats), for an emit that walks the same splats.
 template <int kW>
 __device__ __forceinline__ void count_block(
     const RasterParams& P, const float* __restrict__ means2d,
@@ -424,7 +455,8 @@ __device__ __forceinline__ void count_block(
     int32_t* __restrict__ splat_count, int32_t* __restrict__ block_sums,
     uint32_t* __restrict__ zero_words, int64_t n_zero_words, int vb, int nvb,
     CountLds<kW>& S, uint32_t* lds_hist = nullptr,
-    uint32_t* __restrict__ hist_row = nullptr, int hist_shift = 0) {
+    uint32_t* __restrict__ hist_row = nullptr, int hist_shift = 0,
+    uint64_t* __restrict__ hit_bits = nullptr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int64_t i = (int64_t)vb * (64 * kW) + threadIdx.x; i < n_zero_words;
        i += (int64_t)nvb * (64 * kW))
@@ -452,11 +484,18 @@ __device__ __forceinline__ void count_block(
   // previous lane's.
   const int my_end = lane < kWalkSplats ? W.cend[lane] : 0;
   int run = 0, hits_to_end = 0;
-  walk_candidates(P, W, total, [&](uint64_t hm, bool hit, int, int tile,
-                                   int c0) {
+  // the recorded ballots, one store by the first lane per step (holding
+  // them in the lanes until 64 are stored together costs the walk more)
+  uint64_t* const rec =
+      hit_bits != nullptr ? hit_bits + (int64_t)(vb * kW + wave) * kHitSlab
+                          : nullptr;
+  walk_candidates(P, W, total, nullptr, [&](uint64_t hm, bool hit, int,
+                                            int tile, int c0) {
     const int rel = my_end - c0;
     if (rel > 0 && rel <= 64) hits_to_end = run + hits_below(hm, rel);
     run += __popcll(hm);
+    if (rec != nullptr && lane == 0 && (c0 >> 6) < kHitSlab)
+      rec[c0 >> 6] = hm;
     if (lds_hist != nullptr && hit)
       atomicAdd(&lds_hist[(lane & 1) * 257 + (((uint32_t)tile >> hist_shift) & 255u)], 1u);
   });
@@ -508,11 +547,13 @@ __global__ __launch_bounds__(kThreads) void count_kernel(
     const float* __restrict__ conics, const float* __restrict__ opacities,
     const float* __restrict__ colors, float4* __restrict__ rec_orig,
     int32_t* __restrict__ splat_count, int32_t* __restrict__ block_sums,
-    uint32_t* __restrict__ zero_words, int64_t n_zero_words) {
+    uint32_t* __restrict__ zero_words, int64_t n_zero_words,
+    uint64_t* __restrict__ hit_bits) {
   __shared__ CountLds<kWaves> S;
   count_block<kWaves>(P, means2d, conics, opacities, colors, rec_orig,
                       splat_count, block_sums, zero_words, n_zero_words,
-                      (int)blockIdx.x, (int)gridDim.x, S);
+                      (int)blockIdx.x, (int)gridDim.x, S, nullptr, nullptr, 0,
+                      hit_bits);
 }
 
 // The count next to the run step of the small-image depth order, in one
@@ -655,7 +696,8 @@ __global__ __launch_bounds__(run_step::kRankBlock) void rank_pack_kernel(
 // orig = perm[gid] into the packed 64-byte record and turns the per-gid
 // tile-hit counts into exclusive offsets splat_offsets in the same launch
 // (workgroup scan + decoupled look-back).  splat_offsets[num_splats] = N, or
-// -1 when N does not fit in int32 (the offsets are then unusable).
+// -1 when N does not fit in int32 (the offsets are then unusable).  With
+// orig_slot also orig_slot[orig] = {offset, gid} (the original-order emit's).
 __global__ __launch_bounds__(kThreads) void pack_kernel(
     RasterParams P, const float* __restrict__ means2d,
     const float* __restrict__ conics, const float* __restrict__ colors,
@@ -663,17 +705,17 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
     const int32_t* __restrict__ splat_count,
     const float4* __restrict__ rec_orig, float4* __restrict__ packed,
     int32_t* __restrict__ splat_offsets, uint64_t* scan_status,
-    uint32_t* scan_ticket, uint32_t* err) {
+    uint32_t* scan_ticket, uint32_t* err, int2* __restrict__ orig_slot) {
   __shared__ int wsum[kThreads / 64];
   __shared__ long long s_prefix;
   const int vb = take_ticket(scan_ticket);
   const int gid = vb * kThreads + threadIdx.x;
-  int n = 0;
+  int n = 0, orig = 0;
   if (gid < P.num_splats) {
     const int batch = gid / P.gpb;
     // (perm is in [0, G) unless a look-back of the depth sort gave up; the
     // clamp keeps the gathers in bounds then, and the status reports it)
-    const int orig = batch * P.gpb + (int)min(perm[gid], (uint32_t)(P.gpb - 1));
+    orig = batch * P.gpb + (int)min(perm[gid], (uint32_t)(P.gpb - 1));
     if (rec_orig != nullptr) {  // the count's record: orig replaces the count
       Record r;
 #pragma unroll
@@ -718,7 +760,10 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
   }
   __syncthreads();
   const long long end = s_prefix + pre + inc;
-  if (gid < P.num_splats) splat_offsets[gid] = (int)(end - n);
+  if (gid < P.num_splats) {
+    splat_offsets[gid] = (int)(end - n);
+    if (orig_slot != nullptr) orig_slot[orig] = make_int2((int)(end - n), gid);
+  }
   if (gid == P.num_splats - 1)
     splat_offsets[P.num_splats] = end > 0x7fffffffLL ? -1 : (int)end;
 }
@@ -734,6 +779,15 @@ __global__ __launch_bounds__(kThreads) void pack_records_kernel(
   if (gid < P.num_splats)
     pack_record(P, means2d, conics, colors, opacities, packed, gid, gid);
 }
+
+// emit_kernel<false, true>: the walk in original order over the count's
+// records, with the count's recorded step ballots.
+struct EmitOrig {
+  const float4* rec;       // the count's original-order records (hit count
+                           // in the slot)
+  const int2* slot;        // per orig: {pair offset, gid} (pack_kernel)
+  const uint64_t* bits;    // the count's step ballots (count_block), or null
+};
 
 // emit_kernel<true>: the pair offsets are scanned by the emit itself.
 struct EmitScan {
@@ -769,8 +823,13 @@ __device__ __forceinline__ void put_pair(uint32_t* __restrict__ keys,
 // no look-back, no order among workgroups), and writes splat_offsets before
 // walking (the offsets, not N, bound the positions then: every pair lies
 // below N by construction).  Otherwise splat_offsets (and N in
-// splat_offsets[num_splats]) come from pack_kernel.
-template <bool kScan>
+// splat_offsets[num_splats]) come from pack_kernel.  kOrig (not with kScan):
+// the workgroups walk the splats in original order, the count's walk, from
+// its records (eo.rec) with its recorded ballots (eo.bits): a splat's pairs
+// start at eo.slot[orig].x, its certain hits first, then its walk hits,
+// numbered by the wavefront's walk hits of the splats before it (its count
+// less its certain hits).
+template <bool kScan, bool kOrig>
 __global__ __launch_bounds__(kThreads) void emit_kernel(
     RasterParams P, const float4* __restrict__ packed,
     const int32_t* __restrict__ splat_offsets, int64_t capacity,
@@ -778,9 +837,14 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
     uint8_t* __restrict__ key_bytes, int pair_passes, int hist_shift,
     uint32_t* __restrict__ hist_partials,
     uint32_t* ghist_direct, uint32_t* pair_status, int64_t pair_status_words,
-    EmitScan sc) {
+    EmitScan sc, EmitOrig eo) {
+  static_assert(!(kScan && kOrig), "one source of offsets");
   __shared__ WalkSlots walk[kWaves];
   __shared__ int base[kWaves][kWalkSplats];
+  // kOrig: per splat the first position of its walk hits less the wave's
+  // walk hits before it, and its gid
+  __shared__ int wbase[kOrig ? kWaves : 1][kWalkSplats];
+  __shared__ int wgid[kOrig ? kWaves : 1][kWalkSplats];
   // the pair sort's digit histograms in kHistCopies copies (lane l adds to
   // copy l % kHistCopies; rows 257 words apart, so that one digit's copies
   // lie in different LDS banks): hits of one tile row share the row's
@@ -796,12 +860,14 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
   for (int i = t; i < 4 * kHistCopies * 257; i += kThreads) (&h[0][0][0])[i] = 0u;
   const int vb = (int)blockIdx.x;
   __syncthreads();
-  // (2) pair emission
+  // (2) pair emission (gid: the splat's index in the walk's order, its
+  // original index with kOrig)
   const int gid = (vb * kWaves + wave) * kWalkSplats + lane;
   const bool valid = lane < kWalkSplats && gid < P.num_splats;
   const int g = valid ? gid : P.num_splats - 1;
-  const float4 p0 = packed[kRecordVec4 * (int64_t)g + 0];
-  const float4 p1 = packed[kRecordVec4 * (int64_t)g + 1];
+  const float4* __restrict__ src = kOrig ? eo.rec : packed;
+  const float4 p0 = src[kRecordVec4 * (int64_t)g + 0];
+  const float4 p1 = src[kRecordVec4 * (int64_t)g + 1];
   const SplatGeom s{p0.x, p0.y, p0.z, p0.w, p1.x, p1.y};
   WalkSlots& W = walk[wave];
   int64_t n_eff;
@@ -842,6 +908,27 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
     if (valid && gid == P.num_splats - 1)
       sc.splat_offsets[P.num_splats] = end > 0x7fffffffLL ? -1 : (int)end;
     n_eff = capacity;
+  } else if (kOrig) {
+    const int n =
+        valid ? (int)(__float_as_uint(src[kRecordVec4 * (int64_t)g + 2].y) &
+                      0x7fffffffu)
+              : 0;
+    const int2 sg = valid ? eo.slot[g] : make_int2(0, 0);
+    n_eff = min(capacity, (int64_t)max(splat_offsets[P.num_splats], 0));
+    total = walk_setup(P, valid, s, g / P.gpb, W, n_inner);
+    // walk hits of the wavefront's splats up to this one
+    const int w = n - n_inner;
+    int inc = w;
+#pragma unroll
+    for (int off = 1; off < kWalkSplats; off <<= 1) {
+      const int y = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += y;
+    }
+    if (lane < kWalkSplats) {
+      base[wave][lane] = sg.x;
+      wbase[kOrig ? wave : 0][lane] = sg.x + n_inner - (inc - w);
+      wgid[kOrig ? wave : 0][lane] = sg.y;
+    }
   } else {
     if (lane < kWalkSplats) base[wave][lane] = splat_offsets[g];
     n_eff = min(capacity, (int64_t)max(splat_offsets[P.num_splats], 0));
@@ -856,14 +943,24 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
   // to its own.
   const int64_t wave_base = base[wave][0];
   int64_t run = 0;
-  walk_candidates(P, W, total, [&](uint64_t hm, bool hit, int sl, int tile,
-                                   int) {
+  const uint64_t* const rec =
+      (kOrig && eo.bits != nullptr)
+          ? eo.bits + (int64_t)(vb * kWaves + wave) * kHitSlab
+          : nullptr;
+  walk_candidates(P, W, total, rec, [&](uint64_t hm, bool hit, int sl,
+                                        int tile, int) {
     const int64_t pos =
-        wave_base + run + hits_below(hm, lane) + (hit ? W.ni_incl[sl] : 0);
+        kOrig ? (hit ? (int64_t)wbase[kOrig ? wave : 0][sl] : 0) + run +
+                    hits_below(hm, lane)
+              : wave_base + run + hits_below(hm, lane) +
+                    (hit ? W.ni_incl[sl] : 0);
     run += __popcll(hm);
-    if (hit && pos < n_eff) {  // pos >= 0 whenever n_eff > 0
+    // (pos >= 0 whenever n_eff > 0, unless a look-back of the depth sort
+    // gave up and left the original-order offsets unwritten)
+    if (hit && pos < n_eff && (!kOrig || pos >= 0)) {
       put_pair(keys, vals, key_bytes, pos, (uint32_t)tile,
-               (uint32_t)(gid0 + sl));
+               kOrig ? (uint32_t)wgid[kOrig ? wave : 0][sl]
+                     : (uint32_t)(gid0 + sl));
       for (int p = 0; p < pair_passes; ++p)
         atomicAdd(&h[p][lane % kHistCopies]
                      [((uint32_t)tile >> (hist_shift + 8 * p)) & 255u],
@@ -878,14 +975,15 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(
     const int ni = in.z * in.w;
     const int4 bx = W.box[sl];
     const int64_t off = base[wave][sl];
+    const uint32_t sg = kOrig ? (uint32_t)wgid[kOrig ? wave : 0][sl]
+                              : (uint32_t)(gid0 + sl);
     for (int i = lane; i < ni; i += 64) {
       const int dy = div_small(i, in.z);
       const int tile = bx.w + (bx.y + in.y + dy) * P.tiles_x +
                        (bx.x + in.x + (i - dy * in.z));
       const int64_t pos = off + i;
-      if (pos < n_eff) {
-        put_pair(keys, vals, key_bytes, pos, (uint32_t)tile,
-                 (uint32_t)(gid0 + sl));
+      if (pos < n_eff && (!kOrig || pos >= 0)) {
+        put_pair(keys, vals, key_bytes, pos, (uint32_t)tile, sg);
         for (int p = 0; p < pair_passes; ++p)
           atomicAdd(&h[p][lane % kHistCopies]
                        [((uint32_t)tile >> (hist_shift + 8 * p)) & 255u],
@@ -1295,17 +1393,21 @@ int count_blocks(const RasterParams& P) {
   return (P.num_splats + kWalkBlockSplats - 1) / kWalkBlockSplats;
 }
 
+size_t hit_bits_words(const RasterParams& P) {
+  return (size_t)count_blocks(P) * kWaves * kHitSlab;
+}
+
 int launch_count(const RasterParams& P, const float* means2d,
                  const float* conics, const float* opacities,
                  int32_t* splat_count, int32_t* block_sums,
                  int32_t* pair_count, uint32_t* zero_words,
                  int64_t n_zero_words, hipStream_t stream,
-                 const float* colors, float* rec_orig) {
+                 const float* colors, float* rec_orig, uint64_t* hit_bits) {
   const int nblk = count_blocks(P);
   launch_traced("count_kernel", count_kernel, dim3((unsigned)nblk),
                 dim3(kThreads), 0, stream, P, means2d, conics, opacities,
                 colors, reinterpret_cast<float4*>(rec_orig), splat_count,
-                block_sums, zero_words, n_zero_words);
+                block_sums, zero_words, n_zero_words, hit_bits);
   int rc = check_launch("count_kernel");
   if (rc || pair_count == nullptr) return rc;
   launch_traced("sum_kernel", sum_kernel, dim3(1), dim3(kThreads), 0, stream,
@@ -1369,14 +1471,14 @@ int launch_pack(const RasterParams& P, const float* means2d,
                 const int32_t* splat_count, float* packed,
                 int32_t* splat_offsets, uint64_t* scan_status,
                 uint32_t* scan_ticket, uint32_t* err, hipStream_t stream,
-                const float* rec_orig) {
+                const float* rec_orig, int32_t* orig_slot) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const unsigned grid = (unsigned)((P.num_splats + kThreads - 1) / kThreads);
   launch_traced("pack_kernel", pack_kernel, dim3(grid), dim3(kThreads), 0,
                 stream, P, means2d, conics, colors, opacities, perm,
                 splat_count, reinterpret_cast<const float4*>(rec_orig),
                 reinterpret_cast<float4*>(packed), splat_offsets, scan_status,
-                scan_ticket, err);
+                scan_ticket, err, reinterpret_cast<int2*>(orig_slot));
   return check_launch("pack_kernel");
 }
 
@@ -1406,7 +1508,7 @@ int launch_emit(const RasterParams& P, const float* packed,
                 uint32_t* pair_ghist, uint32_t* pair_status,
                 int64_t pair_status_words, hipStream_t stream,
                 const EmitScanArgs* scan, int hist_shift,
-                uint8_t* key_bytes) {
+                uint8_t* key_bytes, const EmitOrigArgs* orig) {
   if (P.num_splats == 0) return GSPLAT_OK;
   const int nblk = emit_blocks(P);
   // Few workgroups add their histograms atomically (pair_ghist is zeroed
@@ -1415,20 +1517,31 @@ int launch_emit(const RasterParams& P, const float* packed,
   if (scan != nullptr) {
     const EmitScan sc{scan->gid_count, scan->splat_offsets,
                       scan->block_totals};
-    launch_traced("emit_kernel<true>", emit_kernel<true>, dim3((unsigned)nblk),
-                  dim3(kThreads), 0, stream, P,
+    launch_traced("emit_kernel<true>", emit_kernel<true, false>,
+                  dim3((unsigned)nblk), dim3(kThreads), 0, stream, P,
                   reinterpret_cast<const float4*>(packed), nullptr, capacity,
                   keys, vals, key_bytes, pair_passes, hist_shift, hist_partials,
                   direct ? pair_ghist : nullptr, pair_status, pair_status_words,
-                  sc);
-  } else {
-    launch_traced("emit_kernel<false>", emit_kernel<false>,
+                  sc, EmitOrig{});
+  } else if (orig != nullptr) {
+    const EmitOrig eo{reinterpret_cast<const float4*>(orig->rec_orig),
+                      reinterpret_cast<const int2*>(orig->orig_slot),
+                      orig->hit_bits};
+    launch_traced("emit_kernel<orig>", emit_kernel<false, true>,
                   dim3((unsigned)nblk), dim3(kThreads), 0, stream, P,
                   reinterpret_cast<const float4*>(packed), splat_offsets,
                   capacity, keys, vals, key_bytes, pair_passes, hist_shift,
                   hist_partials,
                   direct ? pair_ghist : nullptr, pair_status, pair_status_words,
-                  EmitScan{});
+                  EmitScan{}, eo);
+  } else {
+    launch_traced("emit_kernel<false>", emit_kernel<false, false>,
+                  dim3((unsigned)nblk), dim3(kThreads), 0, stream, P,
+                  reinterpret_cast<const float4*>(packed), splat_offsets,
+                  capacity, keys, vals, key_bytes, pair_passes, hist_shift,
+                  hist_partials,
+                  direct ? pair_ghist : nullptr, pair_status, pair_status_words,
+                  EmitScan{}, EmitOrig{});
   }
   int rc = check_launch("emit_kernel");
   if (rc || pair_passes == 0 || direct) return rc;

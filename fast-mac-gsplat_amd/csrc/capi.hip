@@ -173,7 +173,8 @@ int null_check(std::initializer_list<const void*> ptrs, const char* what) {
 struct CountLayout {
   gs::RadixPlan depth;
   size_t scan_status, scan_ticket, pair_ghist, pair_tickets, ctl_end;
-  size_t splat_count, block_sums, gid_count, depth_buffers, rec_orig, total;
+  size_t splat_count, block_sums, gid_count, depth_buffers, rec_orig;
+  size_t orig_slot, hit_bits, total;
 };
 
 CountLayout count_layout(const RasterParams& P) {
@@ -205,6 +206,12 @@ CountLayout count_layout(const RasterParams& P) {
   L.rec_orig = off;  // the count's original-order records (gsplat_hip_bin)
   off += gs::align_up((size_t)P.num_splats * GSPLAT_RECORD_FLOATS * sizeof(float),
                       256);
+  // gsplat_hip_bin's original-order emit: per splat {pair offset, gid}, and
+  // the count's recorded step ballots
+  L.orig_slot = off;
+  off += gs::align_up((size_t)P.num_splats * 2 * sizeof(int32_t), 256);
+  L.hit_bits = off;
+  off += gs::align_up(gs::hit_bits_words(P) * sizeof(uint64_t), 256);
   L.total = off;
   return L;
 }
@@ -336,6 +343,9 @@ int bin_count_impl(const gsplat_raster_meta* meta, const float* means2d,
                           colors,
                           colors != nullptr
                               ? reinterpret_cast<float*>(base + L.rec_orig)
+                              : nullptr,
+                          colors != nullptr
+                              ? reinterpret_cast<uint64_t*>(base + L.hit_bits)
                               : nullptr);
 }
 }  // namespace
@@ -407,7 +417,8 @@ int gsplat_hip_pack_records(const gsplat_raster_meta* meta,
 
 namespace {
 // gsplat_hip_bin_pack; use_records: copy the count's original-order records
-// (bin_count_impl with colors) instead of gathering the attributes.
+// (bin_count_impl with colors) instead of gathering the attributes, and
+// write the original-order emit's offsets and gids.
 int bin_pack_impl(const gsplat_raster_meta* meta, const float* means2d,
                   const float* conics, const float* colors,
                   const float* opacities, const int32_t* perm, float* packed,
@@ -439,6 +450,9 @@ int bin_pack_impl(const gsplat_raster_meta* meta, const float* means2d,
                          s,
                          use_records
                              ? reinterpret_cast<const float*>(base + L.rec_orig)
+                             : nullptr,
+                         use_records
+                             ? reinterpret_cast<int32_t*>(base + L.orig_slot)
                              : nullptr);
   return rc;
 }
@@ -485,7 +499,10 @@ int bucket_low_bits(const RasterParams& P, int64_t n_pairs) {
 }
 
 // hist_counted: the bucket form's histogram is already in the control block
-// (counted by the count launch, summed by the rank launch).
+// (counted by the count launch, summed by the rank launch).  orig_walk: the
+// count wrote its records and step ballots and the pack the original-order
+// offsets (bin_count_impl with colors, bin_pack_impl with use_records), so
+// the emit walks in original order and reuses the ballots.
 int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
                   const int32_t* splat_offsets, int64_t n_pairs,
                   int32_t* binned_ids, int32_t* tile_counts,
@@ -494,7 +511,7 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
                   void* workspace, size_t workspace_bytes, void* stream,
                   int32_t* long_flag, const gs::ZeroSpan* zero = nullptr,
                   const gs::EmitScanArgs* scan = nullptr,
-                  bool hist_counted = false) {
+                  bool hist_counted = false, bool orig_walk = false) {
   RasterParams P;
   int rc = make_params(meta, P);
   if (rc) return rc;
@@ -546,6 +563,11 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
   // bin_pack); n_pairs is the capacity of the buffers and every stage takes
   // the first min(N, n_pairs) pairs.
   const int32_t* n_dev = splat_offsets + P.num_splats;
+  const gs::EmitOrigArgs orig_args{
+      reinterpret_cast<const float*>(cbase + C.rec_orig),
+      reinterpret_cast<const int32_t*>(cbase + C.orig_slot),
+      reinterpret_cast<const uint64_t*>(cbase + C.hit_bits)};
+  const gs::EmitOrigArgs* orig = orig_walk && scan == nullptr ? &orig_args : nullptr;
   // Images of 2^9..2^16 tiles whose buffers hold at most kBucketChunk pairs
   // per bucket on average: the sort is one onesweep pass on the tile bits
   // above the low ones (bits - 8 of them: 2^(bits-8) tiles per bucket, at
@@ -560,7 +582,8 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
     rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals,
                          hist_counted ? 0 : 1,
                          reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
-                         ctl.status, L.pairs.status_words, s, scan, low_bits);
+                         ctl.status, L.pairs.status_words, s, scan, low_bits,
+                         nullptr, orig);
     if (!rc)
       rc = gs::radix_passes(high, ctl, base + L.buffers, keys, vals, nullptr,
                             sorted_keys, high_vals, s, n_dev);
@@ -598,10 +621,12 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
     uint8_t* key_bytes = reinterpret_cast<uint8_t*>(sorted_keys);
     int64_t zero_words = 0;
     uint32_t* zero_span = gs::radix_pair_zero_span(L.pairs, ctl, &zero_words);
-    rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals,
-                         L.pairs.passes,
-                         reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
-                         zero_span, zero_words, s, scan, 0, key_bytes);
+    // the emit counts the second pass's digits (the high tile bits) only:
+    // the first pass's histogram comes from its block scan
+    rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals, 1,
+                         reinterpret_cast<uint32_t*>(base + L.hist),
+                         ctl.ghist + 256, zero_span, zero_words, s, scan, 8,
+                         key_bytes, orig);
     if (!rc)
       rc = gs::radix_pair_sort_ranges(
           L.pairs, ctl, base + L.buffers, key_bytes, keys,
@@ -617,7 +642,8 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
   rc = gs::launch_emit(P, packed, splat_offsets, n_pairs, keys, vals,
                        L.pairs.passes,
                        reinterpret_cast<uint32_t*>(base + L.hist), ctl.ghist,
-                       ctl.status, L.pairs.status_words, s, scan);
+                       ctl.status, L.pairs.status_words, s, scan, 0, nullptr,
+                       orig);
   // 2. stable sort by tile
   if (!rc)
     rc = gs::radix_passes(L.pairs, ctl, base + L.buffers, keys, vals, nullptr,
@@ -813,7 +839,7 @@ int bin_impl(const gsplat_raster_meta* meta, const float* means2d,
   rc = bin_emit_impl(meta, packed, splat_offsets, capacity, binned_ids,
                      nullptr, tile_offsets, status_dev, cws, cbytes, ews,
                      ebytes, s, host_words != nullptr ? long_dev : nullptr,
-                     zero);
+                     zero, nullptr, false, true);
   if (rc || host_words == nullptr) return rc;
   // 5. N (from the pack scan), the status and the long-range flag to the host
   return report(splat_offsets + P.num_splats);

@@ -145,13 +145,19 @@ int launch_depth_ranks_small(void* buffers, int32_t* perm, int64_t G,
 int count_blocks(const RasterParams& P);
 // With colors and rec_orig (float [BG*16]) the count also writes each
 // splat's packed record in original order with its hit count in the orig
-// slot, for launch_pack's rec_orig.
+// slot, for launch_pack's rec_orig.  With hit_bits (hit_bits_words(P)
+// words) it records each wavefront's first kHitSlab walk steps' hit
+// ballots, which launch_emit's original-order walk then reads instead of
+// testing those candidates again.
+constexpr int kHitSlab = 128;
+size_t hit_bits_words(const RasterParams& P);
 int launch_count(const RasterParams& P, const float* means2d,
                  const float* conics, const float* opacities,
                  int32_t* splat_count, int32_t* block_sums,
                  int32_t* pair_count, uint32_t* zero_words,
                  int64_t n_zero_words, hipStream_t stream,
-                 const float* colors = nullptr, float* rec_orig = nullptr);
+                 const float* colors = nullptr, float* rec_orig = nullptr,
+                 uint64_t* hit_bits = nullptr);
 // count_depth_runs: the count (splat_count, zero_words as above; no block
 // sums and no N) and the first launch of the small-image depth order (runs
 // into depth_buffers) as one launch.  Requires P.num_splats > 0 and
@@ -178,13 +184,15 @@ int launch_count_depth_runs(const RasterParams& P, const float* means2d,
 // of splat_count[perm]) via a look-back scan whose status
 // (count_scan_blocks(P) words) and ticket must be zero.
 // err: the give-up status word of the look-back (zero before the launch).
+// orig_slot (int32 [BG][2], may be null): per original index {pair offset,
+// gid}, for launch_emit's original-order walk.
 int launch_pack(const RasterParams& P, const float* means2d,
                 const float* conics, const float* colors,
                 const float* opacities, const uint32_t* perm,
                 const int32_t* splat_count, float* packed,
                 int32_t* splat_offsets, uint64_t* scan_status,
                 uint32_t* scan_ticket, uint32_t* err, hipStream_t stream,
-                const float* rec_orig = nullptr);
+                const float* rec_orig = nullptr, int32_t* orig_slot = nullptr);
 int count_scan_blocks(const RasterParams& P);
 // pack_records: the packed records of splats already in depth order
 // (record gid from attributes gid, orig = gid).
@@ -215,13 +223,23 @@ struct EmitScanArgs {
   int32_t* splat_offsets;
   const uint32_t* block_totals;
 };
+// With orig (not with scan), the emit walks the splats in original order,
+// as the count did: from the count's records (rec_orig, launch_count's),
+// the pack's orig_slot and the count's hit_bits (may be null: every
+// candidate is tested), writing the same pairs at the same positions.
+struct EmitOrigArgs {
+  const float* rec_orig;
+  const int32_t* orig_slot;
+  const uint64_t* hit_bits;
+};
 int launch_emit(const RasterParams& P, const float* packed,
                 const int32_t* splat_offsets, int64_t capacity, uint32_t* keys,
                 uint32_t* vals, int pair_passes, uint32_t* hist_partials,
                 uint32_t* pair_ghist, uint32_t* pair_status,
                 int64_t pair_status_words, hipStream_t stream,
                 const EmitScanArgs* scan = nullptr, int hist_shift = 0,
-                uint8_t* key_bytes = nullptr);
+                uint8_t* key_bytes = nullptr,
+                const EmitOrigArgs* orig = nullptr);
 // Second half of the pair sort when one onesweep pass has ordered the pairs
 // by the tile bits above low_bits (a bucket = 2^low_bits consecutive tiles;
 // at most 256 buckets): one workgroup per bucket sorts its pairs stably on

@@ -322,11 +322,13 @@ __global__ __launch_bounds__(kThreads) void rs_block_counts_kernel(
 // thread t of a group for digit t) takes chunk c: group q sums the totals of
 // every kScanQ-th chunk before it from q on (no order among workgroups) and
 // the counts of the chunk's rows q kRows .. q kRows + kRows - 1; the groups
-// combine their sums in LDS, then each scans its rows.
+// combine their sums in LDS, then each scans its rows.  The workgroup of the
+// last chunk also writes each digit's total to digit_tot[0..255] (the pass's
+// global histogram; may be null).
 template <int kBlockRounds>
 __global__ __launch_bounds__(256 * kScanQ) void rs_block_scan_kernel(
     uint32_t* status, const uint32_t* chunk_tot, int64_t n_cap,
-    const int32_t* n_dev) {
+    const int32_t* n_dev, uint32_t* digit_tot) {
   constexpr int64_t kItems = (int64_t)kThreads * kBlockRounds;
   constexpr int kRows = kScanChunk / kScanQ;
   __shared__ uint32_t part[kScanQ][256];
@@ -363,6 +365,9 @@ __global__ __launch_bounds__(256 * kScanQ) void rs_block_scan_kernel(
     if (row < nb) status[(int64_t)(b0 + row) * 256 + t] = run;
     run += v[k];
   }
+  // (the last group's run ends at the digit's total)
+  if (digit_tot != nullptr && b0 + nb == nblk && q == kScanQ - 1)
+    digit_tot[t] = run;
 }
 
 // A block of 256 kR elements is ranked by onesweep_waves(kR) wavefronts of
@@ -820,8 +825,10 @@ int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
              C.status + status_per_pass, C.err,
              C.ghist, tile_offsets, num_tiles};
   // The first pass takes its block prefixes from a count and a scan of the
-  // key bytes (1 B/pair read); the second looks back (its counts would cost
-  // a read of the 4-byte words, more than its look-back does).
+  // key bytes (1 B/pair read), and its global histogram (ghist[0..255]) from
+  // the scan; the second looks back (its counts would cost a read of the
+  // 4-byte words, more than its look-back does), with the histogram of the
+  // high tile bits at ghist[256..511] from the emit.
   constexpr int kA = kValsIn | kKeyBytes | kPreCounts;
   constexpr int kB = kPairRanges;
   uint32_t* chunk_a = C.status + 2 * (int64_t)L.nblk * 256;
@@ -833,7 +840,7 @@ int radix_pair_sort_ranges(const RadixPlan& L, const RadixCtl& C,
                 chunk_a);                                                    \
   launch_traced("rs_block_scan_kernel(pairs:lo)", (rs_block_scan_kernel<R>), \
                 chunks, dim3(256 * kScanQ), 0, stream, a.status, chunk_a,     \
-                L.n_seg, n_dev);                                             \
+                L.n_seg, n_dev, C.ghist);                                    \
   launch_traced("rs_onesweep_kernel(pairs:lo)", (rs_onesweep_kernel<kA, R>), \
                 grid, dim3(64 * onesweep_waves(R)), 0, stream, a);           \
   launch_traced("rs_onesweep_kernel(pairs:hi)", (rs_onesweep_kernel<kB, R>), \
