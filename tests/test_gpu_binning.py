@@ -459,6 +459,47 @@ def test_binning_large_splats(gpu, seed, H, W, G, elong):
         _assert_bins_equal(_gpu_bins(sc, H, W, 1, G), ob, sc, 1, G)
 
 
+def test_large_image_emit_with_recorded_ballots(gpu):
+    """Images above 131,072 splats: the one-call binning's count records each wavefront's first 128
+    walk-step hit ballots, and the emit walks the count's wavefronts in original order, taking a
+    recorded step's hits from its ballot (a step without hits is skipped) and testing the steps past
+    the record itself.  The first 32 splats (one count wavefront) are long thin splats at about 45
+    degrees, each with thousands of candidate tiles and few hits, so that wavefront walks thousands
+    of steps past its record; the rest are ordinary small splats.  Bit-exact against the oracle on
+    the four-call binning and on the one-call path."""
+    rng = np.random.default_rng(61)
+    H, W, B, G = 2048, 2048, 1, 140_000
+    print(f"large image, recorded ballots {W}x{H} G={G}", flush=True)
+    sc = make_scene_2d(1, seed=61, G=G, B=B, H=H, W=W)
+    n = 32
+    s1 = rng.uniform(500.0, 700.0, n)     # along the axis (px)
+    s2 = rng.uniform(1.5, 3.0, n)         # across it
+    th = np.pi / 4 + rng.uniform(-0.05, 0.05, n)
+    c, s = np.cos(th), np.sin(th)
+    ix, iy = 1 / s1 ** 2, 1 / s2 ** 2
+    q = np.stack([c * c * ix + s * s * iy, c * s * (ix - iy), s * s * ix + c * c * iy], -1)
+    o = rng.uniform(0.5, 1.0, n)
+    sc["means2d"][0, :n] = torch.from_numpy(rng.uniform(700.0, 1300.0, (n, 2)).astype(np.float32))
+    sc["conics"][0, :n] = torch.from_numpy(q.astype(np.float32))
+    sc["opacities"][0, :n] = torch.from_numpy(o.astype(np.float32))
+    # the wavefront's candidates (its splats' clipped boxes, a lower bound) far exceed its record's
+    # 128 steps of 64
+    a_, b_, c_ = q[:, 0], q[:, 1], q[:, 2]
+    det = a_ * c_ - b_ * b_
+    tau = 2.0 * np.log(o * 255.0)
+    hx, hy = np.sqrt(tau * c_ / det), np.sqrt(tau * a_ / det)
+    mx, my = sc["means2d"][0, :n, 0].numpy(), sc["means2d"][0, :n, 1].numpy()
+    bw = np.floor(np.minimum(mx + hx, W - 1) / 16) - np.floor(np.maximum(mx - hx, 0) / 16) + 1
+    bh = np.floor(np.minimum(my + hy, H - 1) / 16) - np.floor(np.maximum(my - hy, 0) / 16) + 1
+    assert (bw * bh).sum() > 4 * 128 * 64
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    print(f"  pairs {ob.binned_ids.size}, wavefront 0 candidates >= {int((bw * bh).sum())}", flush=True)
+    key = _capacity_key(B, G, H, W)
+    _ops._capacity.pop(key, None)
+    for _ in range(2):   # the four-call binning, then the one-call path with the remembered buffer
+        _assert_bins_equal(_gpu_bins(sc, H, W, B, G), ob, sc, B, G)
+
+
 def test_binning_all_culled(gpu):
     B, G, H, W = 1, 100, 32, 32
     sc = make_scene_2d(0, seed=1, G=G, H=H, W=W)
