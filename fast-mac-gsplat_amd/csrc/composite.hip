@@ -1106,8 +1106,9 @@ __global__ __launch_bounds__(256) void render_grads_unpack_kernel(GradOut G,
 // them (with the same workspace layout) and the tile's stop exceeds one.
 __device__ __forceinline__ bool heavy_backward(const HeavyState& H, int tile,
                                                int nstop) {
-  return H.tile_slot != nullptr && H.counters[2] == H.max_slots &&
-         H.tile_slot[tile] >= 0 && nstop > kSegSplats;
+  // (the stop first: most tiles need neither of the loads after it)
+  if (nstop <= kSegSplats || H.tile_slot == nullptr) return false;
+  return H.counters[2] == H.max_slots && H.tile_slot[tile] >= 0;
 }
 
 // Decodes segment slot m: tile, segment index k, segment count and the range
@@ -1160,12 +1161,15 @@ __attribute__((amdgpu_waves_per_eu(kWaves, 8))) void render_bwd_kernel(
       // seg_blocks is a multiple of 8, so the XCD-aware mapping is kept
       tile = xcd_remap(bid - seg_blocks, P.num_tiles);
       hi = tile_stop[tile];
-      if (hi <= 0) return;
-      if (heavy_backward(H, tile, hi)) return;  // walked as segments
     }
+    // the tile's range start and pixel state are loaded before its stop is
+    // waited for (an empty tile's loads are wasted: few tiles are empty)
+    const int start = tile_offsets[tile];
     const TileCoord tc = tile_coord_of(P, tile);
     BwdPixels Q;
     load_bwd_pixels(P, tc, final_T, last_in, grad_rgb, Q);
+    // (a tile walked as segments returns here)
+    if (!seg && (hi <= 0 || heavy_backward(H, tile, hi))) return;
     {
       if (kseg < nseg - 1) {
         // Pixels composited past this segment: T and gT at its end from the
@@ -1203,11 +1207,9 @@ __attribute__((amdgpu_waves_per_eu(kWaves, 8))) void render_bwd_kernel(
     // Q.Tc holds T_final, or T at the segment's end for pixels alive past it
     // (T_end > T_final > threshold), so the test sees the final state.
     if (needs_last_test(P, tc, Q))
-      bwd_walk<true, kAcc>(P, packed, binned, tile_offsets[tile], lo, hi, tc,
-                           SH, Q, G);
+      bwd_walk<true, kAcc>(P, packed, binned, start, lo, hi, tc, SH, Q, G);
     else
-      bwd_walk<false, kAcc>(P, packed, binned, tile_offsets[tile], lo, hi, tc,
-                            SH, Q, G);
+      bwd_walk<false, kAcc>(P, packed, binned, start, lo, hi, tc, SH, Q, G);
   }
 }
 
