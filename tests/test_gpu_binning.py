@@ -189,6 +189,44 @@ def test_two_pass_pair_sort(gpu, B, G, H, W, cap):
         _assert_bins_equal(_gpu_bins(sc, H, W, B, G), ob, sc, B, G)
 
 
+def _check_short_buffer(st, ob, n, cap):
+    """A binning into a buffer of cap < N pairs: the first `cap` pairs of the full order, each
+    tile's kept pairs in order, and every pair of a splat whose range ends by cap kept."""
+    assert st.capacity == cap
+    offsets = st.tile_offsets.cpu().numpy()
+    assert offsets[0] == 0 and offsets[-1] == cap and np.all(np.diff(offsets) >= 0)
+    assert not st.confirm() and st.n_pairs == n
+    got = st.pairs[:cap].cpu().numpy()
+    splat_end = st.splat_offsets.cpu().numpy()[1:]
+    for t in range(ob.tile_offsets.size - 1):
+        want = ob.binned_ids[ob.tile_offsets[t]:ob.tile_offsets[t + 1]]
+        have = got[offsets[t]:offsets[t + 1]]
+        assert np.all(np.diff(have) > 0) and np.isin(have, want).all()
+        assert np.isin(want[splat_end[want] <= cap], have).all()
+
+
+def test_large_image_short_buffer(gpu):
+    """Images above 131,072 splats bin with the emit in original order over the count's records
+    and recorded ballots: with a pair buffer below N the one-call binning keeps exactly the first
+    `capacity` pairs, as the depth-order emit does."""
+    B, G, H, W = 1, 140_000, 512, 512
+    print(f"large image, short buffer B={B} G={G} {H}x{W}", flush=True)
+    sc = make_scene_2d(1, seed=43, G=G, B=B, H=H, W=W)
+    sc["conics"] = sc["conics"] / 16.0   # splats 4 times larger
+    _, _, ob = _oracle_bins(sc, H, W, B, G)
+    n = ob.binned_ids.size
+    print(f"  pairs {n}", flush=True)
+    key = _capacity_key(B, G, H, W)
+    dev = torch.device("cuda:0")
+    meta = _lib.make_raster_meta(H, W, B, G, 1.0 / 255.0, 1e-4, (0.0, 0.0, 0.0))
+    flat = [sc[k].reshape(B * G, -1).squeeze(-1).contiguous().to(dev) for k in KEYS]
+    cap = n // 2
+    _ops._capacity[key] = cap
+    _check_short_buffer(_ops.bin_gaussians(meta, *flat, defer_check=True), ob, n, cap)
+    _ops._capacity[key] = n + 1000   # and a buffer that holds them all: bit-exact
+    _assert_bins_equal(_gpu_bins(sc, H, W, B, G), ob, sc, B, G)
+
+
 def test_two_pass_pair_sort_empty_and_short(gpu):
     """The two-pass sort with no pair at all (every splat culled, a large remembered buffer) leaves
     every range empty, and with a buffer below N keeps exactly the first `capacity` pairs."""
@@ -207,17 +245,7 @@ def test_two_pass_pair_sort_empty_and_short(gpu):
     _ops._capacity[key] = cap
     flat = [sc[k].reshape(B * G, -1).squeeze(-1).contiguous().to(dev) for k in KEYS]
     st = _ops.bin_gaussians(meta, *flat, defer_check=True)
-    assert st.capacity == cap
-    offsets = st.tile_offsets.cpu().numpy()
-    assert offsets[0] == 0 and offsets[-1] == cap and np.all(np.diff(offsets) >= 0)
-    assert not st.confirm() and st.n_pairs == n
-    got = st.pairs[:cap].cpu().numpy()
-    splat_end = st.splat_offsets.cpu().numpy()[1:]
-    for t in range(ob.tile_offsets.size - 1):
-        want = ob.binned_ids[ob.tile_offsets[t]:ob.tile_offsets[t + 1]]
-        have = got[offsets[t]:offsets[t + 1]]
-        assert np.all(np.diff(have) > 0) and np.isin(have, want).all()
-        assert np.isin(want[splat_end[want] <= cap], have).all()
+    _check_short_buffer(st, ob, n, cap)
     # every splat culled, the buffer remembered from above
     _ops._capacity[key] = 2 * n
     sc0 = dict(sc)
