@@ -567,7 +567,8 @@ int bin_emit_impl(const gsplat_raster_meta* meta, const float* packed,
       reinterpret_cast<const float*>(cbase + C.rec_orig),
       reinterpret_cast<const int32_t*>(cbase + C.orig_slot),
       reinterpret_cast<const uint64_t*>(cbase + C.hit_bits)};
-  const gs::EmitOrigArgs* orig = orig_walk && scan == nullptr ? &orig_args : nullptr;
+  const gs::EmitOrigArgs* orig =
+      orig_walk && scan == nullptr ? &orig_args : nullptr;
   // Images of 2^9..2^16 tiles whose buffers hold at most kBucketChunk pairs
   // per bucket on average: the sort is one onesweep pass on the tile bits
   // above the low ones (bits - 8 of them: 2^(bits-8) tiles per bucket, at
