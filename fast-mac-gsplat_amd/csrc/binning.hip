@@ -46,6 +46,13 @@
 //   buffer holds at most 4096 pairs per bucket on average).
 // host_report_kernel  the binning's report to host memory where the
 //   forward compositor does not write it.
+//
+// Larger images in one call: count_kernel also keeps each wavefront's first
+// kHitSlab step ballots and the splats' records in original order;
+// pack_kernel gives each original index its pair offset and gid; and
+// emit_kernel<false, true> walks the splats in the count's original order,
+// taking the hits of the recorded steps from the ballots instead of testing
+// them again.
 #include <algorithm>
 
 #include "gs_internal.h"
